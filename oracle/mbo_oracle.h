@@ -1,0 +1,120 @@
+/*
+ * mbo_oracle.h — CPU restatement of MacBoost's tree-build hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * implementation in macboost_amd/.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it, and only as the checker or as the
+ * timed CPU baseline — never as the thing measured or shipped.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the MacBoost v1.0.0 source tree).  Histogram sums are exact integers
+ * (int64) over the reference's quantised gradient words, dequantised once per
+ * candidate; this is the deterministic summation the HIP path also uses (the
+ * reference dequantises per 4096-row group and sums float atomics, which is
+ * run-to-run nondeterministic, MacBoostTests.swift:8-10).
+ */
+#ifndef MBO_ORACLE_H
+#define MBO_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_FLAG_DEFAULT_LEFT 1u
+#define ORC_FLAG_CATEGORICAL 2u
+
+/* Objectives, numbered as Booster.swift:5-14. */
+enum { ORC_OBJ_L2 = 0, ORC_OBJ_LOGISTIC = 1, ORC_OBJ_MAE = 2, ORC_OBJ_HUBER = 3,
+       ORC_OBJ_QUANTILE = 4, ORC_OBJ_POISSON = 5, ORC_OBJ_TWEEDIE = 6 };
+
+typedef struct {
+    int32_t num_trees;
+    int32_t max_depth;
+    int32_t num_bins;          /* includes the reserved missing bin */
+    int32_t objective;
+    int32_t num_leaves;        /* 0 = level-wise growth */
+    float learning_rate;
+    float lambda;
+    float min_child_hess;
+    float min_split_gain;
+    float cat_smooth;
+    float alpha;
+    float aux;                 /* scale_pos_weight (logistic) / variance power (tweedie) */
+} orc_params;
+
+/* One split candidate result: SplitResult (Shaders.swift:334) plus the exact
+ * integer left sums the decision step needs. */
+typedef struct {
+    float gain;
+    uint32_t bin;
+    float gl, hl;
+    uint32_t flags;
+    int64_t gl_int, hl_int;
+} orc_split;
+
+/* Flat forest, nodes_per_tree heap slots per tree (Booster.swift:119-146). */
+typedef struct {
+    int32_t num_trees;
+    int32_t nodes_per_tree;
+    int32_t *feature;          /* < 0 => leaf */
+    float *threshold;
+    float *leaf;
+    uint8_t *flags;
+    uint32_t *cat_mask;        /* 8 words per node, may be NULL */
+    float *gain;
+    float *cover;
+    uint32_t *split_bin;       /* bin of each split (oracle extra, parity aid) */
+} orc_forest;
+
+/* --- data generation (DataGen.swift) ------------------------------------ */
+uint64_t orc_splitmix_next(uint64_t *state);
+float orc_splitmix_uniform(uint64_t *state);
+float orc_splitmix_normal(uint64_t *state);
+void orc_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise,
+                  float *x_fm, float *y);
+
+/* --- binning (Binner.swift, Shaders.swift:46-76) ------------------------- */
+void orc_compute_edges(const float *x, int64_t rows, int32_t cols,
+                       int64_t row_stride, int64_t col_stride, int32_t num_bins,
+                       const uint8_t *is_cat, int64_t sample_cap, float *edges);
+uint8_t orc_bin_value(float v, const float *edges_f, int32_t num_bins, int is_cat);
+void orc_bin_matrix(const float *x, int64_t rows, int32_t cols, int64_t row_stride,
+                    int64_t col_stride, const float *edges, const uint8_t *is_cat,
+                    int32_t num_bins, uint8_t *bins_fm);
+
+/* --- gradients / quantisation (Shaders.swift:96-192) --------------------- */
+float orc_base_score(const float *y, const float *w, int64_t rows, int32_t objective,
+                     float scale_pos_weight);
+void orc_gradients(const float *preds, const float *y, const float *w, int64_t rows,
+                   int32_t objective, float alpha, float aux, float *g, float *h,
+                   float *max_g, float *max_h);
+void orc_quantize(const float *g, const float *h, int64_t rows, float max_g,
+                  float max_h, uint32_t *ghq);
+
+/* --- histogram / split search (Shaders.swift:212-464) ------------------- */
+void orc_hist_node(const uint8_t *bins_fm, int64_t rows, int32_t cols, int32_t num_bins,
+                   const uint32_t *ghq, const uint32_t *row_idx, int64_t n,
+                   int64_t *hg, int64_t *hh);
+void orc_find_split(const int64_t *hg, const int64_t *hh, int32_t num_bins, int is_cat,
+                    int monotone, int64_t g_tot, int64_t h_tot, float g_inv, float h_inv,
+                    float lambda, float min_child_hess, float cat_smooth, orc_split *out);
+int32_t orc_cat_order(const int64_t *hg, const int64_t *hh, int32_t num_bins,
+                      float g_inv, float h_inv, float cat_smooth, uint16_t *order);
+
+/* --- training (Booster.swift:445-1701 level-wise / :967-1310 leaf-wise) -- */
+int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t cols,
+            const float *y, const float *w, const uint8_t *is_cat, const int8_t *monotone,
+            const float *edges, float base_score, float *preds, orc_forest *out);
+
+/* --- inference (Booster.swift:2035-2074, SHAP.swift:56-325) ------------ */
+void orc_predict(const orc_forest *m, float base_score, int32_t data_bins,
+                 const float *x_fm, int64_t rows, int32_t cols, float *out);
+void orc_treeshap(const orc_forest *m, float base_score, int32_t data_bins,
+                  const float *x_fm, int64_t rows, int32_t cols, float *out);
+double orc_shap_bias(const orc_forest *m, float base_score);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

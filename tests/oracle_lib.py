@@ -1,0 +1,345 @@
+"""ctypes front end of the CPU oracle (oracle/liboracle.so).
+
+Test infrastructure only: tests, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` use it as the checker.  Every function
+mirrors one entry of ``oracle/mbo_oracle.h``.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = ROOT / "oracle" / "liboracle.so"
+
+FLAG_DEFAULT_LEFT = 1
+FLAG_CATEGORICAL = 2
+OBJ_L2, OBJ_LOGISTIC, OBJ_MAE, OBJ_HUBER, OBJ_QUANTILE, OBJ_POISSON, OBJ_TWEEDIE = range(7)
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _configure(_lib)
+    return _lib
+
+
+class OrcParams(ctypes.Structure):
+    _fields_ = [
+        ("num_trees", ctypes.c_int32), ("max_depth", ctypes.c_int32),
+        ("num_bins", ctypes.c_int32), ("objective", ctypes.c_int32),
+        ("num_leaves", ctypes.c_int32), ("learning_rate", ctypes.c_float),
+        ("lambda_", ctypes.c_float), ("min_child_hess", ctypes.c_float),
+        ("min_split_gain", ctypes.c_float), ("cat_smooth", ctypes.c_float),
+        ("alpha", ctypes.c_float), ("aux", ctypes.c_float),
+    ]
+
+
+class OrcSplit(ctypes.Structure):
+    _fields_ = [
+        ("gain", ctypes.c_float), ("bin", ctypes.c_uint32), ("gl", ctypes.c_float),
+        ("hl", ctypes.c_float), ("flags", ctypes.c_uint32),
+        ("gl_int", ctypes.c_int64), ("hl_int", ctypes.c_int64),
+    ]
+
+
+class OrcForest(ctypes.Structure):
+    _fields_ = [
+        ("num_trees", ctypes.c_int32), ("nodes_per_tree", ctypes.c_int32),
+        ("feature", ctypes.c_void_p), ("threshold", ctypes.c_void_p),
+        ("leaf", ctypes.c_void_p), ("flags", ctypes.c_void_p),
+        ("cat_mask", ctypes.c_void_p), ("gain", ctypes.c_void_p),
+        ("cover", ctypes.c_void_p), ("split_bin", ctypes.c_void_p),
+    ]
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+
+
+def _configure(l: ctypes.CDLL) -> None:
+    l.orc_splitmix_next.restype = ctypes.c_uint64
+    l.orc_splitmix_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    l.orc_friedman.argtypes = [_I64, _I32, ctypes.c_uint64, _F, _P, _P]
+    l.orc_compute_edges.argtypes = [_P, _I64, _I32, _I64, _I64, _I32, _P, _I64, _P]
+    l.orc_bin_matrix.argtypes = [_P, _I64, _I32, _I64, _I64, _P, _P, _I32, _P]
+    l.orc_base_score.restype = _F
+    l.orc_base_score.argtypes = [_P, _P, _I64, _I32, _F]
+    l.orc_gradients.argtypes = [_P, _P, _P, _I64, _I32, _F, _F, _P, _P, _P, _P]
+    l.orc_quantize.argtypes = [_P, _P, _I64, _F, _F, _P]
+    l.orc_hist_node.argtypes = [_P, _I64, _I32, _I32, _P, _P, _I64, _P, _P]
+    l.orc_find_split.argtypes = [_P, _P, _I32, ctypes.c_int, ctypes.c_int, _I64, _I64, _F,
+                                 _F, _F, _F, _F, ctypes.POINTER(OrcSplit)]
+    l.orc_cat_order.restype = _I32
+    l.orc_cat_order.argtypes = [_P, _P, _I32, _F, _F, _F, _P]
+    l.orc_fit.restype = ctypes.c_int
+    l.orc_fit.argtypes = [ctypes.POINTER(OrcParams), _P, _I64, _I32, _P, _P, _P, _P, _P, _F,
+                          _P, ctypes.POINTER(OrcForest)]
+    l.orc_predict.argtypes = [ctypes.POINTER(OrcForest), _F, _I32, _P, _I64, _I32, _P]
+    l.orc_treeshap.argtypes = [ctypes.POINTER(OrcForest), _F, _I32, _P, _I64, _I32, _P]
+    l.orc_shap_bias.restype = ctypes.c_double
+    l.orc_shap_bias.argtypes = [ctypes.POINTER(OrcForest), _F]
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+# --------------------------------------------------------------------------
+# data generation / binning
+# --------------------------------------------------------------------------
+
+def splitmix_stream(seed: int, n: int) -> np.ndarray:
+    s = ctypes.c_uint64(seed)
+    return np.array([lib().orc_splitmix_next(ctypes.byref(s)) for _ in range(n)], dtype=np.uint64)
+
+
+def friedman(rows: int, cols: int, seed: int, noise: float = 1.0):
+    """Feature-major X [cols, rows] and y, DataGen.friedman."""
+    x = np.empty((cols, rows), dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    lib().orc_friedman(rows, cols, ctypes.c_uint64(seed), noise, _ptr(x), _ptr(y))
+    return x, y
+
+
+def compute_edges(x_fm: np.ndarray, num_bins: int, is_cat=None, sample_cap: int = 200_000):
+    cols, rows = x_fm.shape
+    x_fm = np.ascontiguousarray(x_fm, dtype=np.float32)
+    cat = None if is_cat is None else np.ascontiguousarray(is_cat, dtype=np.uint8)
+    edges = np.zeros((cols, num_bins - 2), dtype=np.float32)
+    lib().orc_compute_edges(_ptr(x_fm), rows, cols, 1, rows, num_bins, _ptr(cat), sample_cap,
+                            _ptr(edges))
+    return edges
+
+
+def bin_matrix(x_fm: np.ndarray, edges: np.ndarray, num_bins: int, is_cat=None):
+    cols, rows = x_fm.shape
+    x_fm = np.ascontiguousarray(x_fm, dtype=np.float32)
+    cat = None if is_cat is None else np.ascontiguousarray(is_cat, dtype=np.uint8)
+    out = np.empty((cols, rows), dtype=np.uint8)
+    lib().orc_bin_matrix(_ptr(x_fm), rows, cols, 1, rows, _ptr(edges), _ptr(cat), num_bins,
+                         _ptr(out))
+    return out
+
+
+# --------------------------------------------------------------------------
+# gradients / histograms / splits
+# --------------------------------------------------------------------------
+
+def base_score(y, w=None, objective=OBJ_L2, scale_pos_weight=1.0) -> float:
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    return float(lib().orc_base_score(_ptr(y), _ptr(w), len(y), objective, scale_pos_weight))
+
+
+def gradients(preds, y, w=None, objective=OBJ_L2, alpha=0.9, aux=1.0):
+    n = len(y)
+    preds = np.ascontiguousarray(preds, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    g = np.empty(n, np.float32)
+    h = np.empty(n, np.float32)
+    mg = np.zeros(1, np.float32)
+    mh = np.zeros(1, np.float32)
+    lib().orc_gradients(_ptr(preds), _ptr(y), _ptr(w), n, objective, alpha, aux, _ptr(g),
+                        _ptr(h), _ptr(mg), _ptr(mh))
+    return g, h, float(mg[0]), float(mh[0])
+
+
+def quantize(g, h, max_g, max_h):
+    out = np.empty(len(g), np.uint32)
+    lib().orc_quantize(_ptr(np.ascontiguousarray(g, np.float32)),
+                       _ptr(np.ascontiguousarray(h, np.float32)), len(g), max_g, max_h,
+                       _ptr(out))
+    return out
+
+
+def hist_node(bins_fm, num_bins, ghq, rows_idx=None):
+    cols, rows = bins_fm.shape
+    bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
+    ghq = np.ascontiguousarray(ghq, np.uint32)
+    idx = None if rows_idx is None else np.ascontiguousarray(rows_idx, np.uint32)
+    n = rows if idx is None else len(idx)
+    hg = np.empty((cols, num_bins), np.int64)
+    hh = np.empty((cols, num_bins), np.int64)
+    lib().orc_hist_node(_ptr(bins_fm), rows, cols, num_bins, _ptr(ghq), _ptr(idx), n, _ptr(hg),
+                        _ptr(hh))
+    return hg, hh
+
+
+def find_split(hg, hh, is_cat, monotone, g_tot, h_tot, g_inv, h_inv, lam=1.0, mch=1.0,
+               cat_smooth=10.0) -> OrcSplit:
+    hg = np.ascontiguousarray(hg, np.int64)
+    hh = np.ascontiguousarray(hh, np.int64)
+    r = OrcSplit()
+    lib().orc_find_split(_ptr(hg), _ptr(hh), len(hg), int(is_cat), int(monotone), int(g_tot),
+                         int(h_tot), g_inv, h_inv, lam, mch, cat_smooth, ctypes.byref(r))
+    return r
+
+
+def cat_order(hg, hh, g_inv, h_inv, cat_smooth=10.0):
+    hg = np.ascontiguousarray(hg, np.int64)
+    hh = np.ascontiguousarray(hh, np.int64)
+    order = np.zeros(256, np.uint16)
+    m = lib().orc_cat_order(_ptr(hg), _ptr(hh), len(hg), g_inv, h_inv, cat_smooth, _ptr(order))
+    return order[:m]
+
+
+# --------------------------------------------------------------------------
+# models
+# --------------------------------------------------------------------------
+
+@dataclass
+class Forest:
+    """Flat heap forest, [num_trees, nodes_per_tree] per array."""
+    feature: np.ndarray
+    threshold: np.ndarray
+    leaf: np.ndarray
+    flags: np.ndarray
+    cat_mask: np.ndarray | None
+    gain: np.ndarray
+    cover: np.ndarray
+    split_bin: np.ndarray | None = None
+
+    @property
+    def num_trees(self):
+        return self.feature.shape[0]
+
+    @property
+    def nodes_per_tree(self):
+        return self.feature.shape[1]
+
+    @classmethod
+    def empty(cls, num_trees, nodes, with_cats=True):
+        return cls(
+            feature=np.full((num_trees, nodes), -1, np.int32),
+            threshold=np.zeros((num_trees, nodes), np.float32),
+            leaf=np.zeros((num_trees, nodes), np.float32),
+            flags=np.zeros((num_trees, nodes), np.uint8),
+            cat_mask=np.zeros((num_trees, nodes, 8), np.uint32) if with_cats else None,
+            gain=np.zeros((num_trees, nodes), np.float32),
+            cover=np.zeros((num_trees, nodes), np.float32),
+            split_bin=np.zeros((num_trees, nodes), np.uint32),
+        )
+
+    def c(self) -> OrcForest:
+        for name in ("feature", "threshold", "leaf", "flags", "gain", "cover"):
+            assert getattr(self, name).flags.c_contiguous
+        f = OrcForest()
+        f.num_trees = self.num_trees
+        f.nodes_per_tree = self.nodes_per_tree
+        f.feature = _ptr(self.feature)
+        f.threshold = _ptr(self.threshold)
+        f.leaf = _ptr(self.leaf)
+        f.flags = _ptr(self.flags)
+        f.cat_mask = _ptr(self.cat_mask)
+        f.gain = _ptr(self.gain)
+        f.cover = _ptr(self.cover)
+        f.split_bin = _ptr(self.split_bin)
+        return f
+
+
+@dataclass
+class OracleModel:
+    forest: Forest
+    base_score: float
+    num_bins: int
+    preds: np.ndarray
+    edges: np.ndarray
+
+
+def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objective=OBJ_L2,
+        num_leaves=0, learning_rate=0.1, lam=1.0, min_child_hess=1.0, min_split_gain=0.0,
+        cat_smooth=10.0, alpha=0.9, aux=1.0, w=None, is_cat=None, monotone=None,
+        base=None) -> OracleModel:
+    cols, rows = bins_fm.shape
+    p = OrcParams(num_trees, max_depth, num_bins, objective, num_leaves, learning_rate, lam,
+                  min_child_hess, min_split_gain, cat_smooth, alpha, aux)
+    y = np.ascontiguousarray(y, np.float32)
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    if base is None:
+        base = base_score(y, w, objective, aux if objective == OBJ_LOGISTIC else 1.0)
+    preds = np.full(rows, base, np.float32)
+    nodes = (1 << (max_depth + 1)) - 1
+    forest = Forest.empty(num_trees, nodes)
+    cat = None if is_cat is None else np.ascontiguousarray(is_cat, np.uint8)
+    mono = None if monotone is None else np.ascontiguousarray(monotone, np.int8)
+    edges = np.ascontiguousarray(edges, np.float32)
+    fc = forest.c()
+    rc = lib().orc_fit(ctypes.byref(p), _ptr(np.ascontiguousarray(bins_fm, np.uint8)), rows,
+                       cols, _ptr(y), _ptr(w), _ptr(cat), _ptr(mono), _ptr(edges), base,
+                       _ptr(preds), ctypes.byref(fc))
+    if rc != 0:
+        raise RuntimeError(f"orc_fit failed: {rc}")
+    return OracleModel(forest, float(base), num_bins, preds, edges)
+
+
+def predict(forest: Forest, base: float, num_bins: int, x_fm) -> np.ndarray:
+    cols, rows = x_fm.shape
+    out = np.empty(rows, np.float32)
+    fc = forest.c()
+    lib().orc_predict(ctypes.byref(fc), base, num_bins - 1,
+                      _ptr(np.ascontiguousarray(x_fm, np.float32)), rows, cols, _ptr(out))
+    return out
+
+
+def treeshap(forest: Forest, base: float, num_bins: int, x_fm) -> np.ndarray:
+    cols, rows = x_fm.shape
+    out = np.empty((rows, cols + 1), np.float32)
+    fc = forest.c()
+    lib().orc_treeshap(ctypes.byref(fc), base, num_bins - 1,
+                       _ptr(np.ascontiguousarray(x_fm, np.float32)), rows, cols, _ptr(out))
+    return out
+
+
+def shap_bias(forest: Forest, base: float) -> float:
+    fc = forest.c()
+    return float(lib().orc_shap_bias(ctypes.byref(fc), base))
+
+
+def fit_raw(x_fm, y, num_bins=256, is_cat=None, **kw) -> OracleModel:
+    """Edges + binning + fit, the whole reference fit path on raw features."""
+    edges = compute_edges(x_fm, num_bins, is_cat)
+    bins = bin_matrix(x_fm, edges, num_bins, is_cat)
+    return fit(bins, y, edges=edges, num_bins=num_bins, is_cat=is_cat, **kw)
+
+
+
+
+class SplitMix:
+    """SplitMix64 stream (DataGen.swift:6-26) driven through the oracle."""
+
+    def __init__(self, seed: int):
+        self.state = ctypes.c_uint64(seed & 0xFFFFFFFFFFFFFFFF)
+        l = lib()
+        l.orc_splitmix_uniform.restype = ctypes.c_float
+        l.orc_splitmix_uniform.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        l.orc_splitmix_normal.restype = ctypes.c_float
+        l.orc_splitmix_normal.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+
+    def next(self) -> int:
+        return int(lib().orc_splitmix_next(ctypes.byref(self.state)))
+
+    def uniform(self) -> float:
+        return lib().orc_splitmix_uniform(ctypes.byref(self.state))
+
+    def normal(self) -> float:
+        return lib().orc_splitmix_normal(ctypes.byref(self.state))
+
+    def uniforms(self, n: int) -> np.ndarray:
+        return np.array([self.uniform() for _ in range(n)], dtype=np.float32)

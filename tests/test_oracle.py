@@ -1,0 +1,498 @@
+"""Pins the CPU oracle against the reference's own known-answer and invariant
+tests (re-expressed here; the reference ships no fixture files) and against
+what the mathematics fixes: published RNG vectors, brute-force histograms and
+split searches, Fisher's grouping theorem, brute-force Shapley values.
+
+Reference tests cited per case are in Tests/MacBoostTests/*.swift.
+"""
+import itertools
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+
+def rmse(a, b):
+    d = np.asarray(a, np.float64) - np.asarray(b, np.float64)
+    return float(np.sqrt(np.mean(d * d)))
+
+
+def fit_raw(x, y, **kw):
+    nb = kw.pop("num_bins", 256)
+    is_cat = kw.pop("is_cat", None)
+    m = O.fit_raw(x, y, num_bins=nb, is_cat=is_cat, **kw)
+    return m
+
+
+def predict(m, x):
+    return O.predict(m.forest, m.base_score, m.num_bins, x)
+
+
+# --------------------------------------------------------------------------
+# generators and binning
+# --------------------------------------------------------------------------
+
+def test_splitmix_published_vector(oracle):
+    # Vigna's splitmix64, seed 0: the published first outputs.
+    assert [int(v) for v in O.splitmix_stream(0, 3)] == [
+        0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+def test_friedman_matches_closed_form(oracle):
+    # DataGen.swift:68-94: x ~ U[0,1), y = f(x) + N(0,1).
+    x, y = O.friedman(100_000, 7, seed=42)
+    assert x.min() >= 0.0 and x.max() < 1.0
+    f = (10 * np.sin(np.pi * x[0] * x[1]) + 20 * (x[2] - 0.5) ** 2 + 10 * x[3] + 5 * x[4])
+    r = y.astype(np.float64) - f
+    assert abs(r.mean()) < 0.02 and abs(r.std() - 1.0) < 0.02
+    # independent per-feature streams
+    c = np.corrcoef(x[5], x[6])[0, 1]
+    assert abs(c) < 0.02
+    # noise=0 reproduces f exactly up to float rounding
+    x0, y0 = O.friedman(1000, 5, seed=3, noise=0.0)
+    f0 = 10 * np.sin(np.pi * x0[0] * x0[1]) + 20 * (x0[2] - 0.5) ** 2 + 10 * x0[3] + 5 * x0[4]
+    assert np.max(np.abs(y0 - f0)) < 1e-4
+
+
+def test_edges_quantiles_and_bin_invariant(oracle):
+    # Binner.swift:48-51 edges are sample quantiles; bin(v) <= b <=> v <= edge[b]
+    # (the reason binned and raw routing agree, MacBoostTests.swift:291-305).
+    x, _ = O.friedman(60_000, 5, seed=11)
+    nb = 256
+    e = O.compute_edges(x, nb)
+    k = np.arange(nb - 2)
+    assert np.max(np.abs(e[0] - (k + 1) / (nb - 1))) < 0.01
+    assert np.all(np.diff(e, axis=1) >= 0)
+    bins = O.bin_matrix(x, e, nb)
+    rng = np.random.default_rng(0)
+    for f in range(5):
+        for b in rng.integers(0, nb - 2, size=20):
+            assert np.array_equal(bins[f] <= b, x[f] <= e[f, b])
+    xx = np.array([[np.nan, 0.0, 2.5, 3.5, 300.0, -4.0]], np.float32)
+    cat = O.bin_matrix(xx, np.zeros((1, nb - 2), np.float32), nb, is_cat=[1])
+    assert cat.tolist() == [[255, 0, 2, 4, 254, 0]]
+    num = O.bin_matrix(xx[:, :1], e[:1], nb)
+    assert num[0, 0] == nb - 1                              # NaN -> missing bin
+
+
+def test_quantize_range(oracle):
+    rng = np.random.default_rng(1)
+    preds = rng.normal(size=5000).astype(np.float32)
+    y = rng.normal(size=5000).astype(np.float32)
+    g, h, mg, mh = O.gradients(preds, y)
+    assert mg == np.max(np.abs(g)) and mh == 1.0
+    q = O.quantize(g, h, mg, mh)
+    qg = (q >> 16).astype(np.uint16).astype(np.int16).astype(np.int64)
+    qh = (q & 0x7F).astype(np.int64)
+    assert qg.min() >= -32767 and qg.max() <= 32767
+    assert np.max(np.abs(qg)) == 32767 and np.all(qh == 127)
+    assert np.max(np.abs(qg / 32767 * mg - g)) <= mg / 32767
+
+
+def test_logistic_gradient_closed_form(oracle):
+    f = np.linspace(-8, 8, 101).astype(np.float32)
+    y = (np.arange(101) % 2).astype(np.float32)
+    g, h, mg, mh = O.gradients(f, y, objective=O.OBJ_LOGISTIC, aux=2.0)
+    q = 1 / (1 + np.exp(-f.astype(np.float64)))
+    w = np.where(y > 0.5, 2.0, 1.0)
+    assert np.allclose(g, (q - y) * w, rtol=1e-6, atol=3e-7)
+    assert np.allclose(h, np.maximum(q * (1 - q), 1e-6) * w, rtol=1e-6, atol=3e-7)
+
+
+# --------------------------------------------------------------------------
+# histograms and split search against brute force
+# --------------------------------------------------------------------------
+
+def test_hist_matches_bruteforce(oracle):
+    rng = np.random.default_rng(2)
+    rows, cols, nb = 3000, 7, 64
+    bins = rng.integers(0, nb, size=(cols, rows)).astype(np.uint8)
+    qg = rng.integers(-32767, 32768, size=rows)
+    qh = rng.integers(0, 128, size=rows)
+    ghq = ((qg & 0xFFFF).astype(np.uint32) << 16) | qh.astype(np.uint32)
+    idx = np.sort(rng.choice(rows, 1234, replace=False)).astype(np.uint32)
+    hg, hh = O.hist_node(bins, nb, ghq, idx)
+    for f in range(cols):
+        eg = np.zeros(nb, np.int64)
+        eh = np.zeros(nb, np.int64)
+        np.add.at(eg, bins[f, idx], qg[idx])
+        np.add.at(eh, bins[f, idx], qh[idx])
+        assert np.array_equal(hg[f], eg) and np.array_equal(hh[f], eh)
+
+
+def _gain(gl, hl, gr, hr, lam, parent):
+    return gl * gl / (hl + lam) + gr * gr / (hr + lam) - parent
+
+
+def test_find_split_numeric_bruteforce(oracle):
+    rng = np.random.default_rng(3)
+    nb = 32
+    for trial in range(40):
+        hg = rng.integers(-20000, 20000, size=nb).astype(np.int64)
+        hh = rng.integers(0, 3000, size=nb).astype(np.int64)
+        if trial % 3 == 0:
+            hh[nb - 1] = 0; hg[nb - 1] = 0                   # no missing values
+        gi, hi = 7e-4, 1 / 127
+        G, H = hg.sum(), hh.sum()
+        lam, mch = 1.0, 1.0
+        r = O.find_split(hg, hh, False, 0, G, H, gi, hi, lam, mch)
+        parent = (G * gi) ** 2 / (H * hi + lam)
+        best, arg = -math.inf, None
+        for b in range(nb - 2):
+            GL, HL = hg[: b + 1].sum(), hh[: b + 1].sum()
+            for miss_left in (False, True):
+                if miss_left and hh[nb - 1] == 0:
+                    continue
+                L_g = GL + (hg[nb - 1] if miss_left else 0)
+                L_h = HL + (hh[nb - 1] if miss_left else 0)
+                gl, hl, gr, hr = L_g * gi, L_h * hi, (G - L_g) * gi, (H - L_h) * hi
+                if hl < mch or hr < mch:
+                    continue
+                v = _gain(gl, hl, gr, hr, lam, parent)
+                if v > best * (1 + 1e-9) + 1e-12:
+                    best, arg = v, (b, miss_left)
+        assert r.gain == pytest.approx(best, rel=1e-5, abs=1e-6)
+        assert (r.bin, bool(r.flags & O.FLAG_DEFAULT_LEFT)) == arg
+
+
+def test_find_split_min_child_hess_and_monotone(oracle):
+    hg = np.array([-500, -400, 300, 600, 0], np.int64)
+    hh = np.array([10, 10, 10, 10, 0], np.int64)
+    r = O.find_split(hg, hh, False, 0, hg.sum(), hh.sum(), 1.0, 1.0, 1.0, 41.0)
+    assert r.gain == -math.inf                               # every child < mch
+    # negative gradients on the left give left leaves above right leaves, so
+    # only a decreasing (-1) constraint admits a split here
+    dn = O.find_split(hg, hh, False, -1, hg.sum(), hh.sum(), 1.0, 1.0, 1.0, 1.0)
+    assert dn.gain > 0 and -dn.gl / (dn.hl + 1) >= -(hg.sum() - dn.gl) / (40 - dn.hl + 1)
+    up = O.find_split(hg, hh, False, +1, hg.sum(), hh.sum(), 1.0, 1.0, 1.0, 1.0)
+    assert up.gain == -math.inf
+
+
+def test_cat_order_is_stable_sort(oracle):
+    rng = np.random.default_rng(4)
+    nb = 64
+    hg = rng.integers(-50, 50, size=nb).astype(np.int64)
+    hh = rng.integers(0, 4, size=nb).astype(np.int64)
+    hg[::5] = hg[0]; hh[::5] = hh[0]                         # forced key ties
+    gi, hi, sm = np.float32(0.5), np.float32(0.25), np.float32(10.0)
+    order = O.cat_order(hg, hh, gi, hi, sm)
+    hb = (hh.astype(np.float32) * hi).astype(np.float32)
+    nz = np.nonzero(hb > 0)[0]
+    key = ((hg[nz].astype(np.float32) * gi).astype(np.float32) / (hb[nz] + sm)).astype(np.float32)
+    want = nz[np.argsort(key, kind="stable")]
+    assert order.tolist() == want.tolist()
+
+
+def test_categorical_prefix_is_best_subset(oracle):
+    # Fisher (1958): for the separable gain G_S^2/H_S + G_S'^2/H_S', the best
+    # two-way grouping is a contiguous run of the g/h ordering, so the scan
+    # over sorted prefixes finds the best of all 2^k subsets (catSmooth -> 0).
+    rng = np.random.default_rng(5)
+    nb = 9                                                    # 8 categories + missing
+    for _ in range(25):
+        hg = rng.integers(-5000, 5000, size=nb).astype(np.int64)
+        hh = rng.integers(1, 400, size=nb).astype(np.int64)
+        G, H = hg.sum(), hh.sum()
+        r = O.find_split(hg, hh, True, 0, G, H, 1e-3, 1e-2, 0.0, 0.0, 1e-6)
+        best = -math.inf
+        for k in range(1, nb):
+            for S in itertools.combinations(range(nb), k):
+                S = list(S)
+                gl, hl = hg[S].sum() * 1e-3, hh[S].sum() * 1e-2
+                gr, hr = (G - hg[S].sum()) * 1e-3, (H - hh[S].sum()) * 1e-2
+                best = max(best, _gain(gl, hl, gr, hr, 0.0, (G * 1e-3) ** 2 / (H * 1e-2)))
+        assert r.gain == pytest.approx(best, rel=1e-4, abs=1e-4)
+        assert r.flags == O.FLAG_CATEGORICAL
+
+
+# --------------------------------------------------------------------------
+# whole-model known answers (MacBoostTests.swift, FeatureTests.swift)
+# --------------------------------------------------------------------------
+
+def test_exact_split_and_leaf_values(oracle):
+    # MacBoostTests.swift:54-70
+    x = np.array([[0, 0, 1, 1]], np.float32)
+    y = np.array([0, 0, 10, 10], np.float32)
+    m = fit_raw(x, y, num_trees=1, max_depth=1, learning_rate=0.1, lam=0.0,
+                min_child_hess=1.0)
+    assert m.base_score == pytest.approx(5.0, abs=1e-5)
+    assert m.forest.feature[0, 0] == 0
+    p = predict(m, np.array([[0, 1]], np.float32))
+    assert p[0] == pytest.approx(4.5, abs=1e-4) and p[1] == pytest.approx(5.5, abs=1e-4)
+
+
+def _int_data(rows, cols, levels, seed):
+    rng = O.SplitMix(seed)
+    return np.array([rng.next() % levels for _ in range(rows * cols)],
+                    np.float32).reshape(cols, rows)
+
+
+def test_root_split_matches_bruteforce(oracle):
+    # MacBoostTests.swift:75-113
+    rows, cols = 2000, 5
+    x = _int_data(rows, cols, 10, 7)
+    rng = O.SplitMix(8)
+    y = np.array([np.float32(x[0, i] * x[0, i]) - np.float32(3 * x[2, i])
+                  + np.float32(0.1) * np.float32(rng.normal()) for i in range(rows)], np.float32)
+    m = fit_raw(x, y, num_trees=1, max_depth=1, lam=1.0)
+    f0 = m.forest.feature[0, 0]
+    assert f0 >= 0
+    mean = y.astype(np.float64).mean()
+
+    def gain(f, v):
+        g = mean - y.astype(np.float64)
+        left = x[f] <= v
+        gl, hl = g[left].sum(), left.sum()
+        hr, gr = rows - hl, g.sum() - gl
+        if hl < 1 or hr < 1:
+            return -math.inf
+        return gl * gl / (hl + 1) + gr * gr / (hr + 1) - g.sum() ** 2 / (rows + 1)
+
+    best = max(gain(f, v) for f in range(cols) for v in range(9))
+    chosen = gain(f0, m.forest.threshold[0, 0])
+    assert chosen == pytest.approx(best, abs=max(1e-3 * best, 1e-3))
+
+
+def test_min_child_hess_blocks_all_splits(oracle):
+    # MacBoostTests.swift:185-193
+    x, y = O.friedman(5000, 6, 6)
+    m = fit_raw(x, y, num_trees=5, max_depth=6, min_child_hess=5001.0)
+    assert np.all(m.forest.feature[:, 0] == -1)
+
+
+def test_constant_labels(oracle):
+    # MacBoostTests.swift:199-211
+    rows, cols = 5000, 5
+    x = O.SplitMix(9).uniforms(rows * cols).reshape(cols, rows)
+    y = np.full(rows, 3.25, np.float32)
+    m = fit_raw(x, y, num_trees=10, max_depth=5)
+    assert np.all(np.abs(predict(m, x) - 3.25) < 1e-4)
+    assert np.all(m.forest.feature[:, 0] == -1)
+
+
+@pytest.mark.parametrize("missing_joins_zero", [True, False])
+def test_missing_value_learned_direction(oracle, missing_joins_zero):
+    # FeatureTests.swift:19-38
+    x = np.array([[0.0] * 100 + [1.0] * 100 + [np.nan] * 100], np.float32)
+    y = np.array([10.0] * 100 + [0.0] * 100 + [10.0 if missing_joins_zero else 0.0] * 100,
+                 np.float32)
+    m = fit_raw(x, y, num_trees=30, max_depth=1, learning_rate=0.3)
+    p = predict(m, np.array([[0.0, 1.0, np.nan]], np.float32))
+    assert p[0] == pytest.approx(10, abs=0.2) and p[1] == pytest.approx(0, abs=0.2)
+    assert p[2] == pytest.approx(10 if missing_joins_zero else 0, abs=0.2)
+
+
+def test_categorical_subset_split(oracle):
+    # FeatureTests.swift:82-107
+    rows = 4000
+    rng = O.SplitMix(25)
+    cat = np.array([rng.next() % 4 for _ in range(rows)], np.float32)
+    y = np.where((cat == 0) | (cat == 3), 10.0, 0.0).astype(np.float32)
+    x = cat[None, :]
+    kw = dict(num_trees=1, max_depth=1, learning_rate=1.0, lam=0.0, cat_smooth=0.01)
+    mc = fit_raw(x, y, is_cat=[1], **kw)
+    mn = fit_raw(x, y, **kw)
+    assert rmse(predict(mc, x), y) < 0.05
+    assert rmse(predict(mn, x), y) > 1.0
+    assert mc.forest.flags[0, 0] == O.FLAG_CATEGORICAL
+
+
+def test_categorical_with_missing(oracle):
+    # FeatureTests.swift:111-132
+    rows = 6000
+    rng = O.SplitMix(26)
+    xs, ys = [], []
+    for _ in range(rows):
+        r = rng.next() % 5
+        if r == 4:
+            xs.append(np.nan); ys.append(5.0)
+        else:
+            xs.append(float(r)); ys.append(10.0 if r in (1, 2) else 0.0)
+    x = np.array([xs], np.float32)
+    y = np.array(ys, np.float32)
+    m = fit_raw(x, y, num_trees=40, max_depth=2, learning_rate=0.3, is_cat=[1])
+    p = predict(m, np.array([[0.0, 1.0, np.nan]], np.float32))
+    assert p.tolist() == pytest.approx([0.0, 10.0, 5.0], abs=0.3)
+
+
+def test_cover_consistency(oracle):
+    # ObjectiveTests.swift:261-274
+    rows = 10_000
+    x, y = O.friedman(rows, 6, 96)
+    m = fit_raw(x, y, num_trees=5, max_depth=5)
+    fo = m.forest
+    for t in range(5):
+        assert fo.cover[t, 0] == rows
+        for n in range((fo.nodes_per_tree - 1) // 2):
+            if fo.feature[t, n] >= 0:
+                assert fo.cover[t, 2 * n + 1] + fo.cover[t, 2 * n + 2] == fo.cover[t, n]
+
+
+def test_regression_accuracy_floor(oracle):
+    # MacBoostTests.swift:119-127
+    x, y = O.friedman(50_000, 10, 1)
+    m = fit_raw(x, y, num_trees=100, max_depth=6)
+    xv, yv = O.friedman(10_000, 10, 2)
+    assert rmse(predict(m, xv), yv) < 1.15
+    # running training predictions equal a from-scratch raw-threshold predict
+    # (MacBoostTests.swift:291-305: binned and raw routing agree)
+    assert np.array_equal(m.preds, predict(m, x))
+
+
+def test_binary_logistic_floor(oracle):
+    # MacBoostTests.swift:129-148
+    rows, cols = 20_000, 4
+    rng = O.SplitMix(3)
+    x = rng.uniforms(rows * cols).reshape(cols, rows)
+    y = np.array([1.0 if (x[0, i] + x[1, i] + np.float32(0.3) * np.float32(rng.normal())) > 1
+                  else 0.0 for i in range(rows)], np.float32)
+    m = fit_raw(x, y, num_trees=50, max_depth=5, objective=O.OBJ_LOGISTIC)
+    s = predict(m, x).astype(np.float64)
+    p = 1 / (1 + np.exp(-s))
+    ll = -np.mean(y * np.log(np.maximum(p, 1e-12)) + (1 - y) * np.log(np.maximum(1 - p, 1e-12)))
+    assert ll < 0.42
+
+
+def test_monotone_structural_audit(oracle):
+    # ObjectiveTests.swift:283-333 (smaller tree count)
+    x, y = O.friedman(30_000, 6, 101)
+    mono = [0, 0, 0, 1, 0, 0]
+    m = fit_raw(x, y, num_trees=60, max_depth=6, monotone=mono)
+    fo = m.forest
+
+    def leaf_range(t, root):
+        mn, mx, stack = math.inf, -math.inf, [root]
+        while stack:
+            n = stack.pop()
+            if fo.feature[t, n] >= 0:
+                stack += [2 * n + 1, 2 * n + 2]
+            elif fo.cover[t, n] > 0:
+                mn, mx = min(mn, fo.leaf[t, n]), max(mx, fo.leaf[t, n])
+        return mn, mx
+
+    for t in range(fo.num_trees):
+        for n in np.nonzero(fo.feature[t] == 3)[0]:
+            _, lmax = leaf_range(t, 2 * n + 1)
+            rmin, _ = leaf_range(t, 2 * n + 2)
+            assert lmax <= rmin + 1e-6
+    rng = O.SplitMix(102)
+    probe = np.repeat(rng.uniforms(6)[:, None], 30, axis=1)
+    probe[3] = np.linspace(0, 1, 30, dtype=np.float32)
+    out = predict(m, probe)
+    assert np.all(np.diff(out) >= -1e-5)
+
+
+# --------------------------------------------------------------------------
+# leaf-wise growth (LeafWiseTests.swift)
+# --------------------------------------------------------------------------
+
+def test_leafwise_budget_and_stumps(oracle):
+    # LeafWiseTests.swift:68-103 (budget), :219-240 (numLeaves=2 -> stumps)
+    x, y = O.friedman(8000, 6, 521)
+    m = fit_raw(x, y, num_trees=20, max_depth=10, num_leaves=31)
+    for t in range(20):
+        assert np.sum(m.forest.feature[t] < 0) - np.sum(m.forest.cover[t] == 0) <= 31
+        n_split = np.sum(m.forest.feature[t] >= 0)
+        assert n_split <= 30
+    s = fit_raw(x, y, num_trees=10, num_leaves=2)
+    assert np.all(s.forest.feature[:, 3:] < 0)
+    assert np.array_equal(s.preds, predict(s, x))
+
+
+def test_leafwise_full_budget_equals_levelwise(oracle):
+    # Each node's best split depends only on its own rows, so best-first growth
+    # with numLeaves = 2^maxDepth splits exactly the nodes level-wise splits.
+    x, y = O.friedman(6000, 8, 77)
+    lv = fit_raw(x, y, num_trees=15, max_depth=4)
+    lf = fit_raw(x, y, num_trees=15, max_depth=4, num_leaves=16)
+    for name in ("feature", "threshold", "leaf", "flags", "gain", "cover"):
+        assert np.array_equal(getattr(lv.forest, name), getattr(lf.forest, name)), name
+    assert np.array_equal(lv.preds, lf.preds)
+
+
+# --------------------------------------------------------------------------
+# TreeSHAP (SHAP.swift, ObjectiveTests.swift:402-513)
+# --------------------------------------------------------------------------
+
+def _mixed_data(rows, seed_a, seed_b, nan_frac=0.1):
+    x, y = O.friedman(rows, 6, seed_a)
+    rng = O.SplitMix(seed_b)
+    for i in range(rows):
+        if rng.uniform() < nan_frac:
+            x[1, i] = np.nan
+    cat = np.array([rng.next() % 5 for _ in range(rows)], np.float32)
+    x = np.vstack([x, cat[None, :]])
+    y = (y + np.where(cat == 2, 3.0, 0.0)).astype(np.float32)
+    return x, y
+
+
+def test_shap_sums_to_prediction(oracle):
+    # ObjectiveTests.swift:402-435
+    x, y = _mixed_data(1500, 111, 112)
+    m = fit_raw(x, y, num_trees=40, max_depth=6, is_cat=[0, 0, 0, 0, 0, 0, 1])
+    c = O.treeshap(m.forest, m.base_score, 256, x)
+    raw = predict(m, x)
+    gap = np.abs(c.astype(np.float64).sum(axis=1) - raw)
+    assert gap.max() < 1e-4                                   # reference bound: 2e-2
+    mass = np.abs(c[:, :7]).sum(axis=0)
+    assert mass[3] > 5 * mass[5] and mass[6] > 2 * mass[5]
+
+
+def _route_left(fo, t, n, v, data_bins):
+    fl = fo.flags[t, n]
+    if fl & O.FLAG_CATEGORICAL:
+        cat = data_bins
+        if np.isfinite(v):
+            r = np.rint(v)
+            if 0 <= r < data_bins:
+                cat = int(r)
+        return bool((fo.cat_mask[t, n, cat // 32] >> (cat % 32)) & 1)
+    if np.isnan(v):
+        return bool(fl & O.FLAG_DEFAULT_LEFT)
+    return bool(v <= fo.threshold[t, n])
+
+
+def _cond_expectation(fo, t, xrow, S, data_bins, n=0):
+    if fo.feature[t, n] < 0:
+        return float(fo.leaf[t, n])
+    f = fo.feature[t, n]
+    if f in S:
+        nxt = 2 * n + 1 if _route_left(fo, t, n, xrow[f], data_bins) else 2 * n + 2
+        return _cond_expectation(fo, t, xrow, S, data_bins, nxt)
+    c = float(fo.cover[t, n])
+    out = 0.0
+    for ch in (2 * n + 1, 2 * n + 2):
+        w = float(fo.cover[t, ch]) / c if c > 0 else 0.0
+        if w:
+            out += w * _cond_expectation(fo, t, xrow, S, data_bins, ch)
+    return out
+
+
+def test_shap_matches_bruteforce_shapley(oracle):
+    # Exact Shapley values of v(S) = E[f(x) | x_S] with cover as the
+    # background distribution, by enumeration over all feature subsets.
+    x, y = _mixed_data(600, 5, 6, nan_frac=0.2)
+    x = x[[0, 1, 3, 6]]
+    m = fit_raw(x, y, num_trees=3, max_depth=3, is_cat=[0, 0, 0, 1])
+    fo = m.forest
+    c = O.treeshap(fo, m.base_score, 256, x[:, :25])
+    M = x.shape[0]
+    for i in range(25):
+        xrow = x[:, i]
+        phi = np.zeros(M)
+        for t in range(fo.num_trees):
+            v = {}
+            for k in range(M + 1):
+                for S in itertools.combinations(range(M), k):
+                    v[S] = _cond_expectation(fo, t, xrow, set(S), 255)
+            for j in range(M):
+                others = [q for q in range(M) if q != j]
+                for k in range(M):
+                    for S in itertools.combinations(others, k):
+                        wgt = math.factorial(k) * math.factorial(M - k - 1) / math.factorial(M)
+                        Sj = tuple(sorted(S + (j,)))
+                        phi[j] += wgt * (v[Sj] - v[S])
+        assert np.allclose(c[i, :M], phi, rtol=1e-5, atol=1e-6)
+    assert c[0, M] == pytest.approx(O.shap_bias(fo, m.base_score), rel=1e-6)
