@@ -1,0 +1,140 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X tree-build path.
+
+Workload (the headline metric): Friedman #1 regression, 10M rows x 100 fp32
+features, 256 bins, level-wise depth 6, lr 0.1, L2.  A step is one boosting
+iteration (one depth-6 tree) over the binned matrix resident in HBM.  W
+untimed warm-up trees, then K timed trees; value = K / seconds (trees/s).
+
+Also reported: the histogram kernel's roofline (algorithmic bytes = sum over
+built nodes of rows*(features+4), timed with HIP events on the kernel's own
+stream), the end-to-end fit time including edges/upload/binning, and the CPU
+oracle timed on this host (single thread) on a bounded sample of the same
+workload.  Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+REFERENCE_TREES_PER_S = 25.6      # 100 trees in 3.9 s on an M4 Max (README.md:73)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(x, y, rows, cols, trees):
+    """The oracle (single-threaded C) on the first `rows` rows, `trees` trees."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    xs = np.ascontiguousarray(x[:, :rows])
+    ys = np.ascontiguousarray(y[:rows])
+    t0 = time.perf_counter()
+    edges = O.compute_edges(xs, 256)
+    bins = O.bin_matrix(xs, edges, 256)
+    t_bin = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.fit(bins, ys, edges=edges, num_trees=trees, max_depth=6, num_bins=256)
+    t_fit = time.perf_counter() - t0
+    return t_bin, t_fit
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--rows", type=int, default=10_000_000)
+    ap.add_argument("--cols", type=int, default=100)
+    ap.add_argument("--cpu-rows", type=int, default=2_000_000)
+    ap.add_argument("--cpu-trees", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+
+    import macboost_amd as mb
+
+    rows, cols = args.rows, args.cols
+    log(f"generating Friedman #1 {rows} x {cols}")
+    t0 = time.perf_counter()
+    x, y = mb.friedman(rows, cols, 42)
+    log(f"data in {time.perf_counter() - t0:.2f}s")
+    params = {"num_trees": args.steps + args.warmup, "max_depth": 6, "num_bins": 256,
+              "learning_rate": 0.1}
+    t0 = time.perf_counter()
+    tr = mb.Trainer(params, x, y, feature_major=True)
+    t_setup = time.perf_counter() - t0
+    t_edges, t_bin = tr.setup_seconds()
+    log(f"setup {t_setup:.2f}s (edges {t_edges:.2f}s, upload+bin {t_bin:.2f}s)")
+    tr.grow(args.warmup)
+    log(f"warm-up {args.warmup} trees done")
+    tr.profile(True)
+    t0 = time.perf_counter()
+    tr.grow(args.steps)
+    elapsed = time.perf_counter() - t0
+    launches, hist_ms, hist_bytes = tr.hist_stats()
+    value = args.steps / elapsed
+    log(f"{args.steps} trees in {elapsed:.3f}s = {value:.1f} trees/s; hist {launches} launches "
+        f"{hist_ms:.1f} ms")
+    h = tr.booster()
+    # quality check: held-out RMSE (README.md:73 reports 1.033 for the reference)
+    xv, yv = mb.friedman(200_000, cols, 42 + 999)
+    pv = mb.predict(h, xv, feature_major=True)
+    rmse = float(np.sqrt(np.mean((pv.astype(np.float64) - yv) ** 2)))
+    log(f"valid RMSE {rmse:.4f} after {args.steps + args.warmup} trees")
+    tr.close()
+
+    achieved = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms > 0 else None
+    per_launch_bytes = hist_bytes / launches if launches else None
+    roofline = {
+        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": None,
+        "kernel": "k_hist", "launches": launches, "avg_launch_ms": hist_ms / launches if launches else None,
+        "algorithmic_bytes_per_launch": per_launch_bytes,
+    }
+    cpu = None
+    if not args.no_cpu:
+        cr = min(args.cpu_rows, rows)
+        log(f"cpu baseline: oracle on {cr} rows, {args.cpu_trees} tree(s)")
+        t_cbin, t_cfit = cpu_baseline(x, y, cr, cols, args.cpu_trees)
+        per_tree_full = t_cfit / args.cpu_trees * (rows / cr)
+        cpu = {"value": 1.0 / per_tree_full, "unit": "trees/s", "cores": 1, "kind": "port",
+               "sample": f"{args.cpu_trees} depth-6 tree(s) on the first {cr} of {rows} rows "
+                         f"x {cols} features (binned once, {t_cbin:.1f}s, untimed), "
+                         f"{t_cfit:.2f}s, scaled linearly to {rows} rows"}
+        log(f"cpu {t_cfit:.2f}s for {args.cpu_trees} tree(s) on {cr} rows")
+    fit_total = t_setup + elapsed / args.steps * 100
+    out = {
+        "metric": "trees/s fitting 10M×100 depth-6; histogram HBM GB/s as % of peak",
+        "value": value, "unit": "trees/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": value / REFERENCE_TREES_PER_S,
+        "dtype": "u8 bins, int64 histograms, f32 gains", "data": "synthetic",
+        "config": {"workload": "friedman1-regression-levelwise", "rows": rows, "features": cols,
+                   "bins": 256, "max_depth": 6, "learning_rate": 0.1, "objective": "l2",
+                   "parallelism": "single-gpu"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "rows_per_s": rows * value,
+        "fit_seconds_100_trees_incl_binning": fit_total,
+        "setup_seconds": {"edges_host": t_edges, "upload_and_bin": t_bin, "total": t_setup},
+        "valid_rmse": rmse,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

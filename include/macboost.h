@@ -1,0 +1,167 @@
+/*
+ * macboost.h — C ABI of the MI355X tree-build library (libmacboostc.so).
+ *
+ * Part 1 replaces the reference's public C ABI one symbol for one symbol
+ * (Sources/MacBoostC/CAPI.swift, MacBoost v1.0.0): same names, argument order,
+ * widths, return codes and ownership.  Errors never cross the ABI as
+ * exceptions: a failing call stores a malloc'd message in *err (free it with
+ * macboost_free_string) and returns NULL / -1 (1 for macboost_select_features).
+ * All arrays are borrowed for the duration of the call.  A handle is not safe
+ * for concurrent use.
+ *
+ * Part 2 is the kernel seam (MetalEngine.dispatch, MetalEngine.swift:87-118):
+ * device-pointer entry points a host written in another language can drive.
+ *
+ * Part 3 holds extensions with no counterpart in the reference: an
+ * incremental trainer used by the benchmark to time boosting iterations with
+ * the binned matrix already resident in HBM.
+ */
+#ifndef MACBOOST_H
+#define MACBOOST_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================= Part 1: reference C ABI ======================== */
+
+/* CAPI.swift:86-136.  params_json keys as CAPI.swift:9-37; x is row-major
+ * [rows][cols] when row_major != 0 else feature-major [cols][rows]; w,
+ * x_valid (feature-major) and y_valid may be NULL.  Returns a handle or NULL. */
+void *macboost_train(const char *params_json, const float *x, int64_t rows, int64_t cols,
+                     int32_t row_major, const float *y, const float *w, const float *x_valid,
+                     int64_t valid_rows, const float *y_valid, char **err);
+
+/* CAPI.swift:138-183 (Boruta feature selection).  Returns 0 / 1. */
+int32_t macboost_select_features(const char *params_json, const float *x, int64_t rows,
+                                 int64_t cols, const float *y, const float *w, int32_t rounds,
+                                 int32_t trees, float alpha, int64_t seed, int32_t *out_hits,
+                                 int32_t *out_decision, float *out_gain_ratio, char **err);
+
+/* CAPI.swift:185-202.  x feature-major; out holds rows*num_classes floats. */
+int32_t macboost_predict(void *handle, const float *x, int64_t rows, int64_t cols, float *out,
+                         char **err);
+
+/* CAPI.swift:204-208.  -1 for a NULL handle. */
+int64_t macboost_num_classes(void *handle);
+
+/* CAPI.swift:210-220.  type 0 = gain, 1 = split; out holds num_features. */
+int32_t macboost_feature_importance(void *handle, int32_t type, float *out);
+
+/* CAPI.swift:222-240.  out holds rows*num_classes*(cols+1) floats. */
+int32_t macboost_predict_contrib(void *handle, const float *x, int64_t rows, int64_t cols,
+                                 float *out, char **err);
+
+/* CAPI.swift:242-255 / :257-270: the reference's model JSON. */
+int32_t macboost_save(void *handle, const char *path, char **err);
+void *macboost_load(const char *path, char **err);
+
+/* CAPI.swift:272-288.  -1 for a NULL handle. */
+int64_t macboost_num_trees(void *handle);
+int64_t macboost_num_features(void *handle);
+int64_t macboost_best_iteration(void *handle);
+
+/* CAPI.swift:290-297: newline-joined fit warnings or NULL; caller frees. */
+char *macboost_warnings(void *handle);
+
+/* CAPI.swift:299-308. */
+void macboost_free(void *handle);
+void macboost_free_string(char *s);
+
+/* ======================= Part 2: kernel seam ============================ */
+
+typedef struct mbk_context mbk_context;
+
+/* One device + one stream.  Replaces MetalEngine.init (MetalEngine.swift:43-65). */
+int mbk_context_create(int32_t device, mbk_context **out, char **err);
+void mbk_context_destroy(mbk_context *ctx);
+int mbk_device_alloc(mbk_context *ctx, size_t bytes, void **out, char **err);
+void mbk_device_free(mbk_context *ctx, void *ptr);
+int mbk_copy_to_device(mbk_context *ctx, void *dst, const void *src, size_t bytes, char **err);
+int mbk_copy_to_host(mbk_context *ctx, void *dst, const void *src, size_t bytes, char **err);
+int mbk_synchronize(mbk_context *ctx, char **err);
+
+/* bin_data (Shaders.swift:46-76): raw f32 -> bins in two layouts, the
+ * gather layout bins_tiled [ceil(cols/tile_width)][rows][tile_width] and the
+ * feature-major bins_fm [cols][rows].  edges: cols*(num_bins-2) f32. */
+int mbk_bin_data(mbk_context *ctx, const float *x, int64_t rows, int32_t cols,
+                 int64_t row_stride, int64_t col_stride, const float *edges,
+                 const uint8_t *is_cat, int32_t num_bins, int32_t tile_width,
+                 uint8_t *bins_tiled, uint8_t *bins_fm, char **err);
+
+/* compute_gradients + quantize_gradients (Shaders.swift:96-192).
+ * Writes max_gh[2] (f32 bit patterns of max|g|, max h) and entries[rows][2]
+ * = (row, (qg << 16) | qh). */
+int mbk_quantize(mbk_context *ctx, int32_t objective, float alpha, float aux,
+                 const float *preds, const float *labels, const float *weights, int64_t rows,
+                 uint32_t *max_gh, uint32_t *entries, char **err);
+
+/* One split candidate (SplitResult, Shaders.swift:334, plus exact left sums
+ * and the categorical left-subset mask). */
+typedef struct {
+    float gain;
+    uint32_t bin;
+    float gl, hl;
+    uint32_t flags;
+    uint32_t pad;
+    int64_t gl_int, hl_int;
+    uint32_t mask[8];
+} mbk_split_result;
+
+/* build_histograms + find_splits for one node (Shaders.swift:212-464): the
+ * node's rows are entries[0..n).  hist_out: [cols][num_bins][2] int64
+ * (gradient sum, hessian sum) of quantised words; results: [cols]. */
+int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t rows,
+                        int32_t cols, int32_t num_bins, int32_t tile_width,
+                        const uint32_t *entries, int64_t n, const uint32_t *max_gh,
+                        const uint8_t *is_cat, const int8_t *monotone, float lambda,
+                        float min_child_hess, float cat_smooth, int64_t *hist_out,
+                        mbk_split_result *results, char **err);
+
+/* predict_forest (Shaders.swift:1541-1584) on device buffers: flat forest of
+ * num_trees*nodes_per_tree heap slots; mask may be NULL when no node is
+ * categorical.  x feature-major [cols][rows]; out[rows]. */
+int mbk_predict_forest(mbk_context *ctx, const int32_t *feature, const float *threshold,
+                       const uint8_t *flags, const float *leaf, const uint32_t *mask,
+                       int32_t num_trees, int32_t nodes_per_tree, const float *x, int64_t rows,
+                       int32_t data_bins, float base_score, float *out, char **err);
+
+/* ======================= Part 3: extensions ============================= */
+
+/* No counterpart in the reference.  An incremental trainer: validates and
+ * bins like macboost_train, then grows trees on demand with the binned
+ * matrix resident in HBM.  Used to time boosting iterations. */
+void *mbx_trainer_create(const char *params_json, const float *x, int64_t rows, int64_t cols,
+                         int32_t row_major, const float *y, const float *w,
+                         const float *x_valid, int64_t valid_rows, const float *y_valid,
+                         char **err);
+/* Enqueue num_trees boosting iterations and wait for them. */
+int mbx_trainer_grow(void *trainer, int32_t num_trees, char **err);
+/* 1 = record HIP events around every histogram launch from now on. */
+int mbx_trainer_profile(void *trainer, int32_t enable, char **err);
+/* Histogram-kernel totals since profiling was enabled: launches, total
+ * milliseconds, and algorithmic bytes (sum over built nodes of rows*(cols+4)). */
+int mbx_trainer_hist_stats(void *trainer, int64_t *launches, double *ms, double *bytes,
+                           char **err);
+/* Wall-clock seconds of the last mbx_trainer_create phases: edges (host),
+ * upload + device binning. */
+int mbx_trainer_setup_seconds(void *trainer, double *edges_s, double *bin_s);
+/* Finish training: read the trees back and return a booster handle usable
+ * by every Part 1 call (free it with macboost_free).  The trainer stays
+ * valid and must still be freed. */
+void *mbx_trainer_booster(void *trainer, char **err);
+void mbx_trainer_free(void *trainer);
+
+/* SplitMix64 Friedman #1 generator (DataGen.swift:68-94), multithreaded:
+ * x feature-major [cols][rows], y[rows]. */
+void mbx_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise, float *x, float *y);
+
+/* Library version string (static). */
+const char *mbx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

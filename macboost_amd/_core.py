@@ -1,0 +1,415 @@
+"""ctypes binding to libmacboostc.so, the MI355X build of MacBoost's C ABI.
+
+Mirrors the reference binding (python/macboost/_core.py): the same symbols,
+argtypes (_core.py:59-96), the row-major fast path of ``train``
+(_core.py:135-177), feature-major ``predict``/``predict_contrib``
+(_core.py:210-231) and error-string ownership (_core.py:103-107).  The
+library is loaded from this package directory; when it is missing every call
+raises — there is no pure-Python fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libmacboostc.so"
+
+_c_char_pp = ctypes.POINTER(ctypes.c_char_p)
+_f32_p = ctypes.POINTER(ctypes.c_float)
+_P = ctypes.c_void_p
+
+_lib_instance = None
+
+
+class MacBoostError(RuntimeError):
+    pass
+
+
+def _find_library() -> str:
+    env = os.environ.get("MACBOOST_LIB")
+    for c in ([Path(env)] if env else []) + [LIB_PATH]:
+        if c.is_file():
+            return str(c)
+    raise OSError(f"{LIB_PATH} not found; build it with `make -C macboost_amd/csrc` "
+                  "(or __graft_entry__.build())")
+
+
+def lib() -> ctypes.CDLL:
+    global _lib_instance
+    if _lib_instance is None:
+        _lib_instance = ctypes.CDLL(_find_library())
+        _configure(_lib_instance)
+    return _lib_instance
+
+
+def _configure(l):
+    l.macboost_train.restype = ctypes.c_void_p
+    l.macboost_train.argtypes = [
+        ctypes.c_char_p, _f32_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+        _f32_p, _f32_p, _f32_p, ctypes.c_int64, _f32_p, _c_char_pp,
+    ]
+    l.macboost_select_features.restype = ctypes.c_int32
+    l.macboost_select_features.argtypes = [
+        ctypes.c_char_p, _f32_p, ctypes.c_int64, ctypes.c_int64, _f32_p, _f32_p,
+        ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_int64,
+        ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32), _f32_p, _c_char_pp,
+    ]
+    l.macboost_predict_contrib.restype = ctypes.c_int32
+    l.macboost_predict_contrib.argtypes = [
+        ctypes.c_void_p, _f32_p, ctypes.c_int64, ctypes.c_int64, _f32_p, _c_char_pp,
+    ]
+    l.macboost_feature_importance.restype = ctypes.c_int32
+    l.macboost_feature_importance.argtypes = [ctypes.c_void_p, ctypes.c_int32, _f32_p]
+    l.macboost_predict.restype = ctypes.c_int32
+    l.macboost_predict.argtypes = [
+        ctypes.c_void_p, _f32_p, ctypes.c_int64, ctypes.c_int64, _f32_p, _c_char_pp,
+    ]
+    l.macboost_save.restype = ctypes.c_int32
+    l.macboost_save.argtypes = [ctypes.c_void_p, ctypes.c_char_p, _c_char_pp]
+    l.macboost_load.restype = ctypes.c_void_p
+    l.macboost_load.argtypes = [ctypes.c_char_p, _c_char_pp]
+    for name in ("macboost_num_trees", "macboost_num_features", "macboost_best_iteration",
+                 "macboost_num_classes"):
+        fn = getattr(l, name)
+        fn.restype = ctypes.c_int64
+        fn.argtypes = [ctypes.c_void_p]
+    l.macboost_warnings.restype = ctypes.c_void_p
+    l.macboost_warnings.argtypes = [ctypes.c_void_p]
+    l.macboost_free.restype = None
+    l.macboost_free.argtypes = [ctypes.c_void_p]
+    l.macboost_free_string.restype = None
+    l.macboost_free_string.argtypes = [ctypes.c_void_p]
+    # kernel seam
+    l.mbk_context_create.restype = ctypes.c_int
+    l.mbk_context_create.argtypes = [ctypes.c_int32, ctypes.POINTER(_P), _c_char_pp]
+    l.mbk_context_destroy.restype = None
+    l.mbk_context_destroy.argtypes = [_P]
+    l.mbk_device_alloc.restype = ctypes.c_int
+    l.mbk_device_alloc.argtypes = [_P, ctypes.c_size_t, ctypes.POINTER(_P), _c_char_pp]
+    l.mbk_device_free.restype = None
+    l.mbk_device_free.argtypes = [_P, _P]
+    for n in ("mbk_copy_to_device", "mbk_copy_to_host"):
+        getattr(l, n).restype = ctypes.c_int
+        getattr(l, n).argtypes = [_P, _P, _P, ctypes.c_size_t, _c_char_pp]
+    l.mbk_synchronize.restype = ctypes.c_int
+    l.mbk_synchronize.argtypes = [_P, _c_char_pp]
+    l.mbk_bin_data.restype = ctypes.c_int
+    l.mbk_bin_data.argtypes = [_P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                               ctypes.c_int64, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P,
+                               _c_char_pp]
+    l.mbk_quantize.restype = ctypes.c_int
+    l.mbk_quantize.argtypes = [_P, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _P, _P, _P,
+                               ctypes.c_int64, _P, _P, _c_char_pp]
+    l.mbk_node_hist_split.restype = ctypes.c_int
+    l.mbk_node_hist_split.argtypes = [_P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                      ctypes.c_int32, _P, ctypes.c_int64, _P, _P, _P,
+                                      ctypes.c_float, ctypes.c_float, ctypes.c_float, _P, _P,
+                                      _c_char_pp]
+    l.mbk_predict_forest.restype = ctypes.c_int
+    l.mbk_predict_forest.argtypes = [_P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P,
+                                     ctypes.c_int64, ctypes.c_int32, ctypes.c_float, _P,
+                                     _c_char_pp]
+    # extensions
+    l.mbx_trainer_create.restype = ctypes.c_void_p
+    l.mbx_trainer_create.argtypes = l.macboost_train.argtypes
+    l.mbx_trainer_grow.restype = ctypes.c_int
+    l.mbx_trainer_grow.argtypes = [_P, ctypes.c_int32, _c_char_pp]
+    l.mbx_trainer_profile.restype = ctypes.c_int
+    l.mbx_trainer_profile.argtypes = [_P, ctypes.c_int32, _c_char_pp]
+    l.mbx_trainer_hist_stats.restype = ctypes.c_int
+    l.mbx_trainer_hist_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int64),
+                                         ctypes.POINTER(ctypes.c_double),
+                                         ctypes.POINTER(ctypes.c_double), _c_char_pp]
+    l.mbx_trainer_setup_seconds.restype = ctypes.c_int
+    l.mbx_trainer_setup_seconds.argtypes = [_P, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_double)]
+    l.mbx_trainer_booster.restype = ctypes.c_void_p
+    l.mbx_trainer_booster.argtypes = [_P, _c_char_pp]
+    l.mbx_trainer_free.restype = None
+    l.mbx_trainer_free.argtypes = [_P]
+    l.mbx_friedman.restype = None
+    l.mbx_friedman.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float,
+                               _P, _P]
+    l.mbx_version.restype = ctypes.c_char_p
+    l.mbx_version.argtypes = []
+
+
+EXPORTED = (
+    "macboost_train", "macboost_select_features", "macboost_predict", "macboost_num_classes",
+    "macboost_feature_importance", "macboost_predict_contrib", "macboost_save", "macboost_load",
+    "macboost_num_trees", "macboost_num_features", "macboost_best_iteration",
+    "macboost_warnings", "macboost_free", "macboost_free_string",
+    "mbk_context_create", "mbk_context_destroy", "mbk_device_alloc", "mbk_device_free",
+    "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_bin_data", "mbk_quantize",
+    "mbk_node_hist_split", "mbk_predict_forest",
+    "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
+    "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
+    "mbx_version",
+)
+
+
+def _take_error(err: ctypes.c_char_p) -> str:
+    msg = err.value.decode() if err.value else "unknown error"
+    lib().macboost_free_string(ctypes.cast(err, ctypes.c_void_p))
+    return msg
+
+
+def _feature_major(X):
+    a = np.asarray(X, dtype=np.float32)
+    if a.ndim != 2:
+        raise ValueError(f"X must be 2-dimensional, got shape {a.shape}")
+    rows, cols = a.shape
+    return np.ascontiguousarray(a.T), rows, cols
+
+
+def _f32(a):
+    return None if a is None else a.ctypes.data_as(_f32_p)
+
+
+class _Handle:
+    """Owns a booster handle and frees it on GC."""
+
+    def __init__(self, ptr: int):
+        self.ptr = ptr
+
+    def __del__(self):
+        if getattr(self, "ptr", None) and _lib_instance is not None:
+            _lib_instance.macboost_free(self.ptr)
+            self.ptr = None
+
+
+def _prep_train(config, X, y, eval_set, sample_weight, layout_fm=False):
+    a = np.asarray(X, dtype=np.float32)
+    if layout_fm:
+        xf = np.ascontiguousarray(a, dtype=np.float32)
+        cols, rows = xf.shape
+        row_major = 0
+    else:
+        if a.ndim != 2:
+            raise ValueError(f"X must be 2-dimensional, got shape {a.shape}")
+        xf = np.ascontiguousarray(a)
+        rows, cols = xf.shape
+        row_major = 1
+    yv = np.ascontiguousarray(y, dtype=np.float32)
+    w = None if sample_weight is None else np.ascontiguousarray(sample_weight, dtype=np.float32)
+    xv = yvv = None
+    vrows = 0
+    if eval_set is not None:
+        xv, vrows, vcols = _feature_major(eval_set[0])
+        yvv = np.ascontiguousarray(eval_set[1], dtype=np.float32)
+    cfg = json.dumps(config).encode()
+    return cfg, xf, rows, cols, row_major, yv, w, xv, vrows, yvv
+
+
+def train(config: dict, X, y, eval_set=None, sample_weight=None, feature_major=False) -> _Handle:
+    """macboost_train; X is (rows, cols) row-major, or (cols, rows) with feature_major."""
+    cfg, xf, rows, cols, rm, yv, w, xv, vrows, yvv = _prep_train(
+        config, X, y, eval_set, sample_weight, feature_major)
+    err = ctypes.c_char_p()
+    ptr = lib().macboost_train(cfg, _f32(xf), rows, cols, rm, _f32(yv), _f32(w), _f32(xv),
+                               vrows, _f32(yvv), ctypes.byref(err))
+    if not ptr:
+        raise MacBoostError(_take_error(err))
+    return _Handle(ptr)
+
+
+def predict(handle: _Handle, X, feature_major=False) -> np.ndarray:
+    if feature_major:
+        xf = np.ascontiguousarray(X, dtype=np.float32)
+        cols, rows = xf.shape
+    else:
+        xf, rows, cols = _feature_major(X)
+    k = max(1, num_classes(handle))
+    out = np.empty(rows * k, dtype=np.float32)
+    err = ctypes.c_char_p()
+    if lib().macboost_predict(handle.ptr, _f32(xf), rows, cols, _f32(out), ctypes.byref(err)) != 0:
+        raise MacBoostError(_take_error(err))
+    return out if k == 1 else out.reshape(rows, k)
+
+
+def predict_contrib(handle: _Handle, X, feature_major=False) -> np.ndarray:
+    if feature_major:
+        xf = np.ascontiguousarray(X, dtype=np.float32)
+        cols, rows = xf.shape
+    else:
+        xf, rows, cols = _feature_major(X)
+    k = max(1, num_classes(handle))
+    out = np.empty(rows * k * (cols + 1), dtype=np.float32)
+    err = ctypes.c_char_p()
+    if lib().macboost_predict_contrib(handle.ptr, _f32(xf), rows, cols, _f32(out),
+                                      ctypes.byref(err)) != 0:
+        raise MacBoostError(_take_error(err))
+    return out.reshape(rows, k * (cols + 1))
+
+
+def feature_importance(handle: _Handle, importance_type: str = "gain") -> np.ndarray:
+    out = np.empty(num_features(handle), dtype=np.float32)
+    t = 1 if importance_type == "split" else 0
+    if lib().macboost_feature_importance(handle.ptr, t, _f32(out)) != 0:
+        raise MacBoostError("feature_importance failed")
+    return out
+
+
+def save(handle: _Handle, path) -> None:
+    err = ctypes.c_char_p()
+    if lib().macboost_save(handle.ptr, str(path).encode(), ctypes.byref(err)) != 0:
+        raise MacBoostError(_take_error(err))
+
+
+def load(path) -> _Handle:
+    err = ctypes.c_char_p()
+    ptr = lib().macboost_load(str(path).encode(), ctypes.byref(err))
+    if not ptr:
+        raise MacBoostError(_take_error(err))
+    return _Handle(ptr)
+
+
+def num_trees(handle):
+    return int(lib().macboost_num_trees(handle.ptr))
+
+
+def num_features(handle):
+    return int(lib().macboost_num_features(handle.ptr))
+
+
+def num_classes(handle):
+    return int(lib().macboost_num_classes(handle.ptr))
+
+
+def best_iteration(handle):
+    return int(lib().macboost_best_iteration(handle.ptr))
+
+
+def warnings(handle) -> list[str]:
+    p = lib().macboost_warnings(handle.ptr)
+    if not p:
+        return []
+    s = ctypes.cast(p, ctypes.c_char_p).value.decode()
+    lib().macboost_free_string(p)
+    return s.split("\n")
+
+
+def version() -> str:
+    return lib().mbx_version().decode()
+
+
+def friedman(rows: int, cols: int, seed: int, noise: float = 1.0):
+    """Friedman #1 data (DataGen.friedman): feature-major X [cols, rows] and y."""
+    x = np.empty((cols, rows), dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    lib().mbx_friedman(rows, cols, ctypes.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), noise,
+                       x.ctypes.data, y.ctypes.data)
+    return x, y
+
+
+class Trainer:
+    """Incremental trainer (mbx_trainer_*): bins once, grows trees on demand."""
+
+    def __init__(self, config: dict, X, y, eval_set=None, sample_weight=None,
+                 feature_major=False):
+        cfg, xf, rows, cols, rm, yv, w, xv, vrows, yvv = _prep_train(
+            config, X, y, eval_set, sample_weight, feature_major)
+        err = ctypes.c_char_p()
+        self.ptr = lib().mbx_trainer_create(cfg, _f32(xf), rows, cols, rm, _f32(yv), _f32(w),
+                                            _f32(xv), vrows, _f32(yvv), ctypes.byref(err))
+        if not self.ptr:
+            raise MacBoostError(_take_error(err))
+        self.rows, self.cols = rows, cols
+
+    def grow(self, n: int) -> None:
+        err = ctypes.c_char_p()
+        if lib().mbx_trainer_grow(self.ptr, n, ctypes.byref(err)) != 0:
+            raise MacBoostError(_take_error(err))
+
+    def profile(self, enable: bool = True) -> None:
+        err = ctypes.c_char_p()
+        lib().mbx_trainer_profile(self.ptr, 1 if enable else 0, ctypes.byref(err))
+
+    def hist_stats(self):
+        n = ctypes.c_int64()
+        ms = ctypes.c_double()
+        b = ctypes.c_double()
+        err = ctypes.c_char_p()
+        if lib().mbx_trainer_hist_stats(self.ptr, ctypes.byref(n), ctypes.byref(ms),
+                                        ctypes.byref(b), ctypes.byref(err)) != 0:
+            raise MacBoostError(_take_error(err))
+        return int(n.value), float(ms.value), float(b.value)
+
+    def setup_seconds(self):
+        e = ctypes.c_double()
+        b = ctypes.c_double()
+        lib().mbx_trainer_setup_seconds(self.ptr, ctypes.byref(e), ctypes.byref(b))
+        return float(e.value), float(b.value)
+
+    def booster(self) -> _Handle:
+        err = ctypes.c_char_p()
+        ptr = lib().mbx_trainer_booster(self.ptr, ctypes.byref(err))
+        if not ptr:
+            raise MacBoostError(_take_error(err))
+        return _Handle(ptr)
+
+    def close(self):
+        if getattr(self, "ptr", None) and _lib_instance is not None:
+            _lib_instance.mbx_trainer_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        self.close()
+
+
+class Context:
+    """Kernel seam (mbk_*): one device, one stream, device buffers."""
+
+    def __init__(self, device: int = 0):
+        self.ptr = _P()
+        err = ctypes.c_char_p()
+        if lib().mbk_context_create(device, ctypes.byref(self.ptr), ctypes.byref(err)) != 0:
+            raise MacBoostError(_take_error(err))
+        self._bufs = []
+
+    def _check(self, rc, err):
+        if rc != 0:
+            raise MacBoostError(_take_error(err))
+
+    def alloc(self, nbytes: int) -> int:
+        p = _P()
+        err = ctypes.c_char_p()
+        self._check(lib().mbk_device_alloc(self.ptr, nbytes, ctypes.byref(p), ctypes.byref(err)),
+                    err)
+        self._bufs.append(p.value)
+        return p.value
+
+    def upload(self, arr: np.ndarray) -> int:
+        a = np.ascontiguousarray(arr)
+        d = self.alloc(a.nbytes)
+        err = ctypes.c_char_p()
+        self._check(lib().mbk_copy_to_device(self.ptr, d, a.ctypes.data, a.nbytes,
+                                             ctypes.byref(err)), err)
+        return d
+
+    def download(self, dptr: int, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        err = ctypes.c_char_p()
+        self._check(lib().mbk_copy_to_host(self.ptr, out.ctypes.data, dptr, out.nbytes,
+                                           ctypes.byref(err)), err)
+        return out
+
+    def sync(self):
+        err = ctypes.c_char_p()
+        self._check(lib().mbk_synchronize(self.ptr, ctypes.byref(err)), err)
+
+    def close(self):
+        if getattr(self, "ptr", None) and self.ptr.value and _lib_instance is not None:
+            for b in self._bufs:
+                _lib_instance.mbk_device_free(self.ptr, b)
+            self._bufs = []
+            _lib_instance.mbk_context_destroy(self.ptr)
+            self.ptr = _P()
+
+    def __del__(self):
+        self.close()

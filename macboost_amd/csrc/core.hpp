@@ -1,0 +1,183 @@
+// core.hpp — host-side types of the MI355X MacBoost library: parameters
+// (BoosterParams, Booster.swift:18-64), trees (Booster.swift:114-146), the
+// device context and the booster model.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <memory>
+#include <set>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "mbk.h"
+
+namespace mb {
+
+// Errors carry the reference's message text (MacBoostError.description,
+// MetalEngine.swift:11-20).
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+[[noreturn]] inline void invalid(const std::string &m) { throw Error("Invalid input: " + m); }
+[[noreturn]] inline void internal(const std::string &m) { throw Error("Internal error: " + m); }
+
+#define MB_HIP(expr)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            ::mb::internal(std::string(#expr) + " failed: " + hipGetErrorString(e_));        \
+    } while (0)
+
+enum Objective : int {
+    OBJ_L2 = 0, OBJ_LOGISTIC = 1, OBJ_MAE = 2, OBJ_HUBER = 3, OBJ_QUANTILE = 4,
+    OBJ_POISSON = 5, OBJ_TWEEDIE = 6, OBJ_MULTICLASS = 7,
+};
+
+struct Params {
+    int num_trees = 100;
+    int max_depth = 6;
+    float learning_rate = 0.1f;
+    float lambda = 1.0f;
+    float min_child_hess = 1.0f;
+    float min_split_gain = 0.0f;
+    int num_bins = 256;
+    int objective = OBJ_L2;
+    std::set<int> categorical;
+    float cat_smooth = 10.0f;
+    bool goss = false;
+    float goss_top_rate = 0.2f;
+    float goss_other_rate = 0.1f;
+    float alpha = 0.9f;
+    float tweedie_power = 1.5f;
+    float scale_pos_weight = 1.0f;
+    float subsample = 1.0f;
+    float feature_fraction = 1.0f;
+    bool has_monotone = false;
+    std::vector<int> monotone;
+    std::string metric = "auto";
+    int num_classes = 1;
+    int num_leaves = 0;              // 0 = level-wise growth
+    bool has_allowed = false;
+    std::set<int> allowed;
+    // C-ABI-only keys (CAPI.swift:20-22, :34)
+    int early_stopping_rounds = 0;
+    int eval_every = 0;
+    bool verbose = false;
+    std::string init_model;
+};
+
+Params parse_params(const char *json);
+void validate_params(const Params &p);     // Booster.swift:262-330
+std::string objective_name(int obj);
+
+// A trained tree in implicit-heap layout (Booster.swift:119-146).
+struct Tree {
+    std::vector<int32_t> feature;
+    std::vector<float> threshold;
+    std::vector<float> leaf;
+    std::vector<uint8_t> flags;
+    std::vector<uint32_t> cat_mask;  // 8 words per node, empty without categoricals
+    std::vector<float> gain;
+    std::vector<float> cover;
+};
+
+struct Device {
+    int id = 0;
+    hipStream_t stream = nullptr;
+    int num_cus = 0;
+    explicit Device(int device_id);
+    ~Device();
+    Device(const Device &) = delete;
+    Device &operator=(const Device &) = delete;
+};
+
+template <typename T>
+struct DevBuf {
+    T *ptr = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t count) { alloc(count); }
+    ~DevBuf() { release(); }
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : ptr(o.ptr), n(o.n) { o.ptr = nullptr; o.n = 0; }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        if (this != &o) { release(); ptr = o.ptr; n = o.n; o.ptr = nullptr; o.n = 0; }
+        return *this;
+    }
+    void alloc(size_t count) {
+        release();
+        n = count;
+        if (count) MB_HIP(hipMalloc(reinterpret_cast<void **>(&ptr), count * sizeof(T)));
+    }
+    void release() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        n = 0;
+    }
+    size_t bytes() const { return n * sizeof(T); }
+};
+
+// Flattened forest resident on the device (forestBuffers, Booster.swift:1944-1985).
+struct ForestCache {
+    bool valid = false;
+    int nodes_per_tree = 0;
+    int num_trees = 0;
+    bool has_mask = false;
+    DevBuf<int32_t> feature;
+    DevBuf<float> threshold;
+    DevBuf<uint8_t> flags;
+    DevBuf<float> leaf;
+    DevBuf<uint32_t> mask;
+};
+
+struct Booster {
+    Params params;
+    std::vector<Tree> trees;
+    float base_score = 0.0f;
+    int num_features = 0;
+    int trained_num_bins = 256;
+    std::set<int> trained_categorical;
+    std::vector<float> base_scores{0.0f};
+    int trained_num_classes = 1;
+    bool has_feature_names = false;
+    std::vector<std::string> feature_names;
+    int best_iteration = -1;         // -1 = nil
+    std::vector<float> eval_history;
+    std::vector<std::string> warnings;
+
+    std::unique_ptr<Device> dev;
+    ForestCache forest;
+
+    Device &device();
+    void build_forest();
+    std::vector<float> predict(const float *x_fm, int64_t rows, int64_t cols);
+    std::vector<float> predict_contrib(const float *x_fm, int64_t rows, int64_t cols);
+    std::vector<float> feature_importance(int type) const;
+    double shap_bias() const;
+    std::string to_json() const;
+    static Booster *from_json(const std::string &text);
+};
+
+// Incremental trainer (fitImpl, Booster.swift:445-1701).
+struct Trainer;
+Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t cols,
+                        bool row_major, const float *y, const float *w, const float *xv,
+                        int64_t vrows, const float *yv);
+void trainer_grow(Trainer *t, int num_trees);
+void trainer_profile(Trainer *t, bool enable);
+void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes);
+void trainer_setup_seconds(Trainer *t, double *edges_s, double *bin_s);
+Booster *trainer_booster(Trainer *t);
+void trainer_free(Trainer *t);
+
+// Shared helpers.
+std::vector<float> compute_edges(const float *x, int64_t rows, int64_t cols, int64_t rs,
+                                 int64_t cs, int num_bins, const std::vector<uint8_t> &is_cat);
+std::string swift_float(float v);
+int host_threads();
+
+}  // namespace mb

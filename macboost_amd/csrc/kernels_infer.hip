@@ -1,0 +1,207 @@
+// kernels_infer.hip — gfx950 inference kernels: batch forest prediction on raw
+// features (predict_forest, Shaders.swift:1541-1584), the binned single-tree
+// walk used for per-iteration validation (predict_tree_binned, :1763-1781) and
+// exact TreeSHAP (gpu_treeshap, :1656-1734).
+//
+// TreeSHAP here gives each lane one row and walks every root-to-leaf path in
+// wave-uniform order, extending/unwinding in double precision and
+// accumulating phi in an LDS slice owned by the lane: no global atomics, a
+// fixed summation order, and a single rounding to f32 at the end.
+#include "mbk.h"
+
+#include <math.h>
+
+namespace mbk {
+
+__device__ __forceinline__ bool raw_goes_left(float v, uint32_t flags, float thr,
+                                              const uint32_t *mask_node, int32_t data_bins) {
+    if (flags & FLAG_CATEGORICAL) {
+        uint32_t cat = (uint32_t)data_bins;            // unseen -> missing
+        if (isfinite(v)) {
+            const float r = rintf(v);
+            if (r >= 0.0f && (int64_t)r < data_bins) cat = (uint32_t)r;
+        }
+        return mask_node ? ((mask_node[cat >> 5] >> (cat & 31u)) & 1u) != 0 : false;
+    }
+    if (isnan(v)) return (flags & FLAG_DEFAULT_LEFT) != 0;
+    return v <= thr;
+}
+
+__global__ __launch_bounds__(256) void k_predict_forest(ForestDev f, const float *__restrict__ x,
+                                                        int64_t rows, int32_t data_bins, float base,
+                                                        float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows) return;
+    float acc = base;                                  // seeded with the base, trees in order
+    for (int32_t t = 0; t < f.num_trees; ++t) {
+        const int64_t b = (int64_t)t * f.nodes_per_tree;
+        int32_t n = 0;
+        int32_t feat = f.feature[b];
+        while (feat >= 0) {
+            const float v = x[(int64_t)feat * rows + i];
+            const bool left = raw_goes_left(v, f.flags[b + n], f.threshold[b + n],
+                                            f.mask ? f.mask + (b + n) * 8 : nullptr, data_bins);
+            n = 2 * n + 1 + (left ? 0 : 1);
+            feat = f.feature[b + n];
+        }
+        acc += f.leaf[b + n];
+    }
+    out[i] = acc;
+}
+
+hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float *x, int64_t rows,
+                                 int32_t data_bins, float base, float *out) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_predict_forest, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, f,
+                       x, rows, data_bins, base, out);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_predict_binned(const uint8_t *__restrict__ bins_fm,
+                                                        int64_t rows, int32_t nb, int32_t max_depth,
+                                                        TreeOut tree, float *__restrict__ preds) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows) return;
+    uint32_t n = 0;
+    for (int32_t d = 0; d < max_depth; ++d) {
+        const NodeSplit s = tree.split[n];
+        if (s.feature < 0) break;
+        const uint32_t b = bins_fm[(int64_t)s.feature * rows + i];
+        bool left;
+        if (s.flags & FLAG_CATEGORICAL) left = ((tree.mask[n * 8 + (b >> 5)] >> (b & 31u)) & 1u) != 0;
+        else if (b == (uint32_t)(nb - 1)) left = (s.flags & FLAG_DEFAULT_LEFT) != 0;
+        else left = b <= s.bin;
+        n = 2 * n + 1 + (left ? 0 : 1);
+    }
+    preds[i] += tree.leaf[n];
+}
+
+hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                                 int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                                 float *preds) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_predict_binned, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
+                       bins_fm, rows, num_bins, max_depth, tree, preds);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// TreeSHAP
+// ---------------------------------------------------------------------------
+
+constexpr int SHAP_MAX_U = 12;                         // maxDepth <= 12
+
+__global__ __launch_bounds__(64) void k_treeshap(const float *__restrict__ x, int64_t rows,
+                                                 int32_t cols, int32_t data_bins,
+                                                 const uint32_t *__restrict__ masks,
+                                                 const ShapPath *__restrict__ paths,
+                                                 int32_t num_paths,
+                                                 const ShapElem *__restrict__ elems,
+                                                 const ShapUniq *__restrict__ uniq, float bias,
+                                                 float *__restrict__ out,
+                                                 double *__restrict__ phi_global) {
+    extern __shared__ double phi_lds[];                // [cols][64] when phi_global is null
+    const int lane = threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+    const bool valid = i < rows;
+    const int64_t irow = valid ? i : 0;
+    double *phi = phi_global ? phi_global + (int64_t)blockIdx.x * 64 * cols : phi_lds;
+    for (int f = 0; f < cols; ++f) phi[f * 64 + lane] = 0.0;
+    for (int32_t p = 0; p < num_paths; ++p) {
+        const ShapPath P = paths[p];
+        double one[SHAP_MAX_U], zero[SHAP_MAX_U];
+        int feat[SHAP_MAX_U];
+#pragma unroll
+        for (int u = 0; u < SHAP_MAX_U; ++u) {
+            one[u] = 1.0;
+            zero[u] = 1.0;
+            feat[u] = 0;
+            if (u < P.num_uniq) {
+                const ShapUniq q = uniq[P.uniq_start + u];
+                zero[u] = q.zero;
+                feat[u] = q.feature;
+            }
+        }
+        for (int e = 0; e < P.num_elem; ++e) {
+            const ShapElem el = elems[P.elem_start + e];
+            const float v = x[(int64_t)el.feature * rows + irow];
+            const bool left = raw_goes_left(v, el.flags, el.threshold,
+                                            masks ? masks + (int64_t)el.node * 8 : nullptr,
+                                            data_bins);
+            const double o = (left == ((el.flags & 0x100u) != 0)) ? 1.0 : 0.0;
+#pragma unroll
+            for (int u = 0; u < SHAP_MAX_U; ++u)
+                if (u == el.uniq) one[u] *= o;
+        }
+        const int U = P.num_uniq;
+        // EXTEND with the dummy element at index 0 (SHAP.swift:266-279)
+        double pw[SHAP_MAX_U + 1];
+        pw[0] = 1.0;
+#pragma unroll
+        for (int j = 1; j <= SHAP_MAX_U; ++j) {
+            pw[j] = 0.0;
+            if (j <= U) {
+                const double o = one[j - 1], z = zero[j - 1];
+#pragma unroll
+                for (int q = j - 1; q >= 0; --q) {
+                    pw[q + 1] += o * pw[q] * (double)(q + 1) / (double)(j + 1);
+                    pw[q] = z * pw[q] * (double)(j - q) / (double)(j + 1);
+                }
+            }
+        }
+        // unwound sums per unique feature (SHAP.swift:307-325)
+#pragma unroll
+        for (int u = 0; u < SHAP_MAX_U; ++u) {
+            if (u < U) {
+                const double o = one[u], z = zero[u];
+                double total = 0.0;
+                if (o != 0.0) {
+                    double next = 0.0;
+#pragma unroll
+                    for (int q = SHAP_MAX_U; q >= 0; --q)
+                        if (q == U) next = pw[q];
+#pragma unroll
+                    for (int q = SHAP_MAX_U - 1; q >= 0; --q) {
+                        if (q < U) {
+                            const double tmp = next / ((double)(q + 1) * o);
+                            total += tmp;
+                            next = pw[q] - tmp * z * (double)(U - q);
+                        }
+                    }
+                } else if (z != 0.0) {
+#pragma unroll
+                    for (int q = SHAP_MAX_U - 1; q >= 0; --q)
+                        if (q < U) total += pw[q] / (z * (double)(U - q));
+                }
+                const double contrib = total * (double)(U + 1) * (o - z) * P.leaf;
+                phi[feat[u] * 64 + lane] += contrib;
+            }
+        }
+    }
+    if (!valid) return;
+    float *orow = out + i * (int64_t)(cols + 1);
+    for (int f = 0; f < cols; ++f) orow[f] = (float)phi[f * 64 + lane];
+    orow[cols] = bias;
+}
+
+hipError_t launch_treeshap(hipStream_t s, const float *x, int64_t rows, int32_t cols,
+                           int32_t data_bins, const uint32_t *masks, const ShapPath *paths,
+                           int32_t num_paths, const ShapElem *elems, const ShapUniq *uniq,
+                           float bias, float *out, double *phi_global) {
+    if (rows <= 0) return hipSuccess;
+    const unsigned blocks = (unsigned)((rows + 63) / 64);
+    const size_t lds = phi_global ? 0 : (size_t)cols * 64 * sizeof(double);
+    hipLaunchKernelGGL(k_treeshap, dim3(blocks), dim3(64), lds, s, x, rows, cols, data_bins, masks,
+                       paths, num_paths, elems, uniq, bias, out, phi_global);
+    return hipGetLastError();
+}
+
+// Largest column count whose per-lane phi slices fit in LDS.
+int treeshap_lds_max_cols() { return (int)(160 * 1024 / (64 * sizeof(double))) - 1; }
+
+hipError_t treeshap_set_lds_limit(int cols) {
+    return hipFuncSetAttribute((const void *)k_treeshap, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               cols * 64 * (int)sizeof(double));
+}
+
+}  // namespace mbk

@@ -1,0 +1,241 @@
+// mbk.h — internal device data structures and kernel launchers of the MI355X
+// tree-build path.  Shared by the HIP kernels (kernels_*.hip) and the C++ host
+// (booster.cpp).  All structs are plain 4/8-byte-field PODs.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mbk {
+
+constexpr uint32_t FLAG_DEFAULT_LEFT = 1u;
+constexpr uint32_t FLAG_CATEGORICAL = 2u;
+
+// Rows are routed by the level-wise partition in blocks of this many order
+// entries (256 threads x 8 entries).
+constexpr int ROUTE_THREADS = 256;
+constexpr int ROUTE_PER_THREAD = 8;
+constexpr int ROUTE_BLOCK = ROUTE_THREADS * ROUTE_PER_THREAD;
+
+// A histogram item accumulates at most this many rows in one packed LDS word:
+// high 32 bits = sum of 16-bit quantised gradients (|sum| <= 65535*32767 < 2^31),
+// low 32 bits = sum of 7-bit quantised hessians (no carry into the high half).
+constexpr uint32_t HIST_CHUNK_MAX = 65535;
+
+// NodeSplit (Shaders.swift:466): feature < 0 marks a leaf.
+struct NodeSplit {
+    int32_t feature;
+    uint32_t bin;
+    uint32_t flags;
+};
+
+// One (node, feature) split candidate: SplitResult (Shaders.swift:334) plus the
+// exact integer left sums and, for categorical splits, the left-subset mask.
+struct SplitResult {
+    float gain;
+    uint32_t bin;
+    float gl, hl;
+    uint32_t flags;
+    uint32_t pad;
+    int64_t gl_int, hl_int;
+    uint32_t mask[8];
+};
+
+// Order entry: a row index travelling with its packed quantised gradient word
+// (qg << 16 | qh, Shaders.swift:189-191).
+struct Entry {
+    uint32_t row;
+    uint32_t ghq;
+};
+
+// Histogram work item: rows [start, start+count) of the level's order buffer,
+// one feature tile, contributing to the built node of `pair`.
+struct HistItem {
+    uint32_t pair;
+    uint32_t tile;
+    uint32_t start;
+    uint32_t count;
+};
+
+// Sibling pair for the split kernel: the built child (histogram from partials),
+// the derived child (parent - built) and the parent's slot in the previous
+// level's histograms.  derived == 0xFFFFFFFF for the root.
+struct Pair {
+    uint32_t built;      // level-local node index (slot in hist_cur)
+    uint32_t derived;    // level-local node index or NONE
+    uint32_t parent;     // slot in hist_prev
+    uint32_t item_first; // first HistItem of the built node
+    uint32_t nchunks;    // chunks per tile
+    uint32_t pad[3];
+};
+constexpr uint32_t NONE = 0xFFFFFFFFu;
+
+// Global per-fit constants.
+struct Shape {
+    int64_t rows;        // N
+    int32_t cols;        // F
+    int32_t num_bins;    // B (incl. missing bin)
+    int32_t tile_w;      // W, features per row tile of the gather layout
+    int32_t num_tiles;   // T = ceil(F / W)
+};
+
+struct SplitParams {
+    float lambda;
+    float min_child_hess;
+    float min_split_gain;
+    float cat_smooth;
+    float learning_rate;
+    int32_t max_depth;
+};
+
+// Device-resident per-tree control block (counters written by kernels).
+struct TreeCtl {
+    uint32_t max_gh[2];      // f32 bit patterns of max|g| and max h
+    uint32_t num_items;      // histogram items of the current level
+    uint32_t num_pairs;      // sibling pairs of the current level
+    uint32_t chunk;          // rows per histogram chunk of the current level
+    uint32_t pad[3];
+    uint32_t level_active[16];  // live order entries per level
+    uint32_t level_built[16];   // rows of built (histogrammed) nodes per level
+};
+
+// ---------------------------------------------------------------------------
+// Launchers (kernels_*.hip).  All enqueue on `s` and return hipError_t.
+// ---------------------------------------------------------------------------
+
+hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t cols,
+                           int64_t row_stride, int64_t col_stride, const float *edges,
+                           const uint8_t *is_cat, int32_t num_bins, int32_t tile_w,
+                           int32_t num_tiles, uint8_t *bins_tiled, uint8_t *bins_fm);
+
+hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl);
+
+// Objectives numbered as Booster.swift:5-14.
+struct GradParams {
+    int32_t objective;
+    float alpha;
+    float aux;
+    int32_t has_weights;
+};
+hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *preds,
+                           const float *labels, const float *weights, int64_t rows,
+                           TreeCtl *ctl);
+hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
+                           const float *labels, const float *weights, int64_t rows,
+                           const TreeCtl *ctl, Entry *order);
+
+// Histogram items -> packed partials [item][W][B].
+hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
+                       const Entry *order, const HistItem *items, const TreeCtl *ctl,
+                       uint64_t *partials, int grid);
+hipError_t hist_set_lds_limit(int tile_w, int num_bins);
+
+// Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
+struct LevelArgs {
+    int32_t level;           // d
+    uint32_t level_start;    // heap index of the level's first node
+    uint32_t num_level;      // 2^d
+    uint32_t terminal;       // 1: children of the routed level are final leaves
+};
+
+struct TreeOut {             // one tree's model arrays (heap layout)
+    NodeSplit *split;
+    float *leaf;
+    float *gain;
+    float *cover;
+    uint32_t *mask;          // 8 words per node
+};
+
+// Reduce partials, derive siblings, search splits for both nodes of each pair.
+hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp,
+                        const Pair *pairs, uint32_t max_pairs, const uint64_t *partials,
+                        const int64_t *hist_prev, int64_t *hist_cur, const uint8_t *is_cat,
+                        const int8_t *monotone, const uint8_t *feat_mask,
+                        const TreeCtl *ctl, const uint32_t *count, int64_t *node_g,
+                        int64_t *node_h, uint32_t level_start, SplitResult *results);
+
+hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active,
+                            uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
+                            uint32_t *seg_start, uint32_t *count, Pair *pairs,
+                            HistItem *items, float *cover, float2 *bounds,
+                            float root_lo, float root_hi, uint32_t *scratch);
+
+hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
+                         const LevelArgs &la, const SplitResult *results,
+                         const uint32_t *count, int64_t *node_g, int64_t *node_h,
+                         float2 *bounds, const int8_t *monotone, const TreeCtl *ctl,
+                         uint32_t *left_count, TreeOut out);
+
+hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const LevelArgs &la,
+                               const uint32_t *count, const int64_t *node_g,
+                               const int64_t *node_h, const float2 *bounds,
+                               const TreeCtl *ctl, TreeOut out);
+
+// la = the level being routed (d-1).
+hipError_t launch_route_count(hipStream_t s, const Shape &sh, const LevelArgs &la,
+                              const uint8_t *bins_fm, const Entry *order_in,
+                              const uint32_t *seg_start, const TreeOut out,
+                              const TreeCtl *ctl, uint8_t *dir, uint32_t *left_count,
+                              uint32_t *block_left, uint32_t max_blocks);
+
+// la = the level being planned (d); reads level d-1's routed counts.
+hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
+                             uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
+                             uint32_t *seg_start_next, uint32_t *count,
+                             const uint32_t *left_count, uint32_t *node_left_prefix,
+                             uint32_t *block_left, const TreeOut out, Pair *pairs,
+                             HistItem *items, uint32_t *scratch);
+
+// la = the level being routed (d-1).
+hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs &la,
+                                const Entry *order_in, Entry *order_out, const uint8_t *dir,
+                                const uint32_t *seg_start, const uint32_t *seg_start_next,
+                                const uint32_t *node_left_prefix, const uint32_t *block_off,
+                                const TreeOut out, const TreeCtl *ctl, float *preds,
+                                uint32_t max_blocks);
+
+// Inference.
+struct ForestDev {
+    const int32_t *feature;
+    const float *threshold;
+    const uint8_t *flags;
+    const float *leaf;
+    const uint32_t *mask;      // 8 words per node or NULL when no node is categorical
+    int32_t num_trees;
+    int32_t nodes_per_tree;
+};
+hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float *x,
+                                 int64_t rows, int32_t data_bins, float base, float *out);
+hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                                 int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                                 float *preds);
+
+struct ShapPath {
+    int32_t elem_start;   // first element
+    int32_t num_elem;     // elements on the path (root first)
+    int32_t uniq_start;   // first unique-feature slot
+    int32_t num_uniq;     // unique features U
+    double leaf;          // leaf value
+};
+struct ShapElem {
+    int32_t node;         // global node index (tree * nodes_per_tree + node)
+    int32_t feature;
+    float threshold;
+    uint32_t flags;       // split flags | 0x100 when the path continues left
+    int32_t uniq;         // index of its unique-feature slot within the path
+    int32_t pad;
+};
+struct ShapUniq {
+    int32_t feature;
+    int32_t pad;
+    double zero;          // product of cover fractions along the path
+};
+// phi_global: NULL to keep each lane's phi slice in LDS (cols <=
+// treeshap_lds_max_cols()), else a [ceil(rows/64)][cols][64] double scratch.
+hipError_t launch_treeshap(hipStream_t s, const float *x, int64_t rows, int32_t cols,
+                           int32_t data_bins, const uint32_t *masks, const ShapPath *paths,
+                           int32_t num_paths, const ShapElem *elems, const ShapUniq *uniq,
+                           float bias, float *out, double *phi_global);
+int treeshap_lds_max_cols();
+hipError_t treeshap_set_lds_limit(int cols);
+
+}  // namespace mbk

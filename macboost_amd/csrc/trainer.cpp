@@ -1,0 +1,857 @@
+// trainer.cpp — the training driver: fitImpl (Booster.swift:445-1701) restated
+// for one MI355X.  Edges are computed on the host (Binner.swift:33-56), the raw
+// matrix is binned on the device, and every tree is a fixed sequence of
+// kernels on one HIP stream with all split decisions kept on the device; the
+// host touches the stream again only to read finished trees (or, with a
+// validation set, the per-iteration metric).
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdlib>
+#include <cstdio>
+#include <cstring>
+#include <thread>
+
+#include "core.hpp"
+
+namespace mb {
+
+int host_threads() {
+    unsigned n = std::thread::hardware_concurrency();
+    if (n == 0) n = 1;
+    if (n > 16) n = 16;
+    return (int)n;
+}
+
+template <typename Fn>
+static void parallel_for(int64_t n, Fn fn) {
+    int nt = host_threads();
+    if (n < 2 || nt < 2) {
+        for (int64_t i = 0; i < n; ++i) fn(i);
+        return;
+    }
+    std::vector<std::thread> th;
+    std::atomic<int64_t> next{0};
+    for (int k = 0; k < nt; ++k)
+        th.emplace_back([&] {
+            for (int64_t i = next++; i < n; i = next++) fn(i);
+        });
+    for (auto &t : th) t.join();
+}
+
+static double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+// Quantile edges: stride subsample of <= 200k non-NaN values per feature,
+// sorted, edge k = sample[min(m-1, (k+1)*m / dataBins)] (Binner.swift:33-56).
+std::vector<float> compute_edges(const float *x, int64_t rows, int64_t cols, int64_t rs,
+                                 int64_t cs, int num_bins, const std::vector<uint8_t> &is_cat) {
+    const int data_bins = num_bins - 1, num_edges = data_bins - 1;
+    int64_t step = rows / 200000;
+    if (step < 1) step = 1;
+    std::vector<float> edges((size_t)cols * num_edges, 0.0f);
+    parallel_for(cols, [&](int64_t f) {
+        if (is_cat[f]) return;
+        std::vector<float> sample;
+        sample.reserve((size_t)(rows / step + 1));
+        for (int64_t i = 0; i < rows; i += step) {
+            float v = x[i * rs + f * cs];
+            if (!std::isnan(v)) sample.push_back(v);
+        }
+        if (sample.empty()) return;
+        std::sort(sample.begin(), sample.end());
+        const int64_t m = (int64_t)sample.size();
+        for (int k = 0; k < num_edges; ++k) {
+            int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
+            if (idx > m - 1) idx = m - 1;
+            edges[(size_t)f * num_edges + k] = sample[(size_t)idx];
+        }
+    });
+    return edges;
+}
+
+std::string swift_float(float v) {
+    if (std::isnan(v)) return "nan";
+    if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
+    char buf[64];
+    if (v == std::floor(v) && std::fabs(v) < 1e16f) {
+        std::snprintf(buf, sizeof buf, "%.1f", (double)v);
+        return buf;
+    }
+    std::snprintf(buf, sizeof buf, "%.9g", (double)v);
+    // shortest representation that round-trips
+    for (int prec = 1; prec <= 9; ++prec) {
+        char b2[64];
+        std::snprintf(b2, sizeof b2, "%.*g", prec, (double)v);
+        if (std::strtof(b2, nullptr) == v) return b2;
+    }
+    return buf;
+}
+
+Device::Device(int device_id) : id(device_id) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= device_id)
+        throw Error("No HIP GPU available");
+    MB_HIP(hipSetDevice(device_id));
+    MB_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    hipDeviceProp_t prop;
+    MB_HIP(hipGetDeviceProperties(&prop, device_id));
+    num_cus = prop.multiProcessorCount;
+}
+
+Device::~Device() {
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+// ---------------------------------------------------------------------------
+
+struct Trainer {
+    Params p;
+    std::unique_ptr<Device> dev;
+    mbk::Shape sh{};
+    mbk::SplitParams sp{};
+    mbk::GradParams gp{};
+    int D = 6, total_nodes = 0, max_level_nodes = 1;
+    int64_t rows = 0;
+    int cols = 0, nb = 256;
+    std::vector<float> edges;
+    std::vector<uint8_t> is_cat_h, mask_base;
+    std::vector<int8_t> mono_h;
+    std::vector<float> labels_h, vlabels_h;
+    bool has_weights = false, has_valid = false, has_cats = false;
+    int64_t vrows = 0;
+    float base = 0.0f;
+
+    DevBuf<uint8_t> bins_tiled, bins_fm, vbins_fm;
+    DevBuf<float> labels, weights, preds, vpreds;
+    DevBuf<uint8_t> is_cat, feat_mask;
+    DevBuf<int8_t> mono;
+    DevBuf<mbk::Entry> order_a, order_b;
+    DevBuf<uint8_t> dir;
+    DevBuf<uint32_t> block_left;
+    DevBuf<uint64_t> partials;
+    DevBuf<mbk::HistItem> items;
+    DevBuf<mbk::Pair> pairs;
+    DevBuf<int64_t> hist_a, hist_b;
+    DevBuf<mbk::SplitResult> results;
+    DevBuf<uint32_t> count, seg_a, seg_b, left_count, node_left_prefix, scratch;
+    DevBuf<int64_t> node_g, node_h;
+    DevBuf<float2> bounds;
+    DevBuf<mbk::TreeCtl> ctl, ctl_hist;
+    DevBuf<mbk::NodeSplit> m_split;
+    DevBuf<float> m_leaf, m_gain, m_cover;
+    DevBuf<uint32_t> m_mask;
+    int capacity = 0, grown = 0;
+    int hist_grid = 256, target_items = 512, min_chunk = 2048;
+    uint32_t max_blocks = 1;
+    std::vector<std::vector<uint8_t>> tree_masks;
+
+    bool profiling = false;
+    int prof_first_tree = 0;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+    int64_t prof_launches = 0;
+    double prof_ms = 0.0;
+
+    // metrics / early stopping (Booster.swift:1650-1696)
+    int best_iter = 0;
+    float best_metric = 0.0f;
+    int stale = 0;
+    bool stopped = false;
+    std::vector<float> eval_history;
+    std::vector<std::string> warnings;
+    double t_edges = 0.0, t_bin = 0.0;
+
+    ~Trainer() {
+        for (auto &e : events) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
+    }
+
+    mbk::TreeOut tree_out(int t) {
+        mbk::TreeOut o;
+        size_t base_n = (size_t)t * total_nodes;
+        o.split = m_split.ptr + base_n;
+        o.leaf = m_leaf.ptr + base_n;
+        o.gain = m_gain.ptr + base_n;
+        o.cover = m_cover.ptr + base_n;
+        o.mask = m_mask.ptr + base_n * 8;
+        return o;
+    }
+
+    void ensure_capacity(int n) {
+        if (n <= capacity) return;
+        int cap = std::max(n, capacity * 2);
+        auto grow = [&](auto &buf, size_t per_tree) {
+            using T = typename std::remove_reference<decltype(*buf.ptr)>::type;
+            DevBuf<T> nbuf((size_t)cap * per_tree);
+            MB_HIP(hipMemsetAsync(nbuf.ptr, 0, nbuf.bytes(), dev->stream));
+            if (buf.ptr && capacity)
+                MB_HIP(hipMemcpyAsync(nbuf.ptr, buf.ptr, (size_t)capacity * per_tree * sizeof(T),
+                                      hipMemcpyDeviceToDevice, dev->stream));
+            MB_HIP(hipStreamSynchronize(dev->stream));
+            buf = std::move(nbuf);
+        };
+        grow(m_split, total_nodes);
+        grow(m_leaf, total_nodes);
+        grow(m_gain, total_nodes);
+        grow(m_cover, total_nodes);
+        grow(m_mask, (size_t)total_nodes * 8);
+        grow(ctl_hist, 1);
+        capacity = cap;
+    }
+};
+
+static void validate_labels(const Params &p, const float *y, int64_t n) {   // :1724-1765
+    const bool logistic = p.objective == OBJ_LOGISTIC;
+    const bool nonneg = p.objective == OBJ_POISSON || p.objective == OBJ_TWEEDIE;
+    for (int64_t i = 0; i < n; ++i) {
+        float v = y[i];
+        if (!std::isfinite(v))
+            invalid("label at row " + std::to_string(i) + " is " + swift_float(v) +
+                    "; labels must be finite");
+        if (logistic && v != 0.0f && v != 1.0f)
+            invalid("label at row " + std::to_string(i) + " is " + swift_float(v) +
+                    "; binary objective requires labels in {0, 1}");
+        if (nonneg && v < 0.0f)
+            invalid("label at row " + std::to_string(i) + " is " + swift_float(v) + "; " +
+                    objective_name(p.objective) + " requires labels >= 0");
+    }
+}
+
+static void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_t cols,
+                                  int64_t rs, int64_t cs) {          // :1810-1826
+    const int data_bins = p.num_bins - 1;
+    for (int f : p.categorical) {
+        if (f < 0 || f >= cols)
+            internal("categorical feature index " + std::to_string(f) + " out of range");
+        for (int64_t i = 0; i < rows; ++i) {
+            float v = x[i * rs + (int64_t)f * cs];
+            if (std::isnan(v)) continue;
+            float c = std::nearbyint(v);
+            if (!(c >= 0.0f) || !std::isfinite(c) || (int64_t)c >= data_bins)
+                throw Error("Categorical feature " + std::to_string(f) + " has value " +
+                            swift_float(v) + "; expected integer ids in 0..<" +
+                            std::to_string(data_bins) + " or NaN");
+        }
+    }
+}
+
+// Cheap target-leakage guard (Booster.swift:1771-1808).
+static void check_leakage(Trainer &t, const float *x, int64_t rows, int64_t cols, int64_t rs,
+                          int64_t cs, const float *y) {
+    int64_t step = std::max<int64_t>(1, rows / 4096);
+    std::vector<int64_t> idx;
+    for (int64_t i = 0; i < rows; i += step) idx.push_back(i);
+    if (idx.size() < 50) return;
+    double ym = 0;
+    for (auto i : idx) ym += (double)y[i];
+    ym /= (double)idx.size();
+    for (int64_t f = 0; f < cols; ++f) {
+        double sxy = 0, sxx = 0, syy = 0, xm = 0;
+        int64_t n = 0;
+        for (auto i : idx) {
+            float v = x[i * rs + f * cs];
+            if (std::isfinite(v)) { xm += (double)v; ++n; }
+        }
+        if (n < 50) continue;
+        xm /= (double)n;
+        for (auto i : idx) {
+            double v = (double)x[i * rs + f * cs];
+            if (!std::isfinite(v)) continue;
+            double dx = v - xm, dy = (double)y[i] - ym;
+            sxy += dx * dy; sxx += dx * dx; syy += dy * dy;
+        }
+        if (!(sxx > 0 && syy > 0)) continue;
+        double r = sxy / (std::sqrt(sxx) * std::sqrt(syy));
+        if (std::fabs(r) > 0.999) {
+            char buf[256];
+            std::snprintf(buf, sizeof buf,
+                          "[MacBoost] [Warning] feature %lld correlates with the label at "
+                          "|r|=%.4f on a subsample — possible target leakage (is the label or a "
+                          "prediction included in X?)",
+                          (long long)f, std::fabs(r));
+            t.warnings.push_back(buf);
+            if (t.p.verbose) std::printf("%s\n", buf);
+        }
+    }
+}
+
+static float base_score(const Params &p, const float *y, const float *w, int64_t n) {
+    if (p.objective == OBJ_LOGISTIC) {                     // :802-830
+        double pos = 0, tot = 0;
+        const double spw = (double)p.scale_pos_weight;
+        for (int64_t i = 0; i < n; ++i) {
+            double wi = w ? (double)w[i] : 1.0;
+            if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
+        }
+        float pr = (float)(pos / std::max(tot, 1e-12));
+        pr = std::min(std::max(pr, 1e-6f), 1.0f - 1e-6f);
+        return std::log(pr / (1.0f - pr));
+    }
+    double num = 0, den = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        double wi = w ? (double)w[i] : 1.0;
+        num += wi * (double)y[i];
+        den += wi;
+    }
+    float m = den > 0 ? (float)(num / den) : 0.0f;
+    if (p.objective == OBJ_POISSON || p.objective == OBJ_TWEEDIE) {
+        if (!(m > 0)) invalid(objective_name(p.objective) + " requires a positive label mean");
+        return std::log(m);
+    }
+    return m;
+}
+
+static std::string effective_metric(const Params &p) {
+    if (p.metric != "auto") return p.metric;
+    switch (p.objective) {
+    case OBJ_MAE: return "mae";
+    case OBJ_QUANTILE: return "pinball";
+    case OBJ_LOGISTIC: return "logloss";
+    case OBJ_POISSON: return "poisson";
+    case OBJ_TWEEDIE: return "tweedie";
+    case OBJ_MULTICLASS: return "multi_logloss";
+    default: return "rmse";
+    }
+}
+
+// evalMetricRaw (Booster.swift:1855-1918).
+static float eval_metric(const Params &p, const float *pred, const float *y, int64_t n) {
+    const std::string m = effective_metric(p);
+    if (m == "rmse" || m == "auto") {
+        double s = 0;
+        for (int64_t i = 0; i < n; ++i) { double d = (double)pred[i] - y[i]; s += d * d; }
+        return (float)std::sqrt(s / (double)n);
+    }
+    if (m == "mae") {
+        double s = 0;
+        for (int64_t i = 0; i < n; ++i) s += std::fabs((double)pred[i] - y[i]);
+        return (float)(s / (double)n);
+    }
+    if (m == "pinball") {
+        double a = p.alpha, s = 0;
+        for (int64_t i = 0; i < n; ++i) { double d = (double)y[i] - pred[i]; s += d >= 0 ? a * d : (a - 1) * d; }
+        return (float)(s / (double)n);
+    }
+    if (m == "logloss") {
+        double s = 0;
+        for (int64_t i = 0; i < n; ++i) {
+            double q = 1 / (1 + std::exp(-(double)pred[i])), yy = y[i];
+            s += -(yy * std::log(std::max(q, 1e-12)) + (1 - yy) * std::log(std::max(1 - q, 1e-12)));
+        }
+        return (float)(s / (double)n);
+    }
+    if (m == "auc") {
+        std::vector<int64_t> idx((size_t)n);
+        for (int64_t i = 0; i < n; ++i) idx[(size_t)i] = i;
+        std::stable_sort(idx.begin(), idx.end(), [&](int64_t a, int64_t b) { return pred[a] < pred[b]; });
+        double pos_rank = 0, npos = 0;
+        int64_t i = 0;
+        while (i < n) {
+            int64_t j = i;
+            while (j < n && pred[idx[(size_t)j]] == pred[idx[(size_t)i]]) ++j;
+            double avg = (double)(i + j + 1) / 2;
+            for (int64_t k = i; k < j; ++k)
+                if (y[idx[(size_t)k]] > 0.5f) { pos_rank += avg; npos += 1; }
+            i = j;
+        }
+        double nneg = (double)n - npos;
+        if (!(npos > 0 && nneg > 0)) return 0.5f;
+        return (float)((pos_rank - npos * (npos + 1) / 2) / (npos * nneg));
+    }
+    if (m == "poisson") {
+        double s = 0;
+        for (int64_t i = 0; i < n; ++i) {
+            double mu = std::exp((double)pred[i]), yy = y[i];
+            s += 2 * ((yy > 0 ? yy * std::log(yy / mu) : 0) - (yy - mu));
+        }
+        return (float)(s / (double)n);
+    }
+    if (m == "tweedie") {
+        double rho = p.tweedie_power, s = 0;
+        for (int64_t i = 0; i < n; ++i) {
+            double mu = std::exp((double)pred[i]), yy = y[i];
+            double a = yy > 0 ? std::pow(yy, 2 - rho) / ((1 - rho) * (2 - rho)) : 0;
+            s += 2 * (a - yy * std::pow(mu, 1 - rho) / (1 - rho) + std::pow(mu, 2 - rho) / (2 - rho));
+        }
+        return (float)(s / (double)n);
+    }
+    return 0.0f;
+}
+
+Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t cols,
+                        bool row_major, const float *y, const float *w, const float *xv,
+                        int64_t vrows, const float *yv) {
+    if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
+    validate_params(pin);
+    auto tr = std::make_unique<Trainer>();
+    Trainer &t = *tr;
+    t.p = pin;
+    const Params &p = t.p;
+    if (p.goss) invalid("goss is not supported by this build yet");
+    if (p.subsample < 1.0f) invalid("subsample < 1 is not supported by this build yet");
+    if (p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE)
+        invalid("objective '" + objective_name(p.objective) +
+                "' (leaf renewal) is not supported by this build yet");
+    if (p.objective == OBJ_MULTICLASS) invalid("multiclass is not supported by this build yet");
+    if (p.num_leaves > 0) invalid("leaf-wise growth (num_leaves) is not supported by this build yet");
+    if (!p.init_model.empty()) invalid("init_model (warm start) is not supported by this build yet");
+    // data validation (Booster.swift:451-529)
+    validate_labels(p, y, rows);
+    if (w)
+        for (int64_t i = 0; i < rows; ++i)
+            if (!(std::isfinite(w[i]) && w[i] >= 0))
+                invalid("weight at row " + std::to_string(i) + " is " + swift_float(w[i]) +
+                        "; weights must be finite and >= 0");
+    if (xv && yv && vrows > 0) validate_labels(p, yv, vrows);
+    if (p.has_monotone && (int64_t)p.monotone.size() != cols)
+        invalid("monotoneConstraints has " + std::to_string(p.monotone.size()) +
+                " entries, X has " + std::to_string(cols) + " features");
+    if (p.has_allowed) {
+        bool ok = !p.allowed.empty();
+        for (int f : p.allowed) ok = ok && f >= 0 && f < cols;
+        if (!ok) invalid("allowedFeatures must be non-empty indices within 0..<" + std::to_string(cols));
+    }
+    const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
+    if (rows > 0xFFFFFFF0LL) invalid("more than 2^32 rows are not supported");
+    check_leakage(t, x, rows, cols, rs, cs, y);
+    validate_categoricals(p, x, rows, cols, rs, cs);
+    if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
+
+    t.dev = std::make_unique<Device>(0);
+    hipStream_t s = t.dev->stream;
+    t.rows = rows;
+    t.cols = (int)cols;
+    t.nb = p.num_bins;
+    t.D = p.max_depth;
+    t.total_nodes = (1 << (t.D + 1)) - 1;
+    t.max_level_nodes = 1 << (t.D - 1);
+    t.is_cat_h.assign((size_t)cols, 0);
+    for (int f : p.categorical) t.is_cat_h[(size_t)f] = 1;
+    t.has_cats = !p.categorical.empty();
+    t.mono_h.assign((size_t)cols, 0);
+    if (p.has_monotone)
+        for (int64_t f = 0; f < cols; ++f) t.mono_h[(size_t)f] = (int8_t)p.monotone[(size_t)f];
+    t.mask_base.assign((size_t)cols, 1);
+    if (p.has_allowed)
+        for (int64_t f = 0; f < cols; ++f) t.mask_base[(size_t)f] = p.allowed.count((int)f) ? 1 : 0;
+
+    // gather-layout tile width: features per row tile
+    int tile_w = 32;
+    if (const char *e = std::getenv("MACBOOST_TILE_W")) tile_w = std::atoi(e);
+    if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) tile_w = 32;
+    t.sh.rows = rows;
+    t.sh.cols = (int)cols;
+    t.sh.num_bins = p.num_bins;
+    t.sh.tile_w = tile_w;
+    t.sh.num_tiles = (int)((cols + tile_w - 1) / tile_w);
+    t.sp.lambda = p.lambda;
+    t.sp.min_child_hess = p.min_child_hess;
+    t.sp.min_split_gain = p.min_split_gain;
+    t.sp.cat_smooth = p.cat_smooth;
+    t.sp.learning_rate = p.learning_rate;
+    t.sp.max_depth = p.max_depth;
+    t.gp.objective = p.objective;
+    t.gp.alpha = p.alpha;
+    t.gp.aux = p.objective == OBJ_LOGISTIC ? p.scale_pos_weight
+             : p.objective == OBJ_TWEEDIE ? p.tweedie_power : 0.0f;
+    t.gp.has_weights = w ? 1 : 0;
+
+    // rows-per-bin hint (Booster.swift:730-738)
+    if (rows / p.num_bins < 64 && p.num_bins > 64) {
+        int suggest = 64;
+        while (suggest > 32 && rows / suggest < 64) suggest /= 2;
+        t.warnings.push_back(
+            "max_bin=" + std::to_string(p.num_bins) + " gives ~" +
+            std::to_string(std::max<int64_t>(1, rows / p.num_bins)) + " rows per bin at " +
+            std::to_string(rows) + " rows; max_bin=" + std::to_string(suggest) +
+            " is typically 2-4x faster here with equal accuracy (histogram cost scales with "
+            "bins, resolution does not once bins exceed rows per node)");
+    }
+
+    // --- binning: host edges, device bin_data ---------------------------
+    double t0 = now_s();
+    t.edges = compute_edges(x, rows, cols, rs, cs, p.num_bins, t.is_cat_h);
+    t.t_edges = now_s() - t0;
+    t0 = now_s();
+    {
+        DevBuf<float> xd((size_t)rows * (size_t)cols);
+        DevBuf<float> ed(std::max<size_t>(1, t.edges.size()));
+        t.is_cat.alloc((size_t)cols);
+        MB_HIP(hipMemcpyAsync(t.is_cat.ptr, t.is_cat_h.data(), (size_t)cols, hipMemcpyHostToDevice, s));
+        MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, s));
+        if (!t.edges.empty())
+            MB_HIP(hipMemcpyAsync(ed.ptr, t.edges.data(), t.edges.size() * 4, hipMemcpyHostToDevice, s));
+        t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
+        t.bins_fm.alloc((size_t)rows * (size_t)cols);
+        MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
+        MB_HIP(mbk::launch_bin_data(s, xd.ptr, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
+                                    p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
+                                    t.bins_fm.ptr));
+        if (xv && yv && vrows > 0) {
+            t.has_valid = true;
+            t.vrows = vrows;
+            DevBuf<float> xvd((size_t)vrows * (size_t)cols);
+            DevBuf<uint8_t> vt((size_t)t.sh.num_tiles * (size_t)vrows * (size_t)tile_w);
+            t.vbins_fm.alloc((size_t)vrows * (size_t)cols);
+            MB_HIP(hipMemcpyAsync(xvd.ptr, xv, xvd.bytes(), hipMemcpyHostToDevice, s));
+            MB_HIP(mbk::launch_bin_data(s, xvd.ptr, vrows, (int)cols, 1, vrows, ed.ptr,
+                                        t.is_cat.ptr, p.num_bins, tile_w, t.sh.num_tiles, vt.ptr,
+                                        t.vbins_fm.ptr));
+            MB_HIP(hipStreamSynchronize(s));
+        }
+        MB_HIP(hipStreamSynchronize(s));
+    }
+    t.t_bin = now_s() - t0;
+
+    // --- persistent buffers ---------------------------------------------
+    t.labels_h.assign(y, y + rows);
+    t.labels.alloc((size_t)rows);
+    t.preds.alloc((size_t)rows);
+    MB_HIP(hipMemcpyAsync(t.labels.ptr, y, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+    if (w) {
+        t.has_weights = true;
+        t.weights.alloc((size_t)rows);
+        MB_HIP(hipMemcpyAsync(t.weights.ptr, w, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+    }
+    t.base = base_score(p, y, w, rows);
+    {
+        uint32_t bits;
+        std::memcpy(&bits, &t.base, 4);
+        MB_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(t.preds.ptr), (int)bits,
+                                 (size_t)rows, s));
+        if (t.has_valid) {
+            t.vlabels_h.assign(yv, yv + vrows);
+            t.vpreds.alloc((size_t)vrows);
+            MB_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(t.vpreds.ptr), (int)bits,
+                                     (size_t)vrows, s));
+        }
+    }
+    t.mono.alloc((size_t)cols);
+    MB_HIP(hipMemcpyAsync(t.mono.ptr, t.mono_h.data(), (size_t)cols, hipMemcpyHostToDevice, s));
+    t.feat_mask.alloc((size_t)cols);
+    MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, t.mask_base.data(), (size_t)cols, hipMemcpyHostToDevice, s));
+
+    t.order_a.alloc((size_t)rows);
+    t.order_b.alloc((size_t)rows);
+    t.dir.alloc((size_t)rows + 16);
+    t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
+    t.block_left.alloc(t.max_blocks + 1);
+
+    // histogram work decomposition
+    const size_t lds = (size_t)tile_w * p.num_bins * 8;
+    int wg_per_cu = (int)std::min<size_t>(2, std::max<size_t>(1, (160 * 1024) / lds));
+    t.hist_grid = t.dev->num_cus * wg_per_cu;
+    t.target_items = 2 * t.hist_grid;
+    t.min_chunk = 2048;
+    const int64_t T = t.sh.num_tiles;
+    int64_t max_items = std::max<int64_t>(t.target_items, T * ((rows + mbk::HIST_CHUNK_MAX - 1) /
+                                                               mbk::HIST_CHUNK_MAX)) +
+                        T * (int64_t)t.max_level_nodes + T;
+    max_items = std::min<int64_t>(max_items, T * ((rows + t.min_chunk - 1) / t.min_chunk +
+                                                  t.max_level_nodes + 1));
+    MB_HIP(mbk::hist_set_lds_limit(tile_w, p.num_bins));
+    t.partials.alloc((size_t)max_items * (size_t)tile_w * (size_t)p.num_bins);
+    t.items.alloc((size_t)max_items);
+    t.pairs.alloc((size_t)t.max_level_nodes);
+    const size_t hist_n = (size_t)t.max_level_nodes * cols * p.num_bins * 2;
+    t.hist_a.alloc(hist_n);
+    t.hist_b.alloc(hist_n);
+    t.results.alloc((size_t)t.max_level_nodes * cols);
+    t.count.alloc((size_t)t.total_nodes);
+    t.node_g.alloc((size_t)t.total_nodes);
+    t.node_h.alloc((size_t)t.total_nodes);
+    t.bounds.alloc((size_t)t.total_nodes);
+    t.seg_a.alloc((size_t)1 << t.D);
+    t.seg_b.alloc((size_t)1 << t.D);
+    t.left_count.alloc((size_t)t.max_level_nodes);
+    t.node_left_prefix.alloc((size_t)t.max_level_nodes);
+    t.scratch.alloc(((size_t)1 << t.D) + 64);
+    t.ctl.alloc(1);
+    t.ensure_capacity(std::max(1, p.num_trees));
+    MB_HIP(hipStreamSynchronize(s));
+    t.best_metric = effective_metric(p) == "auc" ? -INFINITY : INFINITY;
+    return tr.release();
+}
+
+// Per-tree column sample (Booster.swift:1386-1400).
+static const uint8_t *tree_feature_mask(Trainer &t, int tree) {
+    if (!(t.p.feature_fraction < 1.0f)) return nullptr;
+    std::vector<uint8_t> m((size_t)t.cols, 0);
+    uint64_t s = 0xC0150001ULL + (uint64_t)tree * 0x9E3779B97F4A7C15ULL;
+    auto next = [&]() {
+        s += 0x9E3779B97F4A7C15ULL;
+        uint64_t z = s;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        return z ^ (z >> 31);
+    };
+    bool any = false;
+    for (int f = 0; f < t.cols; ++f) {
+        bool keep = t.mask_base[(size_t)f] == 1 &&
+                    (float)(next() >> 40) * (1.0f / 16777216.0f) < t.p.feature_fraction;
+        m[(size_t)f] = keep ? 1 : 0;
+        any = any || keep;
+    }
+    if (!any) {
+        std::vector<int> cand;
+        for (int f = 0; f < t.cols; ++f)
+            if (t.mask_base[(size_t)f] == 1) cand.push_back(f);
+        m[(size_t)cand[(size_t)(next() % cand.size())]] = 1;
+    }
+    t.tree_masks.push_back(std::move(m));
+    return t.tree_masks.back().data();
+}
+
+static void grow_levelwise(Trainer &t, int tree) {
+    hipStream_t s = t.dev->stream;
+    const mbk::Shape &sh = t.sh;
+    mbk::TreeOut out = t.tree_out(tree);
+    if (const uint8_t *m = tree_feature_mask(t, tree))
+        MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
+    mbk::TreeCtl *ctl = t.ctl.ptr;
+    MB_HIP(mbk::launch_tree_init(s, ctl));
+    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl));
+    MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
+                                t.order_a.ptr));
+    MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)t.rows, (uint32_t)t.target_items,
+                                 (uint32_t)t.min_chunk, ctl, t.seg_a.ptr, t.count.ptr, t.pairs.ptr,
+                                 t.items.ptr, out.cover, t.bounds.ptr, -INFINITY, INFINITY,
+                                 t.scratch.ptr));
+    mbk::Entry *ord_cur = t.order_a.ptr, *ord_next = t.order_b.ptr;
+    uint32_t *seg_cur = t.seg_a.ptr, *seg_next = t.seg_b.ptr;
+    int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
+
+    auto hist = [&](const mbk::Entry *ord) {
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (t.profiling) {
+            MB_HIP(hipEventCreate(&e0));
+            MB_HIP(hipEventCreate(&e1));
+            MB_HIP(hipEventRecord(e0, s));
+        }
+        MB_HIP(mbk::launch_hist(s, sh, t.bins_tiled.ptr, ord, t.items.ptr, ctl, t.partials.ptr,
+                                t.hist_grid));
+        if (t.profiling) {
+            MB_HIP(hipEventRecord(e1, s));
+            t.events.emplace_back(e0, e1);
+        }
+    };
+
+    // level 0
+    hist(ord_cur);
+    MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
+                             t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
+                             t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
+    mbk::LevelArgs l0{0, 0, 1, 0};
+    MB_HIP(mbk::launch_decide(s, sh, t.sp, l0, t.results.ptr, t.count.ptr, t.node_g.ptr,
+                              t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.left_count.ptr, out));
+    for (int d = 1; d <= t.D; ++d) {
+        const bool terminal = d == t.D;
+        mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
+        mbk::LevelArgs ln{d, (uint32_t)((1u << d) - 1), 1u << d, terminal ? 1u : 0u};
+        MB_HIP(mbk::launch_route_count(s, sh, lp, t.bins_fm.ptr, ord_cur, seg_cur, out, ctl,
+                                       t.dir.ptr, t.left_count.ptr, t.block_left.ptr,
+                                       t.max_blocks));
+        MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
+                                      ctl, seg_next, t.count.ptr, t.left_count.ptr,
+                                      t.node_left_prefix.ptr, t.block_left.ptr, out, t.pairs.ptr,
+                                      t.items.ptr, t.scratch.ptr));
+        if (terminal)
+            MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
+                                            t.bounds.ptr, ctl, out));
+        MB_HIP(mbk::launch_route_scatter(s, sh, lp, ord_cur, ord_next, t.dir.ptr, seg_cur,
+                                         seg_next, t.node_left_prefix.ptr, t.block_left.ptr, out,
+                                         ctl, t.preds.ptr, t.max_blocks));
+        if (terminal) break;
+        std::swap(ord_cur, ord_next);
+        std::swap(seg_cur, seg_next);
+        std::swap(h_cur, h_prev);
+        hist(ord_cur);
+        MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1u << (d - 1), t.partials.ptr, h_prev,
+                                 h_cur, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
+                                 t.count.ptr, t.node_g.ptr, t.node_h.ptr, ln.level_start,
+                                 t.results.ptr));
+        MB_HIP(mbk::launch_decide(s, sh, t.sp, ln, t.results.ptr, t.count.ptr, t.node_g.ptr,
+                                  t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.left_count.ptr,
+                                  out));
+    }
+    if (t.has_valid)
+        MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
+                                          t.vpreds.ptr));
+    MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
+                          hipMemcpyDeviceToDevice, s));
+}
+
+void trainer_grow(Trainer *tp, int num_trees) {
+    Trainer &t = *tp;
+    hipStream_t s = t.dev->stream;
+    t.ensure_capacity(t.grown + num_trees);
+    const bool metric_each_tree = t.has_valid;
+    std::vector<float> vp;
+    for (int k = 0; k < num_trees && !t.stopped; ++k) {
+        const int tree = t.grown;
+        grow_levelwise(t, tree);
+        t.grown += 1;
+        const int round = t.grown;
+        const bool is_last = k + 1 == num_trees;
+        const bool log_now = t.p.eval_every > 0 && (round % t.p.eval_every == 0 || is_last);
+        if (!metric_each_tree && !log_now) continue;
+        MB_HIP(hipStreamSynchronize(s));
+        std::string line;
+        if (log_now) {
+            std::vector<float> tp_h((size_t)t.rows);
+            MB_HIP(hipMemcpy(tp_h.data(), t.preds.ptr, (size_t)t.rows * 4, hipMemcpyDeviceToHost));
+            char buf[128];
+            std::snprintf(buf, sizeof buf, "[%4d] train-%s: %.5f", round,
+                          effective_metric(t.p).c_str(),
+                          eval_metric(t.p, tp_h.data(), t.labels_h.data(), t.rows));
+            line = buf;
+        }
+        if (t.has_valid) {
+            vp.resize((size_t)t.vrows);
+            MB_HIP(hipMemcpy(vp.data(), t.vpreds.ptr, (size_t)t.vrows * 4, hipMemcpyDeviceToHost));
+            const float vm = eval_metric(t.p, vp.data(), t.vlabels_h.data(), t.vrows);
+            t.eval_history.push_back(vm);
+            const bool higher = effective_metric(t.p) == "auc";
+            if (higher ? vm > t.best_metric : vm < t.best_metric) {
+                t.best_metric = vm;
+                t.best_iter = round;
+                t.stale = 0;
+            } else {
+                t.stale += 1;
+            }
+            if (log_now) {
+                char buf[96];
+                std::snprintf(buf, sizeof buf, "   valid-%s: %.5f", effective_metric(t.p).c_str(), vm);
+                line += buf;
+            }
+            if (t.p.early_stopping_rounds > 0 && t.stale >= t.p.early_stopping_rounds) {
+                if (t.p.verbose && !line.empty()) std::printf("%s\n", line.c_str());
+                if (t.p.verbose)
+                    std::printf("early stopping at iteration %d (best: %d, valid-%s %.5f)\n", round,
+                                t.best_iter, effective_metric(t.p).c_str(), t.best_metric);
+                t.stopped = true;
+                break;
+            }
+        }
+        if (t.p.verbose && !line.empty()) std::printf("%s\n", line.c_str());
+    }
+    MB_HIP(hipStreamSynchronize(s));
+    if (t.profiling) {
+        for (auto &e : t.events) {
+            float ms = 0;
+            MB_HIP(hipEventElapsedTime(&ms, e.first, e.second));
+            t.prof_ms += ms;
+            t.prof_launches += 1;
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        t.events.clear();
+    }
+}
+
+void trainer_profile(Trainer *t, bool enable) {
+    if (enable && !t->profiling) {
+        t->prof_first_tree = t->grown;
+        t->prof_ms = 0;
+        t->prof_launches = 0;
+    }
+    t->profiling = enable;
+}
+
+void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes) {
+    MB_HIP(hipStreamSynchronize(t->dev->stream));
+    const int n = t->grown - t->prof_first_tree;
+    double b = 0;
+    if (n > 0) {
+        std::vector<mbk::TreeCtl> h((size_t)n);
+        MB_HIP(hipMemcpy(h.data(), t->ctl_hist.ptr + t->prof_first_tree, (size_t)n * sizeof(mbk::TreeCtl),
+                         hipMemcpyDeviceToHost));
+        for (auto &c : h)
+            for (int d = 0; d < t->D; ++d) b += (double)c.level_built[d] * (double)(t->cols + 4);
+    }
+    if (launches) *launches = t->prof_launches;
+    if (ms) *ms = t->prof_ms;
+    if (bytes) *bytes = b;
+}
+
+void trainer_setup_seconds(Trainer *t, double *edges_s, double *bin_s) {
+    if (edges_s) *edges_s = t->t_edges;
+    if (bin_s) *bin_s = t->t_bin;
+}
+
+// Read finished trees back (drainPending, Booster.swift:903-948): reachable
+// nodes only, numeric thresholds from the bin edges.
+Booster *trainer_booster(Trainer *tp) {
+    Trainer &t = *tp;
+    MB_HIP(hipStreamSynchronize(t.dev->stream));
+    const int n = t.grown;
+    const size_t tn = (size_t)t.total_nodes;
+    std::vector<mbk::NodeSplit> sp((size_t)n * tn);
+    std::vector<float> leaf((size_t)n * tn), gain((size_t)n * tn), cover((size_t)n * tn);
+    std::vector<uint32_t> mask((size_t)n * tn * 8);
+    if (n > 0) {
+        MB_HIP(hipMemcpy(sp.data(), t.m_split.ptr, sp.size() * sizeof(mbk::NodeSplit), hipMemcpyDeviceToHost));
+        MB_HIP(hipMemcpy(leaf.data(), t.m_leaf.ptr, leaf.size() * 4, hipMemcpyDeviceToHost));
+        MB_HIP(hipMemcpy(gain.data(), t.m_gain.ptr, gain.size() * 4, hipMemcpyDeviceToHost));
+        MB_HIP(hipMemcpy(cover.data(), t.m_cover.ptr, cover.size() * 4, hipMemcpyDeviceToHost));
+        MB_HIP(hipMemcpy(mask.data(), t.m_mask.ptr, mask.size() * 4, hipMemcpyDeviceToHost));
+    }
+    auto b = std::make_unique<Booster>();
+    b->params = t.p;
+    b->num_features = t.cols;
+    b->trained_num_bins = t.nb;
+    b->trained_categorical = t.p.categorical;
+    b->base_score = t.base;
+    b->base_scores = {t.base};
+    b->trained_num_classes = 1;
+    b->warnings = t.warnings;
+    b->eval_history = t.eval_history;
+    const int data_bins = t.nb - 1;
+    int keep = n;
+    if (t.has_valid) {
+        b->best_iteration = t.best_iter;
+        if (t.p.early_stopping_rounds > 0 && keep > t.best_iter) keep = t.best_iter;
+    }
+    b->trees.reserve((size_t)keep);
+    for (int k = 0; k < keep; ++k) {
+        Tree tr;
+        tr.feature.assign(tn, -1);
+        tr.threshold.assign(tn, 0.0f);
+        tr.leaf.assign(tn, 0.0f);
+        tr.flags.assign(tn, 0);
+        if (t.has_cats) tr.cat_mask.assign(tn * 8, 0u);
+        tr.gain.assign(tn, 0.0f);
+        tr.cover.assign(tn, 0.0f);
+        const size_t base_n = (size_t)k * tn;
+        std::vector<int> stack{0};
+        while (!stack.empty()) {
+            int nd = stack.back();
+            stack.pop_back();
+            const mbk::NodeSplit &s = sp[base_n + nd];
+            tr.cover[nd] = cover[base_n + nd];
+            if (s.feature >= 0) {
+                tr.feature[nd] = s.feature;
+                tr.flags[nd] = (uint8_t)s.flags;
+                tr.gain[nd] = gain[base_n + nd];
+                if (s.flags & mbk::FLAG_CATEGORICAL) {
+                    if (t.has_cats)
+                        for (int w = 0; w < 8; ++w)
+                            tr.cat_mask[(size_t)nd * 8 + w] = mask[(base_n + nd) * 8 + w];
+                } else {
+                    tr.threshold[nd] = t.edges[(size_t)s.feature * (data_bins - 1) + s.bin];
+                }
+                stack.push_back(2 * nd + 1);
+                stack.push_back(2 * nd + 2);
+            } else {
+                tr.leaf[nd] = leaf[base_n + nd];
+            }
+        }
+        b->trees.push_back(std::move(tr));
+    }
+    return b.release();
+}
+
+void trainer_free(Trainer *t) { delete t; }
+
+}  // namespace mb

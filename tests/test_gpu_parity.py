@@ -1,0 +1,283 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Integer/byte work (binning, quantisation, histograms) and the whole trained
+model are compared bit for bit; TreeSHAP within 1e-5 relative (+1e-6 abs)
+of the oracle's double-precision recursive TreeSHAP.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import macboost_amd as mb
+import model_io
+import oracle_lib as O
+from macboost_amd import _core
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = mb.Context(0)
+    yield c
+    c.close()
+
+
+def gpu_fit(x_fm, y, params, **kw):
+    h = mb.train(params, x_fm, y, feature_major=True, **kw)
+    obj = model_io.saved_model(h)
+    return h, obj
+
+
+def oracle_fit(x_fm, y, params, is_cat=None):
+    p = dict(params)
+    kw = dict(num_trees=p.pop("num_trees", 100), max_depth=p.pop("max_depth", 6),
+              num_leaves=p.pop("num_leaves", 0), learning_rate=p.pop("learning_rate", 0.1),
+              lam=p.pop("lambda", 1.0), min_child_hess=p.pop("min_child_weight", 1.0),
+              min_split_gain=p.pop("min_split_gain", 0.0), cat_smooth=p.pop("cat_smooth", 10.0))
+    nb = p.pop("num_bins", 256)
+    obj = p.pop("objective", "regression")
+    kw["objective"] = {"regression": O.OBJ_L2, "binary": O.OBJ_LOGISTIC}[obj]
+    mono = p.pop("monotone_constraints", None)
+    p.pop("categorical_features", None)
+    assert not p, p
+    return O.fit_raw(x_fm, y, num_bins=nb, is_cat=is_cat, monotone=mono, **kw)
+
+
+def check_identical(x_fm, y, params, is_cat=None, x_test=None):
+    h, obj = gpu_fit(x_fm, y, params)
+    ref = oracle_fit(x_fm, y, params, is_cat)
+    nodes = ref.forest.nodes_per_tree
+    got = model_io.forest_from_json(obj, nodes)
+    assert np.float32(obj["baseScore"]) == np.float32(ref.base_score)
+    has_cats = is_cat is not None and any(is_cat)
+    model_io.assert_same_forest(got, ref.forest, with_cats=has_cats)
+    # training predictions: GPU predict on the train matrix == oracle's running preds
+    assert np.array_equal(mb.predict(h, x_fm, feature_major=True), ref.preds)
+    if x_test is not None:
+        gp = mb.predict(h, x_test, feature_major=True)
+        cp = O.predict(ref.forest, ref.base_score, ref.num_bins, x_test)
+        assert np.array_equal(gp, cp)
+    return h, ref
+
+
+# --------------------------------------------------------------------------
+# kernel seam (mbk_*)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tile_w", [8, 16, 32, 64])
+def test_bin_data_matches_oracle(ctx, tile_w):
+    rows, cols, nb = 5003, 37, 256
+    x, _ = O.friedman(rows, cols, 3)
+    x[2, ::7] = np.nan
+    x[5] = np.floor(x[5] * 40)
+    is_cat = np.zeros(cols, np.uint8)
+    is_cat[5] = 1
+    e = O.compute_edges(x, nb, is_cat)
+    want = O.bin_matrix(x, e, nb, is_cat)
+    T = (cols + tile_w - 1) // tile_w
+    dx, de, dc = ctx.upload(x), ctx.upload(e), ctx.upload(is_cat)
+    dt, df = ctx.alloc(T * rows * tile_w), ctx.alloc(cols * rows)
+    err = ctypes.c_char_p()
+    rc = _core.lib().mbk_bin_data(ctx.ptr, dx, rows, cols, 1, rows, de, dc, nb, tile_w, dt, df,
+                                  ctypes.byref(err))
+    assert rc == 0, err.value
+    fm = ctx.download(df, (cols, rows), np.uint8)
+    tiled = ctx.download(dt, (T, rows, tile_w), np.uint8)
+    assert np.array_equal(fm, want)
+    for f in range(cols):
+        assert np.array_equal(tiled[f // tile_w, :, f % tile_w], want[f])
+    pad = T * tile_w - cols
+    if pad:
+        assert not tiled[T - 1, :, tile_w - pad:].any()
+
+
+@pytest.mark.parametrize("objective", [O.OBJ_L2, O.OBJ_LOGISTIC])
+def test_quantize_matches_oracle(ctx, objective):
+    rng = np.random.default_rng(9)
+    n = 40_000
+    preds = rng.normal(size=n).astype(np.float32)
+    y = (rng.random(n) < 0.4).astype(np.float32) if objective == O.OBJ_LOGISTIC else \
+        rng.normal(size=n).astype(np.float32)
+    w = rng.random(n).astype(np.float32)
+    g, h, mg, mh = O.gradients(preds, y, w, objective=objective, aux=1.5)
+    want = O.quantize(g, h, mg, mh)
+    dp, dy, dw = ctx.upload(preds), ctx.upload(y), ctx.upload(w)
+    dm, de = ctx.alloc(8), ctx.alloc(8 * n)
+    err = ctypes.c_char_p()
+    rc = _core.lib().mbk_quantize(ctx.ptr, objective, 0.9, 1.5, dp, dy, dw, n, dm, de,
+                                  ctypes.byref(err))
+    assert rc == 0, err.value
+    m = ctx.download(dm, 2, np.uint32)
+    assert m.view(np.float32).tolist() == [mg, mh]
+    ent = ctx.download(de, (n, 2), np.uint32)
+    assert np.array_equal(ent[:, 0], np.arange(n))
+    assert np.array_equal(ent[:, 1], want)
+
+
+@pytest.mark.parametrize("tile_w,nb,n", [(8, 256, 70_000), (32, 64, 150_001), (64, 256, 2500),
+                                         (16, 17, 9000)])
+def test_node_hist_and_splits_match_oracle(ctx, tile_w, nb, n):
+    rng = np.random.default_rng(tile_w + nb)
+    rows, cols = 200_000, 45
+    bins = rng.integers(0, nb, size=(cols, rows)).astype(np.uint8)
+    bins[3, rng.random(rows) < 0.3] = nb - 1              # missing values
+    bins[4] = rng.integers(0, 5, size=rows)               # low-cardinality categorical
+    bins[4, rng.random(rows) < 0.1] = nb - 1
+    is_cat = np.zeros(cols, np.uint8)
+    is_cat[4] = 1
+    mono = np.zeros(cols, np.int8)
+    mono[7], mono[8] = 1, -1
+    qg = rng.integers(-32767, 32768, size=rows)
+    qh = rng.integers(0, 128, size=rows)
+    ghq = (((qg & 0xFFFF).astype(np.uint32) << 16) | qh.astype(np.uint32)).astype(np.uint32)
+    idx = np.sort(rng.choice(rows, n, replace=False)).astype(np.uint32)
+    T = (cols + tile_w - 1) // tile_w
+    tiled = np.zeros((T, rows, tile_w), np.uint8)
+    for f in range(cols):
+        tiled[f // tile_w, :, f % tile_w] = bins[f]
+    ent = np.stack([idx, ghq[idx]], axis=1).astype(np.uint32)
+    max_g, max_h = np.float32(3.5), np.float32(0.25)
+    mgh = np.array([max_g, max_h], np.float32).view(np.uint32)
+    dt, de, dm = ctx.upload(tiled), ctx.upload(ent), ctx.upload(mgh)
+    dc, dmo = ctx.upload(is_cat), ctx.upload(mono)
+    dh = ctx.alloc(cols * nb * 2 * 8)
+    dr = ctx.alloc(cols * 72)
+    err = ctypes.c_char_p()
+    lam, mch, sm = 1.0, 1.0, 10.0
+    rc = _core.lib().mbk_node_hist_split(ctx.ptr, dt, rows, cols, nb, tile_w, de, n, dm, dc, dmo,
+                                         lam, mch, sm, dh, dr, ctypes.byref(err))
+    assert rc == 0, err.value
+    hist = ctx.download(dh, (cols, nb, 2), np.int64)
+    hg, hh = O.hist_node(bins, nb, ghq, idx)
+    assert np.array_equal(hist[:, :, 0], hg) and np.array_equal(hist[:, :, 1], hh)
+    raw = ctx.download(dr, (cols, 72), np.uint8)
+    g_inv, h_inv = np.float32(max_g / np.float32(32767)), np.float32(max_h / np.float32(127))
+    G, H = int(hg[0].sum()), int(hh[0].sum())
+    for f in range(cols):
+        r = O.find_split(hg[f], hh[f], is_cat[f], int(mono[f]), G, H, g_inv, h_inv, lam, mch, sm)
+        gain = raw[f, 0:4].view(np.float32)[0]
+        b, fl = raw[f, 4:8].view(np.uint32)[0], raw[f, 16:20].view(np.uint32)[0]
+        gl, hl = raw[f, 8:12].view(np.float32)[0], raw[f, 12:16].view(np.float32)[0]
+        gli, hli = raw[f, 24:32].view(np.int64)[0], raw[f, 32:40].view(np.int64)[0]
+        assert np.float32(r.gain).tobytes() == gain.tobytes(), f
+        if np.isfinite(r.gain):
+            assert (b, fl, gli, hli) == (r.bin, r.flags, r.gl_int, r.hl_int), f
+            assert gl == np.float32(r.gl) and hl == np.float32(r.hl), f
+            if is_cat[f]:
+                mask = raw[f, 40:72].view(np.uint32)
+                order = O.cat_order(hg[f], hh[f], g_inv, h_inv, sm)
+                want = np.zeros(8, np.uint32)
+                for c in order[: r.bin]:
+                    want[c >> 5] |= np.uint32(1) << np.uint32(c & 31)
+                assert np.array_equal(mask, want), f
+
+
+# --------------------------------------------------------------------------
+# whole fits: identical trees, bit-exact predictions
+# --------------------------------------------------------------------------
+
+def test_c1_friedman_identical_trees_and_bitexact_predict():
+    # 20k x 100 Friedman, max_bin 64, 100 trees, depth 6, lr 0.1;
+    # held-out 20k rows predicted bit-exactly.
+    x, y = mb.friedman(20_000, 100, 42)
+    xt, _ = mb.friedman(20_000, 100, 42 + 999)
+    check_identical(x, y, {"num_trees": 100, "max_depth": 6, "num_bins": 64}, x_test=xt)
+
+
+def test_nan_and_categorical_identical_trees():
+    rows = 30_000
+    x, y = O.friedman(rows, 10, 21)
+    rng = O.SplitMix(22)
+    miss = O.SplitMix(23).uniforms(5 * rows).reshape(5, rows) < 0.2
+    x[:5][miss] = np.nan
+    cat = np.array([rng.next() % 13 for _ in range(rows)], np.float32)
+    cat[::17] = np.nan
+    x = np.vstack([x, cat[None, :]])
+    y = (y + np.where(cat % 4 == 1, 3.0, 0.0)).astype(np.float32)
+    is_cat = [0] * 10 + [1]
+    params = {"num_trees": 30, "max_depth": 6, "num_bins": 256, "categorical_features": [10]}
+    xt = x[:, :5000].copy()
+    xt[10, :50] = 200.0                                   # unseen category -> missing
+    h, ref = check_identical(x, y, params, is_cat=is_cat, x_test=xt)
+    assert (ref.forest.flags & O.FLAG_CATEGORICAL).any()
+    assert (ref.forest.flags & O.FLAG_DEFAULT_LEFT).any()
+
+
+def test_logistic_and_monotone_identical_trees():
+    rows = 20_000
+    rng = O.SplitMix(3)
+    x = rng.uniforms(rows * 4).reshape(4, rows)
+    y = np.array([1.0 if (x[0, i] + x[1, i] + np.float32(0.3) * np.float32(rng.normal())) > 1
+                  else 0.0 for i in range(rows)], np.float32)
+    check_identical(x, y, {"num_trees": 30, "max_depth": 5, "objective": "binary"})
+    xr, yr = O.friedman(15_000, 6, 101)
+    check_identical(xr, yr, {"num_trees": 30, "max_depth": 6,
+                             "monotone_constraints": [0, 0, 0, 1, 0, -1]})
+
+
+def test_reference_known_answers_on_gpu():
+    # MacBoostTests.swift:54-70
+    h, _ = gpu_fit(np.array([[0, 0, 1, 1]], np.float32), np.array([0, 0, 10, 10], np.float32),
+                   {"num_trees": 1, "max_depth": 1, "learning_rate": 0.1, "lambda": 0.0})
+    p = mb.predict(h, np.array([[0, 1]], np.float32), feature_major=True)
+    assert p[0] == pytest.approx(4.5, abs=1e-4) and p[1] == pytest.approx(5.5, abs=1e-4)
+    # FeatureTests.swift:19-38
+    for joins_zero in (True, False):
+        x = np.array([[0.0] * 100 + [1.0] * 100 + [np.nan] * 100], np.float32)
+        y = np.array([10.0] * 100 + [0.0] * 100 + [10.0 if joins_zero else 0.0] * 100, np.float32)
+        h, _ = gpu_fit(x, y, {"num_trees": 30, "max_depth": 1, "learning_rate": 0.3})
+        p = mb.predict(h, np.array([[0.0, 1.0, np.nan]], np.float32), feature_major=True)
+        assert p.tolist() == pytest.approx([10, 0, 10 if joins_zero else 0], abs=0.2)
+    # MacBoostTests.swift:185-211: min_child_weight blocks all splits; constant labels
+    x, y = O.friedman(5000, 6, 6)
+    _, obj = gpu_fit(x, y, {"num_trees": 5, "max_depth": 6, "min_child_weight": 5001.0})
+    assert all(t["feature"][0] == -1 for t in obj["trees"])
+    h, obj = gpu_fit(x, np.full(5000, 3.25, np.float32), {"num_trees": 10, "max_depth": 5})
+    assert np.all(np.abs(mb.predict(h, x, feature_major=True) - 3.25) < 1e-4)
+
+
+def test_depth_extremes_identical():
+    x, y = O.friedman(3000, 5, 221)
+    check_identical(x, y, {"num_trees": 4, "max_depth": 12, "num_bins": 32})
+    check_identical(x, y, {"num_trees": 10, "max_depth": 1, "num_bins": 4})
+
+
+def test_save_load_bitwise(tmp_path):
+    # FeatureTests.swift:307-341
+    x, y = _mixed(8000)
+    h, _ = gpu_fit(x, y, {"num_trees": 20, "max_depth": 5, "categorical_features": [6]})
+    mb.save(h, tmp_path / "m.json")
+    h2 = mb.load(tmp_path / "m.json")
+    assert np.array_equal(mb.predict(h, x, feature_major=True),
+                          mb.predict(h2, x, feature_major=True))
+
+
+# --------------------------------------------------------------------------
+# TreeSHAP
+# --------------------------------------------------------------------------
+
+def _mixed(rows, seed_a=211, seed_b=212, nan_frac=0.15):
+    x, y = O.friedman(rows, 6, seed_a)
+    rng = O.SplitMix(seed_b)
+    nan = O.SplitMix(seed_b + 1).uniforms(rows) < nan_frac
+    x[1, nan] = np.nan
+    cat = np.array([rng.next() % 5 for _ in range(rows)], np.float32)
+    x = np.vstack([x, cat[None, :]])
+    y = (y + np.where(cat == 2, 3.0, 0.0)).astype(np.float32)
+    return x, y
+
+
+@pytest.mark.parametrize("depth", [6, 12])
+def test_treeshap_matches_oracle(depth):
+    # ObjectiveTests.swift:440-478 (tolerance tightened from 5e-3 abs)
+    x, y = _mixed(3000)
+    h, obj = gpu_fit(x, y, {"num_trees": 40 if depth == 6 else 8, "max_depth": depth,
+                            "categorical_features": [6]})
+    c = mb.predict_contrib(h, x, feature_major=True)
+    forest = model_io.forest_from_json(obj)
+    want = O.treeshap(forest, obj["baseScore"], obj["numBins"], x)
+    assert np.allclose(c, want, rtol=1e-5, atol=1e-6)
+    raw = mb.predict(h, x, feature_major=True)
+    assert np.max(np.abs(c.astype(np.float64).sum(axis=1) - raw)) < 1e-4
