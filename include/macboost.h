@@ -111,7 +111,7 @@ typedef struct {
 } mbk_split_result;
 
 /* build_histograms + find_splits for one node (Shaders.swift:212-464): the
- * node's rows are entries[0..n).  hist_out: [cols][num_bins][2] int64
+ * node's rows are entries[0..n).  hist_out: [num_bins][cols][2] int64
  * (gradient sum, hessian sum) of quantised words; results: [cols]. */
 int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t rows,
                         int32_t cols, int32_t num_bins, int32_t tile_width,

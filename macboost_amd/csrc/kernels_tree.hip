@@ -282,69 +282,139 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 
 // ---------------------------------------------------------------------------
 // histograms: packed 64-bit LDS words, one item per (node chunk, tile)
+//
+// Lane f of a wavefront owns feature f of a W-feature tile (64/W rows per
+// instruction, one LDS copy per row slot), and the LDS histogram is laid out
+// [bin][feature]: lane f always lands in banks 2f and 2f+1 whatever the bin,
+// so the per-row ds_add_u64 has no bank conflicts by construction.  Each
+// wavefront gathers 16B (8B for W=8) row-tile slices with coalesced loads,
+// stages them in a private LDS buffer and reads back one byte per lane.
 // ---------------------------------------------------------------------------
 
+constexpr int HIST_THREADS = 1024;
+constexpr int HIST_STAGE_BYTES = 1024;               // per wavefront: one gathered group
+
 template <int W>
-__global__ __launch_bounds__(1024) void k_hist(const uint8_t *__restrict__ tiled,
-                                               const Entry *__restrict__ order,
-                                               const HistItem *__restrict__ items,
-                                               const TreeCtl *ctl, uint64_t *__restrict__ partials,
-                                               int64_t rows, int32_t cols, int32_t nb) {
-    extern __shared__ uint64_t hist_lds[];           // [W][nb]
-    constexpr int BYTES = W >= 16 ? 16 : 8;
-    constexpr int LPR = W / BYTES;                    // lanes per row
+__global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
+                                                       const Entry *__restrict__ order,
+                                                       const HistItem *__restrict__ items,
+                                                       const TreeCtl *ctl,
+                                                       uint64_t *__restrict__ partials,
+                                                       int64_t rows, int32_t cols, int32_t nb) {
+    constexpr int R = 64 / W;                          // rows per atomic instruction
+    constexpr int LOADB = W >= 16 ? 16 : 8;            // bytes per lane per gather load
+    constexpr int LPR = W / LOADB;                     // lanes per row in a gather load
+    constexpr int GROUP = 64 / LPR;                    // rows per gather load (one group)
+    constexpr int NGROUPS = 64 / GROUP;                // gather loads in flight per 64 rows
+    extern __shared__ uint64_t hist_lds[];             // [R][nb][W], then staging
     const int tid = threadIdx.x;
-    const int nthr = blockDim.x;
-    const int words = W * nb;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = HIST_THREADS / 64;
+    const int words = R * nb * W;
+    uint8_t *stage = reinterpret_cast<uint8_t *>(hist_lds + words) + wave * HIST_STAGE_BYTES;
+    const int slot = lane / W, f = lane % W;
+    const int gr = lane / LPR, gq = lane % LPR;        // this lane's row/part in a gather
     const uint32_t nitems = ctl->num_items;
-    const int q = tid % LPR;
-    const int r0 = tid / LPR;
-    const int rstep = nthr / LPR;
     for (uint32_t it = blockIdx.x; it < nitems; it += gridDim.x) {
         const HistItem item = items[it];
         const int nfeat = min(W, cols - (int)item.tile * W);
-        for (int k = tid; k < words; k += nthr) hist_lds[k] = 0;
+        const bool active_lane = f < nfeat;
+        for (int k = tid; k < words; k += HIST_THREADS) hist_lds[k] = 0;
         __syncthreads();
         const uint8_t *tile = tiled + (size_t)item.tile * (size_t)rows * W;
         const Entry *ent = order + item.start;
-        for (uint32_t s = r0; s < item.count; s += rstep) {
-            const Entry e = ent[s];
-            const int32_t qg = (int32_t)(int16_t)(uint16_t)(e.ghq >> 16);
-            const uint64_t v = ((uint64_t)(uint32_t)qg << 32) + (uint64_t)(e.ghq & 0x7Fu);
-            const uint8_t *p = tile + (size_t)e.row * W + q * BYTES;
-            uint32_t wv[BYTES / 4];
-            if constexpr (BYTES == 16) {
-                const uint4 bb = *reinterpret_cast<const uint4 *>(p);
-                wv[0] = bb.x; wv[1] = bb.y; wv[2] = bb.z; wv[3] = bb.w;
-            } else {
-                const uint2 bb = *reinterpret_cast<const uint2 *>(p);
-                wv[0] = bb.x; wv[1] = bb.y;
+        uint64_t *my_hist = hist_lds + (size_t)slot * nb * W;
+        for (uint32_t g0 = (uint32_t)wave * 64; g0 < item.count; g0 += (uint32_t)nwaves * 64) {
+            const uint32_t n_in = min(64u, item.count - g0);
+            // one entry per lane
+            uint32_t row = 0, vlo = 0, vhi = 0;
+            if (lane < (int)n_in) {
+                const Entry e = ent[g0 + lane];
+                row = e.row;
+                const int32_t qg = (int32_t)(int16_t)(uint16_t)(e.ghq >> 16);
+                const uint64_t v = ((uint64_t)(uint32_t)qg << 32) + (uint64_t)(e.ghq & 0x7Fu);
+                vlo = (uint32_t)v;
+                vhi = (uint32_t)(v >> 32);
+            }
+            // all gathers of the 64 rows in flight at once (16B per lane each)
+            uint4 data[NGROUPS];
+#pragma unroll
+            for (int g = 0; g < NGROUPS; ++g) {
+                const int r = g * GROUP + gr;
+                const uint32_t rr = (uint32_t)__shfl((int)row, r, 64);
+                data[g] = make_uint4(0, 0, 0, 0);
+                if (r < (int)n_in) {
+                    const uint8_t *src = tile + (size_t)rr * W + gq * LOADB;
+                    if constexpr (LOADB == 16) {
+                        data[g] = *reinterpret_cast<const uint4 *>(src);
+                    } else {
+                        const uint2 d2 = *reinterpret_cast<const uint2 *>(src);
+                        data[g].x = d2.x; data[g].y = d2.y;
+                    }
+                }
             }
 #pragma unroll
-            for (int k = 0; k < BYTES; ++k) {
-                const int fl = q * BYTES + k;
-                const uint32_t b = (wv[k >> 2] >> (8 * (k & 3))) & 0xFFu;
-                if (fl < nfeat && b < (uint32_t)nb) {
-                    atomicAdd(reinterpret_cast<unsigned long long *>(&hist_lds[fl * nb + b]),
-                              (unsigned long long)v);
+            for (int g = 0; g < NGROUPS; ++g) {
+                // transpose through the wave's staging buffer: row-major bytes in,
+                // one byte per lane (= feature) out
+                if constexpr (LOADB == 16)
+                    *reinterpret_cast<uint4 *>(stage + lane * 16) = data[g];
+                else
+                    *reinterpret_cast<uint2 *>(stage + lane * 8) = make_uint2(data[g].x, data[g].y);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int j = 0; j < GROUP / R; ++j) {
+                    const int rl = j * R + slot;             // row within the group
+                    const int r = g * GROUP + rl;            // row within the 64
+                    uint64_t vr;
+                    if constexpr (R == 1) {
+                        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)vlo, g * GROUP + j);
+                        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)vhi, g * GROUP + j);
+                        vr = ((uint64_t)hi << 32) | lo;
+                    } else {
+                        const uint32_t lo = (uint32_t)__shfl((int)vlo, r, 64);
+                        const uint32_t hi = (uint32_t)__shfl((int)vhi, r, 64);
+                        vr = ((uint64_t)hi << 32) | lo;
+                    }
+                    if (r < (int)n_in && active_lane) {
+                        const uint32_t b = stage[rl * W + f];
+                        if (b < (uint32_t)nb)
+                            atomicAdd(reinterpret_cast<unsigned long long *>(&my_hist[b * W + f]),
+                                      (unsigned long long)vr);
+                    }
                 }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
         }
         __syncthreads();
-        uint64_t *out = partials + (size_t)it * (size_t)words;
-        for (int k = tid; k < words; k += nthr) out[k] = hist_lds[k];
+        // sum the row-slot copies into the item's partial, layout [nb][W]
+        uint64_t *out = partials + (size_t)it * (size_t)(nb * W);
+        for (int k = tid; k < nb * W; k += HIST_THREADS) {
+            uint64_t acc = hist_lds[k];
+#pragma unroll
+            for (int c = 1; c < R; ++c) acc += hist_lds[(size_t)c * nb * W + k];
+            out[k] = acc;
+        }
         __syncthreads();
     }
 }
 
+static size_t hist_lds_bytes(int tile_w, int nb) {
+    (void)tile_w;   // R = 64/W copies of [nb][W] words: 64*nb words for every W
+    return (size_t)64 * (size_t)nb * sizeof(uint64_t) + (size_t)(HIST_THREADS / 64) * HIST_STAGE_BYTES;
+}
+
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, const Entry *order,
                        const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid) {
-    size_t lds = (size_t)sh.tile_w * (size_t)sh.num_bins * sizeof(uint64_t);
+    const size_t lds = hist_lds_bytes(sh.tile_w, sh.num_bins);
     switch (sh.tile_w) {
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
-        hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(1024), lds, s, tiled, order, items, ctl, \
-                           partials, sh.rows, sh.cols, sh.num_bins);                             \
+        hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), lds, s, tiled, order,     \
+                           items, ctl, partials, sh.rows, sh.cols, sh.num_bins);                 \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)
@@ -357,7 +427,7 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
 }
 
 hipError_t hist_set_lds_limit(int tile_w, int num_bins) {
-    int bytes = tile_w * num_bins * (int)sizeof(uint64_t);
+    const int bytes = (int)hist_lds_bytes(tile_w, num_bins);
     hipError_t e = hipSuccess;
     switch (tile_w) {
     case 8: e = hipFuncSetAttribute((const void *)k_hist<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); break;
@@ -367,6 +437,69 @@ hipError_t hist_set_lds_limit(int tile_w, int num_bins) {
     default: return hipErrorInvalidValue;
     }
     return e;
+}
+
+size_t hist_lds_size(int tile_w, int num_bins) { return hist_lds_bytes(tile_w, num_bins); }
+
+// ---------------------------------------------------------------------------
+// partial reduction + sibling subtraction (subtract_histograms, :313-326):
+// one thread per (pair, tile, bin, feature), fully coalesced; histograms are
+// stored [node][bin][feature][g,h] as exact int64.
+// ---------------------------------------------------------------------------
+
+constexpr int REDUCE_SLICES = 4;
+
+__global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict__ pairs,
+                                                const uint64_t *__restrict__ partials,
+                                                const int64_t *__restrict__ hist_prev,
+                                                int64_t *__restrict__ hist_cur, const TreeCtl *ctl,
+                                                uint32_t blocks_per_tile) {
+    __shared__ int64_t red[REDUCE_SLICES][64][2];
+    const int W = sh.tile_w, nb = sh.num_bins, F = sh.cols, T = sh.num_tiles;
+    const uint32_t bpt = blockIdx.x % blocks_per_tile;
+    const uint32_t rest = blockIdx.x / blocks_per_tile;
+    const int tile = (int)(rest % (uint32_t)T);
+    const uint32_t pair_idx = rest / (uint32_t)T;
+    if (pair_idx >= ctl->num_pairs) return;          // uniform per block
+    const int kk = threadIdx.x & 63, slice = threadIdx.x >> 6;
+    const int k = (int)bpt * 64 + kk;                 // (bin, feature) index in the tile
+    const Pair pr = pairs[pair_idx];
+    int64_t g = 0, h = 0;
+    if (k < nb * W) {
+        const size_t stride = (size_t)(nb * W);
+        const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile * pr.nchunks) * stride + k;
+        for (uint32_t c = (uint32_t)slice; c < pr.nchunks; c += REDUCE_SLICES) {
+            const uint64_t w = src[(size_t)c * stride];
+            g += (int64_t)(int32_t)(uint32_t)(w >> 32);
+            h += (int64_t)(uint32_t)w;
+        }
+    }
+    red[slice][kk][0] = g;
+    red[slice][kk][1] = h;
+    __syncthreads();
+    if (slice != 0 || k >= nb * W) return;
+    for (int s2 = 1; s2 < REDUCE_SLICES; ++s2) { g += red[s2][kk][0]; h += red[s2][kk][1]; }
+    const int b = k / W, fl = k % W, f = tile * W + fl;
+    if (f >= F) return;
+    int64_t *hb = hist_cur + (((size_t)pr.built * nb + b) * F + f) * 2;
+    hb[0] = g;
+    hb[1] = h;
+    if (pr.derived != NONE) {
+        const int64_t *hp = hist_prev + (((size_t)pr.parent * nb + b) * F + f) * 2;
+        int64_t *hd = hist_cur + (((size_t)pr.derived * nb + b) * F + f) * 2;
+        hd[0] = hp[0] - g;
+        hd[1] = hp[1] - h;
+    }
+}
+
+hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
+                         const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
+                         const TreeCtl *ctl) {
+    const uint32_t bpt = (uint32_t)((sh.num_bins * sh.tile_w + 63) / 64);
+    const uint32_t grid = max_pairs * (uint32_t)sh.num_tiles * bpt;
+    hipLaunchKernelGGL(k_reduce, dim3(grid), dim3(256), 0, s, sh, pairs, partials, hist_prev,
+                       hist_cur, ctl, bpt);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -565,9 +698,7 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
 
 __global__ __launch_bounds__(64) void k_split(Shape sh, SplitParams sp,
                                               const Pair *__restrict__ pairs,
-                                              const uint64_t *__restrict__ partials,
-                                              const int64_t *__restrict__ hist_prev,
-                                              int64_t *__restrict__ hist_cur,
+                                              const int64_t *__restrict__ hist_cur,
                                               const uint8_t *__restrict__ is_cat,
                                               const int8_t *__restrict__ monotone,
                                               const uint8_t *__restrict__ feat_mask,
@@ -576,85 +707,46 @@ __global__ __launch_bounds__(64) void k_split(Shape sh, SplitParams sp,
                                               uint32_t level_start,
                                               SplitResult *__restrict__ results) {
     __shared__ CatScratch cs;
-    const int F = sh.cols, nb = sh.num_bins, W = sh.tile_w;
+    const int F = sh.cols, nb = sh.num_bins;
     const uint32_t pair_idx = blockIdx.x / (uint32_t)F;
     const int f = (int)(blockIdx.x % (uint32_t)F);
     if (pair_idx >= ctl->num_pairs) return;          // uniform per block (one wave)
     const Pair pr = pairs[pair_idx];
     const int lane = lane_id();
-    const int tile = f / W, fl = f % W;
     const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
     const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
-
-    // built node: reduce its partials for feature f
-    int64_t bg[4] = {0, 0, 0, 0}, bh[4] = {0, 0, 0, 0};
-    for (uint32_t c = 0; c < pr.nchunks; ++c) {
-        const size_t item = (size_t)pr.item_first + (size_t)tile * pr.nchunks + c;
-        const uint64_t *src = partials + (item * (size_t)W + (size_t)fl) * (size_t)nb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = 4 * lane + j;
-            if (b < nb) {
-                const uint64_t w = src[b];
-                bg[j] += (int64_t)(int32_t)(uint32_t)(w >> 32);
-                bh[j] += (int64_t)(uint32_t)w;
-            }
-        }
-    }
-    int64_t *hb = hist_cur + (((size_t)pr.built * F + f) * nb) * 2;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int b = 4 * lane + j;
-        if (b < nb) { hb[2 * b] = bg[j]; hb[2 * b + 1] = bh[j]; }
-    }
     const bool cat = is_cat[f] != 0;
     const int cst = cat ? 0 : (int)monotone[f];
     const bool allowed = feat_mask[f] != 0;
-    const uint32_t nb_abs = level_start + pr.built;
-    if (f == 0) {
-        const int64_t G = wave_sum(bg[0] + bg[1] + bg[2] + bg[3]);
-        const int64_t H = wave_sum(bh[0] + bh[1] + bh[2] + bh[3]);
-        if (lane == 0) { node_g[nb_abs] = G; node_h[nb_abs] = H; }
-    }
-    SplitResult *rb = results + (size_t)pr.built * F + f;
-    if (allowed && count[nb_abs] >= 1) {
-        node_split(bg, bh, nb, cat, cst, g_inv, h_inv, sp, &cs, rb);
-    } else if (lane == 0) {
-        SplitResult r = {};
-        r.gain = -INFINITY;
-        *rb = r;
-    }
-    if (pr.derived == NONE) return;
-
-    // derived sibling = parent - built (exact), Shaders.swift:313-326
-    const int64_t *hp = hist_prev + (((size_t)pr.parent * F + f) * nb) * 2;
-    int64_t dg[4], dh[4];
+    for (int side = 0; side < 2; ++side) {
+        const uint32_t local = side == 0 ? pr.built : pr.derived;
+        if (local == NONE) break;
+        int64_t hg[4], hh[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int b = 4 * lane + j;
-        dg[j] = 0; dh[j] = 0;
-        if (b < nb) { dg[j] = hp[2 * b] - bg[j]; dh[j] = hp[2 * b + 1] - bh[j]; }
-    }
-    int64_t *hd = hist_cur + (((size_t)pr.derived * F + f) * nb) * 2;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int b = 4 * lane + j;
-        if (b < nb) { hd[2 * b] = dg[j]; hd[2 * b + 1] = dh[j]; }
-    }
-    const uint32_t nd_abs = level_start + pr.derived;
-    if (f == 0) {
-        const int64_t G = wave_sum(dg[0] + dg[1] + dg[2] + dg[3]);
-        const int64_t H = wave_sum(dh[0] + dh[1] + dh[2] + dh[3]);
-        if (lane == 0) { node_g[nd_abs] = G; node_h[nd_abs] = H; }
-    }
-    SplitResult *rd = results + (size_t)pr.derived * F + f;
-    __syncthreads();
-    if (allowed && count[nd_abs] >= 1) {
-        node_split(dg, dh, nb, cat, cst, g_inv, h_inv, sp, &cs, rd);
-    } else if (lane == 0) {
-        SplitResult r = {};
-        r.gain = -INFINITY;
-        *rd = r;
+        for (int j = 0; j < 4; ++j) {
+            const int b = 4 * lane + j;
+            hg[j] = 0; hh[j] = 0;
+            if (b < nb) {
+                const int64_t *src = hist_cur + (((size_t)local * nb + b) * F + f) * 2;
+                hg[j] = src[0];
+                hh[j] = src[1];
+            }
+        }
+        const uint32_t abs_n = level_start + local;
+        if (f == 0) {
+            const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
+            const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
+            if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
+        }
+        SplitResult *dst = results + (size_t)local * F + f;
+        __syncthreads();
+        if (allowed && count[abs_n] >= 1) {
+            node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs, dst);
+        } else if (lane == 0) {
+            SplitResult r = {};
+            r.gain = -INFINITY;
+            *dst = r;
+        }
     }
 }
 
@@ -665,9 +757,11 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp, c
                         int64_t *node_g, int64_t *node_h, uint32_t level_start,
                         SplitResult *results) {
     if (sh.num_bins > 256) return hipErrorInvalidValue;
+    hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_split, dim3(max_pairs * (uint32_t)sh.cols), dim3(64), 0, s, sh, sp, pairs,
-                       partials, hist_prev, hist_cur, is_cat, monotone, feat_mask, ctl, count,
-                       node_g, node_h, level_start, results);
+                       hist_cur, is_cat, monotone, feat_mask, ctl, count, node_g, node_h,
+                       level_start, results);
     return hipGetLastError();
 }
 
@@ -685,7 +779,7 @@ __global__ __launch_bounds__(64) void k_decide(Shape sh, SplitParams sp, LevelAr
     const uint32_t n = la.level_start + local;
     const int lane = lane_id();
     const int F = sh.cols;
-    if (lane == 0) left_count[local] = 0;
+    (void)left_count;
     if (count[n] < 1) {
         if (lane == 0) {
             NodeSplit leaf = {-1, 0, 0};
@@ -908,7 +1002,8 @@ hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active
 // Shaders.swift:1454-1488, with counts from the partition).
 __global__ __launch_bounds__(1024) void k_plan_level(
     Shape sh, LevelArgs la, uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
-    uint32_t *seg_start_next, uint32_t *count, const uint32_t *left_count,
+    const uint32_t *seg_start_prev, uint32_t *seg_start_next, uint32_t *count,
+    uint32_t *left_count,
     uint32_t *node_left_prefix, uint32_t *block_left, const TreeOut out, Pair *pairs,
     HistItem *items, uint32_t *scratch) {
     __shared__ uint32_t wave_tot[17];
@@ -918,11 +1013,21 @@ __global__ __launch_bounds__(1024) void k_plan_level(
     const uint32_t active_prev = ctl->level_active[la.level - 1];
     const uint32_t nblk = (active_prev + ROUTE_BLOCK - 1) / ROUTE_BLOCK;
     // 1. block offsets for the scatter's global left scan
-    block_exclusive_scan(block_left, nblk, wave_tot);
-    // 2. per-node exclusive left prefix over level d-1
-    for (uint32_t p = tid; p < num_prev; p += blockDim.x) node_left_prefix[p] = left_count[p];
+    const uint32_t total_left = block_exclusive_scan(block_left, nblk, wave_tot);
+    // 2. global left prefix at each node's segment start, S(a) = offset of a's
+    //    block + lefts before a inside it (left_count holds the latter), and
+    //    each node's left count S(next start) - S(start).
+    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
+        const uint32_t a = seg_start_prev[p];
+        node_left_prefix[p] = a < active_prev ? block_left[a / ROUTE_BLOCK] + left_count[p]
+                                              : total_left;
+    }
     __syncthreads();
-    block_exclusive_scan(node_left_prefix, num_prev, wave_tot);
+    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
+        const uint32_t next = p + 1 < num_prev ? node_left_prefix[p + 1] : total_left;
+        left_count[p] = next - node_left_prefix[p];
+    }
+    __syncthreads();
     // 3. child counts, covers and segment starts
     for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
         const uint32_t n = ls_prev + p;
@@ -977,19 +1082,25 @@ __global__ __launch_bounds__(1024) void k_plan_level(
 
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
-                             uint32_t *seg_start_next, uint32_t *count,
-                             const uint32_t *left_count, uint32_t *node_left_prefix,
+                             const uint32_t *seg_start_prev, uint32_t *seg_start_next,
+                             uint32_t *count, uint32_t *left_count, uint32_t *node_left_prefix,
                              uint32_t *block_left, const TreeOut out, Pair *pairs,
                              HistItem *items, uint32_t *scratch) {
     hipLaunchKernelGGL(k_plan_level, dim3(1), dim3(1024), 0, s, sh, la, target_items, min_chunk,
-                       ctl, seg_start_next, count, left_count, node_left_prefix, block_left, out,
-                       pairs, items, scratch);
+                       ctl, seg_start_prev, seg_start_next, count, left_count, node_left_prefix,
+                       block_left, out, pairs, items, scratch);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // stable row partition: count pass, then scatter pass (route_samples,
-// Shaders.swift:1241-1311, made order-preserving)
+// Shaders.swift:1241-1311, made order-preserving and atomic-free).
+// Block b owns entries [b*2048, b*2048+2048); lane t of pass k handles entry
+// b*2048 + k*256 + t, so every load and store is coalesced.  The count pass
+// records, for every node whose segment starts inside the block, the number
+// of left-going entries of the block before that start; with the scanned
+// per-block totals this gives every node's left count and left prefix
+// without a single global atomic.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ uint32_t owner_of(const uint32_t *seg, uint32_t n, uint32_t s) {
@@ -1002,80 +1113,95 @@ __device__ __forceinline__ uint32_t owner_of(const uint32_t *seg, uint32_t n, ui
     return lo;
 }
 
+constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
+
+// In-block exclusive prefix of `x` in entry order (pass k, then lane order).
+// tot must hold ROUTE_PER_THREAD*ROUTE_WAVES+1 words; on return tot[k*W+w]
+// is the prefix of slice (k, w) and tot[last] the block total.
+__device__ __forceinline__ void route_block_scan(const uint32_t (&x)[ROUTE_PER_THREAD],
+                                                 uint32_t (&ex)[ROUTE_PER_THREAD],
+                                                 uint32_t *tot) {
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
+        const uint32_t inc = wave_inclusive_scan(x[k]);
+        ex[k] = inc - x[k];
+        if (lane_id() == 63) tot[k * ROUTE_WAVES + w] = inc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t acc = 0;
+        for (int i = 0; i < ROUTE_PER_THREAD * ROUTE_WAVES; ++i) {
+            const uint32_t t = tot[i];
+            tot[i] = acc;
+            acc += t;
+        }
+        tot[ROUTE_PER_THREAD * ROUTE_WAVES] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < ROUTE_PER_THREAD; ++k) ex[k] += tot[k * ROUTE_WAVES + w];
+}
+
 // dir: 0 = left child, 1 = right child, 2 = node is a leaf
 __global__ __launch_bounds__(ROUTE_THREADS) void k_route_count(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     const uint32_t *__restrict__ seg_start, const TreeOut out, const TreeCtl *ctl,
-    uint8_t *__restrict__ dir, uint32_t *left_count, uint32_t *block_left) {
-    extern __shared__ uint32_t rc_lds[];             // seg[num_level], cnt[num_level]
+    uint8_t *__restrict__ dir, uint32_t *__restrict__ node_start_prefix,
+    uint32_t *__restrict__ block_left) {
+    extern __shared__ uint32_t rc_lds[];             // seg[num_level]
+    __shared__ uint32_t tot[ROUTE_PER_THREAD * ROUTE_WAVES + 1];
     uint32_t *seg = rc_lds;
-    uint32_t *cnt = rc_lds + la.num_level;
-    __shared__ uint32_t wsum[ROUTE_THREADS / 64];
     const int tid = threadIdx.x;
-    for (uint32_t k = tid; k < la.num_level; k += blockDim.x) { seg[k] = seg_start[k]; cnt[k] = 0; }
+    for (uint32_t k = tid; k < la.num_level; k += blockDim.x) seg[k] = seg_start[k];
     __syncthreads();
     const uint32_t active = ctl->level_active[la.level];
-    const uint32_t base = blockIdx.x * ROUTE_BLOCK + tid * ROUTE_PER_THREAD;
-    uint32_t lefts = 0;
-    uint32_t run_node = 0xFFFFFFFFu, run_cnt = 0;   // this thread's entries are contiguous
-    uint8_t d8[ROUTE_PER_THREAD];
+    const uint32_t base = blockIdx.x * ROUTE_BLOCK + tid;
+    uint32_t x[ROUTE_PER_THREAD], ex[ROUTE_PER_THREAD], loc[ROUTE_PER_THREAD];
 #pragma unroll
     for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k;
-        d8[k] = 2;
+        const uint32_t s = base + k * ROUTE_THREADS;
+        x[k] = 0;
+        loc[k] = 0;
         if (s < active) {
             const uint32_t local = owner_of(seg, la.num_level, s);
             const uint32_t n = la.level_start + local;
             const NodeSplit sp = out.split[n];
+            uint8_t d = 2;
             if (sp.feature >= 0) {
                 const uint32_t row = order_in[s].row;
                 const uint32_t b = bins_fm[(size_t)sp.feature * (size_t)sh.rows + row];
-                const bool left = bin_goes_left(b, sp, sh.num_bins, out.mask + (size_t)n * 8);
-                d8[k] = left ? 0 : 1;
-                if (left) {
-                    ++lefts;
-                    if (local != run_node) {
-                        if (run_cnt) atomicAdd(&cnt[run_node], run_cnt);
-                        run_node = local;
-                        run_cnt = 0;
-                    }
-                    ++run_cnt;
-                }
+                d = bin_goes_left(b, sp, sh.num_bins, out.mask + (size_t)n * 8) ? 0 : 1;
+            }
+            dir[s] = d;
+            x[k] = d == 0 ? 1u : 0u;
+            loc[k] = local;
+        }
+    }
+    route_block_scan(x, ex, tot);
+#pragma unroll
+    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
+        const uint32_t s = base + k * ROUTE_THREADS;
+        if (s < active && seg[loc[k]] == s) {
+            // this entry opens node loc[k] (and any dead nodes sharing the start)
+            for (uint32_t l = loc[k];; --l) {
+                node_start_prefix[l] = ex[k];
+                if (l == 0 || seg[l - 1] != s) break;
             }
         }
     }
-    if (run_cnt) atomicAdd(&cnt[run_node], run_cnt);
-    if (base < active) {
-        if (base + ROUTE_PER_THREAD <= active) {
-            uint2 packed;
-            packed.x = d8[0] | (d8[1] << 8) | (d8[2] << 16) | ((uint32_t)d8[3] << 24);
-            packed.y = d8[4] | (d8[5] << 8) | (d8[6] << 16) | ((uint32_t)d8[7] << 24);
-            *reinterpret_cast<uint2 *>(dir + base) = packed;
-        } else {
-            for (int k = 0; k < ROUTE_PER_THREAD; ++k)
-                if (base + k < active) dir[base + k] = d8[k];
-        }
-    }
-    lefts = wave_sum(lefts);
-    if (lane_id() == 0) wsum[tid >> 6] = lefts;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t t = 0;
-        for (int k = 0; k < ROUTE_THREADS / 64; ++k) t += wsum[k];
-        block_left[blockIdx.x] = t;
-    }
-    for (uint32_t k = tid; k < la.num_level; k += blockDim.x)
-        if (cnt[k]) atomicAdd(&left_count[k], cnt[k]);
+    if (tid == 0) block_left[blockIdx.x] = tot[ROUTE_PER_THREAD * ROUTE_WAVES];
 }
 
 hipError_t launch_route_count(hipStream_t s, const Shape &sh, const LevelArgs &la,
                               const uint8_t *bins_fm, const Entry *order_in,
                               const uint32_t *seg_start, const TreeOut out, const TreeCtl *ctl,
-                              uint8_t *dir, uint32_t *left_count, uint32_t *block_left,
+                              uint8_t *dir, uint32_t *node_start_prefix, uint32_t *block_left,
                               uint32_t max_blocks) {
-    size_t lds = 2 * (size_t)la.num_level * sizeof(uint32_t);
+    size_t lds = (size_t)la.num_level * sizeof(uint32_t);
     hipLaunchKernelGGL(k_route_count, dim3(max_blocks), dim3(ROUTE_THREADS), lds, s, sh, la,
-                       bins_fm, order_in, seg_start, out, ctl, dir, left_count, block_left);
+                       bins_fm, order_in, seg_start, out, ctl, dir, node_start_prefix,
+                       block_left);
     return hipGetLastError();
 }
 
@@ -1086,33 +1212,25 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_scatter(
     const uint32_t *__restrict__ block_off, const TreeOut out, const TreeCtl *ctl,
     float *__restrict__ preds) {
     extern __shared__ uint32_t rs_lds[];             // seg[num_level]
-    __shared__ uint32_t wsum[ROUTE_THREADS / 64 + 1];
+    __shared__ uint32_t tot[ROUTE_PER_THREAD * ROUTE_WAVES + 1];
     uint32_t *seg = rs_lds;
     const int tid = threadIdx.x;
     for (uint32_t k = tid; k < la.num_level; k += blockDim.x) seg[k] = seg_start[k];
     const uint32_t active = ctl->level_active[la.level];
-    const uint32_t base = blockIdx.x * ROUTE_BLOCK + tid * ROUTE_PER_THREAD;
+    const uint32_t base = blockIdx.x * ROUTE_BLOCK + tid;
+    uint32_t x[ROUTE_PER_THREAD], ex[ROUTE_PER_THREAD];
     uint8_t d8[ROUTE_PER_THREAD];
-    uint32_t lefts = 0;
 #pragma unroll
     for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k;
+        const uint32_t s = base + k * ROUTE_THREADS;
         d8[k] = s < active ? dir[s] : 3;
-        lefts += d8[k] == 0 ? 1u : 0u;
+        x[k] = d8[k] == 0 ? 1u : 0u;
     }
-    // block exclusive scan of per-thread left counts
-    const uint32_t inc = wave_inclusive_scan(lefts);
-    if (lane_id() == 63) wsum[tid >> 6] = inc;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t acc = 0;
-        for (int k = 0; k < ROUTE_THREADS / 64; ++k) { uint32_t t = wsum[k]; wsum[k] = acc; acc += t; }
-    }
-    __syncthreads();
-    uint32_t scan_l = block_off[blockIdx.x] + wsum[tid >> 6] + inc - lefts;
+    route_block_scan(x, ex, tot);                    // also orders the seg[] loads
+    const uint32_t boff = block_off[blockIdx.x];
 #pragma unroll
     for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k;
+        const uint32_t s = base + k * ROUTE_THREADS;
         if (d8[k] > 2) continue;
         const uint32_t local = owner_of(seg, la.num_level, s);
         const uint32_t n = la.level_start + local;
@@ -1122,13 +1240,11 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_scatter(
         } else if (la.terminal) {
             preds[e.row] += out.leaf[2 * n + 1 + d8[k]];
         } else {
-            const uint32_t lrank = scan_l - node_left_prefix[local];
-            uint32_t pos;
-            if (d8[k] == 0) pos = seg_start_next[2 * local] + lrank;
-            else pos = seg_start_next[2 * local + 1] + (s - seg[local]) - lrank;
+            const uint32_t lrank = boff + ex[k] - node_left_prefix[local];
+            const uint32_t pos = d8[k] == 0 ? seg_start_next[2 * local] + lrank
+                                            : seg_start_next[2 * local + 1] + (s - seg[local]) - lrank;
             order_out[pos] = e;
         }
-        if (d8[k] == 0) ++scan_l;
     }
 }
 

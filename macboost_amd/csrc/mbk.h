@@ -123,11 +123,13 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order);
 
-// Histogram items -> packed partials [item][W][B].
+// Histogram items -> packed partials [item][B][W] (64-bit words: quantised
+// gradient sum << 32 | hessian sum).
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
                        uint64_t *partials, int grid);
 hipError_t hist_set_lds_limit(int tile_w, int num_bins);
+size_t hist_lds_size(int tile_w, int num_bins);
 
 // Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
 struct LevelArgs {
@@ -145,7 +147,8 @@ struct TreeOut {             // one tree's model arrays (heap layout)
     uint32_t *mask;          // 8 words per node
 };
 
-// Reduce partials, derive siblings, search splits for both nodes of each pair.
+// Reduce partials into hist_cur [node][B][F][g,h] (int64), derive siblings
+// from hist_prev, then search splits for both nodes of each pair.
 hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp,
                         const Pair *pairs, uint32_t max_pairs, const uint64_t *partials,
                         const int64_t *hist_prev, int64_t *hist_cur, const uint8_t *is_cat,
@@ -174,14 +177,14 @@ hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const Level
 hipError_t launch_route_count(hipStream_t s, const Shape &sh, const LevelArgs &la,
                               const uint8_t *bins_fm, const Entry *order_in,
                               const uint32_t *seg_start, const TreeOut out,
-                              const TreeCtl *ctl, uint8_t *dir, uint32_t *left_count,
+                              const TreeCtl *ctl, uint8_t *dir, uint32_t *node_start_prefix,
                               uint32_t *block_left, uint32_t max_blocks);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
-                             uint32_t *seg_start_next, uint32_t *count,
-                             const uint32_t *left_count, uint32_t *node_left_prefix,
+                             const uint32_t *seg_start_prev, uint32_t *seg_start_next,
+                             uint32_t *count, uint32_t *left_count, uint32_t *node_left_prefix,
                              uint32_t *block_left, const TreeOut out, Pair *pairs,
                              HistItem *items, uint32_t *scratch);
 

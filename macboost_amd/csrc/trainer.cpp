@@ -437,9 +437,11 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         for (int64_t f = 0; f < cols; ++f) t.mask_base[(size_t)f] = p.allowed.count((int)f) ? 1 : 0;
 
     // gather-layout tile width: features per row tile
-    int tile_w = 32;
+    // 64 features per tile fills a wavefront (one lane per feature); narrower
+    // matrices use the smallest tile that holds all features.
+    int tile_w = cols > 32 ? 64 : cols > 16 ? 32 : cols > 8 ? 16 : 8;
     if (const char *e = std::getenv("MACBOOST_TILE_W")) tile_w = std::atoi(e);
-    if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) tile_w = 32;
+    if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) tile_w = 64;
     t.sh.rows = rows;
     t.sh.cols = (int)cols;
     t.sh.num_bins = p.num_bins;
@@ -539,10 +541,10 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.block_left.alloc(t.max_blocks + 1);
 
     // histogram work decomposition
-    const size_t lds = (size_t)tile_w * p.num_bins * 8;
+    const size_t lds = mbk::hist_lds_size(tile_w, p.num_bins);
     int wg_per_cu = (int)std::min<size_t>(2, std::max<size_t>(1, (160 * 1024) / lds));
     t.hist_grid = t.dev->num_cus * wg_per_cu;
-    t.target_items = 2 * t.hist_grid;
+    t.target_items = t.hist_grid;
     t.min_chunk = 2048;
     const int64_t T = t.sh.num_tiles;
     int64_t max_items = std::max<int64_t>(t.target_items, T * ((rows + mbk::HIST_CHUNK_MAX - 1) /
@@ -653,7 +655,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                                        t.dir.ptr, t.left_count.ptr, t.block_left.ptr,
                                        t.max_blocks));
         MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
-                                      ctl, seg_next, t.count.ptr, t.left_count.ptr,
+                                      ctl, seg_cur, seg_next, t.count.ptr, t.left_count.ptr,
                                       t.node_left_prefix.ptr, t.block_left.ptr, out, t.pairs.ptr,
                                       t.items.ptr, t.scratch.ptr));
         if (terminal)

@@ -149,9 +149,9 @@ def test_node_hist_and_splits_match_oracle(ctx, tile_w, nb, n):
     rc = _core.lib().mbk_node_hist_split(ctx.ptr, dt, rows, cols, nb, tile_w, de, n, dm, dc, dmo,
                                          lam, mch, sm, dh, dr, ctypes.byref(err))
     assert rc == 0, err.value
-    hist = ctx.download(dh, (cols, nb, 2), np.int64)
+    hist = ctx.download(dh, (nb, cols, 2), np.int64)
     hg, hh = O.hist_node(bins, nb, ghq, idx)
-    assert np.array_equal(hist[:, :, 0], hg) and np.array_equal(hist[:, :, 1], hh)
+    assert np.array_equal(hist[:, :, 0].T, hg) and np.array_equal(hist[:, :, 1].T, hh)
     raw = ctx.download(dr, (cols, 72), np.uint8)
     g_inv, h_inv = np.float32(max_g / np.float32(32767)), np.float32(max_h / np.float32(127))
     G, H = int(hg[0].sum()), int(hh[0].sum())
