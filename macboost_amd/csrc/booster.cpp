@@ -720,11 +720,12 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
             mb::invalid("tile_width must be 8, 16, 32 or 64");
         if (n < 0 || n > 0xFFFFFFF0LL) mb::invalid("row count out of range");
         hipStream_t s = ctx->dev->stream;
-        mbk::Shape sh{rows, cols, num_bins, tile_width, (cols + tile_width - 1) / tile_width};
+        mbk::Shape sh{rows, cols, num_bins, tile_width, (cols + tile_width - 1) / tile_width, 0u, 0u};
         mbk::SplitParams sp{lambda, min_child_hess, 0.0f, cat_smooth, 0.1f, 1};
         const int grid = ctx->dev->num_cus;
         const int64_t T = sh.num_tiles;
         const int64_t max_items = T * ((n + 2047) / 2048 + 2) + 2 * grid;
+        sh.item_cap = (uint32_t)max_items;
         mb::DevBuf<mbk::TreeCtl> ctl(1);
         mb::DevBuf<uint64_t> partials((size_t)max_items * tile_width * num_bins);
         mb::DevBuf<mbk::HistItem> items((size_t)max_items);
@@ -738,7 +739,6 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
         MB_HIP(hipMemsetAsync(cat0.ptr, 0, (size_t)cols, s));
         MB_HIP(hipMemsetAsync(mono0.ptr, 0, (size_t)cols, s));
         MB_HIP(hipMemsetAsync(mask1.ptr, 1, (size_t)cols, s));
-        MB_HIP(mbk::hist_set_lds_limit(tile_width, num_bins));
         MB_HIP(mbk::launch_tree_init(s, ctl.ptr));
         MB_HIP(hipMemcpyAsync(ctl.ptr->max_gh, max_gh, 8, hipMemcpyDeviceToDevice, s));
         MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)n, (uint32_t)(2 * grid), 2048u, ctl.ptr, seg.ptr,
@@ -750,7 +750,10 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
                                  is_cat ? is_cat : cat0.ptr, monotone ? monotone : mono0.ptr,
                                  mask1.ptr, ctl.ptr, count.ptr, node_g.ptr, node_h.ptr, 0,
                                  reinterpret_cast<mbk::SplitResult *>(results)));
+        mbk::TreeCtl c{};
+        MB_HIP(hipMemcpyAsync(&c, ctl.ptr, sizeof c, hipMemcpyDeviceToHost, s));
         MB_HIP(hipStreamSynchronize(s));
+        if (c.overflow) mb::internal("histogram item list overflow");
         return 0;
     }, -1);
 }

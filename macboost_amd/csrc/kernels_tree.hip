@@ -283,16 +283,71 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 // ---------------------------------------------------------------------------
 // histograms: packed 64-bit LDS words, one item per (node chunk, tile)
 //
-// Lane f of a wavefront owns feature f of a W-feature tile (64/W rows per
-// instruction, one LDS copy per row slot), and the LDS histogram is laid out
-// [bin][feature]: lane f always lands in banks 2f and 2f+1 whatever the bin,
-// so the per-row ds_add_u64 has no bank conflicts by construction.  Each
-// wavefront gathers 16B (8B for W=8) row-tile slices with coalesced loads,
-// stages them in a private LDS buffer and reads back one byte per lane.
+// Every lane owns one row of the item and a plane of P = min(W, 32) features
+// of that row (W = 64: two lanes per row, one per 32-feature half; W <= 32:
+// one row per lane).  At step s (0 <= s < P) lane r adds its row's value to
+// feature (r & (P-1)) ^ s of its plane, so the 64 lanes of one ds_add_u64
+// always hit 64 distinct cells, spread evenly over the LDS banks, and the
+// row's packed (qg, qh) word never leaves the lane.  The LDS histogram is two
+// planes of [256 bins][32 columns] u64 (128 KiB); cell (plane, bin, column)
+// sits at byte address plane*65536 + bin*256 + column*8, which one v_perm_b32
+// assembles from the bin byte and a per-lane column word.  Each lane gathers
+// its P bytes with 16B loads whose chunk order, and then dword order, are
+// permuted once per row so that step s reads a fixed register and byte.
+// Columns hold feature c (W = 64: 32*plane + c) or copy c / W of feature
+// c % W (W <= 32), summed when the item is flushed.  Loads are pipelined:
+// data four batches ahead, entries eight.
 // ---------------------------------------------------------------------------
 
 constexpr int HIST_THREADS = 1024;
-constexpr int HIST_STAGE_BYTES = 1024;               // per wavefront: one gathered group
+constexpr int HIST_LDS_BYTES = 2 * 256 * 32 * 8;     // two planes of [256][32] u64, static
+constexpr int HIST_DATA_RING = 4;
+constexpr int HIST_ENTRY_RING = 8;
+
+// P bytes of one row as loaded: 16B chunks in the order (u ^ cx)
+template <int P> struct RowRaw { uint32_t d[P / 4]; };
+
+template <int P>
+__device__ __forceinline__ RowRaw<P> load_row_raw(const uint8_t *src, uint32_t cx) {
+    RowRaw<P> out;
+    if constexpr (P == 8) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(src);
+        out.d[0] = v.x;
+        out.d[1] = v.y;
+    } else {
+#pragma unroll
+        for (int u = 0; u < P / 16; ++u) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(src + 16u * ((uint32_t)u ^ cx));
+            out.d[4 * u + 0] = v.x;
+            out.d[4 * u + 1] = v.y;
+            out.d[4 * u + 2] = v.z;
+            out.d[4 * u + 3] = v.w;
+        }
+    }
+    return out;
+}
+
+// dword order within each 16B chunk permuted by (m & 3): d'[v] = d[v ^ (m & 3)]
+template <int P>
+__device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0, bool b1) {
+    RowRaw<P> out;
+    if constexpr (P == 8) {
+        out.d[0] = b0 ? in.d[1] : in.d[0];
+        out.d[1] = b0 ? in.d[0] : in.d[1];
+    } else {
+#pragma unroll
+        for (int u = 0; u < P / 16; ++u) {
+            const uint32_t *v = in.d + 4 * u;
+            const uint32_t x0 = b0 ? v[1] : v[0], x1 = b0 ? v[0] : v[1];
+            const uint32_t x2 = b0 ? v[3] : v[2], x3 = b0 ? v[2] : v[3];
+            out.d[4 * u + 0] = b1 ? x2 : x0;
+            out.d[4 * u + 1] = b1 ? x3 : x1;
+            out.d[4 * u + 2] = b1 ? x0 : x2;
+            out.d[4 * u + 3] = b1 ? x1 : x3;
+        }
+    }
+    return out;
+}
 
 template <int W>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
@@ -301,119 +356,112 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
                                                        int64_t rows, int32_t cols, int32_t nb) {
-    constexpr int R = 64 / W;                          // rows per atomic instruction
-    constexpr int LOADB = W >= 16 ? 16 : 8;            // bytes per lane per gather load
-    constexpr int LPR = W / LOADB;                     // lanes per row in a gather load
-    constexpr int GROUP = 64 / LPR;                    // rows per gather load (one group)
-    constexpr int NGROUPS = 64 / GROUP;                // gather loads in flight per 64 rows
-    extern __shared__ uint64_t hist_lds[];             // [R][nb][W], then staging
+    (void)cols;
+    constexpr int P = W >= 32 ? 32 : W;              // features per lane
+    constexpr int RPB = W == 64 ? 32 : 64;           // rows per wavefront batch
+    constexpr int DR = HIST_DATA_RING, ER = HIST_ENTRY_RING;
+    __shared__ uint64_t hist_lds[HIST_LDS_BYTES / 8];
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, nwaves = HIST_THREADS / 64;
-    const int words = R * nb * W;
-    uint8_t *stage = reinterpret_cast<uint8_t *>(hist_lds + words) + wave * HIST_STAGE_BYTES;
-    const int slot = lane / W, f = lane % W;
-    const int gr = lane / LPR, gq = lane % LPR;        // this lane's row/part in a gather
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: loop bounds stay uniform
+    const uint32_t nwaves = HIST_THREADS / 64;
+    const uint32_t rl = W == 64 ? (uint32_t)(lane & 31) : (uint32_t)lane;
+    const uint32_t byte_off = W == 64 ? (uint32_t)(lane >> 5) * 32u : 0u;
+    const uint32_t m = ((uint32_t)lane & (uint32_t)(P - 1)) >> 2;
+    const uint32_t cx = P == 32 ? (m >> 2) : 0u;
+    const bool b0 = (m & 1u) != 0, b1 = (m & 2u) != 0;
+    uint32_t colw[P];
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+        colw[s] = ((uint32_t)(lane >> 5) << 16) | ((((uint32_t)lane & 31u) ^ (uint32_t)s) << 3);
+    uint32_t sel[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        sel[t] = 0x0C020000u | ((4u + (((uint32_t)lane & 3u) ^ (uint32_t)t)) << 8);
+    char *lds = reinterpret_cast<char *>(hist_lds);
+    const uint32_t stride = nwaves * RPB;
     const uint32_t nitems = ctl->num_items;
     for (uint32_t it = blockIdx.x; it < nitems; it += gridDim.x) {
         const HistItem item = items[it];
-        const int nfeat = min(W, cols - (int)item.tile * W);
-        const bool active_lane = f < nfeat;
-        for (int k = tid; k < words; k += HIST_THREADS) hist_lds[k] = 0;
+        const uint32_t cnt = item.count;            // >= 1
+        const uint32_t last = cnt - 1;
+        for (int k = tid; k < HIST_LDS_BYTES / 16; k += HIST_THREADS)
+            reinterpret_cast<uint4 *>(hist_lds)[k] = make_uint4(0, 0, 0, 0);
         __syncthreads();
-        const uint8_t *tile = tiled + (size_t)item.tile * (size_t)rows * W;
+        const uint8_t *tile = tiled + (size_t)item.tile * (size_t)rows * W + byte_off;
         const Entry *ent = order + item.start;
-        uint64_t *my_hist = hist_lds + (size_t)slot * nb * W;
-        for (uint32_t g0 = (uint32_t)wave * 64; g0 < item.count; g0 += (uint32_t)nwaves * 64) {
-            const uint32_t n_in = min(64u, item.count - g0);
-            // one entry per lane
-            uint32_t row = 0, vlo = 0, vhi = 0;
-            if (lane < (int)n_in) {
-                const Entry e = ent[g0 + lane];
-                row = e.row;
-                const int32_t qg = (int32_t)(int16_t)(uint16_t)(e.ghq >> 16);
-                const uint64_t v = ((uint64_t)(uint32_t)qg << 32) + (uint64_t)(e.ghq & 0x7Fu);
-                vlo = (uint32_t)v;
-                vhi = (uint32_t)(v >> 32);
+        const uint32_t g0 = (uint32_t)wave * RPB;
+        // loads past the item's end read its last entry (in bounds); their
+        // rows are given value 0 when processed
+        Entry er[ER];
+        RowRaw<P> dr[DR];
+#pragma unroll
+        for (int k = 0; k < ER; ++k) er[k] = ent[min(g0 + (uint32_t)k * stride + rl, last)];
+#pragma unroll
+        for (int k = 0; k < DR; ++k) dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * W, cx);
+        auto process = [&](uint32_t g, const Entry &e, const RowRaw<P> &raw) {
+            // rows past the item's end carry value 0
+            const uint32_t ghq = g + rl < cnt ? e.ghq : 0u;
+            const int32_t qg = (int32_t)(int16_t)(uint16_t)(ghq >> 16);
+            const unsigned long long v =
+                ((unsigned long long)(uint32_t)qg << 32) + (unsigned long long)(ghq & 0x7Fu);
+            const RowRaw<P> cur = permute_dwords<P>(raw, b0, b1);
+#pragma unroll
+            for (int s = 0; s < P; ++s) {
+                const uint32_t addr = __builtin_amdgcn_perm(cur.d[s >> 2], colw[s], sel[s & 3]);
+                atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
             }
-            // all gathers of the 64 rows in flight at once (16B per lane each)
-            uint4 data[NGROUPS];
+        };
+        // main rounds: all ER batches exist, no exits inside the round, so the
+        // refill loads stay where they are issued
+        uint32_t base = g0;
+        for (; base + (uint32_t)(ER - 1) * stride < cnt; base += (uint32_t)ER * stride) {
 #pragma unroll
-            for (int g = 0; g < NGROUPS; ++g) {
-                const int r = g * GROUP + gr;
-                const uint32_t rr = (uint32_t)__shfl((int)row, r, 64);
-                data[g] = make_uint4(0, 0, 0, 0);
-                if (r < (int)n_in) {
-                    const uint8_t *src = tile + (size_t)rr * W + gq * LOADB;
-                    if constexpr (LOADB == 16) {
-                        data[g] = *reinterpret_cast<const uint4 *>(src);
-                    } else {
-                        const uint2 d2 = *reinterpret_cast<const uint2 *>(src);
-                        data[g].x = d2.x; data[g].y = d2.y;
-                    }
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < NGROUPS; ++g) {
-                // transpose through the wave's staging buffer: row-major bytes in,
-                // one byte per lane (= feature) out
-                if constexpr (LOADB == 16)
-                    *reinterpret_cast<uint4 *>(stage + lane * 16) = data[g];
-                else
-                    *reinterpret_cast<uint2 *>(stage + lane * 8) = make_uint2(data[g].x, data[g].y);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-                for (int j = 0; j < GROUP / R; ++j) {
-                    const int rl = j * R + slot;             // row within the group
-                    const int r = g * GROUP + rl;            // row within the 64
-                    uint64_t vr;
-                    if constexpr (R == 1) {
-                        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)vlo, g * GROUP + j);
-                        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)vhi, g * GROUP + j);
-                        vr = ((uint64_t)hi << 32) | lo;
-                    } else {
-                        const uint32_t lo = (uint32_t)__shfl((int)vlo, r, 64);
-                        const uint32_t hi = (uint32_t)__shfl((int)vhi, r, 64);
-                        vr = ((uint64_t)hi << 32) | lo;
-                    }
-                    if (r < (int)n_in && active_lane) {
-                        const uint32_t b = stage[rl * W + f];
-                        if (b < (uint32_t)nb)
-                            atomicAdd(reinterpret_cast<unsigned long long *>(&my_hist[b * W + f]),
-                                      (unsigned long long)vr);
-                    }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int k = 0; k < ER; ++k) {
+                const uint32_t g = base + (uint32_t)k * stride;
+                process(g, er[k], dr[k % DR]);
+                // refill: data for batch +DR (its entry is already held), entry for batch +ER
+                dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * W, cx);
+                er[k] = ent[min(g + (uint32_t)ER * stride + rl, last)];
             }
         }
+        // tail: fewer than ER batches left; entries are held, data up to DR ahead
+#pragma unroll
+        for (int k = 0; k < ER; ++k) {
+            const uint32_t g = base + (uint32_t)k * stride;
+            if (g >= cnt) break;                     // uniform per wavefront
+            process(g, er[k], dr[k % DR]);
+            if (k + DR < ER)
+                dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * W, cx);
+        }
         __syncthreads();
-        // sum the row-slot copies into the item's partial, layout [nb][W]
+        // flush to the item's partial, layout [nb][W]
         uint64_t *out = partials + (size_t)it * (size_t)(nb * W);
         for (int k = tid; k < nb * W; k += HIST_THREADS) {
-            uint64_t acc = hist_lds[k];
+            const int b = k / W, f = k % W;
+            uint64_t acc;
+            if constexpr (W == 64) {
+                acc = hist_lds[(f >> 5) * 8192 + b * 32 + (f & 31)];
+            } else {
+                constexpr int CPP = 32 / W;          // copies per plane
+                acc = 0;
 #pragma unroll
-            for (int c = 1; c < R; ++c) acc += hist_lds[(size_t)c * nb * W + k];
+                for (int c = 0; c < 64 / W; ++c)
+                    acc += hist_lds[(c / CPP) * 8192 + b * 32 + (c % CPP) * W + f];
+            }
             out[k] = acc;
         }
         __syncthreads();
     }
 }
 
-static size_t hist_lds_bytes(int tile_w, int nb) {
-    (void)tile_w;   // R = 64/W copies of [nb][W] words: 64*nb words for every W
-    return (size_t)64 * (size_t)nb * sizeof(uint64_t) + (size_t)(HIST_THREADS / 64) * HIST_STAGE_BYTES;
-}
 
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, const Entry *order,
                        const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid) {
-    const size_t lds = hist_lds_bytes(sh.tile_w, sh.num_bins);
     switch (sh.tile_w) {
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
-        hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), lds, s, tiled, order,     \
+        hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,       \
                            items, ctl, partials, sh.rows, sh.cols, sh.num_bins);                 \
         break;
         MBK_HIST_CASE(8)
@@ -426,20 +474,7 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
     return hipGetLastError();
 }
 
-hipError_t hist_set_lds_limit(int tile_w, int num_bins) {
-    const int bytes = (int)hist_lds_bytes(tile_w, num_bins);
-    hipError_t e = hipSuccess;
-    switch (tile_w) {
-    case 8: e = hipFuncSetAttribute((const void *)k_hist<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); break;
-    case 16: e = hipFuncSetAttribute((const void *)k_hist<16>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); break;
-    case 32: e = hipFuncSetAttribute((const void *)k_hist<32>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); break;
-    case 64: e = hipFuncSetAttribute((const void *)k_hist<64>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); break;
-    default: return hipErrorInvalidValue;
-    }
-    return e;
-}
-
-size_t hist_lds_size(int tile_w, int num_bins) { return hist_lds_bytes(tile_w, num_bins); }
+size_t hist_lds_size() { return (size_t)HIST_LDS_BYTES; }
 
 // ---------------------------------------------------------------------------
 // partial reduction + sibling subtraction (subtract_histograms, :313-326):
@@ -920,7 +955,11 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     __syncthreads();
     if (tid == 0) {
         const uint64_t total = s_total;
-        uint64_t c = (total * (uint64_t)sh.num_tiles + target_items - 1) / (target_items ? target_items : 1);
+        // whole rounds of target_items items, each at most HIST_CHUNK_MAX rows
+        const uint64_t work = total * (uint64_t)sh.num_tiles;
+        const uint64_t tgt = target_items ? target_items : 1;
+        const uint64_t rounds = (work + tgt * HIST_CHUNK_MAX - 1) / (tgt * HIST_CHUNK_MAX);
+        uint64_t c = (work + tgt * (rounds ? rounds : 1) - 1) / (tgt * (rounds ? rounds : 1));
         if (c < min_chunk) c = min_chunk;
         if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
         s_chunk = (uint32_t)c;
@@ -940,6 +979,19 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     }
     __syncthreads();
     const uint32_t total_items = block_exclusive_scan(npair_items, num_pairs, wave_tot);
+    if (total_items > sh.item_cap) {
+        // never write past the item list: the level gets no items and the
+        // host reports the overflow after the tree
+        for (uint32_t k = tid; k < num_pairs; k += blockDim.x) {
+            pairs[k].item_first = 0;
+            pairs[k].nchunks = 0;
+        }
+        if (tid == 0) {
+            ctl->num_items = 0;
+            ctl->overflow = 1;
+        }
+        return;
+    }
     for (uint32_t k = tid; k < num_pairs; k += blockDim.x) pairs[k].item_first = npair_items[k];
     if (tid == 0) ctl->num_items = total_items;
     __syncthreads();

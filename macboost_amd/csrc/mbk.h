@@ -76,6 +76,8 @@ struct Shape {
     int32_t num_bins;    // B (incl. missing bin)
     int32_t tile_w;      // W, features per row tile of the gather layout
     int32_t num_tiles;   // T = ceil(F / W)
+    uint32_t item_cap;   // capacity of the histogram item list and its partials
+    uint32_t pad;
 };
 
 struct SplitParams {
@@ -93,7 +95,8 @@ struct TreeCtl {
     uint32_t num_items;      // histogram items of the current level
     uint32_t num_pairs;      // sibling pairs of the current level
     uint32_t chunk;          // rows per histogram chunk of the current level
-    uint32_t pad[3];
+    uint32_t overflow;       // 1 when a level needed more items than Shape::item_cap
+    uint32_t pad[2];
     uint32_t level_active[16];  // live order entries per level
     uint32_t level_built[16];   // rows of built (histogrammed) nodes per level
 };
@@ -128,8 +131,7 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
                        uint64_t *partials, int grid);
-hipError_t hist_set_lds_limit(int tile_w, int num_bins);
-size_t hist_lds_size(int tile_w, int num_bins);
+size_t hist_lds_size();   // static LDS of one histogram workgroup
 
 // Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
 struct LevelArgs {

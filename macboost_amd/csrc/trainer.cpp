@@ -541,18 +541,19 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.block_left.alloc(t.max_blocks + 1);
 
     // histogram work decomposition
-    const size_t lds = mbk::hist_lds_size(tile_w, p.num_bins);
+    const size_t lds = mbk::hist_lds_size();
     int wg_per_cu = (int)std::min<size_t>(2, std::max<size_t>(1, (160 * 1024) / lds));
     t.hist_grid = t.dev->num_cus * wg_per_cu;
     t.target_items = t.hist_grid;
     t.min_chunk = 2048;
     const int64_t T = t.sh.num_tiles;
-    int64_t max_items = std::max<int64_t>(t.target_items, T * ((rows + mbk::HIST_CHUNK_MAX - 1) /
-                                                               mbk::HIST_CHUNK_MAX)) +
-                        T * (int64_t)t.max_level_nodes + T;
+    // a level's items: T*ceil(count/chunk) summed over its built nodes, at most
+    // target*rounds + T*nodes, where target*rounds <= T*rows/HIST_CHUNK_MAX + target
+    int64_t max_items = T * ((rows + mbk::HIST_CHUNK_MAX - 1) / mbk::HIST_CHUNK_MAX) +
+                        t.target_items + 1 + T * (int64_t)t.max_level_nodes;
     max_items = std::min<int64_t>(max_items, T * ((rows + t.min_chunk - 1) / t.min_chunk +
                                                   t.max_level_nodes + 1));
-    MB_HIP(mbk::hist_set_lds_limit(tile_w, p.num_bins));
+    t.sh.item_cap = (uint32_t)max_items;
     t.partials.alloc((size_t)max_items * (size_t)tile_w * (size_t)p.num_bins);
     t.items.alloc((size_t)max_items);
     t.pairs.alloc((size_t)t.max_level_nodes);
@@ -688,6 +689,7 @@ void trainer_grow(Trainer *tp, int num_trees) {
     Trainer &t = *tp;
     hipStream_t s = t.dev->stream;
     t.ensure_capacity(t.grown + num_trees);
+    const int first_tree = t.grown;
     const bool metric_each_tree = t.has_valid;
     std::vector<float> vp;
     for (int k = 0; k < num_trees && !t.stopped; ++k) {
@@ -739,6 +741,13 @@ void trainer_grow(Trainer *tp, int num_trees) {
         if (t.p.verbose && !line.empty()) std::printf("%s\n", line.c_str());
     }
     MB_HIP(hipStreamSynchronize(s));
+    if (t.grown > first_tree) {
+        std::vector<mbk::TreeCtl> c((size_t)(t.grown - first_tree));
+        MB_HIP(hipMemcpy(c.data(), t.ctl_hist.ptr + first_tree, c.size() * sizeof(mbk::TreeCtl),
+                         hipMemcpyDeviceToHost));
+        for (const auto &e : c)
+            if (e.overflow) internal("histogram item list overflow");
+    }
     if (t.profiling) {
         for (auto &e : t.events) {
             float ms = 0;

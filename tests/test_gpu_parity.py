@@ -174,6 +174,39 @@ def test_node_hist_and_splits_match_oracle(ctx, tile_w, nb, n):
                 assert np.array_equal(mask, want), f
 
 
+def test_node_hist_full_size_exact(ctx):
+    # 26M rows x 100 features (two 64-wide tiles), a node holding 4 of every
+    # 5 rows: more items than one round of the grid, so the level is cut into
+    # several rounds of chunks.  Every feature's bins sum to the node totals
+    # (a checksum of checksums), and features at the tile edges match
+    # numpy's weighted bincount exactly.
+    rows, cols, nb, W = 26_000_000, 100, 256, 64
+    rng = np.random.default_rng(2024)
+    tiled = np.frombuffer(rng.bytes(2 * rows * W), np.uint8).reshape(2, rows, W)
+    idx = np.flatnonzero(np.arange(rows) % 5 != 0).astype(np.uint32)
+    n = idx.size
+    qg = rng.integers(-32767, 32768, size=n)
+    qh = rng.integers(0, 128, size=n)
+    ghq = (((qg & 0xFFFF).astype(np.uint32) << 16) | qh.astype(np.uint32)).astype(np.uint32)
+    ent = np.stack([idx, ghq], axis=1)
+    mgh = np.array([1.0, 1.0], np.float32).view(np.uint32)
+    dt, de, dm = ctx.upload(tiled), ctx.upload(ent), ctx.upload(mgh)
+    del ent
+    dh = ctx.alloc(cols * nb * 2 * 8)
+    dr = ctx.alloc(cols * 72)
+    err = ctypes.c_char_p()
+    rc = _core.lib().mbk_node_hist_split(ctx.ptr, dt, rows, cols, nb, W, de, n, dm, None, None,
+                                         1.0, 1.0, 10.0, dh, dr, ctypes.byref(err))
+    assert rc == 0, err.value
+    hist = ctx.download(dh, (nb, cols, 2), np.int64)
+    assert (hist[:, :, 0].sum(axis=0) == int(qg.sum())).all()
+    assert (hist[:, :, 1].sum(axis=0) == int(qh.sum())).all()
+    for f in (0, 31, 32, 63, 64, 95, 96, 99):
+        b = tiled[f // W, idx, f % W]
+        assert np.array_equal(hist[:, f, 0], np.bincount(b, weights=qg, minlength=nb).astype(np.int64)), f
+        assert np.array_equal(hist[:, f, 1], np.bincount(b, weights=qh, minlength=nb).astype(np.int64)), f
+
+
 # --------------------------------------------------------------------------
 # whole fits: identical trees, bit-exact predictions
 # --------------------------------------------------------------------------
