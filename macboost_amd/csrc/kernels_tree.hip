@@ -114,7 +114,8 @@ __device__ __forceinline__ void row_grad(const GradParams &gp, float f, float y,
 }
 
 // ---------------------------------------------------------------------------
-// binning: raw f32 -> bin bytes, written to both layouts
+// binning: raw f32 -> bin bytes, written to both layouts: the gather layout
+// [rows][T][W] (row r's tile t at (r*T + t)*W) and the feature-major [F][rows]
 // ---------------------------------------------------------------------------
 
 template <int W>
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(256) void k_bin_data(const float *__restrict__ x, i
                 words[k >> 2] |= b << (8 * (k & 3));
             }
         }
-        uint8_t *dst = tiled + ((int64_t)t * rows + i) * W;
+        uint8_t *dst = tiled + (i * (int64_t)gridDim.y + t) * W;
         if constexpr (W >= 16) {
 #pragma unroll
             for (int k = 0; k < W / 16; ++k)
@@ -355,8 +356,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                                                        const HistItem *__restrict__ items,
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
-                                                       int64_t rows, int32_t cols, int32_t nb) {
-    (void)cols;
+                                                       int32_t num_tiles, int32_t nb) {
     constexpr int P = W >= 32 ? 32 : W;              // features per lane
     constexpr int RPB = W == 64 ? 32 : 64;           // rows per wavefront batch
     constexpr int DR = HIST_DATA_RING, ER = HIST_ENTRY_RING;
@@ -380,15 +380,25 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         sel[t] = 0x0C020000u | ((4u + (((uint32_t)lane & 3u) ^ (uint32_t)t)) << 8);
     char *lds = reinterpret_cast<char *>(hist_lds);
     const uint32_t stride = nwaves * RPB;
+    const size_t row_bytes = (size_t)num_tiles * W;
     const uint32_t nitems = ctl->num_items;
-    for (uint32_t it = blockIdx.x; it < nitems; it += gridDim.x) {
+    // Items are chunk-major (the tiles of one row chunk are adjacent).  With
+    // workgroups dispatched round-robin over 8 XCDs, block b = 16q + 8h + x
+    // runs on XCD x and takes item 16q + 2x + h, so both tiles of a chunk read
+    // the same 128B row lines through one L2.
+    uint32_t slot = blockIdx.x;
+    if ((gridDim.x & 15u) == 0) {
+        const uint32_t q = blockIdx.x >> 4, h = (blockIdx.x >> 3) & 1u, x = blockIdx.x & 7u;
+        slot = (q << 4) + (x << 1) + h;
+    }
+    for (uint32_t it = slot; it < nitems; it += gridDim.x) {
         const HistItem item = items[it];
         const uint32_t cnt = item.count;            // >= 1
         const uint32_t last = cnt - 1;
         for (int k = tid; k < HIST_LDS_BYTES / 16; k += HIST_THREADS)
             reinterpret_cast<uint4 *>(hist_lds)[k] = make_uint4(0, 0, 0, 0);
         __syncthreads();
-        const uint8_t *tile = tiled + (size_t)item.tile * (size_t)rows * W + byte_off;
+        const uint8_t *tile = tiled + (size_t)item.tile * W + byte_off;
         const Entry *ent = order + item.start;
         const uint32_t g0 = (uint32_t)wave * RPB;
         // loads past the item's end read its last entry (in bounds); their
@@ -398,7 +408,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 #pragma unroll
         for (int k = 0; k < ER; ++k) er[k] = ent[min(g0 + (uint32_t)k * stride + rl, last)];
 #pragma unroll
-        for (int k = 0; k < DR; ++k) dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * W, cx);
+        for (int k = 0; k < DR; ++k) dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * row_bytes, cx);
         auto process = [&](uint32_t g, const Entry &e, const RowRaw<P> &raw) {
             // rows past the item's end carry value 0
             const uint32_t ghq = g + rl < cnt ? e.ghq : 0u;
@@ -421,7 +431,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                 const uint32_t g = base + (uint32_t)k * stride;
                 process(g, er[k], dr[k % DR]);
                 // refill: data for batch +DR (its entry is already held), entry for batch +ER
-                dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * W, cx);
+                dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * row_bytes, cx);
                 er[k] = ent[min(g + (uint32_t)ER * stride + rl, last)];
             }
         }
@@ -432,7 +442,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
             if (g >= cnt) break;                     // uniform per wavefront
             process(g, er[k], dr[k % DR]);
             if (k + DR < ER)
-                dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * W, cx);
+                dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * row_bytes, cx);
         }
         __syncthreads();
         // flush to the item's partial, layout [nb][W]
@@ -462,7 +472,7 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
         hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,       \
-                           items, ctl, partials, sh.rows, sh.cols, sh.num_bins);                 \
+                           items, ctl, partials, sh.num_tiles, sh.num_bins);                 \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)
@@ -502,9 +512,9 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
     int64_t g = 0, h = 0;
     if (k < nb * W) {
         const size_t stride = (size_t)(nb * W);
-        const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile * pr.nchunks) * stride + k;
+        const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile) * stride + k;
         for (uint32_t c = (uint32_t)slice; c < pr.nchunks; c += REDUCE_SLICES) {
-            const uint64_t w = src[(size_t)c * stride];
+            const uint64_t w = src[(size_t)c * (size_t)T * stride];
             g += (int64_t)(int32_t)(uint32_t)(w >> 32);
             h += (int64_t)(uint32_t)w;
         }
@@ -1004,7 +1014,7 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         }
         const Pair pr = pairs[lo];
         const uint32_t rel = it - pr.item_first;
-        const uint32_t t = rel / pr.nchunks, c = rel % pr.nchunks;
+        const uint32_t t = rel % (uint32_t)sh.num_tiles, c = rel / (uint32_t)sh.num_tiles;
         const uint32_t cnt = count_level[pr.built];
         HistItem h;
         h.pair = lo;

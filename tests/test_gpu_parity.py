@@ -84,13 +84,13 @@ def test_bin_data_matches_oracle(ctx, tile_w):
                                   ctypes.byref(err))
     assert rc == 0, err.value
     fm = ctx.download(df, (cols, rows), np.uint8)
-    tiled = ctx.download(dt, (T, rows, tile_w), np.uint8)
+    tiled = ctx.download(dt, (rows, T, tile_w), np.uint8)
     assert np.array_equal(fm, want)
     for f in range(cols):
-        assert np.array_equal(tiled[f // tile_w, :, f % tile_w], want[f])
+        assert np.array_equal(tiled[:, f // tile_w, f % tile_w], want[f])
     pad = T * tile_w - cols
     if pad:
-        assert not tiled[T - 1, :, tile_w - pad:].any()
+        assert not tiled[:, T - 1, tile_w - pad:].any()
 
 
 @pytest.mark.parametrize("objective", [O.OBJ_L2, O.OBJ_LOGISTIC])
@@ -134,9 +134,9 @@ def test_node_hist_and_splits_match_oracle(ctx, tile_w, nb, n):
     ghq = (((qg & 0xFFFF).astype(np.uint32) << 16) | qh.astype(np.uint32)).astype(np.uint32)
     idx = np.sort(rng.choice(rows, n, replace=False)).astype(np.uint32)
     T = (cols + tile_w - 1) // tile_w
-    tiled = np.zeros((T, rows, tile_w), np.uint8)
+    tiled = np.zeros((rows, T, tile_w), np.uint8)
     for f in range(cols):
-        tiled[f // tile_w, :, f % tile_w] = bins[f]
+        tiled[:, f // tile_w, f % tile_w] = bins[f]
     ent = np.stack([idx, ghq[idx]], axis=1).astype(np.uint32)
     max_g, max_h = np.float32(3.5), np.float32(0.25)
     mgh = np.array([max_g, max_h], np.float32).view(np.uint32)
@@ -182,7 +182,7 @@ def test_node_hist_full_size_exact(ctx):
     # numpy's weighted bincount exactly.
     rows, cols, nb, W = 26_000_000, 100, 256, 64
     rng = np.random.default_rng(2024)
-    tiled = np.frombuffer(rng.bytes(2 * rows * W), np.uint8).reshape(2, rows, W)
+    tiled = np.frombuffer(rng.bytes(2 * rows * W), np.uint8).reshape(rows, 2, W)
     idx = np.flatnonzero(np.arange(rows) % 5 != 0).astype(np.uint32)
     n = idx.size
     qg = rng.integers(-32767, 32768, size=n)
@@ -202,7 +202,7 @@ def test_node_hist_full_size_exact(ctx):
     assert (hist[:, :, 0].sum(axis=0) == int(qg.sum())).all()
     assert (hist[:, :, 1].sum(axis=0) == int(qh.sum())).all()
     for f in (0, 31, 32, 63, 64, 95, 96, 99):
-        b = tiled[f // W, idx, f % W]
+        b = tiled[idx, f // W, f % W]
         assert np.array_equal(hist[:, f, 0], np.bincount(b, weights=qg, minlength=nb).astype(np.int64)), f
         assert np.array_equal(hist[:, f, 1], np.bincount(b, weights=qh, minlength=nb).astype(np.int64)), f
 
