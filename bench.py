@@ -85,6 +85,7 @@ def main():
     tr.grow(args.steps)
     elapsed = time.perf_counter() - t0
     launches, hist_ms, hist_bytes = tr.hist_stats()
+    built, active, level_ms = tr.level_stats(6)
     value = args.steps / elapsed
     log(f"{args.steps} trees in {elapsed:.3f}s = {value:.1f} trees/s; hist {launches} launches "
         f"{hist_ms:.1f} ms")
@@ -98,12 +99,24 @@ def main():
 
     achieved = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms > 0 else None
     per_launch_bytes = hist_bytes / launches if launches else None
+    traffic = None
+    tfile = ROOT / "profiles" / "k_hist_traffic_friedman10m.json"
+    if tfile.exists():
+        # HBM bytes per k_hist launch from the committed rocprofv3 --pmc summary
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     roofline = {
         "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": None,
+        "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": traffic,
         "kernel": "k_hist", "launches": launches, "avg_launch_ms": hist_ms / launches if launches else None,
         "algorithmic_bytes_per_launch": per_launch_bytes,
+        "levels": [{"level": d, "built_rows_per_tree": float(built[d]) / args.steps,
+                    "ms_per_tree": float(level_ms[d]) / args.steps,
+                    "GB/s": (float(built[d]) * (cols + 4) / (level_ms[d] / 1e3) / 1e9
+                             if level_ms[d] > 0 else None)} for d in range(6)],
     }
+    for lv in roofline["levels"]:
+        log(f"level {lv['level']}: {lv['built_rows_per_tree']:.0f} rows/tree, "
+            f"{lv['ms_per_tree'] * 1e3:.1f} us/tree, {lv['GB/s'] or 0:.0f} GB/s")
     cpu = None
     if not args.no_cpu:
         cr = min(args.cpu_rows, rows)

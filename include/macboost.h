@@ -146,6 +146,11 @@ int mbx_trainer_profile(void *trainer, int32_t enable, char **err);
  * milliseconds, and algorithmic bytes (sum over built nodes of rows*(cols+4)). */
 int mbx_trainer_hist_stats(void *trainer, int64_t *launches, double *ms, double *bytes,
                            char **err);
+/* Per-level sums over the trees grown since profiling was enabled: rows of
+ * built (histogrammed) nodes, live rows, and histogram-kernel milliseconds,
+ * levels 0..max_levels-1 (16 at most carry data).  Any output may be NULL. */
+int mbx_trainer_level_stats(void *trainer, int32_t max_levels, int64_t *built, int64_t *active,
+                            double *hist_ms, char **err);
 /* Wall-clock seconds of the last mbx_trainer_create phases: edges (host),
  * upload + device binning. */
 int mbx_trainer_setup_seconds(void *trainer, double *edges_s, double *bin_s);

@@ -125,6 +125,8 @@ def _configure(l):
     l.mbx_trainer_hist_stats.argtypes = [_P, ctypes.POINTER(ctypes.c_int64),
                                          ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(ctypes.c_double), _c_char_pp]
+    l.mbx_trainer_level_stats.restype = ctypes.c_int
+    l.mbx_trainer_level_stats.argtypes = [_P, ctypes.c_int32, _P, _P, _P, _c_char_pp]
     l.mbx_trainer_setup_seconds.restype = ctypes.c_int
     l.mbx_trainer_setup_seconds.argtypes = [_P, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_double)]
@@ -148,7 +150,7 @@ EXPORTED = (
     "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_bin_data", "mbk_quantize",
     "mbk_node_hist_split", "mbk_predict_forest",
     "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
-    "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
+    "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
     "mbx_version",
 )
 
@@ -339,6 +341,18 @@ class Trainer:
                                         ctypes.byref(b), ctypes.byref(err)) != 0:
             raise MacBoostError(_take_error(err))
         return int(n.value), float(ms.value), float(b.value)
+
+    def level_stats(self, levels: int):
+        """Per-level (built rows, live rows, histogram ms) summed over the
+        profiled trees."""
+        built = np.zeros(levels, np.int64)
+        active = np.zeros(levels, np.int64)
+        ms = np.zeros(levels, np.float64)
+        err = ctypes.c_char_p()
+        if lib().mbx_trainer_level_stats(self.ptr, levels, built.ctypes.data, active.ctypes.data,
+                                         ms.ctypes.data, ctypes.byref(err)) != 0:
+            raise MacBoostError(_take_error(err))
+        return built, active, ms
 
     def setup_seconds(self):
         e = ctypes.c_double()

@@ -807,6 +807,16 @@ int mbx_trainer_hist_stats(void *trainer, int64_t *launches, double *ms, double 
     }, -1);
 }
 
+int mbx_trainer_level_stats(void *trainer, int32_t max_levels, int64_t *built, int64_t *active,
+                            double *hist_ms, char **err) {
+    if (!trainer || max_levels < 0) { set_err(err, "null argument"); return -1; }
+    return guarded(err, [&]() -> int {
+        mb::trainer_level_stats(static_cast<mb::Trainer *>(trainer), max_levels, built, active,
+                                hist_ms);
+        return 0;
+    }, -1);
+}
+
 int mbx_trainer_setup_seconds(void *trainer, double *edges_s, double *bin_s) {
     if (!trainer) return -1;
     mb::trainer_setup_seconds(static_cast<mb::Trainer *>(trainer), edges_s, bin_s);

@@ -170,6 +170,8 @@ Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t c
 void trainer_grow(Trainer *t, int num_trees);
 void trainer_profile(Trainer *t, bool enable);
 void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes);
+void trainer_level_stats(Trainer *t, int32_t max_levels, int64_t *built, int64_t *active,
+                         double *hist_ms);
 void trainer_setup_seconds(Trainer *t, double *edges_s, double *bin_s);
 Booster *trainer_booster(Trainer *t);
 void trainer_free(Trainer *t);

@@ -965,11 +965,16 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     __syncthreads();
     if (tid == 0) {
         const uint64_t total = s_total;
-        // whole rounds of target_items items, each at most HIST_CHUNK_MAX rows
+        // At most r items per workgroup of the grid (target_items): every
+        // (pair, tile) adds at most one partial chunk, so reserve that slack
+        // (T * pairs) and pick the smallest r whose chunk fits HIST_CHUNK_MAX.
         const uint64_t work = total * (uint64_t)sh.num_tiles;
         const uint64_t tgt = target_items ? target_items : 1;
-        const uint64_t rounds = (work + tgt * HIST_CHUNK_MAX - 1) / (tgt * HIST_CHUNK_MAX);
-        uint64_t c = (work + tgt * (rounds ? rounds : 1) - 1) / (tgt * (rounds ? rounds : 1));
+        const uint64_t slack = (uint64_t)num_pairs * (uint64_t)sh.num_tiles;
+        const uint64_t need = (work + HIST_CHUNK_MAX - 1) / HIST_CHUNK_MAX;
+        uint64_t r = (slack + need + tgt - 1) / tgt;
+        if (tgt * r <= slack) r = slack / tgt + 1;
+        uint64_t c = (work + (tgt * r - slack) - 1) / (tgt * r - slack);
         if (c < min_chunk) c = min_chunk;
         if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
         s_chunk = (uint32_t)c;

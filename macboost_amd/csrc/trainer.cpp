@@ -150,9 +150,11 @@ struct Trainer {
 
     bool profiling = false;
     int prof_first_tree = 0;
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+    struct HistEvent { hipEvent_t start, end; int level; };
+    std::vector<HistEvent> events;
     int64_t prof_launches = 0;
     double prof_ms = 0.0;
+    double prof_level_ms[16] = {};
 
     // metrics / early stopping (Booster.swift:1650-1696)
     int best_iter = 0;
@@ -164,7 +166,7 @@ struct Trainer {
     double t_edges = 0.0, t_bin = 0.0;
 
     ~Trainer() {
-        for (auto &e : events) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
+        for (auto &e : events) { (void)hipEventDestroy(e.start); (void)hipEventDestroy(e.end); }
     }
 
     mbk::TreeOut tree_out(int t) {
@@ -625,7 +627,7 @@ static void grow_levelwise(Trainer &t, int tree) {
     uint32_t *seg_cur = t.seg_a.ptr, *seg_next = t.seg_b.ptr;
     int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
 
-    auto hist = [&](const mbk::Entry *ord) {
+    auto hist = [&](const mbk::Entry *ord, int level) {
         hipEvent_t e0 = nullptr, e1 = nullptr;
         if (t.profiling) {
             MB_HIP(hipEventCreate(&e0));
@@ -636,12 +638,12 @@ static void grow_levelwise(Trainer &t, int tree) {
                                 t.hist_grid));
         if (t.profiling) {
             MB_HIP(hipEventRecord(e1, s));
-            t.events.emplace_back(e0, e1);
+            t.events.push_back({e0, e1, level});
         }
     };
 
     // level 0
-    hist(ord_cur);
+    hist(ord_cur, 0);
     MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
                              t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
                              t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
@@ -669,7 +671,7 @@ static void grow_levelwise(Trainer &t, int tree) {
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
-        hist(ord_cur);
+        hist(ord_cur, d);
         MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1u << (d - 1), t.partials.ptr, h_prev,
                                  h_cur, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
                                  t.count.ptr, t.node_g.ptr, t.node_h.ptr, ln.level_start,
@@ -751,11 +753,12 @@ void trainer_grow(Trainer *tp, int num_trees) {
     if (t.profiling) {
         for (auto &e : t.events) {
             float ms = 0;
-            MB_HIP(hipEventElapsedTime(&ms, e.first, e.second));
+            MB_HIP(hipEventElapsedTime(&ms, e.start, e.end));
             t.prof_ms += ms;
+            t.prof_level_ms[e.level & 15] += ms;
             t.prof_launches += 1;
-            (void)hipEventDestroy(e.first);
-            (void)hipEventDestroy(e.second);
+            (void)hipEventDestroy(e.start);
+            (void)hipEventDestroy(e.end);
         }
         t.events.clear();
     }
@@ -766,6 +769,7 @@ void trainer_profile(Trainer *t, bool enable) {
         t->prof_first_tree = t->grown;
         t->prof_ms = 0;
         t->prof_launches = 0;
+        for (double &v : t->prof_level_ms) v = 0;
     }
     t->profiling = enable;
 }
@@ -784,6 +788,27 @@ void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes
     if (launches) *launches = t->prof_launches;
     if (ms) *ms = t->prof_ms;
     if (bytes) *bytes = b;
+}
+
+void trainer_level_stats(Trainer *t, int32_t max_levels, int64_t *built, int64_t *active,
+                         double *hist_ms) {
+    MB_HIP(hipStreamSynchronize(t->dev->stream));
+    const int n = t->grown - t->prof_first_tree;
+    for (int d = 0; d < max_levels; ++d) {
+        if (built) built[d] = 0;
+        if (active) active[d] = 0;
+        if (hist_ms) hist_ms[d] = d < 16 ? t->prof_level_ms[d] : 0.0;
+    }
+    if (n <= 0) return;
+    std::vector<mbk::TreeCtl> h((size_t)n);
+    MB_HIP(hipMemcpy(h.data(), t->ctl_hist.ptr + t->prof_first_tree, (size_t)n * sizeof(mbk::TreeCtl),
+                     hipMemcpyDeviceToHost));
+    const int L = std::min<int>(max_levels, 16);
+    for (auto &c : h)
+        for (int d = 0; d < L; ++d) {
+            if (built) built[d] += c.level_built[d];
+            if (active) active[d] += c.level_active[d];
+        }
 }
 
 void trainer_setup_seconds(Trainer *t, double *edges_s, double *bin_s) {
