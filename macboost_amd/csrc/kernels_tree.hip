@@ -947,11 +947,12 @@ __device__ uint32_t block_exclusive_scan(uint32_t *v, uint32_t n, uint32_t *wave
     return carry;
 }
 
+// level_built[level] records the built rows (added to, when accumulate).
 __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pairs,
                             HistItem *items, const uint32_t *seg_start,
                             const uint32_t *count_level, uint32_t num_pairs,
                             uint32_t target_items, uint32_t min_chunk, uint32_t *scratch,
-                            uint32_t *wave_tot) {
+                            uint32_t *wave_tot, bool accumulate = false) {
     __shared__ uint32_t s_chunk;
     __shared__ uint32_t s_total;
     const int tid = threadIdx.x;
@@ -979,7 +980,8 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
         s_chunk = (uint32_t)c;
         ctl->chunk = (uint32_t)c;
-        ctl->level_built[level] = (uint32_t)total;
+        if (accumulate) ctl->level_built[level] += (uint32_t)total;
+        else ctl->level_built[level] = (uint32_t)total;
         scratch[0] = 0;
     }
     __syncthreads();
@@ -1325,6 +1327,392 @@ hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs 
     hipLaunchKernelGGL(k_route_scatter, dim3(max_blocks), dim3(ROUTE_THREADS), lds, s, sh, la,
                        order_in, order_out, dir, seg_start, seg_start_next, node_left_prefix,
                        block_off, out, ctl, preds);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// leaf-wise (best-first) growth: leaf_init (:683-716), leaf_pick_apply
+// (:720-871), leaf_step (:879-1091) and the stable segment partition
+// (partition_count/scan/scatter, :520-620).  Every step is a fixed chain of
+// launches that read the device state; once the tree is finished the chain
+// early-outs, so the host never waits inside a tree.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float lw_leaf_value(const SplitParams &sp, int64_t g, int64_t h,
+                                               float g_inv, float h_inv, float lo, float hi) {
+    const float G = (float)g * g_inv, H = (float)h * h_inv;
+    return sp.learning_rate * clampf(-G / (H + sp.lambda), lo, hi);
+}
+
+__global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *ctl, LWState *st,
+                                                  LWOpen *open, uint32_t *slot_seg,
+                                                  uint32_t *slot_count, Pair *pairs,
+                                                  HistItem *items, uint32_t *scratch,
+                                                  TreeOut out) {
+    __shared__ uint32_t wave_tot[17];
+    const int tid = threadIdx.x;
+    for (int n = tid; n < a.total_nodes; n += blockDim.x) {
+        const NodeSplit leaf = {-1, 0, 0};
+        out.split[n] = leaf;
+        out.leaf[n] = 0.0f;
+        out.gain[n] = 0.0f;
+        out.cover[n] = 0.0f;
+    }
+    for (int k = tid; k < a.total_nodes * 8; k += blockDim.x) out.mask[k] = 0u;
+    if (tid == 0) {
+        LWState s = {};
+        s.leaves = 1;
+        s.open_count = 1;
+        s.next_slot = 1;
+        s.eval_first = 0;
+        s.eval_count = 1;
+        *st = s;
+        LWOpen o = {};
+        o.node = 0;
+        o.seg = 0;
+        o.count = a.rows;
+        o.depth = 0;
+        o.slot = 0;
+        o.best_f = -1;
+        o.lo = -INFINITY;
+        o.hi = INFINITY;
+        o.best.gain = -INFINITY;
+        open[0] = o;
+        slot_seg[0] = 0;
+        slot_count[0] = a.rows;
+        Pair p = {};
+        p.built = 0; p.derived = NONE; p.parent = NONE;
+        pairs[0] = p;
+        ctl->num_pairs = 1;
+        ctl->level_active[0] = a.rows;
+        out.cover[0] = (float)a.rows;
+        scratch[0] = 0;
+    }
+    __syncthreads();
+    write_items(sh, ctl, 0, pairs, items, slot_seg, slot_count, 1, a.target_items, a.min_chunk,
+                scratch, wave_tot, true);
+}
+
+hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeCtl *ctl,
+                          LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
+                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out) {
+    hipLaunchKernelGGL(k_lw_init, dim3(1), dim3(1024), 0, s, sh, a, ctl, st, open, slot_seg,
+                       slot_count, pairs, items, scratch, out);
+    return hipGetLastError();
+}
+
+// Best split of each newly evaluated leaf: argmax over features (strict '>',
+// lowest feature wins), one wavefront per leaf.
+__global__ __launch_bounds__(128) void k_lw_eval(Shape sh, SplitParams sp, LWArgs a,
+                                                 const LWState *st, LWOpen *open,
+                                                 const SplitResult *__restrict__ results,
+                                                 const int64_t *slot_g, const int64_t *slot_h,
+                                                 const TreeCtl *ctl, TreeOut out) {
+    (void)a;
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    if (st->done || (uint32_t)w >= st->eval_count) return;
+    const uint32_t e = st->eval_first + (uint32_t)w;
+    const int32_t slot = open[e].slot;
+    if (slot < 0) return;
+    const int F = sh.cols;
+    float bg = -INFINITY;
+    int bf = 0x7FFFFFFF;
+    for (int f = lane; f < F; f += 64) {
+        const float g = results[(size_t)slot * F + f].gain;
+        if (g > bg) { bg = g; bf = f; }
+    }
+    wave_argmax(bg, bf);
+    if (lane != 0) return;
+    LWOpen o = open[e];
+    o.g = slot_g[slot];
+    o.h = slot_h[slot];
+    if (bf != 0x7FFFFFFF) {
+        o.best = results[(size_t)slot * F + bf];
+        o.best_f = bf;
+    } else {
+        o.best_f = -1;
+        o.best.gain = -INFINITY;
+    }
+    open[e] = o;
+    if (o.node == 0) {                               // the root's own leaf value
+        const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
+        const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
+        out.leaf[0] = lw_leaf_value(sp, o.g, o.h, g_inv, h_inv, o.lo, o.hi);
+    }
+}
+
+hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
+                          const LWState *st, LWOpen *open, const SplitResult *results,
+                          const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,
+                          const TreeOut out) {
+    hipLaunchKernelGGL(k_lw_eval, dim3(1), dim3(128), 0, s, sh, sp, a, st, open, results, slot_g,
+                       slot_h, ctl, out);
+    return hipGetLastError();
+}
+
+// Pick the open leaf with the largest gain > minSplitGain (lowest index wins),
+// write its split, its children's statistics, bounds and leaf values, and set
+// up the partition of its segment.
+__global__ __launch_bounds__(64) void k_lw_pick(SplitParams sp, LWArgs a, LWState *st,
+                                                LWOpen *open, const int8_t *monotone,
+                                                TreeCtl *ctl, TreeOut out) {
+    const int lane = lane_id();
+    if (lane == 0) {
+        ctl->num_items = 0;                          // nothing to build unless planned
+        ctl->num_pairs = 0;
+    }
+    if (st->done) return;
+    if ((int32_t)st->leaves >= a.num_leaves) {
+        if (lane == 0) st->done = 1;
+        return;
+    }
+    const uint32_t n_open = st->open_count;
+    float bg = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (uint32_t i = (uint32_t)lane; i < n_open; i += 64) {
+        const LWOpen &o = open[i];
+        const float g = o.best.gain;
+        if (o.best_f >= 0 && isfinite(g) && g > sp.min_split_gain && g > bg) {
+            bg = g;
+            bi = (int)i;
+        }
+    }
+    wave_argmax(bg, bi);
+    if (lane != 0) return;
+    if (bi == 0x7FFFFFFF) {
+        st->done = 1;
+        return;
+    }
+    const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
+    const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
+    const LWOpen o = open[bi];
+    const SplitResult r = o.best;
+    const int32_t n = o.node, bf = o.best_f;
+    const bool cat = (r.flags & FLAG_CATEGORICAL) != 0;
+    const NodeSplit ns = {bf, r.bin, r.flags};
+    out.split[n] = ns;
+    out.leaf[n] = 0.0f;
+    out.gain[n] = r.gain;
+    for (int w = 0; w < 8; ++w) out.mask[(size_t)n * 8 + w] = cat ? r.mask[w] : 0u;
+    // children (monotone bounds: Shaders.swift:1424-1443)
+    const int64_t lg = r.gl_int, lh = r.hl_int, rg = o.g - r.gl_int, rh = o.h - r.hl_int;
+    float llo = o.lo, lhi = o.hi, rlo = o.lo, rhi = o.hi;
+    const int cst = cat ? 0 : (int)monotone[bf];
+    if (cst != 0) {
+        const float vl = -r.gl / (r.hl + sp.lambda);
+        const float gr = (float)rg * g_inv, hr = (float)rh * h_inv;
+        const float vr = -gr / (hr + sp.lambda);
+        const float mid = clampf(0.5f * (vl + vr), o.lo, o.hi);
+        if (cst > 0) { lhi = fminf(lhi, mid); rlo = fmaxf(rlo, mid); }
+        else { llo = fmaxf(llo, mid); rhi = fminf(rhi, mid); }
+    }
+    const int32_t lc = 2 * n + 1, rc = 2 * n + 2;
+    out.leaf[lc] = lw_leaf_value(sp, lg, lh, g_inv, h_inv, llo, lhi);
+    out.leaf[rc] = lw_leaf_value(sp, rg, rh, g_inv, h_inv, rlo, rhi);
+    const uint32_t i0 = n_open;
+    LWOpen c = {};
+    c.depth = o.depth + 1;
+    c.slot = -1;
+    c.best_f = -1;
+    c.best.gain = -INFINITY;
+    c.node = lc; c.g = lg; c.h = lh; c.lo = llo; c.hi = lhi;
+    open[i0] = c;
+    c.node = rc; c.g = rg; c.h = rh; c.lo = rlo; c.hi = rhi;
+    open[i0 + 1] = c;
+    open[bi].best_f = -1;
+    open[bi].best.gain = -INFINITY;
+    st->pick = (uint32_t)bi;
+    st->child0 = i0;
+    st->open_count = n_open + 2;
+    st->eval_count = 0;
+    st->src = o.seg;
+    st->dst = o.seg < a.rows ? o.seg + a.rows : o.seg - a.rows;
+    st->count = o.count;
+    uint32_t chunk = (o.count + a.part_blocks - 1) / a.part_blocks;
+    chunk = (chunk + 255u) & ~255u;
+    st->chunk = chunk ? chunk : 256u;
+    st->feature = bf;
+    st->bin = r.bin;
+    st->flags = r.flags;
+    for (int w = 0; w < 8; ++w) st->mask[w] = cat ? r.mask[w] : 0u;
+}
+
+hipError_t launch_lw_pick(hipStream_t s, const SplitParams &sp, const LWArgs &a, LWState *st,
+                          LWOpen *open, const int8_t *monotone, TreeCtl *ctl, const TreeOut out) {
+    hipLaunchKernelGGL(k_lw_pick, dim3(1), dim3(64), 0, s, sp, a, st, open, monotone, ctl, out);
+    return hipGetLastError();
+}
+
+// Partition count: block b owns segment positions [b*chunk, (b+1)*chunk).
+constexpr int LW_PART_THREADS = 256;
+
+__global__ __launch_bounds__(LW_PART_THREADS) void k_lw_count(LWArgs a, const LWState *st,
+                                                             const uint8_t *__restrict__ bins_fm,
+                                                             const Entry *__restrict__ order,
+                                                             uint8_t *__restrict__ dir,
+                                                             uint32_t *block_left, int32_t nb) {
+    __shared__ uint32_t red[LW_PART_THREADS / 64];
+    __shared__ uint32_t s_mask[8];
+    if (st->done) return;
+    const uint32_t cnt = st->count, chunk = st->chunk;
+    const uint32_t start = blockIdx.x * chunk;
+    const int tid = threadIdx.x;
+    if (start >= cnt) {
+        if (tid == 0) block_left[blockIdx.x] = 0;
+        return;
+    }
+    const uint32_t end = min(start + chunk, cnt);
+    if (tid < 8) s_mask[tid] = st->mask[tid];
+    __syncthreads();
+    const NodeSplit ns = {st->feature, st->bin, st->flags};
+    const uint8_t *col = bins_fm + (size_t)ns.feature * a.rows;
+    const Entry *src = order + st->src;
+    uint32_t lefts = 0;
+    for (uint32_t j = start + (uint32_t)tid; j < end; j += LW_PART_THREADS) {
+        const uint32_t b = col[src[j].row];
+        const bool l = bin_goes_left(b, ns, nb, s_mask);
+        dir[j] = l ? 1 : 0;
+        lefts += l ? 1u : 0u;
+    }
+    lefts = wave_sum(lefts);
+    if (lane_id() == 0) red[tid >> 6] = lefts;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < LW_PART_THREADS / 64; ++w) t += red[w];
+        block_left[blockIdx.x] = t;
+    }
+}
+
+hipError_t launch_lw_count(hipStream_t s, const LWArgs &a, const LWState *st,
+                           const uint8_t *bins_fm, const Entry *order, uint8_t *dir,
+                           uint32_t *block_left, int32_t num_bins) {
+    hipLaunchKernelGGL(k_lw_count, dim3(a.part_blocks), dim3(LW_PART_THREADS), 0, s, a, st,
+                       bins_fm, order, dir, block_left, num_bins);
+    return hipGetLastError();
+}
+
+// Partition plan: block offsets, child segments and covers, whether the
+// children are evaluated, histogram slots and the smaller child's items.
+__global__ __launch_bounds__(1024) void k_lw_plan(Shape sh, LWArgs a, LWState *st, LWOpen *open,
+                                                  uint32_t *block_left, uint32_t *slot_seg,
+                                                  uint32_t *slot_count, TreeCtl *ctl,
+                                                  Pair *pairs, HistItem *items,
+                                                  uint32_t *scratch, TreeOut out) {
+    __shared__ uint32_t wave_tot[17];
+    __shared__ uint32_t s_eval;
+    __shared__ int32_t s_level;
+    if (st->done) return;
+    const uint32_t left = block_exclusive_scan(block_left, a.part_blocks, wave_tot);
+    if (threadIdx.x == 0) {
+        const uint32_t cnt = st->count, right = cnt - left;
+        const LWOpen o = open[st->pick];
+        const uint32_t i0 = st->child0, i1 = i0 + 1;
+        const int32_t lc = 2 * o.node + 1, rc = 2 * o.node + 2;
+        out.cover[lc] = (float)left;
+        out.cover[rc] = (float)right;
+        open[i0].seg = st->dst;
+        open[i0].count = left;
+        open[i1].seg = st->dst + left;
+        open[i1].count = right;
+        st->left = left;
+        const int32_t child_depth = o.depth + 1;
+        const bool can_eval = child_depth < a.max_depth &&
+                              (int32_t)st->leaves + 1 < a.num_leaves && left > 0 && right > 0;
+        st->leaves += 1;
+        s_eval = can_eval ? 1u : 0u;
+        s_level = child_depth;
+        if (can_eval) {
+            // the smaller child (ties: left) gets a new slot; the larger one
+            // takes over the parent's slot (parent - smaller, in place)
+            const bool small_left = left <= right;
+            const uint32_t s_new = st->next_slot++;
+            const uint32_t s_par = (uint32_t)o.slot;
+            const uint32_t is = small_left ? i0 : i1, il = small_left ? i1 : i0;
+            open[is].slot = (int32_t)s_new;
+            open[il].slot = (int32_t)s_par;
+            slot_seg[s_new] = open[is].seg;
+            slot_count[s_new] = open[is].count;
+            slot_seg[s_par] = open[il].seg;
+            slot_count[s_par] = open[il].count;
+            Pair p = {};
+            p.built = s_new;
+            p.derived = s_par;
+            p.parent = s_par;
+            pairs[0] = p;
+            ctl->num_pairs = 1;
+            st->eval_first = i0;
+            st->eval_count = 2;
+        } else {
+            st->eval_count = 0;
+        }
+        scratch[0] = 0;
+    }
+    __syncthreads();
+    if (s_eval)
+        write_items(sh, ctl, min(s_level, 15), pairs, items, slot_seg, slot_count, 1,
+                    a.target_items, a.min_chunk, scratch, wave_tot, true);
+}
+
+hipError_t launch_lw_plan(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
+                          LWOpen *open, uint32_t *block_left, uint32_t *slot_seg,
+                          uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
+                          uint32_t *scratch, const TreeOut out) {
+    hipLaunchKernelGGL(k_lw_plan, dim3(1), dim3(1024), 0, s, sh, a, st, open, block_left,
+                       slot_seg, slot_count, ctl, pairs, items, scratch, out);
+    return hipGetLastError();
+}
+
+// Stable scatter of the segment into the other half: lefts first, then
+// rights, each in their original order.
+__global__ __launch_bounds__(LW_PART_THREADS) void k_lw_scatter(LWArgs a, const LWState *st,
+                                                               Entry *order,
+                                                               const uint8_t *__restrict__ dir,
+                                                               const uint32_t *block_left) {
+    __shared__ uint32_t wt[LW_PART_THREADS / 64 + 1];
+    (void)a;
+    if (st->done) return;
+    const uint32_t cnt = st->count, chunk = st->chunk;
+    const uint32_t start = blockIdx.x * chunk;
+    if (start >= cnt) return;
+    const uint32_t end = min(start + chunk, cnt);
+    const uint32_t left_base = block_left[blockIdx.x];      // lefts before this block
+    const uint32_t right_base = start - left_base;          // rights before this block
+    const uint32_t total_left = st->left;
+    const Entry *src = order + st->src;
+    Entry *dst = order + st->dst;
+    const int tid = threadIdx.x, w = tid >> 6;
+    uint32_t run = 0;                                        // lefts so far in this block
+    for (uint32_t base = start; base < end; base += LW_PART_THREADS) {
+        const uint32_t j = base + (uint32_t)tid;
+        const bool valid = j < end;
+        const uint32_t l = valid ? (uint32_t)dir[j] : 0u;
+        Entry e = {0u, 0u};
+        if (valid) e = src[j];
+        const uint32_t inc = wave_inclusive_scan(l);
+        if (lane_id() == 63) wt[w] = inc;
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t acc = 0;
+            for (int k = 0; k < LW_PART_THREADS / 64; ++k) { const uint32_t t = wt[k]; wt[k] = acc; acc += t; }
+            wt[LW_PART_THREADS / 64] = acc;
+        }
+        __syncthreads();
+        const uint32_t lefts_before = run + wt[w] + inc - l;
+        if (valid) {
+            const uint32_t pos = l ? left_base + lefts_before
+                                   : total_left + right_base + (j - start) - lefts_before;
+            dst[pos] = e;
+        }
+        run += wt[LW_PART_THREADS / 64];
+        __syncthreads();
+    }
+}
+
+hipError_t launch_lw_scatter(hipStream_t s, const LWArgs &a, const LWState *st, Entry *order,
+                             const uint8_t *dir, const uint32_t *block_left) {
+    hipLaunchKernelGGL(k_lw_scatter, dim3(a.part_blocks), dim3(LW_PART_THREADS), 0, s, a, st,
+                       order, dir, block_left);
     return hipGetLastError();
 }
 

@@ -198,6 +198,76 @@ hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs 
                                 const TreeOut out, const TreeCtl *ctl, float *preds,
                                 uint32_t max_blocks);
 
+// ---------------------------------------------------------------------------
+// Leaf-wise (best-first) growth (leaf_reset/leaf_init/leaf_pick_apply/
+// leaf_step and the partition pipeline, Shaders.swift:656-1091).  The order
+// entries live in one buffer of 2*rows: a leaf's segment sits in one half and
+// its partition writes the children into the same range of the other half.
+// Histograms live in slots: the smaller child of a split gets a new slot, the
+// larger child inherits the parent's slot (parent - smaller, in place).
+// ---------------------------------------------------------------------------
+
+struct LWOpen {                 // an unsplit leaf of the current tree
+    int32_t node;               // heap index
+    uint32_t seg;               // first entry (absolute, in the double buffer)
+    uint32_t count;             // rows
+    int32_t depth;
+    int32_t slot;               // histogram slot, -1 when not evaluated
+    int32_t best_f;             // best feature, -1 when it cannot be split
+    float lo, hi;               // monotone bounds of its leaf value
+    int64_t g, h;               // exact quantised sums
+    SplitResult best;           // best split over the allowed features
+};
+
+struct LWState {
+    uint32_t done;              // no further split in this tree
+    uint32_t leaves;            // current leaf count
+    uint32_t open_count;        // entries used in the open list
+    uint32_t next_slot;         // next free histogram slot
+    uint32_t pick;              // open entry split in this step
+    uint32_t child0;            // open entry of the left child (right = child0 + 1)
+    uint32_t eval_first;        // open entries whose best split the eval step fills
+    uint32_t eval_count;
+    // partition of the picked leaf
+    uint32_t src;               // absolute first entry of the segment
+    uint32_t dst;               // same range in the other half
+    uint32_t count;             // rows in the segment
+    uint32_t chunk;             // rows per partition block (multiple of 256)
+    uint32_t left;              // rows going left
+    int32_t feature;
+    uint32_t bin, flags;
+    uint32_t mask[8];
+};
+
+struct LWArgs {
+    int32_t num_leaves;         // L
+    int32_t max_depth;          // D
+    uint32_t rows;              // N (size of one half of the order buffer)
+    uint32_t part_blocks;       // partition grid
+    int32_t total_nodes;        // heap nodes per tree
+    uint32_t target_items, min_chunk;
+    uint32_t pad;
+};
+
+hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeCtl *ctl,
+                          LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
+                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out);
+hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
+                          const LWState *st, LWOpen *open, const SplitResult *results,
+                          const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,
+                          const TreeOut out);
+hipError_t launch_lw_pick(hipStream_t s, const SplitParams &sp, const LWArgs &a, LWState *st,
+                          LWOpen *open, const int8_t *monotone, TreeCtl *ctl, const TreeOut out);
+hipError_t launch_lw_count(hipStream_t s, const LWArgs &a, const LWState *st,
+                           const uint8_t *bins_fm, const Entry *order, uint8_t *dir,
+                           uint32_t *block_left, int32_t num_bins);
+hipError_t launch_lw_plan(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
+                          LWOpen *open, uint32_t *block_left, uint32_t *slot_seg,
+                          uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
+                          uint32_t *scratch, const TreeOut out);
+hipError_t launch_lw_scatter(hipStream_t s, const LWArgs &a, const LWState *st, Entry *order,
+                             const uint8_t *dir, const uint32_t *block_left);
+
 // Inference.
 struct ForestDev {
     const int32_t *feature;

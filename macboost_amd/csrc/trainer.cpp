@@ -140,6 +140,11 @@ struct Trainer {
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
+    // leaf-wise growth
+    bool leafwise = false;
+    mbk::LWArgs lw{};
+    DevBuf<mbk::LWState> lw_state;
+    DevBuf<mbk::LWOpen> lw_open;
     DevBuf<mbk::NodeSplit> m_split;
     DevBuf<float> m_leaf, m_gain, m_cover;
     DevBuf<uint32_t> m_mask;
@@ -396,7 +401,6 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         invalid("objective '" + objective_name(p.objective) +
                 "' (leaf renewal) is not supported by this build yet");
     if (p.objective == OBJ_MULTICLASS) invalid("multiclass is not supported by this build yet");
-    if (p.num_leaves > 0) invalid("leaf-wise growth (num_leaves) is not supported by this build yet");
     if (!p.init_model.empty()) invalid("init_model (warm start) is not supported by this build yet");
     // data validation (Booster.swift:451-529)
     validate_labels(p, y, rows);
@@ -536,11 +540,17 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.feat_mask.alloc((size_t)cols);
     MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, t.mask_base.data(), (size_t)cols, hipMemcpyHostToDevice, s));
 
-    t.order_a.alloc((size_t)rows);
-    t.order_b.alloc((size_t)rows);
+    t.leafwise = p.num_leaves > 0;
+    if (t.leafwise) {
+        t.order_a.alloc((size_t)rows * 2);           // both halves of the partition buffer
+    } else {
+        t.order_a.alloc((size_t)rows);
+        t.order_b.alloc((size_t)rows);
+    }
     t.dir.alloc((size_t)rows + 16);
     t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
-    t.block_left.alloc(t.max_blocks + 1);
+    const uint32_t part_blocks = (uint32_t)std::min<int64_t>(1024, (rows + 255) / 256);
+    t.block_left.alloc(std::max<uint32_t>(t.max_blocks, part_blocks) + 1);
 
     // histogram work decomposition
     const size_t lds = mbk::hist_lds_size();
@@ -559,10 +569,24 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.partials.alloc((size_t)max_items * (size_t)tile_w * (size_t)p.num_bins);
     t.items.alloc((size_t)max_items);
     t.pairs.alloc((size_t)t.max_level_nodes);
-    const size_t hist_n = (size_t)t.max_level_nodes * cols * p.num_bins * 2;
+    // level-wise: two levels of max_level_nodes histograms; leaf-wise: one
+    // slot per evaluated leaf (at most num_leaves)
+    const size_t slots = t.leafwise ? (size_t)p.num_leaves : (size_t)t.max_level_nodes;
+    const size_t hist_n = slots * cols * p.num_bins * 2;
     t.hist_a.alloc(hist_n);
-    t.hist_b.alloc(hist_n);
-    t.results.alloc((size_t)t.max_level_nodes * cols);
+    if (!t.leafwise) t.hist_b.alloc(hist_n);
+    t.results.alloc(std::max(slots, (size_t)t.max_level_nodes) * cols);
+    if (t.leafwise) {
+        t.lw.num_leaves = p.num_leaves;
+        t.lw.max_depth = t.D;
+        t.lw.rows = (uint32_t)rows;
+        t.lw.part_blocks = part_blocks;
+        t.lw.total_nodes = t.total_nodes;
+        t.lw.target_items = (uint32_t)t.target_items;
+        t.lw.min_chunk = (uint32_t)t.min_chunk;
+        t.lw_state.alloc(1);
+        t.lw_open.alloc((size_t)2 * p.num_leaves + 2);
+    }
     t.count.alloc((size_t)t.total_nodes);
     t.node_g.alloc((size_t)t.total_nodes);
     t.node_h.alloc((size_t)t.total_nodes);
@@ -687,6 +711,65 @@ static void grow_levelwise(Trainer &t, int tree) {
                           hipMemcpyDeviceToDevice, s));
 }
 
+// Best-first growth (growLeafWiseTree, Booster.swift:967-1310): root
+// histogram and split, then numLeaves-1 steps of pick -> partition -> smaller
+// child's histogram -> sibling by subtraction -> children's best splits.
+static void grow_leafwise(Trainer &t, int tree) {
+    hipStream_t s = t.dev->stream;
+    const mbk::Shape &sh = t.sh;
+    mbk::TreeOut out = t.tree_out(tree);
+    if (const uint8_t *m = tree_feature_mask(t, tree))
+        MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
+    mbk::TreeCtl *ctl = t.ctl.ptr;
+    mbk::Entry *order = t.order_a.ptr;
+    MB_HIP(mbk::launch_tree_init(s, ctl));
+    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl));
+    MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
+                                order));
+    MB_HIP(mbk::launch_lw_init(s, sh, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
+                               t.count.ptr, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out));
+    auto build_and_eval = [&](int step) {
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (t.profiling) {
+            MB_HIP(hipEventCreate(&e0));
+            MB_HIP(hipEventCreate(&e1));
+            MB_HIP(hipEventRecord(e0, s));
+        }
+        MB_HIP(mbk::launch_hist(s, sh, t.bins_tiled.ptr, order, t.items.ptr, ctl, t.partials.ptr,
+                                t.hist_grid));
+        if (t.profiling) {
+            MB_HIP(hipEventRecord(e1, s));
+            t.events.push_back({e0, e1, std::min(step, 15)});
+        }
+        MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, t.hist_a.ptr,
+                                 t.hist_a.ptr, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
+                                 t.count.ptr, t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
+        MB_HIP(mbk::launch_lw_eval(s, sh, t.sp, t.lw, t.lw_state.ptr, t.lw_open.ptr,
+                                   t.results.ptr, t.node_g.ptr, t.node_h.ptr, ctl, out));
+    };
+    build_and_eval(0);
+    for (int it = 1; it < t.p.num_leaves; ++it) {
+        MB_HIP(mbk::launch_lw_pick(s, t.sp, t.lw, t.lw_state.ptr, t.lw_open.ptr, t.mono.ptr, ctl,
+                                   out));
+        MB_HIP(mbk::launch_lw_count(s, t.lw, t.lw_state.ptr, t.bins_fm.ptr, order, t.dir.ptr,
+                                    t.block_left.ptr, t.nb));
+        MB_HIP(mbk::launch_lw_plan(s, sh, t.lw, t.lw_state.ptr, t.lw_open.ptr, t.block_left.ptr,
+                                   t.seg_a.ptr, t.count.ptr, ctl, t.pairs.ptr, t.items.ptr,
+                                   t.scratch.ptr, out));
+        MB_HIP(mbk::launch_lw_scatter(s, t.lw, t.lw_state.ptr, order, t.dir.ptr,
+                                      t.block_left.ptr));
+        build_and_eval(it);
+    }
+    // training predictions: walk the finished tree on the binned rows
+    // (predict_tree_binned, Shaders.swift:1763-1781)
+    MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr));
+    if (t.has_valid)
+        MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
+                                          t.vpreds.ptr));
+    MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
+                          hipMemcpyDeviceToDevice, s));
+}
+
 void trainer_grow(Trainer *tp, int num_trees) {
     Trainer &t = *tp;
     hipStream_t s = t.dev->stream;
@@ -696,7 +779,8 @@ void trainer_grow(Trainer *tp, int num_trees) {
     std::vector<float> vp;
     for (int k = 0; k < num_trees && !t.stopped; ++k) {
         const int tree = t.grown;
-        grow_levelwise(t, tree);
+        if (t.leafwise) grow_leafwise(t, tree);
+        else grow_levelwise(t, tree);
         t.grown += 1;
         const int round = t.grown;
         const bool is_last = k + 1 == num_trees;

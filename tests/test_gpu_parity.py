@@ -288,6 +288,51 @@ def test_save_load_bitwise(tmp_path):
 
 
 # --------------------------------------------------------------------------
+# leaf-wise (best-first) growth
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("num_leaves,depth", [(31, 6), (2, 6), (64, 6), (17, 12)])
+def test_leafwise_identical_trees(num_leaves, depth):
+    # num_leaves = 2^depth reaches every level (the level-wise shape); 2 gives stumps
+    x, y = mb.friedman(20_000, 30, 77)
+    xt, _ = mb.friedman(5_000, 30, 77 + 999)
+    check_identical(x, y, {"num_trees": 20, "max_depth": depth, "num_leaves": num_leaves,
+                           "num_bins": 128}, x_test=xt)
+
+
+def test_leafwise_nan_categorical_monotone_identical():
+    x, y = _mixed(12_000)
+    params = {"num_trees": 20, "max_depth": 6, "num_leaves": 24, "categorical_features": [6],
+              "monotone_constraints": [0, 0, 0, 1, 0, 0, 0]}
+    h, ref = check_identical(x, y, params, is_cat=[0] * 6 + [1], x_test=x[:, :3000].copy())
+    assert (ref.forest.flags & O.FLAG_CATEGORICAL).any()
+
+
+def _leaves(tree):
+    feat = tree["feature"]
+    reach, n_leaves, stack = set(), 0, [0]
+    while stack:
+        n = stack.pop()
+        reach.add(n)
+        if feat[n] >= 0:
+            stack += [2 * n + 1, 2 * n + 2]
+        else:
+            n_leaves += 1
+    return n_leaves
+
+
+def test_leafwise_budget_and_stumps():
+    # LeafWiseTests.swift:68-103 (leaf budget) and :219-240 (numLeaves=2 stumps)
+    x, y = O.friedman(8000, 8, 5)
+    _, obj = gpu_fit(x, y, {"num_trees": 6, "max_depth": 6, "num_leaves": 7})
+    assert all(_leaves(t) <= 7 for t in obj["trees"])
+    assert max(_leaves(t) for t in obj["trees"]) == 7
+    _, obj = gpu_fit(x, y, {"num_trees": 6, "max_depth": 6, "num_leaves": 2})
+    for t in obj["trees"]:
+        assert t["feature"][0] >= 0 and t["feature"][1] == -1 and t["feature"][2] == -1
+
+
+# --------------------------------------------------------------------------
 # TreeSHAP
 # --------------------------------------------------------------------------
 
