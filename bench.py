@@ -48,6 +48,64 @@ def cpu_baseline(x, y, rows, cols, trees):
     return t_bin, t_fit
 
 
+def measure_extras(mb, x, y, cols, trees, with_cpu):
+    """Leaf-wise growth (63 leaves, depth 6) on the same 10M rows, then batch
+    predict of 500k held-out rows and TreeSHAP of 200k rows with that model.
+    Predict is checked bit for bit and TreeSHAP to 1e-5 relative against the
+    oracle on row samples."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    import model_io
+    out = {}
+    params = {"num_trees": trees + 2, "max_depth": 6, "num_bins": 256, "learning_rate": 0.1,
+              "num_leaves": 63}
+    tr = mb.Trainer(params, x, y, feature_major=True)
+    tr.grow(2)
+    t0 = time.perf_counter()
+    tr.grow(trees)
+    el = time.perf_counter() - t0
+    h = tr.booster()
+    tr.close()
+    out["leafwise"] = {"workload": "friedman1 10M x 100, 63 leaves, depth 6, 256 bins",
+                       "trees": trees, "seconds": el, "trees_per_s": trees / el}
+    log(f"leaf-wise: {trees} trees in {el:.3f}s = {trees / el:.1f} trees/s")
+    obj = model_io.saved_model(h)
+    forest = model_io.forest_from_json(obj)
+    base, nb = obj["baseScore"], obj["numBins"]
+    xp, _ = mb.friedman(500_000, cols, 42 + 999)
+    mb.predict(h, xp[:, :1000], feature_major=True)
+    t0 = time.perf_counter()
+    pp = mb.predict(h, xp, feature_major=True)
+    el = time.perf_counter() - t0
+    sample = np.ascontiguousarray(xp[:, :20_000])
+    t1 = time.perf_counter()
+    want = O.predict(forest, base, nb, sample)
+    cpu_el = time.perf_counter() - t1
+    exact = bool(np.array_equal(pp[:20_000], want))
+    out["predict"] = {"rows": 500_000, "trees": int(forest.num_trees), "seconds": el,
+                      "rows_per_s": 500_000 / el, "bit_exact_vs_oracle_20k_rows": exact,
+                      "note": "through macboost_predict: host X copied to HBM and back",
+                      "cpu_oracle_rows_per_s_1_core": 20_000 / cpu_el}
+    log(f"predict 500k x {forest.num_trees} trees: {el * 1e3:.1f} ms, bit-exact={exact}")
+    xs = np.ascontiguousarray(xp[:, :200_000])
+    mb.predict_contrib(h, xs[:, :1000], feature_major=True)
+    t0 = time.perf_counter()
+    c = mb.predict_contrib(h, xs, feature_major=True)
+    el = time.perf_counter() - t0
+    n_chk = 500
+    t1 = time.perf_counter()
+    ref = O.treeshap(forest, base, nb, np.ascontiguousarray(xs[:, :n_chk]))
+    cpu_el = time.perf_counter() - t1
+    ok = bool(np.allclose(c[:n_chk], ref, rtol=1e-5, atol=1e-6))
+    out["treeshap"] = {"rows": 200_000, "trees": int(forest.num_trees), "seconds": el,
+                       "row_trees_per_s": 200_000 * forest.num_trees / el,
+                       "within_1e-5_rel_vs_oracle_500_rows": ok,
+                       "cpu_oracle_row_trees_per_s_1_core": n_chk * forest.num_trees / cpu_el}
+    log(f"TreeSHAP 200k x {forest.num_trees} trees: {el * 1e3:.1f} ms, within tol={ok}")
+    del h
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,8 +114,11 @@ def main():
     ap.add_argument("--rows", type=int, default=10_000_000)
     ap.add_argument("--cols", type=int, default=100)
     ap.add_argument("--cpu-rows", type=int, default=2_000_000)
-    ap.add_argument("--cpu-trees", type=int, default=1)
+    ap.add_argument("--cpu-trees", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the leaf-wise, predict and TreeSHAP measurements")
+    ap.add_argument("--extra-trees", type=int, default=100)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
@@ -96,6 +157,8 @@ def main():
     rmse = float(np.sqrt(np.mean((pv.astype(np.float64) - yv) ** 2)))
     log(f"valid RMSE {rmse:.4f} after {args.steps + args.warmup} trees")
     tr.close()
+    extras = None if args.no_extras else measure_extras(mb, x, y, cols, args.extra_trees,
+                                                        not args.no_cpu)
 
     achieved = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms > 0 else None
     per_launch_bytes = hist_bytes / launches if launches else None
@@ -145,6 +208,7 @@ def main():
         "fit_seconds_100_trees_incl_binning": fit_total,
         "setup_seconds": {"edges_host": t_edges, "upload_and_bin": t_bin, "total": t_setup},
         "valid_rmse": rmse,
+        "leafwise_predict_treeshap": extras,
     }
     print(json.dumps(out), flush=True)
 
