@@ -697,9 +697,10 @@ int mbk_quantize(mbk_context *ctx, int32_t objective, float alpha, float aux, co
     return guarded(err, [&]() -> int {
         hipStream_t s = ctx->dev->stream;
         mb::DevBuf<mbk::TreeCtl> ctl(1);
+        mb::DevBuf<uint32_t> part(mbk::grad_max_scratch_words());
         mbk::GradParams gp{objective, alpha, aux, weights ? 1 : 0};
         MB_HIP(mbk::launch_tree_init(s, ctl.ptr));
-        MB_HIP(mbk::launch_grad_max(s, gp, preds, labels, weights, rows, ctl.ptr));
+        MB_HIP(mbk::launch_grad_max(s, gp, preds, labels, weights, rows, ctl.ptr, part.ptr));
         MB_HIP(mbk::launch_quantize(s, gp, preds, labels, weights, rows, ctl.ptr,
                                     reinterpret_cast<mbk::Entry *>(entries)));
         MB_HIP(hipMemcpyAsync(max_gh, ctl.ptr->max_gh, 8, hipMemcpyDeviceToDevice, s));

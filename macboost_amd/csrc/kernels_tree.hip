@@ -217,19 +217,44 @@ hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl) {
     return hipGetLastError();
 }
 
+// max |g| and max h as f32 bit patterns (reduce_max_gh, Shaders.swift:87-94).
+// Stage 1: at most GRAD_MAX_BLOCKS blocks, four rows per thread per step
+// (16B loads), one partial pair per block.  Stage 2: one block reduces the
+// partials and stores the result (no same-address atomics).
+constexpr int GRAD_MAX_BLOCKS = 1024;
+
+__device__ __forceinline__ void grad_max_row(const GradParams &gp, float p, float y, float w,
+                                             uint32_t &mg, uint32_t &mh) {
+    float g, h;
+    row_grad(gp, p, y, w, g, h);
+    mg = max(mg, __float_as_uint(fabsf(g)));
+    mh = max(mh, __float_as_uint(h));
+}
+
+template <bool VEC>   // VEC: 16B-aligned inputs, four rows per load
 __global__ __launch_bounds__(256) void k_grad_max(GradParams gp, const float *__restrict__ preds,
                                                   const float *__restrict__ labels,
                                                   const float *__restrict__ weights, int64_t rows,
-                                                  TreeCtl *ctl) {
+                                                  uint32_t *__restrict__ partial) {
     __shared__ uint32_t red[2][4];
-    uint32_t mg = 0, mh = 0;   // max on f32 bit patterns (Shaders.swift:87-94)
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        float g, h;
-        row_grad(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, g, h);
-        mg = max(mg, __float_as_uint(fabsf(g)));
-        mh = max(mh, __float_as_uint(h));
+    uint32_t mg = 0, mh = 0;
+    const int64_t n4 = VEC ? rows >> 2 : 0;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const float4 *p4 = reinterpret_cast<const float4 *>(preds);
+    const float4 *y4 = reinterpret_cast<const float4 *>(labels);
+    const float4 *w4 = reinterpret_cast<const float4 *>(weights);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const float4 p = p4[i], y = y4[i];
+        const float4 w = gp.has_weights ? w4[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        grad_max_row(gp, p.x, y.x, w.x, mg, mh);
+        grad_max_row(gp, p.y, y.y, w.y, mg, mh);
+        grad_max_row(gp, p.z, y.z, w.z, mg, mh);
+        grad_max_row(gp, p.w, y.w, w.w, mg, mh);
     }
+    // rows not covered by the 16B loads (all of them when !VEC)
+    for (int64_t i = (n4 << 2) + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
+         i += stride)
+        grad_max_row(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, mg, mh);
     mg = wave_max_u32(mg);
     mh = wave_max_u32(mh);
     const int w = threadIdx.x >> 6;
@@ -238,21 +263,50 @@ __global__ __launch_bounds__(256) void k_grad_max(GradParams gp, const float *__
     if (threadIdx.x == 0) {
         uint32_t a = red[0][0], b = red[1][0];
         for (int k = 1; k < (int)(blockDim.x >> 6); ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
-        atomicMax(&ctl->max_gh[0], a);
-        atomicMax(&ctl->max_gh[1], b);
+        partial[2 * blockIdx.x] = a;
+        partial[2 * blockIdx.x + 1] = b;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_grad_max_final(const uint32_t *__restrict__ partial,
+                                                        int nblocks, TreeCtl *ctl) {
+    __shared__ uint32_t red[2][4];
+    uint32_t a = 0, b = 0;
+    for (int k = threadIdx.x; k < nblocks; k += blockDim.x) {
+        a = max(a, partial[2 * k]);
+        b = max(b, partial[2 * k + 1]);
+    }
+    a = wave_max_u32(a);
+    b = wave_max_u32(b);
+    const int w = threadIdx.x >> 6;
+    if (lane_id() == 0) { red[0][w] = a; red[1][w] = b; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < (int)(blockDim.x >> 6); ++k) { red[0][0] = max(red[0][0], red[0][k]); red[1][0] = max(red[1][0], red[1][k]); }
+        ctl->max_gh[0] = red[0][0];
+        ctl->max_gh[1] = red[1][0];
     }
 }
 
 hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           TreeCtl *ctl) {
-    int64_t blocks = (rows + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
+                           TreeCtl *ctl, uint32_t *partial) {
+    int64_t blocks = ((rows >> 2) + 255) / 256;
+    if (blocks > GRAD_MAX_BLOCKS) blocks = GRAD_MAX_BLOCKS;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(k_grad_max, dim3((unsigned)blocks), dim3(256), 0, s, gp, preds, labels,
-                       weights, rows, ctl);
+    const bool vec = ((reinterpret_cast<uintptr_t>(preds) | reinterpret_cast<uintptr_t>(labels) |
+                       reinterpret_cast<uintptr_t>(weights)) & 15u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_grad_max<true>, dim3((unsigned)blocks), dim3(256), 0, s, gp, preds,
+                           labels, weights, rows, partial);
+    else
+        hipLaunchKernelGGL(k_grad_max<false>, dim3((unsigned)blocks), dim3(256), 0, s, gp, preds,
+                           labels, weights, rows, partial);
+    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(256), 0, s, partial, (int)blocks, ctl);
     return hipGetLastError();
 }
+
+size_t grad_max_scratch_words() { return 2 * (size_t)GRAD_MAX_BLOCKS; }
 
 __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__restrict__ preds,
                                                   const float *__restrict__ labels,
@@ -1278,8 +1332,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_scatter(
     Shape sh, LevelArgs la, const Entry *__restrict__ order_in, Entry *__restrict__ order_out,
     const uint8_t *__restrict__ dir, const uint32_t *__restrict__ seg_start,
     const uint32_t *__restrict__ seg_start_next, const uint32_t *__restrict__ node_left_prefix,
-    const uint32_t *__restrict__ block_off, const TreeOut out, const TreeCtl *ctl,
-    float *__restrict__ preds) {
+    const uint32_t *__restrict__ block_off, const TreeCtl *ctl) {
     extern __shared__ uint32_t rs_lds[];             // seg[num_level]
     __shared__ uint32_t tot[ROUTE_PER_THREAD * ROUTE_WAVES + 1];
     uint32_t *seg = rs_lds;
@@ -1301,14 +1354,10 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_route_scatter(
     for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
         const uint32_t s = base + k * ROUTE_THREADS;
         if (d8[k] > 2) continue;
+        if (d8[k] == 2) continue;                    // the node became a leaf
         const uint32_t local = owner_of(seg, la.num_level, s);
-        const uint32_t n = la.level_start + local;
         const Entry e = order_in[s];
-        if (d8[k] == 2) {
-            preds[e.row] += out.leaf[n];
-        } else if (la.terminal) {
-            preds[e.row] += out.leaf[2 * n + 1 + d8[k]];
-        } else {
+        {
             const uint32_t lrank = boff + ex[k] - node_left_prefix[local];
             const uint32_t pos = d8[k] == 0 ? seg_start_next[2 * local] + lrank
                                             : seg_start_next[2 * local + 1] + (s - seg[local]) - lrank;
@@ -1321,12 +1370,11 @@ hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs 
                                 const Entry *order_in, Entry *order_out, const uint8_t *dir,
                                 const uint32_t *seg_start, const uint32_t *seg_start_next,
                                 const uint32_t *node_left_prefix, const uint32_t *block_off,
-                                const TreeOut out, const TreeCtl *ctl, float *preds,
-                                uint32_t max_blocks) {
+                                const TreeCtl *ctl, uint32_t max_blocks) {
     size_t lds = (size_t)la.num_level * sizeof(uint32_t);
     hipLaunchKernelGGL(k_route_scatter, dim3(max_blocks), dim3(ROUTE_THREADS), lds, s, sh, la,
                        order_in, order_out, dir, seg_start, seg_start_next, node_left_prefix,
-                       block_off, out, ctl, preds);
+                       block_off, ctl);
     return hipGetLastError();
 }
 

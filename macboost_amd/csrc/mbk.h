@@ -119,9 +119,11 @@ struct GradParams {
     float aux;
     int32_t has_weights;
 };
+// partial: grad_max_scratch_words() u32 of device scratch
 hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           TreeCtl *ctl);
+                           TreeCtl *ctl, uint32_t *partial);
+size_t grad_max_scratch_words();
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order);
@@ -195,8 +197,7 @@ hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs 
                                 const Entry *order_in, Entry *order_out, const uint8_t *dir,
                                 const uint32_t *seg_start, const uint32_t *seg_start_next,
                                 const uint32_t *node_left_prefix, const uint32_t *block_off,
-                                const TreeOut out, const TreeCtl *ctl, float *preds,
-                                uint32_t max_blocks);
+                                const TreeCtl *ctl, uint32_t max_blocks);
 
 // ---------------------------------------------------------------------------
 // Leaf-wise (best-first) growth (leaf_reset/leaf_init/leaf_pick_apply/

@@ -130,7 +130,7 @@ struct Trainer {
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
     DevBuf<uint8_t> dir;
-    DevBuf<uint32_t> block_left;
+    DevBuf<uint32_t> block_left, gmax_part;
     DevBuf<uint64_t> partials;
     DevBuf<mbk::HistItem> items;
     DevBuf<mbk::Pair> pairs;
@@ -548,6 +548,7 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         t.order_b.alloc((size_t)rows);
     }
     t.dir.alloc((size_t)rows + 16);
+    t.gmax_part.alloc(mbk::grad_max_scratch_words());
     t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
     const uint32_t part_blocks = (uint32_t)std::min<int64_t>(1024, (rows + 255) / 256);
     t.block_left.alloc(std::max<uint32_t>(t.max_blocks, part_blocks) + 1);
@@ -640,7 +641,8 @@ static void grow_levelwise(Trainer &t, int tree) {
         MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
     mbk::TreeCtl *ctl = t.ctl.ptr;
     MB_HIP(mbk::launch_tree_init(s, ctl));
-    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl));
+    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
+                                t.gmax_part.ptr));
     MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
                                 t.order_a.ptr));
     MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)t.rows, (uint32_t)t.target_items,
@@ -685,13 +687,14 @@ static void grow_levelwise(Trainer &t, int tree) {
                                       ctl, seg_cur, seg_next, t.count.ptr, t.left_count.ptr,
                                       t.node_left_prefix.ptr, t.block_left.ptr, out, t.pairs.ptr,
                                       t.items.ptr, t.scratch.ptr));
-        if (terminal)
+        if (terminal) {
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out));
+            break;
+        }
         MB_HIP(mbk::launch_route_scatter(s, sh, lp, ord_cur, ord_next, t.dir.ptr, seg_cur,
-                                         seg_next, t.node_left_prefix.ptr, t.block_left.ptr, out,
-                                         ctl, t.preds.ptr, t.max_blocks));
-        if (terminal) break;
+                                         seg_next, t.node_left_prefix.ptr, t.block_left.ptr, ctl,
+                                         t.max_blocks));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
@@ -704,6 +707,10 @@ static void grow_levelwise(Trainer &t, int tree) {
                                   t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.left_count.ptr,
                                   out));
     }
+    // training predictions: one leaf per row from a walk of the finished tree
+    // over the binned rows; the same single addition the partition-time update
+    // makes (route_samples apply, Shaders.swift:1280-1311)
+    MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr));
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
                                           t.vpreds.ptr));
@@ -723,7 +730,8 @@ static void grow_leafwise(Trainer &t, int tree) {
     mbk::TreeCtl *ctl = t.ctl.ptr;
     mbk::Entry *order = t.order_a.ptr;
     MB_HIP(mbk::launch_tree_init(s, ctl));
-    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl));
+    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
+                                t.gmax_part.ptr));
     MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
                                 order));
     MB_HIP(mbk::launch_lw_init(s, sh, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,

@@ -93,17 +93,20 @@ def test_bin_data_matches_oracle(ctx, tile_w):
         assert not tiled[:, T - 1, tile_w - pad:].any()
 
 
-@pytest.mark.parametrize("objective", [O.OBJ_L2, O.OBJ_LOGISTIC])
-def test_quantize_matches_oracle(ctx, objective):
+@pytest.mark.parametrize("objective,offset", [(O.OBJ_L2, 0), (O.OBJ_LOGISTIC, 0),
+                                              (O.OBJ_LOGISTIC, 1)])
+def test_quantize_matches_oracle(ctx, objective, offset):
+    # offset 1: inputs start one float past a 16-byte boundary (no vector loads)
     rng = np.random.default_rng(9)
-    n = 40_000
-    preds = rng.normal(size=n).astype(np.float32)
-    y = (rng.random(n) < 0.4).astype(np.float32) if objective == O.OBJ_LOGISTIC else \
-        rng.normal(size=n).astype(np.float32)
-    w = rng.random(n).astype(np.float32)
-    g, h, mg, mh = O.gradients(preds, y, w, objective=objective, aux=1.5)
+    n = 40_003
+    preds = rng.normal(size=n + 1).astype(np.float32)
+    y = (rng.random(n + 1) < 0.4).astype(np.float32) if objective == O.OBJ_LOGISTIC else \
+        rng.normal(size=n + 1).astype(np.float32)
+    w = rng.random(n + 1).astype(np.float32)
+    g, h, mg, mh = O.gradients(preds[offset:offset + n], y[offset:offset + n],
+                               w[offset:offset + n], objective=objective, aux=1.5)
     want = O.quantize(g, h, mg, mh)
-    dp, dy, dw = ctx.upload(preds), ctx.upload(y), ctx.upload(w)
+    dp, dy, dw = (ctx.upload(a) + 4 * offset for a in (preds, y, w))
     dm, de = ctx.alloc(8), ctx.alloc(8 * n)
     err = ctypes.c_char_p()
     rc = _core.lib().mbk_quantize(ctx.ptr, objective, 0.9, 1.5, dp, dy, dw, n, dm, de,
