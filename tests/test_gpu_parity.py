@@ -9,6 +9,9 @@ import ctypes
 import numpy as np
 import pytest
 
+import dataclasses
+
+import datasets as D
 import macboost_amd as mb
 import model_io
 import oracle_lib as O
@@ -288,6 +291,60 @@ def test_save_load_bitwise(tmp_path):
     h2 = mb.load(tmp_path / "m.json")
     assert np.array_equal(mb.predict(h, x, feature_major=True),
                           mb.predict(h2, x, feature_major=True))
+
+
+# --------------------------------------------------------------------------
+# benchmark configurations (tree counts bounded by the oracle's speed)
+# --------------------------------------------------------------------------
+
+def test_c2_friedman_1m_identical_trees():
+    # 1M x 100 Friedman #1, 256 bins, depth 6; 200k held-out rows
+    x, y = mb.friedman(1_000_000, 100, 42)
+    xt, _ = mb.friedman(200_000, 100, 42 + 999)
+    check_identical(x, y, {"num_trees": 4, "max_depth": 6, "num_bins": 256}, x_test=xt)
+
+
+def test_c3_nan_categorical_identical_trees():
+    # 20% MCAR NaN over the numeric columns, 20 categorical columns
+    x, y, cats = D.c3_mixed(300_000, 42)
+    xv, _, _ = D.c3_mixed(50_000, 42 + 999)
+    h, ref = check_identical(x, y, {"num_trees": 5, "max_depth": 6, "categorical_features": cats},
+                             is_cat=[0] * 80 + [1] * 20, x_test=xv)
+    assert (ref.forest.flags & O.FLAG_CATEGORICAL).any()
+
+
+def test_c4_higgs_like_logistic_identical_trees():
+    # 28 HIGGS-shaped features, logistic objective
+    x, y = D.c4_higgs_like(200_000, 42)
+    xt, _ = D.c4_higgs_like(50_000, 43)
+    check_identical(x, y, {"num_trees": 10, "max_depth": 6, "objective": "binary"}, x_test=xt)
+
+
+def _first_trees(forest, k):
+    return O.Forest(**{f.name: (None if getattr(forest, f.name) is None
+                                else np.ascontiguousarray(getattr(forest, f.name)[:k]))
+                       for f in dataclasses.fields(forest)})
+
+
+def test_valid_eval_and_early_stopping_match_oracle():
+    # Booster.swift:1650-1696: valid RMSE after every tree, stop after 5 stale
+    # rounds, keep the best iteration's trees
+    x, y = O.friedman(3000, 10, 61)
+    xv, yv = O.friedman(3000, 10, 62)
+    params = {"num_trees": 300, "max_depth": 6, "learning_rate": 0.3, "early_stopping_rounds": 5}
+    h = mb.train(params, x, y, eval_set=(xv.T, yv), feature_major=True)
+    best = mb.best_iteration(h)
+    assert 1 <= best < 295 and mb.num_trees(h) == best
+    ref = oracle_fit(x, y, {"num_trees": best + 5, "max_depth": 6, "learning_rate": 0.3})
+    rmse = []
+    for k in range(1, best + 6):
+        p = O.predict(_first_trees(ref.forest, k), ref.base_score, ref.num_bins, xv)
+        rmse.append(np.float32(np.sqrt(np.mean((p.astype(np.float64) - yv) ** 2))))
+    rmse = np.array(rmse)
+    assert int(np.argmin(rmse)) + 1 == best or np.isclose(rmse.min(), rmse[best - 1], rtol=1e-6)
+    assert (rmse[best:] >= rmse[best - 1] * (1 - 1e-6)).all()      # the 5 stale rounds
+    got = model_io.forest_from_json(model_io.saved_model(h), ref.forest.nodes_per_tree)
+    model_io.assert_same_forest(got, _first_trees(ref.forest, best), with_cats=False)
 
 
 # --------------------------------------------------------------------------
