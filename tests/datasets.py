@@ -41,16 +41,19 @@ def normal(seed: int, n: int) -> np.ndarray:
     return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u[1::2])
 
 
-def c3_mixed(rows: int, seed: int = 42):
-    """Returns (x [100, rows] f32, y [rows] f32, categorical column list)."""
+def c3_mixed(rows: int, seed: int = 42, model_seed: int = 42):
+    """Returns (x [100, rows] f32, y [rows] f32, categorical column list).
+    The generating model (cardinalities and category offsets) comes from
+    model_seed; the rows come from seed, so sets drawn with different seeds
+    share one model."""
     import macboost_amd as mb
     x, y = mb.friedman(rows, 100, seed)
     y = y.astype(np.float64)
-    cards = 2 + (splitmix(seed ^ 0xCA7CA7, 20) % np.uint64(63)).astype(np.int64)
+    cards = 2 + (splitmix(model_seed ^ 0xCA7CA7, 20) % np.uint64(63)).astype(np.int64)
     for j in range(20):
         col = 80 + j
         c = (splitmix(seed + 7919 * (j + 1), rows) % np.uint64(cards[j])).astype(np.int64)
-        offsets = normal((seed ^ 0x0FF5E7) + 104729 * (j + 1), int(cards[j]))
+        offsets = normal((model_seed ^ 0x0FF5E7) + 104729 * (j + 1), int(cards[j]))
         y += offsets[c]
         x[col] = c.astype(np.float32)
     miss = uniform(seed ^ 0x4E414E, 80 * rows).reshape(80, rows) < 0.2
@@ -58,9 +61,7 @@ def c3_mixed(rows: int, seed: int = 42):
     return x, y.astype(np.float32), list(range(80, 100))
 
 
-def c4_higgs_like(rows: int, seed: int = 42):
-    """Returns (x [28, rows] f32, y [rows] f32 in {0, 1})."""
-    rng = np.random.Generator(np.random.PCG64(seed))
+def _higgs_features(rows: int, rng) -> np.ndarray:
     x = np.empty((28, rows), np.float32)
     for f in range(21):
         v = rng.exponential(1.0, rows) if f % 3 == 2 else rng.standard_normal(rows)
@@ -75,24 +76,41 @@ def c4_higgs_like(rows: int, seed: int = 42):
     x[25] = np.sqrt(lo[3] ** 2 + lo[4] ** 2 + lo[5] ** 2)
     x[26] = np.sqrt((lo[6:10] ** 2).sum(axis=0))
     x[27] = x[24] * x[25]
-    xf = x.astype(np.float64)
-    # seeded depth-4 interaction tree over the 28 features
+    return x
+
+
+def _higgs_score(xf: np.ndarray, feats, thr, leaves) -> np.ndarray:
+    rows = xf.shape[1]
     node = np.zeros(rows, np.int64)
     for d in range(4):
-        nodes = 1 << d
-        feats = rng.integers(0, 28, size=nodes)
-        qs = rng.uniform(0.25, 0.75, size=nodes)
-        thr = np.array([np.quantile(xf[feats[k], :200_000], qs[k]) for k in range(nodes)])
-        node = 2 * node + (xf[feats[node], np.arange(rows)] > thr[node])
-    f = rng.normal(0.0, 1.5, size=16)[node] + 0.3 * xf[24] - 0.2 * xf[2] + 0.1 * xf[27]
+        base = (1 << d) - 1
+        f = feats[base + node]
+        node = 2 * node + (xf[f, np.arange(rows)] > thr[base + node])
+    return leaves[node] + 0.3 * xf[24] - 0.2 * xf[2] + 0.1 * xf[27]
+
+
+def c4_higgs_like(rows: int, seed: int = 42, model_seed: int = 42):
+    """Returns (x [28, rows] f32, y [rows] f32 in {0, 1}).  The label model (a
+    depth-4 interaction tree, its quantile thresholds and the intercept for
+    ~53% positives) comes from model_seed and a reference sample; the rows and
+    label draws come from seed."""
+    mrng = np.random.Generator(np.random.PCG64(model_seed))
+    ref = _higgs_features(200_000, np.random.Generator(np.random.PCG64(model_seed + 1)))
+    reff = ref.astype(np.float64)
+    feats = mrng.integers(0, 28, size=15)
+    qs = mrng.uniform(0.25, 0.75, size=15)
+    thr = np.array([np.quantile(reff[feats[k]], qs[k]) for k in range(15)])
+    leaves = mrng.normal(0.0, 1.5, size=16)
+    s = _higgs_score(reff, feats, thr, leaves)
     lo_b, hi_b = -10.0, 10.0
-    sample = f[:200_000]
     for _ in range(60):                       # intercept for ~53% positives
         b = 0.5 * (lo_b + hi_b)
-        if np.mean(1.0 / (1.0 + np.exp(-(sample + b)))) < 0.53:
+        if np.mean(1.0 / (1.0 + np.exp(-(s + b)))) < 0.53:
             lo_b = b
         else:
             hi_b = b
-    p = 1.0 / (1.0 + np.exp(-(f + b)))
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = _higgs_features(rows, rng)
+    p = 1.0 / (1.0 + np.exp(-(_higgs_score(x.astype(np.float64), feats, thr, leaves) + b)))
     y = (rng.random(rows) < p).astype(np.float32)
     return x, y
