@@ -1126,53 +1126,36 @@ hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active
 __global__ __launch_bounds__(1024) void k_plan_level(
     Shape sh, LevelArgs la, uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
     const uint32_t *seg_start_prev, uint32_t *seg_start_next, uint32_t *count,
-    uint32_t *left_count,
-    uint32_t *node_left_prefix, uint32_t *block_left, const TreeOut out, Pair *pairs,
-    HistItem *items, uint32_t *scratch) {
+    const uint32_t *cursors, const TreeOut out, Pair *pairs, HistItem *items,
+    uint32_t *scratch) {
     __shared__ uint32_t wave_tot[17];
+    __shared__ uint32_t s_active;
     const int tid = threadIdx.x;
     const uint32_t num_prev = la.num_level >> 1;
     const uint32_t ls_prev = (la.level_start - 1) >> 1;   // (2^d - 1 - 1) / 2 = 2^(d-1) - 1
-    const uint32_t active_prev = ctl->level_active[la.level - 1];
-    const uint32_t nblk = (active_prev + ROUTE_BLOCK - 1) / ROUTE_BLOCK;
-    // 1. block offsets for the scatter's global left scan
-    const uint32_t total_left = block_exclusive_scan(block_left, nblk, wave_tot);
-    // 2. global left prefix at each node's segment start, S(a) = offset of a's
-    //    block + lefts before a inside it (left_count holds the latter), and
-    //    each node's left count S(next start) - S(start).
-    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
-        const uint32_t a = seg_start_prev[p];
-        node_left_prefix[p] = a < active_prev ? block_left[a / ROUTE_BLOCK] + left_count[p]
-                                              : total_left;
-    }
+    if (tid == 0) s_active = 0;
     __syncthreads();
-    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
-        const uint32_t next = p + 1 < num_prev ? node_left_prefix[p + 1] : total_left;
-        left_count[p] = next - node_left_prefix[p];
-    }
-    __syncthreads();
-    // 3. child counts, covers and segment starts
+    // children of a split node share its interval: left [start, start+L),
+    // right [start+L, start+count), with L from the partition's left cursor
+    uint32_t act = 0;
     for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
         const uint32_t n = ls_prev + p;
         const bool split = out.split[n].feature >= 0 && count[n] >= 1;
-        const uint32_t cl = split ? left_count[p] : 0u;
-        const uint32_t cr = split ? count[n] - left_count[p] : 0u;
+        const uint32_t cl = split ? cursors[2 * p] : 0u;
+        const uint32_t cr = split ? count[n] - cl : 0u;
         count[la.level_start + 2 * p] = cl;
         count[la.level_start + 2 * p + 1] = cr;
         out.cover[la.level_start + 2 * p] = (float)cl;
         out.cover[la.level_start + 2 * p + 1] = (float)cr;
-        seg_start_next[2 * p] = cl + cr;              // scanned below
-        seg_start_next[2 * p + 1] = 0;
+        seg_start_next[2 * p] = seg_start_prev[p];
+        seg_start_next[2 * p + 1] = seg_start_prev[p] + cl;
         scratch[1 + p] = split ? 1u : 0u;
+        act += cl + cr;
     }
+    act = wave_sum(act);
+    if (lane_id() == 0) atomicAdd(&s_active, act);
     __syncthreads();
-    const uint32_t active = block_exclusive_scan(seg_start_next, la.num_level, wave_tot);
-    // even slots now hold the prefix of pair totals; right starts follow the left
-    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
-        const uint32_t cl = count[la.level_start + 2 * p];
-        seg_start_next[2 * p + 1] = seg_start_next[2 * p] + cl;
-    }
-    __syncthreads();
+    const uint32_t active = s_active;
     if (tid == 0) ctl->level_active[la.level] = active;
     if (la.terminal) {
         if (tid == 0) { ctl->num_pairs = 0; ctl->num_items = 0; }
@@ -1206,35 +1189,24 @@ __global__ __launch_bounds__(1024) void k_plan_level(
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                              const uint32_t *seg_start_prev, uint32_t *seg_start_next,
-                             uint32_t *count, uint32_t *left_count, uint32_t *node_left_prefix,
-                             uint32_t *block_left, const TreeOut out, Pair *pairs,
-                             HistItem *items, uint32_t *scratch) {
+                             uint32_t *count, const uint32_t *cursors, const TreeOut out,
+                             Pair *pairs, HistItem *items, uint32_t *scratch) {
     hipLaunchKernelGGL(k_plan_level, dim3(1), dim3(1024), 0, s, sh, la, target_items, min_chunk,
-                       ctl, seg_start_prev, seg_start_next, count, left_count, node_left_prefix,
-                       block_left, out, pairs, items, scratch);
+                       ctl, seg_start_prev, seg_start_next, count, cursors, out, pairs, items,
+                       scratch);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// stable row partition: count pass, then scatter pass (route_samples,
-// Shaders.swift:1241-1311, made order-preserving and atomic-free).
-// Block b owns entries [b*2048, b*2048+2048); lane t of pass k handles entry
-// b*2048 + k*256 + t, so every load and store is coalesced.  The count pass
-// records, for every node whose segment starts inside the block, the number
-// of left-going entries of the block before that start; with the scanned
-// per-block totals this gives every node's left count and left prefix
-// without a single global atomic.
+// row partition (route_samples, Shaders.swift:1241-1311): one pass.  Every
+// split node keeps its interval [start, start+count) of the order buffer; its
+// children split that interval, left entries from the front and right
+// entries from the back.  Each block covers 2048 entries of one node, counts
+// its lefts and rights, reserves both ranges with one atomic add each on the
+// node's cursors, and writes its entries there.  Entry order inside a child
+// is not preserved; every consumer (histograms, counts, the next partition)
+// is order-independent.  The left cursor ends as the node's left count.
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ uint32_t owner_of(const uint32_t *seg, uint32_t n, uint32_t s) {
-    // largest local index with seg[idx] <= s (dead nodes repeat the next start)
-    uint32_t lo = 0, hi = n - 1;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi + 1) >> 1;
-        if (seg[mid] <= s) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-}
 
 constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
 
@@ -1266,115 +1238,121 @@ __device__ __forceinline__ void route_block_scan(const uint32_t (&x)[ROUTE_PER_T
     for (int k = 0; k < ROUTE_PER_THREAD; ++k) ex[k] += tot[k * ROUTE_WAVES + w];
 }
 
-// dir: 0 = left child, 1 = right child, 2 = node is a leaf
-__global__ __launch_bounds__(ROUTE_THREADS) void k_route_count(
-    Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
-    const uint32_t *__restrict__ seg_start, const TreeOut out, const TreeCtl *ctl,
-    uint8_t *__restrict__ dir, uint32_t *__restrict__ node_start_prefix,
-    uint32_t *__restrict__ block_left) {
-    extern __shared__ uint32_t rc_lds[];             // seg[num_level]
-    __shared__ uint32_t tot[ROUTE_PER_THREAD * ROUTE_WAVES + 1];
-    uint32_t *seg = rc_lds;
-    const int tid = threadIdx.x;
-    for (uint32_t k = tid; k < la.num_level; k += blockDim.x) seg[k] = seg_start[k];
+// Large blocks keep the cursor atomics few (two per block).
+constexpr int PART_THREADS = 1024;
+constexpr int PART_PER_THREAD = 16;
+constexpr int PART_BLOCK = PART_THREADS * PART_PER_THREAD;
+constexpr int PART_WAVES = PART_THREADS / 64;
+static_assert(PART_BLOCK == PART_ENTRIES, "partition block size");
+static_assert(PART_PER_THREAD * PART_WAVES == 256, "slice scan assumes 256 slices");
+
+// Blocks per split node of the routed level and their prefix; zero cursors.
+__global__ __launch_bounds__(1024) void k_route_plan(LevelArgs la, const uint32_t *count,
+                                                     const TreeOut out, uint32_t *blk_prefix,
+                                                     uint32_t *cursors) {
+    __shared__ uint32_t wave_tot[17];
+    for (uint32_t l = threadIdx.x; l < la.num_level; l += blockDim.x) {
+        const uint32_t n = la.level_start + l;
+        const bool split = out.split[n].feature >= 0 && count[n] >= 1;
+        blk_prefix[l] = split ? (count[n] + PART_BLOCK - 1) / PART_BLOCK : 0u;
+        cursors[2 * l] = 0;
+        cursors[2 * l + 1] = 0;
+    }
     __syncthreads();
-    const uint32_t active = ctl->level_active[la.level];
-    const uint32_t base = blockIdx.x * ROUTE_BLOCK + tid;
-    uint32_t x[ROUTE_PER_THREAD], ex[ROUTE_PER_THREAD], loc[ROUTE_PER_THREAD];
+    const uint32_t total = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
+    if (threadIdx.x == 0) blk_prefix[la.num_level] = total;
+}
+
+__global__ __launch_bounds__(PART_THREADS) void k_route(
+    Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
+    Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
+    const uint32_t *__restrict__ count, const TreeOut out, const uint32_t *__restrict__ blk_prefix,
+    uint32_t *cursors, int write_entries) {
+    __shared__ uint32_t tot[PART_PER_THREAD * PART_WAVES + 1];
+    __shared__ uint32_t s_mask[8];
+    __shared__ uint32_t s_base[2];
+    const uint32_t b = blockIdx.x;
+    if (b >= blk_prefix[la.num_level]) return;       // uniform per block
+    // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
+    uint32_t lo = 0, hi = la.num_level - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        if (blk_prefix[mid] <= b) lo = mid; else hi = mid - 1;
+    }
+    const uint32_t l = lo, n = la.level_start + l;
+    const uint32_t start = seg_start[l], cnt = count[n];
+    const uint32_t first = (b - blk_prefix[l]) * PART_BLOCK;
+    const uint32_t nvalid = min((uint32_t)PART_BLOCK, cnt - first);
+    const NodeSplit sp = out.split[n];
+    const int tid = threadIdx.x, w = tid >> 6;
+    if (tid < 8) s_mask[tid] = out.mask[(size_t)n * 8 + tid];
+    __syncthreads();
+    const Entry *src = order_in + start + first;
+    uint32_t x[PART_PER_THREAD], ex[PART_PER_THREAD];
+    Entry e[PART_PER_THREAD];
 #pragma unroll
-    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k * ROUTE_THREADS;
+    for (int k = 0; k < PART_PER_THREAD; ++k) {
+        const uint32_t i = (uint32_t)(k * PART_THREADS + tid);
         x[k] = 0;
-        loc[k] = 0;
-        if (s < active) {
-            const uint32_t local = owner_of(seg, la.num_level, s);
-            const uint32_t n = la.level_start + local;
-            const NodeSplit sp = out.split[n];
-            uint8_t d = 2;
-            if (sp.feature >= 0) {
-                const uint32_t row = order_in[s].row;
-                const uint32_t b = bins_fm[(size_t)sp.feature * (size_t)sh.rows + row];
-                d = bin_goes_left(b, sp, sh.num_bins, out.mask + (size_t)n * 8) ? 0 : 1;
-            }
-            dir[s] = d;
-            x[k] = d == 0 ? 1u : 0u;
-            loc[k] = local;
+        e[k] = Entry{0u, 0u};
+        if (i < nvalid) e[k] = src[i];
+    }
+#pragma unroll
+    for (int k = 0; k < PART_PER_THREAD; ++k) {
+        const uint32_t i = (uint32_t)(k * PART_THREADS + tid);
+        if (i < nvalid) {
+            const uint32_t bin = bins_fm[(size_t)sp.feature * (size_t)sh.rows + e[k].row];
+            x[k] = bin_goes_left(bin, sp, sh.num_bins, s_mask) ? 1u : 0u;
         }
     }
-    route_block_scan(x, ex, tot);
+    // in-block exclusive prefix of the left flags in entry order (k, then lane)
 #pragma unroll
-    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k * ROUTE_THREADS;
-        if (s < active && seg[loc[k]] == s) {
-            // this entry opens node loc[k] (and any dead nodes sharing the start)
-            for (uint32_t l = loc[k];; --l) {
-                node_start_prefix[l] = ex[k];
-                if (l == 0 || seg[l - 1] != s) break;
-            }
+    for (int k = 0; k < PART_PER_THREAD; ++k) {
+        const uint32_t inc = wave_inclusive_scan(x[k]);
+        ex[k] = inc - x[k];
+        if (lane_id() == 63) tot[k * PART_WAVES + w] = inc;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        // scan the PART_PER_THREAD*PART_WAVES (= 256) slice totals with one wave
+        uint32_t v[4], s = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { v[j] = tot[tid * 4 + j]; s += v[j]; }
+        const uint32_t inc = wave_inclusive_scan(s);
+        uint32_t acc = inc - s;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { tot[tid * 4 + j] = acc; acc += v[j]; }
+        if (tid == 63) {
+            const uint32_t nl = inc;
+            tot[PART_PER_THREAD * PART_WAVES] = nl;
+            s_base[0] = atomicAdd(&cursors[2 * l], nl);
+            s_base[1] = atomicAdd(&cursors[2 * l + 1], nvalid - nl);
         }
     }
-    if (tid == 0) block_left[blockIdx.x] = tot[ROUTE_PER_THREAD * ROUTE_WAVES];
-}
-
-hipError_t launch_route_count(hipStream_t s, const Shape &sh, const LevelArgs &la,
-                              const uint8_t *bins_fm, const Entry *order_in,
-                              const uint32_t *seg_start, const TreeOut out, const TreeCtl *ctl,
-                              uint8_t *dir, uint32_t *node_start_prefix, uint32_t *block_left,
-                              uint32_t max_blocks) {
-    size_t lds = (size_t)la.num_level * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_route_count, dim3(max_blocks), dim3(ROUTE_THREADS), lds, s, sh, la,
-                       bins_fm, order_in, seg_start, out, ctl, dir, node_start_prefix,
-                       block_left);
-    return hipGetLastError();
-}
-
-__global__ __launch_bounds__(ROUTE_THREADS) void k_route_scatter(
-    Shape sh, LevelArgs la, const Entry *__restrict__ order_in, Entry *__restrict__ order_out,
-    const uint8_t *__restrict__ dir, const uint32_t *__restrict__ seg_start,
-    const uint32_t *__restrict__ seg_start_next, const uint32_t *__restrict__ node_left_prefix,
-    const uint32_t *__restrict__ block_off, const TreeCtl *ctl) {
-    extern __shared__ uint32_t rs_lds[];             // seg[num_level]
-    __shared__ uint32_t tot[ROUTE_PER_THREAD * ROUTE_WAVES + 1];
-    uint32_t *seg = rs_lds;
-    const int tid = threadIdx.x;
-    for (uint32_t k = tid; k < la.num_level; k += blockDim.x) seg[k] = seg_start[k];
-    const uint32_t active = ctl->level_active[la.level];
-    const uint32_t base = blockIdx.x * ROUTE_BLOCK + tid;
-    uint32_t x[ROUTE_PER_THREAD], ex[ROUTE_PER_THREAD];
-    uint8_t d8[ROUTE_PER_THREAD];
+    if (!write_entries) return;                      // counts only (terminal level)
+    __syncthreads();
+    const uint32_t base_l = s_base[0], base_r = s_base[1];
+    Entry *dst = order_out + start;
 #pragma unroll
-    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k * ROUTE_THREADS;
-        d8[k] = s < active ? dir[s] : 3;
-        x[k] = d8[k] == 0 ? 1u : 0u;
-    }
-    route_block_scan(x, ex, tot);                    // also orders the seg[] loads
-    const uint32_t boff = block_off[blockIdx.x];
-#pragma unroll
-    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t s = base + k * ROUTE_THREADS;
-        if (d8[k] > 2) continue;
-        if (d8[k] == 2) continue;                    // the node became a leaf
-        const uint32_t local = owner_of(seg, la.num_level, s);
-        const Entry e = order_in[s];
-        {
-            const uint32_t lrank = boff + ex[k] - node_left_prefix[local];
-            const uint32_t pos = d8[k] == 0 ? seg_start_next[2 * local] + lrank
-                                            : seg_start_next[2 * local + 1] + (s - seg[local]) - lrank;
-            order_out[pos] = e;
-        }
+    for (int k = 0; k < PART_PER_THREAD; ++k) {
+        const uint32_t i = (uint32_t)(k * PART_THREADS + tid);
+        if (i >= nvalid) continue;
+        const uint32_t le = ex[k] + tot[k * PART_WAVES + w];
+        const uint32_t pos = x[k] ? base_l + le : cnt - 1u - (base_r + (i - le));
+        dst[pos] = e[k];
     }
 }
 
-hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs &la,
-                                const Entry *order_in, Entry *order_out, const uint8_t *dir,
-                                const uint32_t *seg_start, const uint32_t *seg_start_next,
-                                const uint32_t *node_left_prefix, const uint32_t *block_off,
-                                const TreeCtl *ctl, uint32_t max_blocks) {
-    size_t lds = (size_t)la.num_level * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_route_scatter, dim3(max_blocks), dim3(ROUTE_THREADS), lds, s, sh, la,
-                       order_in, order_out, dir, seg_start, seg_start_next, node_left_prefix,
-                       block_off, ctl);
+hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
+                        const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
+                        const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
+                        uint32_t *blk_prefix, uint32_t *cursors, uint32_t max_blocks,
+                        bool write_entries) {
+    hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(1024), 0, s, la, count, out, blk_prefix,
+                       cursors);
+    hipLaunchKernelGGL(k_route, dim3(max_blocks), dim3(PART_THREADS), 0, s, sh, la, bins_fm,
+                       order_in, order_out, seg_start, count, out, blk_prefix, cursors,
+                       write_entries ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -15,6 +15,7 @@ constexpr uint32_t FLAG_CATEGORICAL = 2u;
 constexpr int ROUTE_THREADS = 256;
 constexpr int ROUTE_PER_THREAD = 8;
 constexpr int ROUTE_BLOCK = ROUTE_THREADS * ROUTE_PER_THREAD;
+constexpr int PART_ENTRIES = 16384;   // entries per level-wise partition block
 
 // A histogram item accumulates at most this many rows in one packed LDS word:
 // high 32 bits = sum of 16-bit quantised gradients (|sum| <= 65535*32767 < 2^31),
@@ -177,27 +178,22 @@ hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const Level
                                const int64_t *node_h, const float2 *bounds,
                                const TreeCtl *ctl, TreeOut out);
 
-// la = the level being routed (d-1).
-hipError_t launch_route_count(hipStream_t s, const Shape &sh, const LevelArgs &la,
-                              const uint8_t *bins_fm, const Entry *order_in,
-                              const uint32_t *seg_start, const TreeOut out,
-                              const TreeCtl *ctl, uint8_t *dir, uint32_t *node_start_prefix,
-                              uint32_t *block_left, uint32_t max_blocks);
+// Partition of the routed level (d-1): every split node's interval is split
+// in place between its children (left from the front, right from the back);
+// cursors[2l] ends as node l's left count.  max_blocks >= ceil(rows/16384) +
+// nodes of the level.  write_entries = false only counts (terminal level).
+hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
+                        const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
+                        const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
+                        uint32_t *blk_prefix, uint32_t *cursors, uint32_t max_blocks,
+                        bool write_entries);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                              const uint32_t *seg_start_prev, uint32_t *seg_start_next,
-                             uint32_t *count, uint32_t *left_count, uint32_t *node_left_prefix,
-                             uint32_t *block_left, const TreeOut out, Pair *pairs,
-                             HistItem *items, uint32_t *scratch);
-
-// la = the level being routed (d-1).
-hipError_t launch_route_scatter(hipStream_t s, const Shape &sh, const LevelArgs &la,
-                                const Entry *order_in, Entry *order_out, const uint8_t *dir,
-                                const uint32_t *seg_start, const uint32_t *seg_start_next,
-                                const uint32_t *node_left_prefix, const uint32_t *block_off,
-                                const TreeCtl *ctl, uint32_t max_blocks);
+                             uint32_t *count, const uint32_t *cursors, const TreeOut out,
+                             Pair *pairs, HistItem *items, uint32_t *scratch);
 
 // ---------------------------------------------------------------------------
 // Leaf-wise (best-first) growth (leaf_reset/leaf_init/leaf_pick_apply/

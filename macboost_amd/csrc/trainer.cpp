@@ -130,7 +130,8 @@ struct Trainer {
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
     DevBuf<uint8_t> dir;
-    DevBuf<uint32_t> block_left, gmax_part;
+    DevBuf<uint32_t> block_left, gmax_part, route_blk, route_cursor;
+    uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
     DevBuf<mbk::HistItem> items;
     DevBuf<mbk::Pair> pairs;
@@ -549,6 +550,11 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     }
     t.dir.alloc((size_t)rows + 16);
     t.gmax_part.alloc(mbk::grad_max_scratch_words());
+    // level-wise partition: one block per 2048 entries of a split node
+    t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES) +
+                   (uint32_t)t.max_level_nodes;
+    t.route_blk.alloc((size_t)t.max_level_nodes + 1);
+    t.route_cursor.alloc((size_t)t.max_level_nodes * 2);
     t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
     const uint32_t part_blocks = (uint32_t)std::min<int64_t>(1024, (rows + 255) / 256);
     t.block_left.alloc(std::max<uint32_t>(t.max_blocks, part_blocks) + 1);
@@ -680,21 +686,17 @@ static void grow_levelwise(Trainer &t, int tree) {
         const bool terminal = d == t.D;
         mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
         mbk::LevelArgs ln{d, (uint32_t)((1u << d) - 1), 1u << d, terminal ? 1u : 0u};
-        MB_HIP(mbk::launch_route_count(s, sh, lp, t.bins_fm.ptr, ord_cur, seg_cur, out, ctl,
-                                       t.dir.ptr, t.left_count.ptr, t.block_left.ptr,
-                                       t.max_blocks));
+        MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
+                                 t.count.ptr, out, t.route_blk.ptr, t.route_cursor.ptr,
+                                 t.route_grid, !terminal));
         MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
-                                      ctl, seg_cur, seg_next, t.count.ptr, t.left_count.ptr,
-                                      t.node_left_prefix.ptr, t.block_left.ptr, out, t.pairs.ptr,
-                                      t.items.ptr, t.scratch.ptr));
+                                      ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr, out,
+                                      t.pairs.ptr, t.items.ptr, t.scratch.ptr));
         if (terminal) {
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out));
             break;
         }
-        MB_HIP(mbk::launch_route_scatter(s, sh, lp, ord_cur, ord_next, t.dir.ptr, seg_cur,
-                                         seg_next, t.node_left_prefix.ptr, t.block_left.ptr, ctl,
-                                         t.max_blocks));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
