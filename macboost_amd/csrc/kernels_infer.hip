@@ -85,6 +85,64 @@ hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t 
     return hipGetLastError();
 }
 
+// The same walk over the training rows, eight rows per thread walked level by
+// level together, that also counts the rows reaching each node of the deepest
+// level (counters in LDS, one global add per non-empty node per block).
+constexpr int WALK_THREADS = 1024;
+constexpr int WALK_ROWS = 8;
+
+__global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__restrict__ bins_fm,
+                                                             int64_t rows, int32_t nb,
+                                                             int32_t max_depth, TreeOut tree,
+                                                             float *__restrict__ preds,
+                                                             uint32_t *__restrict__ count) {
+    extern __shared__ uint32_t wc_lds[];             // 2^max_depth counters
+    const uint32_t deep = 1u << max_depth, deep_start = deep - 1;
+    for (uint32_t k = threadIdx.x; k < deep; k += blockDim.x) wc_lds[k] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * (WALK_THREADS * WALK_ROWS) + threadIdx.x;
+    uint32_t n[WALK_ROWS];
+#pragma unroll
+    for (int k = 0; k < WALK_ROWS; ++k) n[k] = 0;
+    for (int32_t d = 0; d < max_depth; ++d) {
+#pragma unroll
+        for (int k = 0; k < WALK_ROWS; ++k) {
+            const int64_t i = base + (int64_t)k * WALK_THREADS;
+            if (i >= rows) continue;
+            const NodeSplit s = tree.split[n[k]];
+            if (s.feature < 0) continue;
+            const uint32_t b = bins_fm[(int64_t)s.feature * rows + i];
+            bool left;
+            if (s.flags & FLAG_CATEGORICAL)
+                left = ((tree.mask[n[k] * 8 + (b >> 5)] >> (b & 31u)) & 1u) != 0;
+            else if (b == (uint32_t)(nb - 1)) left = (s.flags & FLAG_DEFAULT_LEFT) != 0;
+            else left = b <= s.bin;
+            n[k] = 2 * n[k] + 1 + (left ? 0 : 1);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < WALK_ROWS; ++k) {
+        const int64_t i = base + (int64_t)k * WALK_THREADS;
+        if (i >= rows) continue;
+        preds[i] += tree.leaf[n[k]];
+        if (n[k] >= deep_start) atomicAdd(&wc_lds[n[k] - deep_start], 1u);
+    }
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k < deep; k += blockDim.x)
+        if (wc_lds[k]) atomicAdd(&count[deep_start + k], wc_lds[k]);
+}
+
+hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                             int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                             float *preds, uint32_t *count) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t per = (int64_t)WALK_THREADS * WALK_ROWS;
+    const size_t lds = ((size_t)1 << max_depth) * sizeof(uint32_t);
+    hipLaunchKernelGGL(k_walk_count, dim3((unsigned)((rows + per - 1) / per)), dim3(WALK_THREADS),
+                       lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // TreeSHAP
 // ---------------------------------------------------------------------------

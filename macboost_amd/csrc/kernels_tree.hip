@@ -944,16 +944,22 @@ hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
     return hipGetLastError();
 }
 
-__global__ void k_final_leaves(SplitParams sp, LevelArgs la, const uint32_t *count,
+// Deepest level (final_leaves, Shaders.swift:1495-1511): leaf values of the
+// children of split parents; their row counts are zeroed here and counted by
+// the training walk (k_walk_count), and k_final_fixup then writes covers and
+// sets empty leaves to 0.
+__global__ void k_final_leaves(SplitParams sp, LevelArgs la, uint32_t *count,
                                const int64_t *node_g, const int64_t *node_h,
                                const float2 *bounds, const TreeCtl *ctl, TreeOut out) {
     const uint32_t local = blockIdx.x * blockDim.x + threadIdx.x;
     if (local >= la.num_level) return;
     const uint32_t n = la.level_start + local;
+    const uint32_t parent = (n - 1) >> 1;
     NodeSplit leaf = {-1, 0, 0};
     out.split[n] = leaf;
     out.gain[n] = 0.0f;
-    if (count[n] >= 1) {
+    count[n] = 0;
+    if (out.split[parent].feature >= 0 && count[parent] >= 1) {
         const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
         const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
         const float G = (float)node_g[n] * g_inv, H = (float)node_h[n] * h_inv;
@@ -965,11 +971,27 @@ __global__ void k_final_leaves(SplitParams sp, LevelArgs la, const uint32_t *cou
 }
 
 hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const LevelArgs &la,
-                               const uint32_t *count, const int64_t *node_g,
+                               uint32_t *count, const int64_t *node_g,
                                const int64_t *node_h, const float2 *bounds, const TreeCtl *ctl,
                                TreeOut out) {
     hipLaunchKernelGGL(k_final_leaves, dim3((la.num_level + 255) / 256), dim3(256), 0, s, sp, la,
                        count, node_g, node_h, bounds, ctl, out);
+    return hipGetLastError();
+}
+
+__global__ void k_final_fixup(LevelArgs la, const uint32_t *count, TreeOut out) {
+    const uint32_t local = blockIdx.x * blockDim.x + threadIdx.x;
+    if (local >= la.num_level) return;
+    const uint32_t n = la.level_start + local;
+    const uint32_t c = count[n];
+    out.cover[n] = (float)c;
+    if (c == 0) out.leaf[n] = 0.0f;
+}
+
+hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,
+                              TreeOut out) {
+    hipLaunchKernelGGL(k_final_fixup, dim3((la.num_level + 255) / 256), dim3(256), 0, s, la, count,
+                       out);
     return hipGetLastError();
 }
 

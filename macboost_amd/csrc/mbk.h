@@ -173,10 +173,14 @@ hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
                          float2 *bounds, const int8_t *monotone, const TreeCtl *ctl,
                          uint32_t *left_count, TreeOut out);
 
+// Deepest level: leaf values of split parents' children, counts zeroed
+// (launch_walk_count fills them, launch_final_fixup writes covers).
 hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const LevelArgs &la,
-                               const uint32_t *count, const int64_t *node_g,
+                               uint32_t *count, const int64_t *node_g,
                                const int64_t *node_h, const float2 *bounds,
                                const TreeCtl *ctl, TreeOut out);
+hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,
+                              TreeOut out);
 
 // Partition of the routed level (d-1): every split node's interval is split
 // in place between its children (left from the front, right from the back);
@@ -280,6 +284,11 @@ hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float 
 hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                                  int32_t num_bins, int32_t max_depth, const TreeOut tree,
                                  float *preds);
+// Training-row walk of a finished level-wise tree: preds += leaf, and rows per
+// node of the deepest level added to count[2^D - 1 ...].
+hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                             int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                             float *preds, uint32_t *count);
 
 struct ShapPath {
     int32_t elem_start;   // first element

@@ -686,17 +686,24 @@ static void grow_levelwise(Trainer &t, int tree) {
         const bool terminal = d == t.D;
         mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
         mbk::LevelArgs ln{d, (uint32_t)((1u << d) - 1), 1u << d, terminal ? 1u : 0u};
+        if (terminal) {
+            // deepest level: leaf values, then one walk of the finished tree over
+            // the training rows adds every row's leaf (the single addition the
+            // partition-time update makes, route_samples apply,
+            // Shaders.swift:1280-1311) and counts the deepest nodes' rows
+            MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
+                                            t.bounds.ptr, ctl, out));
+            MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr,
+                                          t.count.ptr));
+            MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
+            break;
+        }
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
                                  t.count.ptr, out, t.route_blk.ptr, t.route_cursor.ptr,
-                                 t.route_grid, !terminal));
+                                 t.route_grid, true));
         MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
                                       ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr, out,
                                       t.pairs.ptr, t.items.ptr, t.scratch.ptr));
-        if (terminal) {
-            MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
-                                            t.bounds.ptr, ctl, out));
-            break;
-        }
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
@@ -709,10 +716,6 @@ static void grow_levelwise(Trainer &t, int tree) {
                                   t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.left_count.ptr,
                                   out));
     }
-    // training predictions: one leaf per row from a walk of the finished tree
-    // over the binned rows; the same single addition the partition-time update
-    // makes (route_samples apply, Shaders.swift:1280-1311)
-    MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr));
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
                                           t.vpreds.ptr));
