@@ -5,13 +5,14 @@
 // search (:336-464), decisions (:1355-1511) and the row partition
 // (:1241-1311), re-designed for CDNA4:
 //   * histograms accumulate one packed 64-bit word per (feature, bin) in LDS
-//     (quantised gradient sum in the high half, hessian sum in the low half),
-//     one ds_add_u64 per (row, feature), and leave exact per-item partials;
-//   * the split search runs one 64-lane wavefront per (sibling pair, feature):
-//     it reduces the partials, derives the larger sibling by exact integer
-//     subtraction and scans all bins with wavefront prefix sums;
-//   * the level-wise row partition is a stable two-pass scan, so every node's
-//     rows stay in ascending row order and the whole tree is deterministic.
+//     (quantised gradient sum above bit 27, hessian sum below), one
+//     ds_add_u64 per (row, feature), and leave exact per-item partials;
+//   * partials are reduced into exact int64 histograms, the larger sibling is
+//     derived by integer subtraction, and the split search runs one 64-lane
+//     wavefront per (sibling pair, feature) with wavefront prefix sums;
+//   * the level-wise row partition is one pass that splits every node's
+//     interval in place between its children; nothing downstream depends on
+//     the order of rows inside a node, so the tree is deterministic.
 #include "mbk.h"
 
 #include <float.h>
@@ -467,8 +468,8 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
             // rows past the item's end carry value 0
             const uint32_t ghq = g + rl < cnt ? e.ghq : 0u;
             const int32_t qg = (int32_t)(int16_t)(uint16_t)(ghq >> 16);
-            const unsigned long long v =
-                ((unsigned long long)(uint32_t)qg << 32) + (unsigned long long)(ghq & 0x7Fu);
+            const unsigned long long v = (unsigned long long)((int64_t)qg * (1ll << HIST_QH_BITS)) +
+                                         (unsigned long long)(ghq & 0x7Fu);
             const RowRaw<P> cur = permute_dwords<P>(raw, b0, b1);
 #pragma unroll
             for (int s = 0; s < P; ++s) {
@@ -569,8 +570,8 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
         const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile) * stride + k;
         for (uint32_t c = (uint32_t)slice; c < pr.nchunks; c += REDUCE_SLICES) {
             const uint64_t w = src[(size_t)c * (size_t)T * stride];
-            g += (int64_t)(int32_t)(uint32_t)(w >> 32);
-            h += (int64_t)(uint32_t)w;
+            g += (int64_t)w >> HIST_QH_BITS;
+            h += (int64_t)(w & ((1ull << HIST_QH_BITS) - 1));
         }
     }
     red[slice][kk][0] = g;

@@ -17,10 +17,14 @@ constexpr int ROUTE_PER_THREAD = 8;
 constexpr int ROUTE_BLOCK = ROUTE_THREADS * ROUTE_PER_THREAD;
 constexpr int PART_ENTRIES = 16384;   // entries per level-wise partition block
 
-// A histogram item accumulates at most this many rows in one packed LDS word:
-// high 32 bits = sum of 16-bit quantised gradients (|sum| <= 65535*32767 < 2^31),
-// low 32 bits = sum of 7-bit quantised hessians (no carry into the high half).
-constexpr uint32_t HIST_CHUNK_MAX = 65535;
+// Packed histogram word: (sum of qg) << HIST_QH_BITS + (sum of qh), as a
+// 64-bit two's-complement sum.  A histogram item accumulates at most
+// HIST_CHUNK_MAX rows, so the hessian field never carries
+// (127 * HIST_CHUNK_MAX < 2^27) and the gradient field never overflows
+// (32767 * HIST_CHUNK_MAX < 2^36); decode with mask and arithmetic shift.
+constexpr int HIST_QH_BITS = 27;
+constexpr uint32_t HIST_CHUNK_MAX = (1u << 20) - 1;
+static_assert(127ull * HIST_CHUNK_MAX < (1ull << HIST_QH_BITS), "hessian field carries");
 
 // NodeSplit (Shaders.swift:466): feature < 0 marks a leaf.
 struct NodeSplit {
@@ -129,8 +133,8 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order);
 
-// Histogram items -> packed partials [item][B][W] (64-bit words: quantised
-// gradient sum << 32 | hessian sum).
+// Histogram items -> packed partials [item][B][W] (64-bit words, see
+// HIST_QH_BITS).
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
                        uint64_t *partials, int grid);
