@@ -309,6 +309,221 @@ hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *pre
 
 size_t grad_max_scratch_words() { return 2 * (size_t)GRAD_MAX_BLOCKS; }
 
+// ---------------------------------------------------------------------------
+// row sampling: GOSS and bagging (goss_grad_hist, goss_threshold, goss_select,
+// Shaders.swift:1093-1199, driven as in Booster.swift:1401-1445)
+// ---------------------------------------------------------------------------
+
+constexpr int GOSS_BUCKETS = 1024;
+constexpr int SEL_THREADS = 1024;
+constexpr int SEL_PER_THREAD = 16;
+constexpr int SEL_BLOCK = SEL_THREADS * SEL_PER_THREAD;
+constexpr int SEL_WAVES = SEL_THREADS / 64;
+static_assert(SEL_PER_THREAD * SEL_WAVES == 256, "slice scan assumes 256 slices");
+
+__device__ __forceinline__ uint32_t wang_hash(uint32_t x) {
+    x = (x ^ 61u) ^ (x >> 16);
+    x *= 9u;
+    x ^= x >> 4;
+    x *= 0x27d4eb2du;
+    x ^= x >> 15;
+    return x;
+}
+
+// |g| / max|g| histogram in 1024 buckets (LDS per block, one add per bucket)
+__global__ __launch_bounds__(256) void k_goss_hist(GradParams gp, const float *__restrict__ preds,
+                                                   const float *__restrict__ labels,
+                                                   const float *__restrict__ weights,
+                                                   int64_t rows, const TreeCtl *ctl,
+                                                   uint32_t *buckets) {
+    __shared__ uint32_t lb[GOSS_BUCKETS];
+    for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) lb[k] = 0;
+    __syncthreads();
+    const float mg = f32_from_bits(ctl->max_gh[0]);
+    if (mg > 0.0f) {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            float g, h;
+            row_grad(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, g, h);
+            const uint32_t b = (uint32_t)(fabsf(g) / mg * (float)GOSS_BUCKETS);
+            atomicAdd(&lb[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
+        }
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x)
+        if (lb[k]) atomicAdd(&buckets[k], lb[k]);
+}
+
+// Threshold = lower edge of the bucket where the count from the top first
+// reaches top_count (b = 1024, i.e. max|g|, when top_count = 0).  One
+// wavefront; leaves the buckets zeroed for the next tree.
+__global__ __launch_bounds__(64) void k_goss_threshold(uint32_t top_count, TreeCtl *ctl,
+                                                       uint32_t *buckets) {
+    const int lane = lane_id();
+    constexpr int PER = GOSS_BUCKETS / 64;
+    uint32_t v[PER], s = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { v[j] = buckets[lane * PER + j]; s += v[j]; }
+    // suffix sums over lanes: from this lane's first bucket to the top
+    uint32_t suf = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_down(suf, o, 64);
+        if (lane + o < 64) suf += t;
+    }
+    const float mg = f32_from_bits(ctl->max_gh[0]);
+    uint32_t b = GOSS_BUCKETS;
+    if (top_count > 0 && mg > 0.0f) {
+        // the crossing lane: the highest lane whose suffix reaches top_count
+        const uint64_t ok = __ballot(suf >= top_count);
+        if (ok == 0) {
+            b = 0;                                   // the whole histogram is below top_count
+        } else {
+            const int L = 63 - __builtin_clzll(ok);
+            const uint32_t above = __shfl(suf - s, L, 64);   // count in lanes above L
+            uint32_t cum = above, bb = (uint32_t)(L * PER + PER);
+            uint32_t w[PER];
+#pragma unroll
+            for (int j = 0; j < PER; ++j) w[j] = __shfl(v[j], L, 64);
+#pragma unroll
+            for (int j = PER - 1; j >= 0; --j) {
+                if (cum < top_count) { bb -= 1; cum += w[j]; }
+            }
+            b = bb;
+        }
+    }
+    if (lane == 0) {
+        const float thr = mg > 0.0f ? (float)b / (float)GOSS_BUCKETS * mg : 0.0f;
+        ctl->sample_thr = __float_as_uint(thr);
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) buckets[lane * PER + j] = 0;
+}
+
+// Keep rows with |g| >= threshold (weight 1) and a hashed uniform sample of
+// the rest (weight sp.weight); compact kept rows into order[] (one cursor add
+// per 16K-row chunk) and leave per-block maxima of |g|*w and h*w.
+__global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
+    GradParams gp, SampleParams sp, const float *__restrict__ preds,
+    const float *__restrict__ labels, const float *__restrict__ weights, int64_t rows,
+    TreeCtl *ctl, uint32_t *__restrict__ partial, Entry *__restrict__ order) {
+    __shared__ uint32_t tot[SEL_PER_THREAD * SEL_WAVES + 1];
+    __shared__ uint32_t s_base;
+    __shared__ uint32_t red[2][SEL_WAVES];
+    const int tid = threadIdx.x, w = tid >> 6;
+    const float thr = f32_from_bits(ctl->sample_thr);
+    uint32_t mg = 0, mh = 0;
+    for (int64_t c0 = (int64_t)blockIdx.x * SEL_BLOCK; c0 < rows;
+         c0 += (int64_t)gridDim.x * SEL_BLOCK) {
+        uint32_t x[SEL_PER_THREAD], amp[SEL_PER_THREAD], ex[SEL_PER_THREAD];
+#pragma unroll
+        for (int k = 0; k < SEL_PER_THREAD; ++k) {
+            const int64_t i = c0 + k * SEL_THREADS + tid;
+            x[k] = 0;
+            amp[k] = 0;
+            if (i < rows) {
+                float g, h;
+                row_grad(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, g, h);
+                const float ag = fabsf(g);
+                float wt = 1.0f;
+                bool keep = ag >= thr;
+                if (!keep) {
+                    const uint32_t hv = wang_hash((uint32_t)i ^ (sp.seed * 0x9E3779B9u));
+                    if ((float)(hv >> 8) * (1.0f / 16777216.0f) < sp.other_prob) {
+                        keep = true;
+                        wt = sp.weight;
+                    }
+                }
+                if (keep) {
+                    x[k] = 1;
+                    amp[k] = wt != 1.0f ? 1u : 0u;
+                    mg = max(mg, __float_as_uint(ag * wt));
+                    mh = max(mh, __float_as_uint(h * wt));
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < SEL_PER_THREAD; ++k) {
+            const uint32_t inc = wave_inclusive_scan(x[k]);
+            ex[k] = inc - x[k];
+            if (lane_id() == 63) tot[k * SEL_WAVES + w] = inc;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            uint32_t v[4], s = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { v[j] = tot[tid * 4 + j]; s += v[j]; }
+            const uint32_t inc = wave_inclusive_scan(s);
+            uint32_t acc = inc - s;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { tot[tid * 4 + j] = acc; acc += v[j]; }
+            if (tid == 63) s_base = atomicAdd(&ctl->sampled, inc);
+        }
+        __syncthreads();
+        const uint32_t base = s_base;
+#pragma unroll
+        for (int k = 0; k < SEL_PER_THREAD; ++k) {
+            if (!x[k]) continue;
+            const int64_t i = c0 + k * SEL_THREADS + tid;
+            order[base + tot[k * SEL_WAVES + w] + ex[k]] = Entry{(uint32_t)i, amp[k]};
+        }
+        __syncthreads();
+    }
+    mg = wave_max_u32(mg);
+    mh = wave_max_u32(mh);
+    if (lane_id() == 0) { red[0][w] = mg; red[1][w] = mh; }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t a = red[0][0], b = red[1][0];
+        for (int k = 1; k < SEL_WAVES; ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
+        partial[2 * blockIdx.x] = a;
+        partial[2 * blockIdx.x + 1] = b;
+    }
+}
+
+// Quantise the kept entries with the weighted maxima (quantize_gradients,
+// Shaders.swift:176-192, over amplified gradients).
+__global__ __launch_bounds__(256) void k_quantize_sampled(GradParams gp, SampleParams sp,
+                                                          const float *__restrict__ preds,
+                                                          const float *__restrict__ labels,
+                                                          const float *__restrict__ weights,
+                                                          const TreeCtl *ctl,
+                                                          Entry *__restrict__ order) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= ctl->sampled) return;
+    Entry e = order[i];
+    const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
+    const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
+    const float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
+    float g, h;
+    row_grad(gp, preds[e.row], labels[e.row], gp.has_weights ? weights[e.row] : 1.0f, g, h);
+    if (e.ghq) { g = g * sp.weight; h = h * sp.weight; }
+    const int qg = (int)rintf(g * gscale);
+    const uint32_t qh = (uint32_t)rintf(h * hscale);
+    e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
+    order[i] = e;
+}
+
+hipError_t launch_sample(hipStream_t s, const GradParams &gp, const SampleParams &sp,
+                         const float *preds, const float *labels, const float *weights,
+                         int64_t rows, TreeCtl *ctl, uint32_t *buckets, uint32_t *partial,
+                         Entry *order) {
+    if (sp.goss && sp.top_count > 0)
+        hipLaunchKernelGGL(k_goss_hist, dim3(256), dim3(256), 0, s, gp, preds, labels, weights,
+                           rows, ctl, buckets);
+    hipLaunchKernelGGL(k_goss_threshold, dim3(1), dim3(64), 0, s, sp.goss ? sp.top_count : 0u,
+                       ctl, buckets);
+    int64_t blocks = (rows + SEL_BLOCK - 1) / SEL_BLOCK;
+    if (blocks > GRAD_MAX_BLOCKS) blocks = GRAD_MAX_BLOCKS;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_goss_select, dim3((unsigned)blocks), dim3(SEL_THREADS), 0, s, gp, sp,
+                       preds, labels, weights, rows, ctl, partial, order);
+    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(256), 0, s, partial, (int)blocks, ctl);
+    hipLaunchKernelGGL(k_quantize_sampled, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
+                       gp, sp, preds, labels, weights, ctl, order);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__restrict__ preds,
                                                   const float *__restrict__ labels,
                                                   const float *__restrict__ weights, int64_t rows,
@@ -949,9 +1164,12 @@ hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
 // children of split parents; their row counts are zeroed here and counted by
 // the training walk (k_walk_count), and k_final_fixup then writes covers and
 // sets empty leaves to 0.
+// With counted != 0 the counts and covers already come from the partition
+// (sampled trees) and empty leaves are 0 here.
 __global__ void k_final_leaves(SplitParams sp, LevelArgs la, uint32_t *count,
                                const int64_t *node_g, const int64_t *node_h,
-                               const float2 *bounds, const TreeCtl *ctl, TreeOut out) {
+                               const float2 *bounds, const TreeCtl *ctl, TreeOut out,
+                               int counted) {
     const uint32_t local = blockIdx.x * blockDim.x + threadIdx.x;
     if (local >= la.num_level) return;
     const uint32_t n = la.level_start + local;
@@ -959,8 +1177,14 @@ __global__ void k_final_leaves(SplitParams sp, LevelArgs la, uint32_t *count,
     NodeSplit leaf = {-1, 0, 0};
     out.split[n] = leaf;
     out.gain[n] = 0.0f;
-    count[n] = 0;
-    if (out.split[parent].feature >= 0 && count[parent] >= 1) {
+    bool filled;
+    if (counted) {
+        filled = count[n] >= 1;
+    } else {
+        count[n] = 0;
+        filled = out.split[parent].feature >= 0 && count[parent] >= 1;
+    }
+    if (filled) {
         const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
         const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
         const float G = (float)node_g[n] * g_inv, H = (float)node_h[n] * h_inv;
@@ -974,9 +1198,9 @@ __global__ void k_final_leaves(SplitParams sp, LevelArgs la, uint32_t *count,
 hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const LevelArgs &la,
                                uint32_t *count, const int64_t *node_g,
                                const int64_t *node_h, const float2 *bounds, const TreeCtl *ctl,
-                               TreeOut out) {
+                               TreeOut out, bool counted) {
     hipLaunchKernelGGL(k_final_leaves, dim3((la.num_level + 255) / 256), dim3(256), 0, s, sp, la,
-                       count, node_g, node_h, bounds, ctl, out);
+                       count, node_g, node_h, bounds, ctl, out, counted ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1117,6 +1341,7 @@ __global__ __launch_bounds__(1024) void k_plan_root(Shape sh, uint32_t rows_acti
                                                     float hi, uint32_t *scratch) {
     __shared__ uint32_t wave_tot[17];
     if (threadIdx.x == 0) {
+        if (rows_active == NONE) rows_active = ctl->sampled;   // a sampled tree's kept rows
         count[0] = rows_active;
         seg_start[0] = 0;
         ctl->level_active[0] = rows_active;
@@ -1397,7 +1622,7 @@ __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *c
                                                   LWOpen *open, uint32_t *slot_seg,
                                                   uint32_t *slot_count, Pair *pairs,
                                                   HistItem *items, uint32_t *scratch,
-                                                  TreeOut out) {
+                                                  TreeOut out, int sampled) {
     __shared__ uint32_t wave_tot[17];
     const int tid = threadIdx.x;
     for (int n = tid; n < a.total_nodes; n += blockDim.x) {
@@ -1408,6 +1633,7 @@ __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *c
         out.cover[n] = 0.0f;
     }
     for (int k = tid; k < a.total_nodes * 8; k += blockDim.x) out.mask[k] = 0u;
+    const uint32_t n0 = sampled ? ctl->sampled : a.rows;   // the tree's rows
     if (tid == 0) {
         LWState s = {};
         s.leaves = 1;
@@ -1419,7 +1645,7 @@ __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *c
         LWOpen o = {};
         o.node = 0;
         o.seg = 0;
-        o.count = a.rows;
+        o.count = n0;
         o.depth = 0;
         o.slot = 0;
         o.best_f = -1;
@@ -1428,13 +1654,13 @@ __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *c
         o.best.gain = -INFINITY;
         open[0] = o;
         slot_seg[0] = 0;
-        slot_count[0] = a.rows;
+        slot_count[0] = n0;
         Pair p = {};
         p.built = 0; p.derived = NONE; p.parent = NONE;
         pairs[0] = p;
         ctl->num_pairs = 1;
-        ctl->level_active[0] = a.rows;
-        out.cover[0] = (float)a.rows;
+        ctl->level_active[0] = n0;
+        out.cover[0] = (float)n0;
         scratch[0] = 0;
     }
     __syncthreads();
@@ -1444,9 +1670,10 @@ __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *c
 
 hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeCtl *ctl,
                           LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
-                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out) {
+                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out,
+                          bool sampled) {
     hipLaunchKernelGGL(k_lw_init, dim3(1), dim3(1024), 0, s, sh, a, ctl, st, open, slot_seg,
-                       slot_count, pairs, items, scratch, out);
+                       slot_count, pairs, items, scratch, out, sampled ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -101,7 +101,8 @@ struct TreeCtl {
     uint32_t num_pairs;      // sibling pairs of the current level
     uint32_t chunk;          // rows per histogram chunk of the current level
     uint32_t overflow;       // 1 when a level needed more items than Shape::item_cap
-    uint32_t pad[2];
+    uint32_t sampled;        // rows kept by GOSS / bagging for this tree
+    uint32_t sample_thr;     // f32 bits of the GOSS keep threshold on |g|
     uint32_t level_active[16];  // live order entries per level
     uint32_t level_built[16];   // rows of built (histogrammed) nodes per level
 };
@@ -129,6 +130,25 @@ hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *pre
                            const float *labels, const float *weights, int64_t rows,
                            TreeCtl *ctl, uint32_t *partial);
 size_t grad_max_scratch_words();
+
+// Row sampling (GOSS / bagging) for one tree: buckets (1024 u32, zero on entry
+// and left zero) hold the |g| histogram.  top_count = 0 is bagging.  Kept
+// rows are compacted into order[0, ctl->sampled) with ghq = 1 marking
+// amplified rows, ctl->max_gh becomes the weighted maxima over kept rows
+// (partial: grad_max_scratch_words() u32), and the entries are then
+// quantised in place.
+struct SampleParams {
+    int32_t goss;            // 1: GOSS histogram threshold; 0: bagging
+    uint32_t top_count;      // floor(rows * top_rate) (0 for bagging)
+    float other_prob;        // keep probability below the threshold
+    float weight;            // amplification of the sampled rest
+    uint32_t seed;           // tree index + 1
+    uint32_t pad[3];
+};
+hipError_t launch_sample(hipStream_t s, const GradParams &gp, const SampleParams &sp,
+                         const float *preds, const float *labels, const float *weights,
+                         int64_t rows, TreeCtl *ctl, uint32_t *buckets, uint32_t *partial,
+                         Entry *order);
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order);
@@ -179,10 +199,11 @@ hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
 
 // Deepest level: leaf values of split parents' children, counts zeroed
 // (launch_walk_count fills them, launch_final_fixup writes covers).
+// counted: the counts come from the partition (sampled trees) instead.
 hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const LevelArgs &la,
                                uint32_t *count, const int64_t *node_g,
                                const int64_t *node_h, const float2 *bounds,
-                               const TreeCtl *ctl, TreeOut out);
+                               const TreeCtl *ctl, TreeOut out, bool counted);
 hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,
                               TreeOut out);
 
@@ -256,7 +277,8 @@ struct LWArgs {
 
 hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeCtl *ctl,
                           LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
-                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out);
+                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out,
+                          bool sampled);
 hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
                           const LWState *st, LWOpen *open, const SplitResult *results,
                           const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,

@@ -130,7 +130,7 @@ struct Trainer {
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
     DevBuf<uint8_t> dir;
-    DevBuf<uint32_t> block_left, gmax_part, route_blk, route_cursor;
+    DevBuf<uint32_t> block_left, gmax_part, route_blk, route_cursor, goss_buckets;
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
     DevBuf<mbk::HistItem> items;
@@ -396,8 +396,6 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     Trainer &t = *tr;
     t.p = pin;
     const Params &p = t.p;
-    if (p.goss) invalid("goss is not supported by this build yet");
-    if (p.subsample < 1.0f) invalid("subsample < 1 is not supported by this build yet");
     if (p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE)
         invalid("objective '" + objective_name(p.objective) +
                 "' (leaf renewal) is not supported by this build yet");
@@ -550,6 +548,10 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     }
     t.dir.alloc((size_t)rows + 16);
     t.gmax_part.alloc(mbk::grad_max_scratch_words());
+    if (p.goss || p.subsample < 1.0f) {
+        t.goss_buckets.alloc(1024);
+        MB_HIP(hipMemsetAsync(t.goss_buckets.ptr, 0, 1024 * sizeof(uint32_t), s));
+    }
     // level-wise partition: one block per 2048 entries of a split node
     t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES) +
                    (uint32_t)t.max_level_nodes;
@@ -639,6 +641,43 @@ static const uint8_t *tree_feature_mask(Trainer &t, int tree) {
     return t.tree_masks.back().data();
 }
 
+// GOSS after ceil(1/learning_rate) warm-up trees, bagging on every tree
+// (gossActive / bagging, Booster.swift:1382-1384, :617).
+static bool tree_sampled(const Params &p, int tree) {
+    if (p.goss) return tree >= (int)std::ceil(1.0f / p.learning_rate);
+    return p.subsample < 1.0f;
+}
+
+// Keep rates and amplification of a sampled tree (Booster.swift:1401-1434).
+static mbk::SampleParams sample_params(const Trainer &t, int tree) {
+    const Params &p = t.p;
+    mbk::SampleParams s{};
+    s.goss = p.goss ? 1 : 0;
+    s.top_count = p.goss ? (uint32_t)((float)t.rows * p.goss_top_rate) : 0u;
+    s.other_prob = p.goss ? p.goss_other_rate / (1.0f - p.goss_top_rate) : p.subsample;
+    s.weight = p.goss ? (1.0f - p.goss_top_rate) / p.goss_other_rate : 1.0f;
+    s.seed = (uint32_t)tree + 1u;
+    return s;
+}
+
+// Gradients, maxima and the tree's order entries: every row quantised, or
+// the rows a GOSS / bagging tree keeps (their count stays on the device).
+static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *order) {
+    hipStream_t s = t.dev->stream;
+    MB_HIP(mbk::launch_tree_init(s, ctl));
+    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
+                                t.gmax_part.ptr));
+    const bool sampled = tree_sampled(t.p, tree);
+    if (sampled)
+        MB_HIP(mbk::launch_sample(s, t.gp, sample_params(t, tree), t.preds.ptr, t.labels.ptr,
+                                  t.weights.ptr, t.rows, ctl, t.goss_buckets.ptr,
+                                  t.gmax_part.ptr, order));
+    else
+        MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
+                                    ctl, order));
+    return sampled;
+}
+
 static void grow_levelwise(Trainer &t, int tree) {
     hipStream_t s = t.dev->stream;
     const mbk::Shape &sh = t.sh;
@@ -646,12 +685,9 @@ static void grow_levelwise(Trainer &t, int tree) {
     if (const uint8_t *m = tree_feature_mask(t, tree))
         MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
     mbk::TreeCtl *ctl = t.ctl.ptr;
-    MB_HIP(mbk::launch_tree_init(s, ctl));
-    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
-                                t.gmax_part.ptr));
-    MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
-                                t.order_a.ptr));
-    MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)t.rows, (uint32_t)t.target_items,
+    const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr);
+    MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
+                                 (uint32_t)t.target_items,
                                  (uint32_t)t.min_chunk, ctl, t.seg_a.ptr, t.count.ptr, t.pairs.ptr,
                                  t.items.ptr, out.cover, t.bounds.ptr, -INFINITY, INFINITY,
                                  t.scratch.ptr));
@@ -686,16 +722,32 @@ static void grow_levelwise(Trainer &t, int tree) {
         const bool terminal = d == t.D;
         mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
         mbk::LevelArgs ln{d, (uint32_t)((1u << d) - 1), 1u << d, terminal ? 1u : 0u};
-        if (terminal) {
+        if (terminal && !sampled) {
             // deepest level: leaf values, then one walk of the finished tree over
             // the training rows adds every row's leaf (the single addition the
             // partition-time update makes, route_samples apply,
             // Shaders.swift:1280-1311) and counts the deepest nodes' rows
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
-                                            t.bounds.ptr, ctl, out));
+                                            t.bounds.ptr, ctl, out, false));
             MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr,
                                           t.count.ptr));
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
+            break;
+        }
+        if (terminal) {
+            // a sampled tree counts its kept rows with the partition; every
+            // row's prediction then comes from one walk (Booster.swift:1568-1580)
+            MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
+                                     t.count.ptr, out, t.route_blk.ptr, t.route_cursor.ptr,
+                                     t.route_grid, false));
+            MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items,
+                                          (uint32_t)t.min_chunk, ctl, seg_cur, seg_next,
+                                          t.count.ptr, t.route_cursor.ptr, out, t.pairs.ptr,
+                                          t.items.ptr, t.scratch.ptr));
+            MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
+                                            t.bounds.ptr, ctl, out, true));
+            MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
+                                              t.preds.ptr));
             break;
         }
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
@@ -734,13 +786,10 @@ static void grow_leafwise(Trainer &t, int tree) {
         MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
     mbk::TreeCtl *ctl = t.ctl.ptr;
     mbk::Entry *order = t.order_a.ptr;
-    MB_HIP(mbk::launch_tree_init(s, ctl));
-    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
-                                t.gmax_part.ptr));
-    MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
-                                order));
+    const bool sampled = tree_entries(t, tree, ctl, order);
     MB_HIP(mbk::launch_lw_init(s, sh, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
-                               t.count.ptr, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out));
+                               t.count.ptr, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out,
+                               sampled));
     auto build_and_eval = [&](int step) {
         hipEvent_t e0 = nullptr, e1 = nullptr;
         if (t.profiling) {

@@ -401,6 +401,9 @@ typedef struct {
     const float *edges;
     const uint32_t *ghq;
     float g_inv, h_inv;
+    const uint32_t *rows_in;    /* the tree's rows (ascending); NULL = all rows */
+    int64_t n_in;
+    int apply_preds;            /* 0: preds are updated by a walk after the tree */
 } fit_ctx;
 
 static void best_over_features(const fit_ctx *c, const int64_t *hg, const int64_t *hh,
@@ -513,7 +516,12 @@ static int grow_levelwise(const fit_ctx *c, float *preds, orc_forest *out, int64
         return -1;
     }
     for (int32_t n = 0; n < total; ++n) { blo[n] = -INFINITY; bhi[n] = INFINITY; }
-    for (int64_t i = 0; i < N; ++i) order[i] = (uint32_t)i;
+    if (c->rows_in) {
+        memcpy(order, c->rows_in, sizeof(uint32_t) * (size_t)c->n_in);
+        N = c->n_in;
+    } else {
+        for (int64_t i = 0; i < N; ++i) order[i] = (uint32_t)i;
+    }
     cnt[0] = N; seg[0] = 0;
     int32_t *split_f = (int32_t *)malloc(sizeof(int32_t) * (size_t)total);
     for (int32_t n = 0; n < total; ++n) split_f[n] = -1;
@@ -576,7 +584,8 @@ static int grow_levelwise(const fit_ctx *c, float *preds, orc_forest *out, int64
                 out->feature[base + n] = -1;
                 out->leaf[base + n] = v;
                 out->gain[base + n] = 0.0f;
-                for (int64_t r = 0; r < cnt[n]; ++r) preds[order[seg[n] + r]] += v;
+                if (c->apply_preds)
+                    for (int64_t r = 0; r < cnt[n]; ++r) preds[order[seg[n] + r]] += v;
             }
         }
         /* Next level's segment layout: children in heap order, every split
@@ -615,7 +624,8 @@ static int grow_levelwise(const fit_ctx *c, float *preds, orc_forest *out, int64
             if (cnt[n] >= 1) {
                 float v = leaf_value(c, gi[n], hi[n], blo[n], bhi[n]);
                 out->leaf[base + n] = v;
-                for (int64_t r = 0; r < cnt[n]; ++r) preds[order[seg[n] + r]] += v;
+                if (c->apply_preds)
+                    for (int64_t r = 0; r < cnt[n]; ++r) preds[order[seg[n] + r]] += v;
             } else {
                 out->leaf[base + n] = 0.0f;
             }
@@ -626,6 +636,26 @@ static int grow_levelwise(const fit_ctx *c, float *preds, orc_forest *out, int64
     free(cnt); free(seg); free(gi); free(hi); free(blo); free(bhi); free(cur_g);
     free(cur_h); free(prv_g); free(prv_h); free(order); free(tmp);
     return 0;
+}
+
+/* Train preds: one walk of the finished tree over every binned row
+ * (predict_tree_binned, Shaders.swift:1763-1781). */
+static void walk_preds(const fit_ctx *c, const orc_forest *out, int64_t base, float *preds) {
+    const int32_t D = c->p->max_depth, nb = c->nb;
+    const int64_t N = c->rows;
+    for (int64_t i = 0; i < N; ++i) {
+        int32_t n = 0;
+        for (int32_t d = 0; d < D; ++d) {
+            int32_t f = out->feature[base + n];
+            if (f < 0) break;
+            uint8_t b = c->fm[(int64_t)f * N + i];
+            const uint32_t *mask = out->cat_mask ? out->cat_mask + (base + n) * 8 : NULL;
+            uint32_t zero[8] = {0};
+            n = 2 * n + 1 + (bin_goes_left(b, out->split_bin[base + n], out->flags[base + n],
+                                           mask ? mask : zero, nb) ? 0 : 1);
+        }
+        preds[i] += out->leaf[base + n];
+    }
 }
 
 /* Leaf-wise (best-first) growth: leaf_reset/leaf_init/leaf_pick_apply and the
@@ -643,6 +673,7 @@ static int grow_leafwise(const fit_ctx *c, float *preds, orc_forest *out, int64_
     int32_t D = p->max_depth, F = c->cols, nb = c->nb, L = p->num_leaves;
     int32_t total = (1 << (D + 1)) - 1;
     int64_t slice = (int64_t)F * nb, N = c->rows;
+    const int64_t n_tree = c->rows_in ? c->n_in : N;
     float *blo = (float *)malloc(sizeof(float) * (size_t)total);
     float *bhi = (float *)malloc(sizeof(float) * (size_t)total);
     lw_open *open = (lw_open *)calloc((size_t)(2 * L + 2), sizeof(lw_open));
@@ -661,16 +692,17 @@ static int grow_leafwise(const fit_ctx *c, float *preds, orc_forest *out, int64_
         if (out->cat_mask) memset(out->cat_mask + (base + n) * 8, 0, 32);
         blo[n] = -FLT_MAX; bhi[n] = FLT_MAX;
     }
-    for (int64_t i = 0; i < N; ++i) order[i] = (uint32_t)i;
+    if (c->rows_in) memcpy(order, c->rows_in, sizeof(uint32_t) * (size_t)n_tree);
+    else for (int64_t i = 0; i < N; ++i) order[i] = (uint32_t)i;
     /* leaf_init (Shaders.swift:683-716) */
-    hist_rows_rm(c->rm, F, nb, c->ghq, order, N, hg, hh);
+    hist_rows_rm(c->rm, F, nb, c->ghq, order, n_tree, hg, hh);
     int64_t G0 = 0, H0 = 0;
     for (int32_t b = 0; b < nb; ++b) { G0 += hg[b]; H0 += hh[b]; }
-    open[0].node = 0; open[0].seg = 0; open[0].count = N; open[0].G = G0; open[0].H = H0;
+    open[0].node = 0; open[0].seg = 0; open[0].count = n_tree; open[0].G = G0; open[0].H = H0;
     open[0].depth = 0;
     best_over_features(c, hg, hh, G0, H0, feat_mask, &open[0].best_f, &open[0].best);
     out->leaf[base + 0] = leaf_value(c, G0, H0, -FLT_MAX, FLT_MAX);
-    out->cover[base + 0] = (float)N;
+    out->cover[base + 0] = (float)n_tree;
     int32_t open_count = 1, leaves = 1, done = 0;
     for (int32_t it = 1; it < L; ++it) {
         if (done || leaves >= L) { done = 1; continue; }
@@ -725,22 +757,79 @@ static int grow_leafwise(const fit_ctx *c, float *preds, orc_forest *out, int64_
         open[i0] = cl;
         open[i1] = cr;
     }
-    /* train preds: predict_tree_binned over every row (Shaders.swift:1763-1781) */
-    for (int64_t i = 0; i < N; ++i) {
-        int32_t n = 0;
-        for (int32_t d = 0; d < D; ++d) {
-            int32_t f = out->feature[base + n];
-            if (f < 0) break;
-            uint8_t b = c->fm[(int64_t)f * N + i];
-            const uint32_t *mask = out->cat_mask ? out->cat_mask + (base + n) * 8 : NULL;
-            uint32_t zero[8] = {0};
-            n = 2 * n + 1 + (bin_goes_left(b, out->split_bin[base + n], out->flags[base + n],
-                                           mask ? mask : zero, nb) ? 0 : 1);
-        }
-        preds[i] += out->leaf[base + n];
-    }
+    walk_preds(c, out, base, preds);
     free(blo); free(bhi); free(open); free(order); free(tmp); free(hg); free(hh);
     return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Row sampling: GOSS and bagging                                           */
+/* ------------------------------------------------------------------------ */
+
+/* gossActive / bagging (Booster.swift:1382-1384): GOSS after ceil(1/lr)
+ * warm-up trees, bagging on every tree. */
+int orc_sampling_active(const orc_params *p, int32_t tree) {
+    if (p->goss) return tree >= (int32_t)ceilf(1.0f / p->learning_rate);
+    return p->subsample < 1.0f;
+}
+
+static inline uint32_t wang_hash(uint32_t x) {                    /* :1144-1148 */
+    x = (x ^ 61u) ^ (x >> 16);
+    x *= 9u;
+    x ^= x >> 4;
+    x *= 0x27d4eb2du;
+    x ^= x >> 15;
+    return x;
+}
+
+int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, int64_t rows,
+                        float max_g, uint8_t *kept, float *wmax_g, float *wmax_h) {
+    const int goss = p->goss != 0;
+    /* keep threshold: lower edge of the |g| bucket where the count from the
+     * top reaches topCount (goss_grad_hist / goss_threshold, :1104-1138);
+     * bagging uses topCount = 0, i.e. the threshold max|g| */
+    uint32_t b = 1024;
+    if (goss && max_g > 0.0f) {
+        uint32_t buckets[1024] = {0};
+        for (int64_t i = 0; i < rows; ++i) {
+            uint32_t k = (uint32_t)(fabsf(g[i]) / max_g * 1024.0f);
+            buckets[k < 1023u ? k : 1023u] += 1;
+        }
+        const uint32_t top = (uint32_t)((float)rows * p->goss_top_rate);
+        uint32_t cum = 0;
+        while (b > 0 && cum < top) { b -= 1; cum += buckets[b]; }
+    }
+    const float thr = max_g > 0.0f ? (float)b / 1024.0f * max_g : 0.0f;
+    const float other = goss ? p->goss_other_rate / (1.0f - p->goss_top_rate) : p->subsample;
+    const float weight = goss ? (1.0f - p->goss_top_rate) / p->goss_other_rate : 1.0f;
+    const uint32_t seed = (uint32_t)tree + 1u;
+    /* keep the top rows, and a hashed uniform sample of the rest amplified by
+     * `weight` (goss_select, :1150-1199) */
+    uint32_t mgb = 0, mhb = 0;
+    int64_t n = 0;
+    for (int64_t i = 0; i < rows; ++i) {
+        const float ag = fabsf(g[i]);
+        int keep = 0;
+        float w = 1.0f;
+        if (ag >= thr) {
+            keep = 1;
+        } else {
+            const uint32_t hv = wang_hash((uint32_t)i ^ (seed * 0x9E3779B9u));
+            if ((float)(hv >> 8) * (1.0f / 16777216.0f) < other) { keep = 1; w = weight; }
+        }
+        const float hw = h[i] * w;
+        kept[i] = (uint8_t)keep;
+        if (!keep) continue;
+        if (w != 1.0f) { g[i] = g[i] * w; h[i] = hw; }
+        const float agw = ag * w;
+        uint32_t u;
+        memcpy(&u, &agw, 4); if (u > mgb) mgb = u;
+        memcpy(&u, &hw, 4); if (u > mhb) mhb = u;
+        ++n;
+    }
+    memcpy(wmax_g, &mgb, 4);
+    memcpy(wmax_h, &mhb, 4);
+    return n;
 }
 
 int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t cols,
@@ -754,8 +843,13 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
     float *g = (float *)malloc(sizeof(float) * (size_t)rows);
     float *h = (float *)malloc(sizeof(float) * (size_t)rows);
     uint32_t *ghq = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)rows);
+    uint8_t *kept = (uint8_t *)malloc((size_t)rows);
+    uint32_t *sel = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)rows);
     uint32_t *split_bin = out->split_bin;
-    if (!rm || !g || !h || !ghq) { free(rm); free(g); free(h); free(ghq); return -1; }
+    if (!rm || !g || !h || !ghq || !kept || !sel) {
+        free(rm); free(g); free(h); free(ghq); free(kept); free(sel);
+        return -1;
+    }
     for (int32_t f = 0; f < cols; ++f)
         for (int64_t i = 0; i < rows; ++i) rm[i * cols + f] = bins_fm[(int64_t)f * rows + i];
     if (!split_bin) out->split_bin = (uint32_t *)calloc((size_t)p->num_trees * total, 4);
@@ -770,14 +864,32 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
         }
         float mg, mh;
         orc_gradients(preds, y, w, rows, p->objective, p->alpha, p->aux, g, h, &mg, &mh);
+        const uint32_t *rows_in = NULL;
+        int64_t n_in = rows;
+        if (orc_sampling_active(p, t)) {
+            /* the tree is built from the kept rows only (Booster.swift:1401-1445) */
+            float wg, wh;
+            n_in = orc_sample_rows(p, t, g, h, rows, mg, kept, &wg, &wh);
+            mg = wg; mh = wh;
+            int64_t k2 = 0;
+            for (int64_t i = 0; i < rows; ++i)
+                if (kept[i]) sel[k2++] = (uint32_t)i;
+            rows_in = sel;
+        }
         orc_quantize(g, h, rows, mg, mh, ghq);
         fit_ctx c;
         c.p = p; c.rm = rm; c.fm = bins_fm; c.rows = rows; c.cols = cols; c.nb = nb;
         c.is_cat = is_cat; c.mono = monotone; c.edges = edges; c.ghq = ghq;
         c.g_inv = mg / 32767.0f;
         c.h_inv = mh / 127.0f;
+        c.rows_in = rows_in;
+        c.n_in = n_in;
+        c.apply_preds = rows_in == NULL;
         rc = p->num_leaves > 0 ? grow_leafwise(&c, preds, out, base, NULL)
                                : grow_levelwise(&c, preds, out, base, NULL);
+        /* sampled level-wise trees: every row's prediction from one walk
+         * (Booster.swift:1568-1580); leaf-wise growth always walks */
+        if (rc == 0 && rows_in && p->num_leaves <= 0) walk_preds(&c, out, base, preds);
         /* reachable nodes only (Booster.swift:918-945) */
         {
             uint8_t *reach = (uint8_t *)calloc((size_t)total, 1);
@@ -807,7 +919,7 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
         }
     }
     if (!split_bin) { free(out->split_bin); out->split_bin = NULL; }
-    free(rm); free(g); free(h); free(ghq);
+    free(rm); free(g); free(h); free(ghq); free(kept); free(sel);
     return rc;
 }
 

@@ -41,6 +41,10 @@ typedef struct {
     float cat_smooth;
     float alpha;
     float aux;                 /* scale_pos_weight (logistic) / variance power (tweedie) */
+    int32_t goss;              /* 1: GOSS after ceil(1/learning_rate) warm-up trees */
+    float goss_top_rate;
+    float goss_other_rate;
+    float subsample;           /* bagging fraction, 1 = off */
 } orc_params;
 
 /* One split candidate result: SplitResult (Shaders.swift:334) plus the exact
@@ -103,6 +107,16 @@ int32_t orc_cat_order(const int64_t *hg, const int64_t *hh, int32_t num_bins,
                       float g_inv, float h_inv, float cat_smooth, uint16_t *order);
 
 /* --- training (Booster.swift:445-1701 level-wise / :967-1310 leaf-wise) -- */
+/* Row sampling for tree `tree` (0-based): goss_grad_hist, goss_threshold and
+ * goss_select (Shaders.swift:1093-1221) as driven by Booster.swift:1382-1445.
+ * orc_sampling_active says whether the tree samples at all.  g and h are the
+ * tree's gradients; amplified rows are scaled in place.  max_g is the
+ * unweighted max |g|.  kept[i] = 1 for kept rows; returns their count and the
+ * maxima of |g|*w and h*w over them (quantisation uses these). */
+int orc_sampling_active(const orc_params *p, int32_t tree);
+int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, int64_t rows,
+                        float max_g, uint8_t *kept, float *wmax_g, float *wmax_h);
+
 int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t cols,
             const float *y, const float *w, const uint8_t *is_cat, const int8_t *monotone,
             const float *edges, float base_score, float *preds, orc_forest *out);

@@ -45,6 +45,8 @@ class OrcParams(ctypes.Structure):
         ("lambda_", ctypes.c_float), ("min_child_hess", ctypes.c_float),
         ("min_split_gain", ctypes.c_float), ("cat_smooth", ctypes.c_float),
         ("alpha", ctypes.c_float), ("aux", ctypes.c_float),
+        ("goss", ctypes.c_int32), ("goss_top_rate", ctypes.c_float),
+        ("goss_other_rate", ctypes.c_float), ("subsample", ctypes.c_float),
     ]
 
 
@@ -266,10 +268,12 @@ class OracleModel:
 def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objective=OBJ_L2,
         num_leaves=0, learning_rate=0.1, lam=1.0, min_child_hess=1.0, min_split_gain=0.0,
         cat_smooth=10.0, alpha=0.9, aux=1.0, w=None, is_cat=None, monotone=None,
-        base=None) -> OracleModel:
+        base=None, goss=False, goss_top_rate=0.2, goss_other_rate=0.1,
+        subsample=1.0) -> OracleModel:
     cols, rows = bins_fm.shape
     p = OrcParams(num_trees, max_depth, num_bins, objective, num_leaves, learning_rate, lam,
-                  min_child_hess, min_split_gain, cat_smooth, alpha, aux)
+                  min_child_hess, min_split_gain, cat_smooth, alpha, aux, int(goss),
+                  goss_top_rate, goss_other_rate, subsample)
     y = np.ascontiguousarray(y, np.float32)
     w = None if w is None else np.ascontiguousarray(w, np.float32)
     if base is None:
@@ -310,6 +314,32 @@ def treeshap(forest: Forest, base: float, num_bins: int, x_fm) -> np.ndarray:
 def shap_bias(forest: Forest, base: float) -> float:
     fc = forest.c()
     return float(lib().orc_shap_bias(ctypes.byref(fc), base))
+
+
+def sample_rows(g, h, max_g, tree, *, learning_rate=0.1, goss=False, goss_top_rate=0.2,
+                goss_other_rate=0.1, subsample=1.0):
+    """orc_sample_rows: (kept mask, amplified g, amplified h, wmax_g, wmax_h),
+    or None when the tree does not sample."""
+    p = OrcParams(1, 6, 256, OBJ_L2, 0, learning_rate, 1.0, 1.0, 0.0, 10.0, 0.9, 1.0,
+                  int(goss), goss_top_rate, goss_other_rate, subsample)
+    l = lib()
+    l.orc_sampling_active.restype = ctypes.c_int
+    l.orc_sampling_active.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+    if not l.orc_sampling_active(ctypes.byref(p), tree):
+        return None
+    g = np.array(g, np.float32)
+    h = np.array(h, np.float32)
+    kept = np.zeros(len(g), np.uint8)
+    wg = np.zeros(1, np.float32)
+    wh = np.zeros(1, np.float32)
+    l.orc_sample_rows.restype = ctypes.c_int64
+    l.orc_sample_rows.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
+                                  ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    n = l.orc_sample_rows(ctypes.byref(p), tree, _ptr(g), _ptr(h), len(g), max_g, _ptr(kept),
+                          _ptr(wg), _ptr(wh))
+    assert n == int(kept.sum())
+    return kept.astype(bool), g, h, float(wg[0]), float(wh[0])
 
 
 def fit_raw(x_fm, y, num_bins=256, is_cat=None, **kw) -> OracleModel:

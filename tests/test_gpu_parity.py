@@ -44,6 +44,9 @@ def oracle_fit(x_fm, y, params, is_cat=None):
     kw["objective"] = {"regression": O.OBJ_L2, "binary": O.OBJ_LOGISTIC}[obj]
     mono = p.pop("monotone_constraints", None)
     p.pop("categorical_features", None)
+    for key in ("goss", "goss_top_rate", "goss_other_rate", "subsample"):
+        if key in p:
+            kw[key] = p.pop(key)
     assert not p, p
     return O.fit_raw(x_fm, y, num_bins=nb, is_cat=is_cat, monotone=mono, **kw)
 
@@ -318,6 +321,29 @@ def test_c4_higgs_like_logistic_identical_trees():
     x, y = D.c4_higgs_like(200_000, 42)
     xt, _ = D.c4_higgs_like(50_000, 43)
     check_identical(x, y, {"num_trees": 10, "max_depth": 6, "objective": "binary"}, x_test=xt)
+
+
+@pytest.mark.parametrize("params", [
+    {"goss": True},
+    {"goss": True, "goss_top_rate": 0.3, "goss_other_rate": 0.2, "num_leaves": 23},
+    {"subsample": 0.5},
+    {"subsample": 0.7, "num_leaves": 31},
+])
+def test_goss_and_bagging_identical_trees(params):
+    # Shaders.swift:1093-1221: the same rows are kept, amplified and
+    # quantised, so the sampled trees and every row's prediction match
+    x, y = mb.friedman(20_000, 12, 31)
+    xt, _ = mb.friedman(4000, 12, 32)
+    check_identical(x, y, dict({"num_trees": 25, "max_depth": 6}, **params), x_test=xt)
+
+
+def test_goss_logistic_nan_categorical_identical_trees():
+    # GOSSTests.swift:108-130 runs GOSS with NaN and categorical features
+    x, y = _mixed(15_000)
+    yb = (y > np.median(y)).astype(np.float32)
+    check_identical(x, yb, {"num_trees": 20, "max_depth": 5, "objective": "binary",
+                            "goss": True, "categorical_features": [6]},
+                    is_cat=[0] * 6 + [1], x_test=x[:, :2000].copy())
 
 
 def _first_trees(forest, k):

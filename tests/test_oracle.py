@@ -496,3 +496,105 @@ def test_shap_matches_bruteforce_shapley(oracle):
                         phi[j] += wgt * (v[Sj] - v[S])
         assert np.allclose(c[i, :M], phi, rtol=1e-5, atol=1e-6)
     assert c[0, M] == pytest.approx(O.shap_bias(fo, m.base_score), rel=1e-6)
+
+
+# --------------------------------------------------------------------------
+# GOSS and bagging (Shaders.swift:1093-1221, Booster.swift:1382-1445)
+# --------------------------------------------------------------------------
+
+def _same_forest(a, b):
+    for name in ("feature", "threshold", "leaf", "flags", "gain", "cover"):
+        if not np.array_equal(getattr(a.forest, name), getattr(b.forest, name)):
+            return False
+    return np.array_equal(a.preds, b.preds)
+
+
+def test_goss_with_everything_kept_equals_full_training(oracle):
+    # top 0.5 + other 0.5: keep probability and amplification are exactly 1,
+    # so every sampled tree sees all rows at weight 1 (GOSSTests.swift:24-40
+    # checks the near-degenerate case to an RMSE tolerance)
+    x, y = O.friedman(8000, 8, 51)
+    full = fit_raw(x, y, num_trees=25, max_depth=5)
+    goss = fit_raw(x, y, num_trees=25, max_depth=5, goss=True, goss_top_rate=0.5,
+                   goss_other_rate=0.5)
+    assert _same_forest(full, goss)
+
+
+def test_goss_warmup_trees_use_full_data(oracle):
+    # GOSSTests.swift:42-60: the first ceil(1/lr) trees are not sampled
+    x, y = O.friedman(8000, 8, 53)
+    full = fit_raw(x, y, num_trees=2, max_depth=5, learning_rate=0.5)
+    goss = fit_raw(x, y, num_trees=2, max_depth=5, learning_rate=0.5, goss=True,
+                   goss_top_rate=0.05, goss_other_rate=0.05)
+    assert _same_forest(full, goss)
+
+
+def test_goss_sampling_engages(oracle):
+    # GOSSTests.swift:62-80: 2% sampling must be visibly worse than full data
+    x, y = O.friedman(30_000, 8, 55)
+    xv, yv = O.friedman(5000, 8, 56)
+    full = fit_raw(x, y, num_trees=80, max_depth=5)
+    tiny = fit_raw(x, y, num_trees=80, max_depth=5, goss=True, goss_top_rate=0.01,
+                   goss_other_rate=0.01)
+    assert rmse(predict(tiny, xv), yv) > rmse(predict(full, xv), yv) + 0.03
+
+
+def test_goss_binary_logistic_floor(oracle):
+    # GOSSTests.swift:84-106
+    rows = 20_000
+    rng = O.SplitMix(57)
+    x = np.array([rng.uniform() for _ in range(rows * 4)], np.float32).reshape(4, rows)
+    y = np.array([1.0 if (x[0, i] + x[1, i] + np.float32(0.3) * np.float32(rng.normal())) > 1
+                  else 0.0 for i in range(rows)], np.float32)
+    m = fit_raw(x, y, num_trees=60, max_depth=5, objective=O.OBJ_LOGISTIC, goss=True)
+    p = 1.0 / (1.0 + np.exp(-predict(m, x).astype(np.float64)))
+    ll = -np.mean(y * np.log(np.maximum(p, 1e-12)) + (1 - y) * np.log(np.maximum(1 - p, 1e-12)))
+    assert ll < 0.44
+
+
+def test_goss_selection_properties(oracle):
+    # The keep rule of goss_select: a |g| threshold on a 1/1024 grid of max|g|
+    # whose top set holds at least floor(rows * topRate) rows, then a hashed
+    # uniform sample of the rest at otherRate / (1 - topRate), amplified by
+    # (1 - topRate) / otherRate; the quantisation maxima are over kept rows.
+    rng = np.random.default_rng(5)
+    n = 200_000
+    g = (rng.standard_normal(n) * rng.exponential(1.0, n)).astype(np.float32)
+    h = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    mg = float(np.max(np.abs(g)))
+    top, other = 0.2, 0.1
+    kept, g2, h2, wg, wh = O.sample_rows(g, h, mg, 10, goss=True, goss_top_rate=top,
+                                         goss_other_rate=other)
+    w = np.float32((np.float32(1) - np.float32(top)) / np.float32(other))
+    unit = kept & (g2 == g)
+    amp = kept & ~unit
+    assert np.array_equal(g2[amp], g[amp] * w) and np.array_equal(h2[amp], h[amp] * w)
+    assert np.array_equal(g2[~amp], g[~amp]) and np.array_equal(h2[~amp], h[~amp])
+    thr = np.abs(g[unit]).min()
+    assert (np.abs(g[~unit]) < thr).all()                 # the top set is a threshold set
+    assert unit.sum() >= int(np.float32(n) * np.float32(top))
+    edge = np.floor(thr / np.float32(mg) * 1024)          # threshold sits on the bucket grid
+    assert (np.abs(g[unit]) >= np.float32(edge / 1024) * np.float32(mg)).all()
+    rest = ~unit
+    frac = amp.sum() / rest.sum()
+    p = other / (1 - top)
+    assert abs(frac - p) < 5 * np.sqrt(p * (1 - p) / rest.sum())
+    assert wg == np.max(np.abs(g2[kept])) and wh == np.max(h2[kept])
+    again = O.sample_rows(g, h, mg, 10, goss=True, goss_top_rate=top, goss_other_rate=other)
+    assert np.array_equal(again[0], kept)                  # deterministic for a tree
+    other_tree = O.sample_rows(g, h, mg, 11, goss=True, goss_top_rate=top, goss_other_rate=other)
+    assert not np.array_equal(other_tree[0], kept)         # reseeded per tree
+    assert O.sample_rows(g, h, mg, 9, goss=True, learning_rate=0.1) is None   # warm-up
+
+
+def test_bagging_selection_properties(oracle):
+    rng = np.random.default_rng(6)
+    n = 200_000
+    g = rng.standard_normal(n).astype(np.float32)
+    h = np.ones(n, np.float32)
+    mg = float(np.max(np.abs(g)))
+    kept, g2, h2, wg, wh = O.sample_rows(g, h, mg, 0, subsample=0.3)
+    assert np.array_equal(g2, g) and np.array_equal(h2, h)   # bagging never amplifies
+    assert kept[np.argmax(np.abs(g))]                       # |g| = max|g| is always kept
+    assert abs(kept.mean() - 0.3) < 5 * np.sqrt(0.3 * 0.7 / n)
+    assert O.sample_rows(g, h, mg, 0) is None               # subsample 1: no sampling
