@@ -261,7 +261,7 @@ def main():
         "cpu_baseline": cpu,
         "rows_per_s": rows * value,
         "fit_seconds_100_trees_incl_binning": fit_total,
-        "setup_seconds": {"edges_host": t_edges, "upload_and_bin": t_bin, "total": t_setup},
+        "setup_seconds": {"edges_device": t_edges, "upload_and_bin": t_bin, "total": t_setup},
         "valid_rmse": rmse,
         "leafwise_predict_treeshap": extras,
     }

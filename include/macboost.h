@@ -83,6 +83,16 @@ int mbk_copy_to_device(mbk_context *ctx, void *dst, const void *src, size_t byte
 int mbk_copy_to_host(mbk_context *ctx, void *dst, const void *src, size_t bytes, char **err);
 int mbk_synchronize(mbk_context *ctx, char **err);
 
+/* computeEdges (Binner.swift:25-56) on the device: per non-categorical
+ * feature, the stride subsample (step = max(1, rows / 200000)) of non-NaN
+ * values, sorted; edges[f*(num_bins-2) + k] = sample[min(m-1, (k+1)*m/(num_bins-1))].
+ * Categorical and all-NaN features get zero edges.  x is device memory read
+ * as x[i*row_stride + f*col_stride]; edges is device memory.  The sort
+ * scratch (2 * cols * ceil(rows/step) u32) is allocated inside the call. */
+int mbk_quantile_edges(mbk_context *ctx, const float *x, int64_t rows, int32_t cols,
+                       int64_t row_stride, int64_t col_stride, int32_t num_bins,
+                       const uint8_t *is_cat, float *edges, char **err);
+
 /* bin_data (Shaders.swift:46-76): raw f32 -> bins in two layouts, the
  * gather layout bins_tiled [rows][ceil(cols/tile_width)][tile_width] (row-major,
  * each row padded to a whole number of tiles with zero bytes) and the

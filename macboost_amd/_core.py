@@ -98,6 +98,9 @@ def _configure(l):
         getattr(l, n).argtypes = [_P, _P, _P, ctypes.c_size_t, _c_char_pp]
     l.mbk_synchronize.restype = ctypes.c_int
     l.mbk_synchronize.argtypes = [_P, _c_char_pp]
+    l.mbk_quantile_edges.restype = ctypes.c_int
+    l.mbk_quantile_edges.argtypes = [_P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                     ctypes.c_int64, ctypes.c_int32, _P, _P, _c_char_pp]
     l.mbk_bin_data.restype = ctypes.c_int
     l.mbk_bin_data.argtypes = [_P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                ctypes.c_int64, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P,
@@ -147,7 +150,7 @@ EXPORTED = (
     "macboost_num_trees", "macboost_num_features", "macboost_best_iteration",
     "macboost_warnings", "macboost_free", "macboost_free_string",
     "mbk_context_create", "mbk_context_destroy", "mbk_device_alloc", "mbk_device_free",
-    "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_bin_data", "mbk_quantize",
+    "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_quantile_edges", "mbk_bin_data", "mbk_quantize",
     "mbk_node_hist_split", "mbk_predict_forest",
     "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
     "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",

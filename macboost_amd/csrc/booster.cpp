@@ -678,6 +678,21 @@ int mbk_synchronize(mbk_context *ctx, char **err) {
     }, -1);
 }
 
+int mbk_quantile_edges(mbk_context *ctx, const float *x, int64_t rows, int32_t cols,
+                       int64_t row_stride, int64_t col_stride, int32_t num_bins,
+                       const uint8_t *is_cat, float *edges, char **err) {
+    return guarded(err, [&]() -> int {
+        if (num_bins < 4 || num_bins > 256) mb::invalid("numBins must be in 4...256");
+        if (rows < 1 || cols < 1) mb::invalid("rows and cols must be positive");
+        const size_t cap = mbk::edge_sample_cap(rows);
+        mb::DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
+        MB_HIP(mbk::launch_edges(ctx->dev->stream, x, rows, cols, row_stride, col_stride,
+                                 num_bins, is_cat, ka.ptr, kb.ptr, cnt.ptr, edges));
+        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
+        return 0;
+    }, -1);
+}
+
 int mbk_bin_data(mbk_context *ctx, const float *x, int64_t rows, int32_t cols, int64_t row_stride,
                  int64_t col_stride, const float *edges, const uint8_t *is_cat, int32_t num_bins,
                  int32_t tile_width, uint8_t *bins_tiled, uint8_t *bins_fm, char **err) {

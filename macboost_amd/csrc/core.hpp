@@ -177,8 +177,6 @@ Booster *trainer_booster(Trainer *t);
 void trainer_free(Trainer *t);
 
 // Shared helpers.
-std::vector<float> compute_edges(const float *x, int64_t rows, int64_t cols, int64_t rs,
-                                 int64_t cs, int num_bins, const std::vector<uint8_t> &is_cat);
 std::string swift_float(float v);
 int host_threads();
 

@@ -205,6 +205,154 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
 }
 
 // ---------------------------------------------------------------------------
+// quantile edges on the device (Binner.swift:25-56): per feature, the stride
+// subsample of non-NaN values, sorted, edge k = sample[min(m-1, (k+1)*m/dataBins)].
+// One 1024-thread workgroup per feature: compact the sample as order-
+// preserving u32 keys, then a stable LSD radix sort (8 passes of 4 bits;
+// ranks inside a wavefront from ballots, wavefronts and tiles in order).
+// ---------------------------------------------------------------------------
+
+constexpr int EDGE_THREADS = 1024;
+constexpr int EDGE_WAVES = EDGE_THREADS / 64;
+
+__device__ __forceinline__ uint32_t float_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+__global__ __launch_bounds__(EDGE_THREADS) void k_edge_sample(const float *__restrict__ x,
+                                                              int64_t rows, int64_t rs,
+                                                              int64_t cs, int64_t step,
+                                                              uint32_t cap,
+                                                              const uint8_t *__restrict__ is_cat,
+                                                              uint32_t *__restrict__ keys,
+                                                              uint32_t *__restrict__ counts) {
+    __shared__ uint32_t wt[EDGE_WAVES + 1];
+    const int f = blockIdx.x, tid = threadIdx.x, w = tid >> 6;
+    uint32_t *out = keys + (size_t)f * cap;
+    uint32_t run = 0;
+    if (!is_cat[f]) {
+        const int64_t ns = (rows + step - 1) / step;     // samples i = 0, step, 2*step, ...
+        for (int64_t base = 0; base < ns; base += EDGE_THREADS) {
+            const int64_t s = base + tid;
+            float v = 0.0f;
+            uint32_t ok = 0;
+            if (s < ns) {
+                v = x[s * step * rs + (int64_t)f * cs];
+                ok = isnan(v) ? 0u : 1u;
+            }
+            const uint32_t inc = wave_inclusive_scan(ok);
+            if (lane_id() == 63) wt[w] = inc;
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t acc = 0;
+                for (int k = 0; k < EDGE_WAVES; ++k) { const uint32_t t = wt[k]; wt[k] = acc; acc += t; }
+                wt[EDGE_WAVES] = acc;
+            }
+            __syncthreads();
+            if (ok) out[run + wt[w] + inc - 1] = float_key(v);
+            run += wt[EDGE_WAVES];
+            __syncthreads();
+        }
+    }
+    if (tid == 0) counts[f] = run;
+}
+
+// Stable LSD radix sort of each feature's keys (a -> b -> a ... 8 passes;
+// the result ends in a).
+__global__ __launch_bounds__(EDGE_THREADS) void k_edge_sort(uint32_t *__restrict__ keys_a,
+                                                            uint32_t *__restrict__ keys_b,
+                                                            uint32_t cap,
+                                                            const uint32_t *__restrict__ counts) {
+    __shared__ uint32_t hist[16];
+    __shared__ uint32_t cnt[EDGE_WAVES][16];
+    __shared__ uint32_t off[EDGE_WAVES][16];
+    const int f = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = lane_id();
+    const uint32_t m = counts[f];
+    uint32_t *src = keys_a + (size_t)f * cap, *dst = keys_b + (size_t)f * cap;
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int pass = 0; pass < 8; ++pass) {
+        const int shift = pass * 4;
+        if (tid < 16) hist[tid] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < m; i += EDGE_THREADS) atomicAdd(&hist[(src[i] >> shift) & 15u], 1u);
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t acc = 0;
+            for (int d = 0; d < 16; ++d) { const uint32_t t = hist[d]; hist[d] = acc; acc += t; }
+        }
+        __syncthreads();
+        for (uint32_t base = 0; base < m; base += EDGE_THREADS) {
+            const uint32_t i = base + tid;
+            const bool valid = i < m;
+            const uint32_t key = valid ? src[i] : 0u;
+            const uint32_t d = (key >> shift) & 15u;
+            uint64_t match = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint64_t bb = __ballot((d >> b) & 1u);
+                match &= ((d >> b) & 1u) ? bb : ~bb;
+            }
+            const uint32_t rank = (uint32_t)__popcll(match & lt);
+            if (tid < EDGE_WAVES * 16) cnt[tid >> 4][tid & 15] = 0;
+            __syncthreads();
+            if (valid && rank == 0) cnt[w][d] = (uint32_t)__popcll(match);
+            __syncthreads();
+            if (tid < 16) {
+                uint32_t acc = hist[tid];
+                for (int ww = 0; ww < EDGE_WAVES; ++ww) { off[ww][tid] = acc; acc += cnt[ww][tid]; }
+                hist[tid] = acc;
+            }
+            __syncthreads();
+            if (valid) dst[off[w][d] + rank] = key;
+            __syncthreads();
+        }
+        uint32_t *t = src; src = dst; dst = t;
+    }
+}
+
+__global__ void k_edge_pick(const uint32_t *__restrict__ keys, uint32_t cap,
+                            const uint32_t *__restrict__ counts, const uint8_t *is_cat,
+                            int32_t num_bins, float *__restrict__ edges) {
+    const int f = blockIdx.x;
+    const int data_bins = num_bins - 1, ne = data_bins - 1;
+    const int64_t m = counts[f];
+    for (int k = threadIdx.x; k < ne; k += blockDim.x) {
+        float e = 0.0f;
+        if (!is_cat[f] && m > 0) {
+            int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
+            if (idx > m - 1) idx = m - 1;
+            e = key_float(keys[(size_t)f * cap + idx]);
+        }
+        edges[(size_t)f * ne + k] = e;
+    }
+}
+
+size_t edge_sample_cap(int64_t rows) {
+    int64_t step = rows / 200000;
+    if (step < 1) step = 1;
+    return (size_t)((rows + step - 1) / step);
+}
+
+hipError_t launch_edges(hipStream_t s, const float *x, int64_t rows, int32_t cols, int64_t rs,
+                        int64_t cs, int32_t num_bins, const uint8_t *is_cat, uint32_t *keys_a,
+                        uint32_t *keys_b, uint32_t *counts, float *edges) {
+    int64_t step = rows / 200000;
+    if (step < 1) step = 1;
+    const uint32_t cap = (uint32_t)edge_sample_cap(rows);
+    hipLaunchKernelGGL(k_edge_sample, dim3(cols), dim3(EDGE_THREADS), 0, s, x, rows, rs, cs, step,
+                       cap, is_cat, keys_a, counts);
+    hipLaunchKernelGGL(k_edge_sort, dim3(cols), dim3(EDGE_THREADS), 0, s, keys_a, keys_b, cap,
+                       counts);
+    hipLaunchKernelGGL(k_edge_pick, dim3(cols), dim3(256), 0, s, keys_a, cap, counts, is_cat,
+                       num_bins, edges);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // per-tree init, gradient maxima, quantisation
 // ---------------------------------------------------------------------------
 

@@ -116,6 +116,15 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            const uint8_t *is_cat, int32_t num_bins, int32_t tile_w,
                            int32_t num_tiles, uint8_t *bins_tiled, uint8_t *bins_fm);
 
+// Quantile edges (Binner.swift:25-56) on the device: x strided as for
+// launch_bin_data, edges[cols][num_bins-2] (0 for categorical or all-NaN
+// columns).  keys_a / keys_b hold edge_sample_cap(rows) u32 per column,
+// counts one u32 per column.
+size_t edge_sample_cap(int64_t rows);
+hipError_t launch_edges(hipStream_t s, const float *x, int64_t rows, int32_t cols, int64_t rs,
+                        int64_t cs, int32_t num_bins, const uint8_t *is_cat, uint32_t *keys_a,
+                        uint32_t *keys_b, uint32_t *counts, float *edges);
+
 hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl);
 
 // Objectives numbered as Booster.swift:5-14.

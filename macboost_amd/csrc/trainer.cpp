@@ -1,6 +1,6 @@
 // trainer.cpp — the training driver: fitImpl (Booster.swift:445-1701) restated
-// for one MI355X.  Edges are computed on the host (Binner.swift:33-56), the raw
-// matrix is binned on the device, and every tree is a fixed sequence of
+// for one MI355X.  The raw matrix is uploaded once; quantile edges
+// (Binner.swift:25-56) and bins are computed on the device, and every tree is a fixed sequence of
 // kernels on one HIP stream with all split decisions kept on the device; the
 // host touches the stream again only to read finished trees (or, with a
 // validation set, the per-iteration metric).
@@ -23,53 +23,9 @@ int host_threads() {
     return (int)n;
 }
 
-template <typename Fn>
-static void parallel_for(int64_t n, Fn fn) {
-    int nt = host_threads();
-    if (n < 2 || nt < 2) {
-        for (int64_t i = 0; i < n; ++i) fn(i);
-        return;
-    }
-    std::vector<std::thread> th;
-    std::atomic<int64_t> next{0};
-    for (int k = 0; k < nt; ++k)
-        th.emplace_back([&] {
-            for (int64_t i = next++; i < n; i = next++) fn(i);
-        });
-    for (auto &t : th) t.join();
-}
-
 static double now_s() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch())
         .count();
-}
-
-// Quantile edges: stride subsample of <= 200k non-NaN values per feature,
-// sorted, edge k = sample[min(m-1, (k+1)*m / dataBins)] (Binner.swift:33-56).
-std::vector<float> compute_edges(const float *x, int64_t rows, int64_t cols, int64_t rs,
-                                 int64_t cs, int num_bins, const std::vector<uint8_t> &is_cat) {
-    const int data_bins = num_bins - 1, num_edges = data_bins - 1;
-    int64_t step = rows / 200000;
-    if (step < 1) step = 1;
-    std::vector<float> edges((size_t)cols * num_edges, 0.0f);
-    parallel_for(cols, [&](int64_t f) {
-        if (is_cat[f]) return;
-        std::vector<float> sample;
-        sample.reserve((size_t)(rows / step + 1));
-        for (int64_t i = 0; i < rows; i += step) {
-            float v = x[i * rs + f * cs];
-            if (!std::isnan(v)) sample.push_back(v);
-        }
-        if (sample.empty()) return;
-        std::sort(sample.begin(), sample.end());
-        const int64_t m = (int64_t)sample.size();
-        for (int k = 0; k < num_edges; ++k) {
-            int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
-            if (idx > m - 1) idx = m - 1;
-            edges[(size_t)f * num_edges + k] = sample[(size_t)idx];
-        }
-    });
-    return edges;
 }
 
 std::string swift_float(float v) {
@@ -476,19 +432,26 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
             "bins, resolution does not once bins exceed rows per node)");
     }
 
-    // --- binning: host edges, device bin_data ---------------------------
+    // --- binning on the device: upload, quantile edges, bin_data ----------
     double t0 = now_s();
-    t.edges = compute_edges(x, rows, cols, rs, cs, p.num_bins, t.is_cat_h);
-    t.t_edges = now_s() - t0;
-    t0 = now_s();
     {
         DevBuf<float> xd((size_t)rows * (size_t)cols);
-        DevBuf<float> ed(std::max<size_t>(1, t.edges.size()));
+        const size_t ne = (size_t)p.num_bins - 2;
+        DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
         t.is_cat.alloc((size_t)cols);
         MB_HIP(hipMemcpyAsync(t.is_cat.ptr, t.is_cat_h.data(), (size_t)cols, hipMemcpyHostToDevice, s));
         MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, s));
-        if (!t.edges.empty())
-            MB_HIP(hipMemcpyAsync(ed.ptr, t.edges.data(), t.edges.size() * 4, hipMemcpyHostToDevice, s));
+        {
+            const double te = now_s();
+            const size_t cap = mbk::edge_sample_cap(rows);
+            DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
+            MB_HIP(mbk::launch_edges(s, xd.ptr, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
+                                     ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
+            t.edges.resize((size_t)cols * ne);
+            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+            MB_HIP(hipStreamSynchronize(s));
+            t.t_edges = now_s() - te;
+        }
         t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
         t.bins_fm.alloc((size_t)rows * (size_t)cols);
         MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
@@ -509,7 +472,7 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         }
         MB_HIP(hipStreamSynchronize(s));
     }
-    t.t_bin = now_s() - t0;
+    t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
 
     // --- persistent buffers ---------------------------------------------
     t.labels_h.assign(y, y + rows);

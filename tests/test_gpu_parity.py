@@ -72,6 +72,51 @@ def check_identical(x_fm, y, params, is_cat=None, x_test=None):
 # kernel seam (mbk_*)
 # --------------------------------------------------------------------------
 
+def _edge_columns(rows, seed):
+    # Columns that stress the sort: NaN holes, heavy ties, +-0 and +-inf,
+    # negatives, an all-NaN column, a categorical column, a constant column.
+    rng = np.random.default_rng(seed)
+    x = np.empty((9, rows), np.float32)
+    x[0] = rng.standard_normal(rows)
+    x[1] = rng.uniform(-1, 1, rows)
+    x[1, rng.random(rows) < 0.3] = np.nan
+    x[2] = np.floor(rng.uniform(-5, 5, rows))                 # 10 distinct values
+    x[3] = rng.choice(np.array([-0.0, 0.0, 1.0, -np.inf, np.inf, -2.5], np.float32), rows)
+    x[4] = np.nan
+    x[5] = np.floor(rng.uniform(0, 30, rows))                 # categorical
+    x[6] = 7.25
+    x[7] = rng.exponential(1.0, rows) * np.where(rng.random(rows) < 0.5, -1e30, 1e-30)
+    x[8] = (rng.standard_normal(rows) * 1e-38).astype(np.float32)   # subnormals
+    is_cat = np.zeros(9, np.uint8)
+    is_cat[5] = 1
+    return x, is_cat
+
+
+@pytest.mark.parametrize("rows,nb,row_major", [(1, 4, False), (777, 64, False),
+                                               (5003, 256, True), (200_001, 256, False),
+                                               (2_500_003, 255, True)])
+def test_quantile_edges_match_oracle(ctx, rows, nb, row_major):
+    # computeEdges (Binner.swift:25-56): step 1 below 400k rows, then a
+    # stride subsample; equal as floats (a +0/-0 tie may pick either zero).
+    x, is_cat = _edge_columns(rows, rows)
+    want = O.compute_edges(x, nb, is_cat)
+    cols = x.shape[0]
+    if row_major:
+        dx, rs, cs = ctx.upload(np.ascontiguousarray(x.T)), cols, 1
+    else:
+        dx, rs, cs = ctx.upload(x), 1, rows
+    dc, de = ctx.upload(is_cat), ctx.alloc(cols * (nb - 2) * 4)
+    err = ctypes.c_char_p()
+    rc = _core.lib().mbk_quantile_edges(ctx.ptr, dx, rows, cols, rs, cs, nb, dc, de,
+                                        ctypes.byref(err))
+    assert rc == 0, err.value
+    got = ctx.download(de, (cols, nb - 2), np.float32)
+    assert np.array_equal(got, want)
+    s = got[[0, 1, 2, 3, 7, 8]]
+    assert (s[:, 1:] >= s[:, :-1]).all()                     # sorted (infs included)
+    assert not got[[4, 5]].any()
+
+
 @pytest.mark.parametrize("tile_w", [8, 16, 32, 64])
 def test_bin_data_matches_oracle(ctx, tile_w):
     rows, cols, nb = 5003, 37, 256
