@@ -108,7 +108,7 @@ def measure_extras(mb, x, y, cols, trees, with_cpu):
 
 
 def measure_configs(mb, trees):
-    """Whole fits through macboost_train (host edges, upload, binning and
+    """Whole fits through macboost_train (upload, device edges and binning,
     trees) on the NaN + categorical and HIGGS-like workloads."""
     import datasets as D
     out = {}
@@ -125,7 +125,7 @@ def measure_configs(mb, trees):
         "workload": "friedman1 1M x 100, 20 categorical columns (cardinality 2..64), 20% NaN, "
                     "200k validation rows evaluated after every tree",
         "trees": trees, "fit_seconds": el, "valid_rmse": rmse,
-        "note": "whole macboost_train call: host edges, upload, binning, trees, readback"}
+        "note": "whole macboost_train call: upload, device edges and binning, trees, readback"}
     log(f"NaN+categorical 1M: {trees} trees in {el:.3f}s, valid RMSE {rmse:.4f}")
     del h, x, xv
     x, y = D.c4_higgs_like(10_500_000, 42)
