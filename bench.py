@@ -219,9 +219,14 @@ def main():
     per_launch_bytes = hist_bytes / launches if launches else None
     traffic = None
     tfile = ROOT / "profiles" / "k_hist_traffic_friedman10m.json"
-    if tfile.exists():
-        # HBM bytes per k_hist launch from the committed rocprofv3 --pmc summary
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    if tfile.exists() and launches:
+        # HBM bytes per k_hist launch from the committed rocprofv3 --pmc summary:
+        # measured read bytes per built row x this run's built rows per launch,
+        # plus the measured partial write-back per launch
+        tj = json.loads(tfile.read_text())
+        if (tj.get("profile_rows"), tj.get("profile_cols")) == (rows, cols):
+            traffic = (tj["fetch_bytes_per_built_row"] * float(sum(built[:6])) / launches
+                       + tj["write_bytes_per_launch"])
     roofline = {
         "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": traffic,

@@ -87,7 +87,9 @@ hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t 
 
 // The same walk over the training rows, eight rows per thread walked level by
 // level together, that also counts the rows reaching each node of the deepest
-// level (counters in LDS, one global add per non-empty node per block).
+// level (counters in LDS, one global add per non-empty node per block).  The
+// split records (feature, bin | flags << 8) and leaf values are staged in LDS,
+// so each level costs one global gather per row: the row's bin byte.
 constexpr int WALK_THREADS = 1024;
 constexpr int WALK_ROWS = 8;
 
@@ -96,27 +98,42 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
                                                              int32_t max_depth, TreeOut tree,
                                                              float *__restrict__ preds,
                                                              uint32_t *__restrict__ count) {
-    extern __shared__ uint32_t wc_lds[];             // 2^max_depth counters
+    extern __shared__ uint32_t wc_lds[];
     const uint32_t deep = 1u << max_depth, deep_start = deep - 1;
-    for (uint32_t k = threadIdx.x; k < deep; k += blockDim.x) wc_lds[k] = 0;
+    const uint32_t internal = deep - 1, total = 2 * deep - 1;
+    uint32_t *s_cnt = wc_lds;                        // [deep]
+    int32_t *s_feat = reinterpret_cast<int32_t *>(wc_lds + deep);    // [internal]
+    uint32_t *s_bf = wc_lds + deep + internal;       // [internal] bin | flags << 8
+    float *s_leaf = reinterpret_cast<float *>(wc_lds + deep + 2 * internal);   // [total]
+    for (uint32_t k = threadIdx.x; k < deep; k += blockDim.x) s_cnt[k] = 0;
+    for (uint32_t k = threadIdx.x; k < internal; k += blockDim.x) {
+        const NodeSplit s = tree.split[k];
+        s_feat[k] = s.feature;
+        s_bf[k] = (s.bin & 0xFFu) | ((s.flags & 0xFFu) << 8);
+    }
+    for (uint32_t k = threadIdx.x; k < total; k += blockDim.x) s_leaf[k] = tree.leaf[k];
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * (WALK_THREADS * WALK_ROWS) + threadIdx.x;
     uint32_t n[WALK_ROWS];
 #pragma unroll
     for (int k = 0; k < WALK_ROWS; ++k) n[k] = 0;
     for (int32_t d = 0; d < max_depth; ++d) {
+        uint32_t b[WALK_ROWS];
 #pragma unroll
         for (int k = 0; k < WALK_ROWS; ++k) {
             const int64_t i = base + (int64_t)k * WALK_THREADS;
-            if (i >= rows) continue;
-            const NodeSplit s = tree.split[n[k]];
-            if (s.feature < 0) continue;
-            const uint32_t b = bins_fm[(int64_t)s.feature * rows + i];
+            const int32_t f = n[k] < internal ? s_feat[n[k]] : -1;
+            b[k] = (i < rows && f >= 0) ? bins_fm[(int64_t)f * rows + i] : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int k = 0; k < WALK_ROWS; ++k) {
+            if (b[k] == 0xFFFFFFFFu) continue;       // past the end, or at a leaf
+            const uint32_t bf = s_bf[n[k]], bin = bf & 0xFFu, flags = bf >> 8;
             bool left;
-            if (s.flags & FLAG_CATEGORICAL)
-                left = ((tree.mask[n[k] * 8 + (b >> 5)] >> (b & 31u)) & 1u) != 0;
-            else if (b == (uint32_t)(nb - 1)) left = (s.flags & FLAG_DEFAULT_LEFT) != 0;
-            else left = b <= s.bin;
+            if (flags & FLAG_CATEGORICAL)
+                left = ((tree.mask[n[k] * 8 + (b[k] >> 5)] >> (b[k] & 31u)) & 1u) != 0;
+            else if (b[k] == (uint32_t)(nb - 1)) left = (flags & FLAG_DEFAULT_LEFT) != 0;
+            else left = b[k] <= bin;
             n[k] = 2 * n[k] + 1 + (left ? 0 : 1);
         }
     }
@@ -124,12 +141,12 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
     for (int k = 0; k < WALK_ROWS; ++k) {
         const int64_t i = base + (int64_t)k * WALK_THREADS;
         if (i >= rows) continue;
-        preds[i] += tree.leaf[n[k]];
-        if (n[k] >= deep_start) atomicAdd(&wc_lds[n[k] - deep_start], 1u);
+        preds[i] += s_leaf[n[k]];
+        if (n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
     }
     __syncthreads();
     for (uint32_t k = threadIdx.x; k < deep; k += blockDim.x)
-        if (wc_lds[k]) atomicAdd(&count[deep_start + k], wc_lds[k]);
+        if (s_cnt[k]) atomicAdd(&count[deep_start + k], s_cnt[k]);
 }
 
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
@@ -137,7 +154,8 @@ hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows
                              float *preds, uint32_t *count) {
     if (rows <= 0) return hipSuccess;
     const int64_t per = (int64_t)WALK_THREADS * WALK_ROWS;
-    const size_t lds = ((size_t)1 << max_depth) * sizeof(uint32_t);
+    const size_t deep = (size_t)1 << max_depth;
+    const size_t lds = (deep + 2 * (deep - 1) + (2 * deep - 1)) * sizeof(uint32_t);
     hipLaunchKernelGGL(k_walk_count, dim3((unsigned)((rows + per - 1) / per)), dim3(WALK_THREADS),
                        lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count);
     return hipGetLastError();

@@ -1597,7 +1597,7 @@ hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la
 // row partition (route_samples, Shaders.swift:1241-1311): one pass.  Every
 // split node keeps its interval [start, start+count) of the order buffer; its
 // children split that interval, left entries from the front and right
-// entries from the back.  Each block covers 2048 entries of one node, counts
+// entries from the back.  Each block covers PART_ENTRIES entries of one node, counts
 // its lefts and rights, reserves both ranges with one atomic add each on the
 // node's cursors, and writes its entries there.  Entry order inside a child
 // is not preserved; every consumer (histograms, counts, the next partition)
@@ -1634,13 +1634,16 @@ __device__ __forceinline__ void route_block_scan(const uint32_t (&x)[ROUTE_PER_T
     for (int k = 0; k < ROUTE_PER_THREAD; ++k) ex[k] += tot[k * ROUTE_WAVES + w];
 }
 
-// Large blocks keep the cursor atomics few (two per block).
+// Large blocks keep the cursor atomics few (two per block); 8 entries per
+// thread keep the kernel under 64 VGPRs, so two blocks share a CU.
 constexpr int PART_THREADS = 1024;
-constexpr int PART_PER_THREAD = 16;
+constexpr int PART_PER_THREAD = PART_ENTRIES / PART_THREADS;
 constexpr int PART_BLOCK = PART_THREADS * PART_PER_THREAD;
 constexpr int PART_WAVES = PART_THREADS / 64;
+constexpr int PART_SLICES = PART_PER_THREAD * PART_WAVES;
+constexpr int PART_SLICES_PER_LANE = PART_SLICES / 64;
 static_assert(PART_BLOCK == PART_ENTRIES, "partition block size");
-static_assert(PART_PER_THREAD * PART_WAVES == 256, "slice scan assumes 256 slices");
+static_assert(PART_SLICES % 64 == 0, "slice scan: whole slices per lane");
 
 // Blocks per split node of the routed level and their prefix; zero cursors.
 __global__ __launch_bounds__(1024) void k_route_plan(LevelArgs la, const uint32_t *count,
@@ -1710,14 +1713,15 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
     }
     __syncthreads();
     if (tid < 64) {
-        // scan the PART_PER_THREAD*PART_WAVES (= 256) slice totals with one wave
-        uint32_t v[4], s = 0;
+        // scan the PART_SLICES slice totals with one wave
+        constexpr int SPL = PART_SLICES_PER_LANE;
+        uint32_t v[SPL], s = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { v[j] = tot[tid * 4 + j]; s += v[j]; }
+        for (int j = 0; j < SPL; ++j) { v[j] = tot[tid * SPL + j]; s += v[j]; }
         const uint32_t inc = wave_inclusive_scan(s);
         uint32_t acc = inc - s;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { tot[tid * 4 + j] = acc; acc += v[j]; }
+        for (int j = 0; j < SPL; ++j) { tot[tid * SPL + j] = acc; acc += v[j]; }
         if (tid == 63) {
             const uint32_t nl = inc;
             tot[PART_PER_THREAD * PART_WAVES] = nl;

@@ -15,7 +15,7 @@ constexpr uint32_t FLAG_CATEGORICAL = 2u;
 constexpr int ROUTE_THREADS = 256;
 constexpr int ROUTE_PER_THREAD = 8;
 constexpr int ROUTE_BLOCK = ROUTE_THREADS * ROUTE_PER_THREAD;
-constexpr int PART_ENTRIES = 16384;   // entries per level-wise partition block
+constexpr int PART_ENTRIES = 8192;    // entries per level-wise partition block
 
 // Packed histogram word: (sum of qg) << HIST_QH_BITS + (sum of qh), as a
 // 64-bit two's-complement sum.  A histogram item accumulates at most
