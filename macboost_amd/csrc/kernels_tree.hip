@@ -1522,7 +1522,7 @@ hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active
 __global__ __launch_bounds__(1024) void k_plan_level(
     Shape sh, LevelArgs la, uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
     const uint32_t *seg_start_prev, uint32_t *seg_start_next, uint32_t *count,
-    const uint32_t *cursors, const TreeOut out, Pair *pairs, HistItem *items,
+    const uint64_t *cursors, const TreeOut out, Pair *pairs, HistItem *items,
     uint32_t *scratch) {
     __shared__ uint32_t wave_tot[17];
     __shared__ uint32_t s_active;
@@ -1537,7 +1537,7 @@ __global__ __launch_bounds__(1024) void k_plan_level(
     for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
         const uint32_t n = ls_prev + p;
         const bool split = out.split[n].feature >= 0 && count[n] >= 1;
-        const uint32_t cl = split ? cursors[2 * p] : 0u;
+        const uint32_t cl = split ? (uint32_t)cursors[(size_t)p * CURSOR_STRIDE] : 0u;
         const uint32_t cr = split ? count[n] - cl : 0u;
         count[la.level_start + 2 * p] = cl;
         count[la.level_start + 2 * p + 1] = cr;
@@ -1585,7 +1585,7 @@ __global__ __launch_bounds__(1024) void k_plan_level(
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                              const uint32_t *seg_start_prev, uint32_t *seg_start_next,
-                             uint32_t *count, const uint32_t *cursors, const TreeOut out,
+                             uint32_t *count, const uint64_t *cursors, const TreeOut out,
                              Pair *pairs, HistItem *items, uint32_t *scratch) {
     hipLaunchKernelGGL(k_plan_level, dim3(1), dim3(1024), 0, s, sh, la, target_items, min_chunk,
                        ctl, seg_start_prev, seg_start_next, count, cursors, out, pairs, items,
@@ -1599,7 +1599,8 @@ hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la
 // children split that interval, left entries from the front and right
 // entries from the back.  Each block covers PART_ENTRIES entries of one node, counts
 // its lefts and rights, reserves both ranges with one atomic add each on the
-// node's cursors, and writes its entries there.  Entry order inside a child
+// node's cursor (one packed 64-bit add: left count low, right count high; each
+// node's cursor on its own 128-B line), and writes its entries there.  Entry order inside a child
 // is not preserved; every consumer (histograms, counts, the next partition)
 // is order-independent.  The left cursor ends as the node's left count.
 // ---------------------------------------------------------------------------
@@ -1648,14 +1649,13 @@ static_assert(PART_SLICES % 64 == 0, "slice scan: whole slices per lane");
 // Blocks per split node of the routed level and their prefix; zero cursors.
 __global__ __launch_bounds__(1024) void k_route_plan(LevelArgs la, const uint32_t *count,
                                                      const TreeOut out, uint32_t *blk_prefix,
-                                                     uint32_t *cursors) {
+                                                     uint64_t *cursors) {
     __shared__ uint32_t wave_tot[17];
     for (uint32_t l = threadIdx.x; l < la.num_level; l += blockDim.x) {
         const uint32_t n = la.level_start + l;
         const bool split = out.split[n].feature >= 0 && count[n] >= 1;
         blk_prefix[l] = split ? (count[n] + PART_BLOCK - 1) / PART_BLOCK : 0u;
-        cursors[2 * l] = 0;
-        cursors[2 * l + 1] = 0;
+        cursors[(size_t)l * CURSOR_STRIDE] = 0;
     }
     __syncthreads();
     const uint32_t total = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
@@ -1666,10 +1666,10 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
     const uint32_t *__restrict__ count, const TreeOut out, const uint32_t *__restrict__ blk_prefix,
-    uint32_t *cursors, int write_entries) {
+    uint64_t *cursors, int write_entries) {
     __shared__ uint32_t tot[PART_PER_THREAD * PART_WAVES + 1];
     __shared__ uint32_t s_mask[8];
-    __shared__ uint32_t s_base[2];
+    __shared__ uint64_t s_base;
     const uint32_t b = blockIdx.x;
     if (b >= blk_prefix[la.num_level]) return;       // uniform per block
     // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
@@ -1725,13 +1725,16 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
         if (tid == 63) {
             const uint32_t nl = inc;
             tot[PART_PER_THREAD * PART_WAVES] = nl;
-            s_base[0] = atomicAdd(&cursors[2 * l], nl);
-            s_base[1] = atomicAdd(&cursors[2 * l + 1], nvalid - nl);
+            // both counts < 2^32: the low word never carries into the high one
+            s_base = atomicAdd(reinterpret_cast<unsigned long long *>(
+                                   &cursors[(size_t)l * CURSOR_STRIDE]),
+                               (unsigned long long)nl |
+                                   ((unsigned long long)(nvalid - nl) << 32));
         }
     }
     if (!write_entries) return;                      // counts only (terminal level)
     __syncthreads();
-    const uint32_t base_l = s_base[0], base_r = s_base[1];
+    const uint32_t base_l = (uint32_t)s_base, base_r = (uint32_t)(s_base >> 32);
     Entry *dst = order_out + start;
 #pragma unroll
     for (int k = 0; k < PART_PER_THREAD; ++k) {
@@ -1746,7 +1749,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
-                        uint32_t *blk_prefix, uint32_t *cursors, uint32_t max_blocks,
+                        uint32_t *blk_prefix, uint64_t *cursors, uint32_t max_blocks,
                         bool write_entries) {
     hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(1024), 0, s, la, count, out, blk_prefix,
                        cursors);

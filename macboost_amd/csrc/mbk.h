@@ -16,6 +16,7 @@ constexpr int ROUTE_THREADS = 256;
 constexpr int ROUTE_PER_THREAD = 8;
 constexpr int ROUTE_BLOCK = ROUTE_THREADS * ROUTE_PER_THREAD;
 constexpr int PART_ENTRIES = 8192;    // entries per level-wise partition block
+constexpr int CURSOR_STRIDE = 16;     // u64 words per node cursor (one 128-B line each)
 
 // Packed histogram word: (sum of qg) << HIST_QH_BITS + (sum of qh), as a
 // 64-bit two's-complement sum.  A histogram item accumulates at most
@@ -217,20 +218,21 @@ hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t
                               TreeOut out);
 
 // Partition of the routed level (d-1): every split node's interval is split
-// in place between its children (left from the front, right from the back);
-// cursors[2l] ends as node l's left count.  max_blocks >= ceil(rows/16384) +
+// in place between its children (left from the front, right from the back).
+// Node l's cursor is cursors[l * CURSOR_STRIDE]: left count in the low word,
+// right count in the high word.  max_blocks >= ceil(rows/PART_ENTRIES) +
 // nodes of the level.  write_entries = false only counts (terminal level).
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
-                        uint32_t *blk_prefix, uint32_t *cursors, uint32_t max_blocks,
+                        uint32_t *blk_prefix, uint64_t *cursors, uint32_t max_blocks,
                         bool write_entries);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                              const uint32_t *seg_start_prev, uint32_t *seg_start_next,
-                             uint32_t *count, const uint32_t *cursors, const TreeOut out,
+                             uint32_t *count, const uint64_t *cursors, const TreeOut out,
                              Pair *pairs, HistItem *items, uint32_t *scratch);
 
 // ---------------------------------------------------------------------------

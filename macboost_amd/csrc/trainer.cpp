@@ -86,7 +86,8 @@ struct Trainer {
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
     DevBuf<uint8_t> dir;
-    DevBuf<uint32_t> block_left, gmax_part, route_blk, route_cursor, goss_buckets;
+    DevBuf<uint32_t> block_left, gmax_part, route_blk, goss_buckets;
+    DevBuf<uint64_t> route_cursor;
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
     DevBuf<mbk::HistItem> items;
@@ -519,7 +520,7 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES) +
                    (uint32_t)t.max_level_nodes;
     t.route_blk.alloc((size_t)t.max_level_nodes + 1);
-    t.route_cursor.alloc((size_t)t.max_level_nodes * 2);
+    t.route_cursor.alloc((size_t)t.max_level_nodes * mbk::CURSOR_STRIDE);
     t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
     const uint32_t part_blocks = (uint32_t)std::min<int64_t>(1024, (rows + 255) / 256);
     t.block_left.alloc(std::max<uint32_t>(t.max_blocks, part_blocks) + 1);
