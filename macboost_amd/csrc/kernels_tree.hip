@@ -1237,12 +1237,13 @@ __global__ __launch_bounds__(64) void k_decide(Shape sh, SplitParams sp, LevelAr
                                                const uint32_t *count, int64_t *node_g,
                                                int64_t *node_h, float2 *bounds,
                                                const int8_t *monotone, const TreeCtl *ctl,
-                                               uint32_t *left_count, TreeOut out) {
+                                               uint64_t *cursors, TreeOut out) {
     const uint32_t local = blockIdx.x;
     const uint32_t n = la.level_start + local;
     const int lane = lane_id();
     const int F = sh.cols;
-    (void)left_count;
+    // the partition of this level starts from zeroed cursors
+    if (lane == 0) cursors[(size_t)local * CURSOR_STRIDE] = 0;
     if (count[n] < 1) {
         if (lane == 0) {
             NodeSplit leaf = {-1, 0, 0};
@@ -1301,10 +1302,10 @@ __global__ __launch_bounds__(64) void k_decide(Shape sh, SplitParams sp, LevelAr
 hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
                          const LevelArgs &la, const SplitResult *results, const uint32_t *count,
                          int64_t *node_g, int64_t *node_h, float2 *bounds,
-                         const int8_t *monotone, const TreeCtl *ctl, uint32_t *left_count,
+                         const int8_t *monotone, const TreeCtl *ctl, uint64_t *cursors,
                          TreeOut out) {
     hipLaunchKernelGGL(k_decide, dim3(la.num_level), dim3(64), 0, s, sh, sp, la, results, count,
-                       node_g, node_h, bounds, monotone, ctl, left_count, out);
+                       node_g, node_h, bounds, monotone, ctl, cursors, out);
     return hipGetLastError();
 }
 
@@ -1646,32 +1647,26 @@ constexpr int PART_SLICES_PER_LANE = PART_SLICES / 64;
 static_assert(PART_BLOCK == PART_ENTRIES, "partition block size");
 static_assert(PART_SLICES % 64 == 0, "slice scan: whole slices per lane");
 
-// Blocks per split node of the routed level and their prefix; zero cursors.
-__global__ __launch_bounds__(1024) void k_route_plan(LevelArgs la, const uint32_t *count,
-                                                     const TreeOut out, uint32_t *blk_prefix,
-                                                     uint64_t *cursors) {
-    __shared__ uint32_t wave_tot[17];
-    for (uint32_t l = threadIdx.x; l < la.num_level; l += blockDim.x) {
-        const uint32_t n = la.level_start + l;
-        const bool split = out.split[n].feature >= 0 && count[n] >= 1;
-        blk_prefix[l] = split ? (count[n] + PART_BLOCK - 1) / PART_BLOCK : 0u;
-        cursors[(size_t)l * CURSOR_STRIDE] = 0;
-    }
-    __syncthreads();
-    const uint32_t total = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
-    if (threadIdx.x == 0) blk_prefix[la.num_level] = total;
-}
-
 __global__ __launch_bounds__(PART_THREADS) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
-    const uint32_t *__restrict__ count, const TreeOut out, const uint32_t *__restrict__ blk_prefix,
-    uint64_t *cursors, int write_entries) {
+    const uint32_t *__restrict__ count, const TreeOut out, uint64_t *cursors,
+    int write_entries) {
+    extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
     __shared__ uint32_t tot[PART_PER_THREAD * PART_WAVES + 1];
     __shared__ uint32_t s_mask[8];
     __shared__ uint64_t s_base;
+    __shared__ uint32_t wave_tot[PART_WAVES + 1];
     const uint32_t b = blockIdx.x;
-    if (b >= blk_prefix[la.num_level]) return;       // uniform per block
+    // blocks per split node of the routed level, and their prefix
+    for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
+        const uint32_t nn = la.level_start + l;
+        const bool split = out.split[nn].feature >= 0 && count[nn] >= 1;
+        blk_prefix[l] = split ? (count[nn] + PART_BLOCK - 1) / PART_BLOCK : 0u;
+    }
+    __syncthreads();
+    const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
+    if (b >= total_blocks) return;                   // uniform per block
     // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
     uint32_t lo = 0, hi = la.num_level - 1;
     while (lo < hi) {
@@ -1749,12 +1744,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
-                        uint32_t *blk_prefix, uint64_t *cursors, uint32_t max_blocks,
-                        bool write_entries) {
-    hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(1024), 0, s, la, count, out, blk_prefix,
-                       cursors);
-    hipLaunchKernelGGL(k_route, dim3(max_blocks), dim3(PART_THREADS), 0, s, sh, la, bins_fm,
-                       order_in, order_out, seg_start, count, out, blk_prefix, cursors,
+                        uint64_t *cursors, uint32_t max_blocks, bool write_entries) {
+    // cursors were zeroed by this level's k_decide
+    const size_t lds = (size_t)la.num_level * sizeof(uint32_t);
+    hipLaunchKernelGGL(k_route, dim3(max_blocks), dim3(PART_THREADS), lds, s, sh, la, bins_fm,
+                       order_in, order_out, seg_start, count, out, cursors,
                        write_entries ? 1 : 0);
     return hipGetLastError();
 }

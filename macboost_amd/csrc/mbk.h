@@ -205,7 +205,7 @@ hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
                          const LevelArgs &la, const SplitResult *results,
                          const uint32_t *count, int64_t *node_g, int64_t *node_h,
                          float2 *bounds, const int8_t *monotone, const TreeCtl *ctl,
-                         uint32_t *left_count, TreeOut out);
+                         uint64_t *cursors, TreeOut out);
 
 // Deepest level: leaf values of split parents' children, counts zeroed
 // (launch_walk_count fills them, launch_final_fixup writes covers).
@@ -220,13 +220,12 @@ hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t
 // Partition of the routed level (d-1): every split node's interval is split
 // in place between its children (left from the front, right from the back).
 // Node l's cursor is cursors[l * CURSOR_STRIDE]: left count in the low word,
-// right count in the high word.  max_blocks >= ceil(rows/PART_ENTRIES) +
+// right count in the high word; the level's k_decide zeroes them.  max_blocks >= ceil(rows/PART_ENTRIES) +
 // nodes of the level.  write_entries = false only counts (terminal level).
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
-                        uint32_t *blk_prefix, uint64_t *cursors, uint32_t max_blocks,
-                        bool write_entries);
+                        uint64_t *cursors, uint32_t max_blocks, bool write_entries);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,

@@ -86,7 +86,7 @@ struct Trainer {
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
     DevBuf<uint8_t> dir;
-    DevBuf<uint32_t> block_left, gmax_part, route_blk, goss_buckets;
+    DevBuf<uint32_t> block_left, gmax_part, goss_buckets;
     DevBuf<uint64_t> route_cursor;
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
@@ -94,7 +94,7 @@ struct Trainer {
     DevBuf<mbk::Pair> pairs;
     DevBuf<int64_t> hist_a, hist_b;
     DevBuf<mbk::SplitResult> results;
-    DevBuf<uint32_t> count, seg_a, seg_b, left_count, node_left_prefix, scratch;
+    DevBuf<uint32_t> count, seg_a, seg_b, scratch;
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
@@ -516,10 +516,9 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         t.goss_buckets.alloc(1024);
         MB_HIP(hipMemsetAsync(t.goss_buckets.ptr, 0, 1024 * sizeof(uint32_t), s));
     }
-    // level-wise partition: one block per 2048 entries of a split node
+    // level-wise partition: one block per PART_ENTRIES entries of a split node
     t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES) +
                    (uint32_t)t.max_level_nodes;
-    t.route_blk.alloc((size_t)t.max_level_nodes + 1);
     t.route_cursor.alloc((size_t)t.max_level_nodes * mbk::CURSOR_STRIDE);
     t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
     const uint32_t part_blocks = (uint32_t)std::min<int64_t>(1024, (rows + 255) / 256);
@@ -566,8 +565,6 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.bounds.alloc((size_t)t.total_nodes);
     t.seg_a.alloc((size_t)1 << t.D);
     t.seg_b.alloc((size_t)1 << t.D);
-    t.left_count.alloc((size_t)t.max_level_nodes);
-    t.node_left_prefix.alloc((size_t)t.max_level_nodes);
     t.scratch.alloc(((size_t)1 << t.D) + 64);
     t.ctl.alloc(1);
     t.ensure_capacity(std::max(1, p.num_trees));
@@ -681,7 +678,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                              t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
     mbk::LevelArgs l0{0, 0, 1, 0};
     MB_HIP(mbk::launch_decide(s, sh, t.sp, l0, t.results.ptr, t.count.ptr, t.node_g.ptr,
-                              t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.left_count.ptr, out));
+                              t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.route_cursor.ptr, out));
     for (int d = 1; d <= t.D; ++d) {
         const bool terminal = d == t.D;
         mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
@@ -702,7 +699,7 @@ static void grow_levelwise(Trainer &t, int tree) {
             // a sampled tree counts its kept rows with the partition; every
             // row's prediction then comes from one walk (Booster.swift:1568-1580)
             MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
-                                     t.count.ptr, out, t.route_blk.ptr, t.route_cursor.ptr,
+                                     t.count.ptr, out, t.route_cursor.ptr,
                                      t.route_grid, false));
             MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items,
                                           (uint32_t)t.min_chunk, ctl, seg_cur, seg_next,
@@ -715,7 +712,7 @@ static void grow_levelwise(Trainer &t, int tree) {
             break;
         }
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
-                                 t.count.ptr, out, t.route_blk.ptr, t.route_cursor.ptr,
+                                 t.count.ptr, out, t.route_cursor.ptr,
                                  t.route_grid, true));
         MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
                                       ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr, out,
@@ -729,7 +726,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                                  t.count.ptr, t.node_g.ptr, t.node_h.ptr, ln.level_start,
                                  t.results.ptr));
         MB_HIP(mbk::launch_decide(s, sh, t.sp, ln, t.results.ptr, t.count.ptr, t.node_g.ptr,
-                                  t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.left_count.ptr,
+                                  t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.route_cursor.ptr,
                                   out));
     }
     if (t.has_valid)
