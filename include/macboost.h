@@ -12,9 +12,10 @@
  * Part 2 is the kernel seam (MetalEngine.dispatch, MetalEngine.swift:87-118):
  * device-pointer entry points a host written in another language can drive.
  *
- * Part 3 holds extensions with no counterpart in the reference: an
+ * Part 3 holds extensions with no counterpart in the reference's C ABI: an
  * incremental trainer used by the benchmark to time boosting iterations with
- * the binned matrix already resident in HBM.
+ * the binned matrix already resident in HBM, and the Swift API's preprocessed
+ * datasets (.mbds).
  */
 #ifndef MACBOOST_H
 #define MACBOOST_H
@@ -169,6 +170,35 @@ int mbx_trainer_setup_seconds(void *trainer, double *edges_s, double *bin_s);
  * valid and must still be freed. */
 void *mbx_trainer_booster(void *trainer, char **err);
 void mbx_trainer_free(void *trainer);
+
+/* Preprocessed datasets: the Swift API's makeDataset / BinnedDataset.save /
+ * BinnedDataset.load / fit(dataset:) (Booster.swift:375-436,
+ * Dataset.swift:11-86), which the reference's C ABI does not export.
+ * mbx_dataset_make validates labels and categoricals, computes quantile edges
+ * and bins on the GPU and keeps the bins host-side in the .mbds tile-8 layout
+ * [ceil(cols/8)][rows][8]; feature_names_json is a JSON string array or NULL.
+ * The file is byte-compatible with the reference's .mbds (little-endian,
+ * version 1).  mbx_dataset_train trains with the dataset's bin count,
+ * categorical layout and labels (params' num_bins / categorical_features are
+ * ignored); w and the feature-major validation set may be NULL.
+ * mbx_dataset_copy copies out any non-NULL array: categorical
+ * (num_categorical i32, ascending), labels (rows), edges (cols*(num_bins-2)),
+ * bins (ceil(cols/8)*rows*8).  mbx_dataset_feature_names returns a JSON array
+ * (free with macboost_free_string) or NULL. */
+void *mbx_dataset_make(const char *params_json, const float *x, int64_t rows, int64_t cols,
+                       int32_t row_major, const float *y, const char *feature_names_json,
+                       char **err);
+int32_t mbx_dataset_save(void *dataset, const char *path, char **err);
+void *mbx_dataset_load(const char *path, char **err);
+int32_t mbx_dataset_info(void *dataset, int64_t *rows, int64_t *cols, int32_t *num_bins,
+                         int32_t *num_categorical);
+int32_t mbx_dataset_copy(void *dataset, int32_t *categorical, float *labels, float *edges,
+                         uint8_t *bins);
+char *mbx_dataset_feature_names(void *dataset);
+void *mbx_dataset_train(const char *params_json, void *dataset, const float *w,
+                        const float *x_valid, int64_t valid_rows, const float *y_valid,
+                        char **err);
+void mbx_dataset_free(void *dataset);
 
 /* SplitMix64 Friedman #1 generator (DataGen.swift:68-94), multithreaded:
  * x feature-major [cols][rows], y[rows]. */

@@ -5,7 +5,7 @@ The compute lives in ``libmacboostc.so`` (HIP kernels + C++ host, built from
 entry points as the reference binding (python/macboost/_core.py).
 """
 from ._core import (  # noqa: F401
-    Context, MacBoostError, Trainer, best_iteration, feature_importance, friedman, load,
-    num_classes, num_features, num_trees, predict, predict_contrib, save, train, version,
-    warnings,
+    Context, Dataset, MacBoostError, Trainer, best_iteration, feature_importance, friedman,
+    load, num_classes, num_features, num_trees, predict, predict_contrib, save, train,
+    train_dataset, version, warnings,
 )

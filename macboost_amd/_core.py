@@ -142,6 +142,25 @@ def _configure(l):
                                _P, _P]
     l.mbx_version.restype = ctypes.c_char_p
     l.mbx_version.argtypes = []
+    l.mbx_dataset_make.restype = ctypes.c_void_p
+    l.mbx_dataset_make.argtypes = [ctypes.c_char_p, _P, ctypes.c_int64, ctypes.c_int64,
+                                   ctypes.c_int32, _P, ctypes.c_char_p, _c_char_pp]
+    l.mbx_dataset_save.restype = ctypes.c_int32
+    l.mbx_dataset_save.argtypes = [_P, ctypes.c_char_p, _c_char_pp]
+    l.mbx_dataset_load.restype = ctypes.c_void_p
+    l.mbx_dataset_load.argtypes = [ctypes.c_char_p, _c_char_pp]
+    l.mbx_dataset_info.restype = ctypes.c_int32
+    l.mbx_dataset_info.argtypes = [_P, ctypes.POINTER(ctypes.c_int64),
+                                   ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
+                                   ctypes.POINTER(ctypes.c_int32)]
+    l.mbx_dataset_copy.restype = ctypes.c_int32
+    l.mbx_dataset_copy.argtypes = [_P, _P, _P, _P, _P]
+    l.mbx_dataset_feature_names.restype = ctypes.c_void_p
+    l.mbx_dataset_feature_names.argtypes = [_P]
+    l.mbx_dataset_train.restype = ctypes.c_void_p
+    l.mbx_dataset_train.argtypes = [ctypes.c_char_p, _P, _P, _P, ctypes.c_int64, _P, _c_char_pp]
+    l.mbx_dataset_free.restype = None
+    l.mbx_dataset_free.argtypes = [_P]
 
 
 EXPORTED = (
@@ -154,7 +173,9 @@ EXPORTED = (
     "mbk_node_hist_split", "mbk_predict_forest",
     "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
     "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
-    "mbx_version",
+    "mbx_version", "mbx_dataset_make", "mbx_dataset_save", "mbx_dataset_load",
+    "mbx_dataset_info", "mbx_dataset_copy", "mbx_dataset_feature_names", "mbx_dataset_train",
+    "mbx_dataset_free",
 )
 
 
@@ -430,3 +451,109 @@ class Context:
 
     def __del__(self):
         self.close()
+
+
+class Dataset:
+    """A preprocessed training set (the reference's BinnedDataset,
+    Dataset.swift:11-86): quantile-binned features in the .mbds tile-8 layout,
+    edges, labels, bin count, categorical layout and feature names.  Build it
+    with Dataset.make (edges and bins on the GPU), or Dataset.load a .mbds
+    file; train_dataset fits from it without binning again."""
+
+    def __init__(self, ptr: int):
+        self.ptr = ptr
+
+    @classmethod
+    def make(cls, config: dict, X, y, feature_names=None, feature_major=False) -> "Dataset":
+        a = np.asarray(X, dtype=np.float32)
+        xf = np.ascontiguousarray(a)
+        if feature_major:
+            cols, rows = xf.shape
+        else:
+            rows, cols = xf.shape
+        yv = np.ascontiguousarray(y, dtype=np.float32)
+        names = None if feature_names is None else json.dumps(list(feature_names)).encode()
+        err = ctypes.c_char_p()
+        ptr = lib().mbx_dataset_make(json.dumps(config).encode(), _f32(xf), rows, cols,
+                                     0 if feature_major else 1, _f32(yv), names,
+                                     ctypes.byref(err))
+        if not ptr:
+            raise MacBoostError(_take_error(err))
+        return cls(ptr)
+
+    @classmethod
+    def load(cls, path) -> "Dataset":
+        err = ctypes.c_char_p()
+        ptr = lib().mbx_dataset_load(str(path).encode(), ctypes.byref(err))
+        if not ptr:
+            raise MacBoostError(_take_error(err))
+        return cls(ptr)
+
+    def save(self, path) -> None:
+        err = ctypes.c_char_p()
+        if lib().mbx_dataset_save(self.ptr, str(path).encode(), ctypes.byref(err)) != 0:
+            raise MacBoostError(_take_error(err))
+
+    def _info(self):
+        r, c = ctypes.c_int64(), ctypes.c_int64()
+        nb, nc = ctypes.c_int32(), ctypes.c_int32()
+        lib().mbx_dataset_info(self.ptr, ctypes.byref(r), ctypes.byref(c), ctypes.byref(nb),
+                               ctypes.byref(nc))
+        return r.value, c.value, nb.value, nc.value
+
+    @property
+    def rows(self) -> int:
+        return self._info()[0]
+
+    @property
+    def cols(self) -> int:
+        return self._info()[1]
+
+    @property
+    def num_bins(self) -> int:
+        return self._info()[2]
+
+    def arrays(self):
+        """(categorical, labels, edges [cols][num_bins-2], bins [ceil(cols/8)][rows][8])."""
+        rows, cols, nb, nc = self._info()
+        cat = np.empty(nc, np.int32)
+        labels = np.empty(rows, np.float32)
+        edges = np.empty((cols, max(nb - 2, 0)), np.float32)
+        bins = np.empty(((cols + 7) // 8, rows, 8), np.uint8)
+        lib().mbx_dataset_copy(self.ptr, cat.ctypes.data, labels.ctypes.data, edges.ctypes.data,
+                               bins.ctypes.data)
+        return cat, labels, edges, bins
+
+    @property
+    def feature_names(self):
+        p = lib().mbx_dataset_feature_names(self.ptr)
+        if not p:
+            return None
+        s = ctypes.cast(p, ctypes.c_char_p).value.decode()
+        lib().macboost_free_string(ctypes.cast(p, ctypes.c_void_p))
+        return json.loads(s)
+
+    def close(self):
+        if getattr(self, "ptr", None) and _lib_instance is not None:
+            _lib_instance.mbx_dataset_free(self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        self.close()
+
+
+def train_dataset(config: dict, dataset: Dataset, eval_set=None, sample_weight=None) -> _Handle:
+    """fit(dataset:) (Booster.swift:375-389): the dataset's bins, bin count,
+    categorical layout and labels are used."""
+    w = None if sample_weight is None else np.ascontiguousarray(sample_weight, dtype=np.float32)
+    xv = yvv = None
+    vrows = 0
+    if eval_set is not None:
+        xv, vrows, _ = _feature_major(eval_set[0])
+        yvv = np.ascontiguousarray(eval_set[1], dtype=np.float32)
+    err = ctypes.c_char_p()
+    ptr = lib().mbx_dataset_train(json.dumps(config).encode(), dataset.ptr, _f32(w), _f32(xv),
+                                  vrows, _f32(yvv), ctypes.byref(err))
+    if not ptr:
+        raise MacBoostError(_take_error(err))
+    return _Handle(ptr)

@@ -848,6 +848,104 @@ void *mbx_trainer_booster(void *trainer, char **err) {
 
 void mbx_trainer_free(void *trainer) { mb::trainer_free(static_cast<mb::Trainer *>(trainer)); }
 
+// --- preprocessed datasets (.mbds) -----------------------------------------
+
+void *mbx_dataset_make(const char *params_json, const float *x, int64_t rows, int64_t cols,
+                       int32_t row_major, const float *y, const char *feature_names_json,
+                       char **err) {
+    return guarded(err, [&]() -> void * {
+        mb::Params p = mb::parse_params(params_json);
+        std::vector<std::string> names;
+        if (feature_names_json) {
+            mbjson::Value v;
+            try {
+                v = mbjson::Parser(feature_names_json).parse();
+            } catch (const std::exception &) {
+                mb::invalid("featureNames must be a JSON array of strings");
+            }
+            if (v.kind != mbjson::Value::Array)
+                mb::invalid("featureNames must be a JSON array of strings");
+            for (const auto &e : v.arr) {
+                if (e.kind != mbjson::Value::String)
+                    mb::invalid("featureNames must be a JSON array of strings");
+                names.push_back(e.str);
+            }
+        }
+        return mb::dataset_make(p, x, rows, cols, row_major != 0, y,
+                                feature_names_json ? &names : nullptr);
+    }, nullptr);
+}
+
+int32_t mbx_dataset_save(void *ds, const char *path, char **err) {
+    if (!ds || !path) { set_err(err, "null argument"); return -1; }
+    return guarded(err, [&]() -> int32_t {
+        mb::dataset_save(*static_cast<mb::BinnedDataset *>(ds), path);
+        return 0;
+    }, -1);
+}
+
+void *mbx_dataset_load(const char *path, char **err) {
+    if (!path) { set_err(err, "null argument"); return nullptr; }
+    return guarded(err, [&]() -> void * { return mb::dataset_load(path); }, nullptr);
+}
+
+int32_t mbx_dataset_info(void *ds, int64_t *rows, int64_t *cols, int32_t *num_bins,
+                         int32_t *num_categorical) {
+    if (!ds) return -1;
+    const auto *d = static_cast<const mb::BinnedDataset *>(ds);
+    if (rows) *rows = d->rows;
+    if (cols) *cols = d->cols;
+    if (num_bins) *num_bins = d->num_bins;
+    if (num_categorical) *num_categorical = (int32_t)d->categorical.size();
+    return 0;
+}
+
+int32_t mbx_dataset_copy(void *ds, int32_t *categorical, float *labels, float *edges,
+                         uint8_t *bins) {
+    if (!ds) return -1;
+    const auto *d = static_cast<const mb::BinnedDataset *>(ds);
+    if (categorical && !d->categorical.empty())
+        std::memcpy(categorical, d->categorical.data(), d->categorical.size() * 4);
+    if (labels && !d->labels.empty()) std::memcpy(labels, d->labels.data(), d->labels.size() * 4);
+    if (edges && !d->edges.empty()) std::memcpy(edges, d->edges.data(), d->edges.size() * 4);
+    if (bins && !d->bins.empty()) std::memcpy(bins, d->bins.data(), d->bins.size());
+    return 0;
+}
+
+char *mbx_dataset_feature_names(void *ds) {
+    if (!ds) return nullptr;
+    const auto *d = static_cast<const mb::BinnedDataset *>(ds);
+    if (!d->has_feature_names) return nullptr;
+    std::string o = "[";
+    for (size_t i = 0; i < d->feature_names.size(); ++i) {
+        if (i) o += ",";
+        mbjson::put_string(o, d->feature_names[i]);
+    }
+    o += "]";
+    return strdup(o.c_str());
+}
+
+void *mbx_dataset_train(const char *params_json, void *ds, const float *w, const float *x_valid,
+                        int64_t valid_rows, const float *y_valid, char **err) {
+    if (!ds) { set_err(err, "null argument"); return nullptr; }
+    return guarded(err, [&]() -> void * {
+        mb::Params p = mb::parse_params(params_json);
+        mb::Trainer *t = mb::trainer_create_binned(p, *static_cast<mb::BinnedDataset *>(ds), w,
+                                                   x_valid, valid_rows, y_valid);
+        try {
+            mb::trainer_grow(t, p.num_trees);
+            Booster *b = mb::trainer_booster(t);
+            mb::trainer_free(t);
+            return b;
+        } catch (...) {
+            mb::trainer_free(t);
+            throw;
+        }
+    }, nullptr);
+}
+
+void mbx_dataset_free(void *ds) { delete static_cast<mb::BinnedDataset *>(ds); }
+
 void mbx_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise, float *x, float *y) {
     // DataGen.swift:68-94: one SplitMix64 stream per feature, one per
     // 65,536-row noise chunk; every stream is independent, so generate in parallel.

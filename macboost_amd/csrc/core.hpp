@@ -162,11 +162,32 @@ struct Booster {
     static Booster *from_json(const std::string &text);
 };
 
+// A preprocessed training set (BinnedDataset, Dataset.swift:11-24): bins in
+// the tile-8 layout [ceil(cols/8)][rows][8], edges cols*(num_bins-2), labels.
+struct BinnedDataset {
+    int64_t rows = 0;
+    int64_t cols = 0;
+    int32_t num_bins = 256;
+    std::vector<int32_t> categorical;        // ascending
+    bool has_feature_names = false;
+    std::vector<std::string> feature_names;
+    std::vector<float> labels;
+    std::vector<uint8_t> bins;
+    std::vector<float> edges;
+};
+BinnedDataset *dataset_make(const Params &p, const float *x, int64_t rows, int64_t cols,
+                            bool row_major, const float *y,
+                            const std::vector<std::string> *feature_names);
+void dataset_save(const BinnedDataset &ds, const std::string &path);
+BinnedDataset *dataset_load(const std::string &path);
+
 // Incremental trainer (fitImpl, Booster.swift:445-1701).
 struct Trainer;
 Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t cols,
                         bool row_major, const float *y, const float *w, const float *xv,
                         int64_t vrows, const float *yv);
+Trainer *trainer_create_binned(const Params &p, const BinnedDataset &ds, const float *w,
+                               const float *xv, int64_t vrows, const float *yv);
 void trainer_grow(Trainer *t, int num_trees);
 void trainer_profile(Trainer *t, bool enable);
 void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes);
@@ -177,6 +198,8 @@ Booster *trainer_booster(Trainer *t);
 void trainer_free(Trainer *t);
 
 // Shared helpers.
+void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_t cols,
+                           int64_t rs, int64_t cs);
 std::string swift_float(float v);
 int host_threads();
 

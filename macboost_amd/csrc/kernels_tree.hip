@@ -205,6 +205,68 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
 }
 
 // ---------------------------------------------------------------------------
+// the .mbds bin layout (Dataset.swift:18, bin_index, Shaders.swift:37-39):
+// 8-feature groups, feature 8g + j of row r at byte (g*rows + r)*8 + j.
+// One thread per (row, group) moves one 8-byte word.
+// ---------------------------------------------------------------------------
+
+__global__ void k_fm_to_tile8(const uint8_t *__restrict__ fm, int64_t rows, int32_t cols,
+                              uint64_t *__restrict__ out) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int g = blockIdx.y;
+    if (r >= rows) return;
+    uint64_t v = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int f = 8 * g + j;
+        if (f < cols) v |= (uint64_t)fm[(int64_t)f * rows + r] << (8 * j);
+    }
+    out[(int64_t)g * rows + r] = v;
+}
+
+// Tile-8 words -> gather layout [rows][T][W] (W a multiple of 8, pre-zeroed)
+// and feature-major [F][rows]; pad bytes past the last feature become 0 and
+// a bin >= nb raises *bad.
+__global__ void k_tile8_to_layouts(const uint64_t *__restrict__ in, int64_t rows, int32_t cols,
+                                   int32_t nb, int32_t W, int32_t T, uint8_t *__restrict__ tiled,
+                                   uint8_t *__restrict__ fm, uint32_t *bad) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int g = blockIdx.y;
+    if (r >= rows) return;
+    uint64_t v = in[(int64_t)g * rows + r];
+    const int nf = min(8, cols - 8 * g);
+    if (nf < 8) v &= (1ull << (8 * nf)) - 1ull;
+    bool over = false;
+    for (int j = 0; j < nf; ++j) {
+        const uint32_t b = (uint32_t)(v >> (8 * j)) & 0xFFu;
+        fm[(int64_t)(8 * g + j) * rows + r] = (uint8_t)b;
+        over = over || b >= (uint32_t)nb;
+    }
+    const int f0 = 8 * g, t = f0 / W, c0 = f0 % W;
+    *reinterpret_cast<uint64_t *>(tiled + ((size_t)r * (size_t)T + (size_t)t) * (size_t)W + c0) = v;
+    if (over) atomicOr(bad, 1u);
+}
+
+hipError_t launch_fm_to_tile8(hipStream_t s, const uint8_t *fm, int64_t rows, int32_t cols,
+                              uint64_t *out) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((rows + 255) / 256), (unsigned)((cols + 7) / 8));
+    hipLaunchKernelGGL(k_fm_to_tile8, grid, dim3(256), 0, s, fm, rows, cols, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile8_to_layouts(hipStream_t s, const uint64_t *in, int64_t rows, int32_t cols,
+                                   int32_t nb, int32_t W, int32_t T, uint8_t *tiled, uint8_t *fm,
+                                   uint32_t *bad) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (W % 8 != 0 || (int64_t)T * W < cols) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((rows + 255) / 256), (unsigned)((cols + 7) / 8));
+    hipLaunchKernelGGL(k_tile8_to_layouts, grid, dim3(256), 0, s, in, rows, cols, nb, W, T, tiled,
+                       fm, bad);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // quantile edges on the device (Binner.swift:25-56): per feature, the stride
 // subsample of non-NaN values, sorted, edge k = sample[min(m-1, (k+1)*m/dataBins)].
 // One 1024-thread workgroup per feature: compact the sample as order-

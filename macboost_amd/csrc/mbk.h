@@ -117,6 +117,15 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            const uint8_t *is_cat, int32_t num_bins, int32_t tile_w,
                            int32_t num_tiles, uint8_t *bins_tiled, uint8_t *bins_fm);
 
+// .mbds tile-8 bins (Dataset.swift:18): feature-major -> [ceil(cols/8)][rows] u64
+// words, and back into the gather [rows][T][W] (pre-zeroed) + feature-major
+// layouts; *bad (pre-zeroed) becomes nonzero if a bin is >= nb.
+hipError_t launch_fm_to_tile8(hipStream_t s, const uint8_t *fm, int64_t rows, int32_t cols,
+                              uint64_t *out);
+hipError_t launch_tile8_to_layouts(hipStream_t s, const uint64_t *in, int64_t rows, int32_t cols,
+                                   int32_t nb, int32_t W, int32_t T, uint8_t *tiled, uint8_t *fm,
+                                   uint32_t *bad);
+
 // Quantile edges (Binner.swift:25-56) on the device: x strided as for
 // launch_bin_data, edges[cols][num_bins-2] (0 for categorical or all-NaN
 // columns).  keys_a / keys_b hold edge_sample_cap(rows) u32 per column,

@@ -64,7 +64,10 @@ Device::~Device() {
 // ---------------------------------------------------------------------------
 
 struct Trainer {
-    Params p;
+    Params p;                        // effective (a dataset's bins and categoricals)
+    Params user_params;              // as given; stored in the model
+    bool has_feature_names = false;
+    std::vector<std::string> feature_names;
     std::unique_ptr<Device> dev;
     mbk::Shape sh{};
     mbk::SplitParams sp{};
@@ -183,7 +186,7 @@ static void validate_labels(const Params &p, const float *y, int64_t n) {   // :
     }
 }
 
-static void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_t cols,
+void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_t cols,
                                   int64_t rs, int64_t cs) {          // :1810-1826
     const int data_bins = p.num_bins - 1;
     for (int f : p.categorical) {
@@ -344,21 +347,14 @@ static float eval_metric(const Params &p, const float *pred, const float *y, int
     return 0.0f;
 }
 
-Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t cols,
-                        bool row_major, const float *y, const float *w, const float *xv,
-                        int64_t vrows, const float *yv) {
-    if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
-    validate_params(pin);
-    auto tr = std::make_unique<Trainer>();
-    Trainer &t = *tr;
-    t.p = pin;
-    const Params &p = t.p;
+// Checks shared by both entry points (Booster.swift:451-529).
+static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
+                            const float *w, const float *xv, int64_t vrows, const float *yv) {
     if (p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE)
         invalid("objective '" + objective_name(p.objective) +
                 "' (leaf renewal) is not supported by this build yet");
     if (p.objective == OBJ_MULTICLASS) invalid("multiclass is not supported by this build yet");
     if (!p.init_model.empty()) invalid("init_model (warm start) is not supported by this build yet");
-    // data validation (Booster.swift:451-529)
     validate_labels(p, y, rows);
     if (w)
         for (int64_t i = 0; i < rows; ++i)
@@ -374,12 +370,13 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         for (int f : p.allowed) ok = ok && f >= 0 && f < cols;
         if (!ok) invalid("allowedFeatures must be non-empty indices within 0..<" + std::to_string(cols));
     }
-    const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
     if (rows > 0xFFFFFFF0LL) invalid("more than 2^32 rows are not supported");
-    check_leakage(t, x, rows, cols, rs, cs, y);
-    validate_categoricals(p, x, rows, cols, rs, cs);
-    if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
+}
 
+// Device, shapes and params-derived constants; t.p holds the effective
+// params (bin count and categorical layout included).
+static void setup_shape(Trainer &t, int64_t rows, int64_t cols) {
+    const Params &p = t.p;
     t.dev = std::make_unique<Device>(0);
     hipStream_t s = t.dev->stream;
     t.rows = rows;
@@ -419,7 +416,8 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.gp.alpha = p.alpha;
     t.gp.aux = p.objective == OBJ_LOGISTIC ? p.scale_pos_weight
              : p.objective == OBJ_TWEEDIE ? p.tweedie_power : 0.0f;
-    t.gp.has_weights = w ? 1 : 0;
+    t.is_cat.alloc((size_t)cols);
+    MB_HIP(hipMemcpyAsync(t.is_cat.ptr, t.is_cat_h.data(), (size_t)cols, hipMemcpyHostToDevice, s));
 
     // rows-per-bin hint (Booster.swift:730-738)
     if (rows / p.num_bins < 64 && p.num_bins > 64) {
@@ -432,49 +430,29 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
             " is typically 2-4x faster here with equal accuracy (histogram cost scales with "
             "bins, resolution does not once bins exceed rows per node)");
     }
+}
 
-    // --- binning on the device: upload, quantile edges, bin_data ----------
-    double t0 = now_s();
-    {
-        DevBuf<float> xd((size_t)rows * (size_t)cols);
-        const size_t ne = (size_t)p.num_bins - 2;
-        DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
-        t.is_cat.alloc((size_t)cols);
-        MB_HIP(hipMemcpyAsync(t.is_cat.ptr, t.is_cat_h.data(), (size_t)cols, hipMemcpyHostToDevice, s));
-        MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, s));
-        {
-            const double te = now_s();
-            const size_t cap = mbk::edge_sample_cap(rows);
-            DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
-            MB_HIP(mbk::launch_edges(s, xd.ptr, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
-                                     ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
-            t.edges.resize((size_t)cols * ne);
-            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
-            MB_HIP(hipStreamSynchronize(s));
-            t.t_edges = now_s() - te;
-        }
-        t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
-        t.bins_fm.alloc((size_t)rows * (size_t)cols);
-        MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
-        MB_HIP(mbk::launch_bin_data(s, xd.ptr, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
-                                    p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
-                                    t.bins_fm.ptr));
-        if (xv && yv && vrows > 0) {
-            t.has_valid = true;
-            t.vrows = vrows;
-            DevBuf<float> xvd((size_t)vrows * (size_t)cols);
-            DevBuf<uint8_t> vt((size_t)t.sh.num_tiles * (size_t)vrows * (size_t)tile_w);
-            t.vbins_fm.alloc((size_t)vrows * (size_t)cols);
-            MB_HIP(hipMemcpyAsync(xvd.ptr, xv, xvd.bytes(), hipMemcpyHostToDevice, s));
-            MB_HIP(mbk::launch_bin_data(s, xvd.ptr, vrows, (int)cols, 1, vrows, ed.ptr,
-                                        t.is_cat.ptr, p.num_bins, tile_w, t.sh.num_tiles, vt.ptr,
-                                        t.vbins_fm.ptr));
-            MB_HIP(hipStreamSynchronize(s));
-        }
-        MB_HIP(hipStreamSynchronize(s));
-    }
-    t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
+// Bins a raw feature-major validation set with the training edges (device).
+static void bin_valid(Trainer &t, const float *xv, int64_t vrows, const float *edges_dev) {
+    hipStream_t s = t.dev->stream;
+    t.has_valid = true;
+    t.vrows = vrows;
+    DevBuf<float> xvd((size_t)vrows * (size_t)t.cols);
+    DevBuf<uint8_t> vt((size_t)t.sh.num_tiles * (size_t)vrows * (size_t)t.sh.tile_w);
+    t.vbins_fm.alloc((size_t)vrows * (size_t)t.cols);
+    MB_HIP(hipMemcpyAsync(xvd.ptr, xv, xvd.bytes(), hipMemcpyHostToDevice, s));
+    MB_HIP(mbk::launch_bin_data(s, xvd.ptr, vrows, t.cols, 1, vrows, edges_dev, t.is_cat.ptr,
+                                t.nb, t.sh.tile_w, t.sh.num_tiles, vt.ptr, t.vbins_fm.ptr));
+    MB_HIP(hipStreamSynchronize(s));
+}
 
+// Labels, weights, predictions and the tree-build buffers.
+static void setup_buffers(Trainer &t, const float *y, const float *w, const float *yv) {
+    const Params &p = t.p;
+    hipStream_t s = t.dev->stream;
+    const int64_t rows = t.rows, cols = t.cols, vrows = t.vrows;
+    const int tile_w = t.sh.tile_w;
+    t.gp.has_weights = w ? 1 : 0;
     // --- persistent buffers ---------------------------------------------
     t.labels_h.assign(y, y + rows);
     t.labels.alloc((size_t)rows);
@@ -570,6 +548,110 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.ensure_capacity(std::max(1, p.num_trees));
     MB_HIP(hipStreamSynchronize(s));
     t.best_metric = effective_metric(p) == "auc" ? -INFINITY : INFINITY;
+}
+
+Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t cols,
+                        bool row_major, const float *y, const float *w, const float *xv,
+                        int64_t vrows, const float *yv) {
+    if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
+    validate_params(pin);
+    validate_inputs(pin, rows, cols, y, w, xv, vrows, yv);
+    auto tr = std::make_unique<Trainer>();
+    Trainer &t = *tr;
+    t.p = pin;
+    t.user_params = pin;
+    const Params &p = t.p;
+    const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
+    check_leakage(t, x, rows, cols, rs, cs, y);
+    validate_categoricals(p, x, rows, cols, rs, cs);
+    if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
+    setup_shape(t, rows, cols);
+    hipStream_t s = t.dev->stream;
+    const int tile_w = t.sh.tile_w;
+
+    // --- binning on the device: upload, quantile edges, bin_data ----------
+    double t0 = now_s();
+    {
+        DevBuf<float> xd((size_t)rows * (size_t)cols);
+        const size_t ne = (size_t)p.num_bins - 2;
+        DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
+        MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, s));
+        {
+            const double te = now_s();
+            const size_t cap = mbk::edge_sample_cap(rows);
+            DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
+            MB_HIP(mbk::launch_edges(s, xd.ptr, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
+                                     ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
+            t.edges.resize((size_t)cols * ne);
+            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+            MB_HIP(hipStreamSynchronize(s));
+            t.t_edges = now_s() - te;
+        }
+        t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
+        t.bins_fm.alloc((size_t)rows * (size_t)cols);
+        MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
+        MB_HIP(mbk::launch_bin_data(s, xd.ptr, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
+                                    p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
+                                    t.bins_fm.ptr));
+        if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
+        MB_HIP(hipStreamSynchronize(s));
+    }
+    t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
+    setup_buffers(t, y, w, yv);
+    return tr.release();
+}
+
+// fit(dataset:) (Booster.swift:375-389): the dataset's bin count,
+// categorical layout, edges and labels are used; binning is skipped and the
+// tile-8 bins are rearranged into the device layouts.
+Trainer *trainer_create_binned(const Params &pin, const BinnedDataset &ds, const float *w,
+                               const float *xv, int64_t vrows, const float *yv) {
+    const int64_t rows = ds.rows, cols = ds.cols;
+    if (rows <= 0 || cols <= 0) invalid("training data is empty (rows=" + std::to_string(rows) +
+                                        ", cols=" + std::to_string(cols) + ")");
+    validate_params(pin);
+    Params pe = pin;
+    pe.num_bins = ds.num_bins;
+    pe.categorical = std::set<int>(ds.categorical.begin(), ds.categorical.end());
+    validate_params(pe);
+    validate_inputs(pe, rows, cols, ds.labels.data(), w, xv, vrows, yv);
+    auto tr = std::make_unique<Trainer>();
+    Trainer &t = *tr;
+    t.p = pe;
+    t.user_params = pin;
+    t.has_feature_names = ds.has_feature_names;
+    t.feature_names = ds.feature_names;
+    if (xv && yv && vrows > 0) validate_categoricals(pe, xv, vrows, cols, 1, vrows);
+    setup_shape(t, rows, cols);
+    hipStream_t s = t.dev->stream;
+    double t0 = now_s();
+    {
+        const int64_t groups = (cols + 7) / 8;
+        DevBuf<uint64_t> in((size_t)groups * (size_t)rows);
+        DevBuf<uint32_t> bad(1);
+        MB_HIP(hipMemcpyAsync(in.ptr, ds.bins.data(), in.bytes(), hipMemcpyHostToDevice, s));
+        MB_HIP(hipMemsetAsync(bad.ptr, 0, 4, s));
+        t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)t.sh.tile_w);
+        t.bins_fm.alloc((size_t)rows * (size_t)cols);
+        MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
+        MB_HIP(mbk::launch_tile8_to_layouts(s, in.ptr, rows, (int)cols, t.nb, t.sh.tile_w,
+                                            t.sh.num_tiles, t.bins_tiled.ptr, t.bins_fm.ptr,
+                                            bad.ptr));
+        uint32_t nbad = 0;
+        MB_HIP(hipMemcpyAsync(&nbad, bad.ptr, 4, hipMemcpyDeviceToHost, s));
+        MB_HIP(hipStreamSynchronize(s));
+        if (nbad) invalid(".mbds bins hold values >= numBins");
+        t.edges = ds.edges;
+        if (xv && yv && vrows > 0) {
+            DevBuf<float> ed(std::max<size_t>(1, t.edges.size()));
+            if (!t.edges.empty())
+                MB_HIP(hipMemcpyAsync(ed.ptr, t.edges.data(), t.edges.size() * 4,
+                                      hipMemcpyHostToDevice, s));
+            bin_valid(t, xv, vrows, ed.ptr);
+        }
+    }
+    t.t_bin = now_s() - t0;
+    setup_buffers(t, ds.labels.data(), w, yv);
     return tr.release();
 }
 
@@ -941,8 +1023,10 @@ Booster *trainer_booster(Trainer *tp) {
         MB_HIP(hipMemcpy(mask.data(), t.m_mask.ptr, mask.size() * 4, hipMemcpyDeviceToHost));
     }
     auto b = std::make_unique<Booster>();
-    b->params = t.p;
+    b->params = t.user_params;
     b->num_features = t.cols;
+    b->has_feature_names = t.has_feature_names;
+    b->feature_names = t.feature_names;
     b->trained_num_bins = t.nb;
     b->trained_categorical = t.p.categorical;
     b->base_score = t.base;
