@@ -326,6 +326,8 @@ def version() -> str:
 
 def friedman(rows: int, cols: int, seed: int, noise: float = 1.0):
     """Friedman #1 data (DataGen.friedman): feature-major X [cols, rows] and y."""
+    if cols < 5:
+        raise ValueError("friedman needs cols >= 5 (DataGen.swift:69)")
     x = np.empty((cols, rows), dtype=np.float32)
     y = np.empty(rows, dtype=np.float32)
     lib().mbx_friedman(rows, cols, ctypes.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), noise,

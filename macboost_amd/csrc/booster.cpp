@@ -957,6 +957,7 @@ void mbx_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise, float 
         return z ^ (z >> 31);
     };
     auto uni = [&](uint64_t &s) { return (float)(next(s) >> 40) * (1.0f / 16777216.0f); };
+    if (cols < 5 || rows <= 0 || !x || !y) return;  // precondition(cols >= 5), DataGen.swift:69
     const int nt = mb::host_threads();
     std::vector<std::thread> th;
     for (int k = 0; k < nt; ++k)

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
     for (int k = 0; k < WALK_ROWS; ++k) {
         const int64_t i = base + (int64_t)k * WALK_THREADS;
         if (i >= rows) continue;
-        preds[i] += s_leaf[n[k]];
+        if (preds) preds[i] += s_leaf[n[k]];        // null: counts only
         if (n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
     }
     __syncthreads();

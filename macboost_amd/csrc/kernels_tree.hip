@@ -1816,6 +1816,175 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
 }
 
 // ---------------------------------------------------------------------------
+// Leaf renewal for the L1 and quantile objectives (Booster.swift:634-639,
+// :1253-1290, :1596-1615): the residuals y - preds of every step-th row,
+// grouped by the leaf the row reaches; a leaf with >= 4 of them becomes
+// lr * min(max(r_(k), lo), hi), r_(k) the k-th smallest with
+// k = min(n-1, (int)((float)n * q)).  Grouping is a counting sort by leaf
+// (per-block LDS counts, one global add per non-empty leaf and block); the
+// order statistic is an MSB-first radix select over order-preserving keys,
+// one workgroup per leaf.
+// ---------------------------------------------------------------------------
+
+constexpr int RENEW_THREADS = 1024;
+
+__device__ __forceinline__ uint32_t walk_binned_row(const uint8_t *__restrict__ bins_fm,
+                                                    int64_t rows, int32_t nb, int32_t max_depth,
+                                                    const TreeOut &tree, int64_t i) {
+    uint32_t n = 0;
+    for (int32_t d = 0; d < max_depth; ++d) {
+        const NodeSplit s = tree.split[n];
+        if (s.feature < 0) break;
+        const uint32_t b = bins_fm[(int64_t)s.feature * rows + i];
+        n = 2 * n + 1 + (bin_goes_left(b, s, nb, tree.mask + (size_t)n * 8) ? 0u : 1u);
+    }
+    return n;
+}
+
+// Leaf and residual key of each sampled row; per-leaf counts (cnt pre-zeroed).
+__global__ __launch_bounds__(RENEW_THREADS) void k_renew_collect(
+    const uint8_t *__restrict__ bins_fm, int64_t rows, int32_t nb, int32_t max_depth,
+    TreeOut tree, const float *__restrict__ labels, const float *__restrict__ preds,
+    int64_t step, uint32_t ns, uint32_t total_nodes, uint32_t *__restrict__ leaf_of,
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ cnt) {
+    extern __shared__ uint32_t rc_lds[];             // [total_nodes]
+    for (uint32_t k = threadIdx.x; k < total_nodes; k += RENEW_THREADS) rc_lds[k] = 0;
+    __syncthreads();
+    const uint32_t s = blockIdx.x * RENEW_THREADS + threadIdx.x;
+    if (s < ns) {
+        const int64_t i = (int64_t)s * step;
+        const uint32_t n = walk_binned_row(bins_fm, rows, nb, max_depth, tree, i);
+        leaf_of[s] = n;
+        keys[s] = float_key(labels[i] - preds[i]);
+        atomicAdd(&rc_lds[n], 1u);
+    }
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k < total_nodes; k += RENEW_THREADS)
+        if (rc_lds[k]) atomicAdd(&cnt[k], rc_lds[k]);
+}
+
+// Exclusive prefix of the per-leaf counts: segment starts and cursors.
+__global__ __launch_bounds__(1024) void k_renew_offsets(const uint32_t *__restrict__ cnt,
+                                                        uint32_t total_nodes, uint32_t *off,
+                                                        uint32_t *cursor) {
+    __shared__ uint32_t wave_tot[17];
+    for (uint32_t k = threadIdx.x; k < total_nodes; k += blockDim.x) off[k] = cnt[k];
+    __syncthreads();
+    block_exclusive_scan(off, total_nodes, wave_tot);
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k < total_nodes; k += blockDim.x) cursor[k] = off[k];
+}
+
+// Keys into their leaf's segment (order inside a segment is free).
+__global__ __launch_bounds__(RENEW_THREADS) void k_renew_scatter(
+    const uint32_t *__restrict__ leaf_of, const uint32_t *__restrict__ keys, uint32_t ns,
+    uint32_t total_nodes, uint32_t *cursor, uint32_t *__restrict__ seg) {
+    extern __shared__ uint32_t rs_lds[];             // [2 * total_nodes]: counts, bases
+    uint32_t *s_cnt = rs_lds, *s_base = rs_lds + total_nodes;
+    for (uint32_t k = threadIdx.x; k < total_nodes; k += RENEW_THREADS) s_cnt[k] = 0;
+    __syncthreads();
+    const uint32_t s = blockIdx.x * RENEW_THREADS + threadIdx.x;
+    uint32_t n = 0, local = 0;
+    if (s < ns) {
+        n = leaf_of[s];
+        local = atomicAdd(&s_cnt[n], 1u);
+    }
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k < total_nodes; k += RENEW_THREADS)
+        if (s_cnt[k]) s_base[k] = atomicAdd(&cursor[k], s_cnt[k]);
+    __syncthreads();
+    if (s < ns) seg[s_base[n] + local] = keys[s];
+}
+
+// One workgroup per node: radix select of the k-th key (4 passes of 8 bits),
+// then the renewed leaf.  With delta != null (leaf-wise) a changed leaf
+// records delta = new - old; every other node gets delta = 0.
+__global__ __launch_bounds__(256) void k_renew_select(const uint32_t *__restrict__ seg,
+                                                      const uint32_t *__restrict__ off,
+                                                      const uint32_t *__restrict__ cnt, float q,
+                                                      float lr, const float2 *__restrict__ bounds,
+                                                      TreeOut tree, float *delta) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_k;
+    const uint32_t n = blockIdx.x;
+    const uint32_t c = cnt[n];
+    if (c < 4) {
+        if (delta && threadIdx.x == 0) delta[n] = 0.0f;
+        return;
+    }
+    const uint32_t *sg = seg + off[n];
+    if (threadIdx.x == 0) {
+        uint32_t k = (uint32_t)((float)c * q);
+        s_k = k < c - 1 ? k : c - 1;
+        s_prefix = 0;
+    }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[threadIdx.x] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix;
+        const uint32_t hi_mask = shift == 24 ? 0u : (0xFFFFFFFFu << (shift + 8));
+        for (uint32_t j = threadIdx.x; j < c; j += 256) {
+            const uint32_t key = sg[j];
+            if ((key & hi_mask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFFu], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t k = s_k, cum = 0, b = 0;
+            for (; b < 255; ++b) {
+                if (cum + hist[b] > k) break;
+                cum += hist[b];
+            }
+            s_prefix = prefix | (b << shift);
+            s_k = k - cum;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x != 0) return;
+    const float2 bd = bounds[n];
+    float v = key_float(s_prefix);
+    v = v > bd.x ? v : bd.x;                         // min(max(q, lo), hi)
+    v = v < bd.y ? v : bd.y;
+    v = lr * v;
+    if (delta) {
+        const float old = tree.leaf[n];
+        delta[n] = v != old ? v - old : 0.0f;
+        tree.leaf[n] = v;
+    } else {
+        tree.leaf[n] = v;
+    }
+}
+
+size_t renew_sample_count(int64_t rows) {
+    int64_t step = rows / 262144;
+    if (step < 1) step = 1;
+    return (size_t)((rows + step - 1) / step);
+}
+
+hipError_t launch_renew(hipStream_t s, const uint8_t *bins_fm, int64_t rows, int32_t nb,
+                        int32_t max_depth, TreeOut tree, const float *labels,
+                        const float *preds, const float2 *bounds, float q, float lr,
+                        uint32_t *leaf_of, uint32_t *keys, uint32_t *seg, uint32_t *cnt,
+                        uint32_t *off, uint32_t *cursor, float *delta) {
+    int64_t step = rows / 262144;
+    if (step < 1) step = 1;
+    const uint32_t ns = (uint32_t)renew_sample_count(rows);
+    const uint32_t total = (1u << (max_depth + 1)) - 1u;
+    const unsigned blocks = (ns + RENEW_THREADS - 1) / RENEW_THREADS;
+    hipError_t e = hipMemsetAsync(cnt, 0, (size_t)total * sizeof(uint32_t), s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_renew_collect, dim3(blocks), dim3(RENEW_THREADS),
+                       (size_t)total * sizeof(uint32_t), s, bins_fm, rows, nb, max_depth, tree,
+                       labels, preds, step, ns, total, leaf_of, keys, cnt);
+    hipLaunchKernelGGL(k_renew_offsets, dim3(1), dim3(1024), 0, s, cnt, total, off, cursor);
+    hipLaunchKernelGGL(k_renew_scatter, dim3(blocks), dim3(RENEW_THREADS),
+                       (size_t)total * 2 * sizeof(uint32_t), s, leaf_of, keys, ns, total, cursor,
+                       seg);
+    hipLaunchKernelGGL(k_renew_select, dim3(total), dim3(256), 0, s, seg, off, cnt, q, lr,
+                       bounds, tree, delta);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // leaf-wise (best-first) growth: leaf_init (:683-716), leaf_pick_apply
 // (:720-871), leaf_step (:879-1091) and the stable segment partition
 // (partition_count/scan/scatter, :520-620).  Every step is a fixed chain of
@@ -2027,6 +2196,20 @@ __global__ __launch_bounds__(64) void k_lw_pick(SplitParams sp, LWArgs a, LWStat
 hipError_t launch_lw_pick(hipStream_t s, const SplitParams &sp, const LWArgs &a, LWState *st,
                           LWOpen *open, const int8_t *monotone, TreeCtl *ctl, const TreeOut out) {
     hipLaunchKernelGGL(k_lw_pick, dim3(1), dim3(64), 0, s, sp, a, st, open, monotone, ctl, out);
+    return hipGetLastError();
+}
+
+// Every open-list node's leaf bounds into bounds[node] (leaf renewal reads
+// them for the finished tree's leaves).
+__global__ void k_lw_bounds(const LWState *st, const LWOpen *open, float2 *bounds) {
+    const uint32_t n = st->open_count;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+        bounds[open[i].node] = make_float2(open[i].lo, open[i].hi);
+}
+
+hipError_t launch_lw_bounds(hipStream_t s, const LWState *st, const LWOpen *open,
+                            float2 *bounds) {
+    hipLaunchKernelGGL(k_lw_bounds, dim3(1), dim3(256), 0, s, st, open, bounds);
     return hipGetLastError();
 }
 

@@ -226,6 +226,18 @@ hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const Level
 hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,
                               TreeOut out);
 
+// Leaf renewal of the L1 / quantile objectives for one finished tree: the
+// sampled rows' residual quantiles replace its leaf values in place.  Scratch:
+// leaf_of, keys, seg hold renew_sample_count(rows) u32; cnt, off, cursor
+// 2^(max_depth+1)-1 u32.  delta (nodes f32, or null) receives new - old for
+// the leaf-wise update of preds that already hold the old leaves.
+size_t renew_sample_count(int64_t rows);
+hipError_t launch_renew(hipStream_t s, const uint8_t *bins_fm, int64_t rows, int32_t nb,
+                        int32_t max_depth, TreeOut tree, const float *labels,
+                        const float *preds, const float2 *bounds, float q, float lr,
+                        uint32_t *leaf_of, uint32_t *keys, uint32_t *seg, uint32_t *cnt,
+                        uint32_t *off, uint32_t *cursor, float *delta);
+
 // Partition of the routed level (d-1): every split node's interval is split
 // in place between its children (left from the front, right from the back).
 // Node l's cursor is cursors[l * CURSOR_STRIDE]: left count in the low word,
@@ -302,6 +314,8 @@ hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp,
                           const LWState *st, LWOpen *open, const SplitResult *results,
                           const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,
                           const TreeOut out);
+hipError_t launch_lw_bounds(hipStream_t s, const LWState *st, const LWOpen *open,
+                            float2 *bounds);
 hipError_t launch_lw_pick(hipStream_t s, const SplitParams &sp, const LWArgs &a, LWState *st,
                           LWOpen *open, const int8_t *monotone, TreeCtl *ctl, const TreeOut out);
 hipError_t launch_lw_count(hipStream_t s, const LWArgs &a, const LWState *st,
@@ -329,8 +343,9 @@ hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float 
 hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                                  int32_t num_bins, int32_t max_depth, const TreeOut tree,
                                  float *preds);
-// Training-row walk of a finished level-wise tree: preds += leaf, and rows per
-// node of the deepest level added to count[2^D - 1 ...].
+// Training-row walk of a finished level-wise tree: preds += leaf (unless
+// preds is null), and rows per node of the deepest level added to
+// count[2^D - 1 ...].
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                              int32_t num_bins, int32_t max_depth, const TreeOut tree,
                              float *preds, uint32_t *count);

@@ -101,6 +101,11 @@ struct Trainer {
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
+    // leaf renewal (L1 / quantile objectives)
+    bool renewal = false;
+    float renewal_q = 0.5f;
+    DevBuf<uint32_t> rn_leaf, rn_keys, rn_seg, rn_cnt, rn_off, rn_cursor;
+    DevBuf<float> rn_delta;
     // leaf-wise growth
     bool leafwise = false;
     mbk::LWArgs lw{};
@@ -245,6 +250,16 @@ static void check_leakage(Trainer &t, const float *x, int64_t rows, int64_t cols
 }
 
 static float base_score(const Params &p, const float *y, const float *w, int64_t n) {
+    if (p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE) {   // :786-794, :798-801
+        const float q = p.objective == OBJ_MAE ? 0.5f : p.alpha;
+        const int64_t step = std::max<int64_t>(1, n / 200000);
+        std::vector<float> s;
+        for (int64_t i = 0; i < n; i += step) s.push_back(y[i]);
+        std::sort(s.begin(), s.end());
+        const int64_t idx = std::min<int64_t>((int64_t)s.size() - 1,
+                                              (int64_t)((float)s.size() * q));
+        return s[(size_t)idx];
+    }
     if (p.objective == OBJ_LOGISTIC) {                     // :802-830
         double pos = 0, tot = 0;
         const double spw = (double)p.scale_pos_weight;
@@ -350,9 +365,6 @@ static float eval_metric(const Params &p, const float *pred, const float *y, int
 // Checks shared by both entry points (Booster.swift:451-529).
 static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
                             const float *w, const float *xv, int64_t vrows, const float *yv) {
-    if (p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE)
-        invalid("objective '" + objective_name(p.objective) +
-                "' (leaf renewal) is not supported by this build yet");
     if (p.objective == OBJ_MULTICLASS) invalid("multiclass is not supported by this build yet");
     if (!p.init_model.empty()) invalid("init_model (warm start) is not supported by this build yet");
     validate_labels(p, y, rows);
@@ -537,6 +549,18 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         t.lw_state.alloc(1);
         t.lw_open.alloc((size_t)2 * p.num_leaves + 2);
     }
+    t.renewal = p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE;
+    if (t.renewal) {
+        t.renewal_q = p.objective == OBJ_MAE ? 0.5f : p.alpha;
+        const size_t ns = mbk::renew_sample_count(rows);
+        t.rn_leaf.alloc(ns);
+        t.rn_keys.alloc(ns);
+        t.rn_seg.alloc(ns);
+        t.rn_cnt.alloc((size_t)t.total_nodes);
+        t.rn_off.alloc((size_t)t.total_nodes);
+        t.rn_cursor.alloc((size_t)t.total_nodes);
+        t.rn_delta.alloc((size_t)t.total_nodes);
+    }
     t.count.alloc((size_t)t.total_nodes);
     t.node_g.alloc((size_t)t.total_nodes);
     t.node_h.alloc((size_t)t.total_nodes);
@@ -684,6 +708,16 @@ static const uint8_t *tree_feature_mask(Trainer &t, int tree) {
     return t.tree_masks.back().data();
 }
 
+// Leaf renewal of a finished tree (L1 / quantile objectives): residual
+// quantiles of the sampled rows replace its leaf values; with delta, the
+// change of each leaf is recorded for preds that already hold the old values.
+static void renew_tree(Trainer &t, const mbk::TreeOut &out, float *delta) {
+    MB_HIP(mbk::launch_renew(t.dev->stream, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
+                             t.labels.ptr, t.preds.ptr, t.bounds.ptr, t.renewal_q,
+                             t.p.learning_rate, t.rn_leaf.ptr, t.rn_keys.ptr, t.rn_seg.ptr,
+                             t.rn_cnt.ptr, t.rn_off.ptr, t.rn_cursor.ptr, delta));
+}
+
 // GOSS after ceil(1/learning_rate) warm-up trees, bagging on every tree
 // (gossActive / bagging, Booster.swift:1382-1384, :617).
 static bool tree_sampled(const Params &p, int tree) {
@@ -772,9 +806,16 @@ static void grow_levelwise(Trainer &t, int tree) {
             // Shaders.swift:1280-1311) and counts the deepest nodes' rows
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, false));
-            MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr,
-                                          t.count.ptr));
+            MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
+                                          t.renewal ? nullptr : t.preds.ptr, t.count.ptr));
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
+            if (t.renewal) {
+                // residuals before the tree (routing applies nothing), then
+                // one walk with the renewed leaves (Booster.swift:1596-1630)
+                renew_tree(t, out, nullptr);
+                MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
+                                                  t.preds.ptr));
+            }
             break;
         }
         if (terminal) {
@@ -789,6 +830,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                                           t.items.ptr, t.scratch.ptr));
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, true));
+            if (t.renewal) renew_tree(t, out, nullptr);
             MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
                                               t.preds.ptr));
             break;
@@ -871,6 +913,19 @@ static void grow_leafwise(Trainer &t, int tree) {
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
                                           t.vpreds.ptr));
+    if (t.renewal) {
+        // residuals after the tree's first leaf values, then each leaf's
+        // change is added (Booster.swift:1253-1290)
+        MB_HIP(mbk::launch_lw_bounds(s, t.lw_state.ptr, t.lw_open.ptr, t.bounds.ptr));
+        renew_tree(t, out, t.rn_delta.ptr);
+        mbk::TreeOut dout = out;
+        dout.leaf = t.rn_delta.ptr;
+        MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, dout,
+                                          t.preds.ptr));
+        if (t.has_valid)
+            MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, dout,
+                                              t.vpreds.ptr));
+    }
     MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
                           hipMemcpyDeviceToDevice, s));
 }

@@ -55,6 +55,7 @@ float orc_splitmix_normal(uint64_t *s) {          /* DataGen.swift:22-25 */
 
 void orc_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise,
                   float *x, float *y) {           /* DataGen.swift:68-94 */
+    if (cols < 5 || rows <= 0) return;              /* precondition(cols >= 5) */
     for (int32_t f = 0; f < cols; ++f) {
         uint64_t s = seed + (uint64_t)f * GOLDEN;
         float *col = x + (int64_t)f * rows;
@@ -168,6 +169,22 @@ float orc_base_score(const float *y, const float *w, int64_t rows, int32_t obj, 
     float m = den > 0 ? (float)(num / den) : 0.0f;
     if (obj == ORC_OBJ_POISSON || obj == ORC_OBJ_TWEEDIE) return logf(m);
     return m;
+}
+
+/* subsampleQuantile (Booster.swift:786-794): the base score of the L1 and
+ * quantile objectives, from every max(1, rows/200000)-th label. */
+float orc_label_quantile(const float *y, int64_t rows, float q) {
+    int64_t step = rows / 200000;
+    if (step < 1) step = 1;
+    float *s = (float *)malloc(sizeof(float) * (size_t)(rows / step + 1));
+    int64_t m = 0;
+    for (int64_t i = 0; i < rows; i += step) s[m++] = y[i];
+    qsort(s, (size_t)m, sizeof(float), cmp_float);
+    int64_t idx = (int64_t)((float)m * q);
+    if (idx > m - 1) idx = m - 1;
+    float v = s[idx];
+    free(s);
+    return v;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -404,6 +421,7 @@ typedef struct {
     const uint32_t *rows_in;    /* the tree's rows (ascending); NULL = all rows */
     int64_t n_in;
     int apply_preds;            /* 0: preds are updated by a walk after the tree */
+    float *node_lo, *node_hi;   /* out: the tree's leaf bounds per node (or NULL) */
 } fit_ctx;
 
 static void best_over_features(const fit_ctx *c, const int64_t *hg, const int64_t *hh,
@@ -633,6 +651,10 @@ static int grow_levelwise(const fit_ctx *c, float *preds, orc_forest *out, int64
     }
     for (int32_t n = 0; n < total; ++n) out->cover[base + n] = (float)cnt[n];
     free(split_f);
+    if (c->node_lo) {
+        memcpy(c->node_lo, blo, sizeof(float) * (size_t)total);
+        memcpy(c->node_hi, bhi, sizeof(float) * (size_t)total);
+    }
     free(cnt); free(seg); free(gi); free(hi); free(blo); free(bhi); free(cur_g);
     free(cur_h); free(prv_g); free(prv_h); free(order); free(tmp);
     return 0;
@@ -758,8 +780,81 @@ static int grow_leafwise(const fit_ctx *c, float *preds, orc_forest *out, int64_
         open[i1] = cr;
     }
     walk_preds(c, out, base, preds);
+    if (c->node_lo) {
+        memcpy(c->node_lo, blo, sizeof(float) * (size_t)total);
+        memcpy(c->node_hi, bhi, sizeof(float) * (size_t)total);
+    }
     free(blo); free(bhi); free(open); free(order); free(tmp); free(hg); free(hh);
     return 0;
+}
+
+/* The leaf a binned row reaches (assign_leaves). */
+static int32_t leaf_of_row(const fit_ctx *c, const orc_forest *out, int64_t base, int64_t i) {
+    const int32_t D = c->p->max_depth, nb = c->nb;
+    static const uint32_t zero[8] = {0};
+    int32_t n = 0;
+    for (int32_t d = 0; d < D; ++d) {
+        int32_t f = out->feature[base + n];
+        if (f < 0) break;
+        uint8_t b = c->fm[(int64_t)f * c->rows + i];
+        const uint32_t *mask = out->cat_mask ? out->cat_mask + (base + n) * 8 : zero;
+        n = 2 * n + 1 + (bin_goes_left(b, out->split_bin[base + n], out->flags[base + n], mask,
+                                       nb) ? 0 : 1);
+    }
+    return n;
+}
+
+/* Leaf renewal for the L1 and quantile objectives (Booster.swift:634-639,
+ * :1596-1615 level-wise, :1253-1290 leaf-wise): residuals y - preds over
+ * the rows i = 0, step, 2*step, ... (step = max(1, rows/262144)), bucketed by
+ * the row's leaf; a leaf with >= 4 sampled residuals becomes
+ * lr * min(max(r[min(n-1, (int)((float)n*q))], lo), hi) over the sorted r.
+ * With delta != NULL (leaf-wise: preds already hold the tree's first leaf
+ * values) a changed leaf records delta[n] = new - old, else delta[n] = 0. */
+static void renew_leaves(const fit_ctx *c, orc_forest *out, int64_t base, const float *y,
+                         const float *preds, float q, float *delta) {
+    const int32_t total = out->nodes_per_tree;
+    const int64_t N = c->rows;
+    int64_t step = N / 262144;
+    if (step < 1) step = 1;
+    const int64_t ns = (N + step - 1) / step;
+    int32_t *leaf = (int32_t *)malloc(sizeof(int32_t) * (size_t)ns);
+    int64_t *cnt = (int64_t *)calloc((size_t)total + 1, sizeof(int64_t));
+    float *res = (float *)malloc(sizeof(float) * (size_t)ns);
+    int64_t *pos = (int64_t *)malloc(sizeof(int64_t) * ((size_t)total + 1));
+    for (int64_t s = 0; s < ns; ++s) {
+        leaf[s] = leaf_of_row(c, out, base, s * step);
+        cnt[leaf[s]]++;
+    }
+    int64_t acc = 0;
+    for (int32_t n = 0; n < total; ++n) { pos[n] = acc; acc += cnt[n]; }
+    int64_t *fill = (int64_t *)malloc(sizeof(int64_t) * (size_t)total);
+    memcpy(fill, pos, sizeof(int64_t) * (size_t)total);
+    for (int64_t s = 0; s < ns; ++s) {
+        int64_t i = s * step;
+        res[fill[leaf[s]]++] = y[i] - preds[i];
+    }
+    for (int32_t n = 0; n < total; ++n) {
+        if (delta) delta[n] = 0.0f;
+        if (cnt[n] < 4) continue;
+        float *r = res + pos[n];
+        qsort(r, (size_t)cnt[n], sizeof(float), cmp_float);
+        int64_t k = (int64_t)((float)cnt[n] * q);
+        if (k > cnt[n] - 1) k = cnt[n] - 1;
+        float v = r[k];
+        v = v > c->node_lo[n] ? v : c->node_lo[n];
+        v = v < c->node_hi[n] ? v : c->node_hi[n];
+        v = c->p->learning_rate * v;
+        if (delta) {
+            if (v != out->leaf[base + n]) {
+                delta[n] = v - out->leaf[base + n];
+                out->leaf[base + n] = v;
+            }
+        } else {
+            out->leaf[base + n] = v;
+        }
+    }
+    free(leaf); free(cnt); free(res); free(pos); free(fill);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -845,9 +940,13 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
     uint32_t *ghq = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)rows);
     uint8_t *kept = (uint8_t *)malloc((size_t)rows);
     uint32_t *sel = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)rows);
+    float *node_lo = (float *)malloc(sizeof(float) * (size_t)total);
+    float *node_hi = (float *)malloc(sizeof(float) * (size_t)total);
+    float *delta = (float *)malloc(sizeof(float) * (size_t)total);
     uint32_t *split_bin = out->split_bin;
-    if (!rm || !g || !h || !ghq || !kept || !sel) {
+    if (!rm || !g || !h || !ghq || !kept || !sel || !node_lo || !node_hi || !delta) {
         free(rm); free(g); free(h); free(ghq); free(kept); free(sel);
+        free(node_lo); free(node_hi); free(delta);
         return -1;
     }
     for (int32_t f = 0; f < cols; ++f)
@@ -884,12 +983,30 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
         c.h_inv = mh / 127.0f;
         c.rows_in = rows_in;
         c.n_in = n_in;
-        c.apply_preds = rows_in == NULL;
+        const int renewal = p->objective == ORC_OBJ_MAE || p->objective == ORC_OBJ_QUANTILE;
+        c.apply_preds = rows_in == NULL && !renewal;
+        c.node_lo = renewal ? node_lo : NULL;
+        c.node_hi = renewal ? node_hi : NULL;
         rc = p->num_leaves > 0 ? grow_leafwise(&c, preds, out, base, NULL)
                                : grow_levelwise(&c, preds, out, base, NULL);
-        /* sampled level-wise trees: every row's prediction from one walk
-         * (Booster.swift:1568-1580); leaf-wise growth always walks */
-        if (rc == 0 && rows_in && p->num_leaves <= 0) walk_preds(&c, out, base, preds);
+        if (rc == 0 && renewal) {
+            const float q = p->objective == ORC_OBJ_MAE ? 0.5f : p->alpha;
+            if (p->num_leaves > 0) {
+                /* leaf-wise: residuals after the tree's first leaf values,
+                 * then the changes are added (Booster.swift:1253-1290) */
+                renew_leaves(&c, out, base, y, preds, q, delta);
+                for (int64_t i = 0; i < rows; ++i) preds[i] += delta[leaf_of_row(&c, out, base, i)];
+            } else {
+                /* level-wise: residuals before the tree (route apply = 0),
+                 * then one walk with the renewed leaves (:1596-1630) */
+                renew_leaves(&c, out, base, y, preds, q, NULL);
+                walk_preds(&c, out, base, preds);
+            }
+        } else if (rc == 0 && rows_in && p->num_leaves <= 0) {
+            /* sampled level-wise trees: every row's prediction from one walk
+             * (Booster.swift:1568-1580); leaf-wise growth always walks */
+            walk_preds(&c, out, base, preds);
+        }
         /* reachable nodes only (Booster.swift:918-945) */
         {
             uint8_t *reach = (uint8_t *)calloc((size_t)total, 1);
@@ -920,6 +1037,7 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
     }
     if (!split_bin) { free(out->split_bin); out->split_bin = NULL; }
     free(rm); free(g); free(h); free(ghq); free(kept); free(sel);
+    free(node_lo); free(node_hi); free(delta);
     return rc;
 }
 

@@ -90,6 +90,9 @@ void orc_bin_matrix(const float *x, int64_t rows, int32_t cols, int64_t row_stri
 /* --- gradients / quantisation (Shaders.swift:96-192) --------------------- */
 float orc_base_score(const float *y, const float *w, int64_t rows, int32_t objective,
                      float scale_pos_weight);
+/* L1 / quantile base score: the q-quantile of every max(1, rows/200000)-th
+ * label (subsampleQuantile, Booster.swift:786-794). */
+float orc_label_quantile(const float *y, int64_t rows, float q);
 void orc_gradients(const float *preds, const float *y, const float *w, int64_t rows,
                    int32_t objective, float alpha, float aux, float *g, float *h,
                    float *max_g, float *max_h);

@@ -82,6 +82,8 @@ def _configure(l: ctypes.CDLL) -> None:
     l.orc_bin_matrix.argtypes = [_P, _I64, _I32, _I64, _I64, _P, _P, _I32, _P]
     l.orc_base_score.restype = _F
     l.orc_base_score.argtypes = [_P, _P, _I64, _I32, _F]
+    l.orc_label_quantile.restype = _F
+    l.orc_label_quantile.argtypes = [_P, _I64, _F]
     l.orc_gradients.argtypes = [_P, _P, _P, _I64, _I32, _F, _F, _P, _P, _P, _P]
     l.orc_quantize.argtypes = [_P, _P, _I64, _F, _F, _P]
     l.orc_hist_node.argtypes = [_P, _I64, _I32, _I32, _P, _P, _I64, _P, _P]
@@ -113,6 +115,8 @@ def splitmix_stream(seed: int, n: int) -> np.ndarray:
 
 def friedman(rows: int, cols: int, seed: int, noise: float = 1.0):
     """Feature-major X [cols, rows] and y, DataGen.friedman."""
+    if cols < 5:
+        raise ValueError("friedman needs cols >= 5 (DataGen.swift:69)")
     x = np.empty((cols, rows), dtype=np.float32)
     y = np.empty(rows, dtype=np.float32)
     lib().orc_friedman(rows, cols, ctypes.c_uint64(seed), noise, _ptr(x), _ptr(y))
@@ -143,9 +147,12 @@ def bin_matrix(x_fm: np.ndarray, edges: np.ndarray, num_bins: int, is_cat=None):
 # gradients / histograms / splits
 # --------------------------------------------------------------------------
 
-def base_score(y, w=None, objective=OBJ_L2, scale_pos_weight=1.0) -> float:
+def base_score(y, w=None, objective=OBJ_L2, scale_pos_weight=1.0, alpha=0.9) -> float:
     y = np.ascontiguousarray(y, dtype=np.float32)
     w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    if objective in (OBJ_MAE, OBJ_QUANTILE):
+        q = 0.5 if objective == OBJ_MAE else alpha
+        return float(lib().orc_label_quantile(_ptr(y), len(y), q))
     return float(lib().orc_base_score(_ptr(y), _ptr(w), len(y), objective, scale_pos_weight))
 
 
@@ -277,7 +284,7 @@ def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objectiv
     y = np.ascontiguousarray(y, np.float32)
     w = None if w is None else np.ascontiguousarray(w, np.float32)
     if base is None:
-        base = base_score(y, w, objective, aux if objective == OBJ_LOGISTIC else 1.0)
+        base = base_score(y, w, objective, aux if objective == OBJ_LOGISTIC else 1.0, alpha)
     preds = np.full(rows, base, np.float32)
     nodes = (1 << (max_depth + 1)) - 1
     forest = Forest.empty(num_trees, nodes)

@@ -41,7 +41,10 @@ def oracle_fit(x_fm, y, params, is_cat=None):
               min_split_gain=p.pop("min_split_gain", 0.0), cat_smooth=p.pop("cat_smooth", 10.0))
     nb = p.pop("num_bins", 256)
     obj = p.pop("objective", "regression")
-    kw["objective"] = {"regression": O.OBJ_L2, "binary": O.OBJ_LOGISTIC}[obj]
+    kw["objective"] = {"regression": O.OBJ_L2, "binary": O.OBJ_LOGISTIC, "mae": O.OBJ_MAE,
+                       "quantile": O.OBJ_QUANTILE}[obj]
+    if "alpha" in p:
+        kw["alpha"] = p.pop("alpha")
     mono = p.pop("monotone_constraints", None)
     p.pop("categorical_features", None)
     for key in ("goss", "goss_top_rate", "goss_other_rate", "subsample"):
@@ -59,8 +62,16 @@ def check_identical(x_fm, y, params, is_cat=None, x_test=None):
     assert np.float32(obj["baseScore"]) == np.float32(ref.base_score)
     has_cats = is_cat is not None and any(is_cat)
     model_io.assert_same_forest(got, ref.forest, with_cats=has_cats)
-    # training predictions: GPU predict on the train matrix == oracle's running preds
-    assert np.array_equal(mb.predict(h, x_fm, feature_major=True), ref.preds)
+    # training predictions: GPU predict on the train matrix == oracle's running
+    # preds.  Leaf-wise renewal adds each tree as (preds + first leaf) + change
+    # (Booster.swift:1253-1290), which rounds differently from one addition of
+    # the final leaf, so there the oracle's own predict is the reference.
+    gp_train = mb.predict(h, x_fm, feature_major=True)
+    if params.get("num_leaves", 0) > 0 and params.get("objective") in ("mae", "quantile"):
+        assert np.array_equal(gp_train, O.predict(ref.forest, ref.base_score, ref.num_bins, x_fm))
+        assert np.allclose(gp_train, ref.preds, rtol=1e-5, atol=1e-4)
+    else:
+        assert np.array_equal(gp_train, ref.preds)
     if x_test is not None:
         gp = mb.predict(h, x_test, feature_major=True)
         cp = O.predict(ref.forest, ref.base_score, ref.num_bins, x_test)
@@ -416,6 +427,49 @@ def test_valid_eval_and_early_stopping_match_oracle():
     assert (rmse[best:] >= rmse[best - 1] * (1 - 1e-6)).all()      # the 5 stale rounds
     got = model_io.forest_from_json(model_io.saved_model(h), ref.forest.nodes_per_tree)
     model_io.assert_same_forest(got, _first_trees(ref.forest, best), with_cats=False)
+
+
+# --------------------------------------------------------------------------
+# L1 / quantile objectives: leaf renewal
+# --------------------------------------------------------------------------
+
+def _outlier_friedman(rows, cols, seed):
+    x, y = O.friedman(rows, cols, seed)
+    rng = np.random.default_rng(seed)
+    y = y.copy()
+    y[rng.random(rows) < 0.02] += 100.0
+    return x, y
+
+
+@pytest.mark.parametrize("params", [
+    {"num_trees": 30, "max_depth": 6, "objective": "mae"},
+    {"num_trees": 30, "max_depth": 5, "objective": "quantile", "alpha": 0.9},
+    {"num_trees": 25, "max_depth": 6, "num_leaves": 20, "objective": "quantile", "alpha": 0.2},
+    {"num_trees": 25, "max_depth": 7, "num_leaves": 40, "objective": "mae"},
+    {"num_trees": 25, "max_depth": 5, "objective": "mae", "goss": True, "learning_rate": 0.3},
+    {"num_trees": 20, "max_depth": 6, "objective": "quantile", "alpha": 0.7,
+     "monotone_constraints": [1, 0, 0, 0, 0, 0, -1, 0]},
+])
+def test_leaf_renewal_identical_trees(params):
+    # Booster.swift:634-639, :1241-1290, :1596-1615
+    x, y = _outlier_friedman(30_000, 8, 91)
+    xt, _ = O.friedman(5000, 8, 92)
+    check_identical(x, y, params, x_test=xt)
+
+
+def test_leaf_renewal_strided_sample_identical():
+    # more than 2 * 262144 rows: renewal samples every other row, and the base
+    # score every third label
+    x, y = _outlier_friedman(600_000, 5, 93)
+    check_identical(x, y, {"num_trees": 4, "max_depth": 6, "objective": "quantile",
+                           "alpha": 0.6})
+
+
+def test_leaf_renewal_nan_categorical_identical():
+    x, y, cats = D.c3_mixed(40_000, 7)
+    is_cat = [0] * 80 + [1] * 20
+    check_identical(x, y, {"num_trees": 10, "max_depth": 6, "objective": "mae",
+                           "categorical_features": cats}, is_cat=is_cat)
 
 
 # --------------------------------------------------------------------------

@@ -598,3 +598,130 @@ def test_bagging_selection_properties(oracle):
     assert kept[np.argmax(np.abs(g))]                       # |g| = max|g| is always kept
     assert abs(kept.mean() - 0.3) < 5 * np.sqrt(0.3 * 0.7 / n)
     assert O.sample_rows(g, h, mg, 0) is None               # subsample 1: no sampling
+
+
+# --------------------------------------------------------------------------
+# L1 / quantile objectives: base score and leaf renewal
+# --------------------------------------------------------------------------
+
+def _np_quantile_pick(values, q):
+    # r[min(n-1, Int(Float(n) * q))] over the ascending sample (Booster.swift:1272, :1611)
+    s = np.sort(np.asarray(values, np.float32))
+    n = s.size
+    return s[min(n - 1, int(np.float32(n) * np.float32(q)))]
+
+
+@pytest.mark.parametrize("rows,q", [(1000, 0.5), (600_001, 0.5), (40_000, 0.9), (7, 0.1)])
+def test_label_quantile_base_score(oracle, rows, q):
+    # subsampleQuantile (Booster.swift:786-794): every max(1, rows/200000)-th label
+    y = np.random.default_rng(rows).standard_normal(rows).astype(np.float32)
+    step = max(1, rows // 200_000)
+    want = _np_quantile_pick(y[::step], q)
+    obj = O.OBJ_MAE if q == 0.5 else O.OBJ_QUANTILE
+    assert O.base_score(y, objective=obj, alpha=q) == want
+
+
+def _stump_rows(m, x):
+    """Rows going left at the root of tree 0 (numeric split, raw values)."""
+    f, thr = m.forest.feature[0, 0], m.forest.threshold[0, 0]
+    v = x[f]
+    left = v <= thr
+    miss = np.isnan(v)
+    left[miss] = bool(m.forest.flags[0, 0] & O.FLAG_DEFAULT_LEFT)
+    return left
+
+
+@pytest.mark.parametrize("rows,obj,q", [(5000, O.OBJ_MAE, 0.5), (600_000, O.OBJ_QUANTILE, 0.8),
+                                        (3000, O.OBJ_QUANTILE, 0.1)])
+def test_levelwise_renewal_closed_form(oracle, rows, obj, q):
+    # Level-wise renewal (Booster.swift:1596-1615): residuals y - preds taken
+    # BEFORE the tree, every max(1, rows/262144)-th row, per leaf; a leaf
+    # with >= 4 of them becomes lr * (its q-th order statistic).
+    rng = np.random.default_rng(rows)
+    x = rng.uniform(0, 1, size=(2, rows)).astype(np.float32)
+    y = (np.where(x[0] > 0.5, 5.0, -3.0) + rng.standard_exponential(rows)).astype(np.float32)
+    lr = 0.3
+    m = fit_raw(x, y, num_trees=1, max_depth=1, objective=obj, alpha=q, learning_rate=lr)
+    base = np.float32(m.base_score)
+    assert m.forest.feature[0, 0] >= 0
+    left = _stump_rows(m, x)
+    step = max(1, rows // 262_144)
+    idx = np.arange(0, rows, step)
+    res = (y - base)[idx]
+    for node, side in ((1, left[idx]), (2, ~left[idx])):
+        want = np.float32(lr) * _np_quantile_pick(res[side], q)
+        assert m.forest.leaf[0, node] == want, node
+    want_preds = base + np.where(left, m.forest.leaf[0, 1], m.forest.leaf[0, 2]).astype(np.float32)
+    assert np.array_equal(m.preds, want_preds)
+
+
+def test_leafwise_renewal_uses_residuals_after_the_tree(oracle):
+    # Leaf-wise renewal (Booster.swift:1241-1290) runs after predict_tree_binned
+    # has added the tree's first leaf values, so its residuals are
+    # y - (base + first leaf); the change is then added to preds.  First leaf
+    # values of the first MAE tree: g = +-1, h = 1 quantised to +-32767 / 127,
+    # leaf = lr * -G / (H + lambda) (Shaders.swift:1491-1511).
+    rows, lr, lam = 4000, 0.5, 1.0
+    rng = np.random.default_rng(9)
+    x = rng.uniform(0, 1, size=(2, rows)).astype(np.float32)
+    y = (np.where(x[1] > 0.3, 2.0, -1.0) + rng.standard_normal(rows)).astype(np.float32)
+    m = fit_raw(x, y, num_trees=1, max_depth=1, num_leaves=2, objective=O.OBJ_MAE,
+                learning_rate=lr, lam=lam)
+    base = np.float32(m.base_score)
+    left = _stump_rows(m, x)
+    g = np.where(base > y, 1, -1)
+    g_inv = np.float32(1.0) / np.float32(32767.0)
+    h_inv = np.float32(1.0) / np.float32(127.0)
+    preds = np.full(rows, base, np.float32)
+    first = {}
+    for node, side in ((1, left), (2, ~left)):
+        G = np.float32(int(g[side].sum()) * 32767) * g_inv
+        H = np.float32(int(side.sum()) * 127) * h_inv
+        first[node] = np.float32(lr) * (-G / (H + np.float32(lam)))
+        preds[side] = base + first[node]
+    for node, side in ((1, left), (2, ~left)):
+        want = np.float32(lr) * _np_quantile_pick((y - preds)[side], 0.5)
+        assert m.forest.leaf[0, node] == want, node
+    want_preds = preds.copy()
+    for node, side in ((1, left), (2, ~left)):
+        want_preds[side] = preds[side] + (m.forest.leaf[0, node] - first[node])
+    assert np.array_equal(m.preds, want_preds)
+
+
+def test_mae_and_huber_robust_to_outliers(oracle):
+    # ObjectiveTests.swift:27-46
+    rows = 20_000
+    x, y = O.friedman(rows, 8, 81)
+    clean = y.copy()
+    rng = O.SplitMix(82)
+    out = np.array([rng.uniform() for _ in range(rows)]) < 0.02
+    y = y.copy()
+    y[out] += 500
+
+    def median_err(obj):
+        m = fit_raw(x, y, num_trees=150, max_depth=5, objective=obj)
+        return float(np.median(np.abs(predict(m, x) - clean)))
+
+    l2 = median_err(O.OBJ_L2)
+    assert median_err(O.OBJ_MAE) < l2
+    assert median_err(O.OBJ_HUBER) < l2
+
+
+@pytest.mark.parametrize("alpha", [0.1, 0.9])
+def test_quantile_coverage(oracle, alpha):
+    # ObjectiveTests.swift:48-63: empirical coverage matches alpha within 0.03
+    rows = 30_000
+    x, y = O.friedman(rows, 8, 83)
+    m = fit_raw(x, y, num_trees=150, max_depth=5, objective=O.OBJ_QUANTILE, alpha=alpha)
+    cov = float(np.mean(y <= predict(m, x)))
+    assert abs(cov - alpha) < 0.03, cov
+
+
+def test_leafwise_quantile_coverage(oracle):
+    # LeafWiseTests.swift:170-185
+    rows = 8000
+    x, y = O.friedman(rows, 5, 551)
+    m = fit_raw(x, y, num_trees=80, max_depth=8, num_leaves=31, objective=O.OBJ_QUANTILE,
+                alpha=0.9)
+    cov = float(np.mean(y <= predict(m, x)))
+    assert abs(cov - 0.9) < 0.05, cov
