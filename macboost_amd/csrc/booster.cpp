@@ -220,18 +220,27 @@ void Booster::build_forest() {                    // forestBuffers, Booster.swif
     forest.valid = true;
 }
 
+// Raw scores, row-major [rows][K]; tree t adds to class t % K
+// (predict_forest, Shaders.swift:1548-1578).
 std::vector<float> Booster::predict(const float *x, int64_t rows, int64_t cols) {
-    std::vector<float> out((size_t)std::max<int64_t>(rows, 0), base_score);
+    const int K = std::max(1, trained_num_classes);
+    std::vector<float> out((size_t)std::max<int64_t>(rows, 0) * (size_t)K, 0.0f);
+    for (int64_t i = 0; i < rows; ++i)
+        for (int k = 0; k < K; ++k)
+            out[(size_t)(i * K + k)] = K > 1 ? base_scores[(size_t)k] : base_score;
     if (rows > 0 && !trees.empty()) {
         Device &d = device();
         build_forest();
-        DevBuf<float> xd((size_t)rows * (size_t)cols), od((size_t)rows);
+        DevBuf<float> xd((size_t)rows * (size_t)cols), od((size_t)rows * (size_t)K);
         MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, d.stream));
-        mbk::ForestDev f{forest.feature.ptr, forest.threshold.ptr, forest.flags.ptr, forest.leaf.ptr,
-                         forest.has_mask ? forest.mask.ptr : nullptr, forest.num_trees,
-                         forest.nodes_per_tree};
-        MB_HIP(mbk::launch_predict_forest(d.stream, f, xd.ptr, rows, trained_num_bins - 1,
-                                          base_score, od.ptr));
+        for (int k = 0; k < K; ++k) {
+            mbk::ForestDev f{forest.feature.ptr, forest.threshold.ptr, forest.flags.ptr,
+                             forest.leaf.ptr, forest.has_mask ? forest.mask.ptr : nullptr,
+                             forest.num_trees, forest.nodes_per_tree, k, K, K};
+            MB_HIP(mbk::launch_predict_forest(d.stream, f, xd.ptr, rows, trained_num_bins - 1,
+                                              K > 1 ? base_scores[(size_t)k] : base_score,
+                                              od.ptr + k));
+        }
         MB_HIP(hipMemcpyAsync(out.data(), od.ptr, od.bytes(), hipMemcpyDeviceToHost, d.stream));
         MB_HIP(hipStreamSynchronize(d.stream));
     }
@@ -240,10 +249,13 @@ std::vector<float> Booster::predict(const float *x, int64_t rows, int64_t cols) 
     return out;
 }
 
-// Expected raw score: base + cover-weighted leaf means (SHAP.swift:56-72).
-double Booster::shap_bias() const {
-    double bias = (double)base_score;
-    for (const auto &tree : trees) {
+// Expected raw score of class k: its base + cover-weighted leaf means of its
+// trees (SHAP.swift:56-72).
+double Booster::shap_bias(int k) const {
+    const int K = std::max(1, trained_num_classes);
+    double bias = K > 1 ? (double)base_scores[(size_t)k] : (double)base_score;
+    for (size_t t = (size_t)k; t < trees.size(); t += (size_t)K) {
+        const Tree &tree = trees[t];
         double total = tree.cover.empty() ? 0.0 : (double)tree.cover[0];
         if (!(total > 0)) continue;
         double mean = 0;
@@ -261,17 +273,34 @@ double Booster::shap_bias() const {
 
 // Root-to-leaf path decomposition (extractShapPaths, SHAP.swift:79-114), with
 // each path's repeated features merged into unique slots.
+// Contributions [rows][K][cols + 1]: class k from its own trees and bias.
 std::vector<float> Booster::predict_contrib(const float *x, int64_t rows, int64_t cols) {
+    const int K = std::max(1, trained_num_classes);
+    if (K == 1) return contrib_class(x, rows, cols, 0);
+    const int64_t width = cols + 1;
+    std::vector<float> out((size_t)std::max<int64_t>(rows, 0) * (size_t)K * (size_t)width, 0.0f);
+    for (int k = 0; k < K; ++k) {
+        const std::vector<float> c = contrib_class(x, rows, cols, k);
+        for (int64_t i = 0; i < rows; ++i)
+            std::memcpy(&out[(size_t)((i * K + k) * width)], &c[(size_t)(i * width)],
+                        (size_t)width * sizeof(float));
+    }
+    return out;
+}
+
+// TreeSHAP of the trees of class k (every tree when K = 1): [rows][cols + 1].
+std::vector<float> Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k) {
+    const int K = std::max(1, trained_num_classes);
     const int64_t width = cols + 1;
     std::vector<float> out((size_t)std::max<int64_t>(rows, 0) * (size_t)width, 0.0f);
-    const float bias = (float)shap_bias();
+    const float bias = (float)shap_bias(k);
     if (rows <= 0) return out;
     build_forest();
     std::vector<mbk::ShapPath> paths;
     std::vector<mbk::ShapElem> elems;
     std::vector<mbk::ShapUniq> uniq;
     struct PE { int node, feature; float thr; uint32_t flags; double zf; };
-    for (size_t t = 0; t < trees.size(); ++t) {
+    for (size_t t = (size_t)k; t < trees.size(); t += (size_t)K) {
         const Tree &tr = trees[t];
         if (tr.cover.size() != tr.feature.size() || !(tr.cover[0] > 0)) continue;
         std::vector<std::pair<int, std::vector<PE>>> stack;
@@ -516,7 +545,7 @@ void *macboost_train(const char *params_json, const float *x, int64_t rows, int6
         mb::Trainer *t = mb::trainer_create(p, x, rows, cols, row_major != 0, y, w, x_valid,
                                             valid_rows, y_valid);
         try {
-            mb::trainer_grow(t, p.num_trees);
+            mb::trainer_grow(t, p.num_trees * mb::trainer_classes(t));
             Booster *b = mb::trainer_booster(t);
             mb::trainer_free(t);
             return b;
@@ -713,7 +742,9 @@ int mbk_quantize(mbk_context *ctx, int32_t objective, float alpha, float aux, co
         hipStream_t s = ctx->dev->stream;
         mb::DevBuf<mbk::TreeCtl> ctl(1);
         mb::DevBuf<uint32_t> part(mbk::grad_max_scratch_words());
-        mbk::GradParams gp{objective, alpha, aux, weights ? 1 : 0};
+        if (objective < 0 || objective > 6)
+            mb::invalid("mbk_quantize takes objectives 0..6 (one output per row)");
+        mbk::GradParams gp{objective, alpha, aux, weights ? 1 : 0, 1, 0, rows};
         MB_HIP(mbk::launch_tree_init(s, ctl.ptr));
         MB_HIP(mbk::launch_grad_max(s, gp, preds, labels, weights, rows, ctl.ptr, part.ptr));
         MB_HIP(mbk::launch_quantize(s, gp, preds, labels, weights, rows, ctl.ptr,
@@ -779,7 +810,7 @@ int mbk_predict_forest(mbk_context *ctx, const int32_t *feature, const float *th
                        int32_t num_trees, int32_t nodes_per_tree, const float *x, int64_t rows,
                        int32_t data_bins, float base_score, float *out, char **err) {
     return guarded(err, [&]() -> int {
-        mbk::ForestDev f{feature, threshold, flags, leaf, mask, num_trees, nodes_per_tree};
+        mbk::ForestDev f{feature, threshold, flags, leaf, mask, num_trees, nodes_per_tree, 0, 1, 1};
         MB_HIP(mbk::launch_predict_forest(ctx->dev->stream, f, x, rows, data_bins, base_score, out));
         return 0;
     }, -1);
@@ -933,7 +964,7 @@ void *mbx_dataset_train(const char *params_json, void *ds, const float *w, const
         mb::Trainer *t = mb::trainer_create_binned(p, *static_cast<mb::BinnedDataset *>(ds), w,
                                                    x_valid, valid_rows, y_valid);
         try {
-            mb::trainer_grow(t, p.num_trees);
+            mb::trainer_grow(t, p.num_trees * mb::trainer_classes(t));
             Booster *b = mb::trainer_booster(t);
             mb::trainer_free(t);
             return b;

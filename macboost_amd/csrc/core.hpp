@@ -157,7 +157,8 @@ struct Booster {
     std::vector<float> predict(const float *x_fm, int64_t rows, int64_t cols);
     std::vector<float> predict_contrib(const float *x_fm, int64_t rows, int64_t cols);
     std::vector<float> feature_importance(int type) const;
-    double shap_bias() const;
+    double shap_bias(int k = 0) const;
+    std::vector<float> contrib_class(const float *x_fm, int64_t rows, int64_t cols, int k);
     std::string to_json() const;
     static Booster *from_json(const std::string &text);
 };
@@ -196,6 +197,7 @@ void trainer_level_stats(Trainer *t, int32_t max_levels, int64_t *built, int64_t
 void trainer_setup_seconds(Trainer *t, double *edges_s, double *bin_s);
 Booster *trainer_booster(Trainer *t);
 void trainer_free(Trainer *t);
+int trainer_classes(const Trainer *t);    // trees per boosting round
 
 // Shared helpers.
 void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_t cols,

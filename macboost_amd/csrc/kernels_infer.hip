@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void k_predict_forest(ForestDev f, const float
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     float acc = base;                                  // seeded with the base, trees in order
-    for (int32_t t = 0; t < f.num_trees; ++t) {
+    for (int32_t t = f.tree_first; t < f.num_trees; t += f.tree_step) {
         const int64_t b = (int64_t)t * f.nodes_per_tree;
         int32_t n = 0;
         int32_t feat = f.feature[b];
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void k_predict_forest(ForestDev f, const float
         }
         acc += f.leaf[b + n];
     }
-    out[i] = acc;
+    out[i * f.out_stride] = acc;
 }
 
 hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float *x, int64_t rows,

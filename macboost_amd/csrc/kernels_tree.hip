@@ -114,6 +114,30 @@ __device__ __forceinline__ void row_grad(const GradParams &gp, float f, float y,
     if (gp.has_weights) { g *= w; h *= w; }
 }
 
+// (g, h) of row i, multiclass included: the softmax gradient of class
+// gp.class_index over preds [K][rows] (compute_gradients_multiclass,
+// Shaders.swift:145-170; each exp in double, rounded once).
+__device__ __forceinline__ void row_grad_at(const GradParams &gp, const float *__restrict__ preds,
+                                            const float *__restrict__ labels,
+                                            const float *__restrict__ weights, int64_t i,
+                                            float &g, float &h) {
+    const float w = gp.has_weights ? weights[i] : 1.0f;
+    if (gp.objective != 7) {
+        row_grad(gp, preds[i], labels[i], w, g, h);
+        return;
+    }
+    float m = -INFINITY;
+    for (int k = 0; k < gp.num_classes; ++k) m = fmaxf(m, preds[(int64_t)k * gp.rows + i]);
+    float sum = 0.0f;
+    for (int k = 0; k < gp.num_classes; ++k)
+        sum += exp_via_double(preds[(int64_t)k * gp.rows + i] - m);
+    const float pk = exp_via_double(preds[(int64_t)gp.class_index * gp.rows + i] - m) / sum;
+    const float yk = (int32_t)labels[i] == gp.class_index ? 1.0f : 0.0f;
+    g = pk - yk;
+    h = fmaxf(2.0f * pk * (1.0f - pk), 1e-6f);
+    if (gp.has_weights) { g *= w; h *= w; }
+}
+
 // ---------------------------------------------------------------------------
 // binning: raw f32 -> bin bytes, written to both layouts: the gather layout
 // [rows][T][W] (row r's tile t at (r*T + t)*W) and the feature-major [F][rows]
@@ -464,8 +488,12 @@ __global__ __launch_bounds__(256) void k_grad_max(GradParams gp, const float *__
     }
     // rows not covered by the 16B loads (all of them when !VEC)
     for (int64_t i = (n4 << 2) + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
-         i += stride)
-        grad_max_row(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, mg, mh);
+         i += stride) {
+        float g, h;
+        row_grad_at(gp, preds, labels, weights, i, g, h);
+        mg = max(mg, __float_as_uint(fabsf(g)));
+        mh = max(mh, __float_as_uint(h));
+    }
     mg = wave_max_u32(mg);
     mh = wave_max_u32(mh);
     const int w = threadIdx.x >> 6;
@@ -505,7 +533,8 @@ hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *pre
     int64_t blocks = ((rows >> 2) + 255) / 256;
     if (blocks > GRAD_MAX_BLOCKS) blocks = GRAD_MAX_BLOCKS;
     if (blocks < 1) blocks = 1;
-    const bool vec = ((reinterpret_cast<uintptr_t>(preds) | reinterpret_cast<uintptr_t>(labels) |
+    const bool vec = gp.objective != 7 &&
+                     ((reinterpret_cast<uintptr_t>(preds) | reinterpret_cast<uintptr_t>(labels) |
                        reinterpret_cast<uintptr_t>(weights)) & 15u) == 0;
     if (vec)
         hipLaunchKernelGGL(k_grad_max<true>, dim3((unsigned)blocks), dim3(256), 0, s, gp, preds,
@@ -554,7 +583,7 @@ __global__ __launch_bounds__(256) void k_goss_hist(GradParams gp, const float *_
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
              i += (int64_t)gridDim.x * blockDim.x) {
             float g, h;
-            row_grad(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, g, h);
+            row_grad_at(gp, preds, labels, weights, i, g, h);
             const uint32_t b = (uint32_t)(fabsf(g) / mg * (float)GOSS_BUCKETS);
             atomicAdd(&lb[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
         }
@@ -633,7 +662,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
             amp[k] = 0;
             if (i < rows) {
                 float g, h;
-                row_grad(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, g, h);
+                row_grad_at(gp, preds, labels, weights, i, g, h);
                 const float ag = fabsf(g);
                 float wt = 1.0f;
                 bool keep = ag >= thr;
@@ -706,7 +735,7 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(GradParams gp, SampleP
     const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
     const float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
     float g, h;
-    row_grad(gp, preds[e.row], labels[e.row], gp.has_weights ? weights[e.row] : 1.0f, g, h);
+    row_grad_at(gp, preds, labels, weights, (int64_t)e.row, g, h);
     if (e.ghq) { g = g * sp.weight; h = h * sp.weight; }
     const int qg = (int)rintf(g * gscale);
     const uint32_t qh = (uint32_t)rintf(h * hscale);
@@ -744,7 +773,7 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
     const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
     const float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
     float g, h;
-    row_grad(gp, preds[i], labels[i], gp.has_weights ? weights[i] : 1.0f, g, h);
+    row_grad_at(gp, preds, labels, weights, i, g, h);
     const int qg = (int)rintf(g * gscale);
     const uint32_t qh = (uint32_t)rintf(h * hscale);
     Entry e;

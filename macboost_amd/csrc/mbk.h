@@ -143,6 +143,9 @@ struct GradParams {
     float alpha;
     float aux;
     int32_t has_weights;
+    int32_t num_classes;     // multiclass: K, preds are [K][rows]
+    int32_t class_index;     // multiclass: the class this tree fits
+    int64_t rows;            // multiclass: the class stride of preds
 };
 // partial: grad_max_scratch_words() u32 of device scratch
 hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *preds,
@@ -337,6 +340,9 @@ struct ForestDev {
     const uint32_t *mask;      // 8 words per node or NULL when no node is categorical
     int32_t num_trees;
     int32_t nodes_per_tree;
+    int32_t tree_first = 0;    // walk trees tree_first, +tree_step, ... (one class of K)
+    int32_t tree_step = 1;
+    int32_t out_stride = 1;    // out[i * out_stride]
 };
 hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float *x,
                                  int64_t rows, int32_t data_bins, float base, float *out);

@@ -101,6 +101,10 @@ struct Trainer {
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
+    // multiclass: K trees per round, preds [K][rows]; tree t fits class t % K
+    int K = 1;
+    std::vector<float> base_scores;
+    float *preds_cur = nullptr, *vpreds_cur = nullptr;   // the current tree's class
     // leaf renewal (L1 / quantile objectives)
     bool renewal = false;
     float renewal_q = 0.5f;
@@ -188,7 +192,28 @@ static void validate_labels(const Params &p, const float *y, int64_t n) {   // :
         if (nonneg && v < 0.0f)
             invalid("label at row " + std::to_string(i) + " is " + swift_float(v) + "; " +
                     objective_name(p.objective) + " requires labels >= 0");
+        if (p.objective == OBJ_MULTICLASS) {
+            const float r = std::nearbyint(v);
+            if (r != v || r < 0.0f || (int64_t)r >= p.num_classes)
+                invalid("label at row " + std::to_string(i) + " is " + swift_float(v) +
+                        "; multiclass requires integer labels in 0..<" +
+                        std::to_string(p.num_classes));
+        }
     }
+}
+
+// multiclassLogloss (Booster.swift:1828-1841) over preds [K][n].
+static float multiclass_logloss(const float *pred, const float *y, int64_t n, int K) {
+    double s = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        double m = -INFINITY;
+        for (int k = 0; k < K; ++k) m = std::max(m, (double)pred[(int64_t)k * n + i]);
+        double sum = 0;
+        for (int k = 0; k < K; ++k) sum += std::exp((double)pred[(int64_t)k * n + i] - m);
+        const int c = (int)y[i];
+        s -= (double)pred[(int64_t)c * n + i] - m - std::log(sum);
+    }
+    return (float)(s / (double)n);
 }
 
 void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_t cols,
@@ -365,7 +390,6 @@ static float eval_metric(const Params &p, const float *pred, const float *y, int
 // Checks shared by both entry points (Booster.swift:451-529).
 static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
                             const float *w, const float *xv, int64_t vrows, const float *yv) {
-    if (p.objective == OBJ_MULTICLASS) invalid("multiclass is not supported by this build yet");
     if (!p.init_model.empty()) invalid("init_model (warm start) is not supported by this build yet");
     validate_labels(p, y, rows);
     if (w)
@@ -466,28 +490,49 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     const int tile_w = t.sh.tile_w;
     t.gp.has_weights = w ? 1 : 0;
     // --- persistent buffers ---------------------------------------------
+    t.K = p.objective == OBJ_MULTICLASS ? p.num_classes : 1;
+    const int K = t.K;
+    t.gp.num_classes = K;
+    t.gp.class_index = 0;
+    t.gp.rows = rows;
     t.labels_h.assign(y, y + rows);
     t.labels.alloc((size_t)rows);
-    t.preds.alloc((size_t)rows);
+    t.preds.alloc((size_t)rows * (size_t)K);
     MB_HIP(hipMemcpyAsync(t.labels.ptr, y, (size_t)rows * 4, hipMemcpyHostToDevice, s));
     if (w) {
         t.has_weights = true;
         t.weights.alloc((size_t)rows);
         MB_HIP(hipMemcpyAsync(t.weights.ptr, w, (size_t)rows * 4, hipMemcpyHostToDevice, s));
     }
-    t.base = base_score(p, y, w, rows);
-    {
-        uint32_t bits;
-        std::memcpy(&bits, &t.base, 4);
-        MB_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(t.preds.ptr), (int)bits,
-                                 (size_t)rows, s));
-        if (t.has_valid) {
-            t.vlabels_h.assign(yv, yv + vrows);
-            t.vpreds.alloc((size_t)vrows);
-            MB_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(t.vpreds.ptr), (int)bits,
-                                     (size_t)vrows, s));
-        }
+    if (K > 1) {
+        // per-class log priors with +1 smoothing (Booster.swift:838-846)
+        std::vector<double> cnt((size_t)K, 1.0);
+        for (int64_t i = 0; i < rows; ++i) cnt[(size_t)y[i]] += w ? (double)w[i] : 1.0;
+        double total = 0;
+        for (double c : cnt) total += c;
+        t.base_scores.resize((size_t)K);
+        for (int k = 0; k < K; ++k) t.base_scores[(size_t)k] = (float)std::log(cnt[(size_t)k] / total);
+        t.base = 0.0f;
+    } else {
+        t.base = base_score(p, y, w, rows);
+        t.base_scores = {t.base};
     }
+    if (t.has_valid) {
+        t.vlabels_h.assign(yv, yv + vrows);
+        t.vpreds.alloc((size_t)vrows * (size_t)K);
+    }
+    for (int k = 0; k < K; ++k) {
+        uint32_t bits;
+        std::memcpy(&bits, &t.base_scores[(size_t)k], 4);
+        MB_HIP(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(t.preds.ptr + (size_t)k * rows),
+                                 (int)bits, (size_t)rows, s));
+        if (t.has_valid)
+            MB_HIP(hipMemsetD32Async(
+                reinterpret_cast<hipDeviceptr_t>(t.vpreds.ptr + (size_t)k * vrows), (int)bits,
+                (size_t)vrows, s));
+    }
+    t.preds_cur = t.preds.ptr;
+    t.vpreds_cur = t.has_valid ? t.vpreds.ptr : nullptr;
     t.mono.alloc((size_t)cols);
     MB_HIP(hipMemcpyAsync(t.mono.ptr, t.mono_h.data(), (size_t)cols, hipMemcpyHostToDevice, s));
     t.feat_mask.alloc((size_t)cols);
@@ -713,7 +758,7 @@ static const uint8_t *tree_feature_mask(Trainer &t, int tree) {
 // change of each leaf is recorded for preds that already hold the old values.
 static void renew_tree(Trainer &t, const mbk::TreeOut &out, float *delta) {
     MB_HIP(mbk::launch_renew(t.dev->stream, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
-                             t.labels.ptr, t.preds.ptr, t.bounds.ptr, t.renewal_q,
+                             t.labels.ptr, t.preds_cur, t.bounds.ptr, t.renewal_q,
                              t.p.learning_rate, t.rn_leaf.ptr, t.rn_keys.ptr, t.rn_seg.ptr,
                              t.rn_cnt.ptr, t.rn_off.ptr, t.rn_cursor.ptr, delta));
 }
@@ -807,14 +852,14 @@ static void grow_levelwise(Trainer &t, int tree) {
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, false));
             MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
-                                          t.renewal ? nullptr : t.preds.ptr, t.count.ptr));
+                                          t.renewal ? nullptr : t.preds_cur, t.count.ptr));
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
             if (t.renewal) {
                 // residuals before the tree (routing applies nothing), then
                 // one walk with the renewed leaves (Booster.swift:1596-1630)
                 renew_tree(t, out, nullptr);
                 MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
-                                                  t.preds.ptr));
+                                                  t.preds_cur));
             }
             break;
         }
@@ -832,7 +877,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                                             t.bounds.ptr, ctl, out, true));
             if (t.renewal) renew_tree(t, out, nullptr);
             MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
-                                              t.preds.ptr));
+                                              t.preds_cur));
             break;
         }
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
@@ -855,7 +900,7 @@ static void grow_levelwise(Trainer &t, int tree) {
     }
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
-                                          t.vpreds.ptr));
+                                          t.vpreds_cur));
     MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
                           hipMemcpyDeviceToDevice, s));
 }
@@ -909,10 +954,10 @@ static void grow_leafwise(Trainer &t, int tree) {
     }
     // training predictions: walk the finished tree on the binned rows
     // (predict_tree_binned, Shaders.swift:1763-1781)
-    MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds.ptr));
+    MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds_cur));
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
-                                          t.vpreds.ptr));
+                                          t.vpreds_cur));
     if (t.renewal) {
         // residuals after the tree's first leaf values, then each leaf's
         // change is added (Booster.swift:1253-1290)
@@ -921,10 +966,10 @@ static void grow_leafwise(Trainer &t, int tree) {
         mbk::TreeOut dout = out;
         dout.leaf = t.rn_delta.ptr;
         MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, dout,
-                                          t.preds.ptr));
+                                          t.preds_cur));
         if (t.has_valid)
             MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, dout,
-                                              t.vpreds.ptr));
+                                              t.vpreds_cur));
     }
     MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
                           hipMemcpyDeviceToDevice, s));
@@ -937,30 +982,41 @@ void trainer_grow(Trainer *tp, int num_trees) {
     const int first_tree = t.grown;
     const bool metric_each_tree = t.has_valid;
     std::vector<float> vp;
+    const int K = t.K;
+    auto metric = [&](const float *pred, const float *y, int64_t n) {
+        return K > 1 ? multiclass_logloss(pred, y, n, K) : eval_metric(t.p, pred, y, n);
+    };
     for (int k = 0; k < num_trees && !t.stopped; ++k) {
         const int tree = t.grown;
+        // tree t fits class t % K (Booster.swift:1315)
+        const int cls = tree % K;
+        t.gp.class_index = cls;
+        t.preds_cur = t.preds.ptr + (size_t)cls * (size_t)t.rows;
+        t.vpreds_cur = t.has_valid ? t.vpreds.ptr + (size_t)cls * (size_t)t.vrows : nullptr;
         if (t.leafwise) grow_leafwise(t, tree);
         else grow_levelwise(t, tree);
         t.grown += 1;
-        const int round = t.grown;
+        // metrics once per round of K trees (Booster.swift:1650-1688)
+        if (t.grown % K != 0) continue;
+        const int round = t.grown / K;
         const bool is_last = k + 1 == num_trees;
         const bool log_now = t.p.eval_every > 0 && (round % t.p.eval_every == 0 || is_last);
         if (!metric_each_tree && !log_now) continue;
         MB_HIP(hipStreamSynchronize(s));
         std::string line;
         if (log_now) {
-            std::vector<float> tp_h((size_t)t.rows);
-            MB_HIP(hipMemcpy(tp_h.data(), t.preds.ptr, (size_t)t.rows * 4, hipMemcpyDeviceToHost));
+            std::vector<float> tp_h((size_t)t.rows * (size_t)K);
+            MB_HIP(hipMemcpy(tp_h.data(), t.preds.ptr, tp_h.size() * 4, hipMemcpyDeviceToHost));
             char buf[128];
             std::snprintf(buf, sizeof buf, "[%4d] train-%s: %.5f", round,
                           effective_metric(t.p).c_str(),
-                          eval_metric(t.p, tp_h.data(), t.labels_h.data(), t.rows));
+                          metric(tp_h.data(), t.labels_h.data(), t.rows));
             line = buf;
         }
         if (t.has_valid) {
-            vp.resize((size_t)t.vrows);
-            MB_HIP(hipMemcpy(vp.data(), t.vpreds.ptr, (size_t)t.vrows * 4, hipMemcpyDeviceToHost));
-            const float vm = eval_metric(t.p, vp.data(), t.vlabels_h.data(), t.vrows);
+            vp.resize((size_t)t.vrows * (size_t)K);
+            MB_HIP(hipMemcpy(vp.data(), t.vpreds.ptr, vp.size() * 4, hipMemcpyDeviceToHost));
+            const float vm = metric(vp.data(), t.vlabels_h.data(), t.vrows);
             t.eval_history.push_back(vm);
             const bool higher = effective_metric(t.p) == "auc";
             if (higher ? vm > t.best_metric : vm < t.best_metric) {
@@ -1085,15 +1141,15 @@ Booster *trainer_booster(Trainer *tp) {
     b->trained_num_bins = t.nb;
     b->trained_categorical = t.p.categorical;
     b->base_score = t.base;
-    b->base_scores = {t.base};
-    b->trained_num_classes = 1;
+    b->base_scores = t.base_scores;
+    b->trained_num_classes = t.K;
     b->warnings = t.warnings;
     b->eval_history = t.eval_history;
     const int data_bins = t.nb - 1;
     int keep = n;
     if (t.has_valid) {
         b->best_iteration = t.best_iter;
-        if (t.p.early_stopping_rounds > 0 && keep > t.best_iter) keep = t.best_iter;
+        if (t.p.early_stopping_rounds > 0 && keep > t.best_iter * t.K) keep = t.best_iter * t.K;
     }
     b->trees.reserve((size_t)keep);
     for (int k = 0; k < keep; ++k) {
@@ -1135,5 +1191,7 @@ Booster *trainer_booster(Trainer *tp) {
 }
 
 void trainer_free(Trainer *t) { delete t; }
+
+int trainer_classes(const Trainer *t) { return t->K; }
 
 }  // namespace mb

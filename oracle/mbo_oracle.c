@@ -237,6 +237,39 @@ void orc_gradients(const float *preds, const float *y, const float *w, int64_t r
     *max_h = bitsf(mh);
 }
 
+void orc_gradients_mc(const float *preds, const float *y, const float *w, int64_t rows,
+                      int32_t K, int32_t cls, float *g_out, float *h_out, float *max_g,
+                      float *max_h) {
+    uint32_t mg = 0, mh = 0;
+    for (int64_t i = 0; i < rows; ++i) {
+        float m = -INFINITY;
+        for (int32_t k = 0; k < K; ++k) m = fmaxf(m, preds[(int64_t)k * rows + i]);
+        float sum = 0.0f;
+        for (int32_t k = 0; k < K; ++k) sum += exp_via_double(preds[(int64_t)k * rows + i] - m);
+        float pk = exp_via_double(preds[(int64_t)cls * rows + i] - m) / sum;
+        float yk = (int32_t)y[i] == cls ? 1.0f : 0.0f;
+        float g = pk - yk;
+        float h = fmaxf(2.0f * pk * (1.0f - pk), 1e-6f);
+        if (w) { g *= w[i]; h *= w[i]; }
+        g_out[i] = g; h_out[i] = h;
+        uint32_t ag = fbits(fabsf(g)), hh = fbits(h);
+        if (ag > mg) mg = ag;
+        if (hh > mh) mh = hh;
+    }
+    *max_g = bitsf(mg);
+    *max_h = bitsf(mh);
+}
+
+void orc_base_scores_mc(const float *y, const float *w, int64_t rows, int32_t K, float *out) {
+    double *cnt = (double *)malloc(sizeof(double) * (size_t)K);
+    for (int32_t k = 0; k < K; ++k) cnt[k] = 1.0;                 /* +1 smoothing */
+    for (int64_t i = 0; i < rows; ++i) cnt[(int32_t)y[i]] += w ? (double)w[i] : 1.0;
+    double total = 0;
+    for (int32_t k = 0; k < K; ++k) total += cnt[k];
+    for (int32_t k = 0; k < K; ++k) out[k] = (float)log(cnt[k] / total);
+    free(cnt);
+}
+
 void orc_quantize(const float *g, const float *h, int64_t rows, float mg, float mh,
                   uint32_t *ghq) {
     float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
@@ -951,10 +984,14 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
     }
     for (int32_t f = 0; f < cols; ++f)
         for (int64_t i = 0; i < rows; ++i) rm[i * cols + f] = bins_fm[(int64_t)f * rows + i];
-    if (!split_bin) out->split_bin = (uint32_t *)calloc((size_t)p->num_trees * total, 4);
+    if (!split_bin) out->split_bin = (uint32_t *)calloc((size_t)out->num_trees * total, 4);
     int rc = 0;
-    for (int32_t t = 0; t < p->num_trees && rc == 0; ++t) {
+    const int32_t K = p->num_classes > 1 ? p->num_classes : 1;
+    if (out->num_trees < p->num_trees * K) rc = -2;
+    for (int32_t t = 0; t < p->num_trees * K && rc == 0; ++t) {
         int64_t base = (int64_t)t * total;
+        const int32_t cls = t % K;
+        float *pc = preds + (int64_t)cls * rows;     /* this tree's class */
         for (int32_t n = 0; n < total; ++n) {
             out->feature[base + n] = -1; out->threshold[base + n] = 0; out->leaf[base + n] = 0;
             out->flags[base + n] = 0; out->gain[base + n] = 0; out->cover[base + n] = 0;
@@ -962,7 +999,8 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
             if (out->cat_mask) memset(out->cat_mask + (base + n) * 8, 0, 32);
         }
         float mg, mh;
-        orc_gradients(preds, y, w, rows, p->objective, p->alpha, p->aux, g, h, &mg, &mh);
+        if (K > 1) orc_gradients_mc(preds, y, w, rows, K, cls, g, h, &mg, &mh);
+        else orc_gradients(preds, y, w, rows, p->objective, p->alpha, p->aux, g, h, &mg, &mh);
         const uint32_t *rows_in = NULL;
         int64_t n_in = rows;
         if (orc_sampling_active(p, t)) {
@@ -987,25 +1025,25 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
         c.apply_preds = rows_in == NULL && !renewal;
         c.node_lo = renewal ? node_lo : NULL;
         c.node_hi = renewal ? node_hi : NULL;
-        rc = p->num_leaves > 0 ? grow_leafwise(&c, preds, out, base, NULL)
-                               : grow_levelwise(&c, preds, out, base, NULL);
+        rc = p->num_leaves > 0 ? grow_leafwise(&c, pc, out, base, NULL)
+                               : grow_levelwise(&c, pc, out, base, NULL);
         if (rc == 0 && renewal) {
             const float q = p->objective == ORC_OBJ_MAE ? 0.5f : p->alpha;
             if (p->num_leaves > 0) {
                 /* leaf-wise: residuals after the tree's first leaf values,
                  * then the changes are added (Booster.swift:1253-1290) */
-                renew_leaves(&c, out, base, y, preds, q, delta);
-                for (int64_t i = 0; i < rows; ++i) preds[i] += delta[leaf_of_row(&c, out, base, i)];
+                renew_leaves(&c, out, base, y, pc, q, delta);
+                for (int64_t i = 0; i < rows; ++i) pc[i] += delta[leaf_of_row(&c, out, base, i)];
             } else {
                 /* level-wise: residuals before the tree (route apply = 0),
                  * then one walk with the renewed leaves (:1596-1630) */
-                renew_leaves(&c, out, base, y, preds, q, NULL);
-                walk_preds(&c, out, base, preds);
+                renew_leaves(&c, out, base, y, pc, q, NULL);
+                walk_preds(&c, out, base, pc);
             }
         } else if (rc == 0 && rows_in && p->num_leaves <= 0) {
             /* sampled level-wise trees: every row's prediction from one walk
              * (Booster.swift:1568-1580); leaf-wise growth always walks */
-            walk_preds(&c, out, base, preds);
+            walk_preds(&c, out, base, pc);
         }
         /* reachable nodes only (Booster.swift:918-945) */
         {

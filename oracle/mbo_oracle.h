@@ -45,6 +45,7 @@ typedef struct {
     float goss_top_rate;
     float goss_other_rate;
     float subsample;           /* bagging fraction, 1 = off */
+    int32_t num_classes;       /* multiclass K (3..128), else 1 */
 } orc_params;
 
 /* One split candidate result: SplitResult (Shaders.swift:334) plus the exact
@@ -96,6 +97,14 @@ float orc_label_quantile(const float *y, int64_t rows, float q);
 void orc_gradients(const float *preds, const float *y, const float *w, int64_t rows,
                    int32_t objective, float alpha, float aux, float *g, float *h,
                    float *max_g, float *max_h);
+/* Softmax gradients of class c over preds [K][rows] (compute_gradients_multiclass,
+ * Shaders.swift:145-170), and the per-class base scores log((1 + w_k) / total)
+ * (Booster.swift:841-846). */
+void orc_gradients_mc(const float *preds, const float *y, const float *w, int64_t rows,
+                      int32_t num_classes, int32_t cls, float *g, float *h, float *max_g,
+                      float *max_h);
+void orc_base_scores_mc(const float *y, const float *w, int64_t rows, int32_t num_classes,
+                        float *out);
 void orc_quantize(const float *g, const float *h, int64_t rows, float max_g,
                   float max_h, uint32_t *ghq);
 
@@ -120,6 +129,9 @@ int orc_sampling_active(const orc_params *p, int32_t tree);
 int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, int64_t rows,
                         float max_g, uint8_t *kept, float *wmax_g, float *wmax_h);
 
+/* Multiclass: K trees per round (tree t fits class t % K, its gradients from
+ * the preds every earlier tree has updated), preds [K][rows], the forest
+ * holds num_trees * K trees. */
 int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t cols,
             const float *y, const float *w, const uint8_t *is_cat, const int8_t *monotone,
             const float *edges, float base_score, float *preds, orc_forest *out);

@@ -18,7 +18,7 @@ LIB_PATH = ROOT / "oracle" / "liboracle.so"
 
 FLAG_DEFAULT_LEFT = 1
 FLAG_CATEGORICAL = 2
-OBJ_L2, OBJ_LOGISTIC, OBJ_MAE, OBJ_HUBER, OBJ_QUANTILE, OBJ_POISSON, OBJ_TWEEDIE = range(7)
+OBJ_L2, OBJ_LOGISTIC, OBJ_MAE, OBJ_HUBER, OBJ_QUANTILE, OBJ_POISSON, OBJ_TWEEDIE, OBJ_MULTICLASS = range(8)
 
 _lib = None
 
@@ -47,6 +47,7 @@ class OrcParams(ctypes.Structure):
         ("alpha", ctypes.c_float), ("aux", ctypes.c_float),
         ("goss", ctypes.c_int32), ("goss_top_rate", ctypes.c_float),
         ("goss_other_rate", ctypes.c_float), ("subsample", ctypes.c_float),
+        ("num_classes", ctypes.c_int32),
     ]
 
 
@@ -84,6 +85,10 @@ def _configure(l: ctypes.CDLL) -> None:
     l.orc_base_score.argtypes = [_P, _P, _I64, _I32, _F]
     l.orc_label_quantile.restype = _F
     l.orc_label_quantile.argtypes = [_P, _I64, _F]
+    l.orc_gradients_mc.restype = None
+    l.orc_gradients_mc.argtypes = [_P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _P]
+    l.orc_base_scores_mc.restype = None
+    l.orc_base_scores_mc.argtypes = [_P, _P, _I64, _I32, _P]
     l.orc_gradients.argtypes = [_P, _P, _P, _I64, _I32, _F, _F, _P, _P, _P, _P]
     l.orc_quantize.argtypes = [_P, _P, _I64, _F, _F, _P]
     l.orc_hist_node.argtypes = [_P, _I64, _I32, _I32, _P, _P, _I64, _P, _P]
@@ -268,26 +273,57 @@ class OracleModel:
     forest: Forest
     base_score: float
     num_bins: int
-    preds: np.ndarray
+    preds: np.ndarray             # [rows], or [K, rows] for multiclass
     edges: np.ndarray
+    base_scores: list = None      # per class (multiclass)
+    num_classes: int = 1
+
+
+def base_scores_mc(y, w, num_classes):
+    y = np.ascontiguousarray(y, np.float32)
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    out = np.empty(num_classes, np.float32)
+    lib().orc_base_scores_mc(_ptr(y), _ptr(w), len(y), num_classes, _ptr(out))
+    return out
+
+
+def gradients_mc(preds_kr, y, num_classes, cls, w=None):
+    preds_kr = np.ascontiguousarray(preds_kr, np.float32)
+    rows = preds_kr.shape[1]
+    y = np.ascontiguousarray(y, np.float32)
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    g = np.empty(rows, np.float32)
+    h = np.empty(rows, np.float32)
+    mg = np.zeros(1, np.float32)
+    mh = np.zeros(1, np.float32)
+    lib().orc_gradients_mc(_ptr(preds_kr), _ptr(y), _ptr(w), rows, num_classes, cls, _ptr(g),
+                           _ptr(h), _ptr(mg), _ptr(mh))
+    return g, h, float(mg[0]), float(mh[0])
 
 
 def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objective=OBJ_L2,
         num_leaves=0, learning_rate=0.1, lam=1.0, min_child_hess=1.0, min_split_gain=0.0,
         cat_smooth=10.0, alpha=0.9, aux=1.0, w=None, is_cat=None, monotone=None,
         base=None, goss=False, goss_top_rate=0.2, goss_other_rate=0.1,
-        subsample=1.0) -> OracleModel:
+        subsample=1.0, num_classes=1) -> OracleModel:
     cols, rows = bins_fm.shape
+    K = num_classes if objective == OBJ_MULTICLASS else 1
     p = OrcParams(num_trees, max_depth, num_bins, objective, num_leaves, learning_rate, lam,
                   min_child_hess, min_split_gain, cat_smooth, alpha, aux, int(goss),
-                  goss_top_rate, goss_other_rate, subsample)
+                  goss_top_rate, goss_other_rate, subsample, K)
     y = np.ascontiguousarray(y, np.float32)
     w = None if w is None else np.ascontiguousarray(w, np.float32)
-    if base is None:
-        base = base_score(y, w, objective, aux if objective == OBJ_LOGISTIC else 1.0, alpha)
-    preds = np.full(rows, base, np.float32)
+    bases = None
+    if K > 1:
+        bases = base_scores_mc(y, w, K)
+        base = 0.0
+        preds = np.ascontiguousarray(np.repeat(bases[:, None], rows, axis=1))
+    else:
+        if base is None:
+            base = base_score(y, w, objective, aux if objective == OBJ_LOGISTIC else 1.0, alpha)
+        preds = np.full(rows, base, np.float32)
     nodes = (1 << (max_depth + 1)) - 1
-    forest = Forest.empty(num_trees, nodes)
+    forest = Forest.empty(num_trees * K, nodes)
     cat = None if is_cat is None else np.ascontiguousarray(is_cat, np.uint8)
     mono = None if monotone is None else np.ascontiguousarray(monotone, np.int8)
     edges = np.ascontiguousarray(edges, np.float32)
@@ -297,7 +333,31 @@ def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objectiv
                        _ptr(preds), ctypes.byref(fc))
     if rc != 0:
         raise RuntimeError(f"orc_fit failed: {rc}")
-    return OracleModel(forest, float(base), num_bins, preds, edges)
+    return OracleModel(forest, float(base), num_bins, preds, edges,
+                       None if bases is None else [float(b) for b in bases], K)
+
+
+def class_forest(forest: Forest, k: int, num_classes: int) -> Forest:
+    """The trees of class k (tree t fits class t % K), in order."""
+    def sel(a):
+        return None if a is None else np.ascontiguousarray(a[k::num_classes])
+    return Forest(sel(forest.feature), sel(forest.threshold), sel(forest.leaf), sel(forest.flags),
+                  sel(forest.cat_mask), sel(forest.gain), sel(forest.cover), sel(forest.split_bin))
+
+
+def predict_mc(forest: Forest, base_scores, num_bins: int, x_fm) -> np.ndarray:
+    """Multiclass raw scores [rows, K]: class k sums its own trees in order
+    from its base score (predict_forest, Shaders.swift:1548-1578)."""
+    K = len(base_scores)
+    return np.stack([predict(class_forest(forest, k, K), base_scores[k], num_bins, x_fm)
+                     for k in range(K)], axis=1)
+
+
+def treeshap_mc(forest: Forest, base_scores, num_bins: int, x_fm) -> np.ndarray:
+    """Multiclass contributions [rows, K * (cols + 1)], one block per class."""
+    K = len(base_scores)
+    return np.concatenate([treeshap(class_forest(forest, k, K), base_scores[k], num_bins, x_fm)
+                           for k in range(K)], axis=1)
 
 
 def predict(forest: Forest, base: float, num_bins: int, x_fm) -> np.ndarray:

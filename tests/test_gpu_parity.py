@@ -42,7 +42,9 @@ def oracle_fit(x_fm, y, params, is_cat=None):
     nb = p.pop("num_bins", 256)
     obj = p.pop("objective", "regression")
     kw["objective"] = {"regression": O.OBJ_L2, "binary": O.OBJ_LOGISTIC, "mae": O.OBJ_MAE,
-                       "quantile": O.OBJ_QUANTILE}[obj]
+                       "quantile": O.OBJ_QUANTILE, "multiclass": O.OBJ_MULTICLASS}[obj]
+    if "num_class" in p:
+        kw["num_classes"] = p.pop("num_class")
     if "alpha" in p:
         kw["alpha"] = p.pop("alpha")
     mono = p.pop("monotone_constraints", None)
@@ -470,6 +472,117 @@ def test_leaf_renewal_nan_categorical_identical():
     is_cat = [0] * 80 + [1] * 20
     check_identical(x, y, {"num_trees": 10, "max_depth": 6, "objective": "mae",
                            "categorical_features": cats}, is_cat=is_cat)
+
+
+# --------------------------------------------------------------------------
+# multiclass (softmax, K trees per round)
+# --------------------------------------------------------------------------
+
+def _quadrant_classes(rows, seed, cols=5):
+    rng = np.random.default_rng(seed)
+    x = rng.uniform(0, 1, size=(cols, rows)).astype(np.float32)
+    a = (x[0] + 0.15 * rng.standard_normal(rows) > 0.5).astype(int)
+    b = (x[1] + 0.15 * rng.standard_normal(rows) > 0.5).astype(int) * 2
+    return x, (a + b).astype(np.float32)
+
+
+def check_identical_mc(x_fm, y, params, is_cat=None, x_test=None):
+    K = params["num_class"]
+    h, obj = gpu_fit(x_fm, y, params)
+    ref = oracle_fit(x_fm, y, params, is_cat)
+    assert mb.num_classes(h) == K and obj["numClasses"] == K
+    assert np.array_equal(np.array(obj["baseScores"], np.float32),
+                          np.array(ref.base_scores, np.float32))
+    got = model_io.forest_from_json(obj, ref.forest.nodes_per_tree)
+    has_cats = is_cat is not None and any(is_cat)
+    model_io.assert_same_forest(got, ref.forest, with_cats=has_cats)
+    # running train preds [K][rows] == the forest walk, bit for bit
+    assert np.array_equal(mb.predict(h, x_fm, feature_major=True), ref.preds.T)
+    if x_test is not None:
+        gp = mb.predict(h, x_test, feature_major=True)
+        assert gp.shape == (x_test.shape[1], K)
+        assert np.array_equal(gp, O.predict_mc(ref.forest, ref.base_scores, ref.num_bins, x_test))
+    return h, ref
+
+
+@pytest.mark.parametrize("params", [
+    {"num_trees": 15, "max_depth": 5, "objective": "multiclass", "num_class": 4},
+    {"num_trees": 10, "max_depth": 6, "objective": "multiclass", "num_class": 3,
+     "learning_rate": 0.3, "lambda": 2.0},
+    {"num_trees": 10, "max_depth": 7, "num_leaves": 15, "objective": "multiclass",
+     "num_class": 4},
+    {"num_trees": 10, "max_depth": 5, "objective": "multiclass", "num_class": 4,
+     "subsample": 0.7},
+])
+def test_multiclass_identical_trees(params):
+    # ObjectiveTests.swift:519-557; LeafWiseTests.swift:105-125
+    x, y = _quadrant_classes(20_000, 121)
+    if params["num_class"] == 3:
+        y = np.minimum(2, (x[0] * 3).astype(int)).astype(np.float32)
+    xt, _ = _quadrant_classes(4000, 122)
+    h, ref = check_identical_mc(x, y, params, x_test=xt)
+    assert mb.num_trees(h) == params["num_trees"] * params["num_class"]
+
+
+def test_multiclass_nan_categorical_identical_trees():
+    rows = 20_000
+    x, y = _quadrant_classes(rows, 7)
+    x[3, ::9] = np.nan
+    x[4] = np.floor(x[4] * 12)
+    y = np.where(x[4] == 5, 3, y).astype(np.float32)
+    check_identical_mc(x, y, {"num_trees": 8, "max_depth": 6, "objective": "multiclass",
+                              "num_class": 4, "categorical_features": [4]},
+                       is_cat=[0, 0, 0, 0, 1], x_test=x[:, :3000].copy())
+
+
+def test_multiclass_shap_and_save_load(tmp_path):
+    # ObjectiveTests.swift:480-513: per-class blocks sum to the class score;
+    # GPU contributions equal the oracle's per class; save/load is bitwise
+    rows, cols, K = 800, 4, 3
+    rng = np.random.default_rng(131)
+    x = rng.uniform(0, 1, size=(cols, rows)).astype(np.float32)
+    y = np.minimum(2, (x[0] * 3).astype(int)).astype(np.float32)
+    params = {"num_trees": 25, "max_depth": 4, "objective": "multiclass", "num_class": K}
+    h = mb.train(params, x, y, feature_major=True)
+    ref = oracle_fit(x, y, params)
+    c = mb.predict_contrib(h, x, feature_major=True).reshape(rows, K, cols + 1)
+    raw = mb.predict(h, x, feature_major=True)
+    assert np.abs(c.sum(axis=2) - raw).max() < 1e-4
+    want = O.treeshap_mc(ref.forest, ref.base_scores, ref.num_bins, x).reshape(rows, K, cols + 1)
+    assert np.allclose(c, want, rtol=1e-5, atol=1e-6)
+    mb.save(h, tmp_path / "mc.json")
+    h2 = mb.load(tmp_path / "mc.json")
+    assert np.array_equal(mb.predict(h2, x, feature_major=True), raw)
+
+
+def test_multiclass_early_stopping_keeps_whole_rounds():
+    # Booster.swift:1650-1696: multi_logloss once per round of K trees; the
+    # best round's K * best trees are kept
+    K = 4
+    x, y = _quadrant_classes(6000, 31)
+    xv, yv = _quadrant_classes(3000, 32)
+    params = {"num_trees": 300, "max_depth": 4, "learning_rate": 0.5, "objective": "multiclass",
+              "num_class": K}
+    h = mb.train(dict(params, early_stopping_rounds=4), x, y, eval_set=(xv.T, yv),
+                 feature_major=True)
+    best = mb.best_iteration(h)
+    assert 1 <= best < 296 and mb.num_trees(h) == best * K
+    ref = oracle_fit(x, y, dict(params, num_trees=best + 4))
+
+    def mlogloss(p):
+        z = p.astype(np.float64)
+        m = z.max(axis=1)
+        lse = np.log(np.exp(z - m[:, None]).sum(axis=1)) + m
+        return float(np.mean(lse - z[np.arange(len(yv)), yv.astype(int)]))
+
+    losses = np.array([mlogloss(O.predict_mc(_first_trees(ref.forest, r * K), ref.base_scores,
+                                             ref.num_bins, xv)) for r in range(1, best + 5)],
+                      np.float32)
+    assert int(np.argmin(losses)) + 1 == best or np.isclose(losses.min(), losses[best - 1],
+                                                             rtol=1e-6)
+    assert (losses[best:] >= losses[best - 1] * (1 - 1e-6)).all()    # the 4 stale rounds
+    got = model_io.forest_from_json(model_io.saved_model(h), ref.forest.nodes_per_tree)
+    model_io.assert_same_forest(got, _first_trees(ref.forest, best * K), with_cats=False)
 
 
 # --------------------------------------------------------------------------

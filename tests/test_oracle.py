@@ -725,3 +725,115 @@ def test_leafwise_quantile_coverage(oracle):
                 alpha=0.9)
     cov = float(np.mean(y <= predict(m, x)))
     assert abs(cov - 0.9) < 0.05, cov
+
+
+# --------------------------------------------------------------------------
+# multiclass (softmax, K trees per round)
+# --------------------------------------------------------------------------
+
+def test_multiclass_gradients_are_softmax(oracle):
+    # compute_gradients_multiclass (Shaders.swift:145-170): g = p_c - [y == c],
+    # h = max(2 p_c (1 - p_c), 1e-6), against a float64 softmax
+    rng = np.random.default_rng(3)
+    K, rows = 5, 4000
+    preds = (rng.standard_normal((K, rows)) * 3).astype(np.float32)
+    y = rng.integers(0, K, rows).astype(np.float32)
+    w = rng.uniform(0.5, 2, rows).astype(np.float32)
+    z = preds.astype(np.float64)
+    p = np.exp(z - z.max(axis=0)) / np.exp(z - z.max(axis=0)).sum(axis=0)
+    gsum = np.zeros(rows)
+    for c in range(K):
+        g, h, mg, mh = O.gradients_mc(preds, y, K, c, w)
+        want_g = (p[c] - (y == c)) * w
+        want_h = np.maximum(2 * p[c] * (1 - p[c]), 1e-6) * w
+        assert np.allclose(g, want_g, rtol=1e-5, atol=1e-6)
+        assert np.allclose(h, want_h, rtol=1e-5, atol=1e-6)
+        assert mg == np.abs(g).max() and mh == h.max()
+        gsum += g / w
+    assert np.abs(gsum).max() < 1e-5                      # sum_c (p_c - y_c) = 0
+
+
+def test_multiclass_base_scores(oracle):
+    # Booster.swift:841-846: log((1 + sum of weights of class k) / total)
+    y = np.array([0, 1, 1, 2, 2, 2, 2], np.float32)
+    w = np.array([1, 2, 1, 1, 1, 1, 0.5], np.float32)
+    got = O.base_scores_mc(y, None, 4)
+    cnt = np.array([2, 3, 5, 1], np.float64)
+    assert np.array_equal(got, np.log(cnt / cnt.sum()).astype(np.float32))
+    got = O.base_scores_mc(y, w, 3)
+    cnt = np.array([2, 4, 4.5], np.float64)
+    assert np.array_equal(got, np.log(cnt / cnt.sum()).astype(np.float32))
+
+
+def _quadrant_classes(rows, seed):
+    rng = O.SplitMix(seed)
+    x = np.array([rng.uniform() for _ in range(rows * 5)], np.float32).reshape(5, rows)
+    a = np.array([1 if x[0, i] + np.float32(0.15) * np.float32(rng.normal()) > 0.5 else 0
+                  for i in range(rows)])
+    b = np.array([2 if x[1, i] + np.float32(0.15) * np.float32(rng.normal()) > 0.5 else 0
+                  for i in range(rows)])
+    return x, (a + b).astype(np.float32)
+
+
+def test_multiclass_accuracy_and_tree_count(oracle):
+    # ObjectiveTests.swift:519-547: K trees per round, accuracy near the
+    # ~0.775 Bayes ceiling
+    rows, K = 20_000, 4
+    x, y = _quadrant_classes(rows, 121)
+    m = fit_raw(x, y, num_trees=60, max_depth=5, objective=O.OBJ_MULTICLASS, num_classes=K)
+    assert m.forest.num_trees == 60 * K
+    raw = O.predict_mc(m.forest, m.base_scores, m.num_bins, x)
+    assert raw.shape == (rows, K)
+    assert np.mean(raw.argmax(axis=1) == y) > 0.74
+    assert np.array_equal(raw.T, m.preds)                 # running preds == forest walk
+
+
+def test_multiclass_trees_see_the_earlier_classes_updates(oracle):
+    # Within a round, tree t (class t % K) takes its gradients from preds that
+    # the round's earlier trees already updated (one command buffer per round
+    # runs them in order, Booster.swift:1315-1365).  Depth-1 trees: class 1's
+    # leaves equal lr * -G / (H + lambda) over the quantised softmax gradients
+    # computed after tree 0.
+    rows, K, lr, lam = 3000, 3, 0.5, 1.0
+    rng = np.random.default_rng(4)
+    x = rng.uniform(0, 1, size=(2, rows)).astype(np.float32)
+    y = np.minimum(2, (x[0] * 3).astype(int)).astype(np.float32)
+    m = fit_raw(x, y, num_trees=1, max_depth=1, objective=O.OBJ_MULTICLASS, num_classes=K,
+                learning_rate=lr, lam=lam)
+    bases = np.array(m.base_scores, np.float32)
+    preds = np.repeat(bases[:, None], rows, axis=1).astype(np.float32)
+    preds[0] = O.predict(O.class_forest(m.forest, 0, K), bases[0], m.num_bins, x)
+    g, h, mg, mh = O.gradients_mc(preds, y, K, 1)
+    qg = np.rint(g * (np.float32(32767) / np.float32(mg))).astype(np.int64)
+    qh = np.rint(h * (np.float32(127) / np.float32(mh))).astype(np.int64)
+    f, thr = m.forest.feature[1, 0], m.forest.threshold[1, 0]
+    left = x[f] <= thr
+    for node, side in ((1, left), (2, ~left)):
+        G = np.float32(qg[side].sum()) * (np.float32(mg) / np.float32(32767))
+        H = np.float32(qh[side].sum()) * (np.float32(mh) / np.float32(127))
+        want = np.float32(lr) * (-G / (H + np.float32(lam)))
+        assert m.forest.leaf[1, node] == want, node
+
+
+def test_multiclass_shap_blocks_sum_to_class_scores(oracle):
+    # ObjectiveTests.swift:480-506
+    rows, cols, K = 800, 4, 3
+    rng = O.SplitMix(131)
+    x = np.array([rng.uniform() for _ in range(rows * cols)], np.float32).reshape(cols, rows)
+    y = np.minimum(2, (x[0] * 3).astype(int)).astype(np.float32)
+    m = fit_raw(x, y, num_trees=25, max_depth=4, objective=O.OBJ_MULTICLASS, num_classes=K)
+    c = O.treeshap_mc(m.forest, m.base_scores, m.num_bins, x).reshape(rows, K, cols + 1)
+    raw = O.predict_mc(m.forest, m.base_scores, m.num_bins, x)
+    assert np.abs(c.sum(axis=2) - raw).max() < 1e-4
+
+
+def test_leafwise_multiclass_accuracy(oracle):
+    # LeafWiseTests.swift:105-125
+    rows = 8000
+    rng = O.SplitMix(531)
+    x = np.array([rng.uniform() for _ in range(rows * 4)], np.float32).reshape(4, rows)
+    y = np.minimum(2, (x[0] * 3).astype(int)).astype(np.float32)
+    m = fit_raw(x, y, num_trees=30, max_depth=8, num_leaves=15, objective=O.OBJ_MULTICLASS,
+                num_classes=3)
+    raw = O.predict_mc(m.forest, m.base_scores, m.num_bins, x)
+    assert np.mean(raw.argmax(axis=1) == y) > 0.95
