@@ -220,9 +220,16 @@ void Booster::build_forest() {                    // forestBuffers, Booster.swif
     forest.valid = true;
 }
 
+std::vector<float> Booster::predict(const float *x, int64_t rows, int64_t cols) {
+    std::vector<float> out = predict_raw(x, rows, cols);
+    if (params.objective == OBJ_POISSON || params.objective == OBJ_TWEEDIE)
+        for (auto &v : out) v = std::exp(v);     // Booster.swift:1992-1997
+    return out;
+}
+
 // Raw scores, row-major [rows][K]; tree t adds to class t % K
 // (predict_forest, Shaders.swift:1548-1578).
-std::vector<float> Booster::predict(const float *x, int64_t rows, int64_t cols) {
+std::vector<float> Booster::predict_raw(const float *x, int64_t rows, int64_t cols) {
     const int K = std::max(1, trained_num_classes);
     std::vector<float> out((size_t)std::max<int64_t>(rows, 0) * (size_t)K, 0.0f);
     for (int64_t i = 0; i < rows; ++i)
@@ -244,9 +251,15 @@ std::vector<float> Booster::predict(const float *x, int64_t rows, int64_t cols) 
         MB_HIP(hipMemcpyAsync(out.data(), od.ptr, od.bytes(), hipMemcpyDeviceToHost, d.stream));
         MB_HIP(hipStreamSynchronize(d.stream));
     }
-    if (params.objective == OBJ_POISSON || params.objective == OBJ_TWEEDIE)
-        for (auto &v : out) v = std::exp(v);     // Booster.swift:1995-1997
     return out;
+}
+
+Booster *load_model_file(const std::string &path) {    // MacBooster.load, :2144-2162
+    std::ifstream f(path, std::ios::binary);
+    if (!f) internal("cannot read " + path);
+    std::stringstream ss;
+    ss << f.rdbuf();
+    return Booster::from_json(ss.str());
 }
 
 // Expected raw score of class k: its base + cover-weighted leaf means of its
@@ -620,13 +633,7 @@ int32_t macboost_save(void *handle, const char *path, char **err) {
 
 void *macboost_load(const char *path, char **err) {
     if (!path) { set_err(err, "null path"); return nullptr; }
-    return guarded(err, [&]() -> void * {
-        std::ifstream f(path, std::ios::binary);
-        if (!f) mb::internal(std::string("cannot read ") + path);
-        std::stringstream ss;
-        ss << f.rdbuf();
-        return Booster::from_json(ss.str());
-    }, nullptr);
+    return guarded(err, [&]() -> void * { return mb::load_model_file(path); }, nullptr);
 }
 
 int64_t macboost_num_trees(void *handle) {

@@ -155,6 +155,7 @@ struct Booster {
     Device &device();
     void build_forest();
     std::vector<float> predict(const float *x_fm, int64_t rows, int64_t cols);
+    std::vector<float> predict_raw(const float *x_fm, int64_t rows, int64_t cols);
     std::vector<float> predict_contrib(const float *x_fm, int64_t rows, int64_t cols);
     std::vector<float> feature_importance(int type) const;
     double shap_bias(int k = 0) const;
@@ -181,6 +182,8 @@ BinnedDataset *dataset_make(const Params &p, const float *x, int64_t rows, int64
                             const std::vector<std::string> *feature_names);
 void dataset_save(const BinnedDataset &ds, const std::string &path);
 BinnedDataset *dataset_load(const std::string &path);
+
+Booster *load_model_file(const std::string &path);
 
 // Incremental trainer (fitImpl, Booster.swift:445-1701).
 struct Trainer;

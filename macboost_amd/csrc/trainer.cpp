@@ -101,6 +101,10 @@ struct Trainer {
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
+    // warm start: the init model's trees prefix the ensemble and its raw
+    // scores seed preds (Booster.swift:849-866, :890-891)
+    std::vector<Tree> init_trees;
+    std::vector<float> seed_train, seed_valid;     // raw scores [rows][K], until uploaded
     // multiclass: K trees per round, preds [K][rows]; tree t fits class t % K
     int K = 1;
     std::vector<float> base_scores;
@@ -390,7 +394,6 @@ static float eval_metric(const Params &p, const float *pred, const float *y, int
 // Checks shared by both entry points (Booster.swift:451-529).
 static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
                             const float *w, const float *xv, int64_t vrows, const float *yv) {
-    if (!p.init_model.empty()) invalid("init_model (warm start) is not supported by this build yet");
     validate_labels(p, y, rows);
     if (w)
         for (int64_t i = 0; i < rows; ++i)
@@ -531,6 +534,27 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
                 reinterpret_cast<hipDeviceptr_t>(t.vpreds.ptr + (size_t)k * vrows), (int)bits,
                 (size_t)vrows, s));
     }
+    if (!t.seed_train.empty()) {
+        // warm start: preds [K][rows] from the init model's raw scores [rows][K]
+        std::vector<float> cm((size_t)rows * (size_t)K);
+        for (int64_t i = 0; i < rows; ++i)
+            for (int k = 0; k < K; ++k)
+                cm[(size_t)k * rows + i] = t.seed_train[(size_t)(i * K + k)];
+        MB_HIP(hipMemcpyAsync(t.preds.ptr, cm.data(), cm.size() * 4, hipMemcpyHostToDevice, s));
+        MB_HIP(hipStreamSynchronize(s));
+        if (t.has_valid && !t.seed_valid.empty()) {
+            std::vector<float> vm((size_t)vrows * (size_t)K);
+            for (int64_t i = 0; i < vrows; ++i)
+                for (int k = 0; k < K; ++k)
+                    vm[(size_t)k * vrows + i] = t.seed_valid[(size_t)(i * K + k)];
+            MB_HIP(hipMemcpyAsync(t.vpreds.ptr, vm.data(), vm.size() * 4, hipMemcpyHostToDevice, s));
+            MB_HIP(hipStreamSynchronize(s));
+        }
+        t.seed_train.clear();
+        t.seed_train.shrink_to_fit();
+        t.seed_valid.clear();
+        t.seed_valid.shrink_to_fit();
+    }
     t.preds_cur = t.preds.ptr;
     t.vpreds_cur = t.has_valid ? t.vpreds.ptr : nullptr;
     t.mono.alloc((size_t)cols);
@@ -631,6 +655,18 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     t.user_params = pin;
     const Params &p = t.p;
     const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
+    std::unique_ptr<Booster> im;
+    if (!p.init_model.empty()) {                     // Booster.swift:487-499
+        im.reset(load_model_file(p.init_model));
+        if (im->num_features != cols)
+            invalid("initModel expects " + std::to_string(im->num_features) + " features, X has " +
+                    std::to_string(cols));
+        if (im->params.objective != p.objective) invalid("initModel objective differs");
+        const int k_want = p.objective == OBJ_MULTICLASS ? p.num_classes : 1;
+        if (std::max(1, im->trained_num_classes) != k_want)
+            invalid("initModel has " + std::to_string(im->trained_num_classes) +
+                    " classes, the params ask for " + std::to_string(k_want));
+    }
     check_leakage(t, x, rows, cols, rs, cs, y);
     validate_categoricals(p, x, rows, cols, rs, cs);
     if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
@@ -666,7 +702,24 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         MB_HIP(hipStreamSynchronize(s));
     }
     t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
+    if (im) {
+        // the init model's raw scores on the training (and validation) rows
+        if (row_major) {
+            std::vector<float> xfm((size_t)rows * (size_t)cols);
+            for (int64_t i = 0; i < rows; ++i)
+                for (int64_t f = 0; f < cols; ++f) xfm[(size_t)(f * rows + i)] = x[i * cols + f];
+            t.seed_train = im->predict_raw(xfm.data(), rows, cols);
+        } else {
+            t.seed_train = im->predict_raw(x, rows, cols);
+        }
+        if (xv && yv && vrows > 0) t.seed_valid = im->predict_raw(xv, vrows, cols);
+        t.init_trees = im->trees;
+    }
     setup_buffers(t, y, w, yv);
+    if (im) {
+        t.base = im->base_score;
+        t.base_scores = im->base_scores;
+    }
     return tr.release();
 }
 
@@ -684,6 +737,8 @@ Trainer *trainer_create_binned(const Params &pin, const BinnedDataset &ds, const
     pe.categorical = std::set<int>(ds.categorical.begin(), ds.categorical.end());
     validate_params(pe);
     validate_inputs(pe, rows, cols, ds.labels.data(), w, xv, vrows, yv);
+    if (!pin.init_model.empty())                     // Booster.swift:487-491
+        invalid("initModel requires raw features (not a prebinned dataset)");
     auto tr = std::make_unique<Trainer>();
     Trainer &t = *tr;
     t.p = pe;
@@ -1151,7 +1206,8 @@ Booster *trainer_booster(Trainer *tp) {
         b->best_iteration = t.best_iter;
         if (t.p.early_stopping_rounds > 0 && keep > t.best_iter * t.K) keep = t.best_iter * t.K;
     }
-    b->trees.reserve((size_t)keep);
+    b->trees = t.init_trees;
+    b->trees.reserve(t.init_trees.size() + (size_t)keep);
     for (int k = 0; k < keep; ++k) {
         Tree tr;
         tr.feature.assign(tn, -1);

@@ -305,7 +305,7 @@ def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objectiv
         num_leaves=0, learning_rate=0.1, lam=1.0, min_child_hess=1.0, min_split_gain=0.0,
         cat_smooth=10.0, alpha=0.9, aux=1.0, w=None, is_cat=None, monotone=None,
         base=None, goss=False, goss_top_rate=0.2, goss_other_rate=0.1,
-        subsample=1.0, num_classes=1) -> OracleModel:
+        subsample=1.0, num_classes=1, init_preds=None) -> OracleModel:
     cols, rows = bins_fm.shape
     K = num_classes if objective == OBJ_MULTICLASS else 1
     p = OrcParams(num_trees, max_depth, num_bins, objective, num_leaves, learning_rate, lam,
@@ -322,6 +322,10 @@ def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objectiv
         if base is None:
             base = base_score(y, w, objective, aux if objective == OBJ_LOGISTIC else 1.0, alpha)
         preds = np.full(rows, base, np.float32)
+    if init_preds is not None:
+        # warm start: running predictions begin at the init model's raw
+        # scores (Booster.swift:849-866)
+        preds = np.ascontiguousarray(np.array(init_preds, np.float32).reshape(preds.shape))
     nodes = (1 << (max_depth + 1)) - 1
     forest = Forest.empty(num_trees * K, nodes)
     cat = None if is_cat is None else np.ascontiguousarray(is_cat, np.uint8)

@@ -586,6 +586,60 @@ def test_multiclass_early_stopping_keeps_whole_rounds():
 
 
 # --------------------------------------------------------------------------
+# warm start (init_model)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("params,rm", [
+    ({"max_depth": 5}, False),
+    ({"max_depth": 6, "num_leaves": 20, "objective": "binary"}, True),
+    ({"max_depth": 4, "objective": "multiclass", "num_class": 3}, False),
+])
+def test_warm_start_continues_one_shot_training(tmp_path, params, rm):
+    # ObjectiveTests.swift:374-393.  The init model's raw scores equal the
+    # running predictions after its trees, so 20 + 20 trees are the one-shot
+    # run's 40 trees.
+    rows = 20_000
+    x, y = O.friedman(rows, 8, 105)
+    if params.get("objective") == "binary":
+        y = (y > np.median(y)).astype(np.float32)
+    if params.get("objective") == "multiclass":
+        y = np.minimum(2, (x[0] * 3).astype(int)).astype(np.float32)
+    first = mb.train(dict(params, num_trees=20), x, y, feature_major=True)
+    mb.save(first, tmp_path / "first.json")
+    xin = np.ascontiguousarray(x.T) if rm else x
+    second = mb.train(dict(params, num_trees=20, init_model=str(tmp_path / "first.json")), xin,
+                      y, feature_major=not rm)
+    full = mb.train(dict(params, num_trees=40), x, y, feature_major=True)
+    K = params.get("num_class", 1)
+    assert mb.num_trees(second) == 40 * K
+    a, b = model_io.saved_model(second), model_io.saved_model(full)
+    nodes = (1 << (params["max_depth"] + 1)) - 1
+    model_io.assert_same_forest(model_io.forest_from_json(a, nodes),
+                                model_io.forest_from_json(b, nodes), with_cats=False)
+    assert a["baseScore"] == b["baseScore"] and a["baseScores"] == b["baseScores"]
+    xt, _ = O.friedman(3000, 8, 106)
+    assert np.array_equal(mb.predict(second, xt, feature_major=True),
+                          mb.predict(full, xt, feature_major=True))
+
+
+def test_warm_start_with_validation_set(tmp_path):
+    x, y = O.friedman(15_000, 8, 107)
+    xv, yv = O.friedman(4000, 8, 108)
+    first = mb.train({"num_trees": 15, "max_depth": 5}, x, y, feature_major=True)
+    mb.save(first, tmp_path / "f.json")
+    p = {"num_trees": 200, "max_depth": 5, "learning_rate": 0.3, "early_stopping_rounds": 5,
+         "init_model": str(tmp_path / "f.json")}
+    second = mb.train(p, x, y, eval_set=(xv.T, yv), feature_major=True)
+    best = mb.best_iteration(second)
+    assert mb.num_trees(second) == 15 + best
+    ref = oracle_fit(x, y, {"num_trees": 15 + best + 5, "max_depth": 5})
+    got = model_io.forest_from_json(model_io.saved_model(second), ref.forest.nodes_per_tree)
+    first_f = model_io.forest_from_json(model_io.saved_model(first), ref.forest.nodes_per_tree)
+    model_io.assert_same_forest(first_f, _first_trees(ref.forest, 15), with_cats=False)
+    assert got.num_trees == 15 + best
+
+
+# --------------------------------------------------------------------------
 # leaf-wise (best-first) growth
 # --------------------------------------------------------------------------
 

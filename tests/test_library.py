@@ -131,3 +131,27 @@ def test_malformed_model_is_rejected(tmp_path):
     p.write_text(json.dumps(obj))
     with pytest.raises(mb.MacBoostError, match="unsupported model file"):
         mb.load(p)
+
+
+def test_init_model_validation_without_gpu(tmp_path):
+    # Booster.swift:487-499: the init model must match the features and
+    # objective, and cannot seed a prebinned dataset
+    x, m = _small_oracle_model()
+    obj = model_io.forest_to_json(m.forest, base=m.base_score, num_bins=64, num_features=6)
+    p = tmp_path / "init.json"
+    p.write_text(json.dumps(obj))
+    x5, y5 = O.friedman(500, 5, 3)
+    with pytest.raises(mb.MacBoostError, match="initModel expects 6 features, X has 5"):
+        mb.train({"init_model": str(p)}, x5, y5, feature_major=True)
+    x6, y6 = O.friedman(500, 6, 3)
+    with pytest.raises(mb.MacBoostError, match="initModel objective differs"):
+        mb.train({"init_model": str(p), "objective": "huber"}, x6, y6, feature_major=True)
+    with pytest.raises(mb.MacBoostError, match="cannot read"):
+        mb.train({"init_model": str(tmp_path / "missing.json")}, x6, y6, feature_major=True)
+    from oracle import mbds as M
+    M.write(tmp_path / "d.mbds", 500, 6, 64, [], None, np.zeros((6, 62), np.float32), y6,
+            M.tile8(np.zeros((6, 500), np.uint8)))
+    ds = mb.Dataset.load(tmp_path / "d.mbds")
+    with pytest.raises(mb.MacBoostError,
+                       match=r"initModel requires raw features \(not a prebinned dataset\)"):
+        mb.train_dataset({"init_model": str(p)}, ds)

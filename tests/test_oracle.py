@@ -837,3 +837,21 @@ def test_leafwise_multiclass_accuracy(oracle):
                 num_classes=3)
     raw = O.predict_mc(m.forest, m.base_scores, m.num_bins, x)
     assert np.mean(raw.argmax(axis=1) == y) > 0.95
+
+
+def test_warm_start_matches_one_shot_training(oracle):
+    # ObjectiveTests.swift:374-393: 50 trees, then 50 more from the first
+    # model's raw scores, against 100 in one go.  Seeded with the first run's
+    # running predictions, the continued trees are the one-shot run's trees.
+    x, y = O.friedman(20_000, 8, 105)
+    xv, yv = O.friedman(5000, 8, 106)
+    first = fit_raw(x, y, num_trees=50, max_depth=5)
+    edges = first.edges
+    bins = O.bin_matrix(x, edges, 256)
+    second = O.fit(bins, y, edges=edges, num_trees=50, max_depth=5, base=first.base_score,
+                   init_preds=first.preds)
+    full = fit_raw(x, y, num_trees=100, max_depth=5)
+    cont = predict(first, xv) + predict(second, xv) - np.float32(first.base_score)
+    assert abs(rmse(cont, yv) - rmse(predict(full, xv), yv)) < 0.03
+    assert np.array_equal(second.forest.leaf, full.forest.leaf[50:])
+    assert np.array_equal(second.forest.feature, full.forest.feature[50:])
