@@ -6,6 +6,6 @@ entry points as the reference binding (python/macboost/_core.py).
 """
 from ._core import (  # noqa: F401
     Context, Dataset, MacBoostError, Trainer, best_iteration, feature_importance, friedman,
-    load, num_classes, num_features, num_trees, predict, predict_contrib, save, train,
-    train_dataset, version, warnings,
+    load, num_classes, num_features, num_trees, predict, predict_contrib, save,
+    select_features, train, train_dataset, version, warnings,
 )

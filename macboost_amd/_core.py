@@ -244,6 +244,32 @@ def train(config: dict, X, y, eval_set=None, sample_weight=None, feature_major=F
     return _Handle(ptr)
 
 
+def select_features(config: dict, X, y, sample_weight=None, rounds: int = 20, trees: int = 0,
+                    alpha: float = 0.05, seed: int = 0, feature_major=False):
+    """macboost_select_features (Boruta, CAPI.swift:138-183): (hits, decision
+    2 confirmed / 1 tentative / 0 rejected, gain ratio) per feature."""
+    if feature_major:
+        xf = np.ascontiguousarray(X, dtype=np.float32)
+        cols, rows = xf.shape
+    else:
+        xf, rows, cols = _feature_major(X)
+    ya = np.ascontiguousarray(np.asarray(y, dtype=np.float32).ravel())
+    if ya.shape[0] != rows:
+        raise ValueError(f"y has {ya.shape[0]} rows, X has {rows}")
+    wa = None if sample_weight is None else np.ascontiguousarray(sample_weight, dtype=np.float32)
+    hits = np.empty(cols, np.int32)
+    decision = np.empty(cols, np.int32)
+    ratio = np.empty(cols, np.float32)
+    err = ctypes.c_char_p()
+    rc = lib().macboost_select_features(
+        json.dumps(config).encode(), _f32(xf), rows, cols, _f32(ya), _f32(wa), rounds, trees,
+        alpha, seed, hits.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+        decision.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), _f32(ratio), ctypes.byref(err))
+    if rc != 0:
+        raise MacBoostError(_take_error(err))
+    return hits, decision, ratio
+
+
 def predict(handle: _Handle, X, feature_major=False) -> np.ndarray:
     if feature_major:
         xf = np.ascontiguousarray(X, dtype=np.float32)

@@ -569,11 +569,25 @@ void *macboost_train(const char *params_json, const float *x, int64_t rows, int6
     }, nullptr);
 }
 
-int32_t macboost_select_features(const char *, const float *, int64_t, int64_t, const float *,
-                                 const float *, int32_t, int32_t, float, int64_t, int32_t *,
-                                 int32_t *, float *, char **err) {
-    set_err(err, "Invalid input: feature selection (Boruta) is not part of this build");
-    return 1;
+// CAPI.swift:138-183.  Returns 0, or 1 with *err set.
+int32_t macboost_select_features(const char *params_json, const float *x, int64_t rows,
+                                 int64_t cols, const float *y, const float *w, int32_t rounds,
+                                 int32_t trees, float alpha, int64_t seed, int32_t *out_hits,
+                                 int32_t *out_decision, float *out_gain_ratio, char **err) {
+    return guarded(err, [&]() -> int32_t {
+        if (!x || !y || rows <= 0 || cols <= 0 || !out_hits || !out_decision || !out_gain_ratio)
+            mb::internal("null or empty selection input");
+        mb::Params p = mb::parse_params(params_json);
+        const mb::SelectionResult r =
+            mb::select_features(p, x, rows, cols, y, w, rounds, trees > 0 ? trees : 0,
+                                (double)alpha, (uint64_t)seed);
+        for (int64_t f = 0; f < cols; ++f) {
+            out_hits[f] = r.hits[(size_t)f];
+            out_decision[f] = r.decision[(size_t)f];
+            out_gain_ratio[f] = r.gain_ratio[(size_t)f];
+        }
+        return 0;
+    }, 1);
 }
 
 int32_t macboost_predict(void *handle, const float *x, int64_t rows, int64_t cols, float *out,

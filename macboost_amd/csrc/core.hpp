@@ -192,6 +192,20 @@ Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t c
                         int64_t vrows, const float *yv);
 Trainer *trainer_create_binned(const Params &p, const BinnedDataset &ds, const float *w,
                                const float *xv, int64_t vrows, const float *yv);
+Trainer *trainer_create_fm(const Params &p, int64_t rows, int64_t cols, const uint8_t *fm_dev,
+                           const std::vector<float> &edges, const float *y, const float *w);
+
+// Boruta feature selection (FeatureSelection.swift:45-190): per feature the
+// rounds it beat the best shadow, the decision (2 confirmed, 1 tentative,
+// 0 rejected) and the gain ratio against the mean best-shadow gain.
+struct SelectionResult {
+    std::vector<int32_t> hits, decision;
+    std::vector<float> gain_ratio;
+};
+SelectionResult select_features(const Params &p, const float *x_fm, int64_t rows, int64_t cols,
+                                const float *y, const float *w, int rounds, int trees,
+                                double alpha, uint64_t seed);
+void validate_label_values(const Params &p, const float *y, int64_t n);
 void trainer_grow(Trainer *t, int num_trees);
 void trainer_profile(Trainer *t, bool enable);
 void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes);

@@ -1845,6 +1845,50 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
 }
 
 // ---------------------------------------------------------------------------
+// Boruta shadow columns (shadow_perm + shadow_bins, Shaders.swift:1596-1631):
+// fm2 [2F][rows] = the real bins, then each column's bins row-permuted by a
+// 4-round Feistel network over 2*hb bits with cycle walking (a bijection of
+// [0, rows), so the walk ends for every row).
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t shadow_perm(uint32_t i, uint32_t n, uint32_t hb,
+                                                uint32_t seed) {
+    const uint32_t mask = (1u << hb) - 1u;
+    do {
+        uint32_t L = i >> hb, R = i & mask;
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r) {
+            const uint32_t t = R;
+            R = L ^ (wang_hash(R ^ (seed + r * 0x9E3779B9u)) & mask);
+            L = t;
+        }
+        i = (L << hb) | R;
+    } while (i >= n);
+    return i;
+}
+
+__global__ __launch_bounds__(256) void k_shadow_bins(const uint8_t *__restrict__ fm, int64_t rows,
+                                                     int32_t cols, uint32_t hb, uint32_t seed,
+                                                     uint8_t *__restrict__ fm2) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int32_t f = blockIdx.y;
+    if (i >= rows) return;
+    fm2[(int64_t)f * rows + i] = fm[(int64_t)f * rows + i];
+    const uint32_t j = shadow_perm((uint32_t)i, (uint32_t)rows, hb, seed ^ wang_hash((uint32_t)f + 1u));
+    fm2[(int64_t)(cols + f) * rows + i] = fm[(int64_t)f * rows + j];
+}
+
+hipError_t launch_shadow_bins(hipStream_t s, const uint8_t *fm, int64_t rows, int32_t cols,
+                              uint32_t half_bits, uint32_t seed, uint8_t *fm2) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (rows > 0xFFFFFFFFLL || 2 * half_bits > 32 || ((uint64_t)1 << (2 * half_bits)) < (uint64_t)rows)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_shadow_bins, dim3((unsigned)((rows + 255) / 256), (unsigned)cols),
+                       dim3(256), 0, s, fm, rows, cols, half_bits, seed, fm2);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Leaf renewal for the L1 and quantile objectives (Booster.swift:634-639,
 // :1253-1290, :1596-1615): the residuals y - preds of every step-th row,
 // grouped by the leaf the row reaches; a leaf with >= 4 of them becomes

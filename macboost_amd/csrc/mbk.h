@@ -117,6 +117,10 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            const uint8_t *is_cat, int32_t num_bins, int32_t tile_w,
                            int32_t num_tiles, uint8_t *bins_tiled, uint8_t *bins_fm);
 
+// Boruta shadows: fm [cols][rows] -> fm2 [2*cols][rows] (real, then permuted).
+hipError_t launch_shadow_bins(hipStream_t s, const uint8_t *fm, int64_t rows, int32_t cols,
+                              uint32_t half_bits, uint32_t seed, uint8_t *fm2);
+
 // .mbds tile-8 bins (Dataset.swift:18): feature-major -> [ceil(cols/8)][rows] u64
 // words, and back into the gather [rows][T][W] (pre-zeroed) + feature-major
 // layouts; *bad (pre-zeroed) becomes nonzero if a bin is >= nb.

@@ -206,6 +206,8 @@ static void validate_labels(const Params &p, const float *y, int64_t n) {   // :
     }
 }
 
+void validate_label_values(const Params &p, const float *y, int64_t n) { validate_labels(p, y, n); }
+
 // multiclassLogloss (Booster.swift:1828-1841) over preds [K][n].
 static float multiclass_logloss(const float *pred, const float *y, int64_t n, int K) {
     double s = 0;
@@ -720,6 +722,38 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         t.base = im->base_score;
         t.base_scores = im->base_scores;
     }
+    return tr.release();
+}
+
+// fitImpl with GPU-resident pre-binned input (GPUBinned, Booster.swift:436-443,
+// feature selection's shadow matrix): feature-major device bins [cols][rows],
+// rearranged into the gather layout on the device.
+Trainer *trainer_create_fm(const Params &pin, int64_t rows, int64_t cols, const uint8_t *fm_dev,
+                           const std::vector<float> &edges, const float *y, const float *w) {
+    validate_params(pin);
+    validate_inputs(pin, rows, cols, y, w, nullptr, 0, nullptr);
+    auto tr = std::make_unique<Trainer>();
+    Trainer &t = *tr;
+    t.p = pin;
+    t.user_params = pin;
+    setup_shape(t, rows, cols);
+    hipStream_t s = t.dev->stream;
+    {
+        const int64_t groups = (cols + 7) / 8;
+        DevBuf<uint64_t> words((size_t)groups * (size_t)rows);
+        DevBuf<uint32_t> bad(1);
+        MB_HIP(hipMemsetAsync(bad.ptr, 0, 4, s));
+        t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)t.sh.tile_w);
+        t.bins_fm.alloc((size_t)rows * (size_t)cols);
+        MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
+        MB_HIP(mbk::launch_fm_to_tile8(s, fm_dev, rows, (int)cols, words.ptr));
+        MB_HIP(mbk::launch_tile8_to_layouts(s, words.ptr, rows, (int)cols, t.nb, t.sh.tile_w,
+                                            t.sh.num_tiles, t.bins_tiled.ptr, t.bins_fm.ptr,
+                                            bad.ptr));
+        MB_HIP(hipStreamSynchronize(s));
+    }
+    t.edges = edges;
+    setup_buffers(t, y, w, nullptr);
     return tr.release();
 }
 

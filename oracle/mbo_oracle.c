@@ -910,6 +910,36 @@ static inline uint32_t wang_hash(uint32_t x) {                    /* :1144-1148 
     return x;
 }
 
+/* Boruta shadows (shadow_perm + shadow_bins, Shaders.swift:1596-1631): a
+ * 4-round Feistel permutation of [0, n) over 2*hb bits with cycle walking;
+ * fm2 [2*cols][rows] holds the real bins, then column f's bins permuted by
+ * the round seed ^ wang_hash(f + 1). */
+uint32_t orc_shadow_perm(uint32_t i, uint32_t n, uint32_t hb, uint32_t seed) {
+    const uint32_t mask = (1u << hb) - 1u;
+    do {
+        uint32_t L = i >> hb, R = i & mask;
+        for (uint32_t r = 0; r < 4; ++r) {
+            uint32_t t = R;
+            R = L ^ (wang_hash(R ^ (seed + r * 0x9E3779B9u)) & mask);
+            L = t;
+        }
+        i = (L << hb) | R;
+    } while (i >= n);
+    return i;
+}
+
+void orc_shadow_bins(const uint8_t *fm, int64_t rows, int32_t cols, uint32_t hb, uint32_t seed,
+                     uint8_t *fm2) {
+    for (int32_t f = 0; f < cols; ++f) {
+        const uint32_t fs = seed ^ wang_hash((uint32_t)f + 1u);
+        for (int64_t i = 0; i < rows; ++i) {
+            fm2[(int64_t)f * rows + i] = fm[(int64_t)f * rows + i];
+            const uint32_t j = orc_shadow_perm((uint32_t)i, (uint32_t)rows, hb, fs);
+            fm2[(int64_t)(cols + f) * rows + i] = fm[(int64_t)f * rows + j];
+        }
+    }
+}
+
 int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, int64_t rows,
                         float max_g, uint8_t *kept, float *wmax_g, float *wmax_h) {
     const int goss = p->goss != 0;

@@ -126,6 +126,11 @@ int32_t orc_cat_order(const int64_t *hg, const int64_t *hh, int32_t num_bins,
  * unweighted max |g|.  kept[i] = 1 for kept rows; returns their count and the
  * maxima of |g|*w and h*w over them (quantisation uses these). */
 int orc_sampling_active(const orc_params *p, int32_t tree);
+/* Boruta shadow columns (Shaders.swift:1596-1631): fm [cols][rows] ->
+ * fm2 [2*cols][rows], real columns then row-permuted copies. */
+uint32_t orc_shadow_perm(uint32_t i, uint32_t n, uint32_t half_bits, uint32_t seed);
+void orc_shadow_bins(const uint8_t *fm, int64_t rows, int32_t cols, uint32_t half_bits,
+                     uint32_t seed, uint8_t *fm2);
 int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, int64_t rows,
                         float max_g, uint8_t *kept, float *wmax_g, float *wmax_h);
 

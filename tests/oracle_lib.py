@@ -444,3 +444,94 @@ class SplitMix:
 
     def uniforms(self, n: int) -> np.ndarray:
         return np.array([self.uniform() for _ in range(n)], dtype=np.float32)
+
+
+# --------------------------------------------------------------------------
+# Boruta feature selection (FeatureSelection.swift:45-190)
+# --------------------------------------------------------------------------
+
+def shadow_bins(bins_fm, half_bits, seed):
+    l = lib()
+    l.orc_shadow_bins.restype = None
+    l.orc_shadow_bins.argtypes = [_P, _I64, _I32, ctypes.c_uint32, ctypes.c_uint32, _P]
+    cols, rows = bins_fm.shape
+    src = np.ascontiguousarray(bins_fm, np.uint8)
+    out = np.empty((2 * cols, rows), np.uint8)
+    l.orc_shadow_bins(_ptr(src), rows, cols, half_bits, seed & 0xFFFFFFFF, _ptr(out))
+    return out
+
+
+def shadow_perm(i, n, half_bits, seed):
+    l = lib()
+    l.orc_shadow_perm.restype = ctypes.c_uint32
+    l.orc_shadow_perm.argtypes = [ctypes.c_uint32] * 4
+    return int(l.orc_shadow_perm(i, n, half_bits, seed & 0xFFFFFFFF))
+
+
+def gain_importance(forest: Forest, num_features: int) -> np.ndarray:
+    """featureImportance(type: .gain) (Booster.swift:1926-1940): per tree a
+    stack walk from the root, f32 sums in that visiting order."""
+    imp = np.zeros(num_features, np.float32)
+    for t in range(forest.num_trees):
+        stack = [0]
+        while stack:
+            n = stack.pop()
+            f = int(forest.feature[t, n])
+            if f < 0:
+                continue
+            imp[f] = np.float32(imp[f] + forest.gain[t, n])
+            stack.append(2 * n + 1)
+            stack.append(2 * n + 2)
+    return imp
+
+
+def binomial_tail(k, rounds):
+    """P[Binomial(rounds, 0.5) >= k], accumulated as FeatureSelection.swift:193-203."""
+    if k <= 0:
+        return 1.0
+    pmf = 0.5 ** rounds
+    tail = 0.0
+    for i in range(rounds + 1):
+        if i >= k:
+            tail += pmf
+        if i < rounds:
+            pmf *= (rounds - i) / (i + 1)
+    return min(1.0, tail)
+
+
+def select_features(x_fm, y, *, rounds=20, trees=None, alpha=0.05, seed=0, num_bins=256,
+                    is_cat=None, num_trees=100, **fit_kw):
+    """Boruta: bins once, then per round a fit on [bins | shadow(bins)] and a
+    vote of each real feature's gain against the best shadow's.  Returns
+    (hits, decision 2/1/0, gain ratio)."""
+    cols, rows = x_fm.shape
+    edges = compute_edges(x_fm, num_bins, is_cat)
+    bins = bin_matrix(x_fm, edges, num_bins, is_cat)
+    edges2 = np.ascontiguousarray(np.vstack([edges, edges]))
+    cat2 = None if is_cat is None else np.concatenate([is_cat, is_cat]).astype(np.uint8)
+    bits = 1
+    while (1 << bits) < rows:
+        bits += 1
+    half = (bits + 1) // 2
+    n_trees = trees if trees is not None else min(num_trees, 100)
+    hits = np.zeros(cols, np.int64)
+    gain_sum = np.zeros(cols, np.float64)
+    shadow_sum = 0.0
+    for r in range(rounds):
+        rseed = (seed + r * 0x9E3779B97F4A7C15 + 1) & 0xFFFFFFFF
+        b2 = shadow_bins(bins, half, rseed)
+        m = fit(b2, y, edges=edges2, num_bins=num_bins, is_cat=cat2, num_trees=n_trees, **fit_kw)
+        g = gain_importance(m.forest, 2 * cols)
+        mx = g[cols:].max()
+        hits += g[:cols] > mx
+        gain_sum += g[:cols].astype(np.float64)
+        shadow_sum += float(mx)
+    cutoff = alpha / cols
+    dec = np.ones(cols, np.int32)
+    for f in range(cols):
+        if binomial_tail(int(hits[f]), rounds) < cutoff:
+            dec[f] = 2
+        elif binomial_tail(rounds - int(hits[f]), rounds) < cutoff:
+            dec[f] = 0
+    ratio = (gain_sum / max(shadow_sum, np.finfo(np.float64).tiny)).astype(np.float32)
+    return hits.astype(np.int32), dec, ratio

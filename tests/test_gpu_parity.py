@@ -640,6 +640,53 @@ def test_warm_start_with_validation_set(tmp_path):
 
 
 # --------------------------------------------------------------------------
+# Boruta feature selection (macboost_select_features)
+# --------------------------------------------------------------------------
+
+def _signal_plus_noise(rows, signal=5, noise=5, seed=311):
+    x, y = O.friedman(rows, signal, seed)
+    rng = np.random.default_rng(seed + 1)
+    return np.vstack([x, rng.uniform(0, 1, (noise, rows)).astype(np.float32)]), y
+
+
+@pytest.mark.parametrize("params,seed", [({"num_trees": 30, "max_depth": 6}, 0),
+                                         ({"num_trees": 20, "max_depth": 5, "num_bins": 64}, 77)])
+def test_select_features_matches_oracle(params, seed):
+    # FeatureSelection.swift:45-190: the same shadows, the same probe models,
+    # so the same votes, decisions and gain ratios
+    x, y = _signal_plus_noise(6000)
+    hits, dec, ratio = mb.select_features(params, x, y, rounds=8, seed=seed, feature_major=True)
+    kw = dict(params)
+    nb = kw.pop("num_bins", 256)
+    nt = kw.pop("num_trees")
+    oh, od, orat = O.select_features(x, y, rounds=8, seed=seed, num_bins=nb, num_trees=nt, **kw)
+    assert np.array_equal(hits, oh) and np.array_equal(dec, od)
+    assert np.array_equal(ratio, orat)
+    assert (hits[:5] >= 7).all()                       # the signal beats every shadow
+
+
+def test_select_features_nan_categorical_and_rows_not_a_power_of_two():
+    # SelectionTests.swift:80-100: shadows of a categorical column stay categorical
+    rows = 5001
+    x, y = O.friedman(rows, 5, 351)
+    rng = np.random.default_rng(352)
+    x = x.copy()
+    x[2, rng.random(rows) < 0.2] = np.nan
+    good = rng.integers(0, 6, rows).astype(np.float32)
+    junk = rng.integers(0, 6, rows).astype(np.float32)
+    y = (y + np.where(good == 3, 4.0, 0.0)).astype(np.float32)
+    x = np.vstack([x, good[None], junk[None]])
+    params = {"num_trees": 25, "max_depth": 5, "categorical_features": [5, 6]}
+    hits, dec, ratio = mb.select_features(params, x, y, rounds=6, trees=20, seed=5,
+                                          feature_major=True)
+    is_cat = np.array([0, 0, 0, 0, 0, 1, 1], np.uint8)
+    oh, od, orat = O.select_features(x, y, rounds=6, trees=20, seed=5, num_trees=25,
+                                     max_depth=5, is_cat=is_cat)
+    assert np.array_equal(hits, oh) and np.array_equal(dec, od) and np.array_equal(ratio, orat)
+    assert hits[5] == 6 and hits[6] < 6
+
+
+# --------------------------------------------------------------------------
 # leaf-wise (best-first) growth
 # --------------------------------------------------------------------------
 

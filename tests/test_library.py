@@ -155,3 +155,22 @@ def test_init_model_validation_without_gpu(tmp_path):
     with pytest.raises(mb.MacBoostError,
                        match=r"initModel requires raw features \(not a prebinned dataset\)"):
         mb.train_dataset({"init_model": str(p)}, ds)
+
+
+def test_select_features_validation_without_gpu():
+    # FeatureSelection.swift:53-69, CAPI.swift:150-152
+    x, y = O.friedman(200, 6, 1)
+    with pytest.raises(mb.MacBoostError,
+                       match=r"Invalid input: selection needs rounds >= 5 for the binomial test"):
+        mb.select_features({}, x, y, rounds=4, feature_major=True)
+    with pytest.raises(mb.MacBoostError, match=r"Invalid input: alpha must be in \(0, 1\)"):
+        mb.select_features({}, x, y, alpha=1.5, feature_major=True)
+    with pytest.raises(mb.MacBoostError, match="binary objective requires labels"):
+        mb.select_features({"objective": "binary"}, x, y, feature_major=True)
+    h = np.empty(6, np.int32)
+    err = _core.ctypes.c_char_p()
+    rc = _core.lib().macboost_select_features(b"{}", None, 200, 6, None, None, 20, 0, 0.05, 0,
+                                              h.ctypes.data_as(_core.ctypes.POINTER(_core.ctypes.c_int32)),
+                                              h.ctypes.data_as(_core.ctypes.POINTER(_core.ctypes.c_int32)),
+                                              None, _core.ctypes.byref(err))
+    assert rc == 1 and b"null or empty selection input" in err.value

@@ -855,3 +855,56 @@ def test_warm_start_matches_one_shot_training(oracle):
     assert abs(rmse(cont, yv) - rmse(predict(full, xv), yv)) < 0.03
     assert np.array_equal(second.forest.leaf, full.forest.leaf[50:])
     assert np.array_equal(second.forest.feature, full.forest.feature[50:])
+
+
+# --------------------------------------------------------------------------
+# Boruta feature selection
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 2, 3, 7, 64, 1000, 4097])
+def test_shadow_permutation_is_a_bijection(oracle, n):
+    # shadow_perm (Shaders.swift:1596-1611) must permute [0, n) for any seed
+    bits = 1
+    while (1 << bits) < n:
+        bits += 1
+    hb = (bits + 1) // 2
+    for seed in (0, 1, 0xDEADBEEF):
+        img = sorted(O.shadow_perm(i, n, hb, seed) for i in range(n))
+        assert img == list(range(n))
+
+
+def test_shadow_bins_copy_then_permute_each_column(oracle):
+    rows, cols = 300, 3
+    fm = np.random.default_rng(0).integers(0, 255, (cols, rows)).astype(np.uint8)
+    out = O.shadow_bins(fm, 5, 1234)
+    assert np.array_equal(out[:cols], fm)
+    for f in range(cols):
+        assert sorted(out[cols + f]) == sorted(fm[f])          # a permutation of the column
+    assert not np.array_equal(out[cols], fm[0])
+    assert not np.array_equal(out[cols + 1][np.argsort(fm[1], kind="stable")],
+                              out[cols][np.argsort(fm[0], kind="stable")])
+
+
+def test_binomial_tail_exact(oracle):
+    from math import comb
+    for rounds in (5, 20):
+        for k in range(rounds + 2):
+            want = sum(comb(rounds, i) for i in range(max(k, 0), rounds + 1)) / 2 ** rounds
+            assert abs(O.binomial_tail(k, rounds) - min(1.0, want)) < 1e-12
+
+
+def _signal_plus_noise(rows, signal=5, noise=5, seed=311):
+    x, y = O.friedman(rows, signal, seed)
+    rng = O.SplitMix(seed + 1)
+    xn = np.array([rng.uniform() for _ in range(rows * noise)], np.float32).reshape(noise, rows)
+    return np.vstack([x, xn]), y
+
+
+def test_boruta_separates_signal_from_noise(oracle):
+    # SelectionTests.swift:26-50
+    x, y = _signal_plus_noise(6000)
+    hits, dec, ratio = O.select_features(x, y, rounds=20, num_trees=60, max_depth=6)
+    conf = np.flatnonzero(dec == 2)
+    assert (conf < 5).sum() >= 4 and (conf < 5).all()
+    assert ((np.flatnonzero(dec == 0)) >= 5).sum() >= 4
+    assert (ratio[conf] > 1).all()
