@@ -1060,6 +1060,14 @@ hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint
 // split search: one wavefront per (sibling pair, feature)
 // ---------------------------------------------------------------------------
 
+// LDS visibility between the lanes of one wavefront (each wave owns its
+// scratch, so no workgroup barrier is needed).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 struct CatScratch {
     float key[256];
     int64_t sg[256];
@@ -1175,7 +1183,7 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
     const uint64_t ne_bits0 = __ballot(ne[0]), ne_bits1 = __ballot(ne[1]);
     const uint64_t ne_bits2 = __ballot(ne[2]), ne_bits3 = __ballot(ne[3]);
     if (lane < 8) cs->mask[lane] = 0;
-    __syncthreads();
+    wave_lds_sync();
     const int m = __popcll(ne_bits0) + __popcll(ne_bits1) + __popcll(ne_bits2) + __popcll(ne_bits3);
     int rank[4];
 #pragma unroll
@@ -1196,11 +1204,11 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
             rank[j] = r;
         }
     }
-    __syncthreads();
+    wave_lds_sync();
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         if (ne[j]) { cs->sg[rank[j]] = hg[j]; cs->sh[rank[j]] = hh[j]; }
-    __syncthreads();
+    wave_lds_sync();
     int64_t pg[4], ph[4];
     int64_t tg = 0, th = 0;
 #pragma unroll
@@ -1239,7 +1247,7 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         if (ne[j] && rank[j] < k) atomicOr(&cs->mask[(b0 + j) >> 5], 1u << ((b0 + j) & 31));
-    __syncthreads();
+    wave_lds_sync();
     if (ws == best_seq && best_gain == wg) {
         SplitResult r = {};
         r.gain = best_gain; r.bin = best_bin; r.gl = best_gl; r.hl = best_hl;
@@ -1250,7 +1258,18 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
     }
 }
 
-__global__ __launch_bounds__(64) void k_split(Shape sh, SplitParams sp,
+// One workgroup per (sibling pair, 4 features): each side's histogram rows
+// [bin][f0 .. f0+3] (64 contiguous bytes per bin) are staged through LDS,
+// eight independent loads per thread, then wavefront w searches feature
+// f0 + w (its 256 bins, 4 per lane).
+constexpr int SPLIT_FEATS = 4;
+constexpr int SPLIT_STAGE_PER_THREAD = 256 * SPLIT_FEATS * 2 / (SPLIT_FEATS * 64);
+constexpr size_t SPLIT_STAGE_BYTES = (size_t)256 * SPLIT_FEATS * 2 * sizeof(int64_t);
+constexpr size_t SPLIT_LDS_BYTES = SPLIT_STAGE_BYTES > SPLIT_FEATS * sizeof(CatScratch)
+                                       ? SPLIT_STAGE_BYTES
+                                       : SPLIT_FEATS * sizeof(CatScratch);
+
+__global__ __launch_bounds__(SPLIT_FEATS * 64) void k_split(Shape sh, SplitParams sp,
                                               const Pair *__restrict__ pairs,
                                               const int64_t *__restrict__ hist_cur,
                                               const uint8_t *__restrict__ is_cat,
@@ -1260,47 +1279,73 @@ __global__ __launch_bounds__(64) void k_split(Shape sh, SplitParams sp,
                                               int64_t *node_g, int64_t *node_h,
                                               uint32_t level_start,
                                               SplitResult *__restrict__ results) {
-    __shared__ CatScratch cs;
+    __shared__ __align__(16) unsigned char split_lds[SPLIT_LDS_BYTES];
+    int64_t *stage = reinterpret_cast<int64_t *>(split_lds);      // [bin][16][2]
+    CatScratch *cs_all = reinterpret_cast<CatScratch *>(split_lds);
     const int F = sh.cols, nb = sh.num_bins;
-    const uint32_t pair_idx = blockIdx.x / (uint32_t)F;
-    const int f = (int)(blockIdx.x % (uint32_t)F);
-    if (pair_idx >= ctl->num_pairs) return;          // uniform per block (one wave)
+    const uint32_t groups = (uint32_t)((F + SPLIT_FEATS - 1) / SPLIT_FEATS);
+    const uint32_t pair_idx = blockIdx.x / groups;
+    const int f0 = (int)(blockIdx.x % groups) * SPLIT_FEATS;
+    if (pair_idx >= ctl->num_pairs) return;          // uniform per block
+    const int nf = min(SPLIT_FEATS, F - f0);
     const Pair pr = pairs[pair_idx];
-    const int lane = lane_id();
+    const int tid = threadIdx.x, lane = lane_id();
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int f = f0 + w;
+    const bool active = w < nf;
     const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
     const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
-    const bool cat = is_cat[f] != 0;
-    const int cst = cat ? 0 : (int)monotone[f];
-    const bool allowed = feat_mask[f] != 0;
+    const bool cat = active && is_cat[f] != 0;
+    const int cst = (!active || cat) ? 0 : (int)monotone[f];
+    const bool allowed = active && feat_mask[f] != 0;
     for (int side = 0; side < 2; ++side) {
         const uint32_t local = side == 0 ? pr.built : pr.derived;
-        if (local == NONE) break;
+        if (local == NONE) break;                    // uniform per block
+        // stage rows [bin][f0 .. f0+nf) (each bin's 2*nf words are contiguous)
+        const int64_t *src = hist_cur + (size_t)local * nb * F * 2;
+        const int row = 2 * nf;
+        int64_t v[SPLIT_STAGE_PER_THREAD];
+#pragma unroll
+        for (int k = 0; k < SPLIT_STAGE_PER_THREAD; ++k) {
+            const int idx = tid + k * SPLIT_FEATS * 64;
+            const int b = idx / row, r = idx - b * row;
+            v[k] = idx < nb * row ? src[((size_t)b * F + f0) * 2 + r] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < SPLIT_STAGE_PER_THREAD; ++k) {
+            const int idx = tid + k * SPLIT_FEATS * 64;
+            const int b = idx / row, r = idx - b * row;
+            if (idx < nb * row) stage[(size_t)b * (2 * SPLIT_FEATS) + r] = v[k];
+        }
+        __syncthreads();
         int64_t hg[4], hh[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int b = 4 * lane + j;
             hg[j] = 0; hh[j] = 0;
-            if (b < nb) {
-                const int64_t *src = hist_cur + (((size_t)local * nb + b) * F + f) * 2;
-                hg[j] = src[0];
-                hh[j] = src[1];
+            if (active && b < nb) {
+                hg[j] = stage[(size_t)b * (2 * SPLIT_FEATS) + 2 * w];
+                hh[j] = stage[(size_t)b * (2 * SPLIT_FEATS) + 2 * w + 1];
             }
         }
-        const uint32_t abs_n = level_start + local;
-        if (f == 0) {
-            const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
-            const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
-            if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
+        __syncthreads();                             // the stage becomes split scratch
+        if (active) {
+            const uint32_t abs_n = level_start + local;
+            if (f == 0) {
+                const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
+                const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
+                if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
+            }
+            SplitResult *dst = results + (size_t)local * F + f;
+            if (allowed && count[abs_n] >= 1) {
+                node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs_all[w], dst);
+            } else if (lane == 0) {
+                SplitResult r = {};
+                r.gain = -INFINITY;
+                *dst = r;
+            }
         }
-        SplitResult *dst = results + (size_t)local * F + f;
-        __syncthreads();
-        if (allowed && count[abs_n] >= 1) {
-            node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs, dst);
-        } else if (lane == 0) {
-            SplitResult r = {};
-            r.gain = -INFINITY;
-            *dst = r;
-        }
+        __syncthreads();                             // before the next side's stage
     }
 }
 
@@ -1313,7 +1358,8 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp, c
     if (sh.num_bins > 256) return hipErrorInvalidValue;
     hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_split, dim3(max_pairs * (uint32_t)sh.cols), dim3(64), 0, s, sh, sp, pairs,
+    const uint32_t groups = (uint32_t)((sh.cols + SPLIT_FEATS - 1) / SPLIT_FEATS);
+    hipLaunchKernelGGL(k_split, dim3(max_pairs * groups), dim3(SPLIT_FEATS * 64), 0, s, sh, sp, pairs,
                        hist_cur, is_cat, monotone, feat_mask, ctl, count, node_g, node_h,
                        level_start, results);
     return hipGetLastError();
@@ -1323,13 +1369,15 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp, c
 // decisions: one wavefront per node (decide_splits phase 1, :1386-1451)
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void k_decide(Shape sh, SplitParams sp, LevelArgs la,
-                                               const SplitResult *__restrict__ results,
-                                               const uint32_t *count, int64_t *node_g,
-                                               int64_t *node_h, float2 *bounds,
-                                               const int8_t *monotone, const TreeCtl *ctl,
-                                               uint64_t *cursors, TreeOut out) {
-    const uint32_t local = blockIdx.x;
+// decide_splits for node `local` of level la (Shaders.swift:1342-1452), run by
+// one wavefront: argmax over features, then the node's split or leaf, the
+// children's sums and monotone bounds; also zeroes the node's partition
+// cursor for the level's partition.
+__device__ void decide_node(const Shape &sh, const SplitParams &sp, const LevelArgs &la,
+                            uint32_t local, const SplitResult *__restrict__ results,
+                            const uint32_t *count, int64_t *node_g, int64_t *node_h,
+                            float2 *bounds, const int8_t *monotone, const TreeCtl *ctl,
+                            uint64_t *cursors, const TreeOut &out) {
     const uint32_t n = la.level_start + local;
     const int lane = lane_id();
     const int F = sh.cols;
@@ -1388,6 +1436,16 @@ __global__ __launch_bounds__(64) void k_decide(Shape sh, SplitParams sp, LevelAr
         const float G = (float)Gt * g_inv, H = (float)Ht * h_inv;
         out.leaf[n] = sp.learning_rate * clampf(-G / (H + sp.lambda), bb.x, bb.y);
     }
+}
+
+__global__ __launch_bounds__(64) void k_decide(Shape sh, SplitParams sp, LevelArgs la,
+                                               const SplitResult *__restrict__ results,
+                                               const uint32_t *count, int64_t *node_g,
+                                               int64_t *node_h, float2 *bounds,
+                                               const int8_t *monotone, const TreeCtl *ctl,
+                                               uint64_t *cursors, TreeOut out) {
+    decide_node(sh, sp, la, blockIdx.x, results, count, node_g, node_h, bounds, monotone, ctl,
+                cursors, out);
 }
 
 hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
