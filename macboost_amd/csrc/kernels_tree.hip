@@ -806,13 +806,20 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 // permuted once per row so that step s reads a fixed register and byte.
 // Columns hold feature c (W = 64: 32*plane + c) or copy c / W of feature
 // c % W (W <= 32), summed when the item is flushed.  Loads are pipelined:
-// data four batches ahead, entries eight.
+// data three batches ahead, entries nine.
 // ---------------------------------------------------------------------------
 
 constexpr int HIST_THREADS = 1024;
 constexpr int HIST_LDS_BYTES = 2 * 256 * 32 * 8;     // two planes of [256][32] u64, static
-constexpr int HIST_DATA_RING = 4;
-constexpr int HIST_ENTRY_RING = 8;
+// ring depths chosen by measurement (3 / 9 beat 2..6 / 6..15 at 10M x 100:
+// deeper data rings cost L2 reuse between the two tiles of a row)
+constexpr int HIST_DATA_RING = 3;
+constexpr int HIST_ENTRY_RING = 9;
+static_assert(HIST_ENTRY_RING > HIST_DATA_RING, "a data refill needs the entry DR batches ahead");
+static_assert(HIST_ENTRY_RING % HIST_DATA_RING == 0, "batch k of every round uses data slot k % DR");
+// true: the per-lane LDS column words sit in a 32-register table; false: each
+// is rebuilt with one XOR per update (frees the table's registers)
+constexpr bool HIST_COLW_TABLE = true;
 
 // P bytes of one row as loaded: 16B chunks in the order (u ^ cx)
 template <int P> struct RowRaw { uint32_t d[P / 4]; };
@@ -879,10 +886,12 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
     const uint32_t m = ((uint32_t)lane & (uint32_t)(P - 1)) >> 2;
     const uint32_t cx = P == 32 ? (m >> 2) : 0u;
     const bool b0 = (m & 1u) != 0, b1 = (m & 2u) != 0;
-    uint32_t colw[P];
+    const uint32_t colbase = ((uint32_t)(lane >> 5) << 16) | (((uint32_t)lane & 31u) << 3);
+    uint32_t colw[HIST_COLW_TABLE ? P : 1];
+    if constexpr (HIST_COLW_TABLE) {
 #pragma unroll
-    for (int s = 0; s < P; ++s)
-        colw[s] = ((uint32_t)(lane >> 5) << 16) | ((((uint32_t)lane & 31u) ^ (uint32_t)s) << 3);
+        for (int s = 0; s < P; ++s) colw[s] = colbase ^ ((uint32_t)s << 3);
+    }
     uint32_t sel[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -927,7 +936,9 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
             const RowRaw<P> cur = permute_dwords<P>(raw, b0, b1);
 #pragma unroll
             for (int s = 0; s < P; ++s) {
-                const uint32_t addr = __builtin_amdgcn_perm(cur.d[s >> 2], colw[s], sel[s & 3]);
+                const uint32_t cw = HIST_COLW_TABLE ? colw[HIST_COLW_TABLE ? s : 0]
+                                                    : colbase ^ ((uint32_t)s << 3);
+                const uint32_t addr = __builtin_amdgcn_perm(cur.d[s >> 2], cw, sel[s & 3]);
                 atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
             }
         };
