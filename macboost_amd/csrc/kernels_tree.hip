@@ -1766,36 +1766,6 @@ hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la
 // is order-independent.  The left cursor ends as the node's left count.
 // ---------------------------------------------------------------------------
 
-constexpr int ROUTE_WAVES = ROUTE_THREADS / 64;
-
-// In-block exclusive prefix of `x` in entry order (pass k, then lane order).
-// tot must hold ROUTE_PER_THREAD*ROUTE_WAVES+1 words; on return tot[k*W+w]
-// is the prefix of slice (k, w) and tot[last] the block total.
-__device__ __forceinline__ void route_block_scan(const uint32_t (&x)[ROUTE_PER_THREAD],
-                                                 uint32_t (&ex)[ROUTE_PER_THREAD],
-                                                 uint32_t *tot) {
-    const int w = threadIdx.x >> 6;
-#pragma unroll
-    for (int k = 0; k < ROUTE_PER_THREAD; ++k) {
-        const uint32_t inc = wave_inclusive_scan(x[k]);
-        ex[k] = inc - x[k];
-        if (lane_id() == 63) tot[k * ROUTE_WAVES + w] = inc;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t acc = 0;
-        for (int i = 0; i < ROUTE_PER_THREAD * ROUTE_WAVES; ++i) {
-            const uint32_t t = tot[i];
-            tot[i] = acc;
-            acc += t;
-        }
-        tot[ROUTE_PER_THREAD * ROUTE_WAVES] = acc;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < ROUTE_PER_THREAD; ++k) ex[k] += tot[k * ROUTE_WAVES + w];
-}
-
 // Large blocks keep the cursor atomics few (two per block); 8 entries per
 // thread keep the kernel under 64 VGPRs, so two blocks share a CU.
 constexpr int PART_THREADS = 1024;
@@ -1807,41 +1777,19 @@ constexpr int PART_SLICES_PER_LANE = PART_SLICES / 64;
 static_assert(PART_BLOCK == PART_ENTRIES, "partition block size");
 static_assert(PART_SLICES % 64 == 0, "slice scan: whole slices per lane");
 
-__global__ __launch_bounds__(PART_THREADS) void k_route(
-    Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
-    Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
-    const uint32_t *__restrict__ count, const TreeOut out, uint64_t *cursors,
-    int write_entries) {
-    extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
-    __shared__ uint32_t tot[PART_PER_THREAD * PART_WAVES + 1];
-    __shared__ uint32_t s_mask[8];
+// One block's share of a node's partition: nvalid (<= PART_BLOCK) entries at
+// src go to the node's interval dst[0, cnt), lefts from the front and rights
+// from the back.  Both ranges are reserved with one packed 64-bit add on
+// *cursor (left count low, right count high; both < 2^32, so the low word
+// never carries).  s_mask is the split's category mask, in LDS.
+__device__ __forceinline__ void route_block(const NodeSplit sp, const uint32_t *s_mask, int32_t nb,
+                                            const uint8_t *__restrict__ col,
+                                            const Entry *__restrict__ src, uint32_t nvalid,
+                                            uint32_t cnt, Entry *__restrict__ dst,
+                                            uint64_t *cursor, bool write_entries) {
+    __shared__ uint32_t tot[PART_SLICES + 1];
     __shared__ uint64_t s_base;
-    __shared__ uint32_t wave_tot[PART_WAVES + 1];
-    const uint32_t b = blockIdx.x;
-    // blocks per split node of the routed level, and their prefix
-    for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
-        const uint32_t nn = la.level_start + l;
-        const bool split = out.split[nn].feature >= 0 && count[nn] >= 1;
-        blk_prefix[l] = split ? (count[nn] + PART_BLOCK - 1) / PART_BLOCK : 0u;
-    }
-    __syncthreads();
-    const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
-    if (b >= total_blocks) return;                   // uniform per block
-    // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
-    uint32_t lo = 0, hi = la.num_level - 1;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi + 1) >> 1;
-        if (blk_prefix[mid] <= b) lo = mid; else hi = mid - 1;
-    }
-    const uint32_t l = lo, n = la.level_start + l;
-    const uint32_t start = seg_start[l], cnt = count[n];
-    const uint32_t first = (b - blk_prefix[l]) * PART_BLOCK;
-    const uint32_t nvalid = min((uint32_t)PART_BLOCK, cnt - first);
-    const NodeSplit sp = out.split[n];
     const int tid = threadIdx.x, w = tid >> 6;
-    if (tid < 8) s_mask[tid] = out.mask[(size_t)n * 8 + tid];
-    __syncthreads();
-    const Entry *src = order_in + start + first;
     uint32_t x[PART_PER_THREAD], ex[PART_PER_THREAD];
     Entry e[PART_PER_THREAD];
 #pragma unroll
@@ -1854,10 +1802,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
 #pragma unroll
     for (int k = 0; k < PART_PER_THREAD; ++k) {
         const uint32_t i = (uint32_t)(k * PART_THREADS + tid);
-        if (i < nvalid) {
-            const uint32_t bin = bins_fm[(size_t)sp.feature * (size_t)sh.rows + e[k].row];
-            x[k] = bin_goes_left(bin, sp, sh.num_bins, s_mask) ? 1u : 0u;
-        }
+        if (i < nvalid) x[k] = bin_goes_left(col[e[k].row], sp, nb, s_mask) ? 1u : 0u;
     }
     // in-block exclusive prefix of the left flags in entry order (k, then lane)
 #pragma unroll
@@ -1879,10 +1824,8 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
         for (int j = 0; j < SPL; ++j) { tot[tid * SPL + j] = acc; acc += v[j]; }
         if (tid == 63) {
             const uint32_t nl = inc;
-            tot[PART_PER_THREAD * PART_WAVES] = nl;
-            // both counts < 2^32: the low word never carries into the high one
-            s_base = atomicAdd(reinterpret_cast<unsigned long long *>(
-                                   &cursors[(size_t)l * CURSOR_STRIDE]),
+            tot[PART_SLICES] = nl;
+            s_base = atomicAdd(reinterpret_cast<unsigned long long *>(cursor),
                                (unsigned long long)nl |
                                    ((unsigned long long)(nvalid - nl) << 32));
         }
@@ -1890,7 +1833,6 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
     if (!write_entries) return;                      // counts only (terminal level)
     __syncthreads();
     const uint32_t base_l = (uint32_t)s_base, base_r = (uint32_t)(s_base >> 32);
-    Entry *dst = order_out + start;
 #pragma unroll
     for (int k = 0; k < PART_PER_THREAD; ++k) {
         const uint32_t i = (uint32_t)(k * PART_THREADS + tid);
@@ -1899,6 +1841,41 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
         const uint32_t pos = x[k] ? base_l + le : cnt - 1u - (base_r + (i - le));
         dst[pos] = e[k];
     }
+}
+
+__global__ __launch_bounds__(PART_THREADS) void k_route(
+    Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
+    Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
+    const uint32_t *__restrict__ count, const TreeOut out, uint64_t *cursors,
+    int write_entries) {
+    extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
+    __shared__ uint32_t s_mask[8];
+    __shared__ uint32_t wave_tot[PART_WAVES + 1];
+    const uint32_t b = blockIdx.x;
+    // blocks per split node of the routed level, and their prefix
+    for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
+        const uint32_t nn = la.level_start + l;
+        const bool split = out.split[nn].feature >= 0 && count[nn] >= 1;
+        blk_prefix[l] = split ? (count[nn] + PART_BLOCK - 1) / PART_BLOCK : 0u;
+    }
+    __syncthreads();
+    const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
+    if (b >= total_blocks) return;                   // uniform per block
+    // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
+    uint32_t lo = 0, hi = la.num_level - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        if (blk_prefix[mid] <= b) lo = mid; else hi = mid - 1;
+    }
+    const uint32_t l = lo, n = la.level_start + l;
+    const uint32_t start = seg_start[l], cnt = count[n];
+    const uint32_t first = (b - blk_prefix[l]) * PART_BLOCK;
+    const NodeSplit sp = out.split[n];
+    if (threadIdx.x < 8) s_mask[threadIdx.x] = out.mask[(size_t)n * 8 + threadIdx.x];
+    __syncthreads();
+    route_block(sp, s_mask, sh.num_bins, bins_fm + (size_t)sp.feature * (size_t)sh.rows,
+                order_in + start + first, min((uint32_t)PART_BLOCK, cnt - first), cnt,
+                order_out + start, &cursors[(size_t)l * CURSOR_STRIDE], write_entries != 0);
 }
 
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
@@ -2128,10 +2105,13 @@ hipError_t launch_renew(hipStream_t s, const uint8_t *bins_fm, int64_t rows, int
 
 // ---------------------------------------------------------------------------
 // leaf-wise (best-first) growth: leaf_init (:683-716), leaf_pick_apply
-// (:720-871), leaf_step (:879-1091) and the stable segment partition
-// (partition_count/scan/scatter, :520-620).  Every step is a fixed chain of
-// launches that read the device state; once the tree is finished the chain
-// early-outs, so the host never waits inside a tree.
+// (:720-871), leaf_step (:879-1091) and the segment partition
+// (partition_count/scan/scatter, :520-620, here one pass like the level-wise
+// one: entry order inside a child is not kept, and nothing depends on it).
+// Every step is a fixed chain of launches (pick with the previous step's
+// evaluations, route, plan, histograms, reduce, split) that read the device
+// state; once the tree is finished the chain early-outs, so the host never
+// waits inside a tree.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ float lw_leaf_value(const SplitParams &sp, int64_t g, int64_t h,
@@ -2199,16 +2179,14 @@ hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeC
     return hipGetLastError();
 }
 
-// Best split of each newly evaluated leaf: argmax over features (strict '>',
-// lowest feature wins), one wavefront per leaf.
-__global__ __launch_bounds__(128) void k_lw_eval(Shape sh, SplitParams sp, LWArgs a,
-                                                 const LWState *st, LWOpen *open,
-                                                 const SplitResult *__restrict__ results,
-                                                 const int64_t *slot_g, const int64_t *slot_h,
-                                                 const TreeCtl *ctl, TreeOut out) {
-    (void)a;
-    const int w = threadIdx.x >> 6, lane = lane_id();
-    if (st->done || (uint32_t)w >= st->eval_count) return;
+// Best split of newly evaluated leaf eval_first + w: argmax over features
+// (strict '>', lowest feature wins), one wavefront per leaf.
+__device__ void lw_eval_leaf(int w, const Shape &sh, const SplitParams &sp, const LWState *st,
+                             LWOpen *open, const SplitResult *__restrict__ results,
+                             const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,
+                             const TreeOut &out) {
+    const int lane = lane_id();
+    if ((uint32_t)w >= st->eval_count) return;
     const uint32_t e = st->eval_first + (uint32_t)w;
     const int32_t slot = open[e].slot;
     if (slot < 0) return;
@@ -2239,27 +2217,50 @@ __global__ __launch_bounds__(128) void k_lw_eval(Shape sh, SplitParams sp, LWArg
     }
 }
 
-hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
+// The last step's evaluations (the root's, when the tree never splits).
+__global__ __launch_bounds__(128) void k_lw_eval(Shape sh, SplitParams sp, const LWState *st,
+                                                 LWOpen *open,
+                                                 const SplitResult *__restrict__ results,
+                                                 const int64_t *slot_g, const int64_t *slot_h,
+                                                 const TreeCtl *ctl, TreeOut out) {
+    if (st->done) return;
+    lw_eval_leaf(threadIdx.x >> 6, sh, sp, st, open, results, slot_g, slot_h, ctl, out);
+}
+
+hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp,
                           const LWState *st, LWOpen *open, const SplitResult *results,
                           const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,
                           const TreeOut out) {
-    hipLaunchKernelGGL(k_lw_eval, dim3(1), dim3(128), 0, s, sh, sp, a, st, open, results, slot_g,
+    hipLaunchKernelGGL(k_lw_eval, dim3(1), dim3(128), 0, s, sh, sp, st, open, results, slot_g,
                        slot_h, ctl, out);
     return hipGetLastError();
 }
 
-// Pick the open leaf with the largest gain > minSplitGain (lowest index wins),
-// write its split, its children's statistics, bounds and leaf values, and set
-// up the partition of its segment.
-__global__ __launch_bounds__(64) void k_lw_pick(SplitParams sp, LWArgs a, LWState *st,
-                                                LWOpen *open, const int8_t *monotone,
-                                                TreeCtl *ctl, TreeOut out) {
-    const int lane = lane_id();
+// Evaluate the leaves the previous step built, then pick the open leaf with
+// the largest gain > minSplitGain (lowest index wins), write its split, its
+// children's statistics, bounds and leaf values, and set up the partition of
+// its segment (the partition cursor starts at zero).
+__global__ __launch_bounds__(128) void k_lw_pick(Shape sh, SplitParams sp, LWArgs a, LWState *st,
+                                                 LWOpen *open,
+                                                 const SplitResult *__restrict__ results,
+                                                 const int64_t *slot_g, const int64_t *slot_h,
+                                                 const int8_t *monotone, TreeCtl *ctl,
+                                                 uint64_t *cursor, TreeOut out) {
+    const int lane = lane_id(), wv = threadIdx.x >> 6;
+    if (st->done) {
+        if (threadIdx.x == 0) {
+            ctl->num_items = 0;
+            ctl->num_pairs = 0;
+        }
+        return;
+    }
+    lw_eval_leaf(wv, sh, sp, st, open, results, slot_g, slot_h, ctl, out);
+    __syncthreads();
+    if (wv != 0) return;
     if (lane == 0) {
         ctl->num_items = 0;                          // nothing to build unless planned
         ctl->num_pairs = 0;
     }
-    if (st->done) return;
     if ((int32_t)st->leaves >= a.num_leaves) {
         if (lane == 0) st->done = 1;
         return;
@@ -2326,18 +2327,19 @@ __global__ __launch_bounds__(64) void k_lw_pick(SplitParams sp, LWArgs a, LWStat
     st->src = o.seg;
     st->dst = o.seg < a.rows ? o.seg + a.rows : o.seg - a.rows;
     st->count = o.count;
-    uint32_t chunk = (o.count + a.part_blocks - 1) / a.part_blocks;
-    chunk = (chunk + 255u) & ~255u;
-    st->chunk = chunk ? chunk : 256u;
+    *cursor = 0ull;
     st->feature = bf;
     st->bin = r.bin;
     st->flags = r.flags;
     for (int w = 0; w < 8; ++w) st->mask[w] = cat ? r.mask[w] : 0u;
 }
 
-hipError_t launch_lw_pick(hipStream_t s, const SplitParams &sp, const LWArgs &a, LWState *st,
-                          LWOpen *open, const int8_t *monotone, TreeCtl *ctl, const TreeOut out) {
-    hipLaunchKernelGGL(k_lw_pick, dim3(1), dim3(64), 0, s, sp, a, st, open, monotone, ctl, out);
+hipError_t launch_lw_pick(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
+                          LWState *st, LWOpen *open, const SplitResult *results,
+                          const int64_t *slot_g, const int64_t *slot_h, const int8_t *monotone,
+                          TreeCtl *ctl, uint64_t *cursor, const TreeOut out) {
+    hipLaunchKernelGGL(k_lw_pick, dim3(1), dim3(128), 0, s, sh, sp, a, st, open, results, slot_g,
+                       slot_h, monotone, ctl, cursor, out);
     return hipGetLastError();
 }
 
@@ -2355,67 +2357,16 @@ hipError_t launch_lw_bounds(hipStream_t s, const LWState *st, const LWOpen *open
     return hipGetLastError();
 }
 
-// Partition count: block b owns segment positions [b*chunk, (b+1)*chunk).
-constexpr int LW_PART_THREADS = 256;
-
-__global__ __launch_bounds__(LW_PART_THREADS) void k_lw_count(LWArgs a, const LWState *st,
-                                                             const uint8_t *__restrict__ bins_fm,
-                                                             const Entry *__restrict__ order,
-                                                             uint8_t *__restrict__ dir,
-                                                             uint32_t *block_left, int32_t nb) {
-    __shared__ uint32_t red[LW_PART_THREADS / 64];
-    __shared__ uint32_t s_mask[8];
-    if (st->done) return;
-    const uint32_t cnt = st->count, chunk = st->chunk;
-    const uint32_t start = blockIdx.x * chunk;
-    const int tid = threadIdx.x;
-    if (start >= cnt) {
-        if (tid == 0) block_left[blockIdx.x] = 0;
-        return;
-    }
-    const uint32_t end = min(start + chunk, cnt);
-    if (tid < 8) s_mask[tid] = st->mask[tid];
-    __syncthreads();
-    const NodeSplit ns = {st->feature, st->bin, st->flags};
-    const uint8_t *col = bins_fm + (size_t)ns.feature * a.rows;
-    const Entry *src = order + st->src;
-    uint32_t lefts = 0;
-    for (uint32_t j = start + (uint32_t)tid; j < end; j += LW_PART_THREADS) {
-        const uint32_t b = col[src[j].row];
-        const bool l = bin_goes_left(b, ns, nb, s_mask);
-        dir[j] = l ? 1 : 0;
-        lefts += l ? 1u : 0u;
-    }
-    lefts = wave_sum(lefts);
-    if (lane_id() == 0) red[tid >> 6] = lefts;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t t = 0;
-        for (int w = 0; w < LW_PART_THREADS / 64; ++w) t += red[w];
-        block_left[blockIdx.x] = t;
-    }
-}
-
-hipError_t launch_lw_count(hipStream_t s, const LWArgs &a, const LWState *st,
-                           const uint8_t *bins_fm, const Entry *order, uint8_t *dir,
-                           uint32_t *block_left, int32_t num_bins) {
-    hipLaunchKernelGGL(k_lw_count, dim3(a.part_blocks), dim3(LW_PART_THREADS), 0, s, a, st,
-                       bins_fm, order, dir, block_left, num_bins);
-    return hipGetLastError();
-}
-
-// Partition plan: block offsets, child segments and covers, whether the
-// children are evaluated, histogram slots and the smaller child's items.
-__global__ __launch_bounds__(1024) void k_lw_plan(Shape sh, LWArgs a, LWState *st, LWOpen *open,
-                                                  uint32_t *block_left, uint32_t *slot_seg,
-                                                  uint32_t *slot_count, TreeCtl *ctl,
-                                                  Pair *pairs, HistItem *items,
-                                                  uint32_t *scratch, TreeOut out) {
+// Partition plan, run by one 1024-thread block once the left count is known:
+// child segments and covers, whether the children are evaluated, histogram
+// slots and the smaller child's items.
+__device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWOpen *open,
+                              uint32_t left, uint32_t *slot_seg, uint32_t *slot_count,
+                              TreeCtl *ctl, Pair *pairs, HistItem *items, uint32_t *scratch,
+                              const TreeOut &out) {
     __shared__ uint32_t wave_tot[17];
     __shared__ uint32_t s_eval;
     __shared__ int32_t s_level;
-    if (st->done) return;
-    const uint32_t left = block_exclusive_scan(block_left, a.part_blocks, wave_tot);
     if (threadIdx.x == 0) {
         const uint32_t cnt = st->count, right = cnt - left;
         const LWOpen o = open[st->pick];
@@ -2466,65 +2417,62 @@ __global__ __launch_bounds__(1024) void k_lw_plan(Shape sh, LWArgs a, LWState *s
                     a.target_items, a.min_chunk, scratch, wave_tot, true);
 }
 
-hipError_t launch_lw_plan(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
-                          LWOpen *open, uint32_t *block_left, uint32_t *slot_seg,
-                          uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
-                          uint32_t *scratch, const TreeOut out) {
-    hipLaunchKernelGGL(k_lw_plan, dim3(1), dim3(1024), 0, s, sh, a, st, open, block_left,
-                       slot_seg, slot_count, ctl, pairs, items, scratch, out);
-    return hipGetLastError();
-}
-
-// Stable scatter of the segment into the other half: lefts first, then
-// rights, each in their original order.
-__global__ __launch_bounds__(LW_PART_THREADS) void k_lw_scatter(LWArgs a, const LWState *st,
-                                                               Entry *order,
-                                                               const uint8_t *__restrict__ dir,
-                                                               const uint32_t *block_left) {
-    __shared__ uint32_t wt[LW_PART_THREADS / 64 + 1];
-    (void)a;
+// Partition of the picked leaf's segment into the other half of the order
+// buffer, PART_BLOCK entries at a time (grid-stride: the grid is sized for
+// the largest segment, the root's, and most steps use a few blocks), lefts
+// from the front and rights from the back (route_block).  The cursor's low
+// word ends as the left count; the last block to finish (counted on
+// *done_blocks, which it resets) runs the plan.
+__global__ __launch_bounds__(PART_THREADS) void k_lw_route(Shape sh, LWArgs a, LWState *st,
+                                                          LWOpen *open,
+                                                          const uint8_t *__restrict__ bins_fm,
+                                                          Entry *order, uint64_t *cursor,
+                                                          uint32_t *done_blocks,
+                                                          uint32_t *slot_seg, uint32_t *slot_count,
+                                                          TreeCtl *ctl, Pair *pairs,
+                                                          HistItem *items, uint32_t *scratch,
+                                                          TreeOut out) {
+    __shared__ uint32_t s_mask[8];
+    __shared__ uint32_t s_last;
     if (st->done) return;
-    const uint32_t cnt = st->count, chunk = st->chunk;
-    const uint32_t start = blockIdx.x * chunk;
-    if (start >= cnt) return;
-    const uint32_t end = min(start + chunk, cnt);
-    const uint32_t left_base = block_left[blockIdx.x];      // lefts before this block
-    const uint32_t right_base = start - left_base;          // rights before this block
-    const uint32_t total_left = st->left;
-    const Entry *src = order + st->src;
-    Entry *dst = order + st->dst;
-    const int tid = threadIdx.x, w = tid >> 6;
-    uint32_t run = 0;                                        // lefts so far in this block
-    for (uint32_t base = start; base < end; base += LW_PART_THREADS) {
-        const uint32_t j = base + (uint32_t)tid;
-        const bool valid = j < end;
-        const uint32_t l = valid ? (uint32_t)dir[j] : 0u;
-        Entry e = {0u, 0u};
-        if (valid) e = src[j];
-        const uint32_t inc = wave_inclusive_scan(l);
-        if (lane_id() == 63) wt[w] = inc;
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t acc = 0;
-            for (int k = 0; k < LW_PART_THREADS / 64; ++k) { const uint32_t t = wt[k]; wt[k] = acc; acc += t; }
-            wt[LW_PART_THREADS / 64] = acc;
-        }
-        __syncthreads();
-        const uint32_t lefts_before = run + wt[w] + inc - l;
-        if (valid) {
-            const uint32_t pos = l ? left_base + lefts_before
-                                   : total_left + right_base + (j - start) - lefts_before;
-            dst[pos] = e;
-        }
-        run += wt[LW_PART_THREADS / 64];
-        __syncthreads();
+    const uint32_t cnt = st->count;
+    // blocks with work (at least one, so that the plan always runs)
+    const uint32_t active = max(1u, min(gridDim.x, (cnt + PART_BLOCK - 1) / PART_BLOCK));
+    if (blockIdx.x >= active) return;                // uniform per block
+    if (threadIdx.x < 8) s_mask[threadIdx.x] = st->mask[threadIdx.x];
+    __syncthreads();
+    const NodeSplit sp = {st->feature, st->bin, st->flags};
+    const uint8_t *col = bins_fm + (size_t)sp.feature * a.rows;
+    for (uint32_t first = blockIdx.x * (uint32_t)PART_BLOCK; first < cnt;
+         first += gridDim.x * (uint32_t)PART_BLOCK) {
+        route_block(sp, s_mask, sh.num_bins, col, order + st->src + first,
+                    min((uint32_t)PART_BLOCK, cnt - first), cnt, order + st->dst, cursor, true);
+        __syncthreads();                             // LDS reuse by the next chunk
     }
+    // This block's cursor add has returned (its result is in LDS) before the
+    // count below is issued, and the plan reads only the cursor, with an
+    // atomic: no fence is needed (an agent-scope fence would write back this
+    // XCD's L2, full of the entries just written).
+    if (threadIdx.x == 0) s_last = atomicAdd(done_blocks, 1u) == active - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!s_last) return;                             // uniform per block
+    __shared__ uint32_t s_left;
+    if (threadIdx.x == 0) {
+        s_left = (uint32_t)atomicAdd(reinterpret_cast<unsigned long long *>(cursor), 0ull);
+        *done_blocks = 0u;
+    }
+    __syncthreads();
+    lw_plan_block(sh, a, st, open, s_left, slot_seg, slot_count, ctl, pairs, items, scratch, out);
 }
 
-hipError_t launch_lw_scatter(hipStream_t s, const LWArgs &a, const LWState *st, Entry *order,
-                             const uint8_t *dir, const uint32_t *block_left) {
-    hipLaunchKernelGGL(k_lw_scatter, dim3(a.part_blocks), dim3(LW_PART_THREADS), 0, s, a, st,
-                       order, dir, block_left);
+hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
+                               LWOpen *open, const uint8_t *bins_fm, Entry *order,
+                               uint64_t *cursor, uint32_t *done_blocks, uint32_t *slot_seg,
+                               uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
+                               uint32_t *scratch, const TreeOut out) {
+    hipLaunchKernelGGL(k_lw_route, dim3(a.part_blocks), dim3(PART_THREADS), 0, s, sh, a, st, open,
+                       bins_fm, order, cursor, done_blocks, slot_seg, slot_count, ctl, pairs,
+                       items, scratch, out);
     return hipGetLastError();
 }
 

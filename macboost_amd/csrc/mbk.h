@@ -10,12 +10,7 @@ namespace mbk {
 constexpr uint32_t FLAG_DEFAULT_LEFT = 1u;
 constexpr uint32_t FLAG_CATEGORICAL = 2u;
 
-// Rows are routed by the level-wise partition in blocks of this many order
-// entries (256 threads x 8 entries).
-constexpr int ROUTE_THREADS = 256;
-constexpr int ROUTE_PER_THREAD = 8;
-constexpr int ROUTE_BLOCK = ROUTE_THREADS * ROUTE_PER_THREAD;
-constexpr int PART_ENTRIES = 8192;    // entries per level-wise partition block
+constexpr int PART_ENTRIES = 8192;    // entries per partition block
 constexpr int CURSOR_STRIDE = 16;     // u64 words per node cursor (one 128-B line each)
 
 // Packed histogram word: (sum of qg) << HIST_QH_BITS + (sum of qh), as a
@@ -296,7 +291,6 @@ struct LWState {
     uint32_t src;               // absolute first entry of the segment
     uint32_t dst;               // same range in the other half
     uint32_t count;             // rows in the segment
-    uint32_t chunk;             // rows per partition block (multiple of 256)
     uint32_t left;              // rows going left
     int32_t feature;
     uint32_t bin, flags;
@@ -307,7 +301,7 @@ struct LWArgs {
     int32_t num_leaves;         // L
     int32_t max_depth;          // D
     uint32_t rows;              // N (size of one half of the order buffer)
-    uint32_t part_blocks;       // partition grid
+    uint32_t part_blocks;       // partition grid (grid-stride over PART_ENTRIES chunks)
     int32_t total_nodes;        // heap nodes per tree
     uint32_t target_items, min_chunk;
     uint32_t pad;
@@ -317,23 +311,24 @@ hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeC
                           LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
                           Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out,
                           bool sampled);
-hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
+// the last step's evaluations (every other step's run inside the next pick)
+hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp,
                           const LWState *st, LWOpen *open, const SplitResult *results,
                           const int64_t *slot_g, const int64_t *slot_h, const TreeCtl *ctl,
                           const TreeOut out);
 hipError_t launch_lw_bounds(hipStream_t s, const LWState *st, const LWOpen *open,
                             float2 *bounds);
-hipError_t launch_lw_pick(hipStream_t s, const SplitParams &sp, const LWArgs &a, LWState *st,
-                          LWOpen *open, const int8_t *monotone, TreeCtl *ctl, const TreeOut out);
-hipError_t launch_lw_count(hipStream_t s, const LWArgs &a, const LWState *st,
-                           const uint8_t *bins_fm, const Entry *order, uint8_t *dir,
-                           uint32_t *block_left, int32_t num_bins);
-hipError_t launch_lw_plan(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
-                          LWOpen *open, uint32_t *block_left, uint32_t *slot_seg,
-                          uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
-                          uint32_t *scratch, const TreeOut out);
-hipError_t launch_lw_scatter(hipStream_t s, const LWArgs &a, const LWState *st, Entry *order,
-                             const uint8_t *dir, const uint32_t *block_left);
+hipError_t launch_lw_pick(hipStream_t s, const Shape &sh, const SplitParams &sp, const LWArgs &a,
+                          LWState *st, LWOpen *open, const SplitResult *results,
+                          const int64_t *slot_g, const int64_t *slot_h, const int8_t *monotone,
+                          TreeCtl *ctl, uint64_t *cursor, const TreeOut out);
+// partition of the picked leaf, then (in the last block) the plan of the
+// children; done_blocks must be zero before the first call and stays so
+hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
+                               LWOpen *open, const uint8_t *bins_fm, Entry *order,
+                               uint64_t *cursor, uint32_t *done_blocks, uint32_t *slot_seg,
+                               uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
+                               uint32_t *scratch, const TreeOut out);
 
 // Inference.
 struct ForestDev {

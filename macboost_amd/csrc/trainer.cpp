@@ -88,8 +88,7 @@ struct Trainer {
     DevBuf<uint8_t> is_cat, feat_mask;
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
-    DevBuf<uint8_t> dir;
-    DevBuf<uint32_t> block_left, gmax_part, goss_buckets;
+    DevBuf<uint32_t> gmax_part, goss_buckets;
     DevBuf<uint64_t> route_cursor;
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
@@ -118,13 +117,13 @@ struct Trainer {
     bool leafwise = false;
     mbk::LWArgs lw{};
     DevBuf<mbk::LWState> lw_state;
+    DevBuf<uint32_t> lw_done;   // leaf-wise partition: blocks finished (last one plans)
     DevBuf<mbk::LWOpen> lw_open;
     DevBuf<mbk::NodeSplit> m_split;
     DevBuf<float> m_leaf, m_gain, m_cover;
     DevBuf<uint32_t> m_mask;
     int capacity = 0, grown = 0;
     int hist_grid = 256, target_items = 512, min_chunk = 2048;
-    uint32_t max_blocks = 1;
     std::vector<std::vector<uint8_t>> tree_masks;
 
     bool profiling = false;
@@ -571,7 +570,6 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         t.order_a.alloc((size_t)rows);
         t.order_b.alloc((size_t)rows);
     }
-    t.dir.alloc((size_t)rows + 16);
     t.gmax_part.alloc(mbk::grad_max_scratch_words());
     if (p.goss || p.subsample < 1.0f) {
         t.goss_buckets.alloc(1024);
@@ -581,9 +579,6 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES) +
                    (uint32_t)t.max_level_nodes;
     t.route_cursor.alloc((size_t)t.max_level_nodes * mbk::CURSOR_STRIDE);
-    t.max_blocks = (uint32_t)((rows + mbk::ROUTE_BLOCK - 1) / mbk::ROUTE_BLOCK);
-    const uint32_t part_blocks = (uint32_t)std::min<int64_t>(1024, (rows + 255) / 256);
-    t.block_left.alloc(std::max<uint32_t>(t.max_blocks, part_blocks) + 1);
 
     // histogram work decomposition
     const size_t lds = mbk::hist_lds_size();
@@ -613,11 +608,14 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         t.lw.num_leaves = p.num_leaves;
         t.lw.max_depth = t.D;
         t.lw.rows = (uint32_t)rows;
-        t.lw.part_blocks = part_blocks;
+        t.lw.part_blocks = (uint32_t)std::min<int64_t>(
+            2 * t.dev->num_cus, (rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES);
         t.lw.total_nodes = t.total_nodes;
         t.lw.target_items = (uint32_t)t.target_items;
         t.lw.min_chunk = (uint32_t)t.min_chunk;
         t.lw_state.alloc(1);
+        t.lw_done.alloc(1);
+        MB_HIP(hipMemsetAsync(t.lw_done.ptr, 0, sizeof(uint32_t), s));
         t.lw_open.alloc((size_t)2 * p.num_leaves + 2);
     }
     t.renewal = p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE;
@@ -1009,7 +1007,7 @@ static void grow_leafwise(Trainer &t, int tree) {
     MB_HIP(mbk::launch_lw_init(s, sh, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
                                t.count.ptr, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out,
                                sampled));
-    auto build_and_eval = [&](int step) {
+    auto build = [&](int step) {
         hipEvent_t e0 = nullptr, e1 = nullptr;
         if (t.profiling) {
             MB_HIP(hipEventCreate(&e0));
@@ -1025,22 +1023,21 @@ static void grow_leafwise(Trainer &t, int tree) {
         MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, t.hist_a.ptr,
                                  t.hist_a.ptr, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
                                  t.count.ptr, t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
-        MB_HIP(mbk::launch_lw_eval(s, sh, t.sp, t.lw, t.lw_state.ptr, t.lw_open.ptr,
-                                   t.results.ptr, t.node_g.ptr, t.node_h.ptr, ctl, out));
     };
-    build_and_eval(0);
+    uint64_t *cursor = t.route_cursor.ptr;
+    build(0);
     for (int it = 1; it < t.p.num_leaves; ++it) {
-        MB_HIP(mbk::launch_lw_pick(s, t.sp, t.lw, t.lw_state.ptr, t.lw_open.ptr, t.mono.ptr, ctl,
-                                   out));
-        MB_HIP(mbk::launch_lw_count(s, t.lw, t.lw_state.ptr, t.bins_fm.ptr, order, t.dir.ptr,
-                                    t.block_left.ptr, t.nb));
-        MB_HIP(mbk::launch_lw_plan(s, sh, t.lw, t.lw_state.ptr, t.lw_open.ptr, t.block_left.ptr,
-                                   t.seg_a.ptr, t.count.ptr, ctl, t.pairs.ptr, t.items.ptr,
-                                   t.scratch.ptr, out));
-        MB_HIP(mbk::launch_lw_scatter(s, t.lw, t.lw_state.ptr, order, t.dir.ptr,
-                                      t.block_left.ptr));
-        build_and_eval(it);
+        // the previous build's leaves are evaluated inside the pick
+        MB_HIP(mbk::launch_lw_pick(s, sh, t.sp, t.lw, t.lw_state.ptr, t.lw_open.ptr,
+                                   t.results.ptr, t.node_g.ptr, t.node_h.ptr, t.mono.ptr, ctl,
+                                   cursor, out));
+        MB_HIP(mbk::launch_lw_partition(s, sh, t.lw, t.lw_state.ptr, t.lw_open.ptr, t.bins_fm.ptr,
+                                        order, cursor, t.lw_done.ptr, t.seg_a.ptr, t.count.ptr,
+                                        ctl, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out));
+        build(it);
     }
+    MB_HIP(mbk::launch_lw_eval(s, sh, t.sp, t.lw_state.ptr, t.lw_open.ptr, t.results.ptr,
+                               t.node_g.ptr, t.node_h.ptr, ctl, out));
     // training predictions: walk the finished tree on the binned rows
     // (predict_tree_binned, Shaders.swift:1763-1781)
     MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds_cur));
