@@ -1558,6 +1558,25 @@ __device__ uint32_t block_exclusive_scan(uint32_t *v, uint32_t n, uint32_t *wave
 }
 
 // level_built[level] records the built rows (added to, when accumulate).
+// Rows per histogram item for `total` built rows in num_pairs nodes.  At most
+// r items per workgroup of the grid (target_items): every (pair, tile) adds at
+// most one partial chunk, so reserve that slack (T * pairs) and pick the
+// smallest r whose chunk fits HIST_CHUNK_MAX.
+__device__ __forceinline__ uint32_t item_chunk(uint64_t total, uint32_t num_pairs,
+                                               int32_t num_tiles, uint32_t target_items,
+                                               uint32_t min_chunk) {
+    const uint64_t work = total * (uint64_t)num_tiles;
+    const uint64_t tgt = target_items ? target_items : 1;
+    const uint64_t slack = (uint64_t)num_pairs * (uint64_t)num_tiles;
+    const uint64_t need = (work + HIST_CHUNK_MAX - 1) / HIST_CHUNK_MAX;
+    uint64_t r = (slack + need + tgt - 1) / tgt;
+    if (tgt * r <= slack) r = slack / tgt + 1;
+    uint64_t c = (work + (tgt * r - slack) - 1) / (tgt * r - slack);
+    if (c < min_chunk) c = min_chunk;
+    if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
+    return (uint32_t)c;
+}
+
 __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pairs,
                             HistItem *items, const uint32_t *seg_start,
                             const uint32_t *count_level, uint32_t num_pairs,
@@ -1576,20 +1595,9 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     __syncthreads();
     if (tid == 0) {
         const uint64_t total = s_total;
-        // At most r items per workgroup of the grid (target_items): every
-        // (pair, tile) adds at most one partial chunk, so reserve that slack
-        // (T * pairs) and pick the smallest r whose chunk fits HIST_CHUNK_MAX.
-        const uint64_t work = total * (uint64_t)sh.num_tiles;
-        const uint64_t tgt = target_items ? target_items : 1;
-        const uint64_t slack = (uint64_t)num_pairs * (uint64_t)sh.num_tiles;
-        const uint64_t need = (work + HIST_CHUNK_MAX - 1) / HIST_CHUNK_MAX;
-        uint64_t r = (slack + need + tgt - 1) / tgt;
-        if (tgt * r <= slack) r = slack / tgt + 1;
-        uint64_t c = (work + (tgt * r - slack) - 1) / (tgt * r - slack);
-        if (c < min_chunk) c = min_chunk;
-        if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
-        s_chunk = (uint32_t)c;
-        ctl->chunk = (uint32_t)c;
+        const uint32_t c = item_chunk(total, num_pairs, sh.num_tiles, target_items, min_chunk);
+        s_chunk = c;
+        ctl->chunk = c;
         if (accumulate) ctl->level_built[level] += (uint32_t)total;
         else ctl->level_built[level] = (uint32_t)total;
         scratch[0] = 0;
@@ -1781,12 +1789,16 @@ static_assert(PART_SLICES % 64 == 0, "slice scan: whole slices per lane");
 // src go to the node's interval dst[0, cnt), lefts from the front and rights
 // from the back.  Both ranges are reserved with one packed 64-bit add on
 // *cursor (left count low, right count high; both < 2^32, so the low word
-// never carries).  s_mask is the split's category mask, in LDS.
-__device__ __forceinline__ void route_block(const NodeSplit sp, const uint32_t *s_mask, int32_t nb,
+// never carries).  s_mask is the split's category mask, in LDS.  With
+// write_entries, returns (in every thread) whether this block's add was the
+// one that reserved the node's last entries, and then the node's left count
+// in *left_total.
+__device__ __forceinline__ bool route_block(const NodeSplit sp, const uint32_t *s_mask, int32_t nb,
                                             const uint8_t *__restrict__ col,
                                             const Entry *__restrict__ src, uint32_t nvalid,
                                             uint32_t cnt, Entry *__restrict__ dst,
-                                            uint64_t *cursor, bool write_entries) {
+                                            uint64_t *cursor, bool write_entries,
+                                            uint32_t *left_total = nullptr) {
     __shared__ uint32_t tot[PART_SLICES + 1];
     __shared__ uint64_t s_base;
     const int tid = threadIdx.x, w = tid >> 6;
@@ -1830,7 +1842,7 @@ __device__ __forceinline__ void route_block(const NodeSplit sp, const uint32_t *
                                    ((unsigned long long)(nvalid - nl) << 32));
         }
     }
-    if (!write_entries) return;                      // counts only (terminal level)
+    if (!write_entries) return false;                // counts only (terminal level)
     __syncthreads();
     const uint32_t base_l = (uint32_t)s_base, base_r = (uint32_t)(s_base >> 32);
 #pragma unroll
@@ -1841,6 +1853,9 @@ __device__ __forceinline__ void route_block(const NodeSplit sp, const uint32_t *
         const uint32_t pos = x[k] ? base_l + le : cnt - 1u - (base_r + (i - le));
         dst[pos] = e[k];
     }
+    if (base_l + base_r + nvalid != cnt) return false;
+    if (left_total) *left_total = base_l + tot[PART_SLICES];
+    return true;
 }
 
 __global__ __launch_bounds__(PART_THREADS) void k_route(
@@ -2321,6 +2336,9 @@ __global__ __launch_bounds__(128) void k_lw_pick(Shape sh, SplitParams sp, LWArg
     open[bi].best_f = -1;
     open[bi].best.gain = -INFINITY;
     st->pick = (uint32_t)bi;
+    st->pick_node = n;
+    st->pick_depth = o.depth;
+    st->pick_slot = o.slot;
     st->child0 = i0;
     st->open_count = n_open + 2;
     st->eval_count = 0;
@@ -2357,122 +2375,135 @@ hipError_t launch_lw_bounds(hipStream_t s, const LWState *st, const LWOpen *open
     return hipGetLastError();
 }
 
-// Partition plan, run by one 1024-thread block once the left count is known:
-// child segments and covers, whether the children are evaluated, histogram
-// slots and the smaller child's items.
+// Partition plan, run by one block once the left count is known: child
+// segments and covers, whether the children are evaluated, histogram slots
+// and the smaller child's items (write_items for one pair: same chunking,
+// computed by one thread from the step state the pick wrote).
 __device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWOpen *open,
                               uint32_t left, uint32_t *slot_seg, uint32_t *slot_count,
-                              TreeCtl *ctl, Pair *pairs, HistItem *items, uint32_t *scratch,
-                              const TreeOut &out) {
-    __shared__ uint32_t wave_tot[17];
-    __shared__ uint32_t s_eval;
-    __shared__ int32_t s_level;
+                              TreeCtl *ctl, Pair *pairs, HistItem *items, const TreeOut &out) {
+    __shared__ uint32_t s_n, s_seg, s_cnt, s_chunk;
     if (threadIdx.x == 0) {
-        const uint32_t cnt = st->count, right = cnt - left;
-        const LWOpen o = open[st->pick];
-        const uint32_t i0 = st->child0, i1 = i0 + 1;
-        const int32_t lc = 2 * o.node + 1, rc = 2 * o.node + 2;
+        const LWState q = *st;
+        const uint32_t cnt = q.count, right = cnt - left;
+        const uint32_t i0 = q.child0, i1 = i0 + 1;
+        const int32_t lc = 2 * q.pick_node + 1, rc = lc + 1;
         out.cover[lc] = (float)left;
         out.cover[rc] = (float)right;
-        open[i0].seg = st->dst;
+        open[i0].seg = q.dst;
         open[i0].count = left;
-        open[i1].seg = st->dst + left;
+        open[i1].seg = q.dst + left;
         open[i1].count = right;
         st->left = left;
-        const int32_t child_depth = o.depth + 1;
+        const int32_t child_depth = q.pick_depth + 1;
         const bool can_eval = child_depth < a.max_depth &&
-                              (int32_t)st->leaves + 1 < a.num_leaves && left > 0 && right > 0;
-        st->leaves += 1;
-        s_eval = can_eval ? 1u : 0u;
-        s_level = child_depth;
+                              (int32_t)q.leaves + 1 < a.num_leaves && left > 0 && right > 0;
+        st->leaves = q.leaves + 1;
+        s_n = 0;
         if (can_eval) {
             // the smaller child (ties: left) gets a new slot; the larger one
             // takes over the parent's slot (parent - smaller, in place)
             const bool small_left = left <= right;
-            const uint32_t s_new = st->next_slot++;
-            const uint32_t s_par = (uint32_t)o.slot;
+            const uint32_t s_new = q.next_slot, s_par = (uint32_t)q.pick_slot;
+            st->next_slot = s_new + 1;
             const uint32_t is = small_left ? i0 : i1, il = small_left ? i1 : i0;
+            const uint32_t seg_s = small_left ? q.dst : q.dst + left;
+            const uint32_t cnt_s = small_left ? left : right;
             open[is].slot = (int32_t)s_new;
             open[il].slot = (int32_t)s_par;
-            slot_seg[s_new] = open[is].seg;
-            slot_count[s_new] = open[is].count;
-            slot_seg[s_par] = open[il].seg;
-            slot_count[s_par] = open[il].count;
+            slot_seg[s_new] = seg_s;
+            slot_count[s_new] = cnt_s;
+            slot_seg[s_par] = small_left ? q.dst + left : q.dst;
+            slot_count[s_par] = cnt - cnt_s;
+            st->eval_first = i0;
+            st->eval_count = 2;
+            const uint32_t chunk = item_chunk(cnt_s, 1, sh.num_tiles, a.target_items, a.min_chunk);
+            const uint32_t nch = (cnt_s + chunk - 1) / chunk;
+            const uint32_t n_items = nch * (uint32_t)sh.num_tiles;
             Pair p = {};
             p.built = s_new;
             p.derived = s_par;
             p.parent = s_par;
-            pairs[0] = p;
+            ctl->chunk = chunk;
+            ctl->level_built[min(child_depth, 15)] += cnt_s;
             ctl->num_pairs = 1;
-            st->eval_first = i0;
-            st->eval_count = 2;
+            if (n_items > sh.item_cap) {
+                // never write past the item list (reported after the tree)
+                ctl->num_items = 0;
+                ctl->overflow = 1;
+            } else {
+                p.item_first = 0;
+                p.nchunks = nch;
+                ctl->num_items = n_items;
+                s_n = n_items;
+            }
+            pairs[0] = p;
+            s_seg = seg_s;
+            s_cnt = cnt_s;
+            s_chunk = chunk;
         } else {
             st->eval_count = 0;
         }
-        scratch[0] = 0;
     }
     __syncthreads();
-    if (s_eval)
-        write_items(sh, ctl, min(s_level, 15), pairs, items, slot_seg, slot_count, 1,
-                    a.target_items, a.min_chunk, scratch, wave_tot, true);
+    const uint32_t n = s_n, T = (uint32_t)sh.num_tiles;
+    for (uint32_t it = threadIdx.x; it < n; it += blockDim.x) {
+        const uint32_t t = it % T, c = it / T;
+        HistItem h;
+        h.pair = 0;
+        h.tile = t;
+        h.start = s_seg + c * s_chunk;
+        h.count = min(s_chunk, s_cnt - c * s_chunk);
+        items[it] = h;
+    }
 }
 
 // Partition of the picked leaf's segment into the other half of the order
 // buffer, PART_BLOCK entries at a time (grid-stride: the grid is sized for
 // the largest segment, the root's, and most steps use a few blocks), lefts
-// from the front and rights from the back (route_block).  The cursor's low
-// word ends as the left count; the last block to finish (counted on
-// *done_blocks, which it resets) runs the plan.
+// from the front and rights from the back (route_block).  The block whose
+// cursor add reserves the segment's last entries knows the left count from
+// that add and runs the plan once its own entries are written; the plan
+// reads nothing that another block of this launch writes.
 __global__ __launch_bounds__(PART_THREADS) void k_lw_route(Shape sh, LWArgs a, LWState *st,
                                                           LWOpen *open,
                                                           const uint8_t *__restrict__ bins_fm,
                                                           Entry *order, uint64_t *cursor,
-                                                          uint32_t *done_blocks,
                                                           uint32_t *slot_seg, uint32_t *slot_count,
                                                           TreeCtl *ctl, Pair *pairs,
-                                                          HistItem *items, uint32_t *scratch,
-                                                          TreeOut out) {
+                                                          HistItem *items, TreeOut out) {
     __shared__ uint32_t s_mask[8];
-    __shared__ uint32_t s_last;
     if (st->done) return;
     const uint32_t cnt = st->count;
-    // blocks with work (at least one, so that the plan always runs)
-    const uint32_t active = max(1u, min(gridDim.x, (cnt + PART_BLOCK - 1) / PART_BLOCK));
-    if (blockIdx.x >= active) return;                // uniform per block
+    if (cnt == 0) {                                  // nothing to move: plan directly
+        if (blockIdx.x == 0)
+            lw_plan_block(sh, a, st, open, 0u, slot_seg, slot_count, ctl, pairs, items, out);
+        return;
+    }
+    if (blockIdx.x * (uint32_t)PART_BLOCK >= cnt) return;   // uniform per block
     if (threadIdx.x < 8) s_mask[threadIdx.x] = st->mask[threadIdx.x];
     __syncthreads();
     const NodeSplit sp = {st->feature, st->bin, st->flags};
     const uint8_t *col = bins_fm + (size_t)sp.feature * a.rows;
+    bool last = false;
+    uint32_t left = 0;
     for (uint32_t first = blockIdx.x * (uint32_t)PART_BLOCK; first < cnt;
          first += gridDim.x * (uint32_t)PART_BLOCK) {
-        route_block(sp, s_mask, sh.num_bins, col, order + st->src + first,
-                    min((uint32_t)PART_BLOCK, cnt - first), cnt, order + st->dst, cursor, true);
+        if (route_block(sp, s_mask, sh.num_bins, col, order + st->src + first,
+                        min((uint32_t)PART_BLOCK, cnt - first), cnt, order + st->dst, cursor,
+                        true, &left))
+            last = true;                             // uniform per block
         __syncthreads();                             // LDS reuse by the next chunk
     }
-    // This block's cursor add has returned (its result is in LDS) before the
-    // count below is issued, and the plan reads only the cursor, with an
-    // atomic: no fence is needed (an agent-scope fence would write back this
-    // XCD's L2, full of the entries just written).
-    if (threadIdx.x == 0) s_last = atomicAdd(done_blocks, 1u) == active - 1 ? 1u : 0u;
-    __syncthreads();
-    if (!s_last) return;                             // uniform per block
-    __shared__ uint32_t s_left;
-    if (threadIdx.x == 0) {
-        s_left = (uint32_t)atomicAdd(reinterpret_cast<unsigned long long *>(cursor), 0ull);
-        *done_blocks = 0u;
-    }
-    __syncthreads();
-    lw_plan_block(sh, a, st, open, s_left, slot_seg, slot_count, ctl, pairs, items, scratch, out);
+    if (last) lw_plan_block(sh, a, st, open, left, slot_seg, slot_count, ctl, pairs, items, out);
 }
 
 hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
                                LWOpen *open, const uint8_t *bins_fm, Entry *order,
-                               uint64_t *cursor, uint32_t *done_blocks, uint32_t *slot_seg,
-                               uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
-                               uint32_t *scratch, const TreeOut out) {
+                               uint64_t *cursor, uint32_t *slot_seg, uint32_t *slot_count,
+                               TreeCtl *ctl, Pair *pairs, HistItem *items, const TreeOut out) {
     hipLaunchKernelGGL(k_lw_route, dim3(a.part_blocks), dim3(PART_THREADS), 0, s, sh, a, st, open,
-                       bins_fm, order, cursor, done_blocks, slot_seg, slot_count, ctl, pairs,
-                       items, scratch, out);
+                       bins_fm, order, cursor, slot_seg, slot_count, ctl, pairs, items, out);
     return hipGetLastError();
 }
 

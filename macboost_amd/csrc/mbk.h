@@ -284,6 +284,7 @@ struct LWState {
     uint32_t open_count;        // entries used in the open list
     uint32_t next_slot;         // next free histogram slot
     uint32_t pick;              // open entry split in this step
+    int32_t pick_node, pick_depth, pick_slot;   // its heap node, depth and slot
     uint32_t child0;            // open entry of the left child (right = child0 + 1)
     uint32_t eval_first;        // open entries whose best split the eval step fills
     uint32_t eval_count;
@@ -322,13 +323,12 @@ hipError_t launch_lw_pick(hipStream_t s, const Shape &sh, const SplitParams &sp,
                           LWState *st, LWOpen *open, const SplitResult *results,
                           const int64_t *slot_g, const int64_t *slot_h, const int8_t *monotone,
                           TreeCtl *ctl, uint64_t *cursor, const TreeOut out);
-// partition of the picked leaf, then (in the last block) the plan of the
-// children; done_blocks must be zero before the first call and stays so
+// partition of the picked leaf, then (in the block that completes it) the
+// plan of the children
 hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
                                LWOpen *open, const uint8_t *bins_fm, Entry *order,
-                               uint64_t *cursor, uint32_t *done_blocks, uint32_t *slot_seg,
-                               uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
-                               uint32_t *scratch, const TreeOut out);
+                               uint64_t *cursor, uint32_t *slot_seg, uint32_t *slot_count,
+                               TreeCtl *ctl, Pair *pairs, HistItem *items, const TreeOut out);
 
 // Inference.
 struct ForestDev {

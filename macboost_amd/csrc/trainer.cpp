@@ -117,7 +117,6 @@ struct Trainer {
     bool leafwise = false;
     mbk::LWArgs lw{};
     DevBuf<mbk::LWState> lw_state;
-    DevBuf<uint32_t> lw_done;   // leaf-wise partition: blocks finished (last one plans)
     DevBuf<mbk::LWOpen> lw_open;
     DevBuf<mbk::NodeSplit> m_split;
     DevBuf<float> m_leaf, m_gain, m_cover;
@@ -614,8 +613,6 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         t.lw.target_items = (uint32_t)t.target_items;
         t.lw.min_chunk = (uint32_t)t.min_chunk;
         t.lw_state.alloc(1);
-        t.lw_done.alloc(1);
-        MB_HIP(hipMemsetAsync(t.lw_done.ptr, 0, sizeof(uint32_t), s));
         t.lw_open.alloc((size_t)2 * p.num_leaves + 2);
     }
     t.renewal = p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE;
@@ -1032,8 +1029,8 @@ static void grow_leafwise(Trainer &t, int tree) {
                                    t.results.ptr, t.node_g.ptr, t.node_h.ptr, t.mono.ptr, ctl,
                                    cursor, out));
         MB_HIP(mbk::launch_lw_partition(s, sh, t.lw, t.lw_state.ptr, t.lw_open.ptr, t.bins_fm.ptr,
-                                        order, cursor, t.lw_done.ptr, t.seg_a.ptr, t.count.ptr,
-                                        ctl, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out));
+                                        order, cursor, t.seg_a.ptr, t.count.ptr,
+                                        ctl, t.pairs.ptr, t.items.ptr, out));
         build(it);
     }
     MB_HIP(mbk::launch_lw_eval(s, sh, t.sp, t.lw_state.ptr, t.lw_open.ptr, t.results.ptr,
