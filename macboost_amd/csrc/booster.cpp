@@ -377,14 +377,14 @@ std::vector<float> Booster::contrib_class(const float *x, int64_t rows, int64_t 
     MB_HIP(hipMemcpyAsync(ed.ptr, elems.data(), ed.bytes(), hipMemcpyHostToDevice, d.stream));
     MB_HIP(hipMemcpyAsync(ud.ptr, uniq.data(), ud.bytes(), hipMemcpyHostToDevice, d.stream));
     DevBuf<double> phi;
-    if (cols > mbk::treeshap_lds_max_cols()) {
+    if (mbk::treeshap_needs_scratch((int)cols))
         phi.alloc((size_t)((rows + 63) / 64) * 64 * (size_t)cols);
-    } else {
-        MB_HIP(mbk::treeshap_set_lds_limit((int)cols));
-    }
+    int32_t max_elems = 1;
+    for (const mbk::ShapPath &P : paths) max_elems = std::max(max_elems, P.num_elem);
     MB_HIP(mbk::launch_treeshap(d.stream, xd.ptr, rows, (int)cols, trained_num_bins - 1,
                                 forest.has_mask ? forest.mask.ptr : nullptr, pd.ptr,
-                                (int)paths.size(), ed.ptr, ud.ptr, bias, od.ptr, phi.ptr));
+                                (int)paths.size(), max_elems, ed.ptr, ud.ptr, bias, od.ptr,
+                                phi.ptr));
     MB_HIP(hipMemcpyAsync(out.data(), od.ptr, od.bytes(), hipMemcpyDeviceToHost, d.stream));
     MB_HIP(hipStreamSynchronize(d.stream));
     return out;

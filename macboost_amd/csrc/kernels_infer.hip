@@ -167,6 +167,9 @@ hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows
 
 constexpr int SHAP_MAX_U = 12;                         // maxDepth <= 12
 
+// Lane-per-row TreeSHAP for wide data (more columns than k_treeshap_rows
+// keeps in LDS): every lane walks all paths for its row, phi in a global
+// [blocks][cols][64] fp64 scratch.
 __global__ __launch_bounds__(64) void k_treeshap(const float *__restrict__ x, int64_t rows,
                                                  int32_t cols, int32_t data_bins,
                                                  const uint32_t *__restrict__ masks,
@@ -176,12 +179,11 @@ __global__ __launch_bounds__(64) void k_treeshap(const float *__restrict__ x, in
                                                  const ShapUniq *__restrict__ uniq, float bias,
                                                  float *__restrict__ out,
                                                  double *__restrict__ phi_global) {
-    extern __shared__ double phi_lds[];                // [cols][64] when phi_global is null
     const int lane = threadIdx.x;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
     const bool valid = i < rows;
     const int64_t irow = valid ? i : 0;
-    double *phi = phi_global ? phi_global + (int64_t)blockIdx.x * 64 * cols : phi_lds;
+    double *phi = phi_global + (int64_t)blockIdx.x * 64 * cols;   // this block's [cols][64]
     for (int f = 0; f < cols; ++f) phi[f * 64 + lane] = 0.0;
     for (int32_t p = 0; p < num_paths; ++p) {
         const ShapPath P = paths[p];
@@ -260,24 +262,145 @@ __global__ __launch_bounds__(64) void k_treeshap(const float *__restrict__ x, in
     orow[cols] = bias;
 }
 
+// Path-parallel TreeSHAP: one wavefront per row (grid-stride), one lane per
+// root-to-leaf path, 64 paths per pass.  The row's feature values and its phi
+// sit in LDS; each lane runs the same fp64 EXTEND/UNWIND as k_treeshap for its
+// path and adds its unique features' contributions to phi with ds_add_f64.
+// One wavefront owns a row's phi, so the order of the adds is fixed (pass
+// order, then the LDS unit's lane order) and the output is deterministic.
+template <int MAXU>
+__global__ __launch_bounds__(64) void k_treeshap_rows(const float *__restrict__ x, int64_t rows,
+                                                      int32_t cols, int32_t data_bins,
+                                                      const uint32_t *__restrict__ masks,
+                                                      const ShapPath *__restrict__ paths,
+                                                      int32_t num_paths,
+                                                      const ShapElem *__restrict__ elems,
+                                                      const ShapUniq *__restrict__ uniq,
+                                                      float bias, float *__restrict__ out) {
+    extern __shared__ double row_lds[];                // phi [cols], then x [cols] as f32
+    double *phi = row_lds;
+    float *xr = reinterpret_cast<float *>(row_lds + cols);
+    const int lane = threadIdx.x;
+    for (int64_t i = blockIdx.x; i < rows; i += gridDim.x) {
+        for (int f = lane; f < cols; f += 64) {
+            xr[f] = x[(int64_t)f * rows + i];
+            phi[f] = 0.0;
+        }
+        __syncthreads();
+        for (int32_t c = 0; c < num_paths; c += 64) {
+            const int32_t p = c + lane;
+            if (p >= num_paths) continue;
+            const ShapPath P = paths[p];
+            const int U = P.num_uniq;
+            // one[u] is a product of 0/1 indicators: held as bit u of `ones`
+            double zero[MAXU];
+            int feat[MAXU];
+#pragma unroll
+            for (int u = 0; u < MAXU; ++u) {
+                zero[u] = 1.0;
+                feat[u] = 0;
+                if (u < U) {
+                    const ShapUniq q = uniq[P.uniq_start + u];
+                    zero[u] = q.zero;
+                    feat[u] = q.feature;
+                }
+            }
+            uint32_t ones = (1u << MAXU) - 1u;
+#pragma unroll
+            for (int e = 0; e < MAXU; ++e) {
+                if (e >= P.num_elem) break;
+                const ShapElem el = elems[P.elem_start + e];
+                const bool left = raw_goes_left(xr[el.feature], el.flags, el.threshold,
+                                                masks ? masks + (int64_t)el.node * 8 : nullptr,
+                                                data_bins);
+                if (left != ((el.flags & 0x100u) != 0)) ones &= ~(1u << el.uniq);
+            }
+            double one[MAXU];
+#pragma unroll
+            for (int u = 0; u < MAXU; ++u) one[u] = ((ones >> u) & 1u) ? 1.0 : 0.0;
+            // EXTEND with the dummy element at index 0 (SHAP.swift:266-279)
+            double pw[MAXU + 1];
+            pw[0] = 1.0;
+#pragma unroll
+            for (int j = 1; j <= MAXU; ++j) {
+                pw[j] = 0.0;
+                if (j <= U) {
+                    const double o = one[j - 1], z = zero[j - 1];
+#pragma unroll
+                    for (int q = j - 1; q >= 0; --q) {
+                        pw[q + 1] += o * pw[q] * (double)(q + 1) / (double)(j + 1);
+                        pw[q] = z * pw[q] * (double)(j - q) / (double)(j + 1);
+                    }
+                }
+            }
+            // unwound sums per unique feature (SHAP.swift:307-325)
+#pragma unroll
+            for (int u = 0; u < MAXU; ++u) {
+                if (u < U) {
+                    const double o = one[u], z = zero[u];
+                    double total = 0.0;
+                    if (o != 0.0) {
+                        double next = 0.0;
+#pragma unroll
+                        for (int q = MAXU; q >= 0; --q)
+                            if (q == U) next = pw[q];
+#pragma unroll
+                        for (int q = MAXU - 1; q >= 0; --q) {
+                            if (q < U) {
+                                const double tmp = next / ((double)(q + 1) * o);
+                                total += tmp;
+                                next = pw[q] - tmp * z * (double)(U - q);
+                            }
+                        }
+                    } else if (z != 0.0) {
+#pragma unroll
+                        for (int q = MAXU - 1; q >= 0; --q)
+                            if (q < U) total += pw[q] / (z * (double)(U - q));
+                    }
+                    atomicAdd(&phi[feat[u]], total * (double)(U + 1) * (o - z) * P.leaf);
+                }
+            }
+        }
+        __syncthreads();
+        float *orow = out + i * (int64_t)(cols + 1);
+        for (int f = lane; f < cols; f += 64) orow[f] = (float)phi[f];
+        if (lane == 0) orow[cols] = bias;
+        __syncthreads();                               // before the next row reuses the LDS
+    }
+}
+
+// Columns up to which k_treeshap_rows runs (12 B of LDS per column).
+constexpr int SHAP_ROW_MAX_COLS = 4096;
+
+bool treeshap_needs_scratch(int cols) { return cols > SHAP_ROW_MAX_COLS; }
+
 hipError_t launch_treeshap(hipStream_t s, const float *x, int64_t rows, int32_t cols,
                            int32_t data_bins, const uint32_t *masks, const ShapPath *paths,
-                           int32_t num_paths, const ShapElem *elems, const ShapUniq *uniq,
-                           float bias, float *out, double *phi_global) {
+                           int32_t num_paths, int32_t max_elems, const ShapElem *elems,
+                           const ShapUniq *uniq, float bias, float *out, double *phi_global) {
     if (rows <= 0) return hipSuccess;
+    if (max_elems < 1 || max_elems > SHAP_MAX_U) return hipErrorInvalidValue;
+    if (!treeshap_needs_scratch(cols)) {
+        // the per-lane path arrays sized to the longest path: fewer registers,
+        // more wavefronts per SIMD
+        const unsigned blocks = (unsigned)std::min<int64_t>(rows, (int64_t)1 << 22);
+        const size_t lds = (size_t)cols * (sizeof(double) + sizeof(float));
+#define MBK_SHAP_ROWS(U)                                                                        \
+        hipLaunchKernelGGL(k_treeshap_rows<U>, dim3(blocks), dim3(64), lds, s, x, rows, cols,   \
+                           data_bins, masks, paths, num_paths, elems, uniq, bias, out)
+        if (max_elems <= 4) MBK_SHAP_ROWS(4);
+        else if (max_elems <= 6) MBK_SHAP_ROWS(6);
+        else if (max_elems <= 8) MBK_SHAP_ROWS(8);
+        else MBK_SHAP_ROWS(SHAP_MAX_U);
+#undef MBK_SHAP_ROWS
+        return hipGetLastError();
+    }
+    if (!phi_global) return hipErrorInvalidValue;      // wide data: phi in the caller's scratch
     const unsigned blocks = (unsigned)((rows + 63) / 64);
-    const size_t lds = phi_global ? 0 : (size_t)cols * 64 * sizeof(double);
-    hipLaunchKernelGGL(k_treeshap, dim3(blocks), dim3(64), lds, s, x, rows, cols, data_bins, masks,
+    hipLaunchKernelGGL(k_treeshap, dim3(blocks), dim3(64), 0, s, x, rows, cols, data_bins, masks,
                        paths, num_paths, elems, uniq, bias, out, phi_global);
     return hipGetLastError();
 }
 
-// Largest column count whose per-lane phi slices fit in LDS.
-int treeshap_lds_max_cols() { return (int)(160 * 1024 / (64 * sizeof(double))) - 1; }
-
-hipError_t treeshap_set_lds_limit(int cols) {
-    return hipFuncSetAttribute((const void *)k_treeshap, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               cols * 64 * (int)sizeof(double));
-}
 
 }  // namespace mbk

@@ -375,13 +375,13 @@ struct ShapUniq {
     int32_t pad;
     double zero;          // product of cover fractions along the path
 };
-// phi_global: NULL to keep each lane's phi slice in LDS (cols <=
-// treeshap_lds_max_cols()), else a [ceil(rows/64)][cols][64] double scratch.
+// max_elems: the longest path's element count (1..12).  phi_global: a
+// [ceil(rows/64)][cols][64] double scratch when treeshap_needs_scratch(cols)
+// (wide data), else unused (may be NULL).
 hipError_t launch_treeshap(hipStream_t s, const float *x, int64_t rows, int32_t cols,
                            int32_t data_bins, const uint32_t *masks, const ShapPath *paths,
-                           int32_t num_paths, const ShapElem *elems, const ShapUniq *uniq,
-                           float bias, float *out, double *phi_global);
-int treeshap_lds_max_cols();
-hipError_t treeshap_set_lds_limit(int cols);
+                           int32_t num_paths, int32_t max_elems, const ShapElem *elems,
+                           const ShapUniq *uniq, float bias, float *out, double *phi_global);
+bool treeshap_needs_scratch(int cols);
 
 }  // namespace mbk
