@@ -746,11 +746,12 @@ def _mixed(rows, seed_a=211, seed_b=212, nan_frac=0.15):
     return x, y
 
 
-@pytest.mark.parametrize("depth", [6, 12])
+@pytest.mark.parametrize("depth", [3, 6, 8, 12])
 def test_treeshap_matches_oracle(depth):
-    # ObjectiveTests.swift:440-478 (tolerance tightened from 5e-3 abs)
+    # ObjectiveTests.swift:440-478 (tolerance tightened from 5e-3 abs); the
+    # depths cover every per-lane array size of the path-parallel kernel
     x, y = _mixed(3000)
-    h, obj = gpu_fit(x, y, {"num_trees": 40 if depth == 6 else 8, "max_depth": depth,
+    h, obj = gpu_fit(x, y, {"num_trees": 40 if depth <= 8 else 8, "max_depth": depth,
                             "categorical_features": [6]})
     c = mb.predict_contrib(h, x, feature_major=True)
     forest = model_io.forest_from_json(obj)
@@ -758,3 +759,15 @@ def test_treeshap_matches_oracle(depth):
     assert np.allclose(c, want, rtol=1e-5, atol=1e-6)
     raw = mb.predict(h, x, feature_major=True)
     assert np.max(np.abs(c.astype(np.float64).sum(axis=1) - raw)) < 1e-4
+
+
+def test_treeshap_wide_data_matches_oracle():
+    # more columns than the path-parallel kernel keeps in LDS: the lane-per-row
+    # kernel with its global phi scratch
+    rows, cols = 1200, 4100
+    x, y = O.friedman(rows, cols, 37)
+    h, obj = gpu_fit(x, y, {"num_trees": 6, "max_depth": 4})
+    c = mb.predict_contrib(h, x, feature_major=True)
+    assert c.shape == (rows, cols + 1)
+    want = O.treeshap(model_io.forest_from_json(obj), obj["baseScore"], obj["numBins"], x)
+    assert np.allclose(c, want, rtol=1e-5, atol=1e-6)
