@@ -287,27 +287,29 @@ double Booster::shap_bias(int k) const {
 // Root-to-leaf path decomposition (extractShapPaths, SHAP.swift:79-114), with
 // each path's repeated features merged into unique slots.
 // Contributions [rows][K][cols + 1]: class k from its own trees and bias.
-std::vector<float> Booster::predict_contrib(const float *x, int64_t rows, int64_t cols) {
+void Booster::predict_contrib(const float *x, int64_t rows, int64_t cols, float *out) {
     const int K = std::max(1, trained_num_classes);
-    if (K == 1) return contrib_class(x, rows, cols, 0);
+    if (K == 1) {
+        contrib_class(x, rows, cols, 0, out);
+        return;
+    }
     const int64_t width = cols + 1;
-    std::vector<float> out((size_t)std::max<int64_t>(rows, 0) * (size_t)K * (size_t)width, 0.0f);
+    std::vector<float> c((size_t)std::max<int64_t>(rows, 0) * (size_t)width);
     for (int k = 0; k < K; ++k) {
-        const std::vector<float> c = contrib_class(x, rows, cols, k);
+        contrib_class(x, rows, cols, k, c.data());
         for (int64_t i = 0; i < rows; ++i)
-            std::memcpy(&out[(size_t)((i * K + k) * width)], &c[(size_t)(i * width)],
+            std::memcpy(out + (size_t)((i * K + k) * width), &c[(size_t)(i * width)],
                         (size_t)width * sizeof(float));
     }
-    return out;
 }
 
-// TreeSHAP of the trees of class k (every tree when K = 1): [rows][cols + 1].
-std::vector<float> Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k) {
+// TreeSHAP of the trees of class k (every tree when K = 1) into out
+// [rows][cols + 1].
+void Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k, float *out) {
     const int K = std::max(1, trained_num_classes);
     const int64_t width = cols + 1;
-    std::vector<float> out((size_t)std::max<int64_t>(rows, 0) * (size_t)width, 0.0f);
     const float bias = (float)shap_bias(k);
-    if (rows <= 0) return out;
+    if (rows <= 0) return;
     build_forest();
     std::vector<mbk::ShapPath> paths;
     std::vector<mbk::ShapElem> elems;
@@ -364,8 +366,11 @@ std::vector<float> Booster::contrib_class(const float *x, int64_t rows, int64_t 
         }
     }
     if (paths.empty()) {
-        for (int64_t i = 0; i < rows; ++i) out[(size_t)(i * width + cols)] = bias;
-        return out;
+        for (int64_t i = 0; i < rows; ++i) {
+            std::fill(out + (size_t)(i * width), out + (size_t)(i * width + cols), 0.0f);
+            out[(size_t)(i * width + cols)] = bias;
+        }
+        return;
     }
     Device &d = device();
     DevBuf<float> xd((size_t)rows * (size_t)cols), od((size_t)rows * (size_t)width);
@@ -385,9 +390,8 @@ std::vector<float> Booster::contrib_class(const float *x, int64_t rows, int64_t 
                                 forest.has_mask ? forest.mask.ptr : nullptr, pd.ptr,
                                 (int)paths.size(), max_elems, ed.ptr, ud.ptr, bias, od.ptr,
                                 phi.ptr));
-    MB_HIP(hipMemcpyAsync(out.data(), od.ptr, od.bytes(), hipMemcpyDeviceToHost, d.stream));
+    MB_HIP(hipMemcpyAsync(out, od.ptr, od.bytes(), hipMemcpyDeviceToHost, d.stream));
     MB_HIP(hipStreamSynchronize(d.stream));
-    return out;
 }
 
 std::vector<float> Booster::feature_importance(int type) const {   // Booster.swift:1926-1940
@@ -627,8 +631,7 @@ int32_t macboost_predict_contrib(void *handle, const float *x, int64_t rows, int
         return -1;
     }
     return guarded(err, [&]() -> int32_t {
-        auto c = b->predict_contrib(x, rows, cols);
-        std::memcpy(out, c.data(), c.size() * sizeof(float));
+        b->predict_contrib(x, rows, cols, out);
         return 0;
     }, -1);
 }

@@ -156,10 +156,10 @@ struct Booster {
     void build_forest();
     std::vector<float> predict(const float *x_fm, int64_t rows, int64_t cols);
     std::vector<float> predict_raw(const float *x_fm, int64_t rows, int64_t cols);
-    std::vector<float> predict_contrib(const float *x_fm, int64_t rows, int64_t cols);
+    void predict_contrib(const float *x_fm, int64_t rows, int64_t cols, float *out);
     std::vector<float> feature_importance(int type) const;
     double shap_bias(int k = 0) const;
-    std::vector<float> contrib_class(const float *x_fm, int64_t rows, int64_t cols, int k);
+    void contrib_class(const float *x_fm, int64_t rows, int64_t cols, int k, float *out);
     std::string to_json() const;
     static Booster *from_json(const std::string &text);
 };
