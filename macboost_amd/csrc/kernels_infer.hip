@@ -333,29 +333,28 @@ __global__ __launch_bounds__(64) void k_treeshap_rows(const float *__restrict__ 
                     }
                 }
             }
-            // unwound sums per unique feature (SHAP.swift:307-325)
+            // unwound sums per unique feature (SHAP.swift:307-325).  The o != 0
+            // and o == 0 forms share one loop (the lanes of a wavefront take
+            // both): per lane the same operations in the same order.
 #pragma unroll
             for (int u = 0; u < MAXU; ++u) {
                 if (u < U) {
                     const double o = one[u], z = zero[u];
+                    const bool on = o != 0.0, live = on || z != 0.0;
                     double total = 0.0;
-                    if (o != 0.0) {
-                        double next = 0.0;
+                    double next = 0.0;
 #pragma unroll
-                        for (int q = MAXU; q >= 0; --q)
-                            if (q == U) next = pw[q];
+                    for (int q = MAXU; q >= 0; --q)
+                        if (q == U) next = pw[q];
 #pragma unroll
-                        for (int q = MAXU - 1; q >= 0; --q) {
-                            if (q < U) {
-                                const double tmp = next / ((double)(q + 1) * o);
-                                total += tmp;
-                                next = pw[q] - tmp * z * (double)(U - q);
-                            }
+                    for (int q = MAXU - 1; q >= 0; --q) {
+                        if (q < U) {
+                            const double num = on ? next : pw[q];
+                            const double den = on ? (double)(q + 1) * o : z * (double)(U - q);
+                            const double tmp = live ? num / den : 0.0;
+                            total += tmp;
+                            if (on) next = pw[q] - tmp * z * (double)(U - q);
                         }
-                    } else if (z != 0.0) {
-#pragma unroll
-                        for (int q = MAXU - 1; q >= 0; --q)
-                            if (q < U) total += pw[q] / (z * (double)(U - q));
                     }
                     atomicAdd(&phi[feat[u]], total * (double)(U + 1) * (o - z) * P.leaf);
                 }
