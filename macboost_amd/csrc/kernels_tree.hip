@@ -1269,29 +1269,34 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
     }
 }
 
-// One workgroup per (sibling pair, 4 features): each side's histogram rows
-// [bin][f0 .. f0+3] (64 contiguous bytes per bin) are staged through LDS,
-// eight independent loads per thread, then wavefront w searches feature
-// f0 + w (its 256 bins, 4 per lane).
+// One workgroup per (sibling pair, 4 features), one wavefront per (side,
+// feature): both sides' histogram rows [bin][f0 .. f0+3] (64 contiguous bytes
+// per bin) are staged through LDS together, eight independent loads per
+// thread, then wavefront (side, w) searches feature f0 + w of that side's node
+// (its 256 bins, 4 per lane).  The two sides' searches run at once.
 constexpr int SPLIT_FEATS = 4;
-constexpr int SPLIT_STAGE_PER_THREAD = 256 * SPLIT_FEATS * 2 / (SPLIT_FEATS * 64);
-constexpr size_t SPLIT_STAGE_BYTES = (size_t)256 * SPLIT_FEATS * 2 * sizeof(int64_t);
-constexpr size_t SPLIT_LDS_BYTES = SPLIT_STAGE_BYTES > SPLIT_FEATS * sizeof(CatScratch)
+constexpr int SPLIT_WAVES = 2 * SPLIT_FEATS;
+constexpr int SPLIT_THREADS = SPLIT_WAVES * 64;
+constexpr int SPLIT_ROW = 2 * SPLIT_FEATS;           // words per bin and side
+constexpr int SPLIT_STAGE_PER_THREAD = 2 * 256 * SPLIT_ROW / SPLIT_THREADS;
+constexpr size_t SPLIT_STAGE_BYTES = (size_t)2 * 256 * SPLIT_ROW * sizeof(int64_t);
+constexpr size_t SPLIT_LDS_BYTES = SPLIT_STAGE_BYTES > SPLIT_WAVES * sizeof(CatScratch)
                                        ? SPLIT_STAGE_BYTES
-                                       : SPLIT_FEATS * sizeof(CatScratch);
+                                       : SPLIT_WAVES * sizeof(CatScratch);
+static_assert(2 * 256 * SPLIT_ROW % SPLIT_THREADS == 0, "whole stage words per thread");
 
-__global__ __launch_bounds__(SPLIT_FEATS * 64) void k_split(Shape sh, SplitParams sp,
-                                              const Pair *__restrict__ pairs,
-                                              const int64_t *__restrict__ hist_cur,
-                                              const uint8_t *__restrict__ is_cat,
-                                              const int8_t *__restrict__ monotone,
-                                              const uint8_t *__restrict__ feat_mask,
-                                              const TreeCtl *ctl, const uint32_t *count,
-                                              int64_t *node_g, int64_t *node_h,
-                                              uint32_t level_start,
-                                              SplitResult *__restrict__ results) {
+__global__ __launch_bounds__(SPLIT_THREADS) void k_split(Shape sh, SplitParams sp,
+                                                         const Pair *__restrict__ pairs,
+                                                         const int64_t *__restrict__ hist_cur,
+                                                         const uint8_t *__restrict__ is_cat,
+                                                         const int8_t *__restrict__ monotone,
+                                                         const uint8_t *__restrict__ feat_mask,
+                                                         const TreeCtl *ctl, const uint32_t *count,
+                                                         int64_t *node_g, int64_t *node_h,
+                                                         uint32_t level_start,
+                                                         SplitResult *__restrict__ results) {
     __shared__ __align__(16) unsigned char split_lds[SPLIT_LDS_BYTES];
-    int64_t *stage = reinterpret_cast<int64_t *>(split_lds);      // [bin][16][2]
+    int64_t *stage = reinterpret_cast<int64_t *>(split_lds);      // [side][bin][SPLIT_ROW]
     CatScratch *cs_all = reinterpret_cast<CatScratch *>(split_lds);
     const int F = sh.cols, nb = sh.num_bins;
     const uint32_t groups = (uint32_t)((F + SPLIT_FEATS - 1) / SPLIT_FEATS);
@@ -1302,61 +1307,61 @@ __global__ __launch_bounds__(SPLIT_FEATS * 64) void k_split(Shape sh, SplitParam
     const Pair pr = pairs[pair_idx];
     const int tid = threadIdx.x, lane = lane_id();
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int f = f0 + w;
-    const bool active = w < nf;
+    const int side = w / SPLIT_FEATS, fw = w % SPLIT_FEATS;
+    const int f = f0 + fw;
+    const uint32_t local = side == 0 ? pr.built : pr.derived;
+    const bool active = fw < nf && local != NONE;
+    // stage both sides' rows (a side without a node stages zeros)
+    const int row = 2 * nf;
+    int64_t v[SPLIT_STAGE_PER_THREAD];
+#pragma unroll
+    for (int k = 0; k < SPLIT_STAGE_PER_THREAD; ++k) {
+        const int idx = tid + k * SPLIT_THREADS;
+        const int sd = idx / (256 * SPLIT_ROW), rem = idx - sd * (256 * SPLIT_ROW);
+        const int b = rem / row, r = rem - b * row;
+        const uint32_t node = sd == 0 ? pr.built : pr.derived;
+        v[k] = (b < nb && node != NONE)
+                   ? hist_cur[(((size_t)node * nb + b) * F + f0) * 2 + r]
+                   : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < SPLIT_STAGE_PER_THREAD; ++k) {
+        const int idx = tid + k * SPLIT_THREADS;
+        const int sd = idx / (256 * SPLIT_ROW), rem = idx - sd * (256 * SPLIT_ROW);
+        const int b = rem / row, r = rem - b * row;
+        if (b < nb) stage[((size_t)sd * 256 + b) * SPLIT_ROW + r] = v[k];
+    }
+    __syncthreads();
+    int64_t hg[4], hh[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int b = 4 * lane + j;
+        hg[j] = 0; hh[j] = 0;
+        if (active && b < nb) {
+            hg[j] = stage[((size_t)side * 256 + b) * SPLIT_ROW + 2 * fw];
+            hh[j] = stage[((size_t)side * 256 + b) * SPLIT_ROW + 2 * fw + 1];
+        }
+    }
+    __syncthreads();                                 // the stage becomes split scratch
+    if (!active) return;                             // uniform per wavefront
     const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
     const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
-    const bool cat = active && is_cat[f] != 0;
-    const int cst = (!active || cat) ? 0 : (int)monotone[f];
-    const bool allowed = active && feat_mask[f] != 0;
-    for (int side = 0; side < 2; ++side) {
-        const uint32_t local = side == 0 ? pr.built : pr.derived;
-        if (local == NONE) break;                    // uniform per block
-        // stage rows [bin][f0 .. f0+nf) (each bin's 2*nf words are contiguous)
-        const int64_t *src = hist_cur + (size_t)local * nb * F * 2;
-        const int row = 2 * nf;
-        int64_t v[SPLIT_STAGE_PER_THREAD];
-#pragma unroll
-        for (int k = 0; k < SPLIT_STAGE_PER_THREAD; ++k) {
-            const int idx = tid + k * SPLIT_FEATS * 64;
-            const int b = idx / row, r = idx - b * row;
-            v[k] = idx < nb * row ? src[((size_t)b * F + f0) * 2 + r] : 0;
-        }
-#pragma unroll
-        for (int k = 0; k < SPLIT_STAGE_PER_THREAD; ++k) {
-            const int idx = tid + k * SPLIT_FEATS * 64;
-            const int b = idx / row, r = idx - b * row;
-            if (idx < nb * row) stage[(size_t)b * (2 * SPLIT_FEATS) + r] = v[k];
-        }
-        __syncthreads();
-        int64_t hg[4], hh[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = 4 * lane + j;
-            hg[j] = 0; hh[j] = 0;
-            if (active && b < nb) {
-                hg[j] = stage[(size_t)b * (2 * SPLIT_FEATS) + 2 * w];
-                hh[j] = stage[(size_t)b * (2 * SPLIT_FEATS) + 2 * w + 1];
-            }
-        }
-        __syncthreads();                             // the stage becomes split scratch
-        if (active) {
-            const uint32_t abs_n = level_start + local;
-            if (f == 0) {
-                const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
-                const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
-                if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
-            }
-            SplitResult *dst = results + (size_t)local * F + f;
-            if (allowed && count[abs_n] >= 1) {
-                node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs_all[w], dst);
-            } else if (lane == 0) {
-                SplitResult r = {};
-                r.gain = -INFINITY;
-                *dst = r;
-            }
-        }
-        __syncthreads();                             // before the next side's stage
+    const bool cat = is_cat[f] != 0;
+    const int cst = cat ? 0 : (int)monotone[f];
+    const bool allowed = feat_mask[f] != 0;
+    const uint32_t abs_n = level_start + local;
+    if (f == 0) {
+        const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
+        const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
+        if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
+    }
+    SplitResult *dst = results + (size_t)local * F + f;
+    if (allowed && count[abs_n] >= 1) {
+        node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs_all[w], dst);
+    } else if (lane == 0) {
+        SplitResult r = {};
+        r.gain = -INFINITY;
+        *dst = r;
     }
 }
 
@@ -1370,7 +1375,7 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp, c
     hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl);
     if (e != hipSuccess) return e;
     const uint32_t groups = (uint32_t)((sh.cols + SPLIT_FEATS - 1) / SPLIT_FEATS);
-    hipLaunchKernelGGL(k_split, dim3(max_pairs * groups), dim3(SPLIT_FEATS * 64), 0, s, sh, sp, pairs,
+    hipLaunchKernelGGL(k_split, dim3(max_pairs * groups), dim3(SPLIT_THREADS), 0, s, sh, sp, pairs,
                        hist_cur, is_cat, monotone, feat_mask, ctl, count, node_g, node_h,
                        level_start, results);
     return hipGetLastError();
