@@ -2478,24 +2478,26 @@ __global__ __launch_bounds__(PART_THREADS) void k_lw_route(Shape sh, LWArgs a, L
                                                           TreeCtl *ctl, Pair *pairs,
                                                           HistItem *items, TreeOut out) {
     __shared__ uint32_t s_mask[8];
-    if (st->done) return;
-    const uint32_t cnt = st->count;
+    // the step state, loaded together before any branch
+    const uint32_t done = st->done, cnt = st->count, src = st->src, dst = st->dst;
+    const NodeSplit sp = {st->feature, st->bin, st->flags};
+    const uint32_t mask_word = threadIdx.x < 8 ? st->mask[threadIdx.x] : 0u;
+    if (done) return;
     if (cnt == 0) {                                  // nothing to move: plan directly
         if (blockIdx.x == 0)
             lw_plan_block(sh, a, st, open, 0u, slot_seg, slot_count, ctl, pairs, items, out);
         return;
     }
     if (blockIdx.x * (uint32_t)PART_BLOCK >= cnt) return;   // uniform per block
-    if (threadIdx.x < 8) s_mask[threadIdx.x] = st->mask[threadIdx.x];
+    if (threadIdx.x < 8) s_mask[threadIdx.x] = mask_word;
     __syncthreads();
-    const NodeSplit sp = {st->feature, st->bin, st->flags};
     const uint8_t *col = bins_fm + (size_t)sp.feature * a.rows;
     bool last = false;
     uint32_t left = 0;
     for (uint32_t first = blockIdx.x * (uint32_t)PART_BLOCK; first < cnt;
          first += gridDim.x * (uint32_t)PART_BLOCK) {
-        if (route_block(sp, s_mask, sh.num_bins, col, order + st->src + first,
-                        min((uint32_t)PART_BLOCK, cnt - first), cnt, order + st->dst, cursor,
+        if (route_block(sp, s_mask, sh.num_bins, col, order + src + first,
+                        min((uint32_t)PART_BLOCK, cnt - first), cnt, order + dst, cursor,
                         true, &left))
             last = true;                             // uniform per block
         __syncthreads();                             // LDS reuse by the next chunk
