@@ -801,7 +801,7 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
         mb::DevBuf<uint64_t> partials((size_t)max_items * tile_width * num_bins);
         mb::DevBuf<mbk::HistItem> items((size_t)max_items);
         mb::DevBuf<mbk::Pair> pairs(1);
-        mb::DevBuf<uint32_t> seg(1), count(1), scratch(64);
+        mb::DevBuf<uint32_t> seg(1), count(1);
         mb::DevBuf<float> cover(1);
         mb::DevBuf<float2> bounds(1);
         mb::DevBuf<int64_t> node_g(1), node_h(1), dummy(2);
@@ -814,7 +814,7 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
         MB_HIP(hipMemcpyAsync(ctl.ptr->max_gh, max_gh, 8, hipMemcpyDeviceToDevice, s));
         MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)n, (uint32_t)(2 * grid), 2048u, ctl.ptr, seg.ptr,
                                      count.ptr, pairs.ptr, items.ptr, cover.ptr, bounds.ptr,
-                                     -INFINITY, INFINITY, scratch.ptr));
+                                     -INFINITY, INFINITY));
         MB_HIP(mbk::launch_hist(s, sh, bins_tiled, reinterpret_cast<const mbk::Entry *>(entries),
                                 items.ptr, ctl.ptr, partials.ptr, grid));
         MB_HIP(mbk::launch_split(s, sh, sp, pairs.ptr, 1, partials.ptr, dummy.ptr, hist_out,

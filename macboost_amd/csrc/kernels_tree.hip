@@ -1582,11 +1582,19 @@ __device__ __forceinline__ uint32_t item_chunk(uint64_t total, uint32_t num_pair
     return (uint32_t)c;
 }
 
+// Pairs a planning block can hold in LDS: the deepest planned level at
+// maxDepth 12 has 2^11 nodes, i.e. at most 1024 sibling pairs.
+constexpr uint32_t PLAN_MAX_PAIRS = 1024;
+
+// Histogram items of num_pairs pairs (already in pairs[], written before a
+// barrier): s_cnt / s_seg hold each pair's built node's rows and first entry
+// (LDS, filled by the caller), s_first is LDS scratch of num_pairs words.
+// Writes the chunk size, each pair's nchunks and item_first, and the items;
+// every read-after-write inside the block goes through LDS.
 __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pairs,
-                            HistItem *items, const uint32_t *seg_start,
-                            const uint32_t *count_level, uint32_t num_pairs,
-                            uint32_t target_items, uint32_t min_chunk, uint32_t *scratch,
-                            uint32_t *wave_tot, bool accumulate = false) {
+                            HistItem *items, const uint32_t *s_cnt, const uint32_t *s_seg,
+                            uint32_t *s_first, uint32_t num_pairs, uint32_t target_items,
+                            uint32_t min_chunk, uint32_t *wave_tot, bool accumulate = false) {
     __shared__ uint32_t s_chunk;
     __shared__ uint32_t s_total;
     const int tid = threadIdx.x;
@@ -1594,7 +1602,7 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     if (tid == 0) s_total = 0;
     __syncthreads();
     uint32_t part = 0;
-    for (uint32_t k = tid; k < num_pairs; k += blockDim.x) part += count_level[pairs[k].built];
+    for (uint32_t k = tid; k < num_pairs; k += blockDim.x) part += s_cnt[k];
     part = wave_sum(part);
     if (lane_id() == 0) atomicAdd(&s_total, part);
     __syncthreads();
@@ -1605,20 +1613,17 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         ctl->chunk = c;
         if (accumulate) ctl->level_built[level] += (uint32_t)total;
         else ctl->level_built[level] = (uint32_t)total;
-        scratch[0] = 0;
     }
     __syncthreads();
     const uint32_t chunk = s_chunk;
-    // items per pair -> exclusive prefix (scratch[1..num_pairs])
-    uint32_t *npair_items = scratch + 1;
+    // items per pair -> exclusive prefix
     for (uint32_t k = tid; k < num_pairs; k += blockDim.x) {
-        const uint32_t c = count_level[pairs[k].built];
-        const uint32_t nch = (c + chunk - 1) / chunk;
+        const uint32_t nch = (s_cnt[k] + chunk - 1) / chunk;
         pairs[k].nchunks = nch;
-        npair_items[k] = nch * (uint32_t)sh.num_tiles;
+        s_first[k] = nch * (uint32_t)sh.num_tiles;
     }
     __syncthreads();
-    const uint32_t total_items = block_exclusive_scan(npair_items, num_pairs, wave_tot);
+    const uint32_t total_items = block_exclusive_scan(s_first, num_pairs, wave_tot);
     if (total_items > sh.item_cap) {
         // never write past the item list: the level gets no items and the
         // host reports the overflow after the tree
@@ -1632,25 +1637,22 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         }
         return;
     }
-    for (uint32_t k = tid; k < num_pairs; k += blockDim.x) pairs[k].item_first = npair_items[k];
+    for (uint32_t k = tid; k < num_pairs; k += blockDim.x) pairs[k].item_first = s_first[k];
     if (tid == 0) ctl->num_items = total_items;
-    __syncthreads();
     for (uint32_t it = tid; it < total_items; it += blockDim.x) {
-        // owning pair: last k with item_first <= it
+        // owning pair: last k with s_first[k] <= it
         uint32_t lo = 0, hi = num_pairs - 1;
         while (lo < hi) {
             const uint32_t mid = (lo + hi + 1) >> 1;
-            if (npair_items[mid] <= it) lo = mid; else hi = mid - 1;
+            if (s_first[mid] <= it) lo = mid; else hi = mid - 1;
         }
-        const Pair pr = pairs[lo];
-        const uint32_t rel = it - pr.item_first;
+        const uint32_t rel = it - s_first[lo];
         const uint32_t t = rel % (uint32_t)sh.num_tiles, c = rel / (uint32_t)sh.num_tiles;
-        const uint32_t cnt = count_level[pr.built];
         HistItem h;
         h.pair = lo;
         h.tile = t;
-        h.start = seg_start[pr.built] + c * chunk;
-        h.count = min(chunk, cnt - c * chunk);
+        h.start = s_seg[lo] + c * chunk;
+        h.count = min(chunk, s_cnt[lo] - c * chunk);
         items[it] = h;
     }
 }
@@ -1660,8 +1662,9 @@ __global__ __launch_bounds__(1024) void k_plan_root(Shape sh, uint32_t rows_acti
                                                     TreeCtl *ctl, uint32_t *seg_start,
                                                     uint32_t *count, Pair *pairs, HistItem *items,
                                                     float *cover, float2 *bounds, float lo,
-                                                    float hi, uint32_t *scratch) {
+                                                    float hi) {
     __shared__ uint32_t wave_tot[17];
+    __shared__ uint32_t s_cnt[1], s_seg[1], s_first[1];
     if (threadIdx.x == 0) {
         if (rows_active == NONE) rows_active = ctl->sampled;   // a sampled tree's kept rows
         count[0] = rows_active;
@@ -1673,97 +1676,102 @@ __global__ __launch_bounds__(1024) void k_plan_root(Shape sh, uint32_t rows_acti
         Pair p = {};
         p.built = 0; p.derived = NONE; p.parent = NONE;
         pairs[0] = p;
-        scratch[0] = 0;
+        s_cnt[0] = rows_active;
+        s_seg[0] = 0;
     }
     __syncthreads();
-    write_items(sh, ctl, 0, pairs, items, seg_start, count, 1, target_items, min_chunk, scratch,
+    write_items(sh, ctl, 0, pairs, items, s_cnt, s_seg, s_first, 1, target_items, min_chunk,
                 wave_tot);
 }
 
 hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active,
                             uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                             uint32_t *seg_start, uint32_t *count, Pair *pairs, HistItem *items,
-                            float *cover, float2 *bounds, float lo, float hi,
-                            uint32_t *scratch) {
+                            float *cover, float2 *bounds, float lo, float hi) {
     hipLaunchKernelGGL(k_plan_root, dim3(1), dim3(1024), 0, s, sh, rows_active, target_items,
-                       min_chunk, ctl, seg_start, count, pairs, items, cover, bounds, lo, hi,
-                       scratch);
+                       min_chunk, ctl, seg_start, count, pairs, items, cover, bounds, lo, hi);
     return hipGetLastError();
 }
 
 // Plan level d from level d-1's routed counts (decide_splits phase 2,
-// Shaders.swift:1454-1488, with counts from the partition).
+// Shaders.swift:1454-1488, with counts from the partition).  Thread p owns
+// parent p (at most PLAN_MAX_PAIRS parents, so one pass); what later steps
+// read back goes through LDS.
 __global__ __launch_bounds__(1024) void k_plan_level(
     Shape sh, LevelArgs la, uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
     const uint32_t *seg_start_prev, uint32_t *seg_start_next, uint32_t *count,
-    const uint64_t *cursors, const TreeOut out, Pair *pairs, HistItem *items,
-    uint32_t *scratch) {
+    const uint64_t *cursors, const TreeOut out, Pair *pairs, HistItem *items) {
     __shared__ uint32_t wave_tot[17];
     __shared__ uint32_t s_active;
+    __shared__ uint32_t s_idx[PLAN_MAX_PAIRS];       // split flag, then pair index
+    __shared__ uint32_t s_cnt[PLAN_MAX_PAIRS], s_seg[PLAN_MAX_PAIRS], s_first[PLAN_MAX_PAIRS];
     const int tid = threadIdx.x;
     const uint32_t num_prev = la.num_level >> 1;
     const uint32_t ls_prev = (la.level_start - 1) >> 1;   // (2^d - 1 - 1) / 2 = 2^(d-1) - 1
     if (tid == 0) s_active = 0;
-    __syncthreads();
     // children of a split node share its interval: left [start, start+L),
     // right [start+L, start+count), with L from the partition's left cursor
-    uint32_t act = 0;
-    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
+    const uint32_t p = (uint32_t)tid;
+    const bool mine = p < num_prev;
+    bool split = false;
+    uint32_t cl = 0, cr = 0, seg = 0;
+    if (mine) {
         const uint32_t n = ls_prev + p;
-        const bool split = out.split[n].feature >= 0 && count[n] >= 1;
-        const uint32_t cl = split ? (uint32_t)cursors[(size_t)p * CURSOR_STRIDE] : 0u;
-        const uint32_t cr = split ? count[n] - cl : 0u;
+        const int32_t feat = out.split[n].feature;
+        const uint32_t cnt = count[n];
+        const uint32_t left = (uint32_t)cursors[(size_t)p * CURSOR_STRIDE];
+        seg = seg_start_prev[p];
+        split = feat >= 0 && cnt >= 1;
+        cl = split ? left : 0u;
+        cr = split ? cnt - left : 0u;
         count[la.level_start + 2 * p] = cl;
         count[la.level_start + 2 * p + 1] = cr;
         out.cover[la.level_start + 2 * p] = (float)cl;
         out.cover[la.level_start + 2 * p + 1] = (float)cr;
-        seg_start_next[2 * p] = seg_start_prev[p];
-        seg_start_next[2 * p + 1] = seg_start_prev[p] + cl;
-        scratch[1 + p] = split ? 1u : 0u;
-        act += cl + cr;
+        seg_start_next[2 * p] = seg;
+        seg_start_next[2 * p + 1] = seg + cl;
+        s_idx[p] = split ? 1u : 0u;
     }
-    act = wave_sum(act);
+    const uint32_t act = wave_sum(cl + cr);
+    __syncthreads();
     if (lane_id() == 0) atomicAdd(&s_active, act);
     __syncthreads();
-    const uint32_t active = s_active;
-    if (tid == 0) ctl->level_active[la.level] = active;
+    if (tid == 0) ctl->level_active[la.level] = s_active;
     if (la.terminal) {
         if (tid == 0) { ctl->num_pairs = 0; ctl->num_items = 0; }
         return;
     }
-    // 4. sibling pairs for split parents: the smaller child builds, ties go left
-    const uint32_t num_pairs = block_exclusive_scan(scratch + 1, num_prev, wave_tot);
-    for (uint32_t p = tid; p < num_prev; p += blockDim.x) {
-        const uint32_t n = ls_prev + p;
-        const bool split = out.split[n].feature >= 0 && count[n] >= 1;
-        if (!split) continue;
-        const uint32_t cl = count[la.level_start + 2 * p];
-        const uint32_t cr = count[la.level_start + 2 * p + 1];
+    // sibling pairs for split parents: the smaller child builds, ties go left
+    const uint32_t num_pairs = block_exclusive_scan(s_idx, num_prev, wave_tot);
+    if (mine && split) {
+        const uint32_t k = s_idx[p];
+        const bool left_built = cl <= cr;
         Pair pr = {};
-        pr.built = cl <= cr ? 2 * p : 2 * p + 1;
-        pr.derived = cl <= cr ? 2 * p + 1 : 2 * p;
+        pr.built = left_built ? 2 * p : 2 * p + 1;
+        pr.derived = left_built ? 2 * p + 1 : 2 * p;
         pr.parent = p;
-        pairs[scratch[1 + p]] = pr;
+        pairs[k] = pr;
+        s_cnt[k] = left_built ? cl : cr;
+        s_seg[k] = left_built ? seg : seg + cl;
     }
-    __syncthreads();
-    if (tid == 0) { ctl->num_pairs = num_pairs; scratch[0] = 0; }
+    if (tid == 0) ctl->num_pairs = num_pairs;
     __syncthreads();
     if (num_pairs == 0) {
         if (tid == 0) ctl->num_items = 0;
         return;
     }
-    write_items(sh, ctl, la.level, pairs, items, seg_start_next, count + la.level_start,
-                num_pairs, target_items, min_chunk, scratch, wave_tot);
+    write_items(sh, ctl, la.level, pairs, items, s_cnt, s_seg, s_first, num_pairs, target_items,
+                min_chunk, wave_tot);
 }
 
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                              const uint32_t *seg_start_prev, uint32_t *seg_start_next,
                              uint32_t *count, const uint64_t *cursors, const TreeOut out,
-                             Pair *pairs, HistItem *items, uint32_t *scratch) {
+                             Pair *pairs, HistItem *items) {
+    if ((la.num_level >> 1) > PLAN_MAX_PAIRS) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_plan_level, dim3(1), dim3(1024), 0, s, sh, la, target_items, min_chunk,
-                       ctl, seg_start_prev, seg_start_next, count, cursors, out, pairs, items,
-                       scratch);
+                       ctl, seg_start_prev, seg_start_next, count, cursors, out, pairs, items);
     return hipGetLastError();
 }
 
@@ -2143,9 +2151,9 @@ __device__ __forceinline__ float lw_leaf_value(const SplitParams &sp, int64_t g,
 __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *ctl, LWState *st,
                                                   LWOpen *open, uint32_t *slot_seg,
                                                   uint32_t *slot_count, Pair *pairs,
-                                                  HistItem *items, uint32_t *scratch,
-                                                  TreeOut out, int sampled) {
+                                                  HistItem *items, TreeOut out, int sampled) {
     __shared__ uint32_t wave_tot[17];
+    __shared__ uint32_t s_cnt[1], s_seg[1], s_first[1];
     const int tid = threadIdx.x;
     for (int n = tid; n < a.total_nodes; n += blockDim.x) {
         const NodeSplit leaf = {-1, 0, 0};
@@ -2183,19 +2191,19 @@ __global__ __launch_bounds__(1024) void k_lw_init(Shape sh, LWArgs a, TreeCtl *c
         ctl->num_pairs = 1;
         ctl->level_active[0] = n0;
         out.cover[0] = (float)n0;
-        scratch[0] = 0;
+        s_cnt[0] = n0;
+        s_seg[0] = 0;
     }
     __syncthreads();
-    write_items(sh, ctl, 0, pairs, items, slot_seg, slot_count, 1, a.target_items, a.min_chunk,
-                scratch, wave_tot, true);
+    write_items(sh, ctl, 0, pairs, items, s_cnt, s_seg, s_first, 1, a.target_items, a.min_chunk,
+                wave_tot, true);
 }
 
 hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeCtl *ctl,
                           LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
-                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out,
-                          bool sampled) {
+                          Pair *pairs, HistItem *items, const TreeOut out, bool sampled) {
     hipLaunchKernelGGL(k_lw_init, dim3(1), dim3(1024), 0, s, sh, a, ctl, st, open, slot_seg,
-                       slot_count, pairs, items, scratch, out, sampled ? 1 : 0);
+                       slot_count, pairs, items, out, sampled ? 1 : 0);
     return hipGetLastError();
 }
 

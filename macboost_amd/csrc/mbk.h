@@ -210,7 +210,7 @@ hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active
                             uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                             uint32_t *seg_start, uint32_t *count, Pair *pairs,
                             HistItem *items, float *cover, float2 *bounds,
-                            float root_lo, float root_hi, uint32_t *scratch);
+                            float root_lo, float root_hi);
 
 hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
                          const LevelArgs &la, const SplitResult *results,
@@ -255,7 +255,7 @@ hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la
                              uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                              const uint32_t *seg_start_prev, uint32_t *seg_start_next,
                              uint32_t *count, const uint64_t *cursors, const TreeOut out,
-                             Pair *pairs, HistItem *items, uint32_t *scratch);
+                             Pair *pairs, HistItem *items);
 
 // ---------------------------------------------------------------------------
 // Leaf-wise (best-first) growth (leaf_reset/leaf_init/leaf_pick_apply/
@@ -310,8 +310,7 @@ struct LWArgs {
 
 hipError_t launch_lw_init(hipStream_t s, const Shape &sh, const LWArgs &a, TreeCtl *ctl,
                           LWState *st, LWOpen *open, uint32_t *slot_seg, uint32_t *slot_count,
-                          Pair *pairs, HistItem *items, uint32_t *scratch, const TreeOut out,
-                          bool sampled);
+                          Pair *pairs, HistItem *items, const TreeOut out, bool sampled);
 // the last step's evaluations (every other step's run inside the next pick)
 hipError_t launch_lw_eval(hipStream_t s, const Shape &sh, const SplitParams &sp,
                           const LWState *st, LWOpen *open, const SplitResult *results,

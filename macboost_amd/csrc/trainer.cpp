@@ -96,7 +96,7 @@ struct Trainer {
     DevBuf<mbk::Pair> pairs;
     DevBuf<int64_t> hist_a, hist_b;
     DevBuf<mbk::SplitResult> results;
-    DevBuf<uint32_t> count, seg_a, seg_b, scratch;
+    DevBuf<uint32_t> count, seg_a, seg_b;
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
@@ -633,7 +633,6 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.bounds.alloc((size_t)t.total_nodes);
     t.seg_a.alloc((size_t)1 << t.D);
     t.seg_b.alloc((size_t)1 << t.D);
-    t.scratch.alloc(((size_t)1 << t.D) + 64);
     t.ctl.alloc(1);
     t.ensure_capacity(std::max(1, p.num_trees));
     MB_HIP(hipStreamSynchronize(s));
@@ -895,8 +894,7 @@ static void grow_levelwise(Trainer &t, int tree) {
     MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
                                  (uint32_t)t.target_items,
                                  (uint32_t)t.min_chunk, ctl, t.seg_a.ptr, t.count.ptr, t.pairs.ptr,
-                                 t.items.ptr, out.cover, t.bounds.ptr, -INFINITY, INFINITY,
-                                 t.scratch.ptr));
+                                 t.items.ptr, out.cover, t.bounds.ptr, -INFINITY, INFINITY));
     mbk::Entry *ord_cur = t.order_a.ptr, *ord_next = t.order_b.ptr;
     uint32_t *seg_cur = t.seg_a.ptr, *seg_next = t.seg_b.ptr;
     int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
@@ -956,7 +954,7 @@ static void grow_levelwise(Trainer &t, int tree) {
             MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items,
                                           (uint32_t)t.min_chunk, ctl, seg_cur, seg_next,
                                           t.count.ptr, t.route_cursor.ptr, out, t.pairs.ptr,
-                                          t.items.ptr, t.scratch.ptr));
+                                          t.items.ptr));
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, true));
             if (t.renewal) renew_tree(t, out, nullptr);
@@ -969,7 +967,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                                  t.route_grid, true));
         MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
                                       ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr, out,
-                                      t.pairs.ptr, t.items.ptr, t.scratch.ptr));
+                                      t.pairs.ptr, t.items.ptr));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
@@ -1002,7 +1000,7 @@ static void grow_leafwise(Trainer &t, int tree) {
     mbk::Entry *order = t.order_a.ptr;
     const bool sampled = tree_entries(t, tree, ctl, order);
     MB_HIP(mbk::launch_lw_init(s, sh, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
-                               t.count.ptr, t.pairs.ptr, t.items.ptr, t.scratch.ptr, out,
+                               t.count.ptr, t.pairs.ptr, t.items.ptr, out,
                                sampled));
     auto build = [&](int step) {
         hipEvent_t e0 = nullptr, e1 = nullptr;
