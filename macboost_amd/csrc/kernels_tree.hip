@@ -1012,38 +1012,59 @@ size_t hist_lds_size() { return (size_t)HIST_LDS_BYTES; }
 // stored [node][bin][feature][g,h] as exact int64.
 // ---------------------------------------------------------------------------
 
-constexpr int REDUCE_SLICES = 4;
-
+// A block of 256 threads covers 256 / S (bin, feature) cells of one (pair,
+// tile); its S slices of threads split that tile's chunks.  Levels with 16 or
+// more pairs (few chunks each) run with S = 1, the others with S = 4.
+template <int S>
 __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict__ pairs,
                                                 const uint64_t *__restrict__ partials,
                                                 const int64_t *__restrict__ hist_prev,
                                                 int64_t *__restrict__ hist_cur, const TreeCtl *ctl,
                                                 uint32_t blocks_per_tile) {
-    __shared__ int64_t red[REDUCE_SLICES][64][2];
+    constexpr int CELLS = 256 / S;
+    __shared__ int64_t red[S > 1 ? S : 1][CELLS][2];
     const int W = sh.tile_w, nb = sh.num_bins, F = sh.cols, T = sh.num_tiles;
     const uint32_t bpt = blockIdx.x % blocks_per_tile;
     const uint32_t rest = blockIdx.x / blocks_per_tile;
     const int tile = (int)(rest % (uint32_t)T);
     const uint32_t pair_idx = rest / (uint32_t)T;
     if (pair_idx >= ctl->num_pairs) return;          // uniform per block
-    const int kk = threadIdx.x & 63, slice = threadIdx.x >> 6;
-    const int k = (int)bpt * 64 + kk;                 // (bin, feature) index in the tile
+    const int kk = threadIdx.x % CELLS, slice = threadIdx.x / CELLS;
+    const int k = (int)bpt * CELLS + kk;             // (bin, feature) index in the tile
     const Pair pr = pairs[pair_idx];
     int64_t g = 0, h = 0;
     if (k < nb * W) {
         const size_t stride = (size_t)(nb * W);
+        const size_t cstride = (size_t)T * stride;   // between chunks of one (pair, tile)
         const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile) * stride + k;
-        for (uint32_t c = (uint32_t)slice; c < pr.nchunks; c += REDUCE_SLICES) {
-            const uint64_t w = src[(size_t)c * (size_t)T * stride];
-            g += (int64_t)w >> HIST_QH_BITS;
-            h += (int64_t)(w & ((1ull << HIST_QH_BITS) - 1));
+        constexpr uint64_t HMASK = (1ull << HIST_QH_BITS) - 1;
+        // four chunks per step, their loads in flight together (integer sums:
+        // the order does not matter)
+        uint32_t c = (uint32_t)slice;
+        for (; c + 3 * S < pr.nchunks; c += 4 * S) {
+            uint64_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = src[(size_t)(c + j * S) * cstride];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                g += (int64_t)w[j] >> HIST_QH_BITS;
+                h += (int64_t)(w[j] & HMASK);
+            }
+        }
+        for (; c < pr.nchunks; c += S) {
+            const uint64_t w1 = src[(size_t)c * cstride];
+            g += (int64_t)w1 >> HIST_QH_BITS;
+            h += (int64_t)(w1 & HMASK);
         }
     }
-    red[slice][kk][0] = g;
-    red[slice][kk][1] = h;
-    __syncthreads();
-    if (slice != 0 || k >= nb * W) return;
-    for (int s2 = 1; s2 < REDUCE_SLICES; ++s2) { g += red[s2][kk][0]; h += red[s2][kk][1]; }
+    if constexpr (S > 1) {
+        red[slice][kk][0] = g;
+        red[slice][kk][1] = h;
+        __syncthreads();
+        if (slice != 0) return;
+        for (int s2 = 1; s2 < S; ++s2) { g += red[s2][kk][0]; h += red[s2][kk][1]; }
+    }
+    if (k >= nb * W) return;
     const int b = k / W, fl = k % W, f = tile * W + fl;
     if (f >= F) return;
     int64_t *hb = hist_cur + (((size_t)pr.built * nb + b) * F + f) * 2;
@@ -1060,10 +1081,16 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
 hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
                          const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
                          const TreeCtl *ctl) {
-    const uint32_t bpt = (uint32_t)((sh.num_bins * sh.tile_w + 63) / 64);
-    const uint32_t grid = max_pairs * (uint32_t)sh.num_tiles * bpt;
-    hipLaunchKernelGGL(k_reduce, dim3(grid), dim3(256), 0, s, sh, pairs, partials, hist_prev,
-                       hist_cur, ctl, bpt);
+    const uint32_t cells = (uint32_t)(sh.num_bins * sh.tile_w);
+    if (max_pairs >= 16) {                           // measured: S = 4 is faster below
+        const uint32_t bpt = (cells + 255) / 256;
+        hipLaunchKernelGGL(k_reduce<1>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
+                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt);
+    } else {
+        const uint32_t bpt = (cells + 63) / 64;
+        hipLaunchKernelGGL(k_reduce<4>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
+                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt);
+    }
     return hipGetLastError();
 }
 
