@@ -344,6 +344,21 @@ def test_depth_extremes_identical():
     check_identical(x, y, {"num_trees": 10, "max_depth": 1, "num_bins": 4})
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 1), (2, 3), (5, 9), (63, 17), (64, 33), (65, 65),
+                                       (130, 100), (8193, 4)])
+def test_tiny_and_ragged_shapes_identical(rows, cols):
+    # rows below, at and past one wavefront and one partition block; every
+    # tile width (8/16/32/64) with partial last tiles; NaN holes
+    rng = np.random.default_rng(rows * 1000 + cols)
+    x = rng.random((cols, rows), dtype=np.float32)
+    x[rng.random((cols, rows)) < 0.1] = np.nan
+    y = (rng.standard_normal(rows) + 3.0 * np.nan_to_num(x[0])).astype(np.float32)
+    xt = rng.random((cols, 97), dtype=np.float32)
+    p = {"num_trees": 4, "max_depth": 6, "num_bins": 32, "min_child_weight": 0.5}
+    check_identical(x, y, p, x_test=xt)
+    check_identical(x, y, dict(p, num_leaves=5), x_test=xt)
+
+
 def test_save_load_bitwise(tmp_path):
     # FeatureTests.swift:307-341
     x, y = _mixed(8000)
