@@ -239,7 +239,7 @@ std::vector<float> Booster::predict_raw(const float *x, int64_t rows, int64_t co
         Device &d = device();
         build_forest();
         DevBuf<float> xd((size_t)rows * (size_t)cols), od((size_t)rows * (size_t)K);
-        MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, d.stream));
+        upload(xd.ptr, x, xd.bytes(), d.stream);
         for (int k = 0; k < K; ++k) {
             mbk::ForestDev f{forest.feature.ptr, forest.threshold.ptr, forest.flags.ptr,
                              forest.leaf.ptr, forest.has_mask ? forest.mask.ptr : nullptr,

@@ -94,6 +94,11 @@ struct Device {
     Device &operator=(const Device &) = delete;
 };
 
+// Host -> device copy of a pageable buffer on stream s.  Copies of 128 MB or
+// more go through pinned staging and have completed on return; smaller ones
+// are one hipMemcpyAsync.
+void upload(void *dst, const void *src, size_t bytes, hipStream_t s);
+
 template <typename T>
 struct DevBuf {
     T *ptr = nullptr;

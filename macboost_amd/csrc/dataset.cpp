@@ -114,7 +114,7 @@ BinnedDataset *dataset_make(const Params &p, const float *x, int64_t rows, int64
     DevBuf<uint8_t> tiled((size_t)rows * 8);     // one 8-wide tile: the kernel's other output
     DevBuf<uint64_t> out((size_t)groups * (size_t)rows);
     MB_HIP(hipMemcpyAsync(cat.ptr, is_cat.data(), (size_t)cols, hipMemcpyHostToDevice, s));
-    MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, s));
+    upload(xd.ptr, x, xd.bytes(), s);
     {
         const size_t cap = mbk::edge_sample_cap(rows);
         DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);

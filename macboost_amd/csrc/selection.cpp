@@ -43,7 +43,7 @@ SelectionResult select_features(const Params &p, const float *x, int64_t rows, i
     DevBuf<uint8_t> cat((size_t)cols), fm((size_t)rows * (size_t)cols);
     DevBuf<uint8_t> fm2((size_t)rows * 2 * (size_t)cols);
     MB_HIP(hipMemcpyAsync(cat.ptr, is_cat.data(), (size_t)cols, hipMemcpyHostToDevice, s));
-    MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, s));
+    upload(xd.ptr, x, xd.bytes(), s);
     {
         const size_t cap = mbk::edge_sample_cap(rows);
         DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
