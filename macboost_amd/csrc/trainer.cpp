@@ -102,8 +102,15 @@ void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
     Staging &st = staging();
     std::lock_guard<std::mutex> lock(st.m);
     for (char *&b : st.buf)
-        if (!b) MB_HIP(hipHostMalloc(reinterpret_cast<void **>(&b), STAGE_CHUNK,
-                                     hipHostMallocPortable));
+        if (!b && hipHostMalloc(reinterpret_cast<void **>(&b), STAGE_CHUNK,
+                                hipHostMallocPortable) != hipSuccess) {
+            b = nullptr;
+            (void)hipGetLastError();
+        }
+    if (!st.buf[0] || !st.buf[1]) {                  // no pinned memory: one pageable copy
+        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+        return;
+    }
     const unsigned threads = std::max(1u, std::min(8u, std::thread::hardware_concurrency() / 2));
     hipEvent_t ev[2] = {nullptr, nullptr};
     MB_HIP(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
