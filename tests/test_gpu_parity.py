@@ -279,8 +279,8 @@ def test_node_hist_full_size_exact(ctx):
 # --------------------------------------------------------------------------
 
 def test_c1_friedman_identical_trees_and_bitexact_predict():
-    # 20k x 100 Friedman, max_bin 64, 100 trees, depth 6, lr 0.1;
-    # held-out 20k rows predicted bit-exactly.
+    # The small Friedman #1 workload: 20k x 100, max_bin 64, 100 trees, depth 6,
+    # lr 0.1; held-out 20k rows predicted bit-exactly.
     x, y = mb.friedman(20_000, 100, 42)
     xt, _ = mb.friedman(20_000, 100, 42 + 999)
     check_identical(x, y, {"num_trees": 100, "max_depth": 6, "num_bins": 64}, x_test=xt)
@@ -374,14 +374,15 @@ def test_save_load_bitwise(tmp_path):
 # --------------------------------------------------------------------------
 
 def test_c2_friedman_1m_identical_trees():
-    # 1M x 100 Friedman #1, 256 bins, depth 6; 200k held-out rows
+    # Friedman #1 at 1M x 100, 256 bins, depth 6; 200k held-out rows
     x, y = mb.friedman(1_000_000, 100, 42)
     xt, _ = mb.friedman(200_000, 100, 42 + 999)
     check_identical(x, y, {"num_trees": 4, "max_depth": 6, "num_bins": 256}, x_test=xt)
 
 
 def test_c3_nan_categorical_identical_trees():
-    # 20% MCAR NaN over the numeric columns, 20 categorical columns
+    # Friedman #1 with 20% MCAR NaN over the numeric columns and 20 integer
+    # categorical columns
     x, y, cats = D.c3_mixed(300_000, 42)
     xv, _, _ = D.c3_mixed(50_000, 42 + 999)
     h, ref = check_identical(x, y, {"num_trees": 5, "max_depth": 6, "categorical_features": cats},
@@ -390,7 +391,7 @@ def test_c3_nan_categorical_identical_trees():
 
 
 def test_c4_higgs_like_logistic_identical_trees():
-    # 28 HIGGS-shaped features, logistic objective
+    # 28 HIGGS-shaped synthetic features, logistic objective
     x, y = D.c4_higgs_like(200_000, 42)
     xt, _ = D.c4_higgs_like(50_000, 43)
     check_identical(x, y, {"num_trees": 10, "max_depth": 6, "objective": "binary"}, x_test=xt)
