@@ -1,9 +1,9 @@
 /*
  * mbo_oracle.c — CPU restatement of MacBoost's tree-build hot path.
  *
- * TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path in
- * macboost_amd/ and the timed CPU baseline of bench.py.  The shipped library
- * never links or calls it.
+ * TEST INFRASTRUCTURE ONLY: the reference results the HIP path in
+ * macboost_amd/ is compared with, and the timed CPU baseline of bench.py.
+ * The shipped library never links or calls it.
  *
  * Single-threaded, plain C11, IEEE float semantics (built with
  * -ffp-contract=off, no fast-math).  Each function names the reference

@@ -1,10 +1,11 @@
 /*
  * mbo_oracle.h — CPU restatement of MacBoost's tree-build hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
- * implementation in macboost_amd/.  Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load it, and only as the checker or as the
- * timed CPU baseline — never as the thing measured or shipped.
+ * TEST INFRASTRUCTURE ONLY.  This library gives the reference results the HIP
+ * implementation in macboost_amd/ is compared with.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only
+ * to compare results or as the timed CPU baseline — never as the thing measured
+ * or shipped.
  *
  * Every function cites the reference file:line it restates (paths relative to
  * the MacBoost v1.0.0 source tree).  Histogram sums are exact integers

@@ -1,7 +1,7 @@
 """ctypes front end of the CPU oracle (oracle/liboracle.so).
 
 Test infrastructure only: tests, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it as the checker.  Every function
+``cpu_baseline`` leg of ``bench.py`` use it to compare results.  Every function
 mirrors one entry of ``oracle/mbo_oracle.h``.
 """
 from __future__ import annotations
