@@ -318,7 +318,10 @@ __global__ __launch_bounds__(64) void k_treeshap_rows(const float *__restrict__ 
             double one[MAXU];
 #pragma unroll
             for (int u = 0; u < MAXU; ++u) one[u] = ((ones >> u) & 1u) ? 1.0 : 0.0;
-            // EXTEND with the dummy element at index 0 (SHAP.swift:266-279)
+            // EXTEND with the dummy element at index 0 (SHAP.swift:266-279).  The
+            // weights (q+1)/(j+1) and (j-q)/(j+1) are compile-time constants here,
+            // one multiply each instead of a multiply and a divide (a rounding
+            // apart from the divided form).
             double pw[MAXU + 1];
             pw[0] = 1.0;
 #pragma unroll
@@ -328,19 +331,29 @@ __global__ __launch_bounds__(64) void k_treeshap_rows(const float *__restrict__ 
                     const double o = one[j - 1], z = zero[j - 1];
 #pragma unroll
                     for (int q = j - 1; q >= 0; --q) {
-                        pw[q + 1] += o * pw[q] * (double)(q + 1) / (double)(j + 1);
-                        pw[q] = z * pw[q] * (double)(j - q) / (double)(j + 1);
+                        const double up = (double)(q + 1) / (double)(j + 1);
+                        const double down = (double)(j - q) / (double)(j + 1);
+                        pw[q + 1] += o * pw[q] * up;
+                        pw[q] = z * pw[q] * down;
                     }
                 }
             }
-            // unwound sums per unique feature (SHAP.swift:307-325).  The o != 0
-            // and o == 0 forms share one loop (the lanes of a wavefront take
-            // both): per lane the same operations in the same order.
+            // 1 / (U - q) for q < U: U divisions per path, shared by every
+            // unique feature's unwinding
+            double inv_uq[MAXU];
+#pragma unroll
+            for (int q = 0; q < MAXU; ++q) inv_uq[q] = q < U ? 1.0 / (double)(U - q) : 0.0;
+            // unwound sums per unique feature (SHAP.swift:307-325).  one[u] is 0
+            // or 1, so the o != 0 form divides by the constant q + 1 (a multiply
+            // by its reciprocal here) and the o == 0 form by z (U - q) (one 1/z
+            // per feature).  Both forms share one loop: a wavefront's lanes take
+            // both.
 #pragma unroll
             for (int u = 0; u < MAXU; ++u) {
                 if (u < U) {
                     const double o = one[u], z = zero[u];
                     const bool on = o != 0.0, live = on || z != 0.0;
+                    const double inv_z = (!on && z != 0.0) ? 1.0 / z : 0.0;
                     double total = 0.0;
                     double next = 0.0;
 #pragma unroll
@@ -349,9 +362,9 @@ __global__ __launch_bounds__(64) void k_treeshap_rows(const float *__restrict__ 
 #pragma unroll
                     for (int q = MAXU - 1; q >= 0; --q) {
                         if (q < U) {
-                            const double num = on ? next : pw[q];
-                            const double den = on ? (double)(q + 1) * o : z * (double)(U - q);
-                            const double tmp = live ? num / den : 0.0;
+                            const double rq = 1.0 / (double)(q + 1);
+                            const double tmp = on ? next * rq
+                                                  : (live ? pw[q] * inv_z * inv_uq[q] : 0.0);
                             total += tmp;
                             if (on) next = pw[q] - tmp * z * (double)(U - q);
                         }
