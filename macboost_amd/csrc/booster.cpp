@@ -377,7 +377,7 @@ void Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k, f
     DevBuf<mbk::ShapPath> pd(paths.size());
     DevBuf<mbk::ShapElem> ed(elems.size());
     DevBuf<mbk::ShapUniq> ud(uniq.size());
-    MB_HIP(hipMemcpyAsync(xd.ptr, x, xd.bytes(), hipMemcpyHostToDevice, d.stream));
+    upload(xd.ptr, x, xd.bytes(), d.stream);
     MB_HIP(hipMemcpyAsync(pd.ptr, paths.data(), pd.bytes(), hipMemcpyHostToDevice, d.stream));
     MB_HIP(hipMemcpyAsync(ed.ptr, elems.data(), ed.bytes(), hipMemcpyHostToDevice, d.stream));
     MB_HIP(hipMemcpyAsync(ud.ptr, uniq.data(), ud.bytes(), hipMemcpyHostToDevice, d.stream));
@@ -390,8 +390,7 @@ void Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k, f
                                 forest.has_mask ? forest.mask.ptr : nullptr, pd.ptr,
                                 (int)paths.size(), max_elems, ed.ptr, ud.ptr, bias, od.ptr,
                                 phi.ptr));
-    MB_HIP(hipMemcpyAsync(out, od.ptr, od.bytes(), hipMemcpyDeviceToHost, d.stream));
-    MB_HIP(hipStreamSynchronize(d.stream));
+    download(out, od.ptr, od.bytes(), d.stream);
 }
 
 std::vector<float> Booster::feature_importance(int type) const {   // Booster.swift:1926-1940

@@ -94,10 +94,13 @@ struct Device {
     Device &operator=(const Device &) = delete;
 };
 
-// Host -> device copy of a pageable buffer on stream s.  Copies of 128 MB or
+// Host -> device copy of a pageable buffer on stream s.  Copies of 64 MB or
 // more go through pinned staging and have completed on return; smaller ones
 // are one hipMemcpyAsync.
 void upload(void *dst, const void *src, size_t bytes, hipStream_t s);
+// Device -> host copy into a pageable buffer after the work queued on s;
+// complete on return (64 MB or more through the pinned staging buffers).
+void download(void *dst, const void *src, size_t bytes, hipStream_t s);
 
 template <typename T>
 struct DevBuf {

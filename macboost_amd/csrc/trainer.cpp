@@ -92,26 +92,36 @@ void parallel_copy(char *dst, const char *src, size_t n, unsigned threads) {
     std::memcpy(dst, src, std::min(n, per));
     for (auto &th : ts) th.join();
 }
-}  // namespace
 
-void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
-    if (bytes < 2 * STAGE_CHUNK) {
-        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
-        return;
-    }
-    Staging &st = staging();
-    std::lock_guard<std::mutex> lock(st.m);
+// Both staging buffers, allocated on first use; false if pinned memory cannot
+// be had (the caller then makes one pageable copy).  Called with st.m held.
+bool staging_ready(Staging &st) {
     for (char *&b : st.buf)
         if (!b && hipHostMalloc(reinterpret_cast<void **>(&b), STAGE_CHUNK,
                                 hipHostMallocPortable) != hipSuccess) {
             b = nullptr;
             (void)hipGetLastError();
         }
-    if (!st.buf[0] || !st.buf[1]) {                  // no pinned memory: one pageable copy
+    return st.buf[0] && st.buf[1];
+}
+
+unsigned copy_threads() {
+    return std::max(1u, std::min(8u, std::thread::hardware_concurrency() / 2));
+}
+}  // namespace
+
+void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes < STAGE_CHUNK) {
         MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
         return;
     }
-    const unsigned threads = std::max(1u, std::min(8u, std::thread::hardware_concurrency() / 2));
+    Staging &st = staging();
+    std::lock_guard<std::mutex> lock(st.m);
+    if (!staging_ready(st)) {                        // no pinned memory: one pageable copy
+        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+        return;
+    }
+    const unsigned threads = copy_threads();
     hipEvent_t ev[2] = {nullptr, nullptr};
     MB_HIP(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
     MB_HIP(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
@@ -129,6 +139,43 @@ void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
     // both buffers drained before another upload may refill them
     MB_HIP(hipEventSynchronize(ev[0]));
     MB_HIP(hipEventSynchronize(ev[1]));
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+}
+
+void download(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes < STAGE_CHUNK) {
+        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+        MB_HIP(hipStreamSynchronize(s));
+        return;
+    }
+    Staging &st = staging();
+    std::lock_guard<std::mutex> lock(st.m);
+    if (!staging_ready(st)) {
+        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+        MB_HIP(hipStreamSynchronize(s));
+        return;
+    }
+    const unsigned threads = copy_threads();
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    MB_HIP(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+    MB_HIP(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
+    const char *from = static_cast<const char *>(src);
+    char *to = static_cast<char *>(dst);
+    const size_t nchunks = (bytes + STAGE_CHUNK - 1) / STAGE_CHUNK;
+    auto issue = [&](size_t k) {                     // DMA of chunk k into buffer k % 2
+        const size_t off = k * STAGE_CHUNK, n = std::min(STAGE_CHUNK, bytes - off);
+        MB_HIP(hipMemcpyAsync(st.buf[k & 1], from + off, n, hipMemcpyDeviceToHost, s));
+        MB_HIP(hipEventRecord(ev[k & 1], s));
+    };
+    issue(0);
+    if (nchunks > 1) issue(1);
+    for (size_t k = 0; k < nchunks; ++k) {
+        const size_t off = k * STAGE_CHUNK, n = std::min(STAGE_CHUNK, bytes - off);
+        MB_HIP(hipEventSynchronize(ev[k & 1]));
+        parallel_copy(to + off, st.buf[k & 1], n, threads);
+        if (k + 2 < nchunks) issue(k + 2);           // the buffer is free again
+    }
     (void)hipEventDestroy(ev[0]);
     (void)hipEventDestroy(ev[1]);
 }
