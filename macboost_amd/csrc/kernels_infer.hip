@@ -3,10 +3,10 @@
 // walk used for per-iteration validation (predict_tree_binned, :1763-1781) and
 // exact TreeSHAP (gpu_treeshap, :1656-1734).
 //
-// TreeSHAP here gives each lane one row and walks every root-to-leaf path in
-// wave-uniform order, extending/unwinding in double precision and
-// accumulating phi in an LDS slice owned by the lane: no global atomics, a
-// fixed summation order, and a single rounding to f32 at the end.
+// TreeSHAP here gives each row a wavefront and each root-to-leaf path a lane,
+// extending/unwinding in double precision and accumulating the row's phi in
+// LDS (the wavefront owns it, so the summation order is fixed), with a single
+// rounding to f32 at the end.
 #include "mbk.h"
 
 #include <math.h>
@@ -54,34 +54,6 @@ hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float 
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_predict_forest, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, f,
                        x, rows, data_bins, base, out);
-    return hipGetLastError();
-}
-
-__global__ __launch_bounds__(256) void k_predict_binned(const uint8_t *__restrict__ bins_fm,
-                                                        int64_t rows, int32_t nb, int32_t max_depth,
-                                                        TreeOut tree, float *__restrict__ preds) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= rows) return;
-    uint32_t n = 0;
-    for (int32_t d = 0; d < max_depth; ++d) {
-        const NodeSplit s = tree.split[n];
-        if (s.feature < 0) break;
-        const uint32_t b = bins_fm[(int64_t)s.feature * rows + i];
-        bool left;
-        if (s.flags & FLAG_CATEGORICAL) left = ((tree.mask[n * 8 + (b >> 5)] >> (b & 31u)) & 1u) != 0;
-        else if (b == (uint32_t)(nb - 1)) left = (s.flags & FLAG_DEFAULT_LEFT) != 0;
-        else left = b <= s.bin;
-        n = 2 * n + 1 + (left ? 0 : 1);
-    }
-    preds[i] += tree.leaf[n];
-}
-
-hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
-                                 int32_t num_bins, int32_t max_depth, const TreeOut tree,
-                                 float *preds) {
-    if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_predict_binned, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
-                       bins_fm, rows, num_bins, max_depth, tree, preds);
     return hipGetLastError();
 }
 
@@ -142,8 +114,9 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
         const int64_t i = base + (int64_t)k * WALK_THREADS;
         if (i >= rows) continue;
         if (preds) preds[i] += s_leaf[n[k]];        // null: counts only
-        if (n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
+        if (count && n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
     }
+    if (!count) return;                              // null: predictions only
     __syncthreads();
     for (uint32_t k = threadIdx.x; k < deep; k += blockDim.x)
         if (s_cnt[k]) atomicAdd(&count[deep_start + k], s_cnt[k]);
@@ -159,6 +132,14 @@ hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows
     hipLaunchKernelGGL(k_walk_count, dim3((unsigned)((rows + per - 1) / per)), dim3(WALK_THREADS),
                        lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count);
     return hipGetLastError();
+}
+
+// Binned single-tree prediction (predict_tree_binned, Shaders.swift:1763-1781):
+// the same walk with the tree staged in LDS, without counts.
+hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                                 int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                                 float *preds) {
+    return launch_walk_count(s, bins_fm, rows, num_bins, max_depth, tree, preds, nullptr);
 }
 
 // ---------------------------------------------------------------------------

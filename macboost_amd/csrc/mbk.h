@@ -347,9 +347,9 @@ hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float 
 hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                                  int32_t num_bins, int32_t max_depth, const TreeOut tree,
                                  float *preds);
-// Training-row walk of a finished level-wise tree: preds += leaf (unless
-// preds is null), and rows per node of the deepest level added to
-// count[2^D - 1 ...].
+// Training-row walk of a finished tree: preds += leaf (unless preds is null),
+// and rows per node of the deepest level added to count[2^D - 1 ...] (unless
+// count is null).
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                              int32_t num_bins, int32_t max_depth, const TreeOut tree,
                              float *preds, uint32_t *count);
