@@ -555,10 +555,11 @@ size_t grad_max_scratch_words() { return 2 * (size_t)GRAD_MAX_BLOCKS; }
 
 constexpr int GOSS_BUCKETS = 1024;
 constexpr int SEL_THREADS = 1024;
-constexpr int SEL_PER_THREAD = 16;
+constexpr int SEL_PER_THREAD = 8;    // 16 spills: the gradient code is inlined per row
 constexpr int SEL_BLOCK = SEL_THREADS * SEL_PER_THREAD;
 constexpr int SEL_WAVES = SEL_THREADS / 64;
-static_assert(SEL_PER_THREAD * SEL_WAVES == 256, "slice scan assumes 256 slices");
+constexpr int SEL_SLICES_PER_LANE = SEL_PER_THREAD * SEL_WAVES / 64;
+static_assert(SEL_PER_THREAD * SEL_WAVES % 64 == 0, "slice scan: whole slices per lane");
 
 __device__ __forceinline__ uint32_t wang_hash(uint32_t x) {
     x = (x ^ 61u) ^ (x >> 16);
@@ -641,7 +642,7 @@ __global__ __launch_bounds__(64) void k_goss_threshold(uint32_t top_count, TreeC
 
 // Keep rows with |g| >= threshold (weight 1) and a hashed uniform sample of
 // the rest (weight sp.weight); compact kept rows into order[] (one cursor add
-// per 16K-row chunk) and leave per-block maxima of |g|*w and h*w.
+// per 8K-row chunk) and leave per-block maxima of |g|*w and h*w.
 __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
     GradParams gp, SampleParams sp, const float *__restrict__ preds,
     const float *__restrict__ labels, const float *__restrict__ weights, int64_t rows,
@@ -689,13 +690,14 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
         }
         __syncthreads();
         if (tid < 64) {
-            uint32_t v[4], s = 0;
+            constexpr int SPL = SEL_SLICES_PER_LANE;
+            uint32_t v[SPL], s = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) { v[j] = tot[tid * 4 + j]; s += v[j]; }
+            for (int j = 0; j < SPL; ++j) { v[j] = tot[tid * SPL + j]; s += v[j]; }
             const uint32_t inc = wave_inclusive_scan(s);
             uint32_t acc = inc - s;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) { tot[tid * 4 + j] = acc; acc += v[j]; }
+            for (int j = 0; j < SPL; ++j) { tot[tid * SPL + j] = acc; acc += v[j]; }
             if (tid == 63) s_base = atomicAdd(&ctl->sampled, inc);
         }
         __syncthreads();
