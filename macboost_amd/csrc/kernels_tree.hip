@@ -576,9 +576,13 @@ __global__ __launch_bounds__(256) void k_goss_hist(GradParams gp, const float *_
                                                    const float *__restrict__ weights,
                                                    int64_t rows, const TreeCtl *ctl,
                                                    uint32_t *buckets) {
-    __shared__ uint32_t lb[GOSS_BUCKETS];
-    for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) lb[k] = 0;
+    // one sub-histogram per wavefront: |g| clusters early in training, and
+    // same-bucket adds from the block's four wavefronts would serialize
+    constexpr int WAVES = 256 / 64;
+    __shared__ uint32_t lb[WAVES][GOSS_BUCKETS];
+    for (int k = threadIdx.x; k < WAVES * GOSS_BUCKETS; k += blockDim.x) (&lb[0][0])[k] = 0;
     __syncthreads();
+    uint32_t *mine = lb[threadIdx.x >> 6];
     const float mg = f32_from_bits(ctl->max_gh[0]);
     if (mg > 0.0f) {
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
@@ -586,12 +590,16 @@ __global__ __launch_bounds__(256) void k_goss_hist(GradParams gp, const float *_
             float g, h;
             row_grad_at(gp, preds, labels, weights, i, g, h);
             const uint32_t b = (uint32_t)(fabsf(g) / mg * (float)GOSS_BUCKETS);
-            atomicAdd(&lb[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
+            atomicAdd(&mine[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
         }
     }
     __syncthreads();
-    for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x)
-        if (lb[k]) atomicAdd(&buckets[k], lb[k]);
+    for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) c += lb[w][k];
+        if (c) atomicAdd(&buckets[k], c);
+    }
 }
 
 // Threshold = lower edge of the bucket where the count from the top first
@@ -749,8 +757,10 @@ hipError_t launch_sample(hipStream_t s, const GradParams &gp, const SampleParams
                          const float *preds, const float *labels, const float *weights,
                          int64_t rows, TreeCtl *ctl, uint32_t *buckets, uint32_t *partial,
                          Entry *order) {
+    // 8 blocks per CU of grid-stride rows: enough loads in flight to stream
+    const unsigned hist_blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
     if (sp.goss && sp.top_count > 0)
-        hipLaunchKernelGGL(k_goss_hist, dim3(256), dim3(256), 0, s, gp, preds, labels, weights,
+        hipLaunchKernelGGL(k_goss_hist, dim3(hist_blocks), dim3(256), 0, s, gp, preds, labels, weights,
                            rows, ctl, buckets);
     hipLaunchKernelGGL(k_goss_threshold, dim3(1), dim3(64), 0, s, sp.goss ? sp.top_count : 0u,
                        ctl, buckets);
