@@ -773,6 +773,8 @@ def test_treeshap_matches_oracle(depth):
     forest = model_io.forest_from_json(obj)
     want = O.treeshap(forest, obj["baseScore"], obj["numBins"], x)
     assert np.allclose(c, want, rtol=1e-5, atol=1e-6)
+    # reproducible run to run (each row's phi is summed by one wavefront)
+    assert np.array_equal(c, mb.predict_contrib(h, x, feature_major=True))
     raw = mb.predict(h, x, feature_major=True)
     assert np.max(np.abs(c.astype(np.float64).sum(axis=1) - raw)) < 1e-4
 
