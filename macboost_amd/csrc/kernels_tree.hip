@@ -878,13 +878,16 @@ __device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0
     return out;
 }
 
+// row_stride: bytes between rows of the gather layout (T * W, or the compact
+// root copy's 16-B multiple, whose last tile runs into the next row: those
+// bytes land in padding columns, which are never reduced).
 template <int W>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
                                                        const Entry *__restrict__ order,
                                                        const HistItem *__restrict__ items,
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
-                                                       int32_t num_tiles, int32_t nb) {
+                                                       int64_t row_stride, int32_t nb) {
     constexpr int P = W >= 32 ? 32 : W;              // features per lane
     constexpr int RPB = W == 64 ? 32 : 64;           // rows per wavefront batch
     constexpr int DR = HIST_DATA_RING, ER = HIST_ENTRY_RING;
@@ -910,7 +913,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         sel[t] = 0x0C020000u | ((4u + (((uint32_t)lane & 3u) ^ (uint32_t)t)) << 8);
     char *lds = reinterpret_cast<char *>(hist_lds);
     const uint32_t stride = nwaves * RPB;
-    const size_t row_bytes = (size_t)num_tiles * W;
+    const size_t row_bytes = (size_t)row_stride;
     const uint32_t nitems = ctl->num_items;
     // Items are chunk-major (the tiles of one row chunk are adjacent).  With
     // workgroups dispatched round-robin over 8 XCDs, block b = 16q + 8h + x
@@ -999,12 +1002,19 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 
 
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, const Entry *order,
-                       const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid) {
+                       const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid,
+                       int64_t row_stride) {
+    if (row_stride <= 0) {
+        row_stride = (int64_t)sh.num_tiles * sh.tile_w;
+    } else if (sh.tile_w != 64 || row_stride % 16 ||
+               row_stride < (int64_t)(sh.num_tiles - 1) * sh.tile_w + 16) {
+        return hipErrorInvalidValue;                 // a compact copy has 64-wide tiles
+    }
     switch (sh.tile_w) {
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
         hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,       \
-                           items, ctl, partials, sh.num_tiles, sh.num_bins);                 \
+                           items, ctl, partials, row_stride, sh.num_bins);                   \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)
@@ -1017,6 +1027,31 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
 }
 
 size_t hist_lds_size() { return (size_t)HIST_LDS_BYTES; }
+
+// Compact copy of the gather layout for the root pass: row r's first `stride`
+// bytes (every feature and its zero padding up to a 16-B multiple) at
+// r * stride.  One thread per 16-B chunk of the output.
+__global__ __launch_bounds__(256) void k_compact_rows(const uint8_t *__restrict__ tiled,
+                                                      int64_t rows, int32_t row_bytes,
+                                                      int32_t stride, uint8_t *__restrict__ out) {
+    const int32_t per_row = stride / 16;
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= rows * per_row) return;
+    const int64_t r = k / per_row, c = k - r * per_row;
+    *reinterpret_cast<uint4 *>(out + r * stride + c * 16) =
+        *reinterpret_cast<const uint4 *>(tiled + r * row_bytes + c * 16);
+}
+
+hipError_t launch_compact_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled,
+                               int32_t stride, uint8_t *out) {
+    const int32_t row_bytes = sh.num_tiles * sh.tile_w;
+    if (stride % 16 || stride > row_bytes) return hipErrorInvalidValue;
+    const int64_t n = sh.rows * (stride / 16);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_compact_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, tiled,
+                       sh.rows, row_bytes, stride, out);
+    return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // partial reduction + sibling subtraction (subtract_histograms, :313-326):

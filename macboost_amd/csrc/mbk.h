@@ -176,10 +176,17 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 
 // Histogram items -> packed partials [item][B][W] (64-bit words, see
 // HIST_QH_BITS).
+// row_stride 0: the gather layout's T * W; else the compact root copy's
+// stride (a 16-B multiple, launch_compact_rows).
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
-                       uint64_t *partials, int grid);
+                       uint64_t *partials, int grid, int64_t row_stride = 0);
 size_t hist_lds_size();   // static LDS of one histogram workgroup
+// Compact copy of the gather layout (row stride `stride` < T * W, 16-B
+// multiple) for streaming passes over every row; out holds rows * stride
+// bytes plus 64 zero bytes (the last row's last tile reads past its end).
+hipError_t launch_compact_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled,
+                               int32_t stride, uint8_t *out);
 
 // Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
 struct LevelArgs {

@@ -203,6 +203,8 @@ struct Trainer {
     float base = 0.0f;
 
     DevBuf<uint8_t> bins_tiled, bins_fm, vbins_fm;
+    DevBuf<uint8_t> bins_root;      // compact copy of bins_tiled for the root pass
+    int64_t root_stride = 0;        // its row stride (0: no copy)
     DevBuf<float> labels, weights, preds, vpreds;
     DevBuf<uint8_t> is_cat, feat_mask;
     DevBuf<int8_t> mono;
@@ -605,6 +607,21 @@ static void bin_valid(Trainer &t, const float *xv, int64_t vrows, const float *e
 }
 
 // Labels, weights, predictions and the tree-build buffers.
+// The root histogram streams every row: with 64-wide tiles it reads T * 64 B
+// per row although the features fill only ceil(F/16)*16 of them (112 of 128
+// at F = 100), so it gets a compact copy at that stride.
+static void build_root_copy(Trainer &t) {
+    t.root_stride = 0;
+    if (t.sh.tile_w != 64 || t.sh.num_tiles < 2) return;
+    const int64_t stride = (t.cols + 15) / 16 * 16;
+    if (stride >= (int64_t)t.sh.num_tiles * 64) return;
+    hipStream_t s = t.dev->stream;
+    t.bins_root.alloc((size_t)(t.rows * stride + 64));
+    MB_HIP(hipMemsetAsync(t.bins_root.ptr + t.rows * stride, 0, 64, s));
+    MB_HIP(mbk::launch_compact_rows(s, t.sh, t.bins_tiled.ptr, (int32_t)stride, t.bins_root.ptr));
+    t.root_stride = stride;
+}
+
 static void setup_buffers(Trainer &t, const float *y, const float *w, const float *yv) {
     const Params &p = t.p;
     hipStream_t s = t.dev->stream;
@@ -754,6 +771,7 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.seg_b.alloc((size_t)1 << t.D);
     t.ctl.alloc(1);
     t.ensure_capacity(std::max(1, p.num_trees));
+    build_root_copy(t);
     MB_HIP(hipStreamSynchronize(s));
     t.best_metric = effective_metric(p) == "auc" ? -INFINITY : INFINITY;
 }
@@ -1025,8 +1043,11 @@ static void grow_levelwise(Trainer &t, int tree) {
             MB_HIP(hipEventCreate(&e1));
             MB_HIP(hipEventRecord(e0, s));
         }
-        MB_HIP(mbk::launch_hist(s, sh, t.bins_tiled.ptr, ord, t.items.ptr, ctl, t.partials.ptr,
-                                t.hist_grid));
+        // an unsampled root streams every row: the compact copy when there is one
+        const bool compact = level == 0 && !sampled && t.root_stride > 0;
+        MB_HIP(mbk::launch_hist(s, sh, compact ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
+                                t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
+                                compact ? t.root_stride : 0));
         if (t.profiling) {
             MB_HIP(hipEventRecord(e1, s));
             t.events.push_back({e0, e1, level});
@@ -1128,8 +1149,10 @@ static void grow_leafwise(Trainer &t, int tree) {
             MB_HIP(hipEventCreate(&e1));
             MB_HIP(hipEventRecord(e0, s));
         }
-        MB_HIP(mbk::launch_hist(s, sh, t.bins_tiled.ptr, order, t.items.ptr, ctl, t.partials.ptr,
-                                t.hist_grid));
+        const bool compact = step == 0 && !sampled && t.root_stride > 0;
+        MB_HIP(mbk::launch_hist(s, sh, compact ? t.bins_root.ptr : t.bins_tiled.ptr, order,
+                                t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
+                                compact ? t.root_stride : 0));
         if (t.profiling) {
             MB_HIP(hipEventRecord(e1, s));
             t.events.push_back({e0, e1, std::min(step, 15)});
