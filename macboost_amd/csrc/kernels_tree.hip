@@ -878,16 +878,16 @@ __device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0
     return out;
 }
 
-// row_stride: bytes between rows of the gather layout (T * W, or the compact
-// root copy's 16-B multiple, whose last tile runs into the next row: those
-// bytes land in padding columns, which are never reduced).
+// lay: where each tile's rows sit (the gather layout, or the planar root
+// copy, whose last tile's loads run into the next row: those bytes land in
+// padding columns, which are never reduced).
 template <int W>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
                                                        const Entry *__restrict__ order,
                                                        const HistItem *__restrict__ items,
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
-                                                       int64_t row_stride, int32_t nb) {
+                                                       HistLayout lay, int32_t nb) {
     constexpr int P = W >= 32 ? 32 : W;              // features per lane
     constexpr int RPB = W == 64 ? 32 : 64;           // rows per wavefront batch
     constexpr int DR = HIST_DATA_RING, ER = HIST_ENTRY_RING;
@@ -913,7 +913,6 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         sel[t] = 0x0C020000u | ((4u + (((uint32_t)lane & 3u) ^ (uint32_t)t)) << 8);
     char *lds = reinterpret_cast<char *>(hist_lds);
     const uint32_t stride = nwaves * RPB;
-    const size_t row_bytes = (size_t)row_stride;
     const uint32_t nitems = ctl->num_items;
     // Items are chunk-major (the tiles of one row chunk are adjacent).  With
     // workgroups dispatched round-robin over 8 XCDs, block b = 16q + 8h + x
@@ -931,7 +930,9 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         for (int k = tid; k < HIST_LDS_BYTES / 16; k += HIST_THREADS)
             reinterpret_cast<uint4 *>(hist_lds)[k] = make_uint4(0, 0, 0, 0);
         __syncthreads();
-        const uint8_t *tile = tiled + (size_t)item.tile * W + byte_off;
+        const uint8_t *tile = tiled + (size_t)item.tile * (size_t)lay.tile_step + byte_off;
+        const size_t row_bytes =
+            (size_t)((int32_t)item.tile == lay.last_tile ? lay.last_stride : lay.stride);
         const Entry *ent = order + item.start;
         const uint32_t g0 = (uint32_t)wave * RPB;
         // loads past the item's end read its last entry (in bounds); their
@@ -1001,20 +1002,38 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 }
 
 
+HistLayout gather_layout(const Shape &sh) {
+    const int32_t row = sh.num_tiles * sh.tile_w;
+    return HistLayout{(int64_t)sh.tile_w, row, row, sh.num_tiles - 1};
+}
+
+HistLayout planar_layout(const Shape &sh) {
+    const int32_t last_feats = sh.cols - (sh.num_tiles - 1) * 64;
+    return HistLayout{sh.rows * 64, 64, (last_feats + 15) / 16 * 16, sh.num_tiles - 1};
+}
+
+size_t planar_bytes(const Shape &sh) {
+    const HistLayout l = planar_layout(sh);
+    return (size_t)l.last_tile * (size_t)l.tile_step + (size_t)sh.rows * (size_t)l.last_stride + 64;
+}
+
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, const Entry *order,
                        const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid,
-                       int64_t row_stride) {
-    if (row_stride <= 0) {
-        row_stride = (int64_t)sh.num_tiles * sh.tile_w;
-    } else if (sh.tile_w != 64 || row_stride % 16 ||
-               row_stride < (int64_t)(sh.num_tiles - 1) * sh.tile_w + 16) {
-        return hipErrorInvalidValue;                 // a compact copy has 64-wide tiles
+                       const HistLayout *layout) {
+    const HistLayout lay = layout ? *layout : gather_layout(sh);
+    if (layout) {
+        // the planar copy: 64-wide tiles, every stride a 16-B multiple
+        const HistLayout p = planar_layout(sh);
+        if (sh.tile_w != 64 || sh.num_tiles < 2 || lay.tile_step != p.tile_step ||
+            lay.stride != p.stride || lay.last_stride != p.last_stride ||
+            lay.last_tile != p.last_tile)
+            return hipErrorInvalidValue;
     }
     switch (sh.tile_w) {
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
         hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,       \
-                           items, ctl, partials, row_stride, sh.num_bins);                   \
+                           items, ctl, partials, lay, sh.num_bins);                              \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)
@@ -1028,28 +1047,33 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
 
 size_t hist_lds_size() { return (size_t)HIST_LDS_BYTES; }
 
-// Compact copy of the gather layout for the root pass: row r's first `stride`
-// bytes (every feature and its zero padding up to a 16-B multiple) at
-// r * stride.  One thread per 16-B chunk of the output.
-__global__ __launch_bounds__(256) void k_compact_rows(const uint8_t *__restrict__ tiled,
-                                                      int64_t rows, int32_t row_bytes,
-                                                      int32_t stride, uint8_t *__restrict__ out) {
-    const int32_t per_row = stride / 16;
+// Planar copy of the gather layout for the root pass (planar_layout): 16-B
+// chunk j of row r (j < 4 * (T - 1) + last_stride / 16, i.e. every feature and
+// its zero padding up to a 16-B multiple) goes to tile j / 4's plane.  One
+// thread per chunk of the output.
+__global__ __launch_bounds__(256) void k_planar_rows(const uint8_t *__restrict__ tiled,
+                                                     int64_t rows, int32_t row_bytes,
+                                                     HistLayout lay, uint8_t *__restrict__ out) {
+    const int32_t full = 4 * lay.last_tile, per_row = full + lay.last_stride / 16;
     const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= rows * per_row) return;
-    const int64_t r = k / per_row, c = k - r * per_row;
-    *reinterpret_cast<uint4 *>(out + r * stride + c * 16) =
-        *reinterpret_cast<const uint4 *>(tiled + r * row_bytes + c * 16);
+    const int64_t r = k / per_row;
+    const int32_t j = (int32_t)(k - r * per_row);
+    const int64_t dst = j < full
+        ? (int64_t)(j >> 2) * lay.tile_step + r * 64 + (j & 3) * 16
+        : (int64_t)lay.last_tile * lay.tile_step + r * lay.last_stride + (j - full) * 16;
+    *reinterpret_cast<uint4 *>(out + dst) =
+        *reinterpret_cast<const uint4 *>(tiled + r * row_bytes + (int64_t)j * 16);
 }
 
-hipError_t launch_compact_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled,
-                               int32_t stride, uint8_t *out) {
+hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled, uint8_t *out) {
+    if (sh.tile_w != 64 || sh.num_tiles < 2) return hipErrorInvalidValue;
+    const HistLayout lay = planar_layout(sh);
     const int32_t row_bytes = sh.num_tiles * sh.tile_w;
-    if (stride % 16 || stride > row_bytes) return hipErrorInvalidValue;
-    const int64_t n = sh.rows * (stride / 16);
+    const int64_t n = sh.rows * (4 * lay.last_tile + lay.last_stride / 16);
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_compact_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, tiled,
-                       sh.rows, row_bytes, stride, out);
+    hipLaunchKernelGGL(k_planar_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, tiled,
+                       sh.rows, row_bytes, lay, out);
     return hipGetLastError();
 }
 

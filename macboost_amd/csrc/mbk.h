@@ -174,19 +174,34 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order);
 
+// Where the histogram kernel finds tile t of row r: at
+// base + t * tile_step + r * (t == last_tile ? last_stride : stride).
+struct HistLayout {
+    int64_t tile_step;
+    int32_t stride;
+    int32_t last_stride;
+    int32_t last_tile;
+};
+// The gather layout [rows][T][W]: tile_step W, both strides T * W.
+HistLayout gather_layout(const Shape &sh);
+// The planar root copy [T][rows][...] (launch_planar_rows): tile t < T - 1 at
+// t * rows * 64 with stride 64, the last tile with stride ceil(F_last/16)*16.
+// Each tile's bytes are then contiguous, so the two tile workgroups of a row
+// chunk stream their own planes.  Only for W = 64 and T >= 2.
+HistLayout planar_layout(const Shape &sh);
+size_t planar_bytes(const Shape &sh);    // including 64 zero bytes of overread
+
 // Histogram items -> packed partials [item][B][W] (64-bit words, see
-// HIST_QH_BITS).
-// row_stride 0: the gather layout's T * W; else the compact root copy's
-// stride (a 16-B multiple, launch_compact_rows).
+// HIST_QH_BITS).  layout null: the gather layout.
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
-                       uint64_t *partials, int grid, int64_t row_stride = 0);
+                       uint64_t *partials, int grid, const HistLayout *layout = nullptr);
 size_t hist_lds_size();   // static LDS of one histogram workgroup
-// Compact copy of the gather layout (row stride `stride` < T * W, 16-B
-// multiple) for streaming passes over every row; out holds rows * stride
-// bytes plus 64 zero bytes (the last row's last tile reads past its end).
-hipError_t launch_compact_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled,
-                               int32_t stride, uint8_t *out);
+// Planar copy of the gather layout for the root pass over every row; out
+// holds planar_bytes(sh) bytes (the last tile's loads run up to 16 B past its
+// rows into the zeroed tail, and into the next row's bytes, which land in
+// padding columns).
+hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled, uint8_t *out);
 
 // Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
 struct LevelArgs {

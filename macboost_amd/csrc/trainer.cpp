@@ -203,8 +203,9 @@ struct Trainer {
     float base = 0.0f;
 
     DevBuf<uint8_t> bins_tiled, bins_fm, vbins_fm;
-    DevBuf<uint8_t> bins_root;      // compact copy of bins_tiled for the root pass
-    int64_t root_stride = 0;        // its row stride (0: no copy)
+    DevBuf<uint8_t> bins_root;      // planar copy of bins_tiled for the root pass
+    bool has_root_copy = false;
+    mbk::HistLayout root_layout{};
     DevBuf<float> labels, weights, preds, vpreds;
     DevBuf<uint8_t> is_cat, feat_mask;
     DevBuf<int8_t> mono;
@@ -607,19 +608,23 @@ static void bin_valid(Trainer &t, const float *xv, int64_t vrows, const float *e
 }
 
 // Labels, weights, predictions and the tree-build buffers.
-// The root histogram streams every row: with 64-wide tiles it reads T * 64 B
-// per row although the features fill only ceil(F/16)*16 of them (112 of 128
-// at F = 100), so it gets a compact copy at that stride.
+// The root histogram streams every row.  With 64-wide tiles the gather layout
+// holds T * 64 B per row although the features fill only ceil(F/16)*16 of
+// them (112 of 128 at F = 100), and the two tile workgroups of a row chunk
+// read halves of the same lines.  The planar copy stores each tile's bytes
+// contiguously at that width, so each workgroup streams its own plane.
 static void build_root_copy(Trainer &t) {
-    t.root_stride = 0;
+    t.has_root_copy = false;
     if (t.sh.tile_w != 64 || t.sh.num_tiles < 2) return;
-    const int64_t stride = (t.cols + 15) / 16 * 16;
-    if (stride >= (int64_t)t.sh.num_tiles * 64) return;
+    const mbk::HistLayout lay = mbk::planar_layout(t.sh);
+    if (lay.last_stride >= 64) return;
     hipStream_t s = t.dev->stream;
-    t.bins_root.alloc((size_t)(t.rows * stride + 64));
-    MB_HIP(hipMemsetAsync(t.bins_root.ptr + t.rows * stride, 0, 64, s));
-    MB_HIP(mbk::launch_compact_rows(s, t.sh, t.bins_tiled.ptr, (int32_t)stride, t.bins_root.ptr));
-    t.root_stride = stride;
+    const size_t bytes = mbk::planar_bytes(t.sh);
+    t.bins_root.alloc(bytes);
+    MB_HIP(hipMemsetAsync(t.bins_root.ptr + bytes - 64, 0, 64, s));
+    MB_HIP(mbk::launch_planar_rows(s, t.sh, t.bins_tiled.ptr, t.bins_root.ptr));
+    t.root_layout = lay;
+    t.has_root_copy = true;
 }
 
 static void setup_buffers(Trainer &t, const float *y, const float *w, const float *yv) {
@@ -1043,11 +1048,11 @@ static void grow_levelwise(Trainer &t, int tree) {
             MB_HIP(hipEventCreate(&e1));
             MB_HIP(hipEventRecord(e0, s));
         }
-        // an unsampled root streams every row: the compact copy when there is one
-        const bool compact = level == 0 && !sampled && t.root_stride > 0;
-        MB_HIP(mbk::launch_hist(s, sh, compact ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
+        // an unsampled root streams every row: the planar copy when there is one
+        const bool planar = level == 0 && !sampled && t.has_root_copy;
+        MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
-                                compact ? t.root_stride : 0));
+                                planar ? &t.root_layout : nullptr));
         if (t.profiling) {
             MB_HIP(hipEventRecord(e1, s));
             t.events.push_back({e0, e1, level});
@@ -1149,10 +1154,10 @@ static void grow_leafwise(Trainer &t, int tree) {
             MB_HIP(hipEventCreate(&e1));
             MB_HIP(hipEventRecord(e0, s));
         }
-        const bool compact = step == 0 && !sampled && t.root_stride > 0;
-        MB_HIP(mbk::launch_hist(s, sh, compact ? t.bins_root.ptr : t.bins_tiled.ptr, order,
+        const bool planar = step == 0 && !sampled && t.has_root_copy;
+        MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, order,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
-                                compact ? t.root_stride : 0));
+                                planar ? &t.root_layout : nullptr));
         if (t.profiling) {
             MB_HIP(hipEventRecord(e1, s));
             t.events.push_back({e0, e1, std::min(step, 15)});
