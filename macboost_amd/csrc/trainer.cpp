@@ -620,6 +620,9 @@ static void build_root_copy(Trainer &t) {
     if (lay.last_stride >= 64) return;
     hipStream_t s = t.dev->stream;
     const size_t bytes = mbk::planar_bytes(t.sh);
+    // an optimisation only: skipped unless it leaves 1/16 of the device free
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess || free_b < bytes + (total_b >> 4)) return;
     t.bins_root.alloc(bytes);
     MB_HIP(hipMemsetAsync(t.bins_root.ptr + bytes - 64, 0, 64, s));
     MB_HIP(mbk::launch_planar_rows(s, t.sh, t.bins_tiled.ptr, t.bins_root.ptr));
