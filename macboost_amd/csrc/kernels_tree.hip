@@ -2486,19 +2486,41 @@ hipError_t launch_lw_bounds(hipStream_t s, const LWState *st, const LWOpen *open
     return hipGetLastError();
 }
 
+// The step state the partition plan needs, loaded with the rest of the step
+// state when the partition kernel starts.
+struct LWPick {
+    uint32_t count, child0, leaves, next_slot, dst;
+    int32_t node, depth, slot;
+};
+
 // Partition plan, run by one block once the left count is known: child
 // segments and covers, whether the children are evaluated, histogram slots
-// and the smaller child's items (write_items for one pair: same chunking,
-// computed by one thread from the step state the pick wrote).
-__device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWOpen *open,
-                              uint32_t left, uint32_t *slot_seg, uint32_t *slot_count,
-                              TreeCtl *ctl, Pair *pairs, HistItem *items, const TreeOut &out) {
-    __shared__ uint32_t s_n, s_seg, s_cnt, s_chunk;
+// and the smaller child's items (write_items for one pair: same chunking).
+// Every thread computes the plan from the preloaded state, so no barrier or
+// global read sits between the last cursor add and the item writes; thread 0
+// writes the scalar results.
+__device__ void lw_plan_block(const Shape &sh, const LWArgs &a, const LWPick &q, LWState *st,
+                              LWOpen *open, uint32_t left, uint32_t *slot_seg,
+                              uint32_t *slot_count, TreeCtl *ctl, Pair *pairs, HistItem *items,
+                              const TreeOut &out) {
+    const uint32_t cnt = q.count, right = cnt - left;
+    const uint32_t i0 = q.child0, i1 = i0 + 1;
+    const int32_t child_depth = q.depth + 1;
+    const bool can_eval = child_depth < a.max_depth && (int32_t)q.leaves + 1 < a.num_leaves &&
+                          left > 0 && right > 0;
+    // the smaller child (ties: left) gets a new slot; the larger one takes
+    // over the parent's slot (parent - smaller, in place)
+    const bool small_left = left <= right;
+    const uint32_t seg_s = small_left ? q.dst : q.dst + left;
+    const uint32_t cnt_s = small_left ? left : right;
+    const uint32_t T = (uint32_t)sh.num_tiles;
+    const uint32_t chunk =
+        can_eval ? item_chunk(cnt_s, 1, sh.num_tiles, a.target_items, a.min_chunk) : 1u;
+    const uint32_t nch = can_eval ? (cnt_s + chunk - 1) / chunk : 0u;
+    const uint32_t n_items = nch * T;
+    const bool fits = n_items <= sh.item_cap;
     if (threadIdx.x == 0) {
-        const LWState q = *st;
-        const uint32_t cnt = q.count, right = cnt - left;
-        const uint32_t i0 = q.child0, i1 = i0 + 1;
-        const int32_t lc = 2 * q.pick_node + 1, rc = lc + 1;
+        const int32_t lc = 2 * q.node + 1, rc = lc + 1;
         out.cover[lc] = (float)left;
         out.cover[rc] = (float)right;
         open[i0].seg = q.dst;
@@ -2506,20 +2528,11 @@ __device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWO
         open[i1].seg = q.dst + left;
         open[i1].count = right;
         st->left = left;
-        const int32_t child_depth = q.pick_depth + 1;
-        const bool can_eval = child_depth < a.max_depth &&
-                              (int32_t)q.leaves + 1 < a.num_leaves && left > 0 && right > 0;
         st->leaves = q.leaves + 1;
-        s_n = 0;
         if (can_eval) {
-            // the smaller child (ties: left) gets a new slot; the larger one
-            // takes over the parent's slot (parent - smaller, in place)
-            const bool small_left = left <= right;
-            const uint32_t s_new = q.next_slot, s_par = (uint32_t)q.pick_slot;
+            const uint32_t s_new = q.next_slot, s_par = (uint32_t)q.slot;
             st->next_slot = s_new + 1;
             const uint32_t is = small_left ? i0 : i1, il = small_left ? i1 : i0;
-            const uint32_t seg_s = small_left ? q.dst : q.dst + left;
-            const uint32_t cnt_s = small_left ? left : right;
             open[is].slot = (int32_t)s_new;
             open[il].slot = (int32_t)s_par;
             slot_seg[s_new] = seg_s;
@@ -2528,17 +2541,14 @@ __device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWO
             slot_count[s_par] = cnt - cnt_s;
             st->eval_first = i0;
             st->eval_count = 2;
-            const uint32_t chunk = item_chunk(cnt_s, 1, sh.num_tiles, a.target_items, a.min_chunk);
-            const uint32_t nch = (cnt_s + chunk - 1) / chunk;
-            const uint32_t n_items = nch * (uint32_t)sh.num_tiles;
             Pair p = {};
             p.built = s_new;
             p.derived = s_par;
             p.parent = s_par;
             ctl->chunk = chunk;
-            ctl->level_built[min(child_depth, 15)] += cnt_s;
+            atomicAdd(&ctl->level_built[min(child_depth, 15)], cnt_s);
             ctl->num_pairs = 1;
-            if (n_items > sh.item_cap) {
+            if (!fits) {
                 // never write past the item list (reported after the tree)
                 ctl->num_items = 0;
                 ctl->overflow = 1;
@@ -2546,25 +2556,20 @@ __device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWO
                 p.item_first = 0;
                 p.nchunks = nch;
                 ctl->num_items = n_items;
-                s_n = n_items;
             }
             pairs[0] = p;
-            s_seg = seg_s;
-            s_cnt = cnt_s;
-            s_chunk = chunk;
         } else {
             st->eval_count = 0;
         }
     }
-    __syncthreads();
-    const uint32_t n = s_n, T = (uint32_t)sh.num_tiles;
-    for (uint32_t it = threadIdx.x; it < n; it += blockDim.x) {
+    if (!can_eval || !fits) return;
+    for (uint32_t it = threadIdx.x; it < n_items; it += blockDim.x) {
         const uint32_t t = it % T, c = it / T;
         HistItem h;
         h.pair = 0;
         h.tile = t;
-        h.start = s_seg + c * s_chunk;
-        h.count = min(s_chunk, s_cnt - c * s_chunk);
+        h.start = seg_s + c * chunk;
+        h.count = min(chunk, cnt_s - c * chunk);
         items[it] = h;
     }
 }
@@ -2576,7 +2581,7 @@ __device__ void lw_plan_block(const Shape &sh, const LWArgs &a, LWState *st, LWO
 // cursor add reserves the segment's last entries knows the left count from
 // that add and runs the plan once its own entries are written; the plan
 // reads nothing that another block of this launch writes.
-__global__ __launch_bounds__(PART_THREADS) void k_lw_route(Shape sh, LWArgs a, LWState *st,
+__global__ __launch_bounds__(PART_THREADS, 8) void k_lw_route(Shape sh, LWArgs a, LWState *st,
                                                           LWOpen *open,
                                                           const uint8_t *__restrict__ bins_fm,
                                                           Entry *order, uint64_t *cursor,
@@ -2588,10 +2593,12 @@ __global__ __launch_bounds__(PART_THREADS) void k_lw_route(Shape sh, LWArgs a, L
     const uint32_t done = st->done, cnt = st->count, src = st->src, dst = st->dst;
     const NodeSplit sp = {st->feature, st->bin, st->flags};
     const uint32_t mask_word = threadIdx.x < 8 ? st->mask[threadIdx.x] : 0u;
+    const LWPick q = {cnt, st->child0, st->leaves, st->next_slot, dst,
+                      st->pick_node, st->pick_depth, st->pick_slot};
     if (done) return;
     if (cnt == 0) {                                  // nothing to move: plan directly
         if (blockIdx.x == 0)
-            lw_plan_block(sh, a, st, open, 0u, slot_seg, slot_count, ctl, pairs, items, out);
+            lw_plan_block(sh, a, q, st, open, 0u, slot_seg, slot_count, ctl, pairs, items, out);
         return;
     }
     if (blockIdx.x * (uint32_t)PART_BLOCK >= cnt) return;   // uniform per block
@@ -2608,7 +2615,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_lw_route(Shape sh, LWArgs a, L
             last = true;                             // uniform per block
         __syncthreads();                             // LDS reuse by the next chunk
     }
-    if (last) lw_plan_block(sh, a, st, open, left, slot_seg, slot_count, ctl, pairs, items, out);
+    if (last) lw_plan_block(sh, a, q, st, open, left, slot_seg, slot_count, ctl, pairs, items, out);
 }
 
 hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, LWState *st,
