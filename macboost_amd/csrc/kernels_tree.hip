@@ -732,6 +732,22 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
 
 // Quantise the kept entries with the weighted maxima (quantize_gradients,
 // Shaders.swift:176-192, over amplified gradients).
+// Entries move as one 64-bit word (row low, ghq high).  Order buffers are
+// written once per pass and read by the next kernels from HBM (80 MB at 10M
+// rows, far past L2), so their stores and the partition's loads are
+// nontemporal: they do not displace the lines the histogram kernel's two tile
+// workgroups share (measured: 3-4% per tree).
+__device__ __forceinline__ void store_entry_nt(Entry *p, const Entry e) {
+    __builtin_nontemporal_store((unsigned long long)e.row | ((unsigned long long)e.ghq << 32),
+                                reinterpret_cast<unsigned long long *>(p));
+}
+
+__device__ __forceinline__ Entry load_entry_nt(const Entry *p) {
+    const unsigned long long v =
+        __builtin_nontemporal_load(reinterpret_cast<const unsigned long long *>(p));
+    return Entry{(uint32_t)v, (uint32_t)(v >> 32)};
+}
+
 __global__ __launch_bounds__(256) void k_quantize_sampled(GradParams gp, SampleParams sp,
                                                           const float *__restrict__ preds,
                                                           const float *__restrict__ labels,
@@ -750,7 +766,7 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(GradParams gp, SampleP
     const int qg = (int)rintf(g * gscale);
     const uint32_t qh = (uint32_t)rintf(h * hscale);
     e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
-    order[i] = e;
+    store_entry_nt(order + i, e);
 }
 
 hipError_t launch_sample(hipStream_t s, const GradParams &gp, const SampleParams &sp,
@@ -791,7 +807,7 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
     Entry e;
     e.row = (uint32_t)i;
     e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
-    order[i] = e;
+    store_entry_nt(order + i, e);
 }
 
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
@@ -995,7 +1011,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                 for (int c = 0; c < 64 / W; ++c)
                     acc += hist_lds[(c / CPP) * 8192 + b * 32 + (c % CPP) * W + f];
             }
-            out[k] = acc;
+            __builtin_nontemporal_store(acc, &out[k]);   // read once, by k_reduce
         }
         __syncthreads();
     }
@@ -1110,12 +1126,14 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
         const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile) * stride + k;
         constexpr uint64_t HMASK = (1ull << HIST_QH_BITS) - 1;
         // four chunks per step, their loads in flight together (integer sums:
-        // the order does not matter)
+        // the order does not matter); partials are read once, so their loads
+        // and the histogram kernel's stores are nontemporal
         uint32_t c = (uint32_t)slice;
         for (; c + 3 * S < pr.nchunks; c += 4 * S) {
             uint64_t w[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = src[(size_t)(c + j * S) * cstride];
+            for (int j = 0; j < 4; ++j)
+                w[j] = __builtin_nontemporal_load(&src[(size_t)(c + j * S) * cstride]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 g += (int64_t)w[j] >> HIST_QH_BITS;
@@ -1123,7 +1141,7 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
             }
         }
         for (; c < pr.nchunks; c += S) {
-            const uint64_t w1 = src[(size_t)c * cstride];
+            const uint64_t w1 = __builtin_nontemporal_load(&src[(size_t)c * cstride]);
             g += (int64_t)w1 >> HIST_QH_BITS;
             h += (int64_t)(w1 & HMASK);
         }
@@ -1920,7 +1938,7 @@ __device__ __forceinline__ bool route_block(const NodeSplit sp, const uint32_t *
         const uint32_t i = (uint32_t)(k * PART_THREADS + tid);
         x[k] = 0;
         e[k] = Entry{0u, 0u};
-        if (i < nvalid) e[k] = src[i];
+        if (i < nvalid) e[k] = load_entry_nt(src + i);
     }
 #pragma unroll
     for (int k = 0; k < PART_PER_THREAD; ++k) {
@@ -1962,7 +1980,7 @@ __device__ __forceinline__ bool route_block(const NodeSplit sp, const uint32_t *
         if (i >= nvalid) continue;
         const uint32_t le = ex[k] + tot[k * PART_WAVES + w];
         const uint32_t pos = x[k] ? base_l + le : cnt - 1u - (base_r + (i - le));
-        dst[pos] = e[k];
+        store_entry_nt(dst + pos, e[k]);
     }
     if (base_l + base_r + nvalid != cnt) return false;
     if (left_total) *left_total = base_l + tot[PART_SLICES];
