@@ -360,9 +360,9 @@ void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_
     }
 }
 
-// Cheap target-leakage guard (Booster.swift:1771-1808).
-static void check_leakage(Trainer &t, const float *x, int64_t rows, int64_t cols, int64_t rs,
-                          int64_t cs, const float *y) {
+// Cheap target-leakage guard (Booster.swift:1771-1808); warnings go to `out`.
+static void check_leakage(bool verbose, const float *x, int64_t rows, int64_t cols, int64_t rs,
+                          int64_t cs, const float *y, std::vector<std::string> &out) {
     int64_t step = std::max<int64_t>(1, rows / 4096);
     std::vector<int64_t> idx;
     for (int64_t i = 0; i < rows; i += step) idx.push_back(i);
@@ -394,8 +394,8 @@ static void check_leakage(Trainer &t, const float *x, int64_t rows, int64_t cols
                           "|r|=%.4f on a subsample — possible target leakage (is the label or a "
                           "prediction included in X?)",
                           (long long)f, std::fabs(r));
-            t.warnings.push_back(buf);
-            if (t.p.verbose) std::printf("%s\n", buf);
+            out.push_back(buf);
+            if (verbose) std::printf("%s\n", buf);
         }
     }
 }
@@ -808,7 +808,16 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
             invalid("initModel has " + std::to_string(im->trained_num_classes) +
                     " classes, the params ask for " + std::to_string(k_want));
     }
-    check_leakage(t, x, rows, cols, rs, cs, y);
+    // the leakage check reads the host matrix only: it runs on a host thread
+    // while the device is set up and the data uploaded and binned
+    std::vector<std::string> leak_warnings;
+    struct Joiner {
+        std::thread th;
+        ~Joiner() { if (th.joinable()) th.join(); }
+    } leak;
+    leak.th = std::thread([&] {
+        check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
+    });
     validate_categoricals(p, x, rows, cols, rs, cs);
     if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
     setup_shape(t, rows, cols);
@@ -843,6 +852,8 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         MB_HIP(hipStreamSynchronize(s));
     }
     t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
+    leak.th.join();
+    t.warnings.insert(t.warnings.begin(), leak_warnings.begin(), leak_warnings.end());
     if (im) {
         // the init model's raw scores on the training (and validation) rows
         if (row_major) {

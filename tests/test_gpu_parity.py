@@ -369,6 +369,20 @@ def test_save_load_bitwise(tmp_path):
                           mb.predict(h2, x, feature_major=True))
 
 
+def test_leakage_and_bin_hint_warnings():
+    # Booster.swift:1771-1808 (a feature that is the label) and :730-738
+    # (10,000 rows at 256 bins: 39 rows per bin), in that order
+    rng = np.random.default_rng(7)
+    x = rng.random((6, 10_000), dtype=np.float32)
+    y = rng.standard_normal(10_000).astype(np.float32)
+    x[3] = y
+    h = mb.train({"num_trees": 2, "max_depth": 3}, x, y, feature_major=True)
+    w = mb.warnings(h)
+    assert len(w) == 2
+    assert "feature 3 correlates with the label" in w[0]
+    assert w[1].startswith("max_bin=256 gives ~39 rows per bin")
+
+
 # --------------------------------------------------------------------------
 # benchmark configurations (tree counts bounded by the oracle's speed)
 # --------------------------------------------------------------------------
