@@ -5,9 +5,12 @@
  * macboost_amd/ is compared with, and the timed CPU baseline of bench.py.
  * The shipped library never links or calls it.
  *
- * Single-threaded, plain C11, IEEE float semantics (built with
- * -ffp-contract=off, no fast-math).  Each function names the reference
- * file:line it follows.  Two deliberate, documented restatements:
+ * Plain C11 with OpenMP, IEEE float semantics (built with
+ * -ffp-contract=off, no fast-math).  Threads split only work whose result
+ * does not depend on the split: per-feature or per-row independent loops,
+ * integer histogram sums and maxima of f32 bit patterns, so the results
+ * are bit-identical at any thread count (orc_set_threads(1) is the scalar
+ * baseline).  Each function names the reference file:line it follows.  Two deliberate, documented restatements:
  *   1. Histogram sums are exact int64 totals of the quantised gradient words
  *      and every split candidate is dequantised once from the exact integer
  *      prefix (reference: per-4096-row-group float dequantisation + float
@@ -24,8 +27,12 @@
 
 #include <float.h>
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
+
+void orc_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : omp_get_num_procs()); }
+int32_t orc_get_threads(void) { return omp_get_max_threads(); }
 
 #define PI_F 3.14159274101257324f   /* Float.pi */
 #define GOLDEN 0x9E3779B97F4A7C15ULL
@@ -93,24 +100,28 @@ void orc_compute_edges(const float *x, int64_t rows, int32_t cols, int64_t rs,
     int32_t data_bins = num_bins - 1, num_edges = data_bins - 1;
     int64_t step = rows / sample_cap;
     if (step < 1) step = 1;
-    float *sample = (float *)malloc(sizeof(float) * (size_t)(rows / step + 1));
     memset(edges, 0, sizeof(float) * (size_t)cols * (size_t)num_edges);
-    for (int32_t f = 0; f < cols; ++f) {
-        if (is_cat && is_cat[f]) continue;
-        int64_t m = 0;
-        for (int64_t i = 0; i < rows; i += step) {
-            float v = x[i * rs + (int64_t)f * cs];
-            if (!isnan(v)) sample[m++] = v;
+#pragma omp parallel
+    {
+        float *sample = (float *)malloc(sizeof(float) * (size_t)(rows / step + 1));
+#pragma omp for schedule(dynamic, 1)
+        for (int32_t f = 0; f < cols; ++f) {
+            if (is_cat && is_cat[f]) continue;
+            int64_t m = 0;
+            for (int64_t i = 0; i < rows; i += step) {
+                float v = x[i * rs + (int64_t)f * cs];
+                if (!isnan(v)) sample[m++] = v;
+            }
+            if (m == 0) continue;                     /* all-NaN column */
+            qsort(sample, (size_t)m, sizeof(float), cmp_float);
+            for (int32_t k = 0; k < num_edges; ++k) {
+                int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
+                if (idx > m - 1) idx = m - 1;
+                edges[(int64_t)f * num_edges + k] = sample[idx];
+            }
         }
-        if (m == 0) continue;                     /* all-NaN column */
-        qsort(sample, (size_t)m, sizeof(float), cmp_float);
-        for (int32_t k = 0; k < num_edges; ++k) {
-            int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
-            if (idx > m - 1) idx = m - 1;
-            edges[(int64_t)f * num_edges + k] = sample[idx];
-        }
+        free(sample);
     }
-    free(sample);
 }
 
 uint8_t orc_bin_value(float v, const float *e, int32_t num_bins, int is_cat) {
@@ -134,6 +145,7 @@ void orc_bin_matrix(const float *x, int64_t rows, int32_t cols, int64_t rs, int6
                     const float *edges, const uint8_t *is_cat, int32_t num_bins,
                     uint8_t *bins_fm) {
     int32_t num_edges = num_bins - 2;
+#pragma omp parallel for schedule(dynamic, 1)
     for (int32_t f = 0; f < cols; ++f) {
         const float *e = edges + (int64_t)f * num_edges;
         int c = is_cat ? is_cat[f] : 0;
@@ -200,6 +212,7 @@ void orc_gradients(const float *preds, const float *y, const float *w, int64_t r
                    int32_t obj, float alpha, float aux, float *g_out, float *h_out,
                    float *max_g, float *max_h) {
     uint32_t mg = 0, mh = 0;   /* max taken on the f32 bit patterns, :87-94 */
+#pragma omp parallel for schedule(static) reduction(max : mg, mh)
     for (int64_t i = 0; i < rows; ++i) {
         float f = preds[i], yy = y[i], g, h;
         switch (obj) {
@@ -274,6 +287,7 @@ void orc_quantize(const float *g, const float *h, int64_t rows, float mg, float 
                   uint32_t *ghq) {
     float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
     float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < rows; ++i) {
         int qg = (int)rintf(g[i] * gscale);
         uint32_t qh = (uint32_t)rintf(h[i] * hscale);
@@ -305,11 +319,11 @@ void orc_hist_node(const uint8_t *bins_fm, int64_t rows, int32_t cols, int32_t n
     }
 }
 
-/* Row-major variant used inside orc_fit (same sums, cache-friendly). */
-static void hist_rows_rm(const uint8_t *rm, int32_t cols, int32_t nb, const uint32_t *ghq,
-                         const uint32_t *idx, int64_t n, int64_t *hg, int64_t *hh) {
-    memset(hg, 0, sizeof(int64_t) * (size_t)cols * (size_t)nb);
-    memset(hh, 0, sizeof(int64_t) * (size_t)cols * (size_t)nb);
+/* Row-major variant used inside orc_fit (same sums, cache-friendly).  Large
+ * nodes are split over threads, each with private tables that are then added
+ * up: integer sums, so the result does not depend on the split. */
+static void hist_rows_serial(const uint8_t *rm, int32_t cols, int32_t nb, const uint32_t *ghq,
+                             const uint32_t *idx, int64_t n, int64_t *hg, int64_t *hh) {
     for (int64_t r = 0; r < n; ++r) {
         int64_t i = idx[r];
         uint32_t q = ghq[i];
@@ -321,6 +335,38 @@ static void hist_rows_rm(const uint8_t *rm, int32_t cols, int32_t nb, const uint
             hh[k] += qh;
         }
     }
+}
+
+static void hist_rows_rm(const uint8_t *rm, int32_t cols, int32_t nb, const uint32_t *ghq,
+                         const uint32_t *idx, int64_t n, int64_t *hg, int64_t *hh) {
+    const int64_t slice = (int64_t)cols * nb;
+    memset(hg, 0, sizeof(int64_t) * (size_t)slice);
+    memset(hh, 0, sizeof(int64_t) * (size_t)slice);
+    const int nt = omp_get_max_threads();
+    if (nt <= 1 || n < 65536) {
+        hist_rows_serial(rm, cols, nb, ghq, idx, n, hg, hh);
+        return;
+    }
+    int64_t *priv = (int64_t *)calloc((size_t)nt * 2 * (size_t)slice, sizeof(int64_t));
+#pragma omp parallel num_threads(nt)
+    {
+        const int t = omp_get_thread_num(), k = omp_get_num_threads();
+        const int64_t a = n * t / k, b = n * (t + 1) / k;
+        int64_t *pg = priv + (int64_t)t * 2 * slice, *ph = pg + slice;
+        hist_rows_serial(rm, cols, nb, ghq, idx + a, b - a, pg, ph);
+#pragma omp barrier
+#pragma omp for schedule(static)
+        for (int64_t j = 0; j < slice; ++j) {
+            int64_t sg = 0, sh = 0;
+            for (int u = 0; u < k; ++u) {
+                sg += priv[(int64_t)u * 2 * slice + j];
+                sh += priv[(int64_t)u * 2 * slice + slice + j];
+            }
+            hg[j] = sg;
+            hh[j] = sh;
+        }
+    }
+    free(priv);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -698,6 +744,7 @@ static int grow_levelwise(const fit_ctx *c, float *preds, orc_forest *out, int64
 static void walk_preds(const fit_ctx *c, const orc_forest *out, int64_t base, float *preds) {
     const int32_t D = c->p->max_depth, nb = c->nb;
     const int64_t N = c->rows;
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < N; ++i) {
         int32_t n = 0;
         for (int32_t d = 0; d < D; ++d) {
@@ -766,6 +813,7 @@ static int grow_leafwise(const fit_ctx *c, float *preds, orc_forest *out, int64_
         for (int32_t i = 0; i < open_count; ++i)
             if (open[i].best_f >= 0 && isfinite(open[i].best.gain) && open[i].best.gain > bg) {
                 bg = open[i].best.gain; bi = i;
+                if (p->plant == ORC_PLANT_FIFO_PICK) break;
             }
         if (bi < 0) { done = 1; continue; }
         lw_open Lp = open[bi];
@@ -972,7 +1020,9 @@ int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, i
         if (ag >= thr) {
             keep = 1;
         } else {
-            const uint32_t hv = wang_hash((uint32_t)i ^ (seed * 0x9E3779B9u));
+            const uint32_t hv = p->plant == ORC_PLANT_GOSS_NO_SEED
+                                    ? wang_hash((uint32_t)i)
+                                    : wang_hash((uint32_t)i ^ (seed * 0x9E3779B9u));
             if ((float)(hv >> 8) * (1.0f / 16777216.0f) < other) { keep = 1; w = weight; }
         }
         const float hw = h[i] * w;
@@ -988,6 +1038,36 @@ int64_t orc_sample_rows(const orc_params *p, int32_t tree, float *g, float *h, i
     memcpy(wmax_g, &mgb, 4);
     memcpy(wmax_h, &mhb, 4);
     return n;
+}
+
+/* Per-tree feature mask (Booster.swift:684-700, :1386-1400): the allowed
+ * features, each kept with probability featureFraction by a SplitMix64
+ * stream seeded 0xC0150001 + t * golden (the uniform is drawn only for an
+ * allowed feature); if none is kept, one allowed feature is drawn with the
+ * stream's next word.  Returns 0 when every feature may split. */
+static int tree_feature_mask(const orc_params *p, int32_t t, int32_t cols, uint8_t *m) {
+    if (!p->allowed && !(p->feature_fraction < 1.0f)) return 0;
+    int32_t n_allowed = 0;
+    for (int32_t f = 0; f < cols; ++f) n_allowed += p->allowed ? p->allowed[f] != 0 : 1;
+    if (!(p->feature_fraction < 1.0f)) {
+        for (int32_t f = 0; f < cols; ++f) m[f] = p->allowed ? p->allowed[f] != 0 : 1;
+        return 1;
+    }
+    uint64_t s = 0xC0150001ULL + (uint64_t)t * GOLDEN;
+    int any = 0;
+    for (int32_t f = 0; f < cols; ++f) {
+        const int base = p->allowed ? p->allowed[f] != 0 : 1;
+        m[f] = (uint8_t)(base && orc_splitmix_uniform(&s) < p->feature_fraction);
+        any |= m[f];
+    }
+    if (!any && n_allowed > 0) {
+        int64_t k = (int64_t)(orc_splitmix_next(&s) % (uint64_t)n_allowed);
+        for (int32_t f = 0; f < cols; ++f) {
+            if (p->allowed && !p->allowed[f]) continue;
+            if (k-- == 0) { m[f] = 1; break; }
+        }
+    }
+    return 1;
 }
 
 int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t cols,
@@ -1006,14 +1086,19 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
     float *node_lo = (float *)malloc(sizeof(float) * (size_t)total);
     float *node_hi = (float *)malloc(sizeof(float) * (size_t)total);
     float *delta = (float *)malloc(sizeof(float) * (size_t)total);
+    uint8_t *fmask = (uint8_t *)malloc((size_t)cols);
     uint32_t *split_bin = out->split_bin;
-    if (!rm || !g || !h || !ghq || !kept || !sel || !node_lo || !node_hi || !delta) {
+    if (!rm || !g || !h || !ghq || !kept || !sel || !node_lo || !node_hi || !delta || !fmask) {
         free(rm); free(g); free(h); free(ghq); free(kept); free(sel);
-        free(node_lo); free(node_hi); free(delta);
+        free(node_lo); free(node_hi); free(delta); free(fmask);
         return -1;
     }
-    for (int32_t f = 0; f < cols; ++f)
-        for (int64_t i = 0; i < rows; ++i) rm[i * cols + f] = bins_fm[(int64_t)f * rows + i];
+#pragma omp parallel for schedule(static)
+    for (int64_t i0 = 0; i0 < rows; i0 += 4096) {
+        const int64_t i1 = i0 + 4096 < rows ? i0 + 4096 : rows;
+        for (int32_t f = 0; f < cols; ++f)
+            for (int64_t i = i0; i < i1; ++i) rm[i * cols + f] = bins_fm[(int64_t)f * rows + i];
+    }
     if (!split_bin) out->split_bin = (uint32_t *)calloc((size_t)out->num_trees * total, 4);
     int rc = 0;
     const int32_t K = p->num_classes > 1 ? p->num_classes : 1;
@@ -1055,8 +1140,9 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
         c.apply_preds = rows_in == NULL && !renewal;
         c.node_lo = renewal ? node_lo : NULL;
         c.node_hi = renewal ? node_hi : NULL;
-        rc = p->num_leaves > 0 ? grow_leafwise(&c, pc, out, base, NULL)
-                               : grow_levelwise(&c, pc, out, base, NULL);
+        const uint8_t *tm = tree_feature_mask(p, t, cols, fmask) ? fmask : NULL;
+        rc = p->num_leaves > 0 ? grow_leafwise(&c, pc, out, base, tm)
+                               : grow_levelwise(&c, pc, out, base, tm);
         if (rc == 0 && renewal) {
             const float q = p->objective == ORC_OBJ_MAE ? 0.5f : p->alpha;
             if (p->num_leaves > 0) {
@@ -1105,7 +1191,7 @@ int orc_fit(const orc_params *p, const uint8_t *bins_fm, int64_t rows, int32_t c
     }
     if (!split_bin) { free(out->split_bin); out->split_bin = NULL; }
     free(rm); free(g); free(h); free(ghq); free(kept); free(sel);
-    free(node_lo); free(node_hi); free(delta);
+    free(node_lo); free(node_hi); free(delta); free(fmask);
     return rc;
 }
 
@@ -1130,6 +1216,8 @@ static inline int raw_goes_left(const orc_forest *m, int64_t k, float v, int32_t
 void orc_predict(const orc_forest *m, float base, int32_t data_bins, const float *x,
                  int64_t rows, int32_t cols, float *out) {
     (void)cols;
+    /* rows in chunks of 16,384 over the host cores (Booster.swift:2041-2045) */
+#pragma omp parallel for schedule(dynamic, 16384)
     for (int64_t i = 0; i < rows; ++i) {
         float acc = base;
         for (int32_t t = 0; t < m->num_trees; ++t) {
@@ -1249,17 +1337,22 @@ void orc_treeshap(const orc_forest *m, float base, int32_t data_bins, const floa
                   int64_t rows, int32_t cols, float *out) {             /* :170-209 */
     int32_t width = cols + 1;
     double bias = orc_shap_bias(m, base);
-    double *phi = (double *)malloc(sizeof(double) * (size_t)width);
-    pe_t empty[1];
-    for (int64_t i = 0; i < rows; ++i) {
-        for (int32_t j = 0; j < width; ++j) phi[j] = 0;
-        for (int32_t t = 0; t < m->num_trees; ++t) {
-            int64_t tb = (int64_t)t * m->nodes_per_tree;
-            if (m->cover[tb] > 0)
-                shap_recurse(m, tb, 0, empty, 0, 1.0, 1.0, -1, x, i, rows, data_bins, phi);
+    /* rows in chunks of 512 over the host cores (SHAP.swift:179-183) */
+#pragma omp parallel
+    {
+        double *phi = (double *)malloc(sizeof(double) * (size_t)width);
+        pe_t empty[1];
+#pragma omp for schedule(dynamic, 512)
+        for (int64_t i = 0; i < rows; ++i) {
+            for (int32_t j = 0; j < width; ++j) phi[j] = 0;
+            for (int32_t t = 0; t < m->num_trees; ++t) {
+                int64_t tb = (int64_t)t * m->nodes_per_tree;
+                if (m->cover[tb] > 0)
+                    shap_recurse(m, tb, 0, empty, 0, 1.0, 1.0, -1, x, i, rows, data_bins, phi);
+            }
+            for (int32_t f = 0; f < cols; ++f) out[i * width + f] = (float)phi[f];
+            out[i * width + cols] = (float)bias;
         }
-        for (int32_t f = 0; f < cols; ++f) out[i * width + f] = (float)phi[f];
-        out[i * width + cols] = (float)bias;
+        free(phi);
     }
-    free(phi);
 }

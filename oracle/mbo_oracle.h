@@ -47,7 +47,19 @@ typedef struct {
     float goss_other_rate;
     float subsample;           /* bagging fraction, 1 = off */
     int32_t num_classes;       /* multiclass K (3..128), else 1 */
+    float feature_fraction;    /* per-tree column sample (colsample_bytree), 1 = off */
+    int32_t plant;             /* TEST ONLY: a planted mistake (ORC_PLANT_*), 0 = faithful */
+    const uint8_t *allowed;    /* [cols] 1 = the feature may split, NULL = every feature */
 } orc_params;
+
+/* Planted mistakes, for tests that show a property check catches them.
+ * Never set outside tests/. */
+#define ORC_PLANT_FIFO_PICK 1      /* leaf-wise: first open leaf with gain > min, not the best */
+#define ORC_PLANT_GOSS_NO_SEED 2   /* GOSS/bagging keep hash without the tree seed */
+
+/* OpenMP threads used by every parallel loop (<= 0: all processors). */
+void orc_set_threads(int32_t n);
+int32_t orc_get_threads(void);
 
 /* One split candidate result: SplitResult (Shaders.swift:334) plus the exact
  * integer left sums the decision step needs. */

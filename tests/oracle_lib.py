@@ -16,11 +16,25 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent.parent
 LIB_PATH = ROOT / "oracle" / "liboracle.so"
 
+# planted mistakes (oracle/mbo_oracle.h ORC_PLANT_*): tests only
+PLANT_FIFO_PICK = 1
+PLANT_GOSS_NO_SEED = 2
+
 FLAG_DEFAULT_LEFT = 1
 FLAG_CATEGORICAL = 2
 OBJ_L2, OBJ_LOGISTIC, OBJ_MAE, OBJ_HUBER, OBJ_QUANTILE, OBJ_POISSON, OBJ_TWEEDIE, OBJ_MULTICLASS = range(8)
 
 _lib = None
+
+
+def set_threads(n: int) -> None:
+    """Threads of the oracle's parallel loops (<= 0: every processor).  Results
+    are identical at any count."""
+    lib().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().orc_get_threads())
 
 
 def build() -> None:
@@ -47,7 +61,8 @@ class OrcParams(ctypes.Structure):
         ("alpha", ctypes.c_float), ("aux", ctypes.c_float),
         ("goss", ctypes.c_int32), ("goss_top_rate", ctypes.c_float),
         ("goss_other_rate", ctypes.c_float), ("subsample", ctypes.c_float),
-        ("num_classes", ctypes.c_int32),
+        ("num_classes", ctypes.c_int32), ("feature_fraction", ctypes.c_float),
+        ("plant", ctypes.c_int32), ("allowed", ctypes.c_void_p),
     ]
 
 
@@ -76,6 +91,10 @@ _F = ctypes.c_float
 
 
 def _configure(l: ctypes.CDLL) -> None:
+    l.orc_set_threads.restype = None
+    l.orc_set_threads.argtypes = [ctypes.c_int32]
+    l.orc_get_threads.restype = ctypes.c_int32
+    l.orc_get_threads.argtypes = []
     l.orc_splitmix_next.restype = ctypes.c_uint64
     l.orc_splitmix_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
     l.orc_friedman.argtypes = [_I64, _I32, ctypes.c_uint64, _F, _P, _P]
@@ -305,12 +324,18 @@ def fit(bins_fm, y, *, edges, num_trees=100, max_depth=6, num_bins=256, objectiv
         num_leaves=0, learning_rate=0.1, lam=1.0, min_child_hess=1.0, min_split_gain=0.0,
         cat_smooth=10.0, alpha=0.9, aux=1.0, w=None, is_cat=None, monotone=None,
         base=None, goss=False, goss_top_rate=0.2, goss_other_rate=0.1,
-        subsample=1.0, num_classes=1, init_preds=None) -> OracleModel:
+        subsample=1.0, num_classes=1, init_preds=None, feature_fraction=1.0,
+        allowed_features=None, plant=0) -> OracleModel:
     cols, rows = bins_fm.shape
     K = num_classes if objective == OBJ_MULTICLASS else 1
+    allowed = None
+    if allowed_features is not None:
+        allowed = np.zeros(cols, np.uint8)
+        allowed[list(allowed_features)] = 1
     p = OrcParams(num_trees, max_depth, num_bins, objective, num_leaves, learning_rate, lam,
                   min_child_hess, min_split_gain, cat_smooth, alpha, aux, int(goss),
-                  goss_top_rate, goss_other_rate, subsample, K)
+                  goss_top_rate, goss_other_rate, subsample, K, feature_fraction, plant,
+                  None if allowed is None else allowed.ctypes.data)
     y = np.ascontiguousarray(y, np.float32)
     w = None if w is None else np.ascontiguousarray(w, np.float32)
     bases = None
@@ -388,11 +413,11 @@ def shap_bias(forest: Forest, base: float) -> float:
 
 
 def sample_rows(g, h, max_g, tree, *, learning_rate=0.1, goss=False, goss_top_rate=0.2,
-                goss_other_rate=0.1, subsample=1.0):
+                goss_other_rate=0.1, subsample=1.0, plant=0):
     """orc_sample_rows: (kept mask, amplified g, amplified h, wmax_g, wmax_h),
     or None when the tree does not sample."""
     p = OrcParams(1, 6, 256, OBJ_L2, 0, learning_rate, 1.0, 1.0, 0.0, 10.0, 0.9, 1.0,
-                  int(goss), goss_top_rate, goss_other_rate, subsample)
+                  int(goss), goss_top_rate, goss_other_rate, subsample, 1, 1.0, plant, None)
     l = lib()
     l.orc_sampling_active.restype = ctypes.c_int
     l.orc_sampling_active.argtypes = [ctypes.c_void_p, ctypes.c_int32]
