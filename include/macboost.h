@@ -200,6 +200,13 @@ void *mbx_dataset_train(const char *params_json, void *dataset, const float *w,
                         char **err);
 void mbx_dataset_free(void *dataset);
 
+/* The per-iteration validation metric of the fit (MacBooster.evalHistory,
+ * Booster.swift:239, :1672): one value per boosting round, including the
+ * rounds after the best one that early stopping examined.  Copies at most
+ * cap values into out (which may be NULL when cap is 0) and returns the
+ * history's length, or -1 for a NULL handle. */
+int64_t mbx_eval_history(void *handle, float *out, int64_t cap);
+
 /* SplitMix64 Friedman #1 generator (DataGen.swift:68-94), multithreaded:
  * x feature-major [cols][rows], y[rows]. */
 void mbx_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise, float *x, float *y);

@@ -5,7 +5,8 @@ The compute lives in ``libmacboostc.so`` (HIP kernels + C++ host, built from
 entry points as the reference binding (python/macboost/_core.py).
 """
 from ._core import (  # noqa: F401
-    Context, Dataset, MacBoostError, Trainer, best_iteration, feature_importance, friedman,
+    Context, Dataset, MacBoostError, Trainer, best_iteration, eval_history,
+    feature_importance, friedman,
     load, num_classes, num_features, num_trees, predict, predict_contrib, save,
     select_features, train, train_dataset, version, warnings,
 )

@@ -140,6 +140,8 @@ def _configure(l):
     l.mbx_friedman.restype = None
     l.mbx_friedman.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float,
                                _P, _P]
+    l.mbx_eval_history.restype = ctypes.c_int64
+    l.mbx_eval_history.argtypes = [_P, _P, ctypes.c_int64]
     l.mbx_version.restype = ctypes.c_char_p
     l.mbx_version.argtypes = []
     l.mbx_dataset_make.restype = ctypes.c_void_p
@@ -175,22 +177,36 @@ EXPORTED = (
     "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
     "mbx_version", "mbx_dataset_make", "mbx_dataset_save", "mbx_dataset_load",
     "mbx_dataset_info", "mbx_dataset_copy", "mbx_dataset_feature_names", "mbx_dataset_train",
-    "mbx_dataset_free",
+    "mbx_dataset_free", "mbx_eval_history",
 )
 
 
 def _take_error(err: ctypes.c_char_p) -> str:
-    msg = err.value.decode() if err.value else "unknown error"
+    """The library's malloc'd error text; the C string is released here."""
+    text = (err.value or b"unknown error").decode()
     lib().macboost_free_string(ctypes.cast(err, ctypes.c_void_p))
-    return msg
+    return text
+
+
+def _matrix(X, name="X") -> np.ndarray:
+    m = np.asarray(X, dtype=np.float32)
+    if m.ndim != 2:
+        raise ValueError(f"{name} must be 2-dimensional, got shape {m.shape}")
+    return m
 
 
 def _feature_major(X):
-    a = np.asarray(X, dtype=np.float32)
-    if a.ndim != 2:
-        raise ValueError(f"X must be 2-dimensional, got shape {a.shape}")
-    rows, cols = a.shape
-    return np.ascontiguousarray(a.T), rows, cols
+    """A (rows, cols) matrix as a contiguous [cols][rows] float32 copy."""
+    m = _matrix(X)
+    return np.ascontiguousarray(m.T), m.shape[0], m.shape[1]
+
+
+def _column(v, rows: int, what: str) -> np.ndarray:
+    """A label or weight vector: float32, flattened, one value per row."""
+    a = np.ascontiguousarray(np.asarray(v, dtype=np.float32).ravel())
+    if a.shape[0] != rows:
+        raise ValueError(f"{what} has {a.shape[0]} rows, X has {rows}")
+    return a
 
 
 def _f32(a):
@@ -198,38 +214,46 @@ def _f32(a):
 
 
 class _Handle:
-    """Owns a booster handle and frees it on GC."""
+    """A booster handle; the booster is released with the Python object."""
 
     def __init__(self, ptr: int):
         self.ptr = ptr
 
     def __del__(self):
-        if getattr(self, "ptr", None) and _lib_instance is not None:
-            _lib_instance.macboost_free(self.ptr)
-            self.ptr = None
+        ptr, self.ptr = getattr(self, "ptr", None), None
+        if ptr and _lib_instance is not None:
+            _lib_instance.macboost_free(ptr)
+
+
+def _eval_arrays(eval_set, cols: int):
+    """(feature-major X, y, rows) of a validation set, shape-checked against
+    the training matrix (the library reads rows*cols and rows floats)."""
+    if eval_set is None:
+        return None, None, 0
+    xv, yv = eval_set
+    xf, vrows, vcols = _feature_major(xv)
+    if vcols != cols:
+        raise ValueError("eval_set feature count differs from X")
+    ya = np.ascontiguousarray(np.asarray(yv, dtype=np.float32).ravel())
+    if ya.shape[0] != vrows:
+        raise ValueError("eval_set X/y row mismatch")
+    return xf, ya, vrows
 
 
 def _prep_train(config, X, y, eval_set, sample_weight, layout_fm=False):
-    a = np.asarray(X, dtype=np.float32)
+    """Every input of macboost_train, checked before the library reads it:
+    X is (rows, cols) row-major, or (cols, rows) with layout_fm."""
+    m = _matrix(X)
+    xf = np.ascontiguousarray(m)
     if layout_fm:
-        xf = np.ascontiguousarray(a, dtype=np.float32)
         cols, rows = xf.shape
-        row_major = 0
     else:
-        if a.ndim != 2:
-            raise ValueError(f"X must be 2-dimensional, got shape {a.shape}")
-        xf = np.ascontiguousarray(a)
         rows, cols = xf.shape
-        row_major = 1
-    yv = np.ascontiguousarray(y, dtype=np.float32)
-    w = None if sample_weight is None else np.ascontiguousarray(sample_weight, dtype=np.float32)
-    xv = yvv = None
-    vrows = 0
-    if eval_set is not None:
-        xv, vrows, vcols = _feature_major(eval_set[0])
-        yvv = np.ascontiguousarray(eval_set[1], dtype=np.float32)
+    yv = _column(y, rows, "y")
+    w = None if sample_weight is None else _column(sample_weight, rows, "sample_weight")
+    xv, yvv, vrows = _eval_arrays(eval_set, cols)
     cfg = json.dumps(config).encode()
-    return cfg, xf, rows, cols, row_major, yv, w, xv, vrows, yvv
+    return cfg, xf, rows, cols, 0 if layout_fm else 1, yv, w, xv, vrows, yvv
 
 
 def train(config: dict, X, y, eval_set=None, sample_weight=None, feature_major=False) -> _Handle:
@@ -248,15 +272,9 @@ def select_features(config: dict, X, y, sample_weight=None, rounds: int = 20, tr
                     alpha: float = 0.05, seed: int = 0, feature_major=False):
     """macboost_select_features (Boruta, CAPI.swift:138-183): (hits, decision
     2 confirmed / 1 tentative / 0 rejected, gain ratio) per feature."""
-    if feature_major:
-        xf = np.ascontiguousarray(X, dtype=np.float32)
-        cols, rows = xf.shape
-    else:
-        xf, rows, cols = _feature_major(X)
-    ya = np.ascontiguousarray(np.asarray(y, dtype=np.float32).ravel())
-    if ya.shape[0] != rows:
-        raise ValueError(f"y has {ya.shape[0]} rows, X has {rows}")
-    wa = None if sample_weight is None else np.ascontiguousarray(sample_weight, dtype=np.float32)
+    xf, rows, cols = _as_feature_major(X, feature_major)
+    ya = _column(y, rows, "y")
+    wa = None if sample_weight is None else _column(sample_weight, rows, "sample_weight")
     hits = np.empty(cols, np.int32)
     decision = np.empty(cols, np.int32)
     ratio = np.empty(cols, np.float32)
@@ -270,12 +288,16 @@ def select_features(config: dict, X, y, sample_weight=None, rounds: int = 20, tr
     return hits, decision, ratio
 
 
-def predict(handle: _Handle, X, feature_major=False) -> np.ndarray:
+def _as_feature_major(X, feature_major):
+    """(contiguous [cols][rows] float32, rows, cols) from either layout."""
     if feature_major:
-        xf = np.ascontiguousarray(X, dtype=np.float32)
-        cols, rows = xf.shape
-    else:
-        xf, rows, cols = _feature_major(X)
+        xf = np.ascontiguousarray(_matrix(X))
+        return xf, xf.shape[1], xf.shape[0]
+    return _feature_major(X)
+
+
+def predict(handle: _Handle, X, feature_major=False) -> np.ndarray:
+    xf, rows, cols = _as_feature_major(X, feature_major)
     k = max(1, num_classes(handle))
     out = np.empty(rows * k, dtype=np.float32)
     err = ctypes.c_char_p()
@@ -285,11 +307,7 @@ def predict(handle: _Handle, X, feature_major=False) -> np.ndarray:
 
 
 def predict_contrib(handle: _Handle, X, feature_major=False) -> np.ndarray:
-    if feature_major:
-        xf = np.ascontiguousarray(X, dtype=np.float32)
-        cols, rows = xf.shape
-    else:
-        xf, rows, cols = _feature_major(X)
+    xf, rows, cols = _as_feature_major(X, feature_major)
     k = max(1, num_classes(handle))
     out = np.empty(rows * k * (cols + 1), dtype=np.float32)
     err = ctypes.c_char_p()
@@ -344,6 +362,15 @@ def warnings(handle) -> list[str]:
     s = ctypes.cast(p, ctypes.c_char_p).value.decode()
     lib().macboost_free_string(p)
     return s.split("\n")
+
+
+def eval_history(handle) -> np.ndarray:
+    """The validation metric after every boosting round of the fit."""
+    n = int(lib().mbx_eval_history(handle.ptr, None, 0))
+    out = np.empty(max(n, 0), np.float32)
+    if n > 0:
+        lib().mbx_eval_history(handle.ptr, out.ctypes.data, n)
+    return out
 
 
 def version() -> str:
@@ -493,13 +520,15 @@ class Dataset:
 
     @classmethod
     def make(cls, config: dict, X, y, feature_names=None, feature_major=False) -> "Dataset":
-        a = np.asarray(X, dtype=np.float32)
-        xf = np.ascontiguousarray(a)
+        xf = np.ascontiguousarray(_matrix(X))
         if feature_major:
             cols, rows = xf.shape
         else:
             rows, cols = xf.shape
-        yv = np.ascontiguousarray(y, dtype=np.float32)
+        yv = _column(y, rows, "y")
+        if feature_names is not None and len(feature_names) != cols:
+            raise ValueError(f"feature_names has {len(feature_names)} entries, X has {cols} "
+                             "features")
         names = None if feature_names is None else json.dumps(list(feature_names)).encode()
         err = ctypes.c_char_p()
         ptr = lib().mbx_dataset_make(json.dumps(config).encode(), _f32(xf), rows, cols,
@@ -573,12 +602,9 @@ class Dataset:
 def train_dataset(config: dict, dataset: Dataset, eval_set=None, sample_weight=None) -> _Handle:
     """fit(dataset:) (Booster.swift:375-389): the dataset's bins, bin count,
     categorical layout and labels are used."""
-    w = None if sample_weight is None else np.ascontiguousarray(sample_weight, dtype=np.float32)
-    xv = yvv = None
-    vrows = 0
-    if eval_set is not None:
-        xv, vrows, _ = _feature_major(eval_set[0])
-        yvv = np.ascontiguousarray(eval_set[1], dtype=np.float32)
+    rows, cols = dataset.rows, dataset.cols
+    w = None if sample_weight is None else _column(sample_weight, rows, "sample_weight")
+    xv, yvv, vrows = _eval_arrays(eval_set, cols)
     err = ctypes.c_char_p()
     ptr = lib().mbx_dataset_train(json.dumps(config).encode(), dataset.ptr, _f32(w), _f32(xv),
                                   vrows, _f32(yvv), ctypes.byref(err))

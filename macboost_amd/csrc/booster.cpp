@@ -303,6 +303,63 @@ void Booster::predict_contrib(const float *x, int64_t rows, int64_t cols, float 
     }
 }
 
+// TreeSHAP path tables (extractShapPaths, SHAP.swift:79-114) of trees
+// first, first + step, ...: one path per reachable leaf, taken leaf by leaf in
+// heap order.  A leaf's splits are found by climbing parent links
+// ((n - 1) / 2) to the root and stored root first; each element carries the
+// cover fraction of the child the path takes (0x100 in its flags when that
+// child is the left one), and repeated features on a path share one unique
+// slot whose zero fraction is the product of theirs.  A tree whose root is a
+// leaf contributes only to the bias.
+ShapTables shap_tables(const std::vector<Tree> &trees, size_t first, size_t step,
+                       int nodes_per_tree) {
+    ShapTables st;
+    std::vector<uint8_t> reach;
+    std::vector<int> up;
+    for (size_t t = first; t < trees.size(); t += step) {
+        const Tree &tr = trees[t];
+        const int nn = (int)tr.feature.size();
+        if (tr.cover.size() != tr.feature.size() || !(tr.cover[0] > 0)) continue;
+        reach.assign((size_t)nn, 0);
+        reach[0] = 1;
+        for (int n = 0; 2 * n + 2 < nn; ++n)
+            if (reach[(size_t)n] && tr.feature[(size_t)n] >= 0)
+                reach[(size_t)(2 * n + 1)] = reach[(size_t)(2 * n + 2)] = 1;
+        for (int leaf = 1; leaf < nn; ++leaf) {
+            if (!reach[(size_t)leaf] || tr.feature[(size_t)leaf] >= 0) continue;
+            up.clear();
+            for (int c = leaf; c > 0; c = (c - 1) / 2) up.push_back(c);
+            if (up.size() > 12) internal("TreeSHAP supports paths of at most 12 splits");
+            mbk::ShapPath P{};
+            P.elem_start = (int32_t)st.elems.size();
+            P.num_elem = (int32_t)up.size();
+            P.uniq_start = (int32_t)st.uniq.size();
+            P.leaf = (double)tr.leaf[(size_t)leaf];
+            for (size_t j = up.size(); j-- > 0;) {
+                const int child = up[j], parent = (child - 1) / 2;
+                const int32_t f = tr.feature[(size_t)parent];
+                const double cp = (double)tr.cover[(size_t)parent];
+                const double zf = cp > 0 ? (double)tr.cover[(size_t)child] / cp : 0.0;
+                int32_t u = 0;
+                while (P.uniq_start + u < (int32_t)st.uniq.size() &&
+                       st.uniq[(size_t)(P.uniq_start + u)].feature != f)
+                    ++u;
+                if (P.uniq_start + u == (int32_t)st.uniq.size())
+                    st.uniq.push_back(mbk::ShapUniq{f, 0, 1.0});
+                st.uniq[(size_t)(P.uniq_start + u)].zero *= zf;
+                const uint32_t side = child == 2 * parent + 1 ? 0x100u : 0u;
+                st.elems.push_back(mbk::ShapElem{(int32_t)(t * (size_t)nodes_per_tree + (size_t)parent),
+                                                 f, tr.threshold[(size_t)parent],
+                                                 (uint32_t)tr.flags[(size_t)parent] | side, u, 0});
+            }
+            P.num_uniq = (int32_t)st.uniq.size() - P.uniq_start;
+            st.max_elems = std::max(st.max_elems, P.num_elem);
+            st.paths.push_back(P);
+        }
+    }
+    return st;
+}
+
 // TreeSHAP of the trees of class k (every tree when K = 1) into out
 // [rows][cols + 1].
 void Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k, float *out) {
@@ -311,60 +368,10 @@ void Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k, f
     const float bias = (float)shap_bias(k);
     if (rows <= 0) return;
     build_forest();
-    std::vector<mbk::ShapPath> paths;
-    std::vector<mbk::ShapElem> elems;
-    std::vector<mbk::ShapUniq> uniq;
-    struct PE { int node, feature; float thr; uint32_t flags; double zf; };
-    for (size_t t = (size_t)k; t < trees.size(); t += (size_t)K) {
-        const Tree &tr = trees[t];
-        if (tr.cover.size() != tr.feature.size() || !(tr.cover[0] > 0)) continue;
-        std::vector<std::pair<int, std::vector<PE>>> stack;
-        stack.push_back({0, {}});
-        while (!stack.empty()) {
-            auto item = std::move(stack.back());
-            stack.pop_back();
-            const int n = item.first;
-            std::vector<PE> &path = item.second;
-            if (tr.feature[n] < 0) {
-                if (path.empty()) continue;               // root-is-leaf: bias only
-                mbk::ShapPath P{};
-                P.elem_start = (int32_t)elems.size();
-                P.num_elem = (int32_t)path.size();
-                P.uniq_start = (int32_t)uniq.size();
-                P.leaf = (double)tr.leaf[n];
-                std::vector<int> feats;
-                for (const PE &e : path) {
-                    int u = -1;
-                    for (size_t k = 0; k < feats.size(); ++k)
-                        if (feats[k] == e.feature) { u = (int)k; break; }
-                    if (u < 0) {
-                        u = (int)feats.size();
-                        feats.push_back(e.feature);
-                        uniq.push_back(mbk::ShapUniq{e.feature, 0, 1.0});
-                    }
-                    uniq[(size_t)P.uniq_start + (size_t)u].zero *= e.zf;
-                    elems.push_back(mbk::ShapElem{e.node, e.feature, e.thr, e.flags, u, 0});
-                }
-                P.num_uniq = (int32_t)feats.size();
-                paths.push_back(P);
-                continue;
-            }
-            if (path.size() + 1 > 12) internal("TreeSHAP supports paths of at most 12 splits");
-            const double cn = (double)tr.cover[n];
-            for (int side = 0; side < 2; ++side) {
-                const int child = 2 * n + 1 + side;
-                PE e;
-                e.node = (int)(t * (size_t)forest.nodes_per_tree + (size_t)n);
-                e.feature = tr.feature[n];
-                e.thr = tr.threshold[n];
-                e.flags = (uint32_t)tr.flags[n] | (side == 0 ? 0x100u : 0u);
-                e.zf = cn > 0 ? (double)tr.cover[child] / cn : 0.0;
-                std::vector<PE> np = path;
-                np.push_back(e);
-                stack.push_back({child, std::move(np)});
-            }
-        }
-    }
+    const ShapTables st = shap_tables(trees, (size_t)k, (size_t)K, forest.nodes_per_tree);
+    const std::vector<mbk::ShapPath> &paths = st.paths;
+    const std::vector<mbk::ShapElem> &elems = st.elems;
+    const std::vector<mbk::ShapUniq> &uniq = st.uniq;
     if (paths.empty()) {
         for (int64_t i = 0; i < rows; ++i) {
             std::fill(out + (size_t)(i * width), out + (size_t)(i * width + cols), 0.0f);
@@ -384,11 +391,9 @@ void Booster::contrib_class(const float *x, int64_t rows, int64_t cols, int k, f
     DevBuf<double> phi;
     if (mbk::treeshap_needs_scratch((int)cols))
         phi.alloc((size_t)((rows + 63) / 64) * 64 * (size_t)cols);
-    int32_t max_elems = 1;
-    for (const mbk::ShapPath &P : paths) max_elems = std::max(max_elems, P.num_elem);
     MB_HIP(mbk::launch_treeshap(d.stream, xd.ptr, rows, (int)cols, trained_num_bins - 1,
                                 forest.has_mask ? forest.mask.ptr : nullptr, pd.ptr,
-                                (int)paths.size(), max_elems, ed.ptr, ud.ptr, bias, od.ptr,
+                                (int)paths.size(), st.max_elems, ed.ptr, ud.ptr, bias, od.ptr,
                                 phi.ptr));
     download(out, od.ptr, od.bytes(), d.stream);
 }
@@ -999,6 +1004,15 @@ void *mbx_dataset_train(const char *params_json, void *ds, const float *w, const
 }
 
 void mbx_dataset_free(void *ds) { delete static_cast<mb::BinnedDataset *>(ds); }
+
+int64_t mbx_eval_history(void *handle, float *out, int64_t cap) {
+    if (!handle) return -1;
+    const auto &hist = static_cast<Booster *>(handle)->eval_history;
+    const int64_t n = (int64_t)hist.size();
+    if (out)
+        for (int64_t i = 0; i < std::min(n, cap); ++i) out[i] = hist[(size_t)i];
+    return n;
+}
 
 void mbx_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise, float *x, float *y) {
     // DataGen.swift:68-94: one SplitMix64 stream per feature, one per

@@ -193,6 +193,17 @@ BinnedDataset *dataset_load(const std::string &path);
 
 Booster *load_model_file(const std::string &path);
 
+// Root-to-leaf path tables of trees first, first + step, ... for the TreeSHAP
+// kernels; max_elems is the longest path's split count.
+struct ShapTables {
+    std::vector<mbk::ShapPath> paths;
+    std::vector<mbk::ShapElem> elems;
+    std::vector<mbk::ShapUniq> uniq;
+    int32_t max_elems = 1;
+};
+ShapTables shap_tables(const std::vector<Tree> &trees, size_t first, size_t step,
+                       int nodes_per_tree);
+
 // Incremental trainer (fitImpl, Booster.swift:445-1701).
 struct Trainer;
 Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t cols,

@@ -10,6 +10,7 @@
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -360,43 +361,54 @@ void validate_categoricals(const Params &p, const float *x, int64_t rows, int64_
     }
 }
 
-// Cheap target-leakage guard (Booster.swift:1771-1808); warnings go to `out`.
+// Target-leakage guard (Booster.swift:1771-1808).  On every
+// max(1, rows / 4096)-th row (at least 50 of them), each feature's finite
+// values are correlated with the label (Pearson r, the label centred on its
+// mean over all sampled rows); |r| > 0.999 over at least 50 finite values
+// adds a warning to `out` (and prints it when verbose).
 static void check_leakage(bool verbose, const float *x, int64_t rows, int64_t cols, int64_t rs,
                           int64_t cs, const float *y, std::vector<std::string> &out) {
-    int64_t step = std::max<int64_t>(1, rows / 4096);
-    std::vector<int64_t> idx;
-    for (int64_t i = 0; i < rows; i += step) idx.push_back(i);
-    if (idx.size() < 50) return;
-    double ym = 0;
-    for (auto i : idx) ym += (double)y[i];
-    ym /= (double)idx.size();
+    const int64_t step = std::max<int64_t>(1, rows / 4096);
+    const int64_t m = (rows + step - 1) / step;          // sampled rows
+    if (m < 50) return;
+    double ysum = 0;
+    for (int64_t k = 0; k < m; ++k) ysum += (double)y[k * step];
+    const double ymean = ysum / (double)m;
+    std::vector<double> dy((size_t)m);
+    for (int64_t k = 0; k < m; ++k) dy[(size_t)k] = (double)y[k * step] - ymean;
+    std::vector<double> xv;                              // the column's finite samples
+    std::vector<int64_t> slot;                           // ... and where they were sampled
     for (int64_t f = 0; f < cols; ++f) {
-        double sxy = 0, sxx = 0, syy = 0, xm = 0;
-        int64_t n = 0;
-        for (auto i : idx) {
-            float v = x[i * rs + f * cs];
-            if (std::isfinite(v)) { xm += (double)v; ++n; }
-        }
-        if (n < 50) continue;
-        xm /= (double)n;
-        for (auto i : idx) {
-            double v = (double)x[i * rs + f * cs];
+        xv.clear();
+        slot.clear();
+        for (int64_t k = 0; k < m; ++k) {
+            const float v = x[k * step * rs + f * cs];
             if (!std::isfinite(v)) continue;
-            double dx = v - xm, dy = (double)y[i] - ym;
-            sxy += dx * dy; sxx += dx * dx; syy += dy * dy;
+            xv.push_back((double)v);
+            slot.push_back(k);
         }
-        if (!(sxx > 0 && syy > 0)) continue;
-        double r = sxy / (std::sqrt(sxx) * std::sqrt(syy));
-        if (std::fabs(r) > 0.999) {
-            char buf[256];
-            std::snprintf(buf, sizeof buf,
-                          "[MacBoost] [Warning] feature %lld correlates with the label at "
-                          "|r|=%.4f on a subsample — possible target leakage (is the label or a "
-                          "prediction included in X?)",
-                          (long long)f, std::fabs(r));
-            out.push_back(buf);
-            if (verbose) std::printf("%s\n", buf);
+        if (xv.size() < 50) continue;
+        double xsum = 0;
+        for (double v : xv) xsum += v;
+        const double xmean = xsum / (double)xv.size();
+        double cxy = 0, cxx = 0, cyy = 0;
+        for (size_t j = 0; j < xv.size(); ++j) {
+            const double a = xv[j] - xmean, b = dy[(size_t)slot[j]];
+            cxy += a * b;
+            cxx += a * a;
+            cyy += b * b;
         }
+        if (!(cxx > 0 && cyy > 0)) continue;
+        const double r = std::fabs(cxy / (std::sqrt(cxx) * std::sqrt(cyy)));
+        if (!(r > 0.999)) continue;
+        char msg[256];
+        std::snprintf(msg, sizeof msg,
+                      "[MacBoost] [Warning] feature %lld correlates with the label at "
+                      "|r|=%.4f on a subsample — possible target leakage (is the label or a "
+                      "prediction included in X?)",
+                      (long long)f, r);
+        out.push_back(msg);
+        if (verbose) std::printf("%s\n", msg);
     }
 }
 
@@ -810,13 +822,19 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     }
     // the leakage check reads the host matrix only: it runs on a host thread
     // while the device is set up and the data uploaded and binned
+    // (a failure there is rethrown on this thread after the join)
     std::vector<std::string> leak_warnings;
+    std::exception_ptr leak_error;
     struct Joiner {
         std::thread th;
         ~Joiner() { if (th.joinable()) th.join(); }
     } leak;
     leak.th = std::thread([&] {
-        check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
+        try {
+            check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
+        } catch (...) {
+            leak_error = std::current_exception();
+        }
     });
     validate_categoricals(p, x, rows, cols, rs, cs);
     if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
@@ -853,6 +871,7 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     }
     t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
     leak.th.join();
+    if (leak_error) std::rethrow_exception(leak_error);
     t.warnings.insert(t.warnings.begin(), leak_warnings.begin(), leak_warnings.end());
     if (im) {
         // the init model's raw scores on the training (and validation) rows

@@ -42,7 +42,17 @@ def oracle_fit(x_fm, y, params, is_cat=None):
     nb = p.pop("num_bins", 256)
     obj = p.pop("objective", "regression")
     kw["objective"] = {"regression": O.OBJ_L2, "binary": O.OBJ_LOGISTIC, "mae": O.OBJ_MAE,
-                       "quantile": O.OBJ_QUANTILE, "multiclass": O.OBJ_MULTICLASS}[obj]
+                       "quantile": O.OBJ_QUANTILE, "multiclass": O.OBJ_MULTICLASS,
+                       "huber": O.OBJ_HUBER, "poisson": O.OBJ_POISSON,
+                       "tweedie": O.OBJ_TWEEDIE}[obj]
+    if obj == "tweedie":
+        kw["aux"] = p.pop("tweedie_variance_power", 1.5)
+    if "scale_pos_weight" in p:
+        kw["aux"] = p.pop("scale_pos_weight")
+    if "feature_fraction" in p:
+        kw["feature_fraction"] = p.pop("feature_fraction")
+    if "allowed_features" in p:
+        kw["allowed_features"] = p.pop("allowed_features")
     if "num_class" in p:
         kw["num_classes"] = p.pop("num_class")
     if "alpha" in p:
@@ -69,6 +79,15 @@ def check_identical(x_fm, y, params, is_cat=None, x_test=None):
     # (Booster.swift:1253-1290), which rounds differently from one addition of
     # the final leaf, so there the oracle's own predict is the reference.
     gp_train = mb.predict(h, x_fm, feature_major=True)
+    if params.get("objective") in ("poisson", "tweedie"):
+        # log link: predict returns exp(raw score) (Booster.swift:1992-1997);
+        # the raw scores are the oracle's running predictions
+        assert np.allclose(gp_train, np.exp(ref.preds.astype(np.float64)), rtol=2e-7, atol=0)
+        if x_test is not None:
+            gp = mb.predict(h, x_test, feature_major=True)
+            cp = O.predict(ref.forest, ref.base_score, ref.num_bins, x_test)
+            assert np.allclose(gp, np.exp(cp.astype(np.float64)), rtol=2e-7, atol=0)
+        return h, ref
     if params.get("num_leaves", 0) > 0 and params.get("objective") in ("mae", "quantile"):
         assert np.array_equal(gp_train, O.predict(ref.forest, ref.base_score, ref.num_bins, x_fm))
         assert np.allclose(gp_train, ref.preds, rtol=1e-5, atol=1e-4)
@@ -432,6 +451,62 @@ def test_goss_logistic_nan_categorical_identical_trees():
     check_identical(x, yb, {"num_trees": 20, "max_depth": 5, "objective": "binary",
                             "goss": True, "categorical_features": [6]},
                     is_cat=[0] * 6 + [1], x_test=x[:, :2000].copy())
+
+
+def _positive_labels(kind, rows, seed):
+    # ObjectiveTests.swift:67-108: Poisson counts with rate exp(0.5 + 1.5 x0)
+    # and zero-inflated positive labels for Tweedie (numpy-drawn here)
+    rng = np.random.default_rng(seed)
+    x = rng.random((5, rows), dtype=np.float32)
+    if kind == "poisson":
+        y = rng.poisson(np.exp(0.5 + 1.5 * x[0])).astype(np.float32)
+    else:
+        y = np.where(rng.random(rows) < 0.6, 0.0,
+                     np.exp(1.0 + 2.0 * x[0]) * (0.5 + rng.random(rows))).astype(np.float32)
+    return x, y
+
+
+@pytest.mark.parametrize("params", [
+    {"objective": "huber", "alpha": 1.5},
+    {"objective": "huber", "alpha": 0.3, "num_leaves": 19},
+    {"objective": "poisson"},
+    {"objective": "poisson", "num_leaves": 23, "subsample": 0.7},
+    {"objective": "tweedie", "tweedie_variance_power": 1.5},
+    {"objective": "tweedie", "tweedie_variance_power": 1.2, "num_leaves": 17, "goss": True,
+     "learning_rate": 0.3},
+])
+def test_huber_poisson_tweedie_identical_trees(params):
+    # compute_gradients cases 3, 5 and 6 (Shaders.swift:116-130): the same
+    # trees, raw scores and log-link predictions as the oracle
+    kind = params["objective"]
+    if kind == "huber":
+        x, y = O.friedman(12_000, 8, 371)
+        y = y.copy()
+        y[np.random.default_rng(372).random(12_000) < 0.02] += 60.0
+    else:
+        x, y = _positive_labels(kind, 12_000, 373)
+    check_identical(x, y, dict({"num_trees": 25, "max_depth": 5}, **params),
+                    x_test=np.ascontiguousarray(x[:, :3000]))
+
+
+@pytest.mark.parametrize("params", [
+    {"feature_fraction": 0.5},
+    {"feature_fraction": 0.3, "num_leaves": 21},
+    {"allowed_features": [0, 1, 2, 3, 4]},
+    {"allowed_features": [1, 3, 4, 6], "feature_fraction": 0.5, "num_leaves": 12},
+    {"feature_fraction": 0.05, "objective": "binary"},
+])
+def test_feature_fraction_and_allowed_features_identical_trees(params):
+    # per-tree column masks (Booster.swift:684-700, :1386-1400): the same
+    # features are offered to every node, so the trees are the oracle's
+    x, y = O.friedman(15_000, 10, 93)
+    if params.get("objective") == "binary":
+        y = (y > np.median(y)).astype(np.float32)
+    h, ref = check_identical(x, y, dict({"num_trees": 30, "max_depth": 5}, **params),
+                             x_test=np.ascontiguousarray(x[:, :3000]))
+    if "allowed_features" in params:
+        banned = [f for f in range(10) if f not in params["allowed_features"]]
+        assert not np.isin(ref.forest.feature, banned).any()
 
 
 def _first_trees(forest, k):

@@ -174,3 +174,54 @@ def test_select_features_validation_without_gpu():
                                               h.ctypes.data_as(_core.ctypes.POINTER(_core.ctypes.c_int32)),
                                               None, _core.ctypes.byref(err))
     assert rc == 1 and b"null or empty selection input" in err.value
+
+
+def _no_library(monkeypatch):
+    def refuse():
+        raise AssertionError("the library was called before the inputs were checked")
+    monkeypatch.setattr(_core, "lib", refuse)
+
+
+@pytest.mark.parametrize("case,msg", [
+    ("short_y", "y has 9 rows, X has 10"),
+    ("long_y", "y has 11 rows, X has 10"),
+    ("short_w", "sample_weight has 3 rows, X has 10"),
+    ("eval_cols", "eval_set feature count differs from X"),
+    ("eval_rows", "eval_set X/y row mismatch"),
+    ("x_1d", "X must be 2-dimensional, got shape (10,)"),
+])
+def test_shape_checks_before_any_library_call(monkeypatch, case, msg):
+    # python/macboost/_core.py:149-167: the binding checks y, sample_weight
+    # and eval_set against X before the library reads rows * cols floats
+    x = np.zeros((10, 3), np.float32)
+    y = np.zeros(10, np.float32)
+    kw = {}
+    if case == "short_y":
+        y = y[:9]
+    elif case == "long_y":
+        y = np.zeros(11, np.float32)
+    elif case == "short_w":
+        kw["sample_weight"] = np.ones(3, np.float32)
+    elif case == "eval_cols":
+        kw["eval_set"] = (np.zeros((5, 2), np.float32), np.zeros(5, np.float32))
+    elif case == "eval_rows":
+        kw["eval_set"] = (np.zeros((5, 3), np.float32), np.zeros(4, np.float32))
+    elif case == "x_1d":
+        x = np.zeros(10, np.float32)
+    _no_library(monkeypatch)
+    for call in (mb.train, mb.Trainer):
+        with pytest.raises(ValueError) as e:
+            call({"num_trees": 1}, x, y, **kw)
+        assert str(e.value) == msg
+    if case in ("short_y", "long_y", "x_1d"):
+        with pytest.raises(ValueError):
+            mb.Dataset.make({}, x, y)
+
+
+def test_labels_are_raveled(monkeypatch):
+    # a (rows, 1) label column is accepted as rows labels
+    cfg, xf, rows, cols, rm, yv, w, xv, vrows, yvv = _core._prep_train(
+        {}, np.zeros((6, 2), np.float32), np.zeros((6, 1), np.float32),
+        (np.zeros((4, 2), np.float32), np.zeros((4, 1), np.float32)), np.ones((6, 1)))
+    assert yv.shape == (6,) and w.shape == (6,) and yvv.shape == (4,) and xv.shape == (2, 4)
+    assert (rows, cols, rm, vrows) == (6, 2, 1, 4)
