@@ -140,6 +140,18 @@ int mbk_predict_forest(mbk_context *ctx, const int32_t *feature, const float *th
                        int32_t num_trees, int32_t nodes_per_tree, const float *x, int64_t rows,
                        int32_t data_bins, float base_score, float *out, char **err);
 
+/* fitImpl (Booster.swift:445-1701) over raw features already in device
+ * memory: x is read as x[i*cols + f] when row_major != 0, else x[f*rows + i];
+ * y, w (nullable) and the feature-major validation set (nullable) are host
+ * arrays, as in macboost_train, whose keys, checks and messages apply.  Device
+ * quantile edges, binning, every tree and the readback of the model happen
+ * inside the call, which first waits for the context's stream.  Returns a
+ * booster handle for every Part 1 call (free it with macboost_free), or NULL
+ * with *err.  initModel is refused (it needs host features). */
+void *mbk_fit(mbk_context *ctx, const char *params_json, const float *x, int64_t rows,
+              int64_t cols, int32_t row_major, const float *y, const float *w,
+              const float *x_valid, int64_t valid_rows, const float *y_valid, char **err);
+
 /* ======================= Part 3: extensions ============================= */
 
 /* No counterpart in the reference.  An incremental trainer: validates and
@@ -162,6 +174,13 @@ int mbx_trainer_hist_stats(void *trainer, int64_t *launches, double *ms, double 
  * levels 0..max_levels-1 (16 at most carry data).  Any output may be NULL. */
 int mbx_trainer_level_stats(void *trainer, int32_t max_levels, int64_t *built, int64_t *active,
                             double *hist_ms, char **err);
+/* The same instrumentation for fits run with mbk_fit on a context: 1 turns
+ * it on (and clears the totals), 0 off.  The totals add up over the fits;
+ * built and level_ms (either may be NULL) hold max_levels entries (16 at
+ * most carry data): rows of built nodes and histogram milliseconds per level. */
+int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err);
+int mbx_context_hist_stats(mbk_context *ctx, int32_t max_levels, int64_t *launches, double *ms,
+                           double *bytes, int64_t *built, double *level_ms, char **err);
 /* Wall-clock seconds of the last mbx_trainer_create phases: edges (host),
  * upload + device binning. */
 int mbx_trainer_setup_seconds(void *trainer, double *edges_s, double *bin_s);

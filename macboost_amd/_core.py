@@ -113,6 +113,10 @@ def _configure(l):
                                       ctypes.c_int32, _P, ctypes.c_int64, _P, _P, _P,
                                       ctypes.c_float, ctypes.c_float, ctypes.c_float, _P, _P,
                                       _c_char_pp]
+    l.mbk_fit.restype = ctypes.c_void_p
+    l.mbk_fit.argtypes = [_P, ctypes.c_char_p, _P, ctypes.c_int64, ctypes.c_int64,
+                          ctypes.c_int32, _f32_p, _f32_p, _f32_p, ctypes.c_int64, _f32_p,
+                          _c_char_pp]
     l.mbk_predict_forest.restype = ctypes.c_int
     l.mbk_predict_forest.argtypes = [_P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P,
                                      ctypes.c_int64, ctypes.c_int32, ctypes.c_float, _P,
@@ -140,6 +144,12 @@ def _configure(l):
     l.mbx_friedman.restype = None
     l.mbx_friedman.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float,
                                _P, _P]
+    l.mbx_context_profile.restype = ctypes.c_int
+    l.mbx_context_profile.argtypes = [_P, ctypes.c_int32, _c_char_pp]
+    l.mbx_context_hist_stats.restype = ctypes.c_int
+    l.mbx_context_hist_stats.argtypes = [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64),
+                                         ctypes.POINTER(ctypes.c_double),
+                                         ctypes.POINTER(ctypes.c_double), _P, _P, _c_char_pp]
     l.mbx_eval_history.restype = ctypes.c_int64
     l.mbx_eval_history.argtypes = [_P, _P, ctypes.c_int64]
     l.mbx_version.restype = ctypes.c_char_p
@@ -172,12 +182,12 @@ EXPORTED = (
     "macboost_warnings", "macboost_free", "macboost_free_string",
     "mbk_context_create", "mbk_context_destroy", "mbk_device_alloc", "mbk_device_free",
     "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_quantile_edges", "mbk_bin_data", "mbk_quantize",
-    "mbk_node_hist_split", "mbk_predict_forest",
+    "mbk_node_hist_split", "mbk_predict_forest", "mbk_fit",
     "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
     "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
     "mbx_version", "mbx_dataset_make", "mbx_dataset_save", "mbx_dataset_load",
     "mbx_dataset_info", "mbx_dataset_copy", "mbx_dataset_feature_names", "mbx_dataset_train",
-    "mbx_dataset_free", "mbx_eval_history",
+    "mbx_dataset_free", "mbx_eval_history", "mbx_context_profile", "mbx_context_hist_stats",
 )
 
 
@@ -491,6 +501,40 @@ class Context:
         self._check(lib().mbk_copy_to_host(self.ptr, out.ctypes.data, dptr, out.nbytes,
                                            ctypes.byref(err)), err)
         return out
+
+    def fit(self, config: dict, x_dev: int, rows: int, cols: int, y, row_major=False,
+            sample_weight=None, eval_set=None) -> _Handle:
+        """mbk_fit: a whole fit over raw features already in device memory
+        (x_dev, [cols][rows] or with row_major [rows][cols] float32)."""
+        yv = _column(y, rows, "y")
+        w = None if sample_weight is None else _column(sample_weight, rows, "sample_weight")
+        xv, yvv, vrows = _eval_arrays(eval_set, cols)
+        err = ctypes.c_char_p()
+        ptr = lib().mbk_fit(self.ptr, json.dumps(config).encode(), x_dev, rows, cols,
+                            1 if row_major else 0, _f32(yv), _f32(w), _f32(xv), vrows,
+                            _f32(yvv), ctypes.byref(err))
+        if not ptr:
+            raise MacBoostError(_take_error(err))
+        return _Handle(ptr)
+
+    def profile(self, enable: bool = True) -> None:
+        """HIP-event timing of every histogram launch of later fits."""
+        err = ctypes.c_char_p()
+        self._check(lib().mbx_context_profile(self.ptr, 1 if enable else 0, ctypes.byref(err)),
+                    err)
+
+    def hist_stats(self, levels: int = 16):
+        """(launches, ms, algorithmic bytes, built rows per level, ms per level)
+        of the histogram kernel over the profiled fits."""
+        n, ms, b = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+        built = np.zeros(levels, np.int64)
+        lms = np.zeros(levels, np.float64)
+        err = ctypes.c_char_p()
+        self._check(lib().mbx_context_hist_stats(self.ptr, levels, ctypes.byref(n),
+                                                 ctypes.byref(ms), ctypes.byref(b),
+                                                 built.ctypes.data, lms.ctypes.data,
+                                                 ctypes.byref(err)), err)
+        return int(n.value), float(ms.value), float(b.value), built, lms
 
     def sync(self):
         err = ctypes.c_char_p()

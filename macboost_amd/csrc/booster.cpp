@@ -687,6 +687,12 @@ void macboost_free_string(char *s) { free(s); }
 
 struct mbk_context {
     std::unique_ptr<mb::Device> dev;
+    // histogram-kernel timing of the fits run through this context
+    bool profiling = false;
+    int64_t prof_launches = 0;
+    double prof_ms = 0, prof_bytes = 0;
+    int64_t prof_built[16] = {};
+    double prof_level_ms[16] = {};
 };
 
 int mbk_context_create(int32_t device, mbk_context **out, char **err) {
@@ -844,9 +850,75 @@ int mbk_predict_forest(mbk_context *ctx, const int32_t *feature, const float *th
     }, -1);
 }
 
+void *mbk_fit(mbk_context *ctx, const char *params_json, const float *x, int64_t rows,
+              int64_t cols, int32_t row_major, const float *y, const float *w,
+              const float *x_valid, int64_t valid_rows, const float *y_valid, char **err) {
+    return guarded(err, [&]() -> void * {
+        if (!ctx) mb::internal("null kernel-seam context");
+        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
+        mb::Params p = mb::parse_params(params_json);
+        mb::Trainer *t = mb::trainer_create_device(p, x, rows, cols, row_major != 0, y, w,
+                                                   x_valid, valid_rows, y_valid);
+        try {
+            if (ctx->profiling) mb::trainer_profile(t, true);
+            mb::trainer_grow(t, p.num_trees * mb::trainer_classes(t));
+            Booster *b = mb::trainer_booster(t);
+            if (ctx->profiling) {
+                int64_t n = 0, built[16];
+                double ms = 0, bytes = 0, lms[16];
+                mb::trainer_hist_stats(t, &n, &ms, &bytes);
+                mb::trainer_level_stats(t, 16, built, nullptr, lms);
+                ctx->prof_launches += n;
+                ctx->prof_ms += ms;
+                ctx->prof_bytes += bytes;
+                for (int d = 0; d < 16; ++d) {
+                    ctx->prof_built[d] += built[d];
+                    ctx->prof_level_ms[d] += lms[d];
+                }
+            }
+            mb::trainer_free(t);
+            return b;
+        } catch (...) {
+            mb::trainer_free(t);
+            throw;
+        }
+    }, nullptr);
+}
+
 // ---------------------------------------------------------------------------
 // extensions
 // ---------------------------------------------------------------------------
+
+int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err) {
+    return guarded(err, [&]() -> int {
+        if (!ctx) mb::internal("null kernel-seam context");
+        if (enable && !ctx->profiling) {
+            ctx->prof_launches = 0;
+            ctx->prof_ms = ctx->prof_bytes = 0;
+            for (int d = 0; d < 16; ++d) {
+                ctx->prof_built[d] = 0;
+                ctx->prof_level_ms[d] = 0;
+            }
+        }
+        ctx->profiling = enable != 0;
+        return 0;
+    }, -1);
+}
+
+int mbx_context_hist_stats(mbk_context *ctx, int32_t max_levels, int64_t *launches, double *ms,
+                           double *bytes, int64_t *built, double *level_ms, char **err) {
+    return guarded(err, [&]() -> int {
+        if (!ctx) mb::internal("null kernel-seam context");
+        if (launches) *launches = ctx->prof_launches;
+        if (ms) *ms = ctx->prof_ms;
+        if (bytes) *bytes = ctx->prof_bytes;
+        for (int d = 0; d < max_levels; ++d) {
+            if (built) built[d] = d < 16 ? ctx->prof_built[d] : 0;
+            if (level_ms) level_ms[d] = d < 16 ? ctx->prof_level_ms[d] : 0.0;
+        }
+        return 0;
+    }, -1);
+}
 
 void *mbx_trainer_create(const char *params_json, const float *x, int64_t rows, int64_t cols,
                          int32_t row_major, const float *y, const float *w, const float *x_valid,

@@ -209,6 +209,10 @@ struct Trainer;
 Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t cols,
                         bool row_major, const float *y, const float *w, const float *xv,
                         int64_t vrows, const float *yv);
+// The same with x in device memory (strided as x): nothing is uploaded.
+Trainer *trainer_create_device(const Params &p, const float *x_dev, int64_t rows, int64_t cols,
+                               bool row_major, const float *y, const float *w, const float *xv,
+                               int64_t vrows, const float *yv);
 Trainer *trainer_create_binned(const Params &p, const BinnedDataset &ds, const float *w,
                                const float *xv, int64_t vrows, const float *yv);
 Trainer *trainer_create_fm(const Params &p, int64_t rows, int64_t cols, const uint8_t *fm_dev,

@@ -273,6 +273,58 @@ __global__ void k_tile8_to_layouts(const uint64_t *__restrict__ in, int64_t rows
     if (over) atomicOr(bad, 1u);
 }
 
+// ---------------------------------------------------------------------------
+// Checks of device-resident raw features (the host path reads host memory):
+// a strided row sample for the leakage check, and the categorical id rule of
+// Booster.swift:1810-1826.
+// ---------------------------------------------------------------------------
+
+// out[k * cols + f] = x[(k * step) * rs + f * cs] for k < m.
+__global__ __launch_bounds__(256) void k_gather_sample(const float *__restrict__ x, int64_t rs,
+                                                       int64_t cs, int64_t step, int64_t m,
+                                                       int32_t cols, float *__restrict__ out) {
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= m * cols) return;
+    const int64_t k = j / cols;
+    const int64_t f = j - k * cols;
+    out[j] = x[k * step * rs + f * cs];
+}
+
+hipError_t launch_gather_sample(hipStream_t s, const float *x, int64_t rs, int64_t cs,
+                                int64_t step, int64_t m, int32_t cols, float *out) {
+    const int64_t n = m * cols;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gather_sample, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, rs,
+                       cs, step, m, cols, out);
+    return hipGetLastError();
+}
+
+// Column cat_cols[j] must hold NaN or an integer id in [0, data_bins):
+// first_bad[j] (all ones on entry) becomes the first row that does not.
+__global__ __launch_bounds__(256) void k_check_categorical(const float *__restrict__ x,
+                                                           int64_t rows, int64_t rs, int64_t cs,
+                                                           const int32_t *__restrict__ cat_cols,
+                                                           int32_t data_bins,
+                                                           uint32_t *first_bad) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows) return;
+    const float v = x[i * rs + (int64_t)cat_cols[blockIdx.y] * cs];
+    if (isnan(v)) return;
+    const float c = rintf(v);
+    if (!(c >= 0.0f) || !isfinite(c) || c >= (float)data_bins)
+        atomicMin(&first_bad[blockIdx.y], (uint32_t)i);
+}
+
+hipError_t launch_check_categorical(hipStream_t s, const float *x, int64_t rows, int64_t rs,
+                                    int64_t cs, const int32_t *cat_cols, int32_t ncat,
+                                    int32_t data_bins, uint32_t *first_bad) {
+    if (rows <= 0 || ncat <= 0) return hipSuccess;
+    if (ncat > 65535 || (rows + 255) / 256 > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_check_categorical, dim3((unsigned)((rows + 255) / 256), (unsigned)ncat),
+                       dim3(256), 0, s, x, rows, rs, cs, cat_cols, data_bins, first_bad);
+    return hipGetLastError();
+}
+
 hipError_t launch_fm_to_tile8(hipStream_t s, const uint8_t *fm, int64_t rows, int32_t cols,
                               uint64_t *out) {
     if (rows <= 0 || cols <= 0) return hipSuccess;

@@ -112,6 +112,16 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            const uint8_t *is_cat, int32_t num_bins, int32_t tile_w,
                            int32_t num_tiles, uint8_t *bins_tiled, uint8_t *bins_fm);
 
+// Checks of device-resident raw features: a strided row sample
+// out[k * cols + f] = x[(k * step) * rs + f * cs] (k < m), and the categorical
+// id rule (NaN, or an integer in [0, data_bins)): first_bad[j] (all ones on
+// entry) becomes the first row of column cat_cols[j] that breaks it.
+hipError_t launch_gather_sample(hipStream_t s, const float *x, int64_t rs, int64_t cs,
+                                int64_t step, int64_t m, int32_t cols, float *out);
+hipError_t launch_check_categorical(hipStream_t s, const float *x, int64_t rows, int64_t rs,
+                                    int64_t cs, const int32_t *cat_cols, int32_t ncat,
+                                    int32_t data_bins, uint32_t *first_bad);
+
 // Boruta shadows: fm [cols][rows] -> fm2 [2*cols][rows] (real, then permuted).
 hipError_t launch_shadow_bins(hipStream_t s, const uint8_t *fm, int64_t rows, int32_t cols,
                               uint32_t half_bits, uint32_t seed, uint8_t *fm2);

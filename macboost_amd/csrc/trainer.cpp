@@ -796,9 +796,55 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.best_metric = effective_metric(p) == "auc" ? -INFINITY : INFINITY;
 }
 
-Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t cols,
-                        bool row_major, const float *y, const float *w, const float *xv,
-                        int64_t vrows, const float *yv) {
+// Leakage and categorical checks of device-resident features: the leakage
+// check reads a strided row sample copied to the host, and the categorical
+// ids are checked on the device (the first offending row of the first
+// offending feature gives the host path's message).
+static void check_device_features(const Params &p, const float *x_dev, int64_t rows,
+                                  int64_t cols, int64_t rs, int64_t cs, const float *y,
+                                  hipStream_t s, std::vector<std::string> &warnings) {
+    const int64_t step = std::max<int64_t>(1, rows / 4096);
+    const int64_t m = (rows + step - 1) / step;
+    if (m >= 50) {
+        DevBuf<float> sd((size_t)(m * cols));
+        std::vector<float> xs((size_t)(m * cols)), ys((size_t)m);
+        MB_HIP(mbk::launch_gather_sample(s, x_dev, rs, cs, step, m, (int)cols, sd.ptr));
+        MB_HIP(hipMemcpyAsync(xs.data(), sd.ptr, sd.bytes(), hipMemcpyDeviceToHost, s));
+        MB_HIP(hipStreamSynchronize(s));
+        for (int64_t k = 0; k < m; ++k) ys[(size_t)k] = y[k * step];
+        // every row of the sample is used (its step is 1: m < 8192)
+        check_leakage(p.verbose, xs.data(), m, cols, cols, 1, ys.data(), warnings);
+    }
+    if (p.categorical.empty()) return;
+    std::vector<int32_t> cat(p.categorical.begin(), p.categorical.end());
+    for (int f : cat)
+        if (f < 0 || f >= cols)
+            internal("categorical feature index " + std::to_string(f) + " out of range");
+    DevBuf<int32_t> cd(cat.size());
+    DevBuf<uint32_t> bad(cat.size());
+    std::vector<uint32_t> first(cat.size());
+    MB_HIP(hipMemcpyAsync(cd.ptr, cat.data(), cd.bytes(), hipMemcpyHostToDevice, s));
+    MB_HIP(hipMemsetAsync(bad.ptr, 0xFF, bad.bytes(), s));
+    MB_HIP(mbk::launch_check_categorical(s, x_dev, rows, rs, cs, cd.ptr, (int)cat.size(),
+                                         p.num_bins - 1, bad.ptr));
+    MB_HIP(hipMemcpyAsync(first.data(), bad.ptr, bad.bytes(), hipMemcpyDeviceToHost, s));
+    MB_HIP(hipStreamSynchronize(s));
+    for (size_t j = 0; j < cat.size(); ++j) {
+        if (first[j] == 0xFFFFFFFFu) continue;
+        float v = 0;
+        MB_HIP(hipMemcpy(&v, x_dev + (int64_t)first[j] * rs + (int64_t)cat[j] * cs, 4,
+                         hipMemcpyDeviceToHost));
+        throw Error("Categorical feature " + std::to_string(cat[j]) + " has value " +
+                    swift_float(v) + "; expected integer ids in 0..<" +
+                    std::to_string(p.num_bins - 1) + " or NaN");
+    }
+}
+
+// fitImpl's setup (Booster.swift:445-600) for raw features in host memory
+// (x_on_device false: uploaded here) or already in device memory.
+static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, int64_t rows,
+                           int64_t cols, bool row_major, const float *y, const float *w,
+                           const float *xv, int64_t vrows, const float *yv) {
     if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
     validate_params(pin);
     validate_inputs(pin, rows, cols, y, w, xv, vrows, yv);
@@ -810,6 +856,7 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
     const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
     std::unique_ptr<Booster> im;
     if (!p.init_model.empty()) {                     // Booster.swift:487-499
+        if (x_on_device) invalid("initModel needs the raw features in host memory");
         im.reset(load_model_file(p.init_model));
         if (im->num_features != cols)
             invalid("initModel expects " + std::to_string(im->num_features) + " features, X has " +
@@ -820,40 +867,48 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
             invalid("initModel has " + std::to_string(im->trained_num_classes) +
                     " classes, the params ask for " + std::to_string(k_want));
     }
-    // the leakage check reads the host matrix only: it runs on a host thread
-    // while the device is set up and the data uploaded and binned
-    // (a failure there is rethrown on this thread after the join)
+    // host features: the leakage check runs on a host thread while the device
+    // is set up and the data uploaded and binned (a failure there is rethrown
+    // on this thread after the join)
     std::vector<std::string> leak_warnings;
     std::exception_ptr leak_error;
     struct Joiner {
         std::thread th;
         ~Joiner() { if (th.joinable()) th.join(); }
     } leak;
-    leak.th = std::thread([&] {
-        try {
-            check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
-        } catch (...) {
-            leak_error = std::current_exception();
-        }
-    });
-    validate_categoricals(p, x, rows, cols, rs, cs);
+    if (!x_on_device) {
+        leak.th = std::thread([&] {
+            try {
+                check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
+            } catch (...) {
+                leak_error = std::current_exception();
+            }
+        });
+        validate_categoricals(p, x, rows, cols, rs, cs);
+    }
     if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
     setup_shape(t, rows, cols);
     hipStream_t s = t.dev->stream;
     const int tile_w = t.sh.tile_w;
+    if (x_on_device) check_device_features(p, x, rows, cols, rs, cs, y, s, leak_warnings);
 
-    // --- binning on the device: upload, quantile edges, bin_data ----------
+    // --- binning on the device: (upload,) quantile edges, bin_data --------
     double t0 = now_s();
     {
-        DevBuf<float> xd((size_t)rows * (size_t)cols);
+        DevBuf<float> xd;
+        const float *xsrc = x;
+        if (!x_on_device) {
+            xd.alloc((size_t)rows * (size_t)cols);
+            upload(xd.ptr, x, xd.bytes(), s);
+            xsrc = xd.ptr;
+        }
         const size_t ne = (size_t)p.num_bins - 2;
         DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
-        upload(xd.ptr, x, xd.bytes(), s);
         {
             const double te = now_s();
             const size_t cap = mbk::edge_sample_cap(rows);
             DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
-            MB_HIP(mbk::launch_edges(s, xd.ptr, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
+            MB_HIP(mbk::launch_edges(s, xsrc, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
                                      ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
             t.edges.resize((size_t)cols * ne);
             MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
@@ -863,14 +918,14 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
         t.bins_fm.alloc((size_t)rows * (size_t)cols);
         MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
-        MB_HIP(mbk::launch_bin_data(s, xd.ptr, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
+        MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
                                     p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
                                     t.bins_fm.ptr));
         if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
         MB_HIP(hipStreamSynchronize(s));
     }
-    t.t_bin = now_s() - t0 - t.t_edges;              // upload + bin_data
-    leak.th.join();
+    t.t_bin = now_s() - t0 - t.t_edges;              // (upload +) bin_data
+    if (leak.th.joinable()) leak.th.join();
     if (leak_error) std::rethrow_exception(leak_error);
     t.warnings.insert(t.warnings.begin(), leak_warnings.begin(), leak_warnings.end());
     if (im) {
@@ -892,6 +947,18 @@ Trainer *trainer_create(const Params &pin, const float *x, int64_t rows, int64_t
         t.base_scores = im->base_scores;
     }
     return tr.release();
+}
+
+Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t cols,
+                        bool row_major, const float *y, const float *w, const float *xv,
+                        int64_t vrows, const float *yv) {
+    return create_raw(p, x, false, rows, cols, row_major, y, w, xv, vrows, yv);
+}
+
+Trainer *trainer_create_device(const Params &p, const float *x_dev, int64_t rows, int64_t cols,
+                               bool row_major, const float *y, const float *w, const float *xv,
+                               int64_t vrows, const float *yv) {
+    return create_raw(p, x_dev, true, rows, cols, row_major, y, w, xv, vrows, yv);
 }
 
 // fitImpl with GPU-resident pre-binned input (GPUBinned, Booster.swift:436-443,

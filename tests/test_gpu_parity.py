@@ -293,6 +293,41 @@ def test_node_hist_full_size_exact(ctx):
         assert np.array_equal(hist[:, f, 1], np.bincount(b, weights=qh, minlength=nb).astype(np.int64)), f
 
 
+def test_fit_from_device_features_equals_macboost_train(ctx):
+    # mbk_fit: the whole fit over raw features already in HBM gives the
+    # model macboost_train gives from host memory, in both layouts, with the
+    # same warnings and the same categorical error
+    rows = 9000
+    x, y = _mixed(rows)
+    x = x.copy()
+    x[3] = y + np.float32(0.0)                       # leakage warning
+    params = {"num_trees": 12, "max_depth": 5, "categorical_features": [6]}
+    want_h = mb.train(params, x, y, feature_major=True)
+    want = model_io.saved_model(want_h)
+    for row_major in (False, True):
+        d = ctx.upload(np.ascontiguousarray(x.T) if row_major else x)
+        h = ctx.fit(params, d, rows, 7, y, row_major=row_major)
+        assert model_io.saved_model(h) == want
+        assert mb.warnings(h) == mb.warnings(want_h)
+        assert any("correlates with the label" in w for w in mb.warnings(h))
+    xv, yv = _mixed(2000, 213, 214)
+    h = ctx.fit(dict(params, early_stopping_rounds=3), ctx.upload(x), rows, 7, y,
+                eval_set=(xv.T, yv))
+    h2 = mb.train(dict(params, early_stopping_rounds=3), x, y, eval_set=(xv.T, yv),
+                  feature_major=True)
+    assert model_io.saved_model(h) == model_io.saved_model(h2)
+    assert np.array_equal(mb.eval_history(h), mb.eval_history(h2))
+    bad = x.copy()
+    bad[6, 4321] = 300.0
+    bad[6, 5000] = -1.0
+    with pytest.raises(mb.MacBoostError) as e1:
+        ctx.fit(params, ctx.upload(bad), rows, 7, y)
+    with pytest.raises(mb.MacBoostError) as e2:
+        mb.train(params, bad, y, feature_major=True)
+    assert str(e1.value) == str(e2.value)
+    assert "Categorical feature 6 has value 300.0" in str(e1.value)
+
+
 # --------------------------------------------------------------------------
 # whole fits: identical trees, bit-exact predictions
 # --------------------------------------------------------------------------
