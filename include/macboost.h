@@ -89,7 +89,8 @@ int mbk_synchronize(mbk_context *ctx, char **err);
  * values, sorted; edges[f*(num_bins-2) + k] = sample[min(m-1, (k+1)*m/(num_bins-1))].
  * Categorical and all-NaN features get zero edges.  x is device memory read
  * as x[i*row_stride + f*col_stride]; edges is device memory.  The sort
- * scratch (2 * cols * ceil(rows/step) u32) is allocated inside the call. */
+ * scratch (2 * cols * ceil(rows/step) u32) belongs to the context: it is
+ * allocated by the first call that needs more than the context holds. */
 int mbk_quantile_edges(mbk_context *ctx, const float *x, int64_t rows, int32_t cols,
                        int64_t row_stride, int64_t col_stride, int32_t num_bins,
                        const uint8_t *is_cat, float *edges, char **err);
@@ -124,7 +125,8 @@ typedef struct {
 
 /* build_histograms + find_splits for one node (Shaders.swift:212-464): the
  * node's rows are entries[0..n).  hist_out: [num_bins][cols][2] int64
- * (gradient sum, hessian sum) of quantised words; results: [cols]. */
+ * (gradient sum, hessian sum) of quantised words; results: [cols].  The
+ * histogram scratch belongs to the context, as for mbk_tree_begin. */
 int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t rows,
                         int32_t cols, int32_t num_bins, int32_t tile_width,
                         const uint32_t *entries, int64_t n, const uint32_t *max_gh,
@@ -139,6 +141,117 @@ int mbk_predict_forest(mbk_context *ctx, const int32_t *feature, const float *th
                        const uint8_t *flags, const float *leaf, const uint32_t *mask,
                        int32_t num_trees, int32_t nodes_per_tree, const float *x, int64_t rows,
                        int32_t data_bins, float base_score, float *out, char **err);
+
+/* ---- one level-wise tree, level by level (fitImpl's level loop,
+ * Booster.swift:1467-1648, and the dispatches it encodes, Shaders.swift:
+ * 203-464, 1223-1511).  All calls enqueue on the context's stream and return
+ * without waiting; split decisions stay on the device.  The caller owns:
+ *   bins_tiled  [rows][ceil(cols/tile_width)][tile_width] u8 (mbk_bin_data)
+ *   bins_fm     [cols][rows] u8
+ *   entries     two buffers of [rows] (row, qg << 16 | qh) u32 pairs; the tree's
+ *               rows are the first n_entries of the first (mbk_quantize)
+ *   hist        two buffers of [2^(max_depth-1)][num_bins][cols][2] int64
+ *   results     [2^(max_depth-1)][cols] mbk_split_result
+ *   the tree's model arrays (mbk_tree_out) and preds [rows] f32.
+ * The context owns every other buffer (segments, counts, node sums, monotone
+ * bounds, partition cursors, histogram items and partials): mbk_tree_begin
+ * sizes them when the shape needs more than the context holds, and no other
+ * call allocates device memory.  is_cat, monotone and feat_mask are [cols]
+ * device arrays or NULL (no categorical, no constraint, every feature).  For
+ * level d = 0 .. max_depth-1:
+ *   mbk_hist_build(d) -> mbk_hist_subtract(d) -> mbk_find_splits(d) ->
+ *   mbk_decide_level(d) -> mbk_route(d)
+ * alternating the entries and hist buffers, then mbk_final_leaves.  A call
+ * out of this order fails with an error. */
+typedef struct {
+    int64_t rows;          /* rows of the bin matrices */
+    int32_t cols;          /* features */
+    int32_t num_bins;      /* bins per feature, the missing bin included: 4..256 */
+    int32_t tile_width;    /* features per row tile of bins_tiled: 8, 16, 32 or 64 */
+    int32_t max_depth;     /* 1..12 */
+} mbk_tree_shape;
+
+typedef struct {           /* BoosterParams (Booster.swift:18-63) */
+    float lambda;
+    float min_child_hess;
+    float min_split_gain;
+    float cat_smooth;
+    float learning_rate;
+} mbk_split_params;
+
+/* NodeSplit (Shaders.swift:466): feature < 0 marks a leaf; flags bit 0 =
+ * missing goes left, bit 1 = categorical. */
+typedef struct {
+    int32_t feature;
+    uint32_t bin;
+    uint32_t flags;
+} mbk_node_split;
+
+/* One tree's model arrays in device memory, heap layout (children of n at
+ * 2n+1 and 2n+2, 2^(max_depth+1) - 1 nodes); mask holds 8 words per node. */
+typedef struct {
+    mbk_node_split *split;
+    float *leaf;
+    float *gain;
+    float *cover;
+    uint32_t *mask;
+} mbk_tree_out;
+
+/* init_tree (Shaders.swift:1313-1340): level 0 holds the first n_entries
+ * entries; max_gh (device, 2 words) are the quantisation maxima. */
+int mbk_tree_begin(mbk_context *ctx, const mbk_tree_shape *shape, const uint32_t *max_gh,
+                   int64_t n_entries, mbk_tree_out out, char **err);
+/* build_histograms (Shaders.swift:203-286): the histograms of level d's
+ * built nodes (the smaller child of each split, the root at level 0). */
+int mbk_hist_build(mbk_context *ctx, int32_t level, const uint8_t *bins_tiled,
+                   const uint32_t *entries, int64_t *hist, char **err);
+/* subtract_histograms (Shaders.swift:307-326): each sibling = parent (in
+ * hist_prev, the previous level's buffer) - built, exact; nothing at level 0. */
+int mbk_hist_subtract(mbk_context *ctx, int32_t level, const int64_t *hist_prev, int64_t *hist,
+                      char **err);
+/* find_splits + cat_sort (Shaders.swift:328-464): the best split of every
+ * (node, feature) of level d. */
+int mbk_find_splits(mbk_context *ctx, int32_t level, const int64_t *hist, const uint8_t *is_cat,
+                    const int8_t *monotone, const uint8_t *feat_mask,
+                    const mbk_split_params *params, mbk_split_result *results, char **err);
+/* decide_splits (Shaders.swift:1342-1451): every node of level d splits on
+ * its best feature or becomes a leaf; children's sums and monotone bounds. */
+int mbk_decide_level(mbk_context *ctx, int32_t level, const mbk_split_result *results,
+                     const int8_t *monotone, const mbk_split_params *params, mbk_tree_out out,
+                     char **err);
+/* route_samples (Shaders.swift:1223-1311): level d's entries partitioned into
+ * their children's segments of entries_out, and level d+1 planned (at the
+ * last level only the children's rows are counted; entries_out is not
+ * written). */
+int mbk_route(mbk_context *ctx, int32_t level, const uint8_t *bins_fm, const uint32_t *entries_in,
+              uint32_t *entries_out, mbk_tree_out out, char **err);
+/* final_leaves (Shaders.swift:1491-1511): leaf values of the deepest level;
+ * preds (may be NULL) += the tree, by one walk of every row of bins_fm.
+ * Waits for the tree, and fails if a level's histogram items did not fit. */
+int mbk_final_leaves(mbk_context *ctx, const uint8_t *bins_fm, const mbk_split_params *params,
+                     mbk_tree_out out, float *preds, char **err);
+/* The whole tree in one call: mbk_tree_begin, the level loop and
+ * mbk_final_leaves.  entries_a holds the tree's entries on entry (it and
+ * entries_b are overwritten). */
+int mbk_grow_tree(mbk_context *ctx, const mbk_tree_shape *shape, const mbk_split_params *params,
+                  const uint8_t *bins_tiled, const uint8_t *bins_fm, const uint8_t *is_cat,
+                  const int8_t *monotone, const uint8_t *feat_mask, const uint32_t *max_gh,
+                  uint32_t *entries_a, uint32_t *entries_b, int64_t n_entries, int64_t *hist_a,
+                  int64_t *hist_b, mbk_split_result *results, mbk_tree_out out, float *preds,
+                  char **err);
+
+/* gpuContributions (SHAP.swift:116-166): TreeSHAP of device rows x
+ * (feature-major [cols][rows]) under a forest given as host arrays of
+ * num_trees*nodes_per_tree heap slots (mask: 8 words per node, NULL without
+ * categorical splits); out (device) receives [rows][cols + 1] f32, the bias
+ * base_score + the trees' cover-weighted leaf means in the last column.  Path
+ * tables and, for more than 4,096 columns, the fp64 accumulators are context
+ * scratch. */
+int mbk_treeshap(mbk_context *ctx, const int32_t *feature, const float *threshold,
+                 const uint8_t *flags, const float *leaf, const float *cover,
+                 const uint32_t *mask, int32_t num_trees, int32_t nodes_per_tree,
+                 float base_score, int32_t data_bins, const float *x, int64_t rows, int32_t cols,
+                 float *out, char **err);
 
 /* fitImpl (Booster.swift:445-1701) over raw features already in device
  * memory: x is read as x[i*cols + f] when row_major != 0, else x[f*rows + i];

@@ -47,6 +47,29 @@ def lib() -> ctypes.CDLL:
     return _lib_instance
 
 
+class MbkTreeShape(ctypes.Structure):
+    """mbk_tree_shape (include/macboost.h)."""
+    _fields_ = [("rows", ctypes.c_int64), ("cols", ctypes.c_int32),
+                ("num_bins", ctypes.c_int32), ("tile_width", ctypes.c_int32),
+                ("max_depth", ctypes.c_int32)]
+
+
+class MbkSplitParams(ctypes.Structure):
+    """mbk_split_params (include/macboost.h)."""
+    _fields_ = [("lambda_", ctypes.c_float), ("min_child_hess", ctypes.c_float),
+                ("min_split_gain", ctypes.c_float), ("cat_smooth", ctypes.c_float),
+                ("learning_rate", ctypes.c_float)]
+
+
+class MbkTreeOut(ctypes.Structure):
+    """mbk_tree_out: device pointers of one tree's model arrays."""
+    _fields_ = [("split", _P), ("leaf", _P), ("gain", _P), ("cover", _P), ("mask", _P)]
+
+
+_SHAPE_P = ctypes.POINTER(MbkTreeShape)
+_SPLIT_P = ctypes.POINTER(MbkSplitParams)
+
+
 def _configure(l):
     l.macboost_train.restype = ctypes.c_void_p
     l.macboost_train.argtypes = [
@@ -113,6 +136,22 @@ def _configure(l):
                                       ctypes.c_int32, _P, ctypes.c_int64, _P, _P, _P,
                                       ctypes.c_float, ctypes.c_float, ctypes.c_float, _P, _P,
                                       _c_char_pp]
+    for name, args in (
+            ("mbk_tree_begin", [_P, _SHAPE_P, _P, ctypes.c_int64, MbkTreeOut, _c_char_pp]),
+            ("mbk_hist_build", [_P, ctypes.c_int32, _P, _P, _P, _c_char_pp]),
+            ("mbk_hist_subtract", [_P, ctypes.c_int32, _P, _P, _c_char_pp]),
+            ("mbk_find_splits", [_P, ctypes.c_int32, _P, _P, _P, _P, _SPLIT_P, _P, _c_char_pp]),
+            ("mbk_decide_level", [_P, ctypes.c_int32, _P, _P, _SPLIT_P, MbkTreeOut,
+                                  _c_char_pp]),
+            ("mbk_route", [_P, ctypes.c_int32, _P, _P, _P, MbkTreeOut, _c_char_pp]),
+            ("mbk_final_leaves", [_P, _P, _SPLIT_P, MbkTreeOut, _P, _c_char_pp]),
+            ("mbk_grow_tree", [_P, _SHAPE_P, _SPLIT_P, _P, _P, _P, _P, _P, _P, _P, _P,
+                               ctypes.c_int64, _P, _P, _P, MbkTreeOut, _P, _c_char_pp]),
+            ("mbk_treeshap", [_P, _P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32,
+                              ctypes.c_float, ctypes.c_int32, _P, ctypes.c_int64, ctypes.c_int32,
+                              _P, _c_char_pp])):
+        getattr(l, name).restype = ctypes.c_int
+        getattr(l, name).argtypes = args
     l.mbk_fit.restype = ctypes.c_void_p
     l.mbk_fit.argtypes = [_P, ctypes.c_char_p, _P, ctypes.c_int64, ctypes.c_int64,
                           ctypes.c_int32, _f32_p, _f32_p, _f32_p, ctypes.c_int64, _f32_p,
@@ -182,7 +221,9 @@ EXPORTED = (
     "macboost_warnings", "macboost_free", "macboost_free_string",
     "mbk_context_create", "mbk_context_destroy", "mbk_device_alloc", "mbk_device_free",
     "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_quantile_edges", "mbk_bin_data", "mbk_quantize",
-    "mbk_node_hist_split", "mbk_predict_forest", "mbk_fit",
+    "mbk_node_hist_split", "mbk_predict_forest", "mbk_fit", "mbk_tree_begin", "mbk_hist_build",
+    "mbk_hist_subtract", "mbk_find_splits", "mbk_decide_level", "mbk_route", "mbk_final_leaves",
+    "mbk_grow_tree", "mbk_treeshap",
     "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
     "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
     "mbx_version", "mbx_dataset_make", "mbx_dataset_save", "mbx_dataset_load",
@@ -417,6 +458,11 @@ class Trainer:
         if lib().mbx_trainer_grow(self.ptr, n, ctypes.byref(err)) != 0:
             raise MacBoostError(_take_error(err))
 
+    def call(self, name: str, *args) -> None:
+        """One mbk_* entry point on this context (the error argument is added)."""
+        err = ctypes.c_char_p()
+        self._check(getattr(lib(), name)(self.ptr, *args, ctypes.byref(err)), err)
+
     def profile(self, enable: bool = True) -> None:
         err = ctypes.c_char_p()
         lib().mbx_trainer_profile(self.ptr, 1 if enable else 0, ctypes.byref(err))
@@ -516,6 +562,11 @@ class Context:
         if not ptr:
             raise MacBoostError(_take_error(err))
         return _Handle(ptr)
+
+    def call(self, name: str, *args) -> None:
+        """One mbk_* entry point on this context (the error argument is added)."""
+        err = ctypes.c_char_p()
+        self._check(getattr(lib(), name)(self.ptr, *args, ctypes.byref(err)), err)
 
     def profile(self, enable: bool = True) -> None:
         """HIP-event timing of every histogram launch of later fits."""

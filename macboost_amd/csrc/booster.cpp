@@ -14,6 +14,7 @@
 #include <thread>
 
 #include "../../include/macboost.h"
+#include "abi.hpp"
 #include "core.hpp"
 #include "json.hpp"
 
@@ -538,22 +539,9 @@ Booster *Booster::from_json(const std::string &text) {
 // ===========================================================================
 
 using mb::Booster;
+using mb::guarded;
+using mb::set_err;
 
-static void set_err(char **err, const std::string &m) {
-    if (err) *err = strdup(m.c_str());
-}
-
-template <typename Fn>
-static auto guarded(char **err, Fn fn, decltype(fn()) on_error) -> decltype(fn()) {
-    try {
-        return fn();
-    } catch (const std::exception &e) {
-        set_err(err, e.what());
-    } catch (...) {
-        set_err(err, "Internal error: unknown failure");
-    }
-    return on_error;
-}
 
 extern "C" {
 
@@ -682,243 +670,8 @@ void macboost_free(void *handle) { delete static_cast<Booster *>(handle); }
 void macboost_free_string(char *s) { free(s); }
 
 // ---------------------------------------------------------------------------
-// kernel seam
+// extensions (the kernel seam mbk_* is in seam.cpp)
 // ---------------------------------------------------------------------------
-
-struct mbk_context {
-    std::unique_ptr<mb::Device> dev;
-    // histogram-kernel timing of the fits run through this context
-    bool profiling = false;
-    int64_t prof_launches = 0;
-    double prof_ms = 0, prof_bytes = 0;
-    int64_t prof_built[16] = {};
-    double prof_level_ms[16] = {};
-};
-
-int mbk_context_create(int32_t device, mbk_context **out, char **err) {
-    return guarded(err, [&]() -> int {
-        auto c = std::make_unique<mbk_context>();
-        c->dev = std::make_unique<mb::Device>(device);
-        *out = c.release();
-        return 0;
-    }, -1);
-}
-
-void mbk_context_destroy(mbk_context *ctx) { delete ctx; }
-
-int mbk_device_alloc(mbk_context *ctx, size_t bytes, void **out, char **err) {
-    return guarded(err, [&]() -> int {
-        MB_HIP(hipSetDevice(ctx->dev->id));
-        MB_HIP(hipMalloc(out, bytes ? bytes : 1));
-        return 0;
-    }, -1);
-}
-
-void mbk_device_free(mbk_context *, void *ptr) {
-    if (ptr) (void)hipFree(ptr);
-}
-
-int mbk_copy_to_device(mbk_context *ctx, void *dst, const void *src, size_t bytes, char **err) {
-    return guarded(err, [&]() -> int {
-        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->dev->stream));
-        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
-        return 0;
-    }, -1);
-}
-
-int mbk_copy_to_host(mbk_context *ctx, void *dst, const void *src, size_t bytes, char **err) {
-    return guarded(err, [&]() -> int {
-        MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->dev->stream));
-        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
-        return 0;
-    }, -1);
-}
-
-int mbk_synchronize(mbk_context *ctx, char **err) {
-    return guarded(err, [&]() -> int {
-        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
-        return 0;
-    }, -1);
-}
-
-int mbk_quantile_edges(mbk_context *ctx, const float *x, int64_t rows, int32_t cols,
-                       int64_t row_stride, int64_t col_stride, int32_t num_bins,
-                       const uint8_t *is_cat, float *edges, char **err) {
-    return guarded(err, [&]() -> int {
-        if (num_bins < 4 || num_bins > 256) mb::invalid("numBins must be in 4...256");
-        if (rows < 1 || cols < 1) mb::invalid("rows and cols must be positive");
-        const size_t cap = mbk::edge_sample_cap(rows);
-        mb::DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
-        MB_HIP(mbk::launch_edges(ctx->dev->stream, x, rows, cols, row_stride, col_stride,
-                                 num_bins, is_cat, ka.ptr, kb.ptr, cnt.ptr, edges));
-        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
-        return 0;
-    }, -1);
-}
-
-int mbk_bin_data(mbk_context *ctx, const float *x, int64_t rows, int32_t cols, int64_t row_stride,
-                 int64_t col_stride, const float *edges, const uint8_t *is_cat, int32_t num_bins,
-                 int32_t tile_width, uint8_t *bins_tiled, uint8_t *bins_fm, char **err) {
-    return guarded(err, [&]() -> int {
-        if (num_bins < 4 || num_bins > 256) mb::invalid("numBins must be in 4...256");
-        const int tiles = (cols + tile_width - 1) / tile_width;
-        MB_HIP(hipMemsetAsync(bins_tiled, 0, (size_t)tiles * rows * tile_width, ctx->dev->stream));
-        MB_HIP(mbk::launch_bin_data(ctx->dev->stream, x, rows, cols, row_stride, col_stride, edges,
-                                    is_cat, num_bins, tile_width, tiles, bins_tiled, bins_fm));
-        return 0;
-    }, -1);
-}
-
-int mbk_quantize(mbk_context *ctx, int32_t objective, float alpha, float aux, const float *preds,
-                 const float *labels, const float *weights, int64_t rows, uint32_t *max_gh,
-                 uint32_t *entries, char **err) {
-    return guarded(err, [&]() -> int {
-        hipStream_t s = ctx->dev->stream;
-        mb::DevBuf<mbk::TreeCtl> ctl(1);
-        mb::DevBuf<uint32_t> part(mbk::grad_max_scratch_words());
-        if (objective < 0 || objective > 6)
-            mb::invalid("mbk_quantize takes objectives 0..6 (one output per row)");
-        mbk::GradParams gp{objective, alpha, aux, weights ? 1 : 0, 1, 0, rows};
-        MB_HIP(mbk::launch_tree_init(s, ctl.ptr));
-        MB_HIP(mbk::launch_grad_max(s, gp, preds, labels, weights, rows, ctl.ptr, part.ptr));
-        MB_HIP(mbk::launch_quantize(s, gp, preds, labels, weights, rows, ctl.ptr,
-                                    reinterpret_cast<mbk::Entry *>(entries)));
-        MB_HIP(hipMemcpyAsync(max_gh, ctl.ptr->max_gh, 8, hipMemcpyDeviceToDevice, s));
-        MB_HIP(hipStreamSynchronize(s));
-        return 0;
-    }, -1);
-}
-
-int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t rows, int32_t cols,
-                        int32_t num_bins, int32_t tile_width, const uint32_t *entries, int64_t n,
-                        const uint32_t *max_gh, const uint8_t *is_cat, const int8_t *monotone,
-                        float lambda, float min_child_hess, float cat_smooth, int64_t *hist_out,
-                        mbk_split_result *results, char **err) {
-    static_assert(sizeof(mbk_split_result) == sizeof(mbk::SplitResult), "SplitResult layout");
-    return guarded(err, [&]() -> int {
-        if (num_bins < 4 || num_bins > 256) mb::invalid("numBins must be in 4...256");
-        if (tile_width != 8 && tile_width != 16 && tile_width != 32 && tile_width != 64)
-            mb::invalid("tile_width must be 8, 16, 32 or 64");
-        if (n < 0 || n > 0xFFFFFFF0LL) mb::invalid("row count out of range");
-        hipStream_t s = ctx->dev->stream;
-        mbk::Shape sh{rows, cols, num_bins, tile_width, (cols + tile_width - 1) / tile_width, 0u, 0u};
-        mbk::SplitParams sp{lambda, min_child_hess, 0.0f, cat_smooth, 0.1f, 1};
-        const int grid = ctx->dev->num_cus;
-        const int64_t T = sh.num_tiles;
-        const int64_t max_items = T * ((n + 2047) / 2048 + 2) + 2 * grid;
-        sh.item_cap = (uint32_t)max_items;
-        mb::DevBuf<mbk::TreeCtl> ctl(1);
-        mb::DevBuf<uint64_t> partials((size_t)max_items * tile_width * num_bins);
-        mb::DevBuf<mbk::HistItem> items((size_t)max_items);
-        mb::DevBuf<mbk::Pair> pairs(1);
-        mb::DevBuf<uint32_t> seg(1), count(1);
-        mb::DevBuf<float> cover(1);
-        mb::DevBuf<float2> bounds(1);
-        mb::DevBuf<int64_t> node_g(1), node_h(1), dummy(2);
-        mb::DevBuf<uint8_t> cat0((size_t)cols), mask1((size_t)cols);
-        mb::DevBuf<int8_t> mono0((size_t)cols);
-        MB_HIP(hipMemsetAsync(cat0.ptr, 0, (size_t)cols, s));
-        MB_HIP(hipMemsetAsync(mono0.ptr, 0, (size_t)cols, s));
-        MB_HIP(hipMemsetAsync(mask1.ptr, 1, (size_t)cols, s));
-        MB_HIP(mbk::launch_tree_init(s, ctl.ptr));
-        MB_HIP(hipMemcpyAsync(ctl.ptr->max_gh, max_gh, 8, hipMemcpyDeviceToDevice, s));
-        MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)n, (uint32_t)(2 * grid), 2048u, ctl.ptr, seg.ptr,
-                                     count.ptr, pairs.ptr, items.ptr, cover.ptr, bounds.ptr,
-                                     -INFINITY, INFINITY));
-        MB_HIP(mbk::launch_hist(s, sh, bins_tiled, reinterpret_cast<const mbk::Entry *>(entries),
-                                items.ptr, ctl.ptr, partials.ptr, grid));
-        MB_HIP(mbk::launch_split(s, sh, sp, pairs.ptr, 1, partials.ptr, dummy.ptr, hist_out,
-                                 is_cat ? is_cat : cat0.ptr, monotone ? monotone : mono0.ptr,
-                                 mask1.ptr, ctl.ptr, count.ptr, node_g.ptr, node_h.ptr, 0,
-                                 reinterpret_cast<mbk::SplitResult *>(results)));
-        mbk::TreeCtl c{};
-        MB_HIP(hipMemcpyAsync(&c, ctl.ptr, sizeof c, hipMemcpyDeviceToHost, s));
-        MB_HIP(hipStreamSynchronize(s));
-        if (c.overflow) mb::internal("histogram item list overflow");
-        return 0;
-    }, -1);
-}
-
-int mbk_predict_forest(mbk_context *ctx, const int32_t *feature, const float *threshold,
-                       const uint8_t *flags, const float *leaf, const uint32_t *mask,
-                       int32_t num_trees, int32_t nodes_per_tree, const float *x, int64_t rows,
-                       int32_t data_bins, float base_score, float *out, char **err) {
-    return guarded(err, [&]() -> int {
-        mbk::ForestDev f{feature, threshold, flags, leaf, mask, num_trees, nodes_per_tree, 0, 1, 1};
-        MB_HIP(mbk::launch_predict_forest(ctx->dev->stream, f, x, rows, data_bins, base_score, out));
-        return 0;
-    }, -1);
-}
-
-void *mbk_fit(mbk_context *ctx, const char *params_json, const float *x, int64_t rows,
-              int64_t cols, int32_t row_major, const float *y, const float *w,
-              const float *x_valid, int64_t valid_rows, const float *y_valid, char **err) {
-    return guarded(err, [&]() -> void * {
-        if (!ctx) mb::internal("null kernel-seam context");
-        MB_HIP(hipStreamSynchronize(ctx->dev->stream));
-        mb::Params p = mb::parse_params(params_json);
-        mb::Trainer *t = mb::trainer_create_device(p, x, rows, cols, row_major != 0, y, w,
-                                                   x_valid, valid_rows, y_valid);
-        try {
-            if (ctx->profiling) mb::trainer_profile(t, true);
-            mb::trainer_grow(t, p.num_trees * mb::trainer_classes(t));
-            Booster *b = mb::trainer_booster(t);
-            if (ctx->profiling) {
-                int64_t n = 0, built[16];
-                double ms = 0, bytes = 0, lms[16];
-                mb::trainer_hist_stats(t, &n, &ms, &bytes);
-                mb::trainer_level_stats(t, 16, built, nullptr, lms);
-                ctx->prof_launches += n;
-                ctx->prof_ms += ms;
-                ctx->prof_bytes += bytes;
-                for (int d = 0; d < 16; ++d) {
-                    ctx->prof_built[d] += built[d];
-                    ctx->prof_level_ms[d] += lms[d];
-                }
-            }
-            mb::trainer_free(t);
-            return b;
-        } catch (...) {
-            mb::trainer_free(t);
-            throw;
-        }
-    }, nullptr);
-}
-
-// ---------------------------------------------------------------------------
-// extensions
-// ---------------------------------------------------------------------------
-
-int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err) {
-    return guarded(err, [&]() -> int {
-        if (!ctx) mb::internal("null kernel-seam context");
-        if (enable && !ctx->profiling) {
-            ctx->prof_launches = 0;
-            ctx->prof_ms = ctx->prof_bytes = 0;
-            for (int d = 0; d < 16; ++d) {
-                ctx->prof_built[d] = 0;
-                ctx->prof_level_ms[d] = 0;
-            }
-        }
-        ctx->profiling = enable != 0;
-        return 0;
-    }, -1);
-}
-
-int mbx_context_hist_stats(mbk_context *ctx, int32_t max_levels, int64_t *launches, double *ms,
-                           double *bytes, int64_t *built, double *level_ms, char **err) {
-    return guarded(err, [&]() -> int {
-        if (!ctx) mb::internal("null kernel-seam context");
-        if (launches) *launches = ctx->prof_launches;
-        if (ms) *ms = ctx->prof_ms;
-        if (bytes) *bytes = ctx->prof_bytes;
-        for (int d = 0; d < max_levels; ++d) {
-            if (built) built[d] = d < 16 ? ctx->prof_built[d] : 0;
-            if (level_ms) level_ms[d] = d < 16 ? ctx->prof_level_ms[d] : 0.0;
-        }
-        return 0;
-    }, -1);
-}
 
 void *mbx_trainer_create(const char *params_json, const float *x, int64_t rows, int64_t cols,
                          int32_t row_major, const float *y, const float *w, const float *x_valid,

@@ -1161,7 +1161,7 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
                                                 const uint64_t *__restrict__ partials,
                                                 const int64_t *__restrict__ hist_prev,
                                                 int64_t *__restrict__ hist_cur, const TreeCtl *ctl,
-                                                uint32_t blocks_per_tile) {
+                                                uint32_t blocks_per_tile, int derive) {
     constexpr int CELLS = 256 / S;
     __shared__ int64_t red[S > 1 ? S : 1][CELLS][2];
     const int W = sh.tile_w, nb = sh.num_bins, F = sh.cols, T = sh.num_tiles;
@@ -1213,7 +1213,7 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
     int64_t *hb = hist_cur + (((size_t)pr.built * nb + b) * F + f) * 2;
     hb[0] = g;
     hb[1] = h;
-    if (pr.derived != NONE) {
+    if (derive && pr.derived != NONE) {
         const int64_t *hp = hist_prev + (((size_t)pr.parent * nb + b) * F + f) * 2;
         int64_t *hd = hist_cur + (((size_t)pr.derived * nb + b) * F + f) * 2;
         hd[0] = hp[0] - g;
@@ -1223,17 +1223,46 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
 
 hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
                          const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
-                         const TreeCtl *ctl) {
+                         const TreeCtl *ctl, bool derive) {
     const uint32_t cells = (uint32_t)(sh.num_bins * sh.tile_w);
+    const int dv = derive ? 1 : 0;
     if (max_pairs >= 16) {                           // measured: S = 4 is faster below
         const uint32_t bpt = (cells + 255) / 256;
         hipLaunchKernelGGL(k_reduce<1>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
-                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt);
+                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
     } else {
         const uint32_t bpt = (cells + 63) / 64;
         hipLaunchKernelGGL(k_reduce<4>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
-                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt);
+                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
     }
+    return hipGetLastError();
+}
+
+// Sibling by subtraction on its own (subtract_histograms, Shaders.swift:313-326):
+// derived = parent - built for every pair of the level, exact int64, one
+// thread per (pair, bin, feature, channel).
+__global__ __launch_bounds__(256) void k_subtract(Shape sh, const Pair *__restrict__ pairs,
+                                                  const int64_t *__restrict__ hist_prev,
+                                                  int64_t *__restrict__ hist_cur,
+                                                  const TreeCtl *ctl, uint32_t blocks_per_pair) {
+    const uint32_t p = blockIdx.x / blocks_per_pair;
+    if (p >= ctl->num_pairs) return;                 // uniform per block
+    const Pair pr = pairs[p];
+    if (pr.derived == NONE) return;
+    const size_t cells = (size_t)sh.num_bins * (size_t)sh.cols * 2;
+    const size_t k = (size_t)(blockIdx.x % blocks_per_pair) * 256 + threadIdx.x;
+    if (k >= cells) return;
+    hist_cur[(size_t)pr.derived * cells + k] =
+        hist_prev[(size_t)pr.parent * cells + k] - hist_cur[(size_t)pr.built * cells + k];
+}
+
+hipError_t launch_subtract(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
+                           const int64_t *hist_prev, int64_t *hist_cur, const TreeCtl *ctl) {
+    const size_t cells = (size_t)sh.num_bins * (size_t)sh.cols * 2;
+    const uint32_t bpp = (uint32_t)((cells + 255) / 256);
+    if (max_pairs == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_subtract, dim3(max_pairs * bpp), dim3(256), 0, s, sh, pairs, hist_prev,
+                       hist_cur, ctl, bpp);
     return hipGetLastError();
 }
 
@@ -1542,8 +1571,19 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp, c
                         int64_t *node_g, int64_t *node_h, uint32_t level_start,
                         SplitResult *results) {
     if (sh.num_bins > 256) return hipErrorInvalidValue;
-    hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl);
+    hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl, true);
     if (e != hipSuccess) return e;
+    return launch_find_splits(s, sh, sp, pairs, max_pairs, hist_cur, is_cat, monotone, feat_mask,
+                              ctl, count, node_g, node_h, level_start, results);
+}
+
+hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams &sp,
+                              const Pair *pairs, uint32_t max_pairs, const int64_t *hist_cur,
+                              const uint8_t *is_cat, const int8_t *monotone,
+                              const uint8_t *feat_mask, const TreeCtl *ctl, const uint32_t *count,
+                              int64_t *node_g, int64_t *node_h, uint32_t level_start,
+                              SplitResult *results) {
+    if (sh.num_bins > 256) return hipErrorInvalidValue;
     const uint32_t groups = (uint32_t)((sh.cols + SPLIT_FEATS - 1) / SPLIT_FEATS);
     hipLaunchKernelGGL(k_split, dim3(max_pairs * groups), dim3(SPLIT_THREADS), 0, s, sh, sp, pairs,
                        hist_cur, is_cat, monotone, feat_mask, ctl, count, node_g, node_h,

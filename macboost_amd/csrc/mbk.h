@@ -238,6 +238,21 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp,
                         const TreeCtl *ctl, const uint32_t *count, int64_t *node_g,
                         int64_t *node_h, uint32_t level_start, SplitResult *results);
 
+// The two halves of launch_split, for the kernel seam: partials -> built
+// histograms (and, with derive, the derived siblings), and the split search
+// over histograms already in hist_cur; plus the subtraction on its own.
+hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
+                         const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
+                         const TreeCtl *ctl, bool derive);
+hipError_t launch_subtract(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
+                           const int64_t *hist_prev, int64_t *hist_cur, const TreeCtl *ctl);
+hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams &sp,
+                              const Pair *pairs, uint32_t max_pairs, const int64_t *hist_cur,
+                              const uint8_t *is_cat, const int8_t *monotone,
+                              const uint8_t *feat_mask, const TreeCtl *ctl, const uint32_t *count,
+                              int64_t *node_g, int64_t *node_h, uint32_t level_start,
+                              SplitResult *results);
+
 hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active,
                             uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
                             uint32_t *seg_start, uint32_t *count, Pair *pairs,

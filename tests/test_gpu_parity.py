@@ -293,6 +293,122 @@ def test_node_hist_full_size_exact(ctx):
         assert np.array_equal(hist[:, f, 1], np.bincount(b, weights=qh, minlength=nb).astype(np.int64)), f
 
 
+class _SeamTree:
+    """Device buffers of a level-wise tree grown through the mbk_* seam alone."""
+
+    def __init__(self, ctx, x_fm, is_cat, nb, tile_w, depth):
+        cols, rows = x_fm.shape
+        self.ctx, self.rows, self.cols, self.nb, self.D = ctx, rows, cols, nb, depth
+        T = (cols + tile_w - 1) // tile_w
+        nodes, lvl = 2 ** (depth + 1) - 1, 2 ** (depth - 1)
+        self.nodes = nodes
+        self.x = ctx.upload(x_fm)
+        self.is_cat = ctx.upload(np.asarray(is_cat, np.uint8))
+        self.edges = ctx.alloc(cols * (nb - 2) * 4)
+        ctx.call("mbk_quantile_edges", self.x, rows, cols, 1, rows, nb, self.is_cat, self.edges)
+        self.tiled, self.fm = ctx.alloc(rows * T * tile_w), ctx.alloc(rows * cols)
+        ctx.call("mbk_bin_data", self.x, rows, cols, 1, rows, self.edges, self.is_cat, nb, tile_w,
+                 self.tiled, self.fm)
+        self.ent = [ctx.alloc(rows * 8), ctx.alloc(rows * 8)]
+        self.hist = [ctx.alloc(lvl * nb * cols * 16), ctx.alloc(lvl * nb * cols * 16)]
+        self.results, self.max_gh = ctx.alloc(lvl * cols * 72), ctx.alloc(8)
+        self.shape = _core.MbkTreeShape(rows, cols, nb, tile_w, depth)
+        self.sp = _core.MbkSplitParams(1.0, 1.0, 0.0, 10.0, 0.1)
+
+    def out(self):
+        c, n = self.ctx, self.nodes
+        o = _core.MbkTreeOut(c.alloc(n * 12), c.alloc(n * 4), c.alloc(n * 4), c.alloc(n * 4),
+                             c.alloc(n * 32))
+        return o
+
+    def read(self, o):
+        c, n = self.ctx, self.nodes
+        split = c.download(o.split, (n, 3), np.int32)
+        return {"feature": split[:, 0], "bin": split[:, 1].view(np.uint32),
+                "flags": split[:, 2].view(np.uint32), "leaf": c.download(o.leaf, n, np.float32),
+                "gain": c.download(o.gain, n, np.float32),
+                "cover": c.download(o.cover, n, np.float32),
+                "mask": c.download(o.mask, (n, 8), np.uint32)}
+
+
+def _assert_tree_equals_oracle(got, ref, t, edges, nb):
+    f = ref.forest
+    assert np.array_equal(got["feature"], f.feature[t])
+    split = got["feature"] >= 0
+    assert np.array_equal(got["bin"][split], f.split_bin[t][split])
+    assert np.array_equal(got["flags"][split], f.flags[t][split])
+    for name in ("leaf", "gain", "cover"):
+        assert np.array_equal(got[name], getattr(f, name)[t]), name
+    if f.cat_mask is not None:
+        assert np.array_equal(got["mask"], f.cat_mask[t])
+    # thresholds come from the edges: edges[f * (nb - 2) + bin] for numeric splits
+    num = split & ((got["flags"] & O.FLAG_CATEGORICAL) == 0)
+    thr = edges.reshape(-1)[got["feature"][num] * (nb - 2) + got["bin"][num]]
+    assert np.array_equal(thr, f.threshold[t][num])
+
+
+@pytest.mark.parametrize("shape", ["mixed", "wide"])
+def test_trees_grown_through_the_seam_equal_the_oracle(ctx, shape):
+    # fitImpl's level loop on the kernel seam alone (Booster.swift:1467-1648):
+    # quantile edges, binning, then per tree quantise -> begin -> per level
+    # hist_build, hist_subtract, find_splits, decide_level, route -> final
+    # leaves; every tree array equals the oracle's, and so do the running
+    # predictions.  Then mbk_grow_tree (the same in one call) and mbk_treeshap.
+    if shape == "mixed":
+        x, y = _mixed(12_000)
+        is_cat, nb, tile_w, depth = [0] * 6 + [1], 64, 8, 5
+        mono = np.array([0, 0, 0, 1, 0, 0, 0], np.int8)
+    else:
+        x, y = mb.friedman(60_000, 100, 17)
+        is_cat, nb, tile_w, depth = [0] * 100, 256, 64, 6
+        mono = np.zeros(100, np.int8)
+    cols, rows = x.shape
+    trees = 3
+    ref = O.fit_raw(x, y, num_bins=nb, is_cat=is_cat, monotone=mono, num_trees=trees,
+                    max_depth=depth)
+    st = _SeamTree(ctx, x, is_cat, nb, tile_w, depth)
+    edges = ctx.download(st.edges, (cols, nb - 2), np.float32)
+    assert np.array_equal(edges, O.compute_edges(x, nb, is_cat))
+    labels = ctx.upload(y)
+    d_mono = ctx.upload(mono)
+    for one_call in (False, True):
+        preds = ctx.upload(np.full(rows, np.float32(ref.base_score), np.float32))
+        for t in range(trees):
+            o = st.out()
+            ctx.call("mbk_quantize", 0, 0.9, 0.0, preds, labels, None, rows, st.max_gh, st.ent[0])
+            if one_call:
+                ctx.call("mbk_grow_tree", ctypes.byref(st.shape), ctypes.byref(st.sp), st.tiled,
+                         st.fm, st.is_cat, d_mono, None, st.max_gh, st.ent[0], st.ent[1], rows,
+                         st.hist[0], st.hist[1], st.results, o, preds)
+            else:
+                ctx.call("mbk_tree_begin", ctypes.byref(st.shape), st.max_gh, rows, o)
+                with pytest.raises(mb.MacBoostError, match="out of order"):
+                    ctx.call("mbk_hist_build", 1, st.tiled, st.ent[0], st.hist[0])
+                for d in range(depth):
+                    cur, nxt = d % 2, 1 - d % 2
+                    ctx.call("mbk_hist_build", d, st.tiled, st.ent[cur], st.hist[cur])
+                    ctx.call("mbk_hist_subtract", d, st.hist[nxt], st.hist[cur])
+                    ctx.call("mbk_find_splits", d, st.hist[cur], st.is_cat, d_mono, None,
+                             ctypes.byref(st.sp), st.results)
+                    ctx.call("mbk_decide_level", d, st.results, d_mono, ctypes.byref(st.sp), o)
+                    ctx.call("mbk_route", d, st.fm, st.ent[cur], st.ent[nxt], o)
+                ctx.call("mbk_final_leaves", st.fm, ctypes.byref(st.sp), o, preds)
+            _assert_tree_equals_oracle(st.read(o), ref, t, edges, nb)
+        assert np.array_equal(ctx.download(preds, rows, np.float32), ref.preds)
+    # TreeSHAP of device rows under the oracle's forest (host arrays)
+    f = ref.forest
+    n = min(rows, 3000)
+    xs = np.ascontiguousarray(x[:, :n])
+    d_xs, d_out = ctx.upload(xs), ctx.alloc(n * (cols + 1) * 4)
+    mask = np.ascontiguousarray(f.cat_mask) if f.cat_mask is not None else None
+    ctx.call("mbk_treeshap", f.feature.ctypes.data, f.threshold.ctypes.data,
+             f.flags.ctypes.data, f.leaf.ctypes.data, f.cover.ctypes.data,
+             None if mask is None else mask.ctypes.data, f.num_trees, f.nodes_per_tree,
+             ref.base_score, nb - 1, d_xs, n, cols, d_out)
+    got = ctx.download(d_out, (n, cols + 1), np.float32)
+    assert np.allclose(got, O.treeshap(f, ref.base_score, nb, xs), rtol=1e-5, atol=1e-6)
+
+
 def test_fit_from_device_features_equals_macboost_train(ctx):
     # mbk_fit: the whole fit over raw features already in HBM gives the
     # model macboost_train gives from host memory, in both layouts, with the
