@@ -134,6 +134,24 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
                         float min_child_hess, float cat_smooth, int64_t *hist_out,
                         mbk_split_result *results, char **err);
 
+/* No counterpart in the reference.  mbk_node_hist_split for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same arguments and results,
+ * with every scratch buffer in one fixed 16 MiB device array of the library
+ * (one per GPU, held until the process ends).  Allocates nothing, fills its
+ * scratch with kernels and returns without waiting for the context's stream.
+ * Limits: 1..4096 features, and the node's histogram items must fit the
+ * array (at tile width 64 and 256 bins: 127 items of 128 KiB, i.e. nodes of
+ * up to ~60M rows); larger inputs fail with an error.  Every call on a GPU
+ * shares that GPU's array, which keeps the last call's contents: calls that
+ * overlap on one GPU (other streams, other threads) race. */
+int mbk_node_hist_split_noalloc(mbk_context *ctx, const uint8_t *bins_tiled, int64_t rows,
+                                int32_t cols, int32_t num_bins, int32_t tile_width,
+                                const uint32_t *entries, int64_t n, const uint32_t *max_gh,
+                                const uint8_t *is_cat, const int8_t *monotone, float lambda,
+                                float min_child_hess, float cat_smooth, int64_t *hist_out,
+                                mbk_split_result *results, char **err);
+
 /* predict_forest (Shaders.swift:1541-1584) on device buffers: flat forest of
  * num_trees*nodes_per_tree heap slots; mask may be NULL when no node is
  * categorical.  x feature-major [cols][rows]; out[rows]. */

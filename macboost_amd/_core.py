@@ -156,6 +156,8 @@ def _configure(l):
     l.mbk_fit.argtypes = [_P, ctypes.c_char_p, _P, ctypes.c_int64, ctypes.c_int64,
                           ctypes.c_int32, _f32_p, _f32_p, _f32_p, ctypes.c_int64, _f32_p,
                           _c_char_pp]
+    l.mbk_node_hist_split_noalloc.restype = ctypes.c_int
+    l.mbk_node_hist_split_noalloc.argtypes = l.mbk_node_hist_split.argtypes
     l.mbk_predict_forest.restype = ctypes.c_int
     l.mbk_predict_forest.argtypes = [_P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P,
                                      ctypes.c_int64, ctypes.c_int32, ctypes.c_float, _P,
@@ -223,7 +225,7 @@ EXPORTED = (
     "mbk_copy_to_device", "mbk_copy_to_host", "mbk_synchronize", "mbk_quantile_edges", "mbk_bin_data", "mbk_quantize",
     "mbk_node_hist_split", "mbk_predict_forest", "mbk_fit", "mbk_tree_begin", "mbk_hist_build",
     "mbk_hist_subtract", "mbk_find_splits", "mbk_decide_level", "mbk_route", "mbk_final_leaves",
-    "mbk_grow_tree", "mbk_treeshap",
+    "mbk_grow_tree", "mbk_treeshap", "mbk_node_hist_split_noalloc",
     "mbx_trainer_create", "mbx_trainer_grow", "mbx_trainer_profile", "mbx_trainer_hist_stats",
     "mbx_trainer_level_stats", "mbx_trainer_setup_seconds", "mbx_trainer_booster", "mbx_trainer_free", "mbx_friedman",
     "mbx_version", "mbx_dataset_make", "mbx_dataset_save", "mbx_dataset_load",

@@ -14,7 +14,13 @@
 
 #include "mbk.h"
 
+struct mbk_context;
+
 namespace mb {
+
+// The device and stream of a kernel-seam context (seam.cpp).
+int context_device(const mbk_context *ctx);
+hipStream_t context_stream(const mbk_context *ctx);
 
 // Errors carry the reference's message text (MacBoostError.description,
 // MetalEngine.swift:11-20).

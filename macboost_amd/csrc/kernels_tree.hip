@@ -1773,25 +1773,6 @@ __device__ uint32_t block_exclusive_scan(uint32_t *v, uint32_t n, uint32_t *wave
 }
 
 // level_built[level] records the built rows (added to, when accumulate).
-// Rows per histogram item for `total` built rows in num_pairs nodes.  At most
-// r items per workgroup of the grid (target_items): every (pair, tile) adds at
-// most one partial chunk, so reserve that slack (T * pairs) and pick the
-// smallest r whose chunk fits HIST_CHUNK_MAX.
-__device__ __forceinline__ uint32_t item_chunk(uint64_t total, uint32_t num_pairs,
-                                               int32_t num_tiles, uint32_t target_items,
-                                               uint32_t min_chunk) {
-    const uint64_t work = total * (uint64_t)num_tiles;
-    const uint64_t tgt = target_items ? target_items : 1;
-    const uint64_t slack = (uint64_t)num_pairs * (uint64_t)num_tiles;
-    const uint64_t need = (work + HIST_CHUNK_MAX - 1) / HIST_CHUNK_MAX;
-    uint64_t r = (slack + need + tgt - 1) / tgt;
-    if (tgt * r <= slack) r = slack / tgt + 1;
-    uint64_t c = (work + (tgt * r - slack) - 1) / (tgt * r - slack);
-    if (c < min_chunk) c = min_chunk;
-    if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
-    return (uint32_t)c;
-}
-
 // Pairs a planning block can hold in LDS: the deepest planned level at
 // maxDepth 12 has 2^11 nodes, i.e. at most 1024 sibling pairs.
 constexpr uint32_t PLAN_MAX_PAIRS = 1024;

@@ -22,6 +22,27 @@ constexpr int HIST_QH_BITS = 27;
 constexpr uint32_t HIST_CHUNK_MAX = (1u << 20) - 1;
 static_assert(127ull * HIST_CHUNK_MAX < (1ull << HIST_QH_BITS), "hessian field carries");
 
+// Rows per histogram item for `total` built rows in num_pairs nodes (host
+// and device: the planning kernels size a level's items with it, and the
+// host can predict the item count).  At most r items per workgroup of the
+// grid (target_items): every (pair, tile) adds at most one partial chunk, so
+// reserve that slack (T * pairs) and pick the smallest r whose chunk fits
+// HIST_CHUNK_MAX.
+__host__ __device__ inline uint32_t item_chunk(uint64_t total, uint32_t num_pairs,
+                                               int32_t num_tiles, uint32_t target_items,
+                                               uint32_t min_chunk) {
+    const uint64_t work = total * (uint64_t)num_tiles;
+    const uint64_t tgt = target_items ? target_items : 1;
+    const uint64_t slack = (uint64_t)num_pairs * (uint64_t)num_tiles;
+    const uint64_t need = (work + HIST_CHUNK_MAX - 1) / HIST_CHUNK_MAX;
+    uint64_t r = (slack + need + tgt - 1) / tgt;
+    if (tgt * r <= slack) r = slack / tgt + 1;
+    uint64_t c = (work + (tgt * r - slack) - 1) / (tgt * r - slack);
+    if (c < min_chunk) c = min_chunk;
+    if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
+    return (uint32_t)c;
+}
+
 // NodeSplit (Shaders.swift:466): feature < 0 marks a leaf.
 struct NodeSplit {
     int32_t feature;

@@ -184,6 +184,11 @@ void check_overflow(mbk_context *ctx) {
 
 }  // namespace
 
+namespace mb {
+int context_device(const mbk_context *ctx) { return ctx->dev->id; }
+hipStream_t context_stream(const mbk_context *ctx) { return ctx->dev->stream; }
+}  // namespace mb
+
 extern "C" {
 
 int mbk_context_create(int32_t device, mbk_context **out, char **err) {
