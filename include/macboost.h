@@ -97,7 +97,8 @@ int mbk_quantile_edges(mbk_context *ctx, const float *x, int64_t rows, int32_t c
 
 /* bin_data (Shaders.swift:46-76): raw f32 -> bins in two layouts, the
  * gather layout bins_tiled [rows][ceil(cols/tile_width)][tile_width] (row-major,
- * each row padded to a whole number of tiles with zero bytes) and the
+ * each row padded to a whole number of tiles with zero bytes, written by the
+ * call) and the
  * feature-major bins_fm [cols][rows].  edges: cols*(num_bins-2) f32. */
 int mbk_bin_data(mbk_context *ctx, const float *x, int64_t rows, int32_t cols,
                  int64_t row_stride, int64_t col_stride, const float *edges,

@@ -12,6 +12,8 @@
 #include <string>
 #include <vector>
 
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include "mbk.h"
 
 struct mbk_context;
@@ -21,6 +23,15 @@ namespace mb {
 // The device and stream of a kernel-seam context (seam.cpp).
 int context_device(const mbk_context *ctx);
 hipStream_t context_stream(const mbk_context *ctx);
+
+// A named range on the ROCm tracer's marker timeline (rocprofv3
+// --marker-trace) around one phase of host work; free when no tool listens.
+struct Phase {
+    explicit Phase(const char *name) { roctxRangePush(name); }
+    ~Phase() { roctxRangePop(); }
+    Phase(const Phase &) = delete;
+    Phase &operator=(const Phase &) = delete;
+};
 
 // Errors carry the reference's message text (MacBoostError.description,
 // MetalEngine.swift:11-20).
@@ -100,9 +111,10 @@ struct Device {
     Device &operator=(const Device &) = delete;
 };
 
-// Host -> device copy of a pageable buffer on stream s.  Copies of 64 MB or
-// more go through pinned staging and have completed on return; smaller ones
-// are one hipMemcpyAsync.
+// Host -> device copy of a pageable buffer on stream s.  Copies of 4 MB or
+// more go through pinned staging (in at least four pieces, host fills
+// overlapping the DMA) and have completed on return; smaller ones are one
+// hipMemcpyAsync.
 void upload(void *dst, const void *src, size_t bytes, hipStream_t s);
 // Device -> host copy into a pageable buffer after the work queued on s;
 // complete on return (64 MB or more through the pinned staging buffers).

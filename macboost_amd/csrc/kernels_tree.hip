@@ -141,66 +141,132 @@ __device__ __forceinline__ void row_grad_at(const GradParams &gp, const float *_
 }
 
 // ---------------------------------------------------------------------------
-// binning: raw f32 -> bin bytes, written to both layouts: the gather layout
-// [rows][T][W] (row r's tile t at (r*T + t)*W) and the feature-major [F][rows]
+// binning (bin_data, Shaders.swift:46-76): raw f32 -> bin bytes, written to
+// both layouts: the gather layout [rows][T][W] (row r's tile t at
+// (r*T + t)*W) and the feature-major [F][rows].
+//
+// A block takes BIN_ROWS rows of one group of G = min(16, W) features (one
+// 16-B chunk of every row's tile, or the whole 8-B tile at W = 8), in
+// sub-chunks of 256 rows, one row per thread.  Each thread loads its row's G
+// values at once (16-B loads for row-major input) and finds each bin by
+// binary lifting over the group's edges in LDS, padded with +inf to 255
+// entries: b = the number of edges below v, found in eight steps of one LDS
+// read, one compare and one select (for the non-decreasing quantile edges
+// this is the reference's binary search result, lower_bound(edges, v)).  It
+// writes its row's G bytes to the gather layout with one store and leaves
+// them in LDS; the block then writes the feature-major bytes as u32 words of
+// four rows.  Groups past the last feature write zero bytes, so the gather
+// layout needs no clearing.
 // ---------------------------------------------------------------------------
 
-template <int W>
-__global__ __launch_bounds__(256) void k_bin_data(const float *__restrict__ x, int64_t rows,
-                                                  int32_t cols, int64_t rs, int64_t cs,
-                                                  const float *__restrict__ edges,
-                                                  const uint8_t *__restrict__ is_cat,
-                                                  int32_t nb, uint8_t *__restrict__ tiled,
-                                                  uint8_t *__restrict__ fm, int rows_per_block) {
-    extern __shared__ float e_lds[];                 // W * (nb - 2)
-    const int t = blockIdx.y;
-    const int ne = nb - 2;
-    const int data_bins = nb - 1;
-    const int f0 = t * W;
-    const int nf = min(W, cols - f0);
-    for (int k = threadIdx.x; k < nf * ne; k += blockDim.x)
-        e_lds[k] = edges[(int64_t)f0 * ne + k];
+constexpr int BIN_THREADS = 256;
+constexpr int BIN_SUB = 256;                          // rows per sub-chunk (one per thread)
+constexpr int BIN_ROWS = 2048;                        // rows per block
+
+template <int G>
+__global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
+    const float *__restrict__ x, int64_t rows, int32_t cols, int64_t rs, int64_t cs,
+    const float *__restrict__ edges, const uint8_t *__restrict__ is_cat, int32_t nb, int32_t W,
+    int32_t T, uint8_t *__restrict__ tiled, uint8_t *__restrict__ fm, int vec_rows) {
+    __shared__ float e_lds[G * 256];                 // [feature][255 edges + pad], +inf padded
+    __shared__ __align__(16) uint8_t b_lds[G][BIN_SUB];
+    const int tid = threadIdx.x;
+    const int ne = nb - 2, data_bins = nb - 1;
+    // groups vary fastest over the blocks: the groups of one row block run
+    // together, so the pieces of each gather-layout row line are written close
+    // in time
+    const int ngroups = T * W / G;
+    const int g = (int)(blockIdx.x % (uint32_t)ngroups);   // features g*G .. g*G+G-1
+    const int64_t row_block = blockIdx.x / (uint32_t)ngroups;
+    const int f0 = g * G;
+    const int nf = max(0, min(G, cols - f0));         // real features of the group
+    const int t = f0 / W, chunk = (f0 % W) / G;       // tile and chunk the group fills
+    for (int k = tid; k < G * 256; k += BIN_THREADS) {
+        const int f = k >> 8, j = k & 255;
+        e_lds[k] = (f < nf && j < ne) ? edges[(int64_t)(f0 + f) * ne + j] : INFINITY;
+    }
+    uint32_t cat_bits = 0;
+    for (int k = 0; k < nf; ++k) cat_bits |= (is_cat[f0 + k] ? 1u : 0u) << k;
     __syncthreads();
-    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t r1 = min(rows, r0 + rows_per_block);
-    for (int64_t i = r0 + threadIdx.x; i < r1; i += blockDim.x) {
-        uint32_t words[W / 4];
+    // row-major input whose group starts 16-B aligned: 16-B loads
+    const bool rm16 = vec_rows != 0 && (f0 & 3) == 0 && nf == G;
+    const int64_t blk0 = row_block * BIN_ROWS;
+    for (int64_t r0 = blk0; r0 < min(rows, blk0 + BIN_ROWS); r0 += BIN_SUB) {
+        const int64_t r = r0 + tid;
+        const bool live = r < rows;
+        float v[G];
+        if (live && rm16) {
+            const float4 *src = reinterpret_cast<const float4 *>(x + r * rs + f0);
 #pragma unroll
-        for (int k = 0; k < W / 4; ++k) words[k] = 0;
+            for (int q = 0; q < G / 4; ++q) {
+                const float4 w = src[q];
+                v[4 * q] = w.x; v[4 * q + 1] = w.y; v[4 * q + 2] = w.z; v[4 * q + 3] = w.w;
+            }
+        } else {
 #pragma unroll
-        for (int k = 0; k < W; ++k) {
-            if (k < nf) {
-                const int f = f0 + k;
-                const float v = x[i * rs + (int64_t)f * cs];
-                uint32_t b;
-                if (isnan(v)) {
-                    b = (uint32_t)data_bins;
-                } else if (is_cat[f]) {
-                    int c = (int)rintf(v);
-                    c = c < 0 ? 0 : (c > data_bins - 1 ? data_bins - 1 : c);
-                    b = (uint32_t)c;
-                } else {
-                    const float *e = e_lds + k * ne;
-                    uint32_t lo = 0, hi = (uint32_t)(data_bins - 1);
-                    while (lo < hi) {
-                        uint32_t mid = (lo + hi) >> 1;
-                        if (v > e[mid]) lo = mid + 1; else hi = mid;
-                    }
-                    b = lo;
+            for (int k = 0; k < G; ++k)
+                v[k] = (live && k < nf) ? x[r * rs + (int64_t)(f0 + k) * cs] : 0.0f;
+        }
+        uint32_t b[G];
+#pragma unroll
+        for (int k0 = 0; k0 < G; k0 += 4) {
+            uint32_t lo[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lo[j] = 0;
+            // lo = #edges < v: padding (+inf) never counts, so lo <= ne
+#pragma unroll
+            for (int s = 128; s >= 1; s >>= 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t up = lo[j] + (uint32_t)s;
+                    lo[j] = v[k0 + j] > e_lds[(k0 + j) * 256 + (int)up - 1] ? up : lo[j];
                 }
-                fm[(int64_t)f * rows + i] = (uint8_t)b;
-                words[k >> 2] |= b << (8 * (k & 3));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = k0 + j;
+                const float val = v[k];
+                uint32_t bb = lo[j];
+                if (isnan(val)) {
+                    bb = (uint32_t)data_bins;
+                } else if ((cat_bits >> k) & 1u) {
+                    int c = (int)rintf(val);
+                    c = c < 0 ? 0 : (c > data_bins - 1 ? data_bins - 1 : c);
+                    bb = (uint32_t)c;
+                }
+                b[k] = k < nf ? bb : 0u;
             }
         }
-        uint8_t *dst = tiled + (i * (int64_t)gridDim.y + t) * W;
-        if constexpr (W >= 16) {
+        uint32_t word[G / 4];
 #pragma unroll
-            for (int k = 0; k < W / 16; ++k)
-                reinterpret_cast<uint4 *>(dst)[k] =
-                    make_uint4(words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]);
-        } else {
-            *reinterpret_cast<uint2 *>(dst) = make_uint2(words[0], words[1]);
+        for (int q = 0; q < G / 4; ++q)
+            word[q] = b[4 * q] | (b[4 * q + 1] << 8) | (b[4 * q + 2] << 16) | (b[4 * q + 3] << 24);
+        if (live) {
+            uint8_t *dst = tiled + (r * T + t) * (int64_t)W + chunk * G;
+            if constexpr (G == 16)
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(word[0], word[1], word[2], word[3]);
+            else
+                *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[1]);
         }
+#pragma unroll
+        for (int k = 0; k < G; ++k) b_lds[k][tid] = (uint8_t)b[k];
+        __syncthreads();
+        // feature-major bytes: u32 words of four rows when the rows of every
+        // feature start 4-B aligned and the sub-chunk is whole, else bytes
+        const int64_t n_here = min((int64_t)BIN_SUB, rows - r0);
+        if ((rows & 3) == 0 && n_here == BIN_SUB) {
+            for (int w = tid; w < nf * (BIN_SUB / 4); w += BIN_THREADS) {
+                const int k = w / (BIN_SUB / 4), q = w % (BIN_SUB / 4);
+                const uint32_t val = *reinterpret_cast<const uint32_t *>(&b_lds[k][4 * q]);
+                *reinterpret_cast<uint32_t *>(fm + (int64_t)(f0 + k) * rows + r0 + 4 * q) = val;
+            }
+        } else {
+            for (int w = tid; w < nf * BIN_SUB; w += BIN_THREADS) {
+                const int k = w / BIN_SUB, j = w % BIN_SUB;
+                if (j < n_here) fm[(int64_t)(f0 + k) * rows + r0 + j] = b_lds[k][j];
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -208,25 +274,19 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            int64_t rs, int64_t cs, const float *edges, const uint8_t *is_cat,
                            int32_t nb, int32_t tile_w, int32_t num_tiles, uint8_t *tiled,
                            uint8_t *fm) {
-    const int rpb = 4096;
-    dim3 grid((unsigned)((rows + rpb - 1) / rpb), (unsigned)num_tiles);
-    size_t lds = (size_t)tile_w * (size_t)(nb - 2) * sizeof(float);
-    hipError_t e = hipSuccess;
-    switch (tile_w) {
-    case 8: e = hipFuncSetAttribute((const void *)k_bin_data<8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); break;
-    case 16: e = hipFuncSetAttribute((const void *)k_bin_data<16>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); break;
-    case 32: e = hipFuncSetAttribute((const void *)k_bin_data<32>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); break;
-    case 64: e = hipFuncSetAttribute((const void *)k_bin_data<64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); break;
-    default: return hipErrorInvalidValue;
-    }
-    if (e != hipSuccess) return e;
-    switch (tile_w) {
-    case 8: hipLaunchKernelGGL(k_bin_data<8>, grid, dim3(256), lds, s, x, rows, cols, rs, cs, edges, is_cat, nb, tiled, fm, rpb); break;
-    case 16: hipLaunchKernelGGL(k_bin_data<16>, grid, dim3(256), lds, s, x, rows, cols, rs, cs, edges, is_cat, nb, tiled, fm, rpb); break;
-    case 32: hipLaunchKernelGGL(k_bin_data<32>, grid, dim3(256), lds, s, x, rows, cols, rs, cs, edges, is_cat, nb, tiled, fm, rpb); break;
-    case 64: hipLaunchKernelGGL(k_bin_data<64>, grid, dim3(256), lds, s, x, rows, cols, rs, cs, edges, is_cat, nb, tiled, fm, rpb); break;
-    default: return hipErrorInvalidValue;
-    }
+    if (nb < 4 || nb > 256 || rows <= 0) return rows == 0 ? hipSuccess : hipErrorInvalidValue;
+    if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) return hipErrorInvalidValue;
+    const int G = tile_w >= 16 ? 16 : 8;
+    const int64_t nblk = (rows + BIN_ROWS - 1) / BIN_ROWS * (int64_t)(num_tiles * tile_w / G);
+    if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)nblk);
+    const int vec_rows = cs == 1 && (rs & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (G == 16)
+        hipLaunchKernelGGL(k_bin_data<16>, grid, dim3(BIN_THREADS), 0, s, x, rows, cols, rs, cs,
+                           edges, is_cat, nb, tile_w, num_tiles, tiled, fm, vec_rows);
+    else
+        hipLaunchKernelGGL(k_bin_data<8>, grid, dim3(BIN_THREADS), 0, s, x, rows, cols, rs, cs,
+                           edges, is_cat, nb, tile_w, num_tiles, tiled, fm, vec_rows);
     return hipGetLastError();
 }
 

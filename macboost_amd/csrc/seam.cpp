@@ -266,7 +266,6 @@ int mbk_bin_data(mbk_context *ctx, const float *x, int64_t rows, int32_t cols, i
     return guarded(err, [&]() -> int {
         if (num_bins < 4 || num_bins > 256) mb::invalid("numBins must be in 4...256");
         const int tiles = (cols + tile_width - 1) / tile_width;
-        MB_HIP(hipMemsetAsync(bins_tiled, 0, (size_t)tiles * rows * tile_width, ctx->dev->stream));
         MB_HIP(mbk::launch_bin_data(ctx->dev->stream, x, rows, cols, row_stride, col_stride, edges,
                                     is_cat, num_bins, tile_width, tiles, bins_tiled, bins_fm));
         return 0;

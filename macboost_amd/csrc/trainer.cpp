@@ -26,6 +26,32 @@ int host_threads() {
     return (int)n;
 }
 
+// Runs fn(begin, end) over [0, n) in blocks of `block` items on up to
+// host_threads() threads (block b is [b*block, min(n, (b+1)*block))), and
+// waits; fn must only write what its own block owns.
+template <typename Fn>
+static void parallel_blocks(int64_t n, int64_t block, Fn fn) {
+    const int64_t nblocks = (n + block - 1) / block;
+    const int nt = (int)std::min<int64_t>(host_threads(), nblocks);
+    if (nt <= 1) {
+        for (int64_t b = 0; b < nblocks; ++b) fn(b * block, std::min(n, (b + 1) * block));
+        return;
+    }
+    std::atomic<int64_t> next{0};
+    auto work = [&] {
+        for (int64_t b = next++; b < nblocks; b = next++) fn(b * block, std::min(n, (b + 1) * block));
+    };
+    std::vector<std::thread> ts;
+    for (int k = 1; k < nt; ++k) ts.emplace_back(work);
+    work();
+    for (auto &th : ts) th.join();
+}
+
+// Rows per block of the sums over every row (base score): each block is
+// summed in row order in double, then the block sums in block order, so
+// the result does not depend on how blocks are spread over threads.
+constexpr int64_t SUM_BLOCK = 65536;
+
 static double now_s() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch())
         .count();
@@ -72,6 +98,7 @@ Device::~Device() {
 
 namespace {
 constexpr size_t STAGE_CHUNK = (size_t)64 << 20;
+constexpr size_t STAGE_MIN = (size_t)4 << 20;     // smaller copies go straight from pageable memory
 
 struct Staging {
     std::mutex m;
@@ -112,7 +139,7 @@ unsigned copy_threads() {
 }  // namespace
 
 void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
-    if (bytes < STAGE_CHUNK) {
+    if (bytes < STAGE_MIN) {
         MB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
         return;
     }
@@ -128,10 +155,12 @@ void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
     MB_HIP(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
     const char *from = static_cast<const char *>(src);
     char *to = static_cast<char *>(dst);
+    // at least four pieces, so the host fill of one overlaps the DMA of another
+    const size_t piece = std::min(STAGE_CHUNK, std::max(STAGE_MIN, (bytes + 3) / 4));
     size_t k = 0;
-    for (size_t off = 0; off < bytes; off += STAGE_CHUNK, ++k) {
+    for (size_t off = 0; off < bytes; off += piece, ++k) {
         const int b = (int)(k & 1);
-        const size_t n = std::min(STAGE_CHUNK, bytes - off);
+        const size_t n = std::min(piece, bytes - off);
         if (k >= 2) MB_HIP(hipEventSynchronize(ev[b]));   // its previous DMA is done
         parallel_copy(st.buf[b], from + off, n, threads);
         MB_HIP(hipMemcpyAsync(to + off, st.buf[b], n, hipMemcpyHostToDevice, s));
@@ -303,10 +332,11 @@ struct Trainer {
     }
 };
 
-static void validate_labels(const Params &p, const float *y, int64_t n) {   // :1724-1765
+// The check of one label; throws the reference's message for row i.
+static void check_label(const Params &p, const float *y, int64_t i) {
     const bool logistic = p.objective == OBJ_LOGISTIC;
     const bool nonneg = p.objective == OBJ_POISSON || p.objective == OBJ_TWEEDIE;
-    for (int64_t i = 0; i < n; ++i) {
+    {
         float v = y[i];
         if (!std::isfinite(v))
             invalid("label at row " + std::to_string(i) + " is " + swift_float(v) +
@@ -325,6 +355,26 @@ static void validate_labels(const Params &p, const float *y, int64_t n) {   // :
                         std::to_string(p.num_classes));
         }
     }
+}
+
+// Labels (Booster.swift:1724-1765), scanned in blocks on the host threads;
+// the first offending row over all blocks gets the message.
+static void validate_labels(const Params &p, const float *y, int64_t n) {
+    const int64_t block = 1 << 18;
+    const int64_t nblocks = (n + block - 1) / block;
+    std::vector<int64_t> first((size_t)nblocks, -1);
+    parallel_blocks(n, block, [&](int64_t a, int64_t b) {
+        for (int64_t i = a; i < b; ++i) {
+            try {
+                check_label(p, y, i);
+            } catch (const Error &) {
+                first[(size_t)(a / block)] = i;
+                return;
+            }
+        }
+    });
+    for (int64_t f : first)
+        if (f >= 0) check_label(p, y, f);
 }
 
 void validate_label_values(const Params &p, const float *y, int64_t n) { validate_labels(p, y, n); }
@@ -423,23 +473,37 @@ static float base_score(const Params &p, const float *y, const float *w, int64_t
                                               (int64_t)((float)s.size() * q));
         return s[(size_t)idx];
     }
+    const int64_t nblocks = (n + SUM_BLOCK - 1) / SUM_BLOCK;
+    std::vector<double> s1((size_t)nblocks, 0.0), s2((size_t)nblocks, 0.0);
     if (p.objective == OBJ_LOGISTIC) {                     // :802-830
-        double pos = 0, tot = 0;
         const double spw = (double)p.scale_pos_weight;
-        for (int64_t i = 0; i < n; ++i) {
-            double wi = w ? (double)w[i] : 1.0;
-            if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
-        }
+        parallel_blocks(n, SUM_BLOCK, [&](int64_t a, int64_t b) {
+            double pos = 0, tot = 0;
+            for (int64_t i = a; i < b; ++i) {
+                double wi = w ? (double)w[i] : 1.0;
+                if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
+            }
+            s1[(size_t)(a / SUM_BLOCK)] = pos;
+            s2[(size_t)(a / SUM_BLOCK)] = tot;
+        });
+        double pos = 0, tot = 0;
+        for (int64_t k = 0; k < nblocks; ++k) { pos += s1[(size_t)k]; tot += s2[(size_t)k]; }
         float pr = (float)(pos / std::max(tot, 1e-12));
         pr = std::min(std::max(pr, 1e-6f), 1.0f - 1e-6f);
         return std::log(pr / (1.0f - pr));
     }
+    parallel_blocks(n, SUM_BLOCK, [&](int64_t a, int64_t b) {
+        double num = 0, den = 0;
+        for (int64_t i = a; i < b; ++i) {
+            double wi = w ? (double)w[i] : 1.0;
+            num += wi * (double)y[i];
+            den += wi;
+        }
+        s1[(size_t)(a / SUM_BLOCK)] = num;
+        s2[(size_t)(a / SUM_BLOCK)] = den;
+    });
     double num = 0, den = 0;
-    for (int64_t i = 0; i < n; ++i) {
-        double wi = w ? (double)w[i] : 1.0;
-        num += wi * (double)y[i];
-        den += wi;
-    }
+    for (int64_t k = 0; k < nblocks; ++k) { num += s1[(size_t)k]; den += s2[(size_t)k]; }
     float m = den > 0 ? (float)(num / den) : 0.0f;
     if (p.objective == OBJ_POISSON || p.objective == OBJ_TWEEDIE) {
         if (!(m > 0)) invalid(objective_name(p.objective) + " requires a positive label mean");
@@ -529,11 +593,18 @@ static float eval_metric(const Params &p, const float *pred, const float *y, int
 static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
                             const float *w, const float *xv, int64_t vrows, const float *yv) {
     validate_labels(p, y, rows);
-    if (w)
-        for (int64_t i = 0; i < rows; ++i)
-            if (!(std::isfinite(w[i]) && w[i] >= 0))
+    if (w) {
+        const int64_t block = 1 << 18;
+        std::vector<int64_t> first((size_t)((rows + block - 1) / block), -1);
+        parallel_blocks(rows, block, [&](int64_t a, int64_t b) {
+            for (int64_t i = a; i < b; ++i)
+                if (!(std::isfinite(w[i]) && w[i] >= 0)) { first[(size_t)(a / block)] = i; return; }
+        });
+        for (int64_t i : first)
+            if (i >= 0)
                 invalid("weight at row " + std::to_string(i) + " is " + swift_float(w[i]) +
                         "; weights must be finite and >= 0");
+    }
     if (xv && yv && vrows > 0) validate_labels(p, yv, vrows);
     if (p.has_monotone && (int64_t)p.monotone.size() != cols)
         invalid("monotoneConstraints has " + std::to_string(p.monotone.size()) +
@@ -654,14 +725,14 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.gp.num_classes = K;
     t.gp.class_index = 0;
     t.gp.rows = rows;
-    t.labels_h.assign(y, y + rows);
+    // the host keeps no copy of the labels: a train metric reads them back
     t.labels.alloc((size_t)rows);
     t.preds.alloc((size_t)rows * (size_t)K);
-    MB_HIP(hipMemcpyAsync(t.labels.ptr, y, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+    upload(t.labels.ptr, y, (size_t)rows * 4, s);
     if (w) {
         t.has_weights = true;
         t.weights.alloc((size_t)rows);
-        MB_HIP(hipMemcpyAsync(t.weights.ptr, w, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+        upload(t.weights.ptr, w, (size_t)rows * 4, s);
     }
     if (K > 1) {
         // per-class log priors with +1 smoothing (Booster.swift:838-846)
@@ -673,6 +744,7 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         for (int k = 0; k < K; ++k) t.base_scores[(size_t)k] = (float)std::log(cnt[(size_t)k] / total);
         t.base = 0.0f;
     } else {
+        Phase ph("base score");
         t.base = base_score(p, y, w, rows);
         t.base_scores = {t.base};
     }
@@ -846,8 +918,12 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
                            int64_t cols, bool row_major, const float *y, const float *w,
                            const float *xv, int64_t vrows, const float *yv) {
     if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
-    validate_params(pin);
-    validate_inputs(pin, rows, cols, y, w, xv, vrows, yv);
+    Phase ph_all("fit setup");
+    {
+        Phase ph("validate inputs");
+        validate_params(pin);
+        validate_inputs(pin, rows, cols, y, w, xv, vrows, yv);
+    }
     auto tr = std::make_unique<Trainer>();
     Trainer &t = *tr;
     t.p = pin;
@@ -890,7 +966,10 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
     setup_shape(t, rows, cols);
     hipStream_t s = t.dev->stream;
     const int tile_w = t.sh.tile_w;
-    if (x_on_device) check_device_features(p, x, rows, cols, rs, cs, y, s, leak_warnings);
+    if (x_on_device) {
+        Phase ph("device feature checks");
+        check_device_features(p, x, rows, cols, rs, cs, y, s, leak_warnings);
+    }
 
     // --- binning on the device: (upload,) quantile edges, bin_data --------
     double t0 = now_s();
@@ -905,6 +984,7 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
         const size_t ne = (size_t)p.num_bins - 2;
         DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
         {
+            Phase ph("quantile edges");
             const double te = now_s();
             const size_t cap = mbk::edge_sample_cap(rows);
             DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
@@ -915,9 +995,9 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
             MB_HIP(hipStreamSynchronize(s));
             t.t_edges = now_s() - te;
         }
+        Phase ph("bin data");
         t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
         t.bins_fm.alloc((size_t)rows * (size_t)cols);
-        MB_HIP(hipMemsetAsync(t.bins_tiled.ptr, 0, t.bins_tiled.bytes(), s));
         MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
                                     p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
                                     t.bins_fm.ptr));
@@ -925,6 +1005,7 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
         MB_HIP(hipStreamSynchronize(s));
     }
     t.t_bin = now_s() - t0 - t.t_edges;              // (upload +) bin_data
+    Phase ph_rest("labels, base score, buffers");
     if (leak.th.joinable()) leak.th.join();
     if (leak_error) std::rethrow_exception(leak_error);
     t.warnings.insert(t.warnings.begin(), leak_warnings.begin(), leak_warnings.end());
@@ -1304,6 +1385,7 @@ static void grow_leafwise(Trainer &t, int tree) {
 }
 
 void trainer_grow(Trainer *tp, int num_trees) {
+    Phase ph("grow trees");
     Trainer &t = *tp;
     hipStream_t s = t.dev->stream;
     t.ensure_capacity(t.grown + num_trees);
@@ -1335,6 +1417,11 @@ void trainer_grow(Trainer *tp, int num_trees) {
         if (log_now) {
             std::vector<float> tp_h((size_t)t.rows * (size_t)K);
             MB_HIP(hipMemcpy(tp_h.data(), t.preds.ptr, tp_h.size() * 4, hipMemcpyDeviceToHost));
+            if (t.labels_h.empty()) {
+                t.labels_h.resize((size_t)t.rows);
+                MB_HIP(hipMemcpy(t.labels_h.data(), t.labels.ptr, t.labels_h.size() * 4,
+                                 hipMemcpyDeviceToHost));
+            }
             char buf[128];
             std::snprintf(buf, sizeof buf, "[%4d] train-%s: %.5f", round,
                           effective_metric(t.p).c_str(),
@@ -1447,6 +1534,7 @@ void trainer_setup_seconds(Trainer *t, double *edges_s, double *bin_s) {
 // Read finished trees back (drainPending, Booster.swift:903-948): reachable
 // nodes only, numeric thresholds from the bin edges.
 Booster *trainer_booster(Trainer *tp) {
+    Phase ph("model readback");
     Trainer &t = *tp;
     MB_HIP(hipStreamSynchronize(t.dev->stream));
     const int n = t.grown;
@@ -1519,7 +1607,10 @@ Booster *trainer_booster(Trainer *tp) {
     return b.release();
 }
 
-void trainer_free(Trainer *t) { delete t; }
+void trainer_free(Trainer *t) {
+    Phase ph("release trainer");
+    delete t;
+}
 
 int trainer_classes(const Trainer *t) { return t->K; }
 

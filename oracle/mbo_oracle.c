@@ -160,24 +160,48 @@ void orc_bin_matrix(const float *x, int64_t rows, int32_t cols, int64_t rs, int6
 /* rounded once (the reference uses vDSP, whose order is unspecified).      */
 /* ------------------------------------------------------------------------ */
 
+/* Sums over every row are taken in blocks of 65,536 rows: each block in row
+ * order in double, then the block sums in block order (the reference's vDSP
+ * sums leave the order unspecified). */
+#define ORC_SUM_BLOCK 65536
+
 float orc_base_score(const float *y, const float *w, int64_t rows, int32_t obj, float spw) {
+    const int64_t nblk = (rows + ORC_SUM_BLOCK - 1) / ORC_SUM_BLOCK;
+    double *s1 = (double *)calloc((size_t)(nblk > 0 ? nblk : 1), sizeof(double));
+    double *s2 = (double *)calloc((size_t)(nblk > 0 ? nblk : 1), sizeof(double));
     if (obj == ORC_OBJ_LOGISTIC) {
-        double pos = 0, tot = 0;
-        for (int64_t i = 0; i < rows; ++i) {
-            double wi = w ? (double)w[i] : 1.0;
-            if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
+#pragma omp parallel for schedule(dynamic, 1)
+        for (int64_t b = 0; b < nblk; ++b) {
+            double pos = 0, tot = 0;
+            const int64_t hi = (b + 1) * ORC_SUM_BLOCK < rows ? (b + 1) * ORC_SUM_BLOCK : rows;
+            for (int64_t i = b * ORC_SUM_BLOCK; i < hi; ++i) {
+                double wi = w ? (double)w[i] : 1.0;
+                if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
+            }
+            s1[b] = pos; s2[b] = tot;
         }
+        double pos = 0, tot = 0;
+        for (int64_t b = 0; b < nblk; ++b) { pos += s1[b]; tot += s2[b]; }
+        free(s1); free(s2);
         float p = (float)(pos / (tot > 1e-12 ? tot : 1e-12));
         if (p < 1e-6f) p = 1e-6f;
         if (p > 1.0f - 1e-6f) p = 1.0f - 1e-6f;
         return logf(p / (1.0f - p));
     }
-    double num = 0, den = 0;
-    for (int64_t i = 0; i < rows; ++i) {
-        double wi = w ? (double)w[i] : 1.0;
-        num += wi * (double)y[i];
-        den += wi;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t b = 0; b < nblk; ++b) {
+        double num = 0, den = 0;
+        const int64_t hi = (b + 1) * ORC_SUM_BLOCK < rows ? (b + 1) * ORC_SUM_BLOCK : rows;
+        for (int64_t i = b * ORC_SUM_BLOCK; i < hi; ++i) {
+            double wi = w ? (double)w[i] : 1.0;
+            num += wi * (double)y[i];
+            den += wi;
+        }
+        s1[b] = num; s2[b] = den;
     }
+    double num = 0, den = 0;
+    for (int64_t b = 0; b < nblk; ++b) { num += s1[b]; den += s2[b]; }
+    free(s1); free(s2);
     float m = den > 0 ? (float)(num / den) : 0.0f;
     if (obj == ORC_OBJ_POISSON || obj == ORC_OBJ_TWEEDIE) return logf(m);
     return m;
