@@ -2122,6 +2122,10 @@ __device__ __forceinline__ bool route_block(const NodeSplit sp, const uint32_t *
     return true;
 }
 
+// A persistent grid: each block computes the level's block prefix once and
+// then takes logical blocks b, b + gridDim.x, ... (the logical blocks a level
+// needs depend on its live rows, known only on the device; a sampled tree
+// needs far fewer than the launch could hold).
 __global__ __launch_bounds__(PART_THREADS) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
@@ -2130,7 +2134,6 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
     extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
     __shared__ uint32_t s_mask[8];
     __shared__ uint32_t wave_tot[PART_WAVES + 1];
-    const uint32_t b = blockIdx.x;
     // blocks per split node of the routed level, and their prefix
     for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
         const uint32_t nn = la.level_start + l;
@@ -2139,22 +2142,24 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
     }
     __syncthreads();
     const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
-    if (b >= total_blocks) return;                   // uniform per block
-    // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
-    uint32_t lo = 0, hi = la.num_level - 1;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi + 1) >> 1;
-        if (blk_prefix[mid] <= b) lo = mid; else hi = mid - 1;
+    for (uint32_t b = blockIdx.x; b < total_blocks; b += gridDim.x) {   // uniform per block
+        // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
+        uint32_t lo = 0, hi = la.num_level - 1;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) >> 1;
+            if (blk_prefix[mid] <= b) lo = mid; else hi = mid - 1;
+        }
+        const uint32_t l = lo, n = la.level_start + l;
+        const uint32_t start = seg_start[l], cnt = count[n];
+        const uint32_t first = (b - blk_prefix[l]) * PART_BLOCK;
+        const NodeSplit sp = out.split[n];
+        if (threadIdx.x < 8) s_mask[threadIdx.x] = out.mask[(size_t)n * 8 + threadIdx.x];
+        __syncthreads();
+        route_block(sp, s_mask, sh.num_bins, bins_fm + (size_t)sp.feature * (size_t)sh.rows,
+                    order_in + start + first, min((uint32_t)PART_BLOCK, cnt - first), cnt,
+                    order_out + start, &cursors[(size_t)l * CURSOR_STRIDE], write_entries != 0);
+        __syncthreads();                             // LDS reuse by the next logical block
     }
-    const uint32_t l = lo, n = la.level_start + l;
-    const uint32_t start = seg_start[l], cnt = count[n];
-    const uint32_t first = (b - blk_prefix[l]) * PART_BLOCK;
-    const NodeSplit sp = out.split[n];
-    if (threadIdx.x < 8) s_mask[threadIdx.x] = out.mask[(size_t)n * 8 + threadIdx.x];
-    __syncthreads();
-    route_block(sp, s_mask, sh.num_bins, bins_fm + (size_t)sp.feature * (size_t)sh.rows,
-                order_in + start + first, min((uint32_t)PART_BLOCK, cnt - first), cnt,
-                order_out + start, &cursors[(size_t)l * CURSOR_STRIDE], write_entries != 0);
 }
 
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,

@@ -311,8 +311,10 @@ hipError_t launch_renew(hipStream_t s, const uint8_t *bins_fm, int64_t rows, int
 // Partition of the routed level (d-1): every split node's interval is split
 // in place between its children (left from the front, right from the back).
 // Node l's cursor is cursors[l * CURSOR_STRIDE]: left count in the low word,
-// right count in the high word; the level's k_decide zeroes them.  max_blocks >= ceil(rows/PART_ENTRIES) +
-// nodes of the level.  write_entries = false only counts (terminal level).
+// right count in the high word; the level's k_decide zeroes them.  max_blocks
+// is the persistent grid (any size >= 1; each block takes every max_blocks-th
+// of the level's PART_ENTRIES-entry blocks).  write_entries = false only
+// counts (terminal level).
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, const uint32_t *count, const TreeOut out,

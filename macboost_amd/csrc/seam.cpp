@@ -128,7 +128,8 @@ void reserve_tree(mbk_context *ctx, const mbk_tree_shape &shape) {
     int64_t items = T * ((rows + mbk::HIST_CHUNK_MAX - 1) / mbk::HIST_CHUNK_MAX) +
                     t.target_items + 1 + T * level_nodes;
     items = std::min<int64_t>(items, T * ((rows + t.min_chunk - 1) / t.min_chunk + level_nodes + 1));
-    t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES + level_nodes);
+    t.route_grid = (uint32_t)std::min<int64_t>(
+        2 * (int64_t)ctx->dev->num_cus, (rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES + level_nodes);
     reserve(t.ctl, 1);
     reserve(t.seg_a, (size_t)1 << D);
     reserve(t.seg_b, (size_t)1 << D);

@@ -803,8 +803,11 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         MB_HIP(hipMemsetAsync(t.goss_buckets.ptr, 0, 1024 * sizeof(uint32_t), s));
     }
     // level-wise partition: one block per PART_ENTRIES entries of a split node
-    t.route_grid = (uint32_t)((rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES) +
-                   (uint32_t)t.max_level_nodes;
+    // persistent partition grid: two 1024-thread blocks per CU, or fewer when
+    // a level can never need that many
+    t.route_grid = (uint32_t)std::min<int64_t>(
+        2 * (int64_t)t.dev->num_cus,
+        (rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES + t.max_level_nodes);
     t.route_cursor.alloc((size_t)t.max_level_nodes * mbk::CURSOR_STRIDE);
 
     // histogram work decomposition
