@@ -7,6 +7,8 @@
 // extending/unwinding in double precision and accumulating the row's phi in
 // LDS (the wavefront owns it, so the summation order is fixed), with a single
 // rounding to f32 at the end.
+#include <algorithm>
+
 #include "mbk.h"
 
 #include <math.h>
@@ -57,6 +59,21 @@ hipError_t launch_predict_forest(hipStream_t s, const ForestDev &f, const float 
     return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device id).
+static int device_cus() {
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 // The same walk over the training rows, eight rows per thread walked level by
 // level together, that also counts the rows reaching each node of the deepest
 // level (counters in LDS, one global add per non-empty node per block).  The
@@ -69,7 +86,8 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
                                                              int64_t rows, int32_t nb,
                                                              int32_t max_depth, TreeOut tree,
                                                              float *__restrict__ preds,
-                                                             uint32_t *__restrict__ count) {
+                                                             uint32_t *__restrict__ count,
+                                                             const uint8_t *__restrict__ kept) {
     extern __shared__ uint32_t wc_lds[];
     const uint32_t deep = 1u << max_depth, deep_start = deep - 1;
     const uint32_t internal = deep - 1, total = 2 * deep - 1;
@@ -85,36 +103,48 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
     }
     for (uint32_t k = threadIdx.x; k < total; k += blockDim.x) s_leaf[k] = tree.leaf[k];
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * (WALK_THREADS * WALK_ROWS) + threadIdx.x;
-    uint32_t n[WALK_ROWS];
+    constexpr int64_t CHUNK = (int64_t)WALK_THREADS * WALK_ROWS;
+    for (int64_t c0 = (int64_t)blockIdx.x * CHUNK; c0 < rows; c0 += (int64_t)gridDim.x * CHUNK) {
+        const int64_t base = c0 + threadIdx.x;
+        uint32_t n[WALK_ROWS];
 #pragma unroll
-    for (int k = 0; k < WALK_ROWS; ++k) n[k] = 0;
-    for (int32_t d = 0; d < max_depth; ++d) {
-        uint32_t b[WALK_ROWS];
+        for (int k = 0; k < WALK_ROWS; ++k) n[k] = 0;
+        // which rows count, loaded up front with the first level's bins
+        uint32_t counts = count ? (1u << WALK_ROWS) - 1u : 0u;
+        if (count && kept) {
+#pragma unroll
+            for (int k = 0; k < WALK_ROWS; ++k) {
+                const int64_t i = base + (int64_t)k * WALK_THREADS;
+                if (i < rows && !kept[i]) counts &= ~(1u << k);
+            }
+        }
+        for (int32_t d = 0; d < max_depth; ++d) {
+            uint32_t b[WALK_ROWS];
+#pragma unroll
+            for (int k = 0; k < WALK_ROWS; ++k) {
+                const int64_t i = base + (int64_t)k * WALK_THREADS;
+                const int32_t f = n[k] < internal ? s_feat[n[k]] : -1;
+                b[k] = (i < rows && f >= 0) ? bins_fm[(int64_t)f * rows + i] : 0xFFFFFFFFu;
+            }
+#pragma unroll
+            for (int k = 0; k < WALK_ROWS; ++k) {
+                if (b[k] == 0xFFFFFFFFu) continue;   // past the end, or at a leaf
+                const uint32_t bf = s_bf[n[k]], bin = bf & 0xFFu, flags = bf >> 8;
+                bool left;
+                if (flags & FLAG_CATEGORICAL)
+                    left = ((tree.mask[n[k] * 8 + (b[k] >> 5)] >> (b[k] & 31u)) & 1u) != 0;
+                else if (b[k] == (uint32_t)(nb - 1)) left = (flags & FLAG_DEFAULT_LEFT) != 0;
+                else left = b[k] <= bin;
+                n[k] = 2 * n[k] + 1 + (left ? 0 : 1);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < WALK_ROWS; ++k) {
             const int64_t i = base + (int64_t)k * WALK_THREADS;
-            const int32_t f = n[k] < internal ? s_feat[n[k]] : -1;
-            b[k] = (i < rows && f >= 0) ? bins_fm[(int64_t)f * rows + i] : 0xFFFFFFFFu;
+            if (i >= rows) continue;
+            if (preds) preds[i] += s_leaf[n[k]];    // null: counts only
+            if (((counts >> k) & 1u) && n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
         }
-#pragma unroll
-        for (int k = 0; k < WALK_ROWS; ++k) {
-            if (b[k] == 0xFFFFFFFFu) continue;       // past the end, or at a leaf
-            const uint32_t bf = s_bf[n[k]], bin = bf & 0xFFu, flags = bf >> 8;
-            bool left;
-            if (flags & FLAG_CATEGORICAL)
-                left = ((tree.mask[n[k] * 8 + (b[k] >> 5)] >> (b[k] & 31u)) & 1u) != 0;
-            else if (b[k] == (uint32_t)(nb - 1)) left = (flags & FLAG_DEFAULT_LEFT) != 0;
-            else left = b[k] <= bin;
-            n[k] = 2 * n[k] + 1 + (left ? 0 : 1);
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < WALK_ROWS; ++k) {
-        const int64_t i = base + (int64_t)k * WALK_THREADS;
-        if (i >= rows) continue;
-        if (preds) preds[i] += s_leaf[n[k]];        // null: counts only
-        if (count && n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
     }
     if (!count) return;                              // null: predictions only
     __syncthreads();
@@ -124,13 +154,15 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
 
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                              int32_t num_bins, int32_t max_depth, const TreeOut tree,
-                             float *preds, uint32_t *count) {
+                             float *preds, uint32_t *count, const uint8_t *kept) {
     if (rows <= 0) return hipSuccess;
     const int64_t per = (int64_t)WALK_THREADS * WALK_ROWS;
     const size_t deep = (size_t)1 << max_depth;
     const size_t lds = (deep + 2 * (deep - 1) + (2 * deep - 1)) * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_walk_count, dim3((unsigned)((rows + per - 1) / per)), dim3(WALK_THREADS),
-                       lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count);
+    // two 1024-thread blocks per CU, or one block per chunk when fewer
+    const int64_t grid = std::min<int64_t>((rows + per - 1) / per, 2 * (int64_t)device_cus());
+    hipLaunchKernelGGL(k_walk_count, dim3((unsigned)grid), dim3(WALK_THREADS),
+                       lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count, kept);
     return hipGetLastError();
 }
 
@@ -139,7 +171,7 @@ hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows
 hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                                  int32_t num_bins, int32_t max_depth, const TreeOut tree,
                                  float *preds) {
-    return launch_walk_count(s, bins_fm, rows, num_bins, max_depth, tree, preds, nullptr);
+    return launch_walk_count(s, bins_fm, rows, num_bins, max_depth, tree, preds, nullptr, nullptr);
 }
 
 // ---------------------------------------------------------------------------

@@ -567,39 +567,72 @@ hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl) {
 }
 
 // max |g| and max h as f32 bit patterns (reduce_max_gh, Shaders.swift:87-94).
-// Stage 1: at most GRAD_MAX_BLOCKS blocks, four rows per thread per step
-// (16B loads), one partial pair per block.  Stage 2: one block reduces the
-// partials and stores the result (no same-address atomics).
+// Stage 1 (k_grad_max): grad_max_blocks(rows) blocks of 256 threads, one
+// 16-B quad of rows per thread and step, one partial pair per block; with
+// STORE every row's g and h also go to g_out / h_out (a sampled tree's later
+// passes read them).  Stage 2 (k_grad_max_final): one wavefront reduces the
+// partial pairs into the control block.  (Folding stage 2 into the next
+// kernel's blocks was measured slower: each block then waits for the
+// partials before its first load.)
+constexpr int GRAD_THREADS = 256;
 constexpr int GRAD_MAX_BLOCKS = 1024;
+constexpr int SAMPLE_MAX_BLOCKS = 4096;   // partial maxima of the row-sampling pass
 
 __device__ __forceinline__ void grad_max_row(const GradParams &gp, float p, float y, float w,
-                                             uint32_t &mg, uint32_t &mh) {
-    float g, h;
+                                             uint32_t &mg, uint32_t &mh, float &g, float &h) {
     row_grad(gp, p, y, w, g, h);
     mg = max(mg, __float_as_uint(fabsf(g)));
     mh = max(mh, __float_as_uint(h));
 }
 
-template <bool VEC>   // VEC: 16B-aligned inputs, four rows per load
-__global__ __launch_bounds__(256) void k_grad_max(GradParams gp, const float *__restrict__ preds,
-                                                  const float *__restrict__ labels,
-                                                  const float *__restrict__ weights, int64_t rows,
-                                                  uint32_t *__restrict__ partial) {
-    __shared__ uint32_t red[2][4];
+// (max over n pairs of partial[2k], max of partial[2k+1]) for every thread of
+// the block: wave 0 reduces, LDS broadcasts.
+__device__ __forceinline__ uint2 reduce_partial_max(const uint32_t *__restrict__ partial, int n,
+                                                    uint2 *s_bcast) {
+    if (threadIdx.x < 64) {
+        uint32_t a = 0, b = 0;
+        for (int k = (int)threadIdx.x; k < n; k += 64) {
+            a = max(a, partial[2 * k]);
+            b = max(b, partial[2 * k + 1]);
+        }
+        a = wave_max_u32(a);
+        b = wave_max_u32(b);
+        if (threadIdx.x == 0) *s_bcast = make_uint2(a, b);
+    }
+    __syncthreads();
+    return *s_bcast;
+}
+
+template <bool VEC, bool STORE>   // VEC: 16B-aligned inputs, four rows per load
+__global__ __launch_bounds__(GRAD_THREADS) void k_grad_max(GradParams gp,
+                                                           const float *__restrict__ preds,
+                                                           const float *__restrict__ labels,
+                                                           const float *__restrict__ weights,
+                                                           int64_t rows,
+                                                           uint32_t *__restrict__ partial,
+                                                           float *__restrict__ g_out,
+                                                           float *__restrict__ h_out) {
+    __shared__ uint32_t red[2][GRAD_THREADS / 64];
     uint32_t mg = 0, mh = 0;
     const int64_t n4 = VEC ? rows >> 2 : 0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const float4 *p4 = reinterpret_cast<const float4 *>(preds);
     const float4 *y4 = reinterpret_cast<const float4 *>(labels);
     const float4 *w4 = reinterpret_cast<const float4 *>(weights);
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        const float4 p = p4[i], y = y4[i];
-        const float4 w = gp.has_weights ? w4[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-        grad_max_row(gp, p.x, y.x, w.x, mg, mh);
-        grad_max_row(gp, p.y, y.y, w.y, mg, mh);
-        grad_max_row(gp, p.z, y.z, w.z, mg, mh);
-        grad_max_row(gp, p.w, y.w, w.w, mg, mh);
-    }
+    const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    auto quad = [&](int64_t q, const float4 &p, const float4 &y, const float4 &w) {
+        float4 g, h;
+        grad_max_row(gp, p.x, y.x, w.x, mg, mh, g.x, h.x);
+        grad_max_row(gp, p.y, y.y, w.y, mg, mh, g.y, h.y);
+        grad_max_row(gp, p.z, y.z, w.z, mg, mh, g.z, h.z);
+        grad_max_row(gp, p.w, y.w, w.w, mg, mh, g.w, h.w);
+        if (STORE) {
+            reinterpret_cast<float4 *>(g_out)[q] = g;
+            reinterpret_cast<float4 *>(h_out)[q] = h;
+        }
+    };
+    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < n4; q += stride)
+        quad(q, p4[q], y4[q], gp.has_weights ? w4[q] : one);
     // rows not covered by the 16B loads (all of them when !VEC)
     for (int64_t i = (n4 << 2) + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
          i += stride) {
@@ -607,6 +640,7 @@ __global__ __launch_bounds__(256) void k_grad_max(GradParams gp, const float *__
         row_grad_at(gp, preds, labels, weights, i, g, h);
         mg = max(mg, __float_as_uint(fabsf(g)));
         mh = max(mh, __float_as_uint(h));
+        if (STORE) { g_out[i] = g; h_out[i] = h; }
     }
     mg = wave_max_u32(mg);
     mh = wave_max_u32(mh);
@@ -615,65 +649,57 @@ __global__ __launch_bounds__(256) void k_grad_max(GradParams gp, const float *__
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t a = red[0][0], b = red[1][0];
-        for (int k = 1; k < (int)(blockDim.x >> 6); ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
+        for (int k = 1; k < GRAD_THREADS / 64; ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
         partial[2 * blockIdx.x] = a;
         partial[2 * blockIdx.x + 1] = b;
     }
 }
 
-__global__ __launch_bounds__(256) void k_grad_max_final(const uint32_t *__restrict__ partial,
-                                                        int nblocks, TreeCtl *ctl) {
-    __shared__ uint32_t red[2][4];
-    uint32_t a = 0, b = 0;
-    for (int k = threadIdx.x; k < nblocks; k += blockDim.x) {
-        a = max(a, partial[2 * k]);
-        b = max(b, partial[2 * k + 1]);
-    }
-    a = wave_max_u32(a);
-    b = wave_max_u32(b);
-    const int w = threadIdx.x >> 6;
-    if (lane_id() == 0) { red[0][w] = a; red[1][w] = b; }
-    __syncthreads();
+__global__ __launch_bounds__(64) void k_grad_max_final(const uint32_t *__restrict__ partial,
+                                                       int nblocks, TreeCtl *ctl) {
+    __shared__ uint2 bc;
+    const uint2 m = reduce_partial_max(partial, nblocks, &bc);
     if (threadIdx.x == 0) {
-        for (int k = 1; k < (int)(blockDim.x >> 6); ++k) { red[0][0] = max(red[0][0], red[0][k]); red[1][0] = max(red[1][0], red[1][k]); }
-        ctl->max_gh[0] = red[0][0];
-        ctl->max_gh[1] = red[1][0];
+        ctl->max_gh[0] = m.x;
+        ctl->max_gh[1] = m.y;
     }
+}
+
+static int grad_max_blocks(int64_t rows) {
+    const int64_t quads = (rows + 3) / 4;
+    return (int)std::max<int64_t>(
+        1, std::min<int64_t>(GRAD_MAX_BLOCKS, (quads + GRAD_THREADS - 1) / GRAD_THREADS));
 }
 
 hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           TreeCtl *ctl, uint32_t *partial) {
-    int64_t blocks = ((rows >> 2) + 255) / 256;
-    if (blocks > GRAD_MAX_BLOCKS) blocks = GRAD_MAX_BLOCKS;
-    if (blocks < 1) blocks = 1;
+                           TreeCtl *ctl, uint32_t *partial, float *g_out, float *h_out) {
+    const int blocks = grad_max_blocks(rows);
+    const bool store = g_out != nullptr && h_out != nullptr;
     const bool vec = gp.objective != 7 &&
                      ((reinterpret_cast<uintptr_t>(preds) | reinterpret_cast<uintptr_t>(labels) |
-                       reinterpret_cast<uintptr_t>(weights)) & 15u) == 0;
-    if (vec)
-        hipLaunchKernelGGL(k_grad_max<true>, dim3((unsigned)blocks), dim3(256), 0, s, gp, preds,
-                           labels, weights, rows, partial);
-    else
-        hipLaunchKernelGGL(k_grad_max<false>, dim3((unsigned)blocks), dim3(256), 0, s, gp, preds,
-                           labels, weights, rows, partial);
-    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(256), 0, s, partial, (int)blocks, ctl);
+                       reinterpret_cast<uintptr_t>(weights) | reinterpret_cast<uintptr_t>(g_out) |
+                       reinterpret_cast<uintptr_t>(h_out)) & 15u) == 0;
+    auto kernel = vec ? (store ? k_grad_max<true, true> : k_grad_max<true, false>)
+                      : (store ? k_grad_max<false, true> : k_grad_max<false, false>);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(GRAD_THREADS), 0, s, gp, preds, labels,
+                       weights, rows, partial, g_out, h_out);
+    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(64), 0, s, partial, blocks, ctl);
     return hipGetLastError();
 }
 
-size_t grad_max_scratch_words() { return 2 * (size_t)GRAD_MAX_BLOCKS; }
+size_t grad_max_scratch_words() { return 2 * (size_t)std::max(GRAD_MAX_BLOCKS, SAMPLE_MAX_BLOCKS); }
 
 // ---------------------------------------------------------------------------
 // row sampling: GOSS and bagging (goss_grad_hist, goss_threshold, goss_select,
-// Shaders.swift:1093-1199, driven as in Booster.swift:1401-1445)
+// Shaders.swift:1093-1199, driven as in Booster.swift:1401-1445).
+// The tree's gradients come from the maxima pass (launch_grad_max with
+// g_out / h_out), so the passes below stream 4-8 B per row and compute no
+// gradient: with the logistic objective's double-precision exp, recomputing
+// g per pass cost more than reading it back.
 // ---------------------------------------------------------------------------
 
 constexpr int GOSS_BUCKETS = 1024;
-constexpr int SEL_THREADS = 1024;
-constexpr int SEL_PER_THREAD = 8;    // 16 spills: the gradient code is inlined per row
-constexpr int SEL_BLOCK = SEL_THREADS * SEL_PER_THREAD;
-constexpr int SEL_WAVES = SEL_THREADS / 64;
-constexpr int SEL_SLICES_PER_LANE = SEL_PER_THREAD * SEL_WAVES / 64;
-static_assert(SEL_PER_THREAD * SEL_WAVES % 64 == 0, "slice scan: whole slices per lane");
 
 __device__ __forceinline__ uint32_t wang_hash(uint32_t x) {
     x = (x ^ 61u) ^ (x >> 16);
@@ -684,28 +710,43 @@ __device__ __forceinline__ uint32_t wang_hash(uint32_t x) {
     return x;
 }
 
-// |g| / max|g| histogram in 1024 buckets (LDS per block, one add per bucket)
-__global__ __launch_bounds__(256) void k_goss_hist(GradParams gp, const float *__restrict__ preds,
-                                                   const float *__restrict__ labels,
-                                                   const float *__restrict__ weights,
-                                                   int64_t rows, const TreeCtl *ctl,
-                                                   uint32_t *buckets) {
-    // one sub-histogram per wavefront: |g| clusters early in training, and
-    // same-bucket adds from the block's four wavefronts would serialize
-    constexpr int WAVES = 256 / 64;
+// |g| / max|g| histogram in 1024 buckets: one LDS sub-histogram per
+// wavefront (|g| clusters early in training, and same-bucket adds from
+// different wavefronts would serialize), merged with one global add per
+// non-empty bucket and block.  Adds to one global address serialize (about
+// 11 ns each on MI355X), so the grid is a few large blocks: GOSS_HIST_BLOCKS
+// of 1024 threads, grid-stride over 16-B quads of g with two in flight per
+// thread; the rows % 4 tail one per thread.
+constexpr int GOSS_HIST_THREADS = 1024;
+constexpr int GOSS_HIST_BLOCKS = 256;
+
+__global__ __launch_bounds__(GOSS_HIST_THREADS) void k_goss_hist(const float *__restrict__ g,
+                                                                 int64_t rows, const TreeCtl *ctl,
+                                                                 uint32_t *buckets) {
+    constexpr int WAVES = GOSS_HIST_THREADS / 64;
     __shared__ uint32_t lb[WAVES][GOSS_BUCKETS];
     for (int k = threadIdx.x; k < WAVES * GOSS_BUCKETS; k += blockDim.x) (&lb[0][0])[k] = 0;
     __syncthreads();
-    uint32_t *mine = lb[threadIdx.x >> 6];
     const float mg = f32_from_bits(ctl->max_gh[0]);
+    uint32_t *mine = lb[threadIdx.x >> 6];
+    auto add = [&](float v) {
+        const uint32_t b = (uint32_t)(fabsf(v) / mg * (float)GOSS_BUCKETS);
+        atomicAdd(&mine[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
+    };
     if (mg > 0.0f) {
-        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows;
-             i += (int64_t)gridDim.x * blockDim.x) {
-            float g, h;
-            row_grad_at(gp, preds, labels, weights, i, g, h);
-            const uint32_t b = (uint32_t)(fabsf(g) / mg * (float)GOSS_BUCKETS);
-            atomicAdd(&mine[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        const float4 *g4 = reinterpret_cast<const float4 *>(g);
+        const int64_t nq = rows >> 2;
+        for (int64_t q = t0; q < nq; q += 2 * stride) {
+            const bool second = q + stride < nq;
+            const float4 a = g4[q];
+            float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (second) b = g4[q + stride];
+            add(a.x); add(a.y); add(a.z); add(a.w);
+            if (second) { add(b.x); add(b.y); add(b.z); add(b.w); }
         }
+        for (int64_t i = (nq << 2) + t0; i < rows; i += stride) add(g[i]);
     }
     __syncthreads();
     for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) {
@@ -717,10 +758,10 @@ __global__ __launch_bounds__(256) void k_goss_hist(GradParams gp, const float *_
 }
 
 // Threshold = lower edge of the bucket where the count from the top first
-// reaches top_count (b = 1024, i.e. max|g|, when top_count = 0).  One
-// wavefront; leaves the buckets zeroed for the next tree.
-__global__ __launch_bounds__(64) void k_goss_threshold(uint32_t top_count, TreeCtl *ctl,
-                                                       uint32_t *buckets) {
+// reaches top_count (b = 1024, i.e. max|g|, when top_count = 0); the value
+// is f32 bits.  Run by one whole wavefront.
+__device__ uint32_t goss_threshold(uint32_t top_count, float mg,
+                                   const uint32_t *__restrict__ buckets) {
     const int lane = lane_id();
     constexpr int PER = GOSS_BUCKETS / 64;
     uint32_t v[PER], s = 0;
@@ -733,7 +774,6 @@ __global__ __launch_bounds__(64) void k_goss_threshold(uint32_t top_count, TreeC
         const uint32_t t = __shfl_down(suf, o, 64);
         if (lane + o < 64) suf += t;
     }
-    const float mg = f32_from_bits(ctl->max_gh[0]);
     uint32_t b = GOSS_BUCKETS;
     if (top_count > 0 && mg > 0.0f) {
         // the crossing lane: the highest lane whose suffix reaches top_count
@@ -754,98 +794,10 @@ __global__ __launch_bounds__(64) void k_goss_threshold(uint32_t top_count, TreeC
             b = bb;
         }
     }
-    if (lane == 0) {
-        const float thr = mg > 0.0f ? (float)b / (float)GOSS_BUCKETS * mg : 0.0f;
-        ctl->sample_thr = __float_as_uint(thr);
-    }
-#pragma unroll
-    for (int j = 0; j < PER; ++j) buckets[lane * PER + j] = 0;
+    const float thr = mg > 0.0f ? (float)b / (float)GOSS_BUCKETS * mg : 0.0f;
+    return __float_as_uint(thr);
 }
 
-// Keep rows with |g| >= threshold (weight 1) and a hashed uniform sample of
-// the rest (weight sp.weight); compact kept rows into order[] (one cursor add
-// per 8K-row chunk) and leave per-block maxima of |g|*w and h*w.
-__global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
-    GradParams gp, SampleParams sp, const float *__restrict__ preds,
-    const float *__restrict__ labels, const float *__restrict__ weights, int64_t rows,
-    TreeCtl *ctl, uint32_t *__restrict__ partial, Entry *__restrict__ order) {
-    __shared__ uint32_t tot[SEL_PER_THREAD * SEL_WAVES + 1];
-    __shared__ uint32_t s_base;
-    __shared__ uint32_t red[2][SEL_WAVES];
-    const int tid = threadIdx.x, w = tid >> 6;
-    const float thr = f32_from_bits(ctl->sample_thr);
-    uint32_t mg = 0, mh = 0;
-    for (int64_t c0 = (int64_t)blockIdx.x * SEL_BLOCK; c0 < rows;
-         c0 += (int64_t)gridDim.x * SEL_BLOCK) {
-        uint32_t x[SEL_PER_THREAD], amp[SEL_PER_THREAD], ex[SEL_PER_THREAD];
-#pragma unroll
-        for (int k = 0; k < SEL_PER_THREAD; ++k) {
-            const int64_t i = c0 + k * SEL_THREADS + tid;
-            x[k] = 0;
-            amp[k] = 0;
-            if (i < rows) {
-                float g, h;
-                row_grad_at(gp, preds, labels, weights, i, g, h);
-                const float ag = fabsf(g);
-                float wt = 1.0f;
-                bool keep = ag >= thr;
-                if (!keep) {
-                    const uint32_t hv = wang_hash((uint32_t)i ^ (sp.seed * 0x9E3779B9u));
-                    if ((float)(hv >> 8) * (1.0f / 16777216.0f) < sp.other_prob) {
-                        keep = true;
-                        wt = sp.weight;
-                    }
-                }
-                if (keep) {
-                    x[k] = 1;
-                    amp[k] = wt != 1.0f ? 1u : 0u;
-                    mg = max(mg, __float_as_uint(ag * wt));
-                    mh = max(mh, __float_as_uint(h * wt));
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < SEL_PER_THREAD; ++k) {
-            const uint32_t inc = wave_inclusive_scan(x[k]);
-            ex[k] = inc - x[k];
-            if (lane_id() == 63) tot[k * SEL_WAVES + w] = inc;
-        }
-        __syncthreads();
-        if (tid < 64) {
-            constexpr int SPL = SEL_SLICES_PER_LANE;
-            uint32_t v[SPL], s = 0;
-#pragma unroll
-            for (int j = 0; j < SPL; ++j) { v[j] = tot[tid * SPL + j]; s += v[j]; }
-            const uint32_t inc = wave_inclusive_scan(s);
-            uint32_t acc = inc - s;
-#pragma unroll
-            for (int j = 0; j < SPL; ++j) { tot[tid * SPL + j] = acc; acc += v[j]; }
-            if (tid == 63) s_base = atomicAdd(&ctl->sampled, inc);
-        }
-        __syncthreads();
-        const uint32_t base = s_base;
-#pragma unroll
-        for (int k = 0; k < SEL_PER_THREAD; ++k) {
-            if (!x[k]) continue;
-            const int64_t i = c0 + k * SEL_THREADS + tid;
-            order[base + tot[k * SEL_WAVES + w] + ex[k]] = Entry{(uint32_t)i, amp[k]};
-        }
-        __syncthreads();
-    }
-    mg = wave_max_u32(mg);
-    mh = wave_max_u32(mh);
-    if (lane_id() == 0) { red[0][w] = mg; red[1][w] = mh; }
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t a = red[0][0], b = red[1][0];
-        for (int k = 1; k < SEL_WAVES; ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
-        partial[2 * blockIdx.x] = a;
-        partial[2 * blockIdx.x + 1] = b;
-    }
-}
-
-// Quantise the kept entries with the weighted maxima (quantize_gradients,
-// Shaders.swift:176-192, over amplified gradients).
 // Entries move as one 64-bit word (row low, ghq high).  Order buffers are
 // written once per pass and read by the next kernels from HBM (80 MB at 10M
 // rows, far past L2), so their stores and the partition's loads are
@@ -862,49 +814,199 @@ __device__ __forceinline__ Entry load_entry_nt(const Entry *p) {
     return Entry{(uint32_t)v, (uint32_t)(v >> 32)};
 }
 
-__global__ __launch_bounds__(256) void k_quantize_sampled(GradParams gp, SampleParams sp,
-                                                          const float *__restrict__ preds,
-                                                          const float *__restrict__ labels,
-                                                          const float *__restrict__ weights,
-                                                          const TreeCtl *ctl,
-                                                          Entry *__restrict__ order) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= ctl->sampled) return;
-    Entry e = order[i];
+// Keep rows with |g| >= threshold (weight 1) and a hashed uniform sample of
+// the rest (weight sp.weight).  512 threads take a 16384-row chunk, thread t
+// the quads k * 512 + t (k < 8) of g and h, so each load instruction reads
+// 4 KiB of contiguous rows.  A thread keeps its 32 keep / amplified decisions
+// as bit masks; the block scans the per-thread counts, takes one cursor add
+// per chunk (adds to one address serialize, so chunks are large), stages the
+// kept rows' chunk offsets (14 bits, amplified flag in bit 15) in LDS and
+// then writes, contiguously, the entries {row, f32 bits of g * w} and
+// h_kept = h * w.  Per-block maxima of |g| * w and h * w go to
+// partial; with kept non-null, kept[i] = 1 for a kept row and 0 otherwise.
+// The entry order inside a chunk follows the staging, not the row order;
+// every consumer sums integers or partitions stably, so the tree does not
+// depend on it.
+constexpr int SEL_THREADS = 512;
+constexpr int SEL_QUADS = 8;
+constexpr int SEL_CHUNK = SEL_THREADS * SEL_QUADS * 4;
+static_assert(SEL_CHUNK <= (1 << 15), "chunk offsets fit 15 bits");
+
+__global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
+    SampleParams sp, const float *__restrict__ g, const float *__restrict__ h, int64_t rows,
+    const uint32_t *__restrict__ buckets, TreeCtl *ctl, uint32_t *__restrict__ partial,
+    Entry *__restrict__ order, float *__restrict__ h_kept, uint8_t *__restrict__ kept) {
+    __shared__ uint16_t s_off[SEL_CHUNK];
+    __shared__ uint32_t s_wave[SEL_THREADS / 64];
+    __shared__ uint32_t s_base, s_total, s_thr;
+    __shared__ uint32_t red[2][SEL_THREADS / 64];
+    const int tid = threadIdx.x, w = tid >> 6;
+    // the keep threshold, from the unweighted max |g| and the |g| histogram
+    // (every block derives it: no separate one-wavefront kernel)
+    if (tid < 64) {
+        const uint32_t t = goss_threshold(sp.goss ? sp.top_count : 0u,
+                                          f32_from_bits(ctl->max_gh[0]), buckets);
+        if (tid == 0) {
+            s_thr = t;
+            if (blockIdx.x == 0) ctl->sample_thr = t;
+        }
+    }
+    __syncthreads();
+    const float thr = f32_from_bits(s_thr);
+    const uint32_t seed_mix = sp.seed * 0x9E3779B9u;
+    const float4 *g4 = reinterpret_cast<const float4 *>(g);
+    const float4 *h4 = reinterpret_cast<const float4 *>(h);
+    uint32_t mg = 0, mh = 0;
+    for (int64_t c0 = (int64_t)blockIdx.x * SEL_CHUNK; c0 < rows;
+         c0 += (int64_t)gridDim.x * SEL_CHUNK) {
+        uint32_t keep = 0, amp = 0;
+#pragma unroll
+        for (int k = 0; k < SEL_QUADS; ++k) {
+            const int64_t r0 = c0 + (int64_t)(k * SEL_THREADS + tid) * 4;
+            float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, hv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (r0 + 3 < rows) {
+                const float4 a = g4[r0 >> 2], b = h4[r0 >> 2];
+                gv[0] = a.x; gv[1] = a.y; gv[2] = a.z; gv[3] = a.w;
+                hv[0] = b.x; hv[1] = b.y; hv[2] = b.z; hv[3] = b.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (r0 + j < rows) { gv[j] = g[r0 + j]; hv[j] = h[r0 + j]; }
+            }
+            uint32_t nib = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t i = r0 + j;
+                if (i >= rows) continue;
+                const float ag = fabsf(gv[j]);
+                float wt = 1.0f;
+                bool kp = ag >= thr;
+                if (!kp) {
+                    const uint32_t hs = wang_hash((uint32_t)i ^ seed_mix);
+                    if ((float)(hs >> 8) * (1.0f / 16777216.0f) < sp.other_prob) {
+                        kp = true;
+                        wt = sp.weight;
+                    }
+                }
+                if (kp) {
+                    nib |= 1u << j;
+                    if (wt != 1.0f) amp |= 1u << (4 * k + j);
+                    mg = max(mg, __float_as_uint(ag * wt));
+                    mh = max(mh, __float_as_uint(hv[j] * wt));
+                }
+            }
+            keep |= nib << (4 * k);
+            if (kept) {
+                if (r0 + 3 < rows) {
+                    *reinterpret_cast<uint32_t *>(kept + r0) =
+                        (nib & 1u) | ((nib >> 1) & 1u) << 8 | ((nib >> 2) & 1u) << 16 |
+                        ((nib >> 3) & 1u) << 24;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (r0 + j < rows) kept[r0 + j] = (uint8_t)((nib >> j) & 1u);
+                }
+            }
+        }
+        // block-exclusive position of this thread's first kept row
+        const uint32_t cnt = (uint32_t)__popc(keep);
+        const uint32_t inc = wave_inclusive_scan(cnt);
+        if (lane_id() == 63) s_wave[w] = inc;
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int v = 0; v < SEL_THREADS / 64; ++v) {
+                const uint32_t t = s_wave[v];
+                s_wave[v] = acc;
+                acc += t;
+            }
+            s_total = acc;
+            s_base = atomicAdd(&ctl->sampled, acc);
+        }
+        __syncthreads();
+        uint32_t pos = s_wave[w] + inc - cnt;
+        for (uint32_t m = keep; m; m &= m - 1) {
+            const uint32_t b = (uint32_t)__builtin_ctz(m);
+            const uint32_t off = ((b >> 2) * SEL_THREADS + (uint32_t)tid) * 4u + (b & 3u);
+            s_off[pos++] = (uint16_t)(off | (((amp >> b) & 1u) << 15));
+        }
+        __syncthreads();
+        const uint32_t total = s_total, base = s_base;
+        for (uint32_t q = (uint32_t)tid; q < total; q += SEL_THREADS) {
+            const uint32_t v = s_off[q];
+            const int64_t i = c0 + (v & 0x7FFFu);
+            float gw = g[i], hw = h[i];              // this chunk's lines: still in L2
+            if (v >> 15) { gw = gw * sp.weight; hw = hw * sp.weight; }
+            store_entry_nt(order + base + q, Entry{(uint32_t)i, __float_as_uint(gw)});
+            __builtin_nontemporal_store(hw, h_kept + base + q);
+        }
+        __syncthreads();                             // s_off / s_wave reuse by the next chunk
+    }
+    mg = wave_max_u32(mg);
+    mh = wave_max_u32(mh);
+    if (lane_id() == 0) { red[0][w] = mg; red[1][w] = mh; }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t a = red[0][0], b = red[1][0];
+        for (int k = 1; k < SEL_THREADS / 64; ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
+        partial[2 * blockIdx.x] = a;
+        partial[2 * blockIdx.x + 1] = b;
+    }
+}
+
+// Quantise the kept entries with the weighted maxima (quantize_gradients,
+// Shaders.swift:176-192, over amplified gradients): ghq holds g * w on entry.
+// The weighted maxima are in the control block; block 0 also zeroes the |g|
+// histogram for the next tree.
+__global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
+                                                          uint32_t *__restrict__ buckets,
+                                                          Entry *__restrict__ order,
+                                                          const float *__restrict__ h_kept) {
+    if (blockIdx.x == 0)
+        for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) buckets[k] = 0;
+    const uint32_t n = ctl->sampled;
     const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
     const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
     const float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
-    float g, h;
-    row_grad_at(gp, preds, labels, weights, (int64_t)e.row, g, h);
-    if (e.ghq) { g = g * sp.weight; h = h * sp.weight; }
-    const int qg = (int)rintf(g * gscale);
-    const uint32_t qh = (uint32_t)rintf(h * hscale);
-    e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
-    store_entry_nt(order + i, e);
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        Entry e = load_entry_nt(order + i);
+        const float gw = __uint_as_float(e.ghq), hw = __builtin_nontemporal_load(h_kept + i);
+        const int qg = (int)rintf(gw * gscale);
+        const uint32_t qh = (uint32_t)rintf(hw * hscale);
+        e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
+        store_entry_nt(order + i, e);
+    }
 }
 
-hipError_t launch_sample(hipStream_t s, const GradParams &gp, const SampleParams &sp,
-                         const float *preds, const float *labels, const float *weights,
-                         int64_t rows, TreeCtl *ctl, uint32_t *buckets, uint32_t *partial,
-                         Entry *order) {
-    // 8 blocks per CU of grid-stride rows: enough loads in flight to stream
-    const unsigned hist_blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
+hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
+                         uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
+                         Entry *order, float *h_kept, uint8_t *kept) {
+    if (((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(h)) & 15u) != 0)
+        return hipErrorInvalidValue;                 // the passes read 16-B quads
+    const int64_t quads = (rows + 3) / 4;
+    const unsigned hist_blocks = (unsigned)std::max<int64_t>(
+        1, std::min<int64_t>(GOSS_HIST_BLOCKS,
+                             (quads + 2 * GOSS_HIST_THREADS - 1) / (2 * GOSS_HIST_THREADS)));
     if (sp.goss && sp.top_count > 0)
-        hipLaunchKernelGGL(k_goss_hist, dim3(hist_blocks), dim3(256), 0, s, gp, preds, labels, weights,
-                           rows, ctl, buckets);
-    hipLaunchKernelGGL(k_goss_threshold, dim3(1), dim3(64), 0, s, sp.goss ? sp.top_count : 0u,
-                       ctl, buckets);
-    int64_t blocks = (rows + SEL_BLOCK - 1) / SEL_BLOCK;
-    if (blocks > GRAD_MAX_BLOCKS) blocks = GRAD_MAX_BLOCKS;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(k_goss_select, dim3((unsigned)blocks), dim3(SEL_THREADS), 0, s, gp, sp,
-                       preds, labels, weights, rows, ctl, partial, order);
-    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(256), 0, s, partial, (int)blocks, ctl);
-    hipLaunchKernelGGL(k_quantize_sampled, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
-                       gp, sp, preds, labels, weights, ctl, order);
+        hipLaunchKernelGGL(k_goss_hist, dim3(hist_blocks), dim3(GOSS_HIST_THREADS), 0, s, g, rows,
+                           ctl, buckets);
+    const int64_t blocks = std::max<int64_t>(
+        1, std::min<int64_t>((rows + SEL_CHUNK - 1) / SEL_CHUNK, SAMPLE_MAX_BLOCKS));
+    hipLaunchKernelGGL(k_goss_select, dim3((unsigned)blocks), dim3(SEL_THREADS), 0, s, sp, g, h,
+                       rows, buckets, ctl, partial, order, h_kept, kept);
+    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(64), 0, s, partial, (int)blocks, ctl);
+    // the kept count is known only on the device: a fixed grid strides over it
+    // (a rows-sized grid of mostly idle blocks measured 7 us slower)
+    const unsigned qblocks =
+        (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
+    hipLaunchKernelGGL(k_quantize_sampled, dim3(qblocks), dim3(256), 0, s, ctl, buckets, order,
+                       h_kept);
     return hipGetLastError();
 }
 
+// Every row quantised (quantize_gradients, Shaders.swift:176-192) into the
+// order entries {row, (qg & 0xFFFF) << 16 | qh}, one row per thread.
 __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__restrict__ preds,
                                                   const float *__restrict__ labels,
                                                   const float *__restrict__ weights, int64_t rows,

@@ -177,18 +177,24 @@ struct GradParams {
     int32_t class_index;     // multiclass: the class this tree fits
     int64_t rows;            // multiclass: the class stride of preds
 };
-// partial: grad_max_scratch_words() u32 of device scratch
+// ctl->max_gh = (max |g|, max h); partial: grad_max_scratch_words() u32 of
+// device scratch.  With g_out and h_out (rows floats each, 16-B aligned)
+// every row's g and h are stored too.
 hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           TreeCtl *ctl, uint32_t *partial);
+                           TreeCtl *ctl, uint32_t *partial, float *g_out = nullptr,
+                           float *h_out = nullptr);
 size_t grad_max_scratch_words();
 
-// Row sampling (GOSS / bagging) for one tree: buckets (1024 u32, zero on entry
-// and left zero) hold the |g| histogram.  top_count = 0 is bagging.  Kept
-// rows are compacted into order[0, ctl->sampled) with ghq = 1 marking
-// amplified rows, ctl->max_gh becomes the weighted maxima over kept rows
-// (partial: grad_max_scratch_words() u32), and the entries are then
-// quantised in place.
+// Row sampling (GOSS / bagging) for one tree over the gradients g, h and
+// maxima that launch_grad_max stored (g, h 16-B aligned): buckets (1024 u32,
+// zero on entry and left zero) hold the |g| histogram; top_count = 0 is
+// bagging.  Kept rows
+// are compacted into order[0, ctl->sampled), h_kept (rows floats of scratch)
+// holds their weighted hessians, ctl->max_gh becomes the weighted maxima over
+// kept rows (partial: grad_max_scratch_words() u32), and the entries are
+// then quantised in place.  With kept non-null, kept[i] (rows bytes) becomes
+// 1 for a kept row and 0 otherwise.
 struct SampleParams {
     int32_t goss;            // 1: GOSS histogram threshold; 0: bagging
     uint32_t top_count;      // floor(rows * top_rate) (0 for bagging)
@@ -197,10 +203,10 @@ struct SampleParams {
     uint32_t seed;           // tree index + 1
     uint32_t pad[3];
 };
-hipError_t launch_sample(hipStream_t s, const GradParams &gp, const SampleParams &sp,
-                         const float *preds, const float *labels, const float *weights,
-                         int64_t rows, TreeCtl *ctl, uint32_t *buckets, uint32_t *partial,
-                         Entry *order);
+hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
+                         uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
+                         Entry *order, float *h_kept, uint8_t *kept);
+// Every row quantised with ctl->max_gh into order[i] = {i, packed (qg, qh)}.
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order);
@@ -419,10 +425,10 @@ hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t 
                                  float *preds);
 // Training-row walk of a finished tree: preds += leaf (unless preds is null),
 // and rows per node of the deepest level added to count[2^D - 1 ...] (unless
-// count is null).
+// count is null; with kept non-null only rows with kept[i] != 0 count).
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                              int32_t num_bins, int32_t max_depth, const TreeOut tree,
-                             float *preds, uint32_t *count);
+                             float *preds, uint32_t *count, const uint8_t *kept);
 
 struct ShapPath {
     int32_t elem_start;   // first element

@@ -241,6 +241,12 @@ struct Trainer {
     DevBuf<int8_t> mono;
     DevBuf<mbk::Entry> order_a, order_b;
     DevBuf<uint32_t> gmax_part, goss_buckets;
+    // a sampled tree's gradients (g, h of every row) and its kept rows'
+    // weighted hessians
+    DevBuf<float> samp_g, samp_h, samp_h_kept;
+    // kept[i] of a sampled level-wise tree, for the terminal walk's counts
+    DevBuf<uint8_t> kept;
+    bool kept_walk = false;
     DevBuf<uint64_t> route_cursor;
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
@@ -799,6 +805,9 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     }
     t.gmax_part.alloc(mbk::grad_max_scratch_words());
     if (p.goss || p.subsample < 1.0f) {
+        t.samp_g.alloc((size_t)rows);
+        t.samp_h.alloc((size_t)rows);
+        t.samp_h_kept.alloc((size_t)rows);
         t.goss_buckets.alloc(1024);
         MB_HIP(hipMemsetAsync(t.goss_buckets.ptr, 0, 1024 * sizeof(uint32_t), s));
     }
@@ -847,6 +856,13 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         t.lw_open.alloc((size_t)2 * p.num_leaves + 2);
     }
     t.renewal = p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE;
+    // A sampled level-wise tree counts its deepest nodes' kept rows in the
+    // terminal walk.  With min_child_hess > 0 every split child holds a kept
+    // row (both sides of a chosen split have hessian >= min_child_hess), so
+    // no leaf the walk applies is later emptied and zeroed.
+    t.kept_walk = !t.leafwise && (p.goss || p.subsample < 1.0f) && p.min_child_hess > 0.0f &&
+                  !t.renewal;
+    if (t.kept_walk) t.kept.alloc((size_t)rows);
     if (t.renewal) {
         t.renewal_q = p.objective == OBJ_MAE ? 0.5f : p.alpha;
         const size_t ns = mbk::renew_sample_count(rows);
@@ -1193,16 +1209,18 @@ static mbk::SampleParams sample_params(const Trainer &t, int tree) {
 
 // Gradients, maxima and the tree's order entries: every row quantised, or
 // the rows a GOSS / bagging tree keeps (their count stays on the device).
-static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *order) {
+static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *order,
+                         uint8_t *kept = nullptr) {
     hipStream_t s = t.dev->stream;
+    const bool sampled = tree_sampled(t.p, tree);
     MB_HIP(mbk::launch_tree_init(s, ctl));
     MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
-                                t.gmax_part.ptr));
-    const bool sampled = tree_sampled(t.p, tree);
+                                t.gmax_part.ptr, sampled ? t.samp_g.ptr : nullptr,
+                                sampled ? t.samp_h.ptr : nullptr));
     if (sampled)
-        MB_HIP(mbk::launch_sample(s, t.gp, sample_params(t, tree), t.preds.ptr, t.labels.ptr,
-                                  t.weights.ptr, t.rows, ctl, t.goss_buckets.ptr,
-                                  t.gmax_part.ptr, order));
+        MB_HIP(mbk::launch_sample(s, sample_params(t, tree), t.rows, ctl, t.goss_buckets.ptr,
+                                  t.gmax_part.ptr, t.samp_g.ptr, t.samp_h.ptr, order,
+                                  t.samp_h_kept.ptr, kept));
     else
         MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
                                     ctl, order));
@@ -1216,7 +1234,8 @@ static void grow_levelwise(Trainer &t, int tree) {
     if (const uint8_t *m = tree_feature_mask(t, tree))
         MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
     mbk::TreeCtl *ctl = t.ctl.ptr;
-    const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr);
+    const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr,
+                                      t.kept_walk ? t.kept.ptr : nullptr);
     MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
                                  (uint32_t)t.target_items,
                                  (uint32_t)t.min_chunk, ctl, t.seg_a.ptr, t.count.ptr, t.pairs.ptr,
@@ -1255,15 +1274,16 @@ static void grow_levelwise(Trainer &t, int tree) {
         const bool terminal = d == t.D;
         mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
         mbk::LevelArgs ln{d, (uint32_t)((1u << d) - 1), 1u << d, terminal ? 1u : 0u};
-        if (terminal && !sampled) {
+        if (terminal && (!sampled || t.kept_walk)) {
             // deepest level: leaf values, then one walk of the finished tree over
             // the training rows adds every row's leaf (the single addition the
             // partition-time update makes, route_samples apply,
-            // Shaders.swift:1280-1311) and counts the deepest nodes' rows
+            // Shaders.swift:1280-1311) and counts the deepest nodes' (kept) rows
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, false));
             MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
-                                          t.renewal ? nullptr : t.preds_cur, t.count.ptr));
+                                          t.renewal ? nullptr : t.preds_cur, t.count.ptr,
+                                          sampled ? t.kept.ptr : nullptr));
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
             if (t.renewal) {
                 // residuals before the tree (routing applies nothing), then
