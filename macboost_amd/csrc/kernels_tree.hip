@@ -2224,18 +2224,34 @@ __device__ __forceinline__ bool route_block(const NodeSplit sp, const uint32_t *
     return true;
 }
 
+// Lanes below this one in the wavefront.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 // A persistent grid: each block computes the level's block prefix once and
 // then takes logical blocks b, b + gridDim.x, ... (the logical blocks a level
 // needs depend on its live rows, known only on the device; a sampled tree
-// needs far fewer than the launch could hold).
-__global__ __launch_bounds__(PART_THREADS) void k_route(
+// needs far fewer than the launch could hold).  The loop is software
+// pipelined: while a block waits for its node cursor add (adds to one
+// address serialize) and writes its entries, the next logical block's split
+// record, mask and entries are already loading, so the bursts of loads and
+// stores of consecutive logical blocks overlap.  Entry slot k of thread t is
+// entry k * PART_THREADS + t of the logical block; a row's left flag lives
+// as bit k of a per-thread mask, and its rank among the left rows of its
+// wavefront slice comes from a ballot at store time.
+__global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
     const uint32_t *__restrict__ count, const TreeOut out, uint64_t *cursors,
     int write_entries) {
     extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
-    __shared__ uint32_t s_mask[8];
+    __shared__ uint32_t s_mask[2][8];
     __shared__ uint32_t wave_tot[PART_WAVES + 1];
+    __shared__ uint32_t tot[PART_SLICES + 1];
+    __shared__ uint64_t s_base;
+    const int tid = threadIdx.x, w = tid >> 6, lane = lane_id();
     // blocks per split node of the routed level, and their prefix
     for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
         const uint32_t nn = la.level_start + l;
@@ -2244,23 +2260,120 @@ __global__ __launch_bounds__(PART_THREADS) void k_route(
     }
     __syncthreads();
     const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
-    for (uint32_t b = blockIdx.x; b < total_blocks; b += gridDim.x) {   // uniform per block
-        // owning node: the largest l with blk_prefix[l] <= b (it has blocks)
+    uint32_t b = blockIdx.x;
+    if (b >= total_blocks) return;                   // uniform per block
+
+    // logical block b: its node slot, segment, count, first entry and split
+    struct Blk {
+        uint32_t l, start, cnt, first, nvalid;
+        NodeSplit sp;
+    };
+    auto locate = [&](uint32_t bb, Blk &k) {
+        // owning node: the largest l with blk_prefix[l] <= bb (it has blocks)
         uint32_t lo = 0, hi = la.num_level - 1;
         while (lo < hi) {
             const uint32_t mid = (lo + hi + 1) >> 1;
-            if (blk_prefix[mid] <= b) lo = mid; else hi = mid - 1;
+            if (blk_prefix[mid] <= bb) lo = mid; else hi = mid - 1;
         }
-        const uint32_t l = lo, n = la.level_start + l;
-        const uint32_t start = seg_start[l], cnt = count[n];
-        const uint32_t first = (b - blk_prefix[l]) * PART_BLOCK;
-        const NodeSplit sp = out.split[n];
-        if (threadIdx.x < 8) s_mask[threadIdx.x] = out.mask[(size_t)n * 8 + threadIdx.x];
+        const uint32_t n = la.level_start + lo;
+        k.l = lo;
+        k.start = seg_start[lo];
+        k.cnt = count[n];
+        k.first = (bb - blk_prefix[lo]) * PART_BLOCK;
+        k.nvalid = min((uint32_t)PART_BLOCK, k.cnt - k.first);
+        k.sp = out.split[n];
+    };
+    auto load_entries = [&](const Blk &k, Entry (&e)[PART_PER_THREAD]) {
+        const Entry *src = order_in + k.start + k.first;
+#pragma unroll
+        for (int j = 0; j < PART_PER_THREAD; ++j) {
+            const uint32_t i = (uint32_t)(j * PART_THREADS + tid);
+            e[j] = Entry{0u, 0u};
+            if (i < k.nvalid) e[j] = load_entry_nt(src + i);
+        }
+    };
+
+    Blk cur;
+    Entry e[PART_PER_THREAD];
+    locate(b, cur);
+    if (tid < 8) s_mask[0][tid] = out.mask[(size_t)(la.level_start + cur.l) * 8 + tid];
+    load_entries(cur, e);
+    int buf = 0;
+    __syncthreads();
+    for (;;) {
+        const uint32_t bn = b + gridDim.x;
+        const bool has_next = bn < total_blocks;     // uniform per block
+        // left flags of this block's entries
+        const uint8_t *col = bins_fm + (size_t)cur.sp.feature * (size_t)sh.rows;
+        uint32_t bins[PART_PER_THREAD];
+#pragma unroll
+        for (int j = 0; j < PART_PER_THREAD; ++j) {
+            const uint32_t i = (uint32_t)(j * PART_THREADS + tid);
+            bins[j] = i < cur.nvalid ? col[e[j].row] : 0u;
+        }
+        uint32_t left = 0;
+#pragma unroll
+        for (int j = 0; j < PART_PER_THREAD; ++j) {
+            const uint32_t i = (uint32_t)(j * PART_THREADS + tid);
+            if (i < cur.nvalid && bin_goes_left(bins[j], cur.sp, sh.num_bins, s_mask[buf]))
+                left |= 1u << j;
+        }
+        // left rows per wavefront slice (slice = (entry slot j, wavefront))
+#pragma unroll
+        for (int j = 0; j < PART_PER_THREAD; ++j) {
+            const uint64_t bal = __ballot((left >> j) & 1u);
+            if (lane == 0) tot[j * PART_WAVES + w] = (uint32_t)__popcll(bal);
+        }
         __syncthreads();
-        route_block(sp, s_mask, sh.num_bins, bins_fm + (size_t)sp.feature * (size_t)sh.rows,
-                    order_in + start + first, min((uint32_t)PART_BLOCK, cnt - first), cnt,
-                    order_out + start, &cursors[(size_t)l * CURSOR_STRIDE], write_entries != 0);
-        __syncthreads();                             // LDS reuse by the next logical block
+        uint64_t old = 0;
+        if (tid < 64) {
+            // scan the PART_SLICES slice totals with one wave
+            constexpr int SPL = PART_SLICES_PER_LANE;
+            uint32_t v[SPL], sum = 0;
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) { v[j] = tot[tid * SPL + j]; sum += v[j]; }
+            const uint32_t inc = wave_inclusive_scan(sum);
+            uint32_t acc = inc - sum;
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) { tot[tid * SPL + j] = acc; acc += v[j]; }
+            if (tid == 63)
+                old = atomicAdd(reinterpret_cast<unsigned long long *>(
+                                    &cursors[(size_t)cur.l * CURSOR_STRIDE]),
+                                (unsigned long long)inc |
+                                    ((unsigned long long)(cur.nvalid - inc) << 32));
+        }
+        // the next logical block loads while the cursor add is in flight
+        Blk nxt = cur;
+        Entry en[PART_PER_THREAD];
+        if (has_next) {
+            locate(bn, nxt);
+            if (tid < 8)
+                s_mask[buf ^ 1][tid] = out.mask[(size_t)(la.level_start + nxt.l) * 8 + tid];
+            load_entries(nxt, en);
+        }
+        if (tid == 63) s_base = old;
+        __syncthreads();
+        if (write_entries) {
+            const uint32_t base_l = (uint32_t)s_base, base_r = (uint32_t)(s_base >> 32);
+            Entry *dst = order_out + cur.start;
+#pragma unroll
+            for (int j = 0; j < PART_PER_THREAD; ++j) {
+                const uint32_t i = (uint32_t)(j * PART_THREADS + tid);
+                const bool is_left = (left >> j) & 1u;
+                const uint32_t le =
+                    tot[j * PART_WAVES + w] + lanes_below(__ballot(is_left));
+                if (i >= cur.nvalid) continue;
+                const uint32_t pos = is_left ? base_l + le : cur.cnt - 1u - (base_r + (i - le));
+                store_entry_nt(dst + pos, e[j]);
+            }
+        }
+        __syncthreads();                             // tot / s_base reuse, the next mask
+        if (!has_next) break;
+        cur = nxt;
+#pragma unroll
+        for (int j = 0; j < PART_PER_THREAD; ++j) e[j] = en[j];
+        buf ^= 1;
+        b = bn;
     }
 }
 
