@@ -1119,7 +1119,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                                                        const HistItem *__restrict__ items,
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
-                                                       HistLayout lay, int32_t nb) {
+                                                       HistLayout lay, int32_t nb, int32_t cols) {
     constexpr int P = W >= 32 ? 32 : W;              // features per lane
     constexpr int RPB = W == 64 ? 32 : 64;           // rows per wavefront batch
     constexpr int DR = HIST_DATA_RING, ER = HIST_ENTRY_RING;
@@ -1213,10 +1213,13 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                 dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * row_bytes, cx);
         }
         __syncthreads();
-        // flush to the item's partial, layout [nb][W]
+        // flush to the item's partial, layout [nb][W]; the last tile's padding
+        // columns are neither written nor read
         uint64_t *out = partials + (size_t)it * (size_t)(nb * W);
+        const int wreal = min(W, cols - (int)item.tile * W);
         for (int k = tid; k < nb * W; k += HIST_THREADS) {
             const int b = k / W, f = k % W;
+            if (f >= wreal) continue;
             uint64_t acc;
             if constexpr (W == 64) {
                 acc = hist_lds[(f >> 5) * 8192 + b * 32 + (f & 31)];
@@ -1265,7 +1268,7 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
         hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,       \
-                           items, ctl, partials, lay, sh.num_bins);                              \
+                           items, ctl, partials, lay, sh.num_bins, sh.cols);                     \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)
@@ -1336,7 +1339,7 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
     const int k = (int)bpt * CELLS + kk;             // (bin, feature) index in the tile
     const Pair pr = pairs[pair_idx];
     int64_t g = 0, h = 0;
-    if (k < nb * W) {
+    if (k < nb * W && tile * W + k % W < F) {         // padding columns hold no partials
         const size_t stride = (size_t)(nb * W);
         const size_t cstride = (size_t)T * stride;   // between chunks of one (pair, tile)
         const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile) * stride + k;
