@@ -256,8 +256,8 @@ def leafwise_predict_shap(mb, ctx, x_dev, rows, cols, y, with_cpu):
     return out
 
 
-def mixed_and_higgs(mb, ctx):
-    """Whole fits (X resident) on the NaN + categorical and HIGGS-like workloads."""
+def mixed_1m(mb, ctx):
+    """Whole fits (X resident) on the NaN + categorical workload."""
     sys.path.insert(0, str(ROOT / "tests"))
     import datasets as D
     out = {}
@@ -274,8 +274,15 @@ def mixed_and_higgs(mb, ctx):
         "reference_fit_seconds": 0.76, "reference_source": "README.md:72 (other generator)"}
     log(f"NaN+categorical 1M: {sec * 1e3:.1f} ms per fit, valid RMSE "
         f"{out['nan_categorical_1m']['valid_rmse']:.4f}")
-    del d, x, xv
+    return out
+
+
+def higgs(mb, ctx):
+    """Whole fits (X resident) on the HIGGS-like workload, plain and with GOSS."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import datasets as D
     from sklearn.metrics import roc_auc_score
+    out = {}
     x, y = D.c4_higgs_like(10_500_000, 42)
     n = 10_000_000
     xtr, ytr = np.ascontiguousarray(x[:, :n]), y[:n]
@@ -333,6 +340,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline fits (no other workloads)")
+    ap.add_argument("--only", choices=["small_1m", "mixed", "higgs"],
+                    help="run one other workload alone and print its record instead of the "
+                         "headline line (for profiling that workload)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
@@ -341,6 +351,11 @@ def main():
 
     import macboost_amd as mb
     ctx = mb.Context(0)
+    if args.only:
+        run = {"small_1m": lambda: small_and_1m(mb, ctx, not args.no_cpu),
+               "mixed": lambda: mixed_1m(mb, ctx), "higgs": lambda: higgs(mb, ctx)}[args.only]
+        print(json.dumps({"only": args.only, **run()}), flush=True)
+        return
     rows, cols = args.rows, args.cols
     x, y, x_dev, sec, value, valid, stats = headline(mb, ctx, args)
     roofline = roofline_of(stats, rows, cols, args.steps, 100)
@@ -350,7 +365,7 @@ def main():
         extras["leafwise_predict_treeshap"] = leafwise_predict_shap(
             mb, ctx, x_dev, rows, cols, y, not args.no_cpu)
         extras["small_and_1m"] = small_and_1m(mb, ctx, not args.no_cpu)
-        extras["mixed_and_higgs"] = mixed_and_higgs(mb, ctx)
+        extras["mixed_and_higgs"] = {**mixed_1m(mb, ctx), **higgs(mb, ctx)}
     cpu = None if args.no_cpu else cpu_baseline(x, y, rows, cols, args.cpu_trees)
     out = {
         "metric": "trees/s fitting 10M×100 depth-6; histogram HBM GB/s as % of peak",

@@ -13,6 +13,8 @@
 //   * the level-wise row partition is one pass that splits every node's
 //     interval in place between its children; nothing downstream depends on
 //     the order of rows inside a node, so the tree is deterministic.
+#include <hip/hip_ext.h>
+
 #include "mbk.h"
 
 #include <float.h>
@@ -1254,7 +1256,7 @@ size_t planar_bytes(const Shape &sh) {
 
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, const Entry *order,
                        const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid,
-                       const HistLayout *layout) {
+                       const HistLayout *layout, hipEvent_t start, hipEvent_t stop) {
     const HistLayout lay = layout ? *layout : gather_layout(sh);
     if (layout) {
         // the planar copy: 64-wide tiles, every stride a 16-B multiple
@@ -1267,8 +1269,13 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
     switch (sh.tile_w) {
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
-        hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,       \
-                           items, ctl, partials, lay, sh.num_bins, sh.cols);                     \
+        if (start || stop)                                                                       \
+            hipExtLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, start, stop, \
+                                  0, tiled, order, items, ctl, partials, lay, sh.num_bins,       \
+                                  sh.cols);                                                      \
+        else                                                                                     \
+            hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,   \
+                               items, ctl, partials, lay, sh.num_bins, sh.cols);                 \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)

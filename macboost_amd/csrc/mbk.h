@@ -229,10 +229,12 @@ HistLayout planar_layout(const Shape &sh);
 size_t planar_bytes(const Shape &sh);    // including 64 zero bytes of overread
 
 // Histogram items -> packed partials [item][B][W] (64-bit words, see
-// HIST_QH_BITS).  layout null: the gather layout.
+// HIST_QH_BITS).  layout null: the gather layout.  With start / stop events
+// (created by the caller), they take the kernel's own dispatch timestamps.
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
-                       uint64_t *partials, int grid, const HistLayout *layout = nullptr);
+                       uint64_t *partials, int grid, const HistLayout *layout = nullptr,
+                       hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 size_t hist_lds_size();   // static LDS of one histogram workgroup
 // Planar copy of the gather layout for the root pass over every row; out
 // holds planar_bytes(sh) bytes (the last tile's loads run up to 16 B past its

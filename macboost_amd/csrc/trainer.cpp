@@ -1245,21 +1245,18 @@ static void grow_levelwise(Trainer &t, int tree) {
     int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
 
     auto hist = [&](const mbk::Entry *ord, int level) {
+        // profiling: the kernel's own dispatch timestamps (no marker packets)
         hipEvent_t e0 = nullptr, e1 = nullptr;
         if (t.profiling) {
             MB_HIP(hipEventCreate(&e0));
             MB_HIP(hipEventCreate(&e1));
-            MB_HIP(hipEventRecord(e0, s));
         }
         // an unsampled root streams every row: the planar copy when there is one
         const bool planar = level == 0 && !sampled && t.has_root_copy;
         MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
-                                planar ? &t.root_layout : nullptr));
-        if (t.profiling) {
-            MB_HIP(hipEventRecord(e1, s));
-            t.events.push_back({e0, e1, level});
-        }
+                                planar ? &t.root_layout : nullptr, e0, e1));
+        if (t.profiling) t.events.push_back({e0, e1, level});
     };
 
     // level 0
@@ -1356,16 +1353,12 @@ static void grow_leafwise(Trainer &t, int tree) {
         if (t.profiling) {
             MB_HIP(hipEventCreate(&e0));
             MB_HIP(hipEventCreate(&e1));
-            MB_HIP(hipEventRecord(e0, s));
         }
         const bool planar = step == 0 && !sampled && t.has_root_copy;
         MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, order,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
-                                planar ? &t.root_layout : nullptr));
-        if (t.profiling) {
-            MB_HIP(hipEventRecord(e1, s));
-            t.events.push_back({e0, e1, std::min(step, 15)});
-        }
+                                planar ? &t.root_layout : nullptr, e0, e1));
+        if (t.profiling) t.events.push_back({e0, e1, std::min(step, 15)});
         MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, t.hist_a.ptr,
                                  t.hist_a.ptr, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
                                  t.count.ptr, t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
