@@ -1978,10 +1978,38 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         else ctl->level_built[level] = (uint32_t)total;
     }
     __syncthreads();
+    if (num_pairs <= 64 && tid < 64) {
+        // Balance: the item chunk c above leaves room for one partial chunk per
+        // (pair, tile), and the level's time is its largest item.  One
+        // wavefront finds the smallest chunk c' whose per-pair chunk counts
+        // still fit the same item budget (binary search between the lower
+        // bound total / budget and c, which fits); each pair then splits its
+        // rows into equal chunks of at most c'.
+        const uint64_t n = (uint32_t)tid < num_pairs ? s_cnt[tid] : 0u;
+        const uint64_t T = (uint64_t)sh.num_tiles;
+        const uint64_t K = item_budget(s_total, num_pairs, sh.num_tiles, target_items) / T;
+        uint64_t hi = s_chunk;
+        uint64_t lo = ((uint64_t)s_total + K - 1) / K;
+        if (lo < min_chunk) lo = min_chunk;
+        if (lo > hi) lo = hi;
+        while (lo < hi) {                            // uniform across the wavefront
+            const uint64_t mid = lo + (hi - lo) / 2;
+            const uint64_t k = (n + mid - 1) / mid;
+            if (wave_sum(k) <= K) hi = mid; else lo = mid + 1;
+        }
+        if (tid == 0) s_chunk = (uint32_t)lo;
+    }
+    __syncthreads();
     const uint32_t chunk = s_chunk;
+    // the chunk of pair k: its rows in equal parts of at most `chunk`
+    auto pair_chunk = [&](uint32_t cnt) {
+        const uint32_t parts = (cnt + chunk - 1) / chunk;
+        return parts ? (cnt + parts - 1) / parts : chunk;
+    };
     // items per pair -> exclusive prefix
     for (uint32_t k = tid; k < num_pairs; k += blockDim.x) {
-        const uint32_t nch = (s_cnt[k] + chunk - 1) / chunk;
+        const uint32_t pc = pair_chunk(s_cnt[k]);
+        const uint32_t nch = (s_cnt[k] + pc - 1) / pc;
         pairs[k].nchunks = nch;
         s_first[k] = nch * (uint32_t)sh.num_tiles;
     }
@@ -2011,11 +2039,12 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         }
         const uint32_t rel = it - s_first[lo];
         const uint32_t t = rel % (uint32_t)sh.num_tiles, c = rel / (uint32_t)sh.num_tiles;
+        const uint32_t pc = pair_chunk(s_cnt[lo]);
         HistItem h;
         h.pair = lo;
         h.tile = t;
-        h.start = s_seg[lo] + c * chunk;
-        h.count = min(chunk, s_cnt[lo] - c * chunk);
+        h.start = s_seg[lo] + c * pc;
+        h.count = min(pc, s_cnt[lo] - c * pc);
         items[it] = h;
     }
 }

@@ -28,16 +28,25 @@ static_assert(127ull * HIST_CHUNK_MAX < (1ull << HIST_QH_BITS), "hessian field c
 // grid (target_items): every (pair, tile) adds at most one partial chunk, so
 // reserve that slack (T * pairs) and pick the smallest r whose chunk fits
 // HIST_CHUNK_MAX.
-__host__ __device__ inline uint32_t item_chunk(uint64_t total, uint32_t num_pairs,
-                                               int32_t num_tiles, uint32_t target_items,
-                                               uint32_t min_chunk) {
+// The level's item budget, target_items * r: no plan below exceeds it.
+__host__ __device__ inline uint64_t item_budget(uint64_t total, uint32_t num_pairs,
+                                               int32_t num_tiles, uint32_t target_items) {
     const uint64_t work = total * (uint64_t)num_tiles;
     const uint64_t tgt = target_items ? target_items : 1;
     const uint64_t slack = (uint64_t)num_pairs * (uint64_t)num_tiles;
     const uint64_t need = (work + HIST_CHUNK_MAX - 1) / HIST_CHUNK_MAX;
     uint64_t r = (slack + need + tgt - 1) / tgt;
     if (tgt * r <= slack) r = slack / tgt + 1;
-    uint64_t c = (work + (tgt * r - slack) - 1) / (tgt * r - slack);
+    return tgt * r;
+}
+
+__host__ __device__ inline uint32_t item_chunk(uint64_t total, uint32_t num_pairs,
+                                               int32_t num_tiles, uint32_t target_items,
+                                               uint32_t min_chunk) {
+    const uint64_t work = total * (uint64_t)num_tiles;
+    const uint64_t slack = (uint64_t)num_pairs * (uint64_t)num_tiles;
+    const uint64_t budget = item_budget(total, num_pairs, num_tiles, target_items);
+    uint64_t c = (work + (budget - slack) - 1) / (budget - slack);
     if (c < min_chunk) c = min_chunk;
     if (c > HIST_CHUNK_MAX) c = HIST_CHUNK_MAX;
     return (uint32_t)c;

@@ -99,14 +99,13 @@ extern "C" int mbk_node_hist_split_noalloc(mbk_context *ctx, const uint8_t *bins
         if (rows < 0 || !bins_tiled || !entries || !max_gh || !hist_out || !results)
             mb::invalid("null or empty argument");
         const int32_t T = (cols + tile_width - 1) / tile_width;
-        // items of the node: the planner's own chunking, predicted here, must
-        // fit both the item list and the partial histograms
+        // items of the node: the planner's budget for it, an upper bound on
+        // what it plans, must fit both the item list and the partial histograms
         const size_t per_item = (size_t)tile_width * (size_t)num_bins * sizeof(uint64_t);
         const size_t cap = std::min(MAX_ITEMS, (SCRATCH_BYTES - OFF_PARTIALS) / per_item);
         const uint32_t target = (uint32_t)std::min<size_t>(256, cap / 2 > 0 ? cap / 2 : 1);
         const uint32_t min_chunk = 2048;
-        const uint32_t chunk = mbk::item_chunk((uint64_t)n, 1, T, target, min_chunk);
-        const uint64_t items = ((uint64_t)n + chunk - 1) / chunk * (uint64_t)T;
+        const uint64_t items = mbk::item_budget((uint64_t)n, 1, T, target);
         if (items > cap)
             mb::invalid("node of " + std::to_string(n) + " rows needs " + std::to_string(items) +
                         " histogram items; the no-allocation scratch holds " +
