@@ -295,7 +295,7 @@ void *mbx_trainer_create(const char *params_json, const float *x, int64_t rows, 
                          char **err);
 /* Enqueue num_trees boosting iterations and wait for them. */
 int mbx_trainer_grow(void *trainer, int32_t num_trees, char **err);
-/* 1 = record HIP events around every histogram launch from now on. */
+/* 1 = time every histogram launch (its own dispatch timestamps) from now on. */
 int mbx_trainer_profile(void *trainer, int32_t enable, char **err);
 /* Histogram-kernel totals since profiling was enabled: launches, total
  * milliseconds, and algorithmic bytes (sum over built nodes of rows*(cols+4)). */

@@ -1224,3 +1224,26 @@ def test_allowed_features_equal_dropping_the_other_columns(oracle):
         used = {int(f) for f in mc.forest.feature[t] if f >= 0}
         mask = _mask_stream(t, 8, 0.5, allowed={0, 1, 2, 3, 4})
         assert all(mask[f] for f in used), t
+
+
+def test_results_do_not_depend_on_the_thread_count(oracle):
+    # the oracle's parallel loops are over independent rows or features or
+    # integer sums, and its double sums run in fixed row blocks: one thread
+    # and every thread give the same edges, bins, base score, trees and
+    # predictions (GOSS and NaN included; 150k rows span several sum blocks)
+    x, y = O.friedman(150_000, 12, 77)
+    x = x.copy()
+    x[3, ::7] = np.nan
+    kw = dict(num_trees=12, max_depth=5, goss=True, learning_rate=0.25)
+    try:
+        O.set_threads(1)
+        a = fit_raw(x, y, **kw)
+        O.set_threads(0)
+        b = fit_raw(x, y, **kw)
+    finally:
+        O.set_threads(0)
+    assert np.array_equal(a.edges, b.edges)
+    assert np.float32(a.base_score) == np.float32(b.base_score)
+    for name in ("feature", "threshold", "leaf", "cover", "gain"):
+        assert np.array_equal(getattr(a.forest, name), getattr(b.forest, name)), name
+    assert np.array_equal(a.preds, b.preds)
