@@ -104,6 +104,7 @@ struct Tree {
 struct Device {
     int id = 0;
     hipStream_t stream = nullptr;
+    hipStream_t copy_stream = nullptr;   // host uploads that overlap work on `stream`
     int num_cus = 0;
     explicit Device(int device_id);
     ~Device();
@@ -120,27 +121,59 @@ void upload(void *dst, const void *src, size_t bytes, hipStream_t s);
 // complete on return (64 MB or more through the pinned staging buffers).
 void download(void *dst, const void *src, size_t bytes, hipStream_t s);
 
+// Device memory cache for buffers that are allocated once per fit with the
+// same sizes fit after fit (the bin matrices, order entries, partials, ...):
+// a released block is kept for the next request of the same byte size on the
+// same device instead of going back through hipFree / hipMalloc, which cost
+// milliseconds per fit at 10M rows.  The cache holds at most half of the
+// device's memory (oldest blocks freed first) and is emptied when a
+// hipMalloc fails.  A block must be released only when no queued work uses
+// it any more.
+void *pool_alloc(size_t bytes, int *device);
+void pool_free(void *p, size_t bytes, int device);
+void pool_trim();                                     // free every cached block
+hipError_t malloc_or_trim(void **p, size_t bytes);    // hipMalloc, once more after pool_trim
+
 template <typename T>
 struct DevBuf {
     T *ptr = nullptr;
     size_t n = 0;
+    bool pooled = false;     // allocate through the device memory cache
+    int device = 0;          // of a pooled block
     DevBuf() = default;
     explicit DevBuf(size_t count) { alloc(count); }
     ~DevBuf() { release(); }
     DevBuf(const DevBuf &) = delete;
     DevBuf &operator=(const DevBuf &) = delete;
-    DevBuf(DevBuf &&o) noexcept : ptr(o.ptr), n(o.n) { o.ptr = nullptr; o.n = 0; }
+    DevBuf(DevBuf &&o) noexcept : ptr(o.ptr), n(o.n), pooled(o.pooled), device(o.device) {
+        o.ptr = nullptr;
+        o.n = 0;
+    }
     DevBuf &operator=(DevBuf &&o) noexcept {
-        if (this != &o) { release(); ptr = o.ptr; n = o.n; o.ptr = nullptr; o.n = 0; }
+        if (this != &o) {
+            release();
+            ptr = o.ptr; n = o.n; pooled = o.pooled; device = o.device;
+            o.ptr = nullptr; o.n = 0;
+        }
         return *this;
     }
     void alloc(size_t count) {
         release();
         n = count;
-        if (count) MB_HIP(hipMalloc(reinterpret_cast<void **>(&ptr), count * sizeof(T)));
+        if (!count) return;
+        if (pooled) {
+            ptr = static_cast<T *>(pool_alloc(count * sizeof(T), &device));
+        } else {
+            void *p = nullptr;
+            MB_HIP(malloc_or_trim(&p, count * sizeof(T)));
+            ptr = static_cast<T *>(p);
+        }
     }
     void release() {
-        if (ptr) (void)hipFree(ptr);
+        if (ptr) {
+            if (pooled) pool_free(ptr, n * sizeof(T), device);
+            else (void)hipFree(ptr);
+        }
         ptr = nullptr;
         n = 0;
     }

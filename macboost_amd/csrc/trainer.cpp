@@ -75,19 +75,124 @@ std::string swift_float(float v) {
     return buf;
 }
 
+// ---------------------------------------------------------------------------
+// Device memory cache (DevBuf::pooled)
+// ---------------------------------------------------------------------------
+
+namespace {
+struct CachedBlock {
+    void *p;
+    size_t bytes;
+    int device;
+    uint64_t tick;
+};
+std::mutex g_pool_mu;
+std::vector<CachedBlock> g_pool;
+size_t g_pool_bytes[64] = {};
+size_t g_pool_limit[64] = {};
+uint64_t g_pool_tick = 0;
+
+size_t pool_limit(int device) {             // with g_pool_mu held
+    if (device < 0 || device >= 64) return 0;
+    if (!g_pool_limit[device]) {
+        size_t free_b = 0, total_b = 0;
+        if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) total_b = 0;
+        g_pool_limit[device] = total_b / 2 + 1;
+    }
+    return g_pool_limit[device];
+}
+}  // namespace
+
+hipError_t malloc_or_trim(void **p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        pool_trim();
+        e = hipMalloc(p, bytes);
+    }
+    return e;
+}
+
+void *pool_alloc(size_t bytes, int *device) {
+    int dev = 0;
+    MB_HIP(hipGetDevice(&dev));
+    *device = dev;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        for (size_t k = 0; k < g_pool.size(); ++k) {
+            if (g_pool[k].device == dev && g_pool[k].bytes == bytes) {
+                void *p = g_pool[k].p;
+                g_pool[k] = g_pool.back();
+                g_pool.pop_back();
+                if (dev >= 0 && dev < 64) g_pool_bytes[dev] -= bytes;
+                return p;
+            }
+        }
+    }
+    void *p = nullptr;
+    MB_HIP(malloc_or_trim(&p, bytes));
+    return p;
+}
+
+void pool_free(void *p, size_t bytes, int device) {
+    std::vector<void *> evict;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        const size_t limit = pool_limit(device);
+        if (device < 0 || device >= 64 || bytes > limit) {
+            evict.push_back(p);
+        } else {
+            g_pool.push_back({p, bytes, device, ++g_pool_tick});
+            g_pool_bytes[device] += bytes;
+            while (g_pool_bytes[device] > limit) {   // oldest blocks of this device first
+                size_t oldest = g_pool.size();
+                for (size_t k = 0; k < g_pool.size(); ++k)
+                    if (g_pool[k].device == device &&
+                        (oldest == g_pool.size() || g_pool[k].tick < g_pool[oldest].tick))
+                        oldest = k;
+                evict.push_back(g_pool[oldest].p);
+                g_pool_bytes[device] -= g_pool[oldest].bytes;
+                g_pool[oldest] = g_pool.back();
+                g_pool.pop_back();
+            }
+        }
+    }
+    for (void *q : evict) (void)hipFree(q);
+}
+
+void pool_trim() {
+    std::vector<CachedBlock> all;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        all.swap(g_pool);
+        for (size_t &b : g_pool_bytes) b = 0;
+    }
+    for (const CachedBlock &b : all) (void)hipFree(b.p);
+}
+
 Device::Device(int device_id) : id(device_id) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= device_id)
         throw Error("No HIP GPU available");
     MB_HIP(hipSetDevice(device_id));
     MB_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
-    hipDeviceProp_t prop;
-    MB_HIP(hipGetDeviceProperties(&prop, device_id));
-    num_cus = prop.multiProcessorCount;
+    MB_HIP(hipStreamCreateWithFlags(&copy_stream, hipStreamNonBlocking));
+    // the CU count, looked up once per device (a properties query costs ~1 ms)
+    static std::mutex mu;
+    static int cus[64] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    if (device_id >= 64 || !cus[device_id]) {
+        int n = 0;
+        MB_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device_id));
+        if (device_id >= 64) { num_cus = n; return; }
+        cus[device_id] = n;
+    }
+    num_cus = cus[device_id];
 }
 
 Device::~Device() {
     if (stream) (void)hipStreamDestroy(stream);
+    if (copy_stream) (void)hipStreamDestroy(copy_stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -246,6 +351,7 @@ struct Trainer {
     DevBuf<float> samp_g, samp_h, samp_h_kept;
     // kept[i] of a sampled level-wise tree, for the terminal walk's counts
     DevBuf<uint8_t> kept;
+    bool labels_ready = false;      // labels already uploaded during the setup
     bool kept_walk = false;
     DevBuf<uint64_t> route_cursor;
     uint32_t route_grid = 1;
@@ -300,7 +406,20 @@ struct Trainer {
     std::vector<std::string> warnings;
     double t_edges = 0.0, t_bin = 0.0;
 
+    Trainer() {
+        // the per-row buffers come from the device memory cache: a fit of the
+        // same shape finds them there
+        for (DevBuf<uint8_t> *b : {&bins_tiled, &bins_fm, &vbins_fm, &bins_root, &kept})
+            b->pooled = true;
+        for (DevBuf<float> *b : {&labels, &weights, &preds, &vpreds, &samp_g, &samp_h, &samp_h_kept})
+            b->pooled = true;
+        order_a.pooled = order_b.pooled = partials.pooled = items.pooled = true;
+        hist_a.pooled = hist_b.pooled = true;
+    }
+
     ~Trainer() {
+        // cached blocks must be idle when they are handed back
+        if (dev && dev->stream) (void)hipStreamSynchronize(dev->stream);
         for (auto &e : events) { (void)hipEventDestroy(e.start); (void)hipEventDestroy(e.end); }
     }
 
@@ -596,8 +715,9 @@ static float eval_metric(const Params &p, const float *pred, const float *y, int
 }
 
 // Checks shared by both entry points (Booster.swift:451-529).
-static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
-                            const float *w, const float *xv, int64_t vrows, const float *yv) {
+// The per-row checks of validate_inputs: labels, weights, validation labels.
+static void validate_rows(const Params &p, int64_t rows, const float *y, const float *w,
+                          const float *xv, int64_t vrows, const float *yv) {
     validate_labels(p, y, rows);
     if (w) {
         const int64_t block = 1 << 18;
@@ -612,6 +732,10 @@ static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const f
                         "; weights must be finite and >= 0");
     }
     if (xv && yv && vrows > 0) validate_labels(p, yv, vrows);
+}
+
+// The shape checks of validate_inputs.
+static void validate_shape(const Params &p, int64_t rows, int64_t cols) {
     if (p.has_monotone && (int64_t)p.monotone.size() != cols)
         invalid("monotoneConstraints has " + std::to_string(p.monotone.size()) +
                 " entries, X has " + std::to_string(cols) + " features");
@@ -621,6 +745,13 @@ static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const f
         if (!ok) invalid("allowedFeatures must be non-empty indices within 0..<" + std::to_string(cols));
     }
     if (rows > 0xFFFFFFF0LL) invalid("more than 2^32 rows are not supported");
+}
+
+// Input checks in the reference's order (Booster.swift:262-330, :1724-1826).
+static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const float *y,
+                            const float *w, const float *xv, int64_t vrows, const float *yv) {
+    validate_rows(p, rows, y, w, xv, vrows, yv);
+    validate_shape(p, rows, cols);
 }
 
 // Device, shapes and params-derived constants; t.p holds the effective
@@ -719,7 +850,26 @@ static void build_root_copy(Trainer &t) {
     t.has_root_copy = true;
 }
 
-static void setup_buffers(Trainer &t, const float *y, const float *w, const float *yv) {
+// Base scores (Booster.swift:786-846): per-class log priors with +1 smoothing
+// for multiclass, else one base_score.
+static std::vector<float> base_scores_of(const Params &p, const float *y, const float *w,
+                                         int64_t rows) {
+    if (p.objective == OBJ_MULTICLASS) {
+        const int K = p.num_classes;
+        std::vector<double> cnt((size_t)K, 1.0);
+        for (int64_t i = 0; i < rows; ++i) cnt[(size_t)y[i]] += w ? (double)w[i] : 1.0;
+        double total = 0;
+        for (double c : cnt) total += c;
+        std::vector<float> out((size_t)K);
+        for (int k = 0; k < K; ++k) out[(size_t)k] = (float)std::log(cnt[(size_t)k] / total);
+        return out;
+    }
+    Phase ph("base score");
+    return {base_score(p, y, w, rows)};
+}
+
+static void setup_buffers(Trainer &t, const float *y, const float *w, const float *yv,
+                          const std::vector<float> *bases = nullptr) {
     const Params &p = t.p;
     hipStream_t s = t.dev->stream;
     const int64_t rows = t.rows, cols = t.cols, vrows = t.vrows;
@@ -732,28 +882,18 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.gp.class_index = 0;
     t.gp.rows = rows;
     // the host keeps no copy of the labels: a train metric reads them back
-    t.labels.alloc((size_t)rows);
+    if (!t.labels_ready) {
+        t.labels.alloc((size_t)rows);
+        upload(t.labels.ptr, y, (size_t)rows * 4, s);
+    }
     t.preds.alloc((size_t)rows * (size_t)K);
-    upload(t.labels.ptr, y, (size_t)rows * 4, s);
     if (w) {
         t.has_weights = true;
         t.weights.alloc((size_t)rows);
         upload(t.weights.ptr, w, (size_t)rows * 4, s);
     }
-    if (K > 1) {
-        // per-class log priors with +1 smoothing (Booster.swift:838-846)
-        std::vector<double> cnt((size_t)K, 1.0);
-        for (int64_t i = 0; i < rows; ++i) cnt[(size_t)y[i]] += w ? (double)w[i] : 1.0;
-        double total = 0;
-        for (double c : cnt) total += c;
-        t.base_scores.resize((size_t)K);
-        for (int k = 0; k < K; ++k) t.base_scores[(size_t)k] = (float)std::log(cnt[(size_t)k] / total);
-        t.base = 0.0f;
-    } else {
-        Phase ph("base score");
-        t.base = base_score(p, y, w, rows);
-        t.base_scores = {t.base};
-    }
+    t.base_scores = bases ? *bases : base_scores_of(p, y, w, rows);
+    t.base = K > 1 ? 0.0f : t.base_scores[0];
     if (t.has_valid) {
         t.vlabels_h.assign(yv, yv + vrows);
         t.vpreds.alloc((size_t)vrows * (size_t)K);
@@ -891,20 +1031,25 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
 // check reads a strided row sample copied to the host, and the categorical
 // ids are checked on the device (the first offending row of the first
 // offending feature gives the host path's message).
+// Device features: the categorical id rule is checked on the device; the
+// rows the leakage check samples (every max(1, rows/4096)-th) are copied to
+// xs [m][cols] with their labels in ys, for check_leakage on the host
+// (every row of that sample is used: its step is 1, m < 8192).
 static void check_device_features(const Params &p, const float *x_dev, int64_t rows,
                                   int64_t cols, int64_t rs, int64_t cs, const float *y,
-                                  hipStream_t s, std::vector<std::string> &warnings) {
+                                  hipStream_t s, std::vector<float> &xs, std::vector<float> &ys) {
     const int64_t step = std::max<int64_t>(1, rows / 4096);
     const int64_t m = (rows + step - 1) / step;
+    xs.clear();
+    ys.clear();
     if (m >= 50) {
         DevBuf<float> sd((size_t)(m * cols));
-        std::vector<float> xs((size_t)(m * cols)), ys((size_t)m);
+        xs.resize((size_t)(m * cols));
+        ys.resize((size_t)m);
         MB_HIP(mbk::launch_gather_sample(s, x_dev, rs, cs, step, m, (int)cols, sd.ptr));
         MB_HIP(hipMemcpyAsync(xs.data(), sd.ptr, sd.bytes(), hipMemcpyDeviceToHost, s));
         MB_HIP(hipStreamSynchronize(s));
         for (int64_t k = 0; k < m; ++k) ys[(size_t)k] = y[k * step];
-        // every row of the sample is used (its step is 1: m < 8192)
-        check_leakage(p.verbose, xs.data(), m, cols, cols, 1, ys.data(), warnings);
     }
     if (p.categorical.empty()) return;
     std::vector<int32_t> cat(p.categorical.begin(), p.categorical.end());
@@ -938,115 +1083,157 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
                            const float *xv, int64_t vrows, const float *yv) {
     if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
     Phase ph_all("fit setup");
-    {
-        Phase ph("validate inputs");
-        validate_params(pin);
-        validate_inputs(pin, rows, cols, y, w, xv, vrows, yv);
-    }
-    auto tr = std::make_unique<Trainer>();
-    Trainer &t = *tr;
-    t.p = pin;
-    t.user_params = pin;
-    const Params &p = t.p;
-    const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
-    std::unique_ptr<Booster> im;
-    if (!p.init_model.empty()) {                     // Booster.swift:487-499
-        if (x_on_device) invalid("initModel needs the raw features in host memory");
-        im.reset(load_model_file(p.init_model));
-        if (im->num_features != cols)
-            invalid("initModel expects " + std::to_string(im->num_features) + " features, X has " +
-                    std::to_string(cols));
-        if (im->params.objective != p.objective) invalid("initModel objective differs");
-        const int k_want = p.objective == OBJ_MULTICLASS ? p.num_classes : 1;
-        if (std::max(1, im->trained_num_classes) != k_want)
-            invalid("initModel has " + std::to_string(im->trained_num_classes) +
-                    " classes, the params ask for " + std::to_string(k_want));
-    }
-    // host features: the leakage check runs on a host thread while the device
-    // is set up and the data uploaded and binned (a failure there is rethrown
-    // on this thread after the join)
-    std::vector<std::string> leak_warnings;
-    std::exception_ptr leak_error;
-    struct Joiner {
+    validate_params(pin);
+    // The per-row checks (labels, weights) and the base scores run on a host
+    // thread while the device is set up and the features binned.  The checks
+    // keep the reference's order: a later check's error is reported only when
+    // the row checks pass.
+    struct HostPrep {
         std::thread th;
-        ~Joiner() { if (th.joinable()) th.join(); }
-    } leak;
-    if (!x_on_device) {
-        leak.th = std::thread([&] {
-            try {
-                check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
-            } catch (...) {
-                leak_error = std::current_exception();
-            }
-        });
-        validate_categoricals(p, x, rows, cols, rs, cs);
-    }
-    if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
-    setup_shape(t, rows, cols);
-    hipStream_t s = t.dev->stream;
-    const int tile_w = t.sh.tile_w;
-    if (x_on_device) {
-        Phase ph("device feature checks");
-        check_device_features(p, x, rows, cols, rs, cs, y, s, leak_warnings);
-    }
-
-    // --- binning on the device: (upload,) quantile edges, bin_data --------
-    double t0 = now_s();
-    {
-        DevBuf<float> xd;
-        const float *xsrc = x;
+        std::exception_ptr err;
+        std::vector<float> bases;
+        void join() { if (th.joinable()) th.join(); }
+        ~HostPrep() { join(); }
+    } prep;
+    prep.th = std::thread([&] {
+        try {
+            Phase ph("validate inputs");
+            validate_rows(pin, rows, y, w, xv, vrows, yv);
+            prep.bases = base_scores_of(pin, y, w, rows);
+        } catch (...) {
+            prep.err = std::current_exception();
+        }
+    });
+    try {
+        validate_shape(pin, rows, cols);
+        auto tr = std::make_unique<Trainer>();
+        Trainer &t = *tr;
+        t.p = pin;
+        t.user_params = pin;
+        const Params &p = t.p;
+        const int64_t rs = row_major ? cols : 1, cs = row_major ? 1 : rows;
+        std::unique_ptr<Booster> im;
+        if (!p.init_model.empty()) {                     // Booster.swift:487-499
+            if (x_on_device) invalid("initModel needs the raw features in host memory");
+            im.reset(load_model_file(p.init_model));
+            if (im->num_features != cols)
+                invalid("initModel expects " + std::to_string(im->num_features) + " features, X has " +
+                        std::to_string(cols));
+            if (im->params.objective != p.objective) invalid("initModel objective differs");
+            const int k_want = p.objective == OBJ_MULTICLASS ? p.num_classes : 1;
+            if (std::max(1, im->trained_num_classes) != k_want)
+                invalid("initModel has " + std::to_string(im->trained_num_classes) +
+                        " classes, the params ask for " + std::to_string(k_want));
+        }
+        // host features: the leakage check runs on a host thread while the device
+        // is set up and the data uploaded and binned (a failure there is rethrown
+        // on this thread after the join)
+        std::vector<std::string> leak_warnings;
+        std::exception_ptr leak_error;
+        std::vector<float> leak_xs, leak_ys;         // device features: the sampled rows
+        struct Joiner {
+            std::thread th;
+            ~Joiner() { if (th.joinable()) th.join(); }
+        } leak;
         if (!x_on_device) {
-            xd.alloc((size_t)rows * (size_t)cols);
-            upload(xd.ptr, x, xd.bytes(), s);
-            xsrc = xd.ptr;
+            leak.th = std::thread([&] {
+                try {
+                    check_leakage(p.verbose, x, rows, cols, rs, cs, y, leak_warnings);
+                } catch (...) {
+                    leak_error = std::current_exception();
+                }
+            });
+            validate_categoricals(p, x, rows, cols, rs, cs);
         }
-        const size_t ne = (size_t)p.num_bins - 2;
-        DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
+        if (xv && yv && vrows > 0) validate_categoricals(p, xv, vrows, cols, 1, vrows);
+        setup_shape(t, rows, cols);
+        hipStream_t s = t.dev->stream;
+        const int tile_w = t.sh.tile_w;
+        if (x_on_device) {
+            Phase ph("device feature checks");
+            check_device_features(p, x, rows, cols, rs, cs, y, s, leak_xs, leak_ys);
+            if (!leak_ys.empty()) {
+                leak.th = std::thread([&] {
+                    try {
+                        check_leakage(p.verbose, leak_xs.data(), (int64_t)leak_ys.size(), cols,
+                                      cols, 1, leak_ys.data(), leak_warnings);
+                    } catch (...) {
+                        leak_error = std::current_exception();
+                    }
+                });
+            }
+        }
+
+        // --- binning on the device: (upload,) quantile edges, bin_data --------
+        double t0 = now_s();
         {
-            Phase ph("quantile edges");
-            const double te = now_s();
-            const size_t cap = mbk::edge_sample_cap(rows);
-            DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
-            MB_HIP(mbk::launch_edges(s, xsrc, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
-                                     ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
-            t.edges.resize((size_t)cols * ne);
-            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+            DevBuf<float> xd;
+            const float *xsrc = x;
+            if (!x_on_device) {
+                xd.alloc((size_t)rows * (size_t)cols);
+                upload(xd.ptr, x, xd.bytes(), s);
+                xsrc = xd.ptr;
+            }
+            const size_t ne = (size_t)p.num_bins - 2;
+            DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
+            {
+                Phase ph("quantile edges");
+                const double te = now_s();
+                const size_t cap = mbk::edge_sample_cap(rows);
+                DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
+                MB_HIP(mbk::launch_edges(s, xsrc, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
+                                         ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
+                // the labels cross PCIe on the copy stream while the device sorts
+                t.labels.alloc((size_t)rows);
+                upload(t.labels.ptr, y, (size_t)rows * 4, t.dev->copy_stream);
+                MB_HIP(hipStreamSynchronize(t.dev->copy_stream));
+                t.labels_ready = true;
+                t.edges.resize((size_t)cols * ne);
+                MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+                MB_HIP(hipStreamSynchronize(s));
+                t.t_edges = now_s() - te;
+            }
+            Phase ph("bin data");
+            t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
+            t.bins_fm.alloc((size_t)rows * (size_t)cols);
+            MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
+                                        p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
+                                        t.bins_fm.ptr));
+            if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
             MB_HIP(hipStreamSynchronize(s));
-            t.t_edges = now_s() - te;
         }
-        Phase ph("bin data");
-        t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
-        t.bins_fm.alloc((size_t)rows * (size_t)cols);
-        MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
-                                    p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
-                                    t.bins_fm.ptr));
-        if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
-        MB_HIP(hipStreamSynchronize(s));
-    }
-    t.t_bin = now_s() - t0 - t.t_edges;              // (upload +) bin_data
-    Phase ph_rest("labels, base score, buffers");
-    if (leak.th.joinable()) leak.th.join();
-    if (leak_error) std::rethrow_exception(leak_error);
-    t.warnings.insert(t.warnings.begin(), leak_warnings.begin(), leak_warnings.end());
-    if (im) {
-        // the init model's raw scores on the training (and validation) rows
-        if (row_major) {
-            std::vector<float> xfm((size_t)rows * (size_t)cols);
-            for (int64_t i = 0; i < rows; ++i)
-                for (int64_t f = 0; f < cols; ++f) xfm[(size_t)(f * rows + i)] = x[i * cols + f];
-            t.seed_train = im->predict_raw(xfm.data(), rows, cols);
-        } else {
-            t.seed_train = im->predict_raw(x, rows, cols);
+        t.t_bin = now_s() - t0 - t.t_edges;              // (upload +) bin_data
+        prep.join();
+        if (prep.err) std::rethrow_exception(prep.err);
+        Phase ph_rest("labels, buffers");
+        if (leak.th.joinable()) leak.th.join();
+        if (leak_error) std::rethrow_exception(leak_error);
+        t.warnings.insert(t.warnings.begin(), leak_warnings.begin(), leak_warnings.end());
+        if (im) {
+            // the init model's raw scores on the training (and validation) rows
+            if (row_major) {
+                std::vector<float> xfm((size_t)rows * (size_t)cols);
+                for (int64_t i = 0; i < rows; ++i)
+                    for (int64_t f = 0; f < cols; ++f) xfm[(size_t)(f * rows + i)] = x[i * cols + f];
+                t.seed_train = im->predict_raw(xfm.data(), rows, cols);
+            } else {
+                t.seed_train = im->predict_raw(x, rows, cols);
+            }
+            if (xv && yv && vrows > 0) t.seed_valid = im->predict_raw(xv, vrows, cols);
+            t.init_trees = im->trees;
         }
-        if (xv && yv && vrows > 0) t.seed_valid = im->predict_raw(xv, vrows, cols);
-        t.init_trees = im->trees;
+        setup_buffers(t, y, w, yv, &prep.bases);
+        if (im) {
+            t.base = im->base_score;
+            t.base_scores = im->base_scores;
+        }
+        return tr.release();
+    } catch (...) {
+        // the row checks come first in the reference's order
+        prep.join();
+        if (prep.err) std::rethrow_exception(prep.err);
+        throw;
     }
-    setup_buffers(t, y, w, yv);
-    if (im) {
-        t.base = im->base_score;
-        t.base_scores = im->base_scores;
-    }
-    return tr.release();
 }
 
 Trainer *trainer_create(const Params &p, const float *x, int64_t rows, int64_t cols,
