@@ -336,7 +336,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2, help="untimed 100-tree fits")
     ap.add_argument("--rows", type=int, default=10_000_000)
     ap.add_argument("--cols", type=int, default=100)
-    ap.add_argument("--cpu-trees", type=int, default=3)
+    ap.add_argument("--cpu-trees", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline fits (no other workloads)")

@@ -595,6 +595,20 @@ def test_goss_and_bagging_identical_trees(params):
     check_identical(x, y, dict({"num_trees": 25, "max_depth": 6}, **params), x_test=xt)
 
 
+@pytest.mark.parametrize("params", [
+    {"goss": True, "min_child_weight": 0.0},
+    {"subsample": 0.6, "min_child_weight": 0.0, "min_split_gain": -1.0},
+])
+def test_sampled_trees_without_a_child_hessian_floor(params):
+    # with min_child_weight = 0 a split may leave a child without kept rows,
+    # so a sampled tree counts its deepest nodes with the partition rather
+    # than in the prediction walk (which would apply such a child's leaf to
+    # rows the sample left out): both paths must give the oracle's trees
+    x, y = mb.friedman(20_000, 12, 35)
+    xt, _ = mb.friedman(4000, 12, 36)
+    check_identical(x, y, dict({"num_trees": 25, "max_depth": 6}, **params), x_test=xt)
+
+
 def test_goss_logistic_nan_categorical_identical_trees():
     # GOSSTests.swift:108-130 runs GOSS with NaN and categorical features
     x, y = _mixed(15_000)
