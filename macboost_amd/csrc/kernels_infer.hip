@@ -9,6 +9,7 @@
 // rounding to f32 at the end.
 #include <algorithm>
 
+#include "grad.h"
 #include "mbk.h"
 
 #include <math.h>
@@ -79,15 +80,28 @@ static int device_cus() {
 // level (counters in LDS, one global add per non-empty node per block).  The
 // split records (feature, bin | flags << 8) and leaf values are staged in LDS,
 // so each level costs one global gather per row: the row's bin byte.
+// With GRAD the walk also starts the next tree's gradient pass on the updated
+// predictions: per-block maxima of |g| and h into gpart (as k_grad_max's
+// partials) and, with g_out / h_out, every row's g and h.
 constexpr int WALK_THREADS = 1024;
 constexpr int WALK_ROWS = 8;
 
-__global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__restrict__ bins_fm,
+struct WalkGrad {
+    GradParams gp;
+    const float *labels;
+    const float *weights;
+    uint32_t *gpart;
+    float *g_out, *h_out;
+};
+
+template <bool GRAD>
+__global__ __launch_bounds__(WALK_THREADS, 8) void k_walk_count(const uint8_t *__restrict__ bins_fm,
                                                              int64_t rows, int32_t nb,
                                                              int32_t max_depth, TreeOut tree,
                                                              float *__restrict__ preds,
                                                              uint32_t *__restrict__ count,
-                                                             const uint8_t *__restrict__ kept) {
+                                                             const uint8_t *__restrict__ kept,
+                                                             WalkGrad wg) {
     extern __shared__ uint32_t wc_lds[];
     const uint32_t deep = 1u << max_depth, deep_start = deep - 1;
     const uint32_t internal = deep - 1, total = 2 * deep - 1;
@@ -104,6 +118,7 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
     for (uint32_t k = threadIdx.x; k < total; k += blockDim.x) s_leaf[k] = tree.leaf[k];
     __syncthreads();
     constexpr int64_t CHUNK = (int64_t)WALK_THREADS * WALK_ROWS;
+    uint32_t mg = 0, mh = 0;
     for (int64_t c0 = (int64_t)blockIdx.x * CHUNK; c0 < rows; c0 += (int64_t)gridDim.x * CHUNK) {
         const int64_t base = c0 + threadIdx.x;
         uint32_t n[WALK_ROWS];
@@ -142,8 +157,34 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
         for (int k = 0; k < WALK_ROWS; ++k) {
             const int64_t i = base + (int64_t)k * WALK_THREADS;
             if (i >= rows) continue;
-            if (preds) preds[i] += s_leaf[n[k]];    // null: counts only
+            if (preds) {                             // null: counts only
+                const float np = preds[i] + s_leaf[n[k]];
+                preds[i] = np;
+                if (GRAD) {
+                    float g, h;
+                    const float w = wg.gp.has_weights ? wg.weights[i] : 1.0f;
+                    row_grad(wg.gp, np, wg.labels[i], w, g, h);
+                    mg = max(mg, __float_as_uint(fabsf(g)));
+                    mh = max(mh, __float_as_uint(h));
+                    if (wg.g_out) { wg.g_out[i] = g; wg.h_out[i] = h; }
+                }
+            }
             if (((counts >> k) & 1u) && n[k] >= deep_start) atomicAdd(&s_cnt[n[k] - deep_start], 1u);
+        }
+    }
+    if (GRAD) {
+        __shared__ uint32_t red[2][WALK_THREADS / 64];
+        for (int o = 32; o > 0; o >>= 1) {
+            mg = max(mg, (uint32_t)__shfl_xor((int)mg, o, 64));
+            mh = max(mh, (uint32_t)__shfl_xor((int)mh, o, 64));
+        }
+        if ((threadIdx.x & 63) == 0) { red[0][threadIdx.x >> 6] = mg; red[1][threadIdx.x >> 6] = mh; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t a = red[0][0], b = red[1][0];
+            for (int k = 1; k < WALK_THREADS / 64; ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
+            wg.gpart[2 * blockIdx.x] = a;
+            wg.gpart[2 * blockIdx.x + 1] = b;
         }
     }
     if (!count) return;                              // null: predictions only
@@ -152,17 +193,40 @@ __global__ __launch_bounds__(WALK_THREADS) void k_walk_count(const uint8_t *__re
         if (s_cnt[k]) atomicAdd(&count[deep_start + k], s_cnt[k]);
 }
 
+static int64_t walk_grid(int64_t rows) {
+    const int64_t per = (int64_t)WALK_THREADS * WALK_ROWS;
+    // two 1024-thread blocks per CU, or one block per chunk when fewer
+    return std::max<int64_t>(1, std::min<int64_t>((rows + per - 1) / per, 2 * (int64_t)device_cus()));
+}
+
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                              int32_t num_bins, int32_t max_depth, const TreeOut tree,
                              float *preds, uint32_t *count, const uint8_t *kept) {
     if (rows <= 0) return hipSuccess;
-    const int64_t per = (int64_t)WALK_THREADS * WALK_ROWS;
     const size_t deep = (size_t)1 << max_depth;
     const size_t lds = (deep + 2 * (deep - 1) + (2 * deep - 1)) * sizeof(uint32_t);
-    // two 1024-thread blocks per CU, or one block per chunk when fewer
-    const int64_t grid = std::min<int64_t>((rows + per - 1) / per, 2 * (int64_t)device_cus());
-    hipLaunchKernelGGL(k_walk_count, dim3((unsigned)grid), dim3(WALK_THREADS),
-                       lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count, kept);
+    hipLaunchKernelGGL(k_walk_count<false>, dim3((unsigned)walk_grid(rows)), dim3(WALK_THREADS),
+                       lds, s, bins_fm, rows, num_bins, max_depth, tree, preds, count, kept,
+                       WalkGrad{});
+    return hipGetLastError();
+}
+
+hipError_t launch_walk_count_grad(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                                  int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                                  float *preds, uint32_t *count, const uint8_t *kept,
+                                  const GradParams &gp, const float *labels,
+                                  const float *weights, uint32_t *gpart, float *g_out,
+                                  float *h_out, int *partials) {
+    *partials = 0;
+    if (rows <= 0 || !preds) return hipErrorInvalidValue;
+    if (gp.objective == 7) return hipErrorInvalidValue;   // one output per row only
+    const size_t deep = (size_t)1 << max_depth;
+    const size_t lds = (deep + 2 * (deep - 1) + (2 * deep - 1)) * sizeof(uint32_t);
+    const int64_t grid = walk_grid(rows);
+    hipLaunchKernelGGL(k_walk_count<true>, dim3((unsigned)grid), dim3(WALK_THREADS), lds, s,
+                       bins_fm, rows, num_bins, max_depth, tree, preds, count, kept,
+                       WalkGrad{gp, labels, weights, gpart, g_out, h_out});
+    *partials = (int)grid;
     return hipGetLastError();
 }
 

@@ -15,6 +15,7 @@
 //     the order of rows inside a node, so the tree is deterministic.
 #include <hip/hip_ext.h>
 
+#include "grad.h"
 #include "mbk.h"
 
 #include <float.h>
@@ -25,13 +26,6 @@ namespace mbk {
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ float clampf(float x, float lo, float hi) {
-    return fminf(fmaxf(x, lo), hi);
-}
-
-// exp evaluated in double and rounded to float once; the oracle does the same.
-__device__ __forceinline__ float exp_via_double(float x) { return (float)exp((double)x); }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
@@ -83,37 +77,6 @@ __device__ __forceinline__ float split_gain(float gl, float hl, float gr, float 
     float a = (gl * gl) / (hl + lambda);
     float b = (gr * gr) / (hr + lambda);
     return (a + b) - parent;
-}
-
-// (g, h) of one row for objective `obj` (Shaders.swift:105-135).
-__device__ __forceinline__ void row_grad(const GradParams &gp, float f, float y, float w, float &g,
-                                         float &h) {
-    switch (gp.objective) {
-    case 1: {
-        float q = 1.0f / (1.0f + exp_via_double(-f));
-        float ww = y > 0.5f ? gp.aux : 1.0f;
-        g = (q - y) * ww;
-        h = fmaxf(q * (1.0f - q), 1e-6f) * ww;
-        break;
-    }
-    case 2: g = f > y ? 1.0f : -1.0f; h = 1.0f; break;
-    case 3: g = clampf(f - y, -gp.alpha, gp.alpha); h = 1.0f; break;
-    case 4: g = f > y ? (1.0f - gp.alpha) : -gp.alpha; h = 1.0f; break;
-    case 5: {
-        float mu = exp_via_double(clampf(f, -30.0f, 30.0f));
-        g = mu - y; h = fmaxf(mu, 1e-6f);
-        break;
-    }
-    case 6: {
-        float fc = clampf(f, -30.0f, 30.0f);
-        float e2 = exp_via_double((2.0f - gp.aux) * fc), e1 = exp_via_double((1.0f - gp.aux) * fc);
-        g = e2 - y * e1;
-        h = fmaxf((2.0f - gp.aux) * e2 - (1.0f - gp.aux) * y * e1, 1e-6f);
-        break;
-    }
-    default: g = f - y; h = 1.0f; break;
-    }
-    if (gp.has_weights) { g *= w; h *= w; }
 }
 
 // (g, h) of row i, multiclass included: the softmax gradient of class
@@ -687,6 +650,12 @@ hipError_t launch_grad_max(hipStream_t s, const GradParams &gp, const float *pre
     hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(GRAD_THREADS), 0, s, gp, preds, labels,
                        weights, rows, partial, g_out, h_out);
     hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(64), 0, s, partial, blocks, ctl);
+    return hipGetLastError();
+}
+
+hipError_t launch_grad_max_final(hipStream_t s, const uint32_t *partial, int nparts,
+                                 TreeCtl *ctl) {
+    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(64), 0, s, partial, nparts, ctl);
     return hipGetLastError();
 }
 
@@ -1985,19 +1954,20 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         // still fit the same item budget (binary search between the lower
         // bound total / budget and c, which fits); each pair then splits its
         // rows into equal chunks of at most c'.
-        const uint64_t n = (uint32_t)tid < num_pairs ? s_cnt[tid] : 0u;
-        const uint64_t T = (uint64_t)sh.num_tiles;
-        const uint64_t K = item_budget(s_total, num_pairs, sh.num_tiles, target_items) / T;
-        uint64_t hi = s_chunk;
-        uint64_t lo = ((uint64_t)s_total + K - 1) / K;
+        // (32-bit arithmetic: 64-bit divisions in the loop cost microseconds)
+        const uint32_t n = (uint32_t)tid < num_pairs ? s_cnt[tid] : 0u;
+        const uint32_t K = (uint32_t)(item_budget(s_total, num_pairs, sh.num_tiles,
+                                                  target_items) / (uint64_t)sh.num_tiles);
+        uint32_t hi = s_chunk;
+        uint32_t lo = s_total / K + (s_total % K != 0u);
         if (lo < min_chunk) lo = min_chunk;
         if (lo > hi) lo = hi;
         while (lo < hi) {                            // uniform across the wavefront
-            const uint64_t mid = lo + (hi - lo) / 2;
-            const uint64_t k = (n + mid - 1) / mid;
-            if (wave_sum(k) <= K) hi = mid; else lo = mid + 1;
+            const uint32_t mid = lo + (hi - lo) / 2;
+            const uint32_t q = n / mid;
+            if (wave_sum(q + (n - q * mid != 0u)) <= K) hi = mid; else lo = mid + 1;
         }
-        if (tid == 0) s_chunk = (uint32_t)lo;
+        if (tid == 0) s_chunk = lo;
     }
     __syncthreads();
     const uint32_t chunk = s_chunk;

@@ -440,6 +440,19 @@ hipError_t launch_predict_binned(hipStream_t s, const uint8_t *bins_fm, int64_t 
 hipError_t launch_walk_count(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
                              int32_t num_bins, int32_t max_depth, const TreeOut tree,
                              float *preds, uint32_t *count, const uint8_t *kept);
+// The same walk (preds required; single-output objectives) that also starts
+// the next tree's gradient pass on the updated predictions: *partials pairs
+// of (max |g|, max h) into gpart (at most grad_max_scratch_words() / 2), and,
+// with g_out / h_out, every row's g and h.  launch_grad_max_final then takes
+// the place of launch_grad_max.
+hipError_t launch_walk_count_grad(hipStream_t s, const uint8_t *bins_fm, int64_t rows,
+                                  int32_t num_bins, int32_t max_depth, const TreeOut tree,
+                                  float *preds, uint32_t *count, const uint8_t *kept,
+                                  const GradParams &gp, const float *labels,
+                                  const float *weights, uint32_t *gpart, float *g_out,
+                                  float *h_out, int *partials);
+hipError_t launch_grad_max_final(hipStream_t s, const uint32_t *partial, int nparts,
+                                 TreeCtl *ctl);
 
 struct ShapPath {
     int32_t elem_start;   // first element

@@ -352,6 +352,9 @@ struct Trainer {
     // kept[i] of a sampled level-wise tree, for the terminal walk's counts
     DevBuf<uint8_t> kept;
     bool labels_ready = false;      // labels already uploaded during the setup
+    // gradient-maxima partials the last tree's walk left for the next tree
+    // (0: the next tree runs its own gradient pass)
+    int walk_gparts = 0;
     bool kept_walk = false;
     DevBuf<uint64_t> route_cursor;
     uint32_t route_grid = 1;
@@ -1401,9 +1404,16 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     hipStream_t s = t.dev->stream;
     const bool sampled = tree_sampled(t.p, tree);
     MB_HIP(mbk::launch_tree_init(s, ctl));
-    MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows, ctl,
-                                t.gmax_part.ptr, sampled ? t.samp_g.ptr : nullptr,
-                                sampled ? t.samp_h.ptr : nullptr));
+    if (t.walk_gparts > 0) {
+        // the previous tree's walk computed these gradients (and stored g, h
+        // for a sampled tree): only the maxima's final reduction is left
+        MB_HIP(mbk::launch_grad_max_final(s, t.gmax_part.ptr, t.walk_gparts, ctl));
+        t.walk_gparts = 0;
+    } else {
+        MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
+                                    ctl, t.gmax_part.ptr, sampled ? t.samp_g.ptr : nullptr,
+                                    sampled ? t.samp_h.ptr : nullptr));
+    }
     if (sampled)
         MB_HIP(mbk::launch_sample(s, sample_params(t, tree), t.rows, ctl, t.goss_buckets.ptr,
                                   t.gmax_part.ptr, t.samp_g.ptr, t.samp_h.ptr, order,
@@ -1412,6 +1422,27 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
         MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
                                     ctl, order));
     return sampled;
+}
+
+// The walk that adds tree `tree` to the training predictions (and counts its
+// deepest nodes' rows when count is non-null).  For single-output objectives
+// without leaf renewal it also computes the next tree's gradient maxima (and
+// g, h when that tree is sampled), so the next tree skips its own gradient
+// pass over the predictions and labels.
+static void training_walk(Trainer &t, int tree, const mbk::TreeOut &out, uint32_t *count,
+                          const uint8_t *kept) {
+    hipStream_t s = t.dev->stream;
+    if (t.K == 1 && !t.renewal) {
+        const bool next_sampled = tree_sampled(t.p, tree + 1);
+        MB_HIP(mbk::launch_walk_count_grad(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds_cur,
+                                           count, kept, t.gp, t.labels.ptr, t.weights.ptr,
+                                           t.gmax_part.ptr, next_sampled ? t.samp_g.ptr : nullptr,
+                                           next_sampled ? t.samp_h.ptr : nullptr,
+                                           &t.walk_gparts));
+    } else {
+        MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
+                                      t.renewal ? nullptr : t.preds_cur, count, kept));
+    }
 }
 
 static void grow_levelwise(Trainer &t, int tree) {
@@ -1465,9 +1496,7 @@ static void grow_levelwise(Trainer &t, int tree) {
             // Shaders.swift:1280-1311) and counts the deepest nodes' (kept) rows
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, false));
-            MB_HIP(mbk::launch_walk_count(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out,
-                                          t.renewal ? nullptr : t.preds_cur, t.count.ptr,
-                                          sampled ? t.kept.ptr : nullptr));
+            training_walk(t, tree, out, t.count.ptr, sampled ? t.kept.ptr : nullptr);
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
             if (t.renewal) {
                 // residuals before the tree (routing applies nothing), then
@@ -1565,8 +1594,12 @@ static void grow_leafwise(Trainer &t, int tree) {
     MB_HIP(mbk::launch_lw_eval(s, sh, t.sp, t.lw_state.ptr, t.lw_open.ptr, t.results.ptr,
                                t.node_g.ptr, t.node_h.ptr, ctl, out));
     // training predictions: walk the finished tree on the binned rows
-    // (predict_tree_binned, Shaders.swift:1763-1781)
-    MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds_cur));
+    // (predict_tree_binned, Shaders.swift:1763-1781); with leaf renewal the
+    // renewed leaves are added after it
+    if (t.renewal)
+        MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds_cur));
+    else
+        training_walk(t, tree, out, nullptr, nullptr);
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
                                           t.vpreds_cur));
