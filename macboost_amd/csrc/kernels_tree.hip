@@ -384,6 +384,36 @@ __device__ __forceinline__ uint32_t float_key(float v) {
     const uint32_t u = __float_as_uint(v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+
+// Wavefront max of unsigned values: DPP row shifts, then row broadcasts
+// (lane 63 holds the maximum), read back into every lane.
+__device__ __forceinline__ uint32_t wave_max_dpp(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x113, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xe, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xc, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// What a pick of node n needs: bit 0 expanded, bit 1 both children hold
+// rows; the children's candidate gains as ordered keys (0: none).
+struct LWBInfo {
+    uint32_t flags, kl, kr, pad;
+};
+// Order key of a gain (+0 and -0 alike, as the float comparisons see them).
+__device__ __forceinline__ uint32_t gain_key(float g) { return float_key(g == 0.0f ? 0.0f : g); }
+constexpr int LWB_EVAL = 4;   // nodes one wavefront evaluates at once
+
+// Open-mask words (one bit per candidate rank) for a tree of depth D.
+constexpr int lwb_mask_words(int depth) { return ((1 << (depth + 1)) - 1 + 63) / 64; }
+
+// Register slots per lane of the repeated-gain replay: an open list of up to
+// 2 * LWB_MAX_LEAVES entries.
+constexpr int LWB_SLOTS = (2 * LWB_MAX_LEAVES + 2 + 63) / 64;
+
 __device__ __forceinline__ float key_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
@@ -1869,19 +1899,20 @@ hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const Level
     return hipGetLastError();
 }
 
-__global__ void k_final_fixup(LevelArgs la, const uint32_t *count, TreeOut out) {
+__global__ void k_final_fixup(LevelArgs la, const uint32_t *count, TreeOut out,
+                              int zero_empty) {
     const uint32_t local = blockIdx.x * blockDim.x + threadIdx.x;
     if (local >= la.num_level) return;
     const uint32_t n = la.level_start + local;
     const uint32_t c = count[n];
     out.cover[n] = (float)c;
-    if (c == 0) out.leaf[n] = 0.0f;
+    if (c == 0 && zero_empty) out.leaf[n] = 0.0f;
 }
 
 hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,
-                              TreeOut out) {
+                              TreeOut out, bool zero_empty) {
     hipLaunchKernelGGL(k_final_fixup, dim3((la.num_level + 255) / 256), dim3(256), 0, s, la, count,
-                       out);
+                       out, zero_empty ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -3006,6 +3037,499 @@ hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, 
                                TreeCtl *ctl, Pair *pairs, HistItem *items, const TreeOut out) {
     hipLaunchKernelGGL(k_lw_route, dim3(a.part_blocks), dim3(PART_THREADS), 0, s, sh, a, st, open,
                        bins_fm, order, cursor, slot_seg, slot_count, ctl, pairs, items, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Leaf-wise growth in depth rounds.  The best-first loop (leaf_pick_apply,
+// :720-871) picks, among the open leaves with a valid candidate, the largest
+// gain (lowest open index on ties) until the tree has num_leaves leaves.  An
+// open leaf Y that n other open leaves beat can only be picked after all of
+// them, so it is never picked once n >= the picks left (num_leaves - leaves);
+// a node that is not open yet is beaten by every open leaf of equal gain.
+// Round r therefore expands (partitions, and builds its children's
+// histograms and splits) every evaluated depth-r node that fewer open leaves
+// beat than picks are left: a superset of the depth-r leaves the loop will
+// pick, and every pick is expanded in the round of its depth.  Each round's
+// select kernel replays the loop as far as the expanded nodes allow, so the
+// picks, their order and therefore the tree are those of the one-leaf loop.
+// Expanded nodes that are never picked cost work, not correctness: their
+// splits live only in the speculative tree the partition reads.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int heap_depth(uint32_t n) { return 31 - __clz((int)(n + 1)); }
+
+
+template <int NW>
+__global__ __launch_bounds__(1024) void k_lwb_select(
+    Shape sh, SplitParams sp, LWBArgs a, int32_t r, const SplitResult *__restrict__ results,
+    uint32_t *count, const int64_t *__restrict__ node_g,
+    const int64_t *__restrict__ node_h, float2 *bounds, const int8_t *__restrict__ monotone,
+    TreeCtl *ctl, uint64_t *cursors, LWBState *st, SplitResult *cand, TreeOut spec,
+    TreeOut out) {
+    __shared__ int32_t s_f[LWB_MAX_NODES], s_open[LWB_MAX_NODES];
+    __shared__ float s_gain[LWB_MAX_NODES];
+    __shared__ uint32_t s_cnt[LWB_MAX_NODES];
+    __shared__ float2 s_bounds[LWB_MAX_NODES];
+    __shared__ int32_t s_olist[2 * LWB_MAX_LEAVES + 2];
+    __shared__ uint32_t s_exp[(LWB_MAX_NODES + 31) / 32];
+    __shared__ int32_t s_seq[LWB_MAX_LEAVES];
+    __shared__ LWBInfo s_info[LWB_MAX_NODES];
+    __shared__ uint32_t s_keys[LWB_MAX_NODES];
+    __shared__ int32_t s_rank[LWB_MAX_NODES];
+    __shared__ uint2 s_rinfo[LWB_MAX_NODES];
+    __shared__ unsigned long long s_omask[NW];
+    __shared__ uint32_t s_dup;
+    __shared__ uint32_t s_state[5];                  // done, leaves, open count, picks, error
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6, nw = blockDim.x >> 6;
+    const int D = a.max_depth, L = a.num_leaves, F = sh.cols;
+    const int rr = r < D ? r : D;
+    const uint32_t M = (1u << (rr + 1)) - 1u;        // the nodes of depth <= r
+    const uint32_t level_start = (1u << rr) - 1u, level_n = 1u << rr;
+    const float msg = sp.min_split_gain;
+    auto valid = [&](int32_t f, float g) { return f >= 0 && isfinite(g) && g > msg; };
+    if (r == 0) {
+        // a new tree: every node a leaf of value 0, only the root open
+        for (int n = tid; n < a.total_nodes; n += blockDim.x) {
+            const NodeSplit leaf = {-1, 0, 0};
+            out.split[n] = leaf;
+            out.leaf[n] = 0.0f;
+            out.gain[n] = 0.0f;
+            out.cover[n] = 0.0f;
+        }
+        for (int k = tid; k < a.total_nodes * 8; k += blockDim.x) out.mask[k] = 0u;
+        for (uint32_t w = tid; w < (LWB_MAX_NODES + 31) / 32; w += blockDim.x) s_exp[w] = 0u;
+        if (tid == 0) {
+            s_f[0] = -1;
+            s_gain[0] = -INFINITY;
+            s_open[0] = 0;
+            s_olist[0] = 0;
+            s_cnt[0] = count[0];
+            s_bounds[0] = bounds[0];
+            s_state[0] = 0; s_state[1] = 1; s_state[2] = 1;
+        }
+    } else {
+        if (tid == 0) {
+            s_state[0] = st->done; s_state[1] = st->leaves; s_state[2] = st->open_count;
+        }
+        for (uint32_t n = tid; n < M; n += blockDim.x) {
+            const int32_t f = st->cand_f[n];
+            s_f[n] = f;
+            s_gain[n] = st->cand_gain[n];
+            s_open[n] = st->open[n];
+            s_cnt[n] = count[n];
+            s_bounds[n] = bounds[n];
+        }
+        for (uint32_t w = tid; w < (LWB_MAX_NODES + 31) / 32; w += blockDim.x)
+            s_exp[w] = st->expanded[w];
+    }
+    if (tid == 0) { s_state[3] = 0; s_state[4] = 0; }
+    __syncthreads();
+    const uint32_t oc0 = s_state[2];
+    for (uint32_t k = tid; r > 0 && k < oc0; k += blockDim.x) s_olist[k] = st->olist[k];
+    auto expanded = [&](uint32_t n) { return ((s_exp[n >> 5] >> (n & 31u)) & 1u) != 0; };
+    if (s_state[0]) {
+        // finished in an earlier round: nothing of this level is partitioned
+        for (uint32_t l = tid; r < D && l < level_n; l += blockDim.x) {
+            const NodeSplit leaf = {-1, 0, 0};
+            spec.split[level_start + l] = leaf;
+        }
+        return;                                      // uniform
+    }
+    const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
+    const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
+    // evaluate the depth-r nodes the last round built: argmax over features
+    // (strict '>', lowest feature wins).  A wavefront takes LWB_EVAL nodes at
+    // once, their gain loads in flight together; the argmax is two DPP
+    // maxima (gain key, then lowest feature).  The candidates themselves are
+    // copied with the state write-back.
+    for (uint32_t l0 = (uint32_t)wv; r < D && l0 < level_n; l0 += (uint32_t)nw * LWB_EVAL) {
+        uint32_t bk[LWB_EVAL], bfe[LWB_EVAL];
+        bool ev[LWB_EVAL];
+#pragma unroll
+        for (int u = 0; u < LWB_EVAL; ++u) {
+            const uint32_t l = l0 + (uint32_t)(u * nw);
+            ev[u] = l < level_n && (r == 0 || expanded((level_start + l - 1) >> 1));
+            bk[u] = 0u;
+            bfe[u] = 0u;
+        }
+        for (int f = lane; f < F; f += 64) {
+#pragma unroll
+            for (int u = 0; u < LWB_EVAL; ++u) {
+                if (!ev[u]) continue;
+                const float g = results[(size_t)(l0 + (uint32_t)(u * nw)) * F + f].gain;
+                const uint32_t k = g > -INFINITY ? gain_key(g) : 0u;   // NaN, -inf: none
+                if (k > bk[u]) { bk[u] = k; bfe[u] = (uint32_t)f; }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < LWB_EVAL; ++u) {
+            const uint32_t l = l0 + (uint32_t)(u * nw);
+            if (l >= level_n) continue;              // uniform
+            const uint32_t n = level_start + l;
+            int32_t bf = -1;
+            float bg = -INFINITY;
+            if (ev[u]) {
+                const uint32_t m = wave_max_dpp(bk[u]);
+                if (m) {
+                    bf = (int32_t)~wave_max_dpp(bk[u] == m ? ~bfe[u] : 0u);
+                    bg = key_float(m);
+                }
+            }
+            if (lane == 0) {
+                s_f[n] = bf;
+                s_gain[n] = bg;
+                if (n == 0)                          // the root's own leaf value
+                    out.leaf[0] = lw_leaf_value(sp, node_g[0], node_h[0], g_inv, h_inv,
+                                                s_bounds[0].x, s_bounds[0].y);
+            }
+        }
+    }
+    __syncthreads();
+    // Candidate ranks: valid candidates of depth <= r by gain key (largest
+    // first, node index on equal keys), 32 comparisons per work item;
+    // s_dup marks a repeated key.
+    for (uint32_t n = tid; n < M; n += blockDim.x) {
+        s_keys[n] = valid(s_f[n], s_gain[n]) ? gain_key(s_gain[n]) : 0u;
+        s_rank[n] = 0;
+    }
+    if (tid < NW) s_omask[tid] = 0ull;
+    if (tid == 0) s_dup = 0u;
+    __syncthreads();
+    {
+        constexpr uint32_t RC = 32;
+        const uint32_t chunks = (M + RC - 1) / RC;
+        for (uint32_t w = tid; w < M * chunks; w += blockDim.x) {
+            const uint32_t n = w / chunks, c0 = (w - n * chunks) * RC;
+            const uint32_t k = s_keys[n];
+            if (!k) continue;
+            uint32_t c = 0;
+            bool dup = false;
+#pragma unroll
+            for (uint32_t j = 0; j < RC; ++j) {
+                const uint32_t u = c0 + j;
+                const uint32_t ku = u < M ? s_keys[u] : 0u;
+                c += (ku > k || (ku == k && u < n)) ? 1u : 0u;
+                dup |= ku == k && u != n;
+            }
+            if (c) atomicAdd(&s_rank[n], (int32_t)c);
+            if (dup) s_dup = 1u;
+        }
+    }
+    __syncthreads();
+    // per rank: node and flags (bit 0 expanded), and the ranks a pick of it
+    // opens (0xFFFF: none; children open as candidates when they hold a
+    // valid candidate, are not at depth D and both hold rows)
+    for (uint32_t n = tid; n < M; n += blockDim.x) {
+        if (!s_keys[n]) continue;
+        const int32_t rk = s_rank[n];
+        uint32_t fl = 0u, rl = 0xFFFFu, rrk = 0xFFFFu;
+        if (expanded(n)) {
+            const uint32_t lc = 2 * n + 1, rc = lc + 1;
+            fl = 1u;
+            if (heap_depth(n) + 1 < D && s_cnt[lc] > 0 && s_cnt[rc] > 0) {
+                if (lc < M && s_keys[lc]) rl = (uint32_t)s_rank[lc];
+                if (rc < M && s_keys[rc]) rrk = (uint32_t)s_rank[rc];
+            }
+        }
+        s_rinfo[rk] = make_uint2(n | (fl << 16), rl | (rrk << 16));
+        if (s_open[n] >= 0) atomicOr(&s_omask[rk >> 6], 1ull << (rk & 63));
+    }
+    __syncthreads();
+    // replay the picks (one wavefront; only lane 0 writes LDS in the loops:
+    // the open list, for the next rounds and the expansion choice below)
+    if (wv == 0) {
+        uint32_t leaves = s_state[1], oc = s_state[2], nc = 0, done = 0, err = 0;
+        if (!s_dup) {
+            // no two candidates share a gain: the pick is the open candidate of
+            // lowest rank, the lowest set bit of the open mask (scalar
+            // registers); the loop records the picks, the open-list
+            // bookkeeping follows them below
+            uint64_t mk[NW];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const uint64_t v = s_omask[w];
+                mk[w] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+            }
+            for (;;) {
+                if ((int)leaves >= L) { done = 1; break; }
+                uint32_t p = 0xFFFFFFFFu;
+#pragma unroll
+                for (int w = NW - 1; w >= 0; --w)
+                    if (mk[w]) p = (uint32_t)(w * 64 + __builtin_ctzll(mk[w]));
+                if (p == 0xFFFFFFFFu) { done = 1; break; }
+                const uint2 q = s_rinfo[p];
+                const uint32_t q0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)q.x);
+                if (!(q0 & 0x10000u)) {
+                    // not partitioned yet: this round's expansion (its depth is r)
+                    if (heap_depth(q0 & 0xFFFFu) != rr || r >= D) { err = 1; done = 1; }
+                    break;
+                }
+                const uint32_t q1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)q.y);
+                const uint32_t rl = q1 & 0xFFFFu, rrk = q1 >> 16;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    if ((uint32_t)w == (p >> 6)) mk[w] &= ~(1ull << (p & 63));
+                    if ((uint32_t)w == (rl >> 6)) mk[w] |= 1ull << (rl & 63);   // none: no word
+                    if ((uint32_t)w == (rrk >> 6)) mk[w] |= 1ull << (rrk & 63);
+                }
+                if (lane == 0) s_seq[nc] = (int32_t)(q0 & 0xFFFFu);
+                leaves += 1;
+                nc += 1;
+            }
+        } else {
+            // repeated gains: open entry i lives in lane i % 64, register
+            // slot i / 64, as its gain key (0: not a valid candidate) and its
+            // node; a pick is the largest key, lowest index on equal keys (two
+            // DPP reductions); what a pick needs of its node comes from one
+            // LDS record written before the loop.
+            for (uint32_t n = (uint32_t)lane; n < M; n += 64) {
+                LWBInfo inf = {0u, 0u, 0u, 0u};
+                if (expanded(n)) {
+                    const uint32_t lc = 2 * n + 1, rc = lc + 1;
+                    inf.flags = 1u | ((s_cnt[lc] > 0 && s_cnt[rc] > 0) ? 2u : 0u);
+                    inf.kl = valid(s_f[lc], s_gain[lc]) ? gain_key(s_gain[lc]) : 0u;
+                    inf.kr = valid(s_f[rc], s_gain[rc]) ? gain_key(s_gain[rc]) : 0u;
+                }
+                s_info[n] = inf;
+            }
+            uint32_t ok[LWB_SLOTS];
+            int32_t on[LWB_SLOTS];
+#pragma unroll
+            for (int k = 0; k < LWB_SLOTS; ++k) {
+                const uint32_t i = (uint32_t)lane + 64u * k;
+                ok[k] = 0u;
+                on[k] = 0;
+                if (i < oc) {
+                    const int32_t n = s_olist[i];
+                    on[k] = n;
+                    if (s_open[n] == (int32_t)i && valid(s_f[n], s_gain[n]))
+                        ok[k] = gain_key(s_gain[n]);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (;;) {
+                if ((int)leaves >= L) { done = 1; break; }
+                const uint32_t slots = (oc + 63u) >> 6;   // uniform
+                uint32_t bk = 0u, bidx = 0u;
+#pragma unroll
+                for (int k = 0; k < LWB_SLOTS; ++k)
+                    if ((uint32_t)k < slots && ok[k] > bk) { bk = ok[k]; bidx = (uint32_t)lane + 64u * k; }
+                const uint32_t m = wave_max_dpp(bk);
+                if (m == 0u) { done = 1; break; }
+                const uint32_t bi = ~wave_max_dpp(bk == m ? ~bidx : 0u);
+                const uint32_t kb = bi >> 6, lb = bi & 63u;
+                int32_t xs = on[0];
+#pragma unroll
+                for (int k = 1; k < LWB_SLOTS; ++k)
+                    if ((uint32_t)k == kb) xs = on[k];
+                const int32_t x = __builtin_amdgcn_readlane(xs, (int)lb);
+                const LWBInfo inf = s_info[x];
+                if (!(inf.flags & 1u)) {
+                    // not partitioned yet: this round's expansion (its depth is r)
+                    if (heap_depth((uint32_t)x) != rr || r >= D) { err = 1; done = 1; }
+                    break;
+                }
+                const bool can_eval = heap_depth((uint32_t)x) + 1 < D && (int)leaves + 1 < L &&
+                                      (inf.flags & 2u);
+                const uint32_t kl = can_eval ? inf.kl : 0u, kr = can_eval ? inf.kr : 0u;
+                const int32_t lc = 2 * x + 1, rc = lc + 1;
+                const uint32_t ka = oc >> 6, la_ = oc & 63u, kb2 = (oc + 1) >> 6, lb2 = (oc + 1) & 63u;
+#pragma unroll
+                for (int k = 0; k < LWB_SLOTS; ++k) {
+                    if ((uint32_t)k == kb && (uint32_t)lane == lb) ok[k] = 0u;
+                    if ((uint32_t)k == ka && (uint32_t)lane == la_) { ok[k] = kl; on[k] = lc; }
+                    if ((uint32_t)k == kb2 && (uint32_t)lane == lb2) { ok[k] = kr; on[k] = rc; }
+                }
+                if (lane == 0) {
+                    if (!can_eval) { s_f[lc] = -1; s_f[rc] = -1; }
+                    s_open[x] = -2;
+                    s_open[lc] = (int32_t)oc;
+                    s_open[rc] = (int32_t)oc + 1;
+                    s_olist[oc] = lc;
+                    s_olist[oc + 1] = rc;
+                    s_seq[nc] = x;
+                }
+                oc += 2;
+                leaves += 1;
+                nc += 1;
+            }
+        }
+        if (!s_dup) oc += 2 * nc;                   // two children per pick
+        if (lane == 0) {
+            s_state[0] = done; s_state[1] = leaves; s_state[2] = oc; s_state[3] = nc;
+            s_state[4] = err;
+        }
+    }
+    __syncthreads();
+    if (!s_dup) {
+        // the fast replay's open-list bookkeeping: pick k appends its children
+        // at open entries oc0 + 2k and oc0 + 2k + 1 (children of a pick made
+        // with no evaluation left are not candidates), then every pick is
+        // marked split (after the appends: a pick may be an earlier child)
+        const uint32_t npk = s_state[3], leaves0 = s_state[1] - npk;
+        for (uint32_t k = tid; k < npk; k += blockDim.x) {
+            const int32_t x = s_seq[k], lc = 2 * x + 1, rc = lc + 1;
+            const uint32_t i = oc0 + 2 * k;
+            const bool can_eval = heap_depth((uint32_t)x) + 1 < D && (int)(leaves0 + k) + 1 < L &&
+                                  s_cnt[lc] > 0 && s_cnt[rc] > 0;
+            if (!can_eval) { s_f[lc] = -1; s_f[rc] = -1; }
+            s_open[lc] = (int32_t)i;
+            s_open[rc] = (int32_t)i + 1;
+            s_olist[i] = lc;
+            s_olist[i + 1] = rc;
+        }
+        __syncthreads();
+        for (uint32_t k = tid; k < npk; k += blockDim.x) s_open[s_seq[k]] = -2;
+        __syncthreads();
+    }
+    const uint32_t done = s_state[0], leaves = s_state[1], oc = s_state[2], nc = s_state[3];
+    // the picks' outputs, parents before children (monotone bounds pass down):
+    // split, gain and mask of the picked node, leaf values, bounds and covers
+    // of its children (Shaders.swift:1424-1443 for the bounds).  Thread k
+    // loads pick k's candidate once; the depth passes read bounds from LDS.
+    {
+        const bool mine = (uint32_t)tid < nc;
+        const int32_t x = mine ? s_seq[tid] : 0;
+        SplitResult c = {};
+        int64_t G = 0, H = 0;
+        int32_t bf = 0;
+        int cst = 0;
+        if (mine) {
+            c = cand[x];
+            G = node_g[x];
+            H = node_h[x];
+            bf = s_f[x];
+            cst = (c.flags & FLAG_CATEGORICAL) ? 0 : (int)monotone[bf];
+        }
+        const int dx = mine ? heap_depth((uint32_t)x) : -1;
+        for (int d = 0; d < rr; ++d) {
+            if (dx == d) {
+                const bool cat = (c.flags & FLAG_CATEGORICAL) != 0;
+                const NodeSplit ns = {bf, c.bin, c.flags};
+                out.split[x] = ns;
+                out.leaf[x] = 0.0f;
+                out.gain[x] = c.gain;
+                for (int w = 0; w < 8; ++w) out.mask[(size_t)x * 8 + w] = cat ? c.mask[w] : 0u;
+                const int64_t lg = c.gl_int, lh = c.hl_int, rg = G - c.gl_int, rh = H - c.hl_int;
+                const float2 pb = s_bounds[x];
+                float llo = pb.x, lhi = pb.y, rlo = pb.x, rhi = pb.y;
+                if (cst != 0) {
+                    const float vl = -c.gl / (c.hl + sp.lambda);
+                    const float gr = (float)rg * g_inv, hr = (float)rh * h_inv;
+                    const float vr = -gr / (hr + sp.lambda);
+                    const float mid = clampf(0.5f * (vl + vr), pb.x, pb.y);
+                    if (cst > 0) { lhi = fminf(lhi, mid); rlo = fmaxf(rlo, mid); }
+                    else { llo = fmaxf(llo, mid); rhi = fminf(rhi, mid); }
+                }
+                const int32_t lc = 2 * x + 1, rc = lc + 1;
+                out.leaf[lc] = lw_leaf_value(sp, lg, lh, g_inv, h_inv, llo, lhi);
+                out.leaf[rc] = lw_leaf_value(sp, rg, rh, g_inv, h_inv, rlo, rhi);
+                if (!(a.deep_walk && dx + 1 == D)) {     // else counted by the walk
+                    out.cover[lc] = (float)s_cnt[lc];
+                    out.cover[rc] = (float)s_cnt[rc];
+                }
+                s_bounds[lc] = make_float2(llo, lhi);
+                s_bounds[rc] = make_float2(rlo, rhi);
+                bounds[lc] = make_float2(llo, lhi);
+                bounds[rc] = make_float2(rlo, rhi);
+            }
+            __syncthreads();
+        }
+    }
+    if (r == 0 && tid == 0) out.cover[0] = (float)s_cnt[0];
+    if (r >= D && a.deep_walk)                       // the walk adds the deepest counts
+        for (uint32_t k = tid; k < (1u << D); k += blockDim.x) count[(1u << D) - 1 + k] = 0;
+    // the depth-r nodes to expand: evaluated, valid, and beaten by fewer open
+    // leaves than picks are left (ballots count the beating entries)
+    const int left_picks = L - (int)leaves;
+    for (uint32_t l = (uint32_t)wv; r < D && l < level_n; l += (uint32_t)nw) {
+        const uint32_t n = level_start + l;
+        const int32_t fy = s_f[n];
+        const float gy = s_gain[n];
+        bool take = false;
+        if (!done && valid(fy, gy)) {
+            const int32_t oy = s_open[n];
+            int beat = 0;
+            for (uint32_t i0 = 0; i0 < oc; i0 += 64) {
+                const uint32_t i = i0 + (uint32_t)lane;
+                bool b = false;
+                if (i < oc) {
+                    const int32_t z = s_olist[i];
+                    if (z != (int32_t)n && s_open[z] == (int32_t)i) {
+                        const float gz = s_gain[z];
+                        b = valid(s_f[z], gz) &&
+                            (gz > gy || (gz == gy && (oy < 0 || (int32_t)i < oy)));
+                    }
+                }
+                beat += __popcll(__ballot(b));
+            }
+            take = beat < left_picks;
+        }
+        if (lane == 0) {
+            NodeSplit ns = {-1, 0, 0};
+            if (take) {
+                const SplitResult &c = results[(size_t)l * F + fy];
+                ns = NodeSplit{fy, c.bin, c.flags};
+                const bool cat = (c.flags & FLAG_CATEGORICAL) != 0;
+                for (int w = 0; w < 8; ++w) spec.mask[(size_t)n * 8 + w] = cat ? c.mask[w] : 0u;
+                atomicOr(&s_exp[n >> 5], 1u << (n & 31u));
+            }
+            spec.split[n] = ns;
+            cursors[(size_t)l * CURSOR_STRIDE] = 0;  // the level's partition starts at zero
+        }
+    }
+    __syncthreads();
+    // keep the state for the next round (a new tree writes every node)
+    const uint32_t keep = r == 0 ? (uint32_t)a.total_nodes : M;
+    for (uint32_t n = tid; n < keep; n += blockDim.x) {
+        st->cand_f[n] = n < M ? s_f[n] : -1;
+        st->cand_gain[n] = n < M ? s_gain[n] : -INFINITY;
+        st->open[n] = n < M ? s_open[n] : -1;
+    }
+    for (uint32_t k = tid; k < oc; k += blockDim.x) st->olist[k] = s_olist[k];
+    // the evaluated depth-r candidates, a word per thread
+    constexpr uint32_t CW = sizeof(SplitResult) / sizeof(uint32_t);
+    for (uint32_t k = tid; r < D && k < level_n * CW; k += blockDim.x) {
+        const uint32_t l = k / CW, w = k - l * CW, n = level_start + l;
+        const int32_t f = s_f[n];
+        if (f >= 0)
+            reinterpret_cast<uint32_t *>(cand + n)[w] =
+                reinterpret_cast<const uint32_t *>(results + (size_t)l * F + f)[w];
+    }
+    for (uint32_t w = tid; w < (LWB_MAX_NODES + 31) / 32; w += blockDim.x)
+        st->expanded[w] = s_exp[w];
+    if (tid == 0) {
+        st->done = (done || r >= D) ? 1u : 0u;
+        st->leaves = leaves;
+        st->open_count = oc;
+        if (s_state[4]) ctl->overflow = LWB_MISSED_PICK;
+    }
+}
+
+hipError_t launch_lwb_select(hipStream_t s, const Shape &sh, const SplitParams &sp,
+                             const LWBArgs &a, int32_t round, const SplitResult *results,
+                             uint32_t *count, const int64_t *node_g, const int64_t *node_h,
+                             float2 *bounds, const int8_t *monotone, TreeCtl *ctl,
+                             uint64_t *cursors, LWBState *st, SplitResult *cand,
+                             const TreeOut spec, const TreeOut out) {
+    if (a.max_depth < 1 || a.max_depth > LWB_MAX_DEPTH || a.num_leaves < 2 ||
+        a.num_leaves > LWB_MAX_LEAVES || a.total_nodes != (1 << (a.max_depth + 1)) - 1 ||
+        round < 0 || round > a.max_depth)
+        return hipErrorInvalidValue;
+    // the open mask's words: as few as the tree's nodes allow
+    const int words = lwb_mask_words(a.max_depth);
+#define MBK_LWB_SELECT(W)                                                                     \
+    hipLaunchKernelGGL(k_lwb_select<W>, dim3(1), dim3(1024), 0, s, sh, sp, a, round, results, \
+                       count, node_g, node_h, bounds, monotone, ctl, cursors, st, cand, spec, out)
+    if (words <= 1) MBK_LWB_SELECT(1);
+    else if (words <= 2) MBK_LWB_SELECT(2);
+    else if (words <= 4) MBK_LWB_SELECT(4);
+    else MBK_LWB_SELECT(lwb_mask_words(LWB_MAX_DEPTH));
+#undef MBK_LWB_SELECT
     return hipGetLastError();
 }
 

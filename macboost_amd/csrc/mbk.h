@@ -310,8 +310,10 @@ hipError_t launch_final_leaves(hipStream_t s, const SplitParams &sp, const Level
                                uint32_t *count, const int64_t *node_g,
                                const int64_t *node_h, const float2 *bounds,
                                const TreeCtl *ctl, TreeOut out, bool counted);
+// Covers of the level's nodes from count; with zero_empty, empty nodes' leaves
+// become 0.
 hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,
-                              TreeOut out);
+                              TreeOut out, bool zero_empty = true);
 
 // Leaf renewal of the L1 / quantile objectives for one finished tree: the
 // sampled rows' residual quantiles replace its leaf values in place.  Scratch:
@@ -415,6 +417,43 @@ hipError_t launch_lw_partition(hipStream_t s, const Shape &sh, const LWArgs &a, 
                                LWOpen *open, const uint8_t *bins_fm, Entry *order,
                                uint64_t *cursor, uint32_t *slot_seg, uint32_t *slot_count,
                                TreeCtl *ctl, Pair *pairs, HistItem *items, const TreeOut out);
+
+// Leaf-wise growth in depth rounds (trees of depth <= LWB_MAX_DEPTH).  Round r
+// builds, for every depth-r leaf that can still be picked, its partition and
+// its children's histograms and splits, with the level-wise kernels on a
+// speculative tree; a single-block select kernel replays the best-first picks
+// over the evaluated candidates and writes the picked nodes into the tree.
+constexpr int LWB_MAX_DEPTH = 8;
+constexpr int LWB_MAX_NODES = (1 << (LWB_MAX_DEPTH + 1)) - 1;
+constexpr int LWB_MAX_LEAVES = 1 << LWB_MAX_DEPTH;
+constexpr uint32_t LWB_MISSED_PICK = 2;   // TreeCtl::overflow: a pick was never expanded
+
+struct LWBState {
+    uint32_t done, leaves, open_count, pad;
+    int32_t cand_f[LWB_MAX_NODES];            // best feature of an evaluated node, -1 none
+    float cand_gain[LWB_MAX_NODES];           // its gain
+    int32_t open[LWB_MAX_NODES];              // open-list index; -1 not open, -2 split
+    int32_t olist[2 * LWB_MAX_LEAVES + 2];    // node at each open-list index
+    uint32_t expanded[(LWB_MAX_NODES + 31) / 32];   // bit per node: partitioned, children built
+};
+
+struct LWBArgs {
+    int32_t num_leaves;         // L <= LWB_MAX_LEAVES
+    int32_t max_depth;          // D <= LWB_MAX_DEPTH
+    int32_t total_nodes;        // 2^(D+1) - 1
+    int32_t deep_walk;          // 1: the training walk counts the depth-D rows (the last
+                                // round partitions nothing); round D zeroes their counts
+};
+
+// Round r < D: evaluate the depth-r nodes the last round built, replay the
+// picks, choose the depth-r nodes to expand (their splits into spec, their
+// level's partition cursors zeroed).  Round D: the remaining picks.
+hipError_t launch_lwb_select(hipStream_t s, const Shape &sh, const SplitParams &sp,
+                             const LWBArgs &a, int32_t round, const SplitResult *results,
+                             uint32_t *count, const int64_t *node_g, const int64_t *node_h,
+                             float2 *bounds, const int8_t *monotone, TreeCtl *ctl,
+                             uint64_t *cursors, LWBState *st, SplitResult *cand,
+                             const TreeOut spec, const TreeOut out);
 
 // Inference.
 struct ForestDev {

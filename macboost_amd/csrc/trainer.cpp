@@ -385,6 +385,15 @@ struct Trainer {
     mbk::LWArgs lw{};
     DevBuf<mbk::LWState> lw_state;
     DevBuf<mbk::LWOpen> lw_open;
+    // leaf-wise growth in depth rounds: the select state, the evaluated
+    // candidates per node and the speculative tree the partition reads
+    bool lw_rounds = false;
+    mbk::LWBArgs lwb{};
+    DevBuf<mbk::LWBState> lwb_state;
+    DevBuf<mbk::SplitResult> lwb_cand;
+    DevBuf<mbk::NodeSplit> spec_split;
+    DevBuf<float> spec_cover;
+    DevBuf<uint32_t> spec_mask;
     DevBuf<mbk::NodeSplit> m_split;
     DevBuf<float> m_leaf, m_gain, m_cover;
     DevBuf<uint32_t> m_mask;
@@ -979,12 +988,29 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.partials.alloc((size_t)max_items * (size_t)tile_w * (size_t)p.num_bins);
     t.items.alloc((size_t)max_items);
     t.pairs.alloc((size_t)t.max_level_nodes);
-    // level-wise: two levels of max_level_nodes histograms; leaf-wise: one
-    // slot per evaluated leaf (at most num_leaves)
-    const size_t slots = t.leafwise ? (size_t)p.num_leaves : (size_t)t.max_level_nodes;
+    // Leaf-wise trees up to depth LWB_MAX_DEPTH grow in depth rounds on the
+    // level-wise buffers, unless two levels of histograms would pass 4 GiB
+    const size_t level_hist_bytes =
+        (size_t)t.max_level_nodes * cols * p.num_bins * 2 * sizeof(int64_t);
+    t.lw_rounds = t.leafwise && t.D <= mbk::LWB_MAX_DEPTH &&
+                  p.num_leaves <= mbk::LWB_MAX_LEAVES && 2 * level_hist_bytes <= ((size_t)4 << 30);
+    // level-wise (and leaf-wise rounds): two levels of max_level_nodes
+    // histograms; leaf-wise steps: one slot per evaluated leaf (at most num_leaves)
+    const bool level_bufs = !t.leafwise || t.lw_rounds;
+    const size_t slots = level_bufs ? (size_t)t.max_level_nodes : (size_t)p.num_leaves;
     const size_t hist_n = slots * cols * p.num_bins * 2;
     t.hist_a.alloc(hist_n);
-    if (!t.leafwise) t.hist_b.alloc(hist_n);
+    if (level_bufs) t.hist_b.alloc(hist_n);
+    if (t.lw_rounds) {
+        t.lwb.num_leaves = p.num_leaves;
+        t.lwb.max_depth = t.D;
+        t.lwb.total_nodes = t.total_nodes;
+        t.lwb_state.alloc(1);
+        t.lwb_cand.alloc((size_t)t.total_nodes);
+        t.spec_split.alloc((size_t)t.total_nodes);
+        t.spec_cover.alloc((size_t)t.total_nodes);
+        t.spec_mask.alloc((size_t)t.total_nodes * 8);
+    }
     t.results.alloc(std::max(slots, (size_t)t.max_level_nodes) * cols);
     if (t.leafwise) {
         t.lw.num_leaves = p.num_leaves;
@@ -1549,6 +1575,9 @@ static void grow_levelwise(Trainer &t, int tree) {
                           hipMemcpyDeviceToDevice, s));
 }
 
+static void finish_leafwise(Trainer &t, int tree, const mbk::TreeOut &out,
+                            bool deep_counts = false);
+
 // Best-first growth (growLeafWiseTree, Booster.swift:967-1310): root
 // histogram and split, then numLeaves-1 steps of pick -> partition -> smaller
 // child's histogram -> sibling by subtraction -> children's best splits.
@@ -1593,20 +1622,34 @@ static void grow_leafwise(Trainer &t, int tree) {
     }
     MB_HIP(mbk::launch_lw_eval(s, sh, t.sp, t.lw_state.ptr, t.lw_open.ptr, t.results.ptr,
                                t.node_g.ptr, t.node_h.ptr, ctl, out));
+    if (t.renewal) MB_HIP(mbk::launch_lw_bounds(s, t.lw_state.ptr, t.lw_open.ptr, t.bounds.ptr));
+    finish_leafwise(t, tree, out);
+}
+
+// A finished leaf-wise tree: training (and validation) predictions, leaf
+// renewal, the tree's control block.  t.bounds holds every leaf's bounds.
+// With deep_counts (no renewal) the walk also counts the rows of the
+// depth-D nodes (zeroed before) and writes their covers.
+static void finish_leafwise(Trainer &t, int tree, const mbk::TreeOut &out, bool deep_counts) {
+    hipStream_t s = t.dev->stream;
     // training predictions: walk the finished tree on the binned rows
     // (predict_tree_binned, Shaders.swift:1763-1781); with leaf renewal the
     // renewed leaves are added after it
-    if (t.renewal)
+    if (t.renewal) {
         MB_HIP(mbk::launch_predict_binned(s, t.bins_fm.ptr, t.rows, t.nb, t.D, out, t.preds_cur));
-    else
-        training_walk(t, tree, out, nullptr, nullptr);
+    } else {
+        training_walk(t, tree, out, deep_counts ? t.count.ptr : nullptr, nullptr);
+        if (deep_counts) {
+            const mbk::LevelArgs ld{t.D, (uint32_t)((1u << t.D) - 1), 1u << t.D, 1u};
+            MB_HIP(mbk::launch_final_fixup(s, ld, t.count.ptr, out, false));
+        }
+    }
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
                                           t.vpreds_cur));
     if (t.renewal) {
         // residuals after the tree's first leaf values, then each leaf's
         // change is added (Booster.swift:1253-1290)
-        MB_HIP(mbk::launch_lw_bounds(s, t.lw_state.ptr, t.lw_open.ptr, t.bounds.ptr));
         renew_tree(t, out, t.rn_delta.ptr);
         mbk::TreeOut dout = out;
         dout.leaf = t.rn_delta.ptr;
@@ -1616,8 +1659,83 @@ static void grow_leafwise(Trainer &t, int tree) {
             MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, dout,
                                               t.vpreds_cur));
     }
-    MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
+    MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, t.ctl.ptr, sizeof(mbk::TreeCtl),
                           hipMemcpyDeviceToDevice, s));
+}
+
+// Leaf-wise growth in depth rounds (trees of depth <= LWB_MAX_DEPTH): the
+// level-wise chain of partition, planning, histograms and split search, over
+// a speculative tree that each round's select kernel fills with the depth-r
+// leaves the best-first loop may still pick (leaf_pick_apply and leaf_step,
+// Shaders.swift:720-1091); the select kernels write the picked nodes into
+// the tree, so it equals the one-leaf-per-step tree.
+static void grow_leafwise_rounds(Trainer &t, int tree) {
+    hipStream_t s = t.dev->stream;
+    const mbk::Shape &sh = t.sh;
+    mbk::TreeOut out = t.tree_out(tree);
+    if (const uint8_t *m = tree_feature_mask(t, tree))
+        MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
+    mbk::TreeCtl *ctl = t.ctl.ptr;
+    const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr);
+    mbk::TreeOut spec{t.spec_split.ptr, t.spec_cover.ptr, t.spec_cover.ptr, t.spec_cover.ptr,
+                      t.spec_mask.ptr};
+    MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
+                                 (uint32_t)t.target_items, (uint32_t)t.min_chunk, ctl, t.seg_a.ptr,
+                                 t.count.ptr, t.pairs.ptr, t.items.ptr, spec.cover, t.bounds.ptr,
+                                 -INFINITY, INFINITY));
+    // the two halves of the leaf-wise order buffer alternate by depth
+    mbk::Entry *ord_cur = t.order_a.ptr, *ord_next = t.order_a.ptr + t.rows;
+    uint32_t *seg_cur = t.seg_a.ptr, *seg_next = t.seg_b.ptr;
+    int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
+    auto hist = [&](const mbk::Entry *ord, int level) {
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (t.profiling) {
+            MB_HIP(hipEventCreate(&e0));
+            MB_HIP(hipEventCreate(&e1));
+        }
+        const bool planar = level == 0 && !sampled && t.has_root_copy;
+        MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
+                                t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
+                                planar ? &t.root_layout : nullptr, e0, e1));
+        if (t.profiling) t.events.push_back({e0, e1, level});
+    };
+    // unsampled trees without renewal: the training walk counts the deepest
+    // rows, so the last round partitions nothing
+    mbk::LWBArgs la = t.lwb;
+    la.deep_walk = !sampled && !t.renewal ? 1 : 0;
+    auto select = [&](int round) {
+        MB_HIP(mbk::launch_lwb_select(s, sh, t.sp, la, round, t.results.ptr, t.count.ptr,
+                                      t.node_g.ptr, t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl,
+                                      t.route_cursor.ptr, t.lwb_state.ptr, t.lwb_cand.ptr, spec,
+                                      out));
+    };
+    hist(ord_cur, 0);
+    MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
+                             t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
+                             t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
+    for (int r = 0; r < t.D; ++r) {
+        const bool last = r + 1 == t.D;
+        select(r);
+        if (last && la.deep_walk) break;
+        mbk::LevelArgs lp{r, (uint32_t)((1u << r) - 1), 1u << r, last ? 1u : 0u};
+        mbk::LevelArgs ln{r + 1, (uint32_t)((1u << (r + 1)) - 1), 1u << (r + 1), last ? 1u : 0u};
+        // the deepest children are never evaluated: count them, move nothing
+        MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
+                                 t.count.ptr, spec, t.route_cursor.ptr, t.route_grid, !last));
+        MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
+                                      ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr,
+                                      spec, t.pairs.ptr, t.items.ptr));
+        if (last) break;
+        std::swap(ord_cur, ord_next);
+        std::swap(seg_cur, seg_next);
+        std::swap(h_cur, h_prev);
+        hist(ord_cur, r + 1);
+        MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1u << r, t.partials.ptr, h_prev, h_cur,
+                                 t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
+                                 t.node_g.ptr, t.node_h.ptr, ln.level_start, t.results.ptr));
+    }
+    select(t.D);
+    finish_leafwise(t, tree, out, la.deep_walk != 0);
 }
 
 void trainer_grow(Trainer *tp, int num_trees) {
@@ -1639,7 +1757,8 @@ void trainer_grow(Trainer *tp, int num_trees) {
         t.gp.class_index = cls;
         t.preds_cur = t.preds.ptr + (size_t)cls * (size_t)t.rows;
         t.vpreds_cur = t.has_valid ? t.vpreds.ptr + (size_t)cls * (size_t)t.vrows : nullptr;
-        if (t.leafwise) grow_leafwise(t, tree);
+        if (t.lw_rounds) grow_leafwise_rounds(t, tree);
+        else if (t.leafwise) grow_leafwise(t, tree);
         else grow_levelwise(t, tree);
         t.grown += 1;
         // metrics once per round of K trees (Booster.swift:1650-1688)
@@ -1699,7 +1818,9 @@ void trainer_grow(Trainer *tp, int num_trees) {
         MB_HIP(hipMemcpy(c.data(), t.ctl_hist.ptr + first_tree, c.size() * sizeof(mbk::TreeCtl),
                          hipMemcpyDeviceToHost));
         for (const auto &e : c)
-            if (e.overflow) internal("histogram item list overflow");
+            if (e.overflow == mbk::LWB_MISSED_PICK)
+                internal("leaf-wise rounds: a picked leaf was never expanded");
+            else if (e.overflow) internal("histogram item list overflow");
     }
     if (t.profiling) {
         for (auto &e : t.events) {

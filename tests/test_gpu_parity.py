@@ -969,6 +969,25 @@ def test_leafwise_identical_trees(num_leaves, depth):
                            "num_bins": 128}, x_test=xt)
 
 
+@pytest.mark.parametrize("num_leaves", [5, 11, 23])
+def test_leafwise_equal_gains_identical(num_leaves):
+    # Two mirrored halves: the same rows, a flag feature that is 0 in one half
+    # and 1 in the other, and integer labels reflected about their mean, so
+    # every L2 gradient of one half is exactly the negation of its twin's.
+    # The root splits on the flag and every node of one subtree has a twin of
+    # exactly equal gain: the best-first picks break ties by open-list order
+    # (5 and 11 leaves end with one more split on the left side than the right).
+    rng = np.random.default_rng(2024)
+    n, c = 3000, 40
+    xa = rng.random((5, n), dtype=np.float32)
+    ya = np.round(12 * xa[0] + 6 * xa[1] ** 2 + rng.integers(0, 3, n)).astype(np.float32)
+    x = np.concatenate([np.concatenate([xa, xa], axis=1),
+                        np.concatenate([np.zeros(n), np.ones(n)])[None].astype(np.float32)])
+    y = np.concatenate([ya, 2 * c - ya]).astype(np.float32)
+    check_identical(np.ascontiguousarray(x), y, {"num_trees": 6, "max_depth": 6,
+                                                 "num_leaves": num_leaves, "num_bins": 64})
+
+
 def test_leafwise_nan_categorical_monotone_identical():
     x, y = _mixed(12_000)
     params = {"num_trees": 20, "max_depth": 6, "num_leaves": 24, "categorical_features": [6],
