@@ -313,8 +313,9 @@ int mbx_trainer_level_stats(void *trainer, int32_t max_levels, int64_t *built, i
 int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err);
 int mbx_context_hist_stats(mbk_context *ctx, int32_t max_levels, int64_t *launches, double *ms,
                            double *bytes, int64_t *built, double *level_ms, char **err);
-/* Wall-clock seconds of the last mbx_trainer_create phases: edges (host),
- * upload + device binning. */
+/* Wall-clock seconds of the last mbx_trainer_create phases: edges_s the
+ * device quantile edges and binning (the label upload overlaps them), bin_s
+ * the upload of host features before them (0 for device features). */
 int mbx_trainer_setup_seconds(void *trainer, double *edges_s, double *bin_s);
 /* Finish training: read the trees back and return a booster handle usable
  * by every Part 1 call (free it with macboost_free).  The trainer stays

@@ -174,8 +174,16 @@ void validate_params(const Params &p) {
 // ---------------------------------------------------------------------------
 
 Device &Booster::device() {
-    if (!dev) dev = std::make_unique<Device>(0);
+    if (!dev) dev = acquire_device(0);
     return *dev;
+}
+
+Booster::~Booster() {
+    if (!dev) return;
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipStreamSynchronize(dev->copy_stream);
+    forest = ForestCache();                          // its buffers before the device goes
+    release_device(std::move(dev));
 }
 
 void Booster::build_forest() {                    // forestBuffers, Booster.swift:1950-1985

@@ -112,6 +112,12 @@ struct Device {
     Device &operator=(const Device &) = delete;
 };
 
+// A device with idle streams: one an earlier owner handed back, or a new one
+// (the calling thread's current device is set either way).
+std::unique_ptr<Device> acquire_device(int device_id);
+// Hands a device back for reuse; both its streams must be idle.
+void release_device(std::unique_ptr<Device> d);
+
 // Host -> device copy of a pageable buffer on stream s.  Copies of 4 MB or
 // more go through pinned staging (in at least four pieces, host fills
 // overlapping the DMA) and have completed on return; smaller ones are one
@@ -211,6 +217,10 @@ struct Booster {
     std::unique_ptr<Device> dev;
     ForestCache forest;
 
+    Booster() = default;
+    Booster(const Booster &) = delete;
+    Booster &operator=(const Booster &) = delete;
+    ~Booster();
     Device &device();
     void build_forest();
     std::vector<float> predict(const float *x_fm, int64_t rows, int64_t cols);

@@ -7,10 +7,13 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <functional>
+#include <memory>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -26,31 +29,119 @@ int host_threads() {
     return (int)n;
 }
 
-// Runs fn(begin, end) over [0, n) in blocks of `block` items on up to
-// host_threads() threads (block b is [b*block, min(n, (b+1)*block))), and
-// waits; fn must only write what its own block owns.
+// Host worker threads for the block loops, started once (starting threads
+// per loop costs more than the loops over a few million labels).  A loop
+// runs on its calling thread and on idle workers, so loops from several
+// threads progress together.  The pool lives until the process ends.
+namespace {
+class HostPool {
+public:
+    static HostPool &get() {
+        static HostPool *pool = new HostPool(host_threads() - 1);
+        return *pool;
+    }
+    // fn(k) for every k in [0, count); returns once all have returned.  fn
+    // must not throw.
+    void run(int64_t count, const std::function<void(int64_t)> &fn) {
+        if (count <= 0) return;
+        if (count == 1 || threads_.empty()) {
+            for (int64_t k = 0; k < count; ++k) fn(k);
+            return;
+        }
+        auto job = std::make_shared<Job>();
+        job->count = count;
+        job->fn = &fn;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            jobs_.push_back(job);
+        }
+        cv_.notify_all();
+        work_on(*job);
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return job->finished.load() == job->count; });
+        jobs_.erase(std::find(jobs_.begin(), jobs_.end(), job));
+    }
+
+private:
+    struct Job {
+        int64_t count = 0;
+        const std::function<void(int64_t)> *fn = nullptr;
+        std::atomic<int64_t> next{0}, finished{0};
+    };
+    explicit HostPool(int workers) {
+        for (int k = 0; k < workers; ++k) threads_.emplace_back([this] { worker(); });
+    }
+    void work_on(Job &j) {
+        for (int64_t k = j.next++; k < j.count; k = j.next++) {
+            (*j.fn)(k);
+            if (++j.finished == j.count) {
+                std::lock_guard<std::mutex> lk(mu_);
+                done_cv_.notify_all();
+            }
+        }
+    }
+    std::shared_ptr<Job> open_job() {            // with mu_ held
+        for (auto &j : jobs_)
+            if (j->next.load() < j->count) return j;
+        return nullptr;
+    }
+    void worker() {
+        for (;;) {
+            std::shared_ptr<Job> j;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return (j = open_job()) != nullptr; });
+            }
+            work_on(*j);
+        }
+    }
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    std::vector<std::shared_ptr<Job>> jobs_;
+    std::vector<std::thread> threads_;
+};
+}  // namespace
+
+// Runs fn(begin, end) over [0, n) in blocks of `block` items on the host
+// pool (block b is [b*block, min(n, (b+1)*block))), and waits; fn must only
+// write what its own block owns.
 template <typename Fn>
 static void parallel_blocks(int64_t n, int64_t block, Fn fn) {
     const int64_t nblocks = (n + block - 1) / block;
-    const int nt = (int)std::min<int64_t>(host_threads(), nblocks);
-    if (nt <= 1) {
-        for (int64_t b = 0; b < nblocks; ++b) fn(b * block, std::min(n, (b + 1) * block));
-        return;
-    }
-    std::atomic<int64_t> next{0};
-    auto work = [&] {
-        for (int64_t b = next++; b < nblocks; b = next++) fn(b * block, std::min(n, (b + 1) * block));
+    const std::function<void(int64_t)> f = [&](int64_t b) {
+        fn(b * block, std::min(n, (b + 1) * block));
     };
-    std::vector<std::thread> ts;
-    for (int k = 1; k < nt; ++k) ts.emplace_back(work);
-    work();
-    for (auto &th : ts) th.join();
+    HostPool::get().run(nblocks, f);
 }
 
 // Rows per block of the sums over every row (base score): each block is
 // summed in row order in double, then the block sums in block order, so
 // the result does not depend on how blocks are spread over threads.
 constexpr int64_t SUM_BLOCK = 65536;
+
+// Per-block double sums (block k: rows [k*SUM_BLOCK, ...) in row order) of
+// two accumulators that add(i, a, b) updates, into s1[k], s2[k].  A task
+// takes four consecutive blocks and steps their rows together: four
+// independent addition chains in flight, each block's sum unchanged.
+template <typename Add>
+static void sum_blocks(int64_t n, double *s1, double *s2, Add add) {
+    constexpr int G = 4;
+    parallel_blocks(n, G * SUM_BLOCK, [&](int64_t a, int64_t b) {
+        double x[G] = {}, y[G] = {};
+        if (b - a == G * SUM_BLOCK) {
+            for (int64_t i = 0; i < SUM_BLOCK; ++i)
+                for (int j = 0; j < G; ++j) add(a + j * SUM_BLOCK + i, x[j], y[j]);
+        } else {                                     // the ragged last task
+            for (int j = 0; j < G; ++j)
+                for (int64_t i = a + j * SUM_BLOCK; i < std::min(b, a + (j + 1) * SUM_BLOCK); ++i)
+                    add(i, x[j], y[j]);
+        }
+        for (int j = 0; j < G && a + j * SUM_BLOCK < b; ++j) {
+            s1[(size_t)(a / SUM_BLOCK) + j] = x[j];
+            s2[(size_t)(a / SUM_BLOCK) + j] = y[j];
+        }
+    });
+}
 
 static double now_s() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch())
@@ -195,6 +286,36 @@ Device::~Device() {
     if (copy_stream) (void)hipStreamDestroy(copy_stream);
 }
 
+// Devices whose owners ended, kept with their streams for the next owner
+// (creating a stream costs about a millisecond).  The list is never torn
+// down: its streams live until the process ends.
+namespace {
+std::mutex g_dev_mu;
+std::vector<Device *> *g_dev_free = new std::vector<Device *>();
+}  // namespace
+
+std::unique_ptr<Device> acquire_device(int device_id) {
+    {
+        std::lock_guard<std::mutex> lock(g_dev_mu);
+        for (size_t k = 0; k < g_dev_free->size(); ++k) {
+            if ((*g_dev_free)[k]->id == device_id) {
+                Device *d = (*g_dev_free)[k];
+                (*g_dev_free)[k] = g_dev_free->back();
+                g_dev_free->pop_back();
+                MB_HIP(hipSetDevice(device_id));
+                return std::unique_ptr<Device>(d);
+            }
+        }
+    }
+    return std::make_unique<Device>(device_id);
+}
+
+void release_device(std::unique_ptr<Device> d) {
+    if (!d) return;
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    if (g_dev_free->size() < 16) g_dev_free->push_back(d.release());
+}
+
 // ---------------------------------------------------------------------------
 // Host -> device upload of large pageable buffers: two pinned staging buffers,
 // each filled by a few host threads while the other one's DMA is in flight.
@@ -216,14 +337,12 @@ Staging &staging() {
 }
 
 void parallel_copy(char *dst, const char *src, size_t n, unsigned threads) {
-    std::vector<std::thread> ts;
     const size_t per = (n + threads - 1) / threads;
-    for (unsigned t = 1; t < threads; ++t) {
+    const std::function<void(int64_t)> f = [&](int64_t t) {
         const size_t a = (size_t)t * per, b = std::min(n, a + per);
-        if (a < b) ts.emplace_back([=] { std::memcpy(dst + a, src + a, b - a); });
-    }
-    std::memcpy(dst, src, std::min(n, per));
-    for (auto &th : ts) th.join();
+        if (a < b) std::memcpy(dst + a, src + a, b - a);
+    };
+    HostPool::get().run((int64_t)threads, f);
 }
 
 // Both staging buffers, allocated on first use; false if pinned memory cannot
@@ -419,20 +538,34 @@ struct Trainer {
     double t_edges = 0.0, t_bin = 0.0;
 
     Trainer() {
-        // the per-row buffers come from the device memory cache: a fit of the
-        // same shape finds them there
-        for (DevBuf<uint8_t> *b : {&bins_tiled, &bins_fm, &vbins_fm, &bins_root, &kept})
+        // Every buffer of a fit comes from the device memory cache: a fit of
+        // the same shape finds them there (the model arrays are taken from it
+        // as they grow).
+        for (DevBuf<uint8_t> *b : {&bins_tiled, &bins_fm, &vbins_fm, &bins_root, &kept, &is_cat,
+                                   &feat_mask})
             b->pooled = true;
-        for (DevBuf<float> *b : {&labels, &weights, &preds, &vpreds, &samp_g, &samp_h, &samp_h_kept})
+        for (DevBuf<float> *b : {&labels, &weights, &preds, &vpreds, &samp_g, &samp_h,
+                                 &samp_h_kept, &rn_delta, &spec_cover})
             b->pooled = true;
+        for (DevBuf<uint32_t> *b : {&gmax_part, &goss_buckets, &count, &seg_a, &seg_b, &rn_leaf,
+                                    &rn_keys, &rn_seg, &rn_cnt, &rn_off, &rn_cursor, &spec_mask})
+            b->pooled = true;
+        for (DevBuf<int64_t> *b : {&hist_a, &hist_b, &node_g, &node_h}) b->pooled = true;
         order_a.pooled = order_b.pooled = partials.pooled = items.pooled = true;
-        hist_a.pooled = hist_b.pooled = true;
+        mono.pooled = route_cursor.pooled = pairs.pooled = results.pooled = true;
+        bounds.pooled = ctl.pooled = true;
+        lw_state.pooled = lw_open.pooled = lwb_state.pooled = lwb_cand.pooled = true;
+        spec_split.pooled = true;
     }
 
     ~Trainer() {
-        // cached blocks must be idle when they are handed back
-        if (dev && dev->stream) (void)hipStreamSynchronize(dev->stream);
+        // cached blocks and the device's streams must be idle when handed back
+        if (dev) {
+            if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+            if (dev->copy_stream) (void)hipStreamSynchronize(dev->copy_stream);
+        }
         for (auto &e : events) { (void)hipEventDestroy(e.start); (void)hipEventDestroy(e.end); }
+        release_device(std::move(dev));
     }
 
     mbk::TreeOut tree_out(int t) {
@@ -451,7 +584,9 @@ struct Trainer {
         int cap = std::max(n, capacity * 2);
         auto grow = [&](auto &buf, size_t per_tree) {
             using T = typename std::remove_reference<decltype(*buf.ptr)>::type;
-            DevBuf<T> nbuf((size_t)cap * per_tree);
+            DevBuf<T> nbuf;                             // the old block goes after the sync
+            nbuf.pooled = true;
+            nbuf.alloc((size_t)cap * per_tree);
             MB_HIP(hipMemsetAsync(nbuf.ptr, 0, nbuf.bytes(), dev->stream));
             if (buf.ptr && capacity)
                 MB_HIP(hipMemcpyAsync(nbuf.ptr, buf.ptr, (size_t)capacity * per_tree * sizeof(T),
@@ -494,21 +629,41 @@ static void check_label(const Params &p, const float *y, int64_t i) {
     }
 }
 
+// First row in [a, b) whose label check_label rejects, or -1: the same
+// rules as a plain predicate, so the scan runs without calls.
+template <int OBJ>
+static int64_t first_bad_label(const float *y, int64_t a, int64_t b, int num_classes) {
+    for (int64_t i = a; i < b; ++i) {
+        const float v = y[i];
+        bool ok = std::isfinite(v);
+        if (OBJ == OBJ_LOGISTIC) ok = ok && (v == 0.0f || v == 1.0f);
+        if (OBJ == OBJ_POISSON || OBJ == OBJ_TWEEDIE) ok = ok && v >= 0.0f;
+        if (OBJ == OBJ_MULTICLASS) {
+            const float r = std::nearbyint(v);
+            ok = ok && r == v && r >= 0.0f && (int64_t)r < num_classes;
+        }
+        if (!ok) return i;
+    }
+    return -1;
+}
+
 // Labels (Booster.swift:1724-1765), scanned in blocks on the host threads;
 // the first offending row over all blocks gets the message.
 static void validate_labels(const Params &p, const float *y, int64_t n) {
     const int64_t block = 1 << 18;
     const int64_t nblocks = (n + block - 1) / block;
     std::vector<int64_t> first((size_t)nblocks, -1);
+    const int obj = p.objective, nc = p.num_classes;
     parallel_blocks(n, block, [&](int64_t a, int64_t b) {
-        for (int64_t i = a; i < b; ++i) {
-            try {
-                check_label(p, y, i);
-            } catch (const Error &) {
-                first[(size_t)(a / block)] = i;
-                return;
-            }
+        int64_t f;
+        switch (obj) {
+        case OBJ_LOGISTIC: f = first_bad_label<OBJ_LOGISTIC>(y, a, b, nc); break;
+        case OBJ_POISSON: f = first_bad_label<OBJ_POISSON>(y, a, b, nc); break;
+        case OBJ_TWEEDIE: f = first_bad_label<OBJ_TWEEDIE>(y, a, b, nc); break;
+        case OBJ_MULTICLASS: f = first_bad_label<OBJ_MULTICLASS>(y, a, b, nc); break;
+        default: f = first_bad_label<-1>(y, a, b, nc); break;
         }
+        first[(size_t)(a / block)] = f;
     });
     for (int64_t f : first)
         if (f >= 0) check_label(p, y, f);
@@ -614,14 +769,9 @@ static float base_score(const Params &p, const float *y, const float *w, int64_t
     std::vector<double> s1((size_t)nblocks, 0.0), s2((size_t)nblocks, 0.0);
     if (p.objective == OBJ_LOGISTIC) {                     // :802-830
         const double spw = (double)p.scale_pos_weight;
-        parallel_blocks(n, SUM_BLOCK, [&](int64_t a, int64_t b) {
-            double pos = 0, tot = 0;
-            for (int64_t i = a; i < b; ++i) {
-                double wi = w ? (double)w[i] : 1.0;
-                if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
-            }
-            s1[(size_t)(a / SUM_BLOCK)] = pos;
-            s2[(size_t)(a / SUM_BLOCK)] = tot;
+        sum_blocks(n, s1.data(), s2.data(), [&](int64_t i, double &pos, double &tot) {
+            const double wi = w ? (double)w[i] : 1.0;
+            if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
         });
         double pos = 0, tot = 0;
         for (int64_t k = 0; k < nblocks; ++k) { pos += s1[(size_t)k]; tot += s2[(size_t)k]; }
@@ -629,15 +779,10 @@ static float base_score(const Params &p, const float *y, const float *w, int64_t
         pr = std::min(std::max(pr, 1e-6f), 1.0f - 1e-6f);
         return std::log(pr / (1.0f - pr));
     }
-    parallel_blocks(n, SUM_BLOCK, [&](int64_t a, int64_t b) {
-        double num = 0, den = 0;
-        for (int64_t i = a; i < b; ++i) {
-            double wi = w ? (double)w[i] : 1.0;
-            num += wi * (double)y[i];
-            den += wi;
-        }
-        s1[(size_t)(a / SUM_BLOCK)] = num;
-        s2[(size_t)(a / SUM_BLOCK)] = den;
+    sum_blocks(n, s1.data(), s2.data(), [&](int64_t i, double &num, double &den) {
+        const double wi = w ? (double)w[i] : 1.0;
+        num += wi * (double)y[i];
+        den += wi;
     });
     double num = 0, den = 0;
     for (int64_t k = 0; k < nblocks; ++k) { num += s1[(size_t)k]; den += s2[(size_t)k]; }
@@ -770,7 +915,7 @@ static void validate_inputs(const Params &p, int64_t rows, int64_t cols, const f
 // params (bin count and categorical layout included).
 static void setup_shape(Trainer &t, int64_t rows, int64_t cols) {
     const Params &p = t.p;
-    t.dev = std::make_unique<Device>(0);
+    t.dev = acquire_device(0);
     hipStream_t s = t.dev->stream;
     t.rows = rows;
     t.cols = (int)cols;
@@ -1072,7 +1217,9 @@ static void check_device_features(const Params &p, const float *x_dev, int64_t r
     xs.clear();
     ys.clear();
     if (m >= 50) {
-        DevBuf<float> sd((size_t)(m * cols));
+        DevBuf<float> sd;                               // released after the stream drained
+        sd.pooled = true;
+        sd.alloc((size_t)(m * cols));
         xs.resize((size_t)(m * cols));
         ys.resize((size_t)m);
         MB_HIP(mbk::launch_gather_sample(s, x_dev, rs, cs, step, m, (int)cols, sd.ptr));
@@ -1204,34 +1351,40 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
                 xsrc = xd.ptr;
             }
             const size_t ne = (size_t)p.num_bins - 2;
-            DevBuf<float> ed(std::max<size_t>(1, (size_t)cols * ne));
+            DevBuf<float> ed;                           // released after the stream drained
+            ed.pooled = true;
+            ed.alloc(std::max<size_t>(1, (size_t)cols * ne));
+            const size_t cap = mbk::edge_sample_cap(rows);
+            DevBuf<uint32_t> ka, kb, cnt;               // released after the stream drained
+            ka.pooled = kb.pooled = cnt.pooled = true;
+            const double te = now_s();
             {
                 Phase ph("quantile edges");
-                const double te = now_s();
-                const size_t cap = mbk::edge_sample_cap(rows);
-                DevBuf<uint32_t> ka((size_t)cols * cap), kb((size_t)cols * cap), cnt((size_t)cols);
+                ka.alloc((size_t)cols * cap);
+                kb.alloc((size_t)cols * cap);
+                cnt.alloc((size_t)cols);
                 MB_HIP(mbk::launch_edges(s, xsrc, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
                                          ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
-                // the labels cross PCIe on the copy stream while the device sorts
-                t.labels.alloc((size_t)rows);
-                upload(t.labels.ptr, y, (size_t)rows * 4, t.dev->copy_stream);
-                MB_HIP(hipStreamSynchronize(t.dev->copy_stream));
-                t.labels_ready = true;
-                t.edges.resize((size_t)cols * ne);
-                MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
-                MB_HIP(hipStreamSynchronize(s));
-                t.t_edges = now_s() - te;
             }
+            // binning follows the edges on the device; meanwhile the labels
+            // cross PCIe on the copy stream and the edges come back to the host
             Phase ph("bin data");
             t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
             t.bins_fm.alloc((size_t)rows * (size_t)cols);
             MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
                                         p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
                                         t.bins_fm.ptr));
+            t.edges.resize((size_t)cols * ne);
+            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+            t.labels.alloc((size_t)rows);
+            upload(t.labels.ptr, y, (size_t)rows * 4, t.dev->copy_stream);
+            MB_HIP(hipStreamSynchronize(t.dev->copy_stream));
+            t.labels_ready = true;
             if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
             MB_HIP(hipStreamSynchronize(s));
+            t.t_edges = now_s() - te;
         }
-        t.t_bin = now_s() - t0 - t.t_edges;              // (upload +) bin_data
+        t.t_bin = now_s() - t0 - t.t_edges;              // the feature upload, if any
         prep.join();
         if (prep.err) std::rethrow_exception(prep.err);
         Phase ph_rest("labels, buffers");
