@@ -44,6 +44,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 REFERENCE_TREES_PER_S = 100 / 3.9    # 100 trees in 3.9 s on an M4 Max (README.md:73)
 LEVELWISE = {"max_depth": 6, "num_bins": 256, "learning_rate": 0.1}
+PROFILE_EVERY = 5    # timed fits: histogram launches of every 5th tree carry timestamps
 
 
 def log(msg):
@@ -77,7 +78,9 @@ def headline(mb, ctx, args):
     for _ in range(args.warmup):
         ctx.fit(params, x_dev, rows, cols, y)
     log(f"{args.warmup} warm-up fits done")
-    ctx.profile(True)
+    # the histogram launches of every PROFILE_EVERY-th tree carry their own
+    # dispatch timestamps (a timestamped launch costs a few microseconds more)
+    ctx.profile(True, every=PROFILE_EVERY)
     sec, h = time_fits(ctx, params, x_dev, rows, cols, y, args.steps)
     ctx.profile(False)
     launches, hist_ms, hist_bytes, built, level_ms = ctx.hist_stats(16)
@@ -102,7 +105,7 @@ def roofline_of(stats, rows, cols, steps, trees):
         if (tj.get("profile_rows"), tj.get("profile_cols")) == (rows, cols):
             traffic = (tj["fetch_bytes_per_built_row"] * float(sum(built[:6])) / launches
                        + tj["write_bytes_per_launch"])
-    n_trees = steps * trees
+    n_trees = steps * ((trees + PROFILE_EVERY - 1) // PROFILE_EVERY)   # the timed trees
     levels = []
     for d in range(6):
         gbs = float(built[d]) * (cols + 4) / (level_ms[d] / 1e3) / 1e9 if level_ms[d] > 0 else None
@@ -114,6 +117,7 @@ def roofline_of(stats, rows, cols, steps, trees):
         "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": traffic,
         "kernel": "k_hist", "launches": launches,
+        "timed_launches": f"every histogram launch of every {PROFILE_EVERY}th tree of the timed fits",
         "avg_launch_ms": hist_ms / launches if launches else None,
         "algorithmic_bytes_per_launch": hist_bytes / launches if launches else None,
         "algorithmic_bytes_definition": "sum over built nodes of rows * (features + 4)",

@@ -295,19 +295,22 @@ void *mbx_trainer_create(const char *params_json, const float *x, int64_t rows, 
                          char **err);
 /* Enqueue num_trees boosting iterations and wait for them. */
 int mbx_trainer_grow(void *trainer, int32_t num_trees, char **err);
-/* 1 = time every histogram launch (its own dispatch timestamps) from now on. */
+/* enable = k >= 1: time the histogram launches (their own dispatch
+ * timestamps) of every k-th tree from now on; 0: stop. */
 int mbx_trainer_profile(void *trainer, int32_t enable, char **err);
-/* Histogram-kernel totals since profiling was enabled: launches, total
- * milliseconds, and algorithmic bytes (sum over built nodes of rows*(cols+4)). */
+/* Histogram-kernel totals over the timed trees since profiling was
+ * enabled: launches, total milliseconds, and algorithmic bytes (sum over
+ * built nodes of rows*(cols+4)). */
 int mbx_trainer_hist_stats(void *trainer, int64_t *launches, double *ms, double *bytes,
                            char **err);
-/* Per-level sums over the trees grown since profiling was enabled: rows of
+/* Per-level sums over the timed trees since profiling was enabled: rows of
  * built (histogrammed) nodes, live rows, and histogram-kernel milliseconds,
  * levels 0..max_levels-1 (16 at most carry data).  Any output may be NULL. */
 int mbx_trainer_level_stats(void *trainer, int32_t max_levels, int64_t *built, int64_t *active,
                             double *hist_ms, char **err);
-/* The same instrumentation for fits run with mbk_fit on a context: 1 turns
- * it on (and clears the totals), 0 off.  The totals add up over the fits;
+/* The same instrumentation for fits run with mbk_fit on a context: k >= 1
+ * turns it on for every k-th tree (and clears the totals), 0 off.  The
+ * totals add up over the fits;
  * built and level_ms (either may be NULL) hold max_levels entries (16 at
  * most carry data): rows of built nodes and histogram milliseconds per level. */
 int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err);

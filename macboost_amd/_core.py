@@ -570,11 +570,12 @@ class Context:
         err = ctypes.c_char_p()
         self._check(getattr(lib(), name)(self.ptr, *args, ctypes.byref(err)), err)
 
-    def profile(self, enable: bool = True) -> None:
-        """HIP-event timing of every histogram launch of later fits."""
+    def profile(self, enable: bool = True, every: int = 1) -> None:
+        """HIP-event timing of the histogram launches of every every-th tree
+        of later fits (enable=False stops it)."""
         err = ctypes.c_char_p()
-        self._check(lib().mbx_context_profile(self.ptr, 1 if enable else 0, ctypes.byref(err)),
-                    err)
+        self._check(lib().mbx_context_profile(self.ptr, max(1, every) if enable else 0,
+                                              ctypes.byref(err)), err)
 
     def hist_stats(self, levels: int = 16):
         """(launches, ms, algorithmic bytes, built rows per level, ms per level)

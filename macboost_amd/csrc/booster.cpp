@@ -702,7 +702,7 @@ int mbx_trainer_grow(void *trainer, int32_t num_trees, char **err) {
 
 int mbx_trainer_profile(void *trainer, int32_t enable, char **err) {
     if (!trainer) { set_err(err, "null argument"); return -1; }
-    mb::trainer_profile(static_cast<mb::Trainer *>(trainer), enable != 0);
+    mb::trainer_profile(static_cast<mb::Trainer *>(trainer), enable > 0 ? enable : 0);
     return 0;
 }
 

@@ -291,7 +291,8 @@ SelectionResult select_features(const Params &p, const float *x_fm, int64_t rows
                                 double alpha, uint64_t seed);
 void validate_label_values(const Params &p, const float *y, int64_t n);
 void trainer_grow(Trainer *t, int num_trees);
-void trainer_profile(Trainer *t, bool enable);
+// every > 0: time the histogram launches of every every-th tree from now on.
+void trainer_profile(Trainer *t, int every);
 void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes);
 void trainer_level_stats(Trainer *t, int32_t max_levels, int64_t *built, int64_t *active,
                          double *hist_ms);

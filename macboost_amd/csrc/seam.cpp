@@ -74,6 +74,7 @@ struct mbk_context {
     Scratch scratch;
     // histogram-kernel timing of the fits run through this context
     bool profiling = false;
+    int prof_every = 1;           // profiled fits time every prof_every-th tree
     int64_t prof_launches = 0;
     double prof_ms = 0, prof_bytes = 0;
     int64_t prof_built[16] = {};
@@ -590,7 +591,7 @@ void *mbk_fit(mbk_context *ctx, const char *params_json, const float *x, int64_t
         mb::Trainer *t = mb::trainer_create_device(p, x, rows, cols, row_major != 0, y, w,
                                                    x_valid, valid_rows, y_valid);
         try {
-            if (ctx->profiling) mb::trainer_profile(t, true);
+            if (ctx->profiling) mb::trainer_profile(t, ctx->prof_every);
             mb::trainer_grow(t, p.num_trees * mb::trainer_classes(t));
             mb::Booster *b = mb::trainer_booster(t);
             if (ctx->profiling) {
@@ -626,7 +627,8 @@ int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err) {
                 ctx->prof_level_ms[d] = 0;
             }
         }
-        ctx->profiling = enable != 0;
+        ctx->profiling = enable > 0;
+        if (enable > 0) ctx->prof_every = enable;
         return 0;
     }, -1);
 }

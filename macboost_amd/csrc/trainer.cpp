@@ -316,6 +316,33 @@ void release_device(std::unique_ptr<Device> d) {
     if (g_dev_free->size() < 16) g_dev_free->push_back(d.release());
 }
 
+// Timing events for the profiled histogram launches, kept for reuse (a fit
+// records two per launch; creating them costs microseconds each).
+namespace {
+std::mutex g_ev_mu;
+std::vector<hipEvent_t> *g_ev_free = new std::vector<hipEvent_t>();
+
+hipEvent_t acquire_event() {
+    {
+        std::lock_guard<std::mutex> lock(g_ev_mu);
+        if (!g_ev_free->empty()) {
+            hipEvent_t e = g_ev_free->back();
+            g_ev_free->pop_back();
+            return e;
+        }
+    }
+    hipEvent_t e = nullptr;
+    MB_HIP(hipEventCreate(&e));
+    return e;
+}
+
+void release_event(hipEvent_t e) {
+    if (!e) return;
+    std::lock_guard<std::mutex> lock(g_ev_mu);
+    g_ev_free->push_back(e);
+}
+}  // namespace
+
 // ---------------------------------------------------------------------------
 // Host -> device upload of large pageable buffers: two pinned staging buffers,
 // each filled by a few host threads while the other one's DMA is in flight.
@@ -522,6 +549,10 @@ struct Trainer {
 
     bool profiling = false;
     int prof_first_tree = 0;
+    int prof_every = 1;             // time the histogram launches of every k-th tree
+    bool prof_tree(int tree) const {
+        return profiling && (tree - prof_first_tree) % prof_every == 0;
+    }
     struct HistEvent { hipEvent_t start, end; int level; };
     std::vector<HistEvent> events;
     int64_t prof_launches = 0;
@@ -564,7 +595,7 @@ struct Trainer {
             if (dev->stream) (void)hipStreamSynchronize(dev->stream);
             if (dev->copy_stream) (void)hipStreamSynchronize(dev->copy_stream);
         }
-        for (auto &e : events) { (void)hipEventDestroy(e.start); (void)hipEventDestroy(e.end); }
+        for (auto &e : events) { release_event(e.start); release_event(e.end); }
         release_device(std::move(dev));
     }
 
@@ -1644,16 +1675,16 @@ static void grow_levelwise(Trainer &t, int tree) {
     auto hist = [&](const mbk::Entry *ord, int level) {
         // profiling: the kernel's own dispatch timestamps (no marker packets)
         hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (t.profiling) {
-            MB_HIP(hipEventCreate(&e0));
-            MB_HIP(hipEventCreate(&e1));
+        if (t.prof_tree(tree)) {
+            e0 = acquire_event();
+            e1 = acquire_event();
         }
         // an unsampled root streams every row: the planar copy when there is one
         const bool planar = level == 0 && !sampled && t.has_root_copy;
         MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
                                 planar ? &t.root_layout : nullptr, e0, e1));
-        if (t.profiling) t.events.push_back({e0, e1, level});
+        if (e0) t.events.push_back({e0, e1, level});
     };
 
     // level 0
@@ -1748,15 +1779,15 @@ static void grow_leafwise(Trainer &t, int tree) {
                                sampled));
     auto build = [&](int step) {
         hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (t.profiling) {
-            MB_HIP(hipEventCreate(&e0));
-            MB_HIP(hipEventCreate(&e1));
+        if (t.prof_tree(tree)) {
+            e0 = acquire_event();
+            e1 = acquire_event();
         }
         const bool planar = step == 0 && !sampled && t.has_root_copy;
         MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, order,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
                                 planar ? &t.root_layout : nullptr, e0, e1));
-        if (t.profiling) t.events.push_back({e0, e1, std::min(step, 15)});
+        if (e0) t.events.push_back({e0, e1, std::min(step, 15)});
         MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, t.hist_a.ptr,
                                  t.hist_a.ptr, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
                                  t.count.ptr, t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
@@ -1842,15 +1873,15 @@ static void grow_leafwise_rounds(Trainer &t, int tree) {
     int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
     auto hist = [&](const mbk::Entry *ord, int level) {
         hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (t.profiling) {
-            MB_HIP(hipEventCreate(&e0));
-            MB_HIP(hipEventCreate(&e1));
+        if (t.prof_tree(tree)) {
+            e0 = acquire_event();
+            e1 = acquire_event();
         }
         const bool planar = level == 0 && !sampled && t.has_root_copy;
         MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
                                 planar ? &t.root_layout : nullptr, e0, e1));
-        if (t.profiling) t.events.push_back({e0, e1, level});
+        if (e0) t.events.push_back({e0, e1, level});
     };
     // unsampled trees without renewal: the training walk counts the deepest
     // rows, so the last round partitions nothing
@@ -1982,34 +2013,41 @@ void trainer_grow(Trainer *tp, int num_trees) {
             t.prof_ms += ms;
             t.prof_level_ms[e.level & 15] += ms;
             t.prof_launches += 1;
-            (void)hipEventDestroy(e.start);
-            (void)hipEventDestroy(e.end);
+            release_event(e.start);
+            release_event(e.end);
         }
         t.events.clear();
     }
 }
 
-void trainer_profile(Trainer *t, bool enable) {
-    if (enable && !t->profiling) {
+void trainer_profile(Trainer *t, int every) {
+    if (every > 0 && !t->profiling) {
         t->prof_first_tree = t->grown;
+        t->prof_every = every;
         t->prof_ms = 0;
         t->prof_launches = 0;
         for (double &v : t->prof_level_ms) v = 0;
     }
-    t->profiling = enable;
+    t->profiling = every > 0;
+}
+
+// The control blocks of the profiled trees since profiling began.
+static std::vector<mbk::TreeCtl> profiled_ctls(Trainer *t) {
+    std::vector<mbk::TreeCtl> out;
+    const int n = t->grown - t->prof_first_tree;
+    if (n <= 0) return out;
+    std::vector<mbk::TreeCtl> h((size_t)n);
+    MB_HIP(hipMemcpy(h.data(), t->ctl_hist.ptr + t->prof_first_tree, (size_t)n * sizeof(mbk::TreeCtl),
+                     hipMemcpyDeviceToHost));
+    for (int k = 0; k < n; k += t->prof_every) out.push_back(h[(size_t)k]);
+    return out;
 }
 
 void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes) {
     MB_HIP(hipStreamSynchronize(t->dev->stream));
-    const int n = t->grown - t->prof_first_tree;
     double b = 0;
-    if (n > 0) {
-        std::vector<mbk::TreeCtl> h((size_t)n);
-        MB_HIP(hipMemcpy(h.data(), t->ctl_hist.ptr + t->prof_first_tree, (size_t)n * sizeof(mbk::TreeCtl),
-                         hipMemcpyDeviceToHost));
-        for (auto &c : h)
-            for (int d = 0; d < t->D; ++d) b += (double)c.level_built[d] * (double)(t->cols + 4);
-    }
+    for (const auto &c : profiled_ctls(t))
+        for (int d = 0; d < t->D; ++d) b += (double)c.level_built[d] * (double)(t->cols + 4);
     if (launches) *launches = t->prof_launches;
     if (ms) *ms = t->prof_ms;
     if (bytes) *bytes = b;
@@ -2018,18 +2056,13 @@ void trainer_hist_stats(Trainer *t, int64_t *launches, double *ms, double *bytes
 void trainer_level_stats(Trainer *t, int32_t max_levels, int64_t *built, int64_t *active,
                          double *hist_ms) {
     MB_HIP(hipStreamSynchronize(t->dev->stream));
-    const int n = t->grown - t->prof_first_tree;
     for (int d = 0; d < max_levels; ++d) {
         if (built) built[d] = 0;
         if (active) active[d] = 0;
         if (hist_ms) hist_ms[d] = d < 16 ? t->prof_level_ms[d] : 0.0;
     }
-    if (n <= 0) return;
-    std::vector<mbk::TreeCtl> h((size_t)n);
-    MB_HIP(hipMemcpy(h.data(), t->ctl_hist.ptr + t->prof_first_tree, (size_t)n * sizeof(mbk::TreeCtl),
-                     hipMemcpyDeviceToHost));
     const int L = std::min<int>(max_levels, 16);
-    for (auto &c : h)
+    for (const auto &c : profiled_ctls(t))
         for (int d = 0; d < L; ++d) {
             if (built) built[d] += c.level_built[d];
             if (active) active[d] += c.level_active[d];
