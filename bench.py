@@ -44,7 +44,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 REFERENCE_TREES_PER_S = 100 / 3.9    # 100 trees in 3.9 s on an M4 Max (README.md:73)
 LEVELWISE = {"max_depth": 6, "num_bins": 256, "learning_rate": 0.1}
-PROFILE_EVERY = 5    # timed fits: histogram launches of every 5th tree carry timestamps
+PROFILE_EVERY = 5    # default: histogram launches of every 5th timed tree carry timestamps
 
 
 def log(msg):
@@ -80,7 +80,7 @@ def headline(mb, ctx, args):
     log(f"{args.warmup} warm-up fits done")
     # the histogram launches of every PROFILE_EVERY-th tree carry their own
     # dispatch timestamps (a timestamped launch costs a few microseconds more)
-    ctx.profile(True, every=PROFILE_EVERY)
+    ctx.profile(True, every=args.profile_every)
     sec, h = time_fits(ctx, params, x_dev, rows, cols, y, args.steps)
     ctx.profile(False)
     launches, hist_ms, hist_bytes, built, level_ms = ctx.hist_stats(16)
@@ -92,7 +92,7 @@ def headline(mb, ctx, args):
     return x, y, x_dev, sec, value, valid, (launches, hist_ms, hist_bytes, built, level_ms)
 
 
-def roofline_of(stats, rows, cols, steps, trees):
+def roofline_of(stats, rows, cols, steps, trees, every):
     launches, hist_ms, hist_bytes, built, level_ms = stats
     achieved = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms > 0 else None
     traffic = None
@@ -105,7 +105,7 @@ def roofline_of(stats, rows, cols, steps, trees):
         if (tj.get("profile_rows"), tj.get("profile_cols")) == (rows, cols):
             traffic = (tj["fetch_bytes_per_built_row"] * float(sum(built[:6])) / launches
                        + tj["write_bytes_per_launch"])
-    n_trees = steps * ((trees + PROFILE_EVERY - 1) // PROFILE_EVERY)   # the timed trees
+    n_trees = steps * ((trees + every - 1) // every)   # the timed trees
     levels = []
     for d in range(6):
         gbs = float(built[d]) * (cols + 4) / (level_ms[d] / 1e3) / 1e9 if level_ms[d] > 0 else None
@@ -117,7 +117,7 @@ def roofline_of(stats, rows, cols, steps, trees):
         "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": traffic,
         "kernel": "k_hist", "launches": launches,
-        "timed_launches": f"every histogram launch of every {PROFILE_EVERY}th tree of the timed fits",
+        "timed_launches": f"every histogram launch of every {every}th tree of the timed fits",
         "avg_launch_ms": hist_ms / launches if launches else None,
         "algorithmic_bytes_per_launch": hist_bytes / launches if launches else None,
         "algorithmic_bytes_definition": "sum over built nodes of rows * (features + 4)",
@@ -341,6 +341,8 @@ def main():
     ap.add_argument("--rows", type=int, default=10_000_000)
     ap.add_argument("--cols", type=int, default=100)
     ap.add_argument("--cpu-trees", type=int, default=10)
+    ap.add_argument("--profile-every", type=int, default=PROFILE_EVERY,
+                    help="time the histogram launches of every k-th tree of the timed fits")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline fits (no other workloads)")
@@ -362,7 +364,7 @@ def main():
         return
     rows, cols = args.rows, args.cols
     x, y, x_dev, sec, value, valid, stats = headline(mb, ctx, args)
-    roofline = roofline_of(stats, rows, cols, args.steps, 100)
+    roofline = roofline_of(stats, rows, cols, args.steps, 100, args.profile_every)
     extras = {}
     if not args.no_extras:
         extras.update(headline_extras(mb, x, y, rows, cols))
