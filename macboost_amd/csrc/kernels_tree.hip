@@ -110,128 +110,130 @@ __device__ __forceinline__ void row_grad_at(const GradParams &gp, const float *_
 // both layouts: the gather layout [rows][T][W] (row r's tile t at
 // (r*T + t)*W) and the feature-major [F][rows].
 //
-// A block takes BIN_ROWS rows of one group of G = min(16, W) features (one
-// 16-B chunk of every row's tile, or the whole 8-B tile at W = 8), in
-// sub-chunks of 256 rows, one row per thread.  Each thread loads its row's G
-// values at once (16-B loads for row-major input) and finds each bin by
-// binary lifting over the group's edges in LDS, padded with +inf to 255
-// entries: b = the number of edges below v, found in eight steps of one LDS
-// read, one compare and one select (for the non-decreasing quantile edges
-// this is the reference's binary search result, lower_bound(edges, v)).  It
-// writes its row's G bytes to the gather layout with one store and leaves
-// them in LDS; the block then writes the feature-major bytes as u32 words of
-// four rows.  Groups past the last feature write zero bytes, so the gather
-// layout needs no clearing.
+// A block bins one whole tile (W features) of BIN_ROWS rows, one row per
+// thread, 16 features at a time: every row's W-byte tile segment is written
+// by one block, the T blocks of a row block run on one XCD (the pieces of a
+// row meet in one L2; pieces from blocks on different XCDs went to HBM as
+// partial lines), and the feature-major bytes go out as
+// one byte per lane, 64 consecutive bytes per wavefront store.  A value's bin
+// is the number of edges below it, lower_bound(edges, v) for the
+// non-decreasing quantile edges (the reference's binary search).  Each
+// feature's edges sit in LDS in breadth-first (Eytzinger) order of the
+// perfect search tree over the 255 slots (+inf padded): search step k reads
+// slots [2^k, 2^(k+1)), a contiguous range, so the lanes of a wavefront hit
+// distinct banks where sorted order put every step's candidates in one bank.
+// Eight steps of one LDS read, compare and index update; slot i - 256 at the
+// end is the bin.  Tiles past the last feature write zero bytes, so the
+// gather layout needs no clearing.
 // ---------------------------------------------------------------------------
 
-constexpr int BIN_THREADS = 256;
-constexpr int BIN_SUB = 256;                          // rows per sub-chunk (one per thread)
-constexpr int BIN_ROWS = 2048;                        // rows per block
+constexpr int BIN_THREADS = 512;
+constexpr int BIN_ROWS = 4096;                        // rows per block
 
-template <int G>
+template <int W>
 __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
     const float *__restrict__ x, int64_t rows, int32_t cols, int64_t rs, int64_t cs,
-    const float *__restrict__ edges, const uint8_t *__restrict__ is_cat, int32_t nb, int32_t W,
-    int32_t T, uint8_t *__restrict__ tiled, uint8_t *__restrict__ fm, int vec_rows) {
-    __shared__ float e_lds[G * 256];                 // [feature][255 edges + pad], +inf padded
-    __shared__ __align__(16) uint8_t b_lds[G][BIN_SUB];
+    const float *__restrict__ edges, const uint8_t *__restrict__ is_cat, int32_t nb, int32_t T,
+    uint8_t *__restrict__ tiled, uint8_t *__restrict__ fm, int vec_rows) {
+    constexpr int G = W < 16 ? W : 16;               // features per pass
+    __shared__ float e_lds[W * 256];                 // [feature][BFS slot 1..255], slot 0 unused
     const int tid = threadIdx.x;
     const int ne = nb - 2, data_bins = nb - 1;
-    // groups vary fastest over the blocks: the groups of one row block run
-    // together, so the pieces of each gather-layout row line are written close
-    // in time
-    const int ngroups = T * W / G;
-    const int g = (int)(blockIdx.x % (uint32_t)ngroups);   // features g*G .. g*G+G-1
-    const int64_t row_block = blockIdx.x / (uint32_t)ngroups;
-    const int f0 = g * G;
-    const int nf = max(0, min(G, cols - f0));         // real features of the group
-    const int t = f0 / W, chunk = (f0 % W) / G;       // tile and chunk the group fills
-    for (int k = tid; k < G * 256; k += BIN_THREADS) {
-        const int f = k >> 8, j = k & 255;
-        e_lds[k] = (f < nf && j < ne) ? edges[(int64_t)(f0 + f) * ne + j] : INFINITY;
+    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8): the T
+    // tiles of a row block are blocks xcd + 8 (q T + t), all on one XCD, so
+    // the pieces of a row's T*W bytes merge in that XCD's L2.
+    const uint32_t xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
+    const int t = (int)(k8 % (uint32_t)T);
+    const int64_t row_block = (int64_t)(k8 / (uint32_t)T) * 8 + xcd;
+    if (row_block * BIN_ROWS >= rows) return;         // grid padding (whole block)
+    const int f0 = t * W;
+    const int nf = max(0, min(W, cols - f0));         // real features of the tile
+    for (int k = tid; k < W * 256; k += BIN_THREADS) {
+        const int f = k >> 8, i = k & 255;
+        float val = INFINITY;
+        if (i > 0 && f < nf) {
+            // BFS slot i of a perfect tree of height 8 holds the sorted slot of
+            // in-order rank ((2q + 1) << (7 - L)), L = depth of i, q = i - 2^L
+            const int L = 31 - __clz(i);
+            const int j = ((2 * (i - (1 << L)) + 1) << (7 - L)) - 1;
+            if (j < ne) val = edges[(int64_t)(f0 + f) * ne + j];
+        }
+        e_lds[k] = val;
     }
-    uint32_t cat_bits = 0;
-    for (int k = 0; k < nf; ++k) cat_bits |= (is_cat[f0 + k] ? 1u : 0u) << k;
+    uint64_t cat_bits = 0;
+    for (int k = 0; k < nf; ++k) cat_bits |= (uint64_t)(is_cat[f0 + k] ? 1u : 0u) << k;
     __syncthreads();
-    // row-major input whose group starts 16-B aligned: 16-B loads
-    const bool rm16 = vec_rows != 0 && (f0 & 3) == 0 && nf == G;
     const int64_t blk0 = row_block * BIN_ROWS;
-    for (int64_t r0 = blk0; r0 < min(rows, blk0 + BIN_ROWS); r0 += BIN_SUB) {
-        const int64_t r = r0 + tid;
-        const bool live = r < rows;
-        float v[G];
-        if (live && rm16) {
-            const float4 *src = reinterpret_cast<const float4 *>(x + r * rs + f0);
+    const int64_t blk1 = min(rows, blk0 + BIN_ROWS);
+    // G values of row r from feature f0 + c on (row-major input 16-B
+    // aligned: 16-B loads)
+    auto load = [&](int64_t r, int c, float (&v)[G]) {
+        const int fc = f0 + c;
+        if (vec_rows != 0 && (fc & 3) == 0 && c + G <= nf) {
+            const float4 *src = reinterpret_cast<const float4 *>(x + r * rs + fc);
 #pragma unroll
             for (int q = 0; q < G / 4; ++q) {
-                const float4 w = src[q];
-                v[4 * q] = w.x; v[4 * q + 1] = w.y; v[4 * q + 2] = w.z; v[4 * q + 3] = w.w;
+                const float4 w4 = src[q];
+                v[4 * q] = w4.x; v[4 * q + 1] = w4.y; v[4 * q + 2] = w4.z; v[4 * q + 3] = w4.w;
             }
         } else {
 #pragma unroll
             for (int k = 0; k < G; ++k)
-                v[k] = (live && k < nf) ? x[r * rs + (int64_t)(f0 + k) * cs] : 0.0f;
+                v[k] = c + k < nf ? x[r * rs + (int64_t)(fc + k) * cs] : 0.0f;
         }
-        uint32_t b[G];
+    };
+    for (int64_t r = blk0 + tid; r < blk1; r += BIN_THREADS) {
+        uint32_t seg[W / 4];                          // the row's W tile bytes
+#pragma unroll 1
+        for (int c = 0; c < W; c += G) {
+            float v[G];
+            load(r, c, v);
+            uint32_t b[G];
 #pragma unroll
-        for (int k0 = 0; k0 < G; k0 += 4) {
-            uint32_t lo[4];
+            for (int k0 = 0; k0 < G; k0 += 4) {
+                uint32_t ix[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) lo[j] = 0;
-            // lo = #edges < v: padding (+inf) never counts, so lo <= ne
+                for (int j = 0; j < 4; ++j) ix[j] = 1;
 #pragma unroll
-            for (int s = 128; s >= 1; s >>= 1) {
+                for (int step = 0; step < 8; ++step) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        ix[j] = 2 * ix[j] + (v[k0 + j] > e_lds[(c + k0 + j) * 256 + (int)ix[j]] ? 1u : 0u);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t up = lo[j] + (uint32_t)s;
-                    lo[j] = v[k0 + j] > e_lds[(k0 + j) * 256 + (int)up - 1] ? up : lo[j];
+                    const int k = k0 + j;
+                    const float val = v[k];
+                    uint32_t bb = ix[j] - 256u;
+                    if (isnan(val)) {
+                        bb = (uint32_t)data_bins;
+                    } else if ((cat_bits >> (c + k)) & 1u) {
+                        int cc = (int)rintf(val);
+                        cc = cc < 0 ? 0 : (cc > data_bins - 1 ? data_bins - 1 : cc);
+                        bb = (uint32_t)cc;
+                    }
+                    b[k] = c + k < nf ? bb : 0u;
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k = k0 + j;
-                const float val = v[k];
-                uint32_t bb = lo[j];
-                if (isnan(val)) {
-                    bb = (uint32_t)data_bins;
-                } else if ((cat_bits >> k) & 1u) {
-                    int c = (int)rintf(val);
-                    c = c < 0 ? 0 : (c > data_bins - 1 ? data_bins - 1 : c);
-                    bb = (uint32_t)c;
-                }
-                b[k] = k < nf ? bb : 0u;
-            }
-        }
-        uint32_t word[G / 4];
+            for (int q = 0; q < G / 4; ++q)
+                seg[c / 4 + q] = b[4 * q] | (b[4 * q + 1] << 8) | (b[4 * q + 2] << 16) | (b[4 * q + 3] << 24);
 #pragma unroll
-        for (int q = 0; q < G / 4; ++q)
-            word[q] = b[4 * q] | (b[4 * q + 1] << 8) | (b[4 * q + 2] << 16) | (b[4 * q + 3] << 24);
-        if (live) {
-            uint8_t *dst = tiled + (r * T + t) * (int64_t)W + chunk * G;
-            if constexpr (G == 16)
-                *reinterpret_cast<uint4 *>(dst) = make_uint4(word[0], word[1], word[2], word[3]);
-            else
-                *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[1]);
+            for (int k = 0; k < G; ++k)
+                if (c + k < nf) fm[(int64_t)(f0 + c + k) * rows + r] = (uint8_t)b[k];
         }
+        // the whole segment in back-to-back stores: a 64-B segment reaches L2
+        // complete (16-B pieces stored a search apart were written back
+        // piecewise, as partial HBM writes)
+        uint8_t *dst = tiled + (r * T + t) * (int64_t)W;
+        if constexpr (W >= 16) {
 #pragma unroll
-        for (int k = 0; k < G; ++k) b_lds[k][tid] = (uint8_t)b[k];
-        __syncthreads();
-        // feature-major bytes: u32 words of four rows when the rows of every
-        // feature start 4-B aligned and the sub-chunk is whole, else bytes
-        const int64_t n_here = min((int64_t)BIN_SUB, rows - r0);
-        if ((rows & 3) == 0 && n_here == BIN_SUB) {
-            for (int w = tid; w < nf * (BIN_SUB / 4); w += BIN_THREADS) {
-                const int k = w / (BIN_SUB / 4), q = w % (BIN_SUB / 4);
-                const uint32_t val = *reinterpret_cast<const uint32_t *>(&b_lds[k][4 * q]);
-                *reinterpret_cast<uint32_t *>(fm + (int64_t)(f0 + k) * rows + r0 + 4 * q) = val;
-            }
+            for (int q = 0; q < W / 16; ++q)
+                reinterpret_cast<uint4 *>(dst)[q] =
+                    make_uint4(seg[4 * q], seg[4 * q + 1], seg[4 * q + 2], seg[4 * q + 3]);
         } else {
-            for (int w = tid; w < nf * BIN_SUB; w += BIN_THREADS) {
-                const int k = w / BIN_SUB, j = w % BIN_SUB;
-                if (j < n_here) fm[(int64_t)(f0 + k) * rows + r0 + j] = b_lds[k][j];
-            }
+            *reinterpret_cast<uint2 *>(dst) = make_uint2(seg[0], seg[1]);
         }
-        __syncthreads();
     }
 }
 
@@ -241,17 +243,19 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            uint8_t *fm) {
     if (nb < 4 || nb > 256 || rows <= 0) return rows == 0 ? hipSuccess : hipErrorInvalidValue;
     if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) return hipErrorInvalidValue;
-    const int G = tile_w >= 16 ? 16 : 8;
-    const int64_t nblk = (rows + BIN_ROWS - 1) / BIN_ROWS * (int64_t)(num_tiles * tile_w / G);
+    if (num_tiles < 1 || (int64_t)num_tiles * tile_w < cols) return hipErrorInvalidValue;
+    const int64_t nblk = ((rows + BIN_ROWS - 1) / BIN_ROWS + 7) / 8 * 8 * (int64_t)num_tiles;
     if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)nblk);
     const int vec_rows = cs == 1 && (rs & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    if (G == 16)
-        hipLaunchKernelGGL(k_bin_data<16>, grid, dim3(BIN_THREADS), 0, s, x, rows, cols, rs, cs,
-                           edges, is_cat, nb, tile_w, num_tiles, tiled, fm, vec_rows);
-    else
-        hipLaunchKernelGGL(k_bin_data<8>, grid, dim3(BIN_THREADS), 0, s, x, rows, cols, rs, cs,
-                           edges, is_cat, nb, tile_w, num_tiles, tiled, fm, vec_rows);
+#define MBK_BIN(WW)                                                                             \
+    hipLaunchKernelGGL(k_bin_data<WW>, grid, dim3(BIN_THREADS), 0, s, x, rows, cols, rs, cs, edges, \
+                       is_cat, nb, num_tiles, tiled, fm, vec_rows)
+    if (tile_w == 64) MBK_BIN(64);
+    else if (tile_w == 32) MBK_BIN(32);
+    else if (tile_w == 16) MBK_BIN(16);
+    else MBK_BIN(8);
+#undef MBK_BIN
     return hipGetLastError();
 }
 
