@@ -376,9 +376,9 @@ hipError_t launch_tile8_to_layouts(hipStream_t s, const uint64_t *in, int64_t ro
 // ---------------------------------------------------------------------------
 // quantile edges on the device (Binner.swift:25-56): per feature, the stride
 // subsample of non-NaN values, sorted, edge k = sample[min(m-1, (k+1)*m/dataBins)].
-// One 1024-thread workgroup per feature: compact the sample as order-
-// preserving u32 keys, then a stable LSD radix sort (8 passes of 4 bits;
-// ranks inside a wavefront from ballots, wavefronts and tiles in order).
+// The sample becomes order-preserving u32 keys (one thread per sample),
+// then one 1024-thread workgroup per feature radix-sorts them (stable LSD,
+// 4-bit digits) and the edges are read at their ranks.
 // ---------------------------------------------------------------------------
 
 constexpr int EDGE_THREADS = 1024;
@@ -422,132 +422,263 @@ __device__ __forceinline__ float key_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-__global__ __launch_bounds__(EDGE_THREADS) void k_edge_sample(const float *__restrict__ x,
-                                                              int64_t rows, int64_t rs,
-                                                              int64_t cs, int64_t step,
-                                                              uint32_t cap,
-                                                              const uint8_t *__restrict__ is_cat,
-                                                              uint32_t *__restrict__ keys,
-                                                              uint32_t *__restrict__ counts) {
-    __shared__ uint32_t wt[EDGE_WAVES + 1];
-    const int f = blockIdx.x, tid = threadIdx.x, w = tid >> 6;
-    uint32_t *out = keys + (size_t)f * cap;
-    uint32_t run = 0;
-    if (!is_cat[f]) {
-        const int64_t ns = (rows + step - 1) / step;     // samples i = 0, step, 2*step, ...
-        for (int64_t base = 0; base < ns; base += EDGE_THREADS) {
-            const int64_t s = base + tid;
-            float v = 0.0f;
-            uint32_t ok = 0;
-            if (s < ns) {
-                v = x[s * step * rs + (int64_t)f * cs];
-                ok = isnan(v) ? 0u : 1u;
-            }
-            const uint32_t inc = wave_inclusive_scan(ok);
-            if (lane_id() == 63) wt[w] = inc;
-            __syncthreads();
-            if (tid == 0) {
-                uint32_t acc = 0;
-                for (int k = 0; k < EDGE_WAVES; ++k) { const uint32_t t = wt[k]; wt[k] = acc; acc += t; }
-                wt[EDGE_WAVES] = acc;
-            }
-            __syncthreads();
-            if (ok) out[run + wt[w] + inc - 1] = float_key(v);
-            run += wt[EDGE_WAVES];
-            __syncthreads();
-        }
-    }
-    if (tid == 0) counts[f] = run;
+// Sample keys: thread s converts sample s (row s * step) of column blockIdx.y
+// into its order-preserving key, NaN into 0xFFFFFFFF (above every number's
+// key, so NaNs sort last and the first m sorted keys are the sample's m
+// non-NaN values).  Categorical columns take no sample.
+constexpr int EDGE_SAMPLE_THREADS = 256;
+
+__global__ __launch_bounds__(EDGE_SAMPLE_THREADS) void k_edge_sample(
+    const float *__restrict__ x, int64_t rs, int64_t cs, int64_t step, uint32_t ns, uint32_t cap,
+    const uint8_t *__restrict__ is_cat, uint32_t *__restrict__ keys) {
+    const int f = blockIdx.y;
+    const uint32_t s = blockIdx.x * EDGE_SAMPLE_THREADS + threadIdx.x;
+    if (is_cat[f] || s >= ns) return;
+    const float v = x[(int64_t)s * step * rs + (int64_t)f * cs];
+    keys[(size_t)f * cap + s] = isnan(v) ? 0xFFFFFFFFu : float_key(v);
 }
 
-// Stable LSD radix sort of each feature's keys (a -> b -> a ... 8 passes;
-// the result ends in a).
-__global__ __launch_bounds__(EDGE_THREADS) void k_edge_sort(uint32_t *__restrict__ keys_a,
-                                                            uint32_t *__restrict__ keys_b,
-                                                            uint32_t cap,
-                                                            const uint32_t *__restrict__ counts) {
-    __shared__ uint32_t hist[16];
-    __shared__ uint32_t cnt[EDGE_WAVES][16];
-    __shared__ uint32_t off[EDGE_WAVES][16];
-    const int f = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = lane_id();
-    const uint32_t m = counts[f];
-    uint32_t *src = keys_a + (size_t)f * cap, *dst = keys_b + (size_t)f * cap;
-    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int pass = 0; pass < 8; ++pass) {
-        const int shift = pass * 4;
-        if (tid < 16) hist[tid] = 0;
-        __syncthreads();
-        for (uint32_t i = tid; i < m; i += EDGE_THREADS) atomicAdd(&hist[(src[i] >> shift) & 15u], 1u);
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t acc = 0;
-            for (int d = 0; d < 16; ++d) { const uint32_t t = hist[d]; hist[d] = acc; acc += t; }
-        }
-        __syncthreads();
-        for (uint32_t base = 0; base < m; base += EDGE_THREADS) {
-            const uint32_t i = base + tid;
-            const bool valid = i < m;
-            const uint32_t key = valid ? src[i] : 0u;
-            const uint32_t d = (key >> shift) & 15u;
-            uint64_t match = __ballot(valid);
+// Stable LSD radix sort of each column's n sample keys, 4-bit digits, 8
+// passes, a column's keys split into B position chunks, one 1024-thread
+// workgroup per (chunk, column).  Each pass is two launches: k_edge_count
+// counts every chunk's digits, then k_edge_pass scatters.  A chunk's keys go
+// in tiles of 8,192 (8 per thread: key tile + j * 1024 + thread), the next
+// tile's keys loading while one is ranked; a key's rank among equal digits in
+// its wavefront comes from four ballots, and tiles, j, wavefronts and lanes
+// keep the input order.  A digit's keys from chunk c start after every
+// smaller digit's keys and after the same digit's keys of chunks < c, so each
+// pass is stable.  Behind each column's n keys, keys_a holds the chunk counts
+// of the current pass and keys_b the NaN counts of the first.
+constexpr int ESORT_KPT = 8;
+constexpr uint32_t ESORT_TILE = EDGE_THREADS * ESORT_KPT;
+constexpr uint32_t ESORT_MAX_CHUNKS = 32;
+constexpr uint32_t ESORT_SCRATCH = 16 * ESORT_MAX_CHUNKS;   // words behind a column's keys
+
+// Per-wavefront digit match of lane's digit d among the valid lanes.
+__device__ __forceinline__ uint64_t digit_match(uint32_t d, uint64_t valid) {
+    uint64_t m = valid;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint64_t bb = __ballot((d >> b) & 1u);
-                match &= ((d >> b) & 1u) ? bb : ~bb;
-            }
-            const uint32_t rank = (uint32_t)__popcll(match & lt);
-            if (tid < EDGE_WAVES * 16) cnt[tid >> 4][tid & 15] = 0;
-            __syncthreads();
-            if (valid && rank == 0) cnt[w][d] = (uint32_t)__popcll(match);
-            __syncthreads();
-            if (tid < 16) {
-                uint32_t acc = hist[tid];
-                for (int ww = 0; ww < EDGE_WAVES; ++ww) { off[ww][tid] = acc; acc += cnt[ww][tid]; }
-                hist[tid] = acc;
-            }
-            __syncthreads();
-            if (valid) dst[off[w][d] + rank] = key;
-            __syncthreads();
-        }
-        uint32_t *t = src; src = dst; dst = t;
+    for (int bt = 0; bt < 4; ++bt) {
+        const uint64_t bb = __ballot((d >> bt) & 1u);
+        m &= ((d >> bt) & 1u) ? bb : ~bb;
+    }
+    return m;
+}
+
+// The 8 keys of tile t0 for this thread (0 at or past end).
+__device__ __forceinline__ void esort_load(const uint32_t *src, uint32_t t0, uint32_t end, int tid,
+                                           uint32_t (&k)[ESORT_KPT]) {
+#pragma unroll
+    for (int j = 0; j < ESORT_KPT; ++j) {
+        const uint32_t i = t0 + (uint32_t)j * EDGE_THREADS + (uint32_t)tid;
+        k[j] = i < end ? src[i] : 0u;
     }
 }
 
-__global__ void k_edge_pick(const uint32_t *__restrict__ keys, uint32_t cap,
-                            const uint32_t *__restrict__ counts, const uint8_t *is_cat,
-                            int32_t num_bins, float *__restrict__ edges) {
+// Digit `pass` counts of chunk blockIdx.x of column blockIdx.y (and, on the
+// first pass, its NaN keys), read from the pass's input (keys_a for even
+// passes).
+__global__ __launch_bounds__(EDGE_THREADS) void k_edge_count(uint32_t *__restrict__ keys_a,
+                                                             uint32_t *__restrict__ keys_b,
+                                                             uint32_t cap, uint32_t n,
+                                                             uint32_t chunk, int pass,
+                                                             const uint8_t *__restrict__ is_cat) {
+    __shared__ uint32_t hist[16], s_nan;
+    const int f = blockIdx.y, tid = threadIdx.x, lane = lane_id();
+    if (is_cat[f]) return;
+    const int shift = pass * 4;
+    const uint32_t c = blockIdx.x, c0 = c * chunk, c1 = min(n, c0 + chunk);
+    if (tid < 16) hist[tid] = 0;
+    if (tid == 0) s_nan = 0;
+    __syncthreads();
+    const uint32_t *src = ((pass & 1) == 0 ? keys_a : keys_b) + (size_t)f * cap;
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    uint32_t nanc = 0, cur[ESORT_KPT], nxt[ESORT_KPT];
+    esort_load(src, c0, c1, tid, nxt);
+    for (uint32_t t0 = c0; t0 < c1; t0 += ESORT_TILE) {
+#pragma unroll
+        for (int j = 0; j < ESORT_KPT; ++j) cur[j] = nxt[j];
+        if (t0 + ESORT_TILE < c1) esort_load(src, t0 + ESORT_TILE, c1, tid, nxt);
+#pragma unroll
+        for (int j = 0; j < ESORT_KPT; ++j) {
+            const bool valid = t0 + (uint32_t)j * EDGE_THREADS + (uint32_t)tid < c1;
+            if (pass == 0 && valid && cur[j] == 0xFFFFFFFFu) ++nanc;
+            const uint32_t d = (cur[j] >> shift) & 15u;
+            const uint64_t m = digit_match(d, __ballot(valid));
+            if (valid && (m & lt) == 0) atomicAdd(&hist[d], (uint32_t)__popcll(m));
+        }
+    }
+    if (pass == 0) {
+        nanc = wave_sum(nanc);
+        if (lane == 0 && nanc) atomicAdd(&s_nan, nanc);
+    }
+    __syncthreads();
+    uint32_t *cnt = keys_a + (size_t)f * cap + n;
+    if (tid < 16) cnt[c * 16 + tid] = hist[tid];
+    if (pass == 0 && tid == 0) keys_b[(size_t)f * cap + n + c] = s_nan;
+}
+
+// One pass: scatter chunk blockIdx.x of column blockIdx.y by digit `pass`
+// from the pass's input (keys_a for even passes) to the other buffer.
+__global__ __launch_bounds__(EDGE_THREADS) void k_edge_pass(uint32_t *__restrict__ keys_a,
+                                                            uint32_t *__restrict__ keys_b,
+                                                            uint32_t cap, uint32_t n,
+                                                            uint32_t chunk, uint32_t nchunks,
+                                                            int pass,
+                                                            const uint8_t *__restrict__ is_cat) {
+    __shared__ uint32_t hist[16];
+    __shared__ uint32_t cc[ESORT_MAX_CHUNKS][16];
+    __shared__ uint32_t cnt[ESORT_KPT][EDGE_WAVES][16];   // leaders' counts, then offsets
+    __shared__ uint32_t tot[ESORT_KPT][16];
+    const int f = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = lane_id();
+    if (is_cat[f]) return;
+    const int shift = pass * 4;
+    const bool even = (pass & 1) == 0;
+    const uint32_t *src = (even ? keys_a : keys_b) + (size_t)f * cap;
+    uint32_t *dst = (even ? keys_b : keys_a) + (size_t)f * cap;
+    const uint32_t c = blockIdx.x, c0 = c * chunk, c1 = min(n, c0 + chunk);
+    // this chunk's first slot per digit, from every chunk's counts
+    const uint32_t *counts = keys_a + (size_t)f * cap + n;
+    for (uint32_t k = tid; k < nchunks * 16; k += EDGE_THREADS) (&cc[0][0])[k] = counts[k];
+    __syncthreads();
+    if (tid < 16) {
+        uint32_t total = 0, before = 0;
+        for (uint32_t q = 0; q < nchunks; ++q) {
+            total += cc[q][tid];
+            if (q < c) before += cc[q][tid];
+        }
+        tot[0][tid] = total;
+        hist[tid] = before;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        for (int d = 0; d < 16; ++d) {
+            hist[d] += acc;
+            acc += tot[0][d];
+        }
+    }
+    __syncthreads();
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+    uint32_t key[ESORT_KPT], nxt[ESORT_KPT];
+    esort_load(src, c0, c1, tid, nxt);
+    for (uint32_t t0 = c0; t0 < c1; t0 += ESORT_TILE) {
+        uint32_t rank[ESORT_KPT];
+        bool valid[ESORT_KPT];
+#pragma unroll
+        for (int j = 0; j < ESORT_KPT; ++j) key[j] = nxt[j];
+        if (t0 + ESORT_TILE < c1) esort_load(src, t0 + ESORT_TILE, c1, tid, nxt);
+        for (int k = tid; k < ESORT_KPT * EDGE_WAVES * 16; k += EDGE_THREADS)
+            (&cnt[0][0][0])[k] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ESORT_KPT; ++j) {
+            valid[j] = t0 + (uint32_t)j * EDGE_THREADS + (uint32_t)tid < c1;
+            const uint32_t d = (key[j] >> shift) & 15u;
+            const uint64_t m = digit_match(d, __ballot(valid[j]));
+            rank[j] = (uint32_t)__popcll(m & lt);
+            if (valid[j] && rank[j] == 0) cnt[j][w][d] = (uint32_t)__popcll(m);
+        }
+        __syncthreads();
+        // offsets: within each (j, d), wavefronts in order ...
+        if (tid < ESORT_KPT * 16) {
+            const int j = tid >> 4, d = tid & 15;
+            uint32_t acc = 0;
+            for (int ww = 0; ww < EDGE_WAVES; ++ww) {
+                const uint32_t v = cnt[j][ww][d];
+                cnt[j][ww][d] = acc;
+                acc += v;
+            }
+            tot[j][d] = acc;
+        }
+        __syncthreads();
+        // ... then j in order, from the digit's next free slot
+        if (tid < 16) {
+            uint32_t acc = hist[tid];
+            for (int j = 0; j < ESORT_KPT; ++j) {
+                const uint32_t v = tot[j][tid];
+                tot[j][tid] = acc;
+                acc += v;
+            }
+            hist[tid] = acc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < ESORT_KPT; ++j) {
+            if (!valid[j]) continue;
+            const uint32_t d = (key[j] >> shift) & 15u;
+            const uint32_t pos = tot[j][d] + cnt[j][w][d] + rank[j];
+            if (pos < n) dst[pos] = key[j];          // always, with consistent counts
+        }
+        __syncthreads();                             // cnt / tot reuse by the next tile
+    }
+}
+
+// Edge k = sorted[min(m - 1, (k + 1) * m / dataBins)] of the m non-NaN
+// sample keys (0 for categorical or all-NaN columns); after the 8 passes the
+// sorted keys are in keys_a.
+__global__ void k_edge_pick(const uint32_t *__restrict__ keys_a,
+                            const uint32_t *__restrict__ keys_b, uint32_t cap, uint32_t n,
+                            uint32_t nchunks, const uint8_t *is_cat, int32_t num_bins,
+                            float *__restrict__ edges) {
+    __shared__ uint32_t s_m;
     const int f = blockIdx.x;
     const int data_bins = num_bins - 1, ne = data_bins - 1;
-    const int64_t m = counts[f];
+    if (threadIdx.x == 0) {
+        uint32_t nan = 0;
+        if (!is_cat[f])
+            for (uint32_t c = 0; c < nchunks; ++c)
+                nan += keys_b[(size_t)f * cap + n + c];
+        s_m = is_cat[f] ? 0u : n - nan;
+    }
+    __syncthreads();
+    const int64_t m = s_m;
+    const uint32_t *keys = keys_a + (size_t)f * cap;
     for (int k = threadIdx.x; k < ne; k += blockDim.x) {
         float e = 0.0f;
-        if (!is_cat[f] && m > 0) {
+        if (m > 0) {
             int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
             if (idx > m - 1) idx = m - 1;
-            e = key_float(keys[(size_t)f * cap + idx]);
+            e = key_float(keys[idx]);
         }
         edges[(size_t)f * ne + k] = e;
     }
 }
 
+// Samples of a column: rows 0, step, 2 step, ... with step = rows / 200000.
+static int64_t edge_step(int64_t rows) { return rows / 200000 < 1 ? 1 : rows / 200000; }
+
 size_t edge_sample_cap(int64_t rows) {
-    int64_t step = rows / 200000;
-    if (step < 1) step = 1;
-    return (size_t)((rows + step - 1) / step);
+    const int64_t step = edge_step(rows);
+    return (size_t)((rows + step - 1) / step) + ESORT_SCRATCH;
 }
 
 hipError_t launch_edges(hipStream_t s, const float *x, int64_t rows, int32_t cols, int64_t rs,
                         int64_t cs, int32_t num_bins, const uint8_t *is_cat, uint32_t *keys_a,
                         uint32_t *keys_b, uint32_t *counts, float *edges) {
-    int64_t step = rows / 200000;
-    if (step < 1) step = 1;
+    (void)counts;
+    if (rows <= 0 || cols <= 0 || cols > 65535) return hipErrorInvalidValue;
+    const int64_t step = edge_step(rows);
     const uint32_t cap = (uint32_t)edge_sample_cap(rows);
-    hipLaunchKernelGGL(k_edge_sample, dim3(cols), dim3(EDGE_THREADS), 0, s, x, rows, rs, cs, step,
-                       cap, is_cat, keys_a, counts);
-    hipLaunchKernelGGL(k_edge_sort, dim3(cols), dim3(EDGE_THREADS), 0, s, keys_a, keys_b, cap,
-                       counts);
-    hipLaunchKernelGGL(k_edge_pick, dim3(cols), dim3(256), 0, s, keys_a, cap, counts, is_cat,
-                       num_bins, edges);
+    const uint32_t ns = (uint32_t)((rows + step - 1) / step);
+    // chunks per column: about 512 workgroups per pass (2048 measured slower:
+    // per-workgroup set-up), each at least one tile
+    uint32_t nch = (uint32_t)std::max(1, 512 / cols);
+    nch = std::min(nch, std::min(ESORT_MAX_CHUNKS, (ns + ESORT_TILE - 1) / ESORT_TILE));
+    const uint32_t chunk = (ns + nch - 1) / nch;
+    nch = (ns + chunk - 1) / chunk;
+    const dim3 sgrid((ns + EDGE_SAMPLE_THREADS - 1) / EDGE_SAMPLE_THREADS, (unsigned)cols);
+    hipLaunchKernelGGL(k_edge_sample, sgrid, dim3(EDGE_SAMPLE_THREADS), 0, s, x, rs, cs, step, ns,
+                       cap, is_cat, keys_a);
+    const dim3 cgrid(nch, (unsigned)cols);
+    for (int pass = 0; pass < 8; ++pass) {
+        hipLaunchKernelGGL(k_edge_count, cgrid, dim3(EDGE_THREADS), 0, s, keys_a, keys_b, cap, ns,
+                           chunk, pass, is_cat);
+        hipLaunchKernelGGL(k_edge_pass, cgrid, dim3(EDGE_THREADS), 0, s, keys_a, keys_b, cap, ns,
+                           chunk, nch, pass, is_cat);
+    }
+    hipLaunchKernelGGL(k_edge_pick, dim3(cols), dim3(256), 0, s, keys_a, keys_b, cap, ns, nch,
+                       is_cat, num_bins, edges);
     return hipGetLastError();
 }
 

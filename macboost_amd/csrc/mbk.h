@@ -167,8 +167,9 @@ hipError_t launch_tile8_to_layouts(hipStream_t s, const uint64_t *in, int64_t ro
 
 // Quantile edges (Binner.swift:25-56) on the device: x strided as for
 // launch_bin_data, edges[cols][num_bins-2] (0 for categorical or all-NaN
-// columns).  keys_a / keys_b hold edge_sample_cap(rows) u32 per column,
-// counts one u32 per column.
+// columns).  keys_a / keys_b hold edge_sample_cap(rows) u32 per column (the
+// sample keys and the sort's chunk counts); counts (one u32 per column) is
+// not used.
 size_t edge_sample_cap(int64_t rows);
 hipError_t launch_edges(hipStream_t s, const float *x, int64_t rows, int32_t cols, int64_t rs,
                         int64_t cs, int32_t num_bins, const uint8_t *is_cat, uint32_t *keys_a,
