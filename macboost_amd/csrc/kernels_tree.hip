@@ -696,6 +696,101 @@ hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl) {
     return hipGetLastError();
 }
 
+// Label (and weight) checks and the base score's sums over the training rows
+// (validateLabels, Booster.swift:1724-1765; the mean of baseScore, :798-830).
+// One wavefront per block of LABEL_BLOCK rows: lane l adds rows l, l + 64,
+// ... of the block in order in double, then the 64 lane sums meet in a fixed
+// tree (lane l adds lane l + s for s = 32, 16, ..., 1), so the block's sums
+// do not depend on the schedule.  Per block: the two sums (logistic: the
+// positive and total weight, scale_pos_weight applied; otherwise the weighted
+// label sum and total weight) and the first row whose label, or weight, the
+// objective rejects.
+constexpr int64_t LABEL_BLOCK = 65536;
+
+constexpr int LABEL_BATCH = 16;                      // rows per lane in flight
+
+__global__ __launch_bounds__(64) void k_label_stats(int32_t obj, int32_t num_classes,
+                                                    const float *__restrict__ y,
+                                                    const float *__restrict__ w, int64_t n,
+                                                    float spw, LabelStats *__restrict__ out) {
+    constexpr int32_t LOGISTIC = 1, POISSON = 5, TWEEDIE = 6, MULTICLASS = 7;
+    constexpr int64_t STEPS = LABEL_BLOCK / 64;
+    const int lane = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * LABEL_BLOCK;
+    const double sp = (double)spw;
+    double a1 = 0.0, a2 = 0.0;
+    int64_t bad_y = INT64_MAX, bad_w = INT64_MAX;
+    // the lane's rows r0 + k * 64 + lane, k = 0, 1, ... in batches, the next
+    // batch loading while one is added (in row order)
+    float yn[LABEL_BATCH], wn[LABEL_BATCH];
+    auto load = [&](int64_t k0) {
+#pragma unroll
+        for (int j = 0; j < LABEL_BATCH; ++j) {
+            const int64_t i = r0 + (k0 + j) * 64 + lane;
+            yn[j] = i < n ? y[i] : 0.0f;
+            wn[j] = (w && i < n) ? w[i] : 1.0f;
+        }
+    };
+    load(0);
+    for (int64_t k0 = 0; k0 < STEPS && r0 + k0 * 64 < n; k0 += LABEL_BATCH) {
+        float yc[LABEL_BATCH], wc[LABEL_BATCH];
+#pragma unroll
+        for (int j = 0; j < LABEL_BATCH; ++j) { yc[j] = yn[j]; wc[j] = wn[j]; }
+        if (k0 + LABEL_BATCH < STEPS) load(k0 + LABEL_BATCH);
+#pragma unroll
+        for (int j = 0; j < LABEL_BATCH; ++j) {
+            const int64_t i = r0 + (k0 + j) * 64 + lane;
+            if (i >= n) break;
+            const float v = yc[j];
+            bool ok = isfinite(v);
+            if (obj == LOGISTIC) ok = ok && (v == 0.0f || v == 1.0f);
+            if (obj == POISSON || obj == TWEEDIE) ok = ok && v >= 0.0f;
+            if (obj == MULTICLASS) {
+                const float r = rintf(v);
+                ok = ok && r == v && r >= 0.0f && (int64_t)r < num_classes;
+            }
+            if (!ok && bad_y == INT64_MAX) bad_y = i;
+            double wd = 1.0;
+            if (w) {
+                const float wf = wc[j];
+                if (!(isfinite(wf) && wf >= 0.0f) && bad_w == INT64_MAX) bad_w = i;
+                wd = (double)wf;
+            }
+            if (obj == LOGISTIC) {
+                if (v > 0.5f) {
+                    a1 += wd * sp;
+                    a2 += wd * sp;
+                } else {
+                    a2 += wd;
+                }
+            } else {
+                a1 += wd * (double)v;
+                a2 += wd;
+            }
+        }
+    }
+    for (int s = 32; s >= 1; s >>= 1) {
+        a1 += __shfl_down(a1, s, 64);
+        a2 += __shfl_down(a2, s, 64);
+        bad_y = min(bad_y, (int64_t)__shfl_down(bad_y, s, 64));
+        bad_w = min(bad_w, (int64_t)__shfl_down(bad_w, s, 64));
+    }
+    if (lane == 0) out[blockIdx.x] = LabelStats{a1, a2, bad_y, bad_w};
+}
+
+size_t label_stats_blocks(int64_t rows) { return (size_t)((rows + LABEL_BLOCK - 1) / LABEL_BLOCK); }
+
+hipError_t launch_label_stats(hipStream_t s, int32_t objective, int32_t num_classes,
+                              const float *y, const float *w, int64_t rows, float spw,
+                              LabelStats *out) {
+    if (rows <= 0) return hipSuccess;
+    const size_t blocks = label_stats_blocks(rows);
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_label_stats, dim3((unsigned)blocks), dim3(64), 0, s, objective,
+                       num_classes, y, w, rows, spw, out);
+    return hipGetLastError();
+}
+
 // max |g| and max h as f32 bit patterns (reduce_max_gh, Shaders.swift:87-94).
 // Stage 1 (k_grad_max): grad_max_blocks(rows) blocks of 256 threads, one
 // 16-B quad of rows per thread and step, one partial pair per block; with

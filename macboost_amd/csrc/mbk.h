@@ -177,6 +177,18 @@ hipError_t launch_edges(hipStream_t s, const float *x, int64_t rows, int32_t col
 
 hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl);
 
+// Per LABEL block of training rows (k_label_stats): the base score's two
+// double sums and the first rejected label / weight row (INT64_MAX: none).
+struct LabelStats {
+    double s1, s2;
+    int64_t bad_label, bad_weight;
+};
+// label_stats_blocks(rows) entries of out; y, w (nullable) in device memory.
+size_t label_stats_blocks(int64_t rows);
+hipError_t launch_label_stats(hipStream_t s, int32_t objective, int32_t num_classes,
+                              const float *y, const float *w, int64_t rows, float spw,
+                              LabelStats *out);
+
 // Objectives numbered as Booster.swift:5-14.
 struct GradParams {
     int32_t objective;

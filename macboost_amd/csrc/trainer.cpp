@@ -114,32 +114,30 @@ static void parallel_blocks(int64_t n, int64_t block, Fn fn) {
     HostPool::get().run(nblocks, f);
 }
 
-// Rows per block of the sums over every row (base score): each block is
-// summed in row order in double, then the block sums in block order, so
-// the result does not depend on how blocks are spread over threads.
+// Rows per block of the sums over every row (base score): a block's rows
+// are summed in double in the order of the device's k_label_stats (lane l of
+// 64 adds rows l, l + 64, ... in order, then lane l adds lane l + s for
+// s = 32, 16, ..., 1), then the block sums in block order, so the result does
+// not depend on how blocks are spread over threads, or on where they run.
 constexpr int64_t SUM_BLOCK = 65536;
 
-// Per-block double sums (block k: rows [k*SUM_BLOCK, ...) in row order) of
-// two accumulators that add(i, a, b) updates, into s1[k], s2[k].  A task
-// takes four consecutive blocks and steps their rows together: four
-// independent addition chains in flight, each block's sum unchanged.
+// Per-block double sums of two accumulators that add(i, a, b) updates, into
+// s1[k], s2[k] for block k (rows [k*SUM_BLOCK, ...)).
 template <typename Add>
 static void sum_blocks(int64_t n, double *s1, double *s2, Add add) {
-    constexpr int G = 4;
-    parallel_blocks(n, G * SUM_BLOCK, [&](int64_t a, int64_t b) {
-        double x[G] = {}, y[G] = {};
-        if (b - a == G * SUM_BLOCK) {
-            for (int64_t i = 0; i < SUM_BLOCK; ++i)
-                for (int j = 0; j < G; ++j) add(a + j * SUM_BLOCK + i, x[j], y[j]);
-        } else {                                     // the ragged last task
-            for (int j = 0; j < G; ++j)
-                for (int64_t i = a + j * SUM_BLOCK; i < std::min(b, a + (j + 1) * SUM_BLOCK); ++i)
-                    add(i, x[j], y[j]);
+    parallel_blocks(n, SUM_BLOCK, [&](int64_t a, int64_t b) {
+        double x[64] = {}, y[64] = {};
+        for (int64_t r = a; r < b; r += 64) {
+            const int m = (int)std::min<int64_t>(64, b - r);
+            for (int l = 0; l < m; ++l) add(r + l, x[l], y[l]);
         }
-        for (int j = 0; j < G && a + j * SUM_BLOCK < b; ++j) {
-            s1[(size_t)(a / SUM_BLOCK) + j] = x[j];
-            s2[(size_t)(a / SUM_BLOCK) + j] = y[j];
-        }
+        for (int st = 32; st >= 1; st >>= 1)
+            for (int l = 0; l < st; ++l) {
+                x[l] += x[l + st];
+                y[l] += y[l + st];
+            }
+        s1[(size_t)(a / SUM_BLOCK)] = x[0];
+        s2[(size_t)(a / SUM_BLOCK)] = y[0];
     });
 }
 
@@ -498,6 +496,7 @@ struct Trainer {
     // kept[i] of a sampled level-wise tree, for the terminal walk's counts
     DevBuf<uint8_t> kept;
     bool labels_ready = false;      // labels already uploaded during the setup
+    bool weights_ready = false;     // weights too
     // gradient-maxima partials the last tree's walk left for the next tree
     // (0: the next tree runs its own gradient pass)
     int walk_gparts = 0;
@@ -785,6 +784,32 @@ static void check_leakage(bool verbose, const float *x, int64_t rows, int64_t co
     }
 }
 
+// The base score from the two sums over every row (baseScore,
+// Booster.swift:798-830): logistic, the log odds of the (scale_pos_weight
+// weighted) positive share; otherwise the weighted label mean (its log for
+// Poisson and Tweedie).
+static float base_from_sums(const Params &p, double s1, double s2) {
+    if (p.objective == OBJ_LOGISTIC) {
+        float pr = (float)(s1 / std::max(s2, 1e-12));
+        pr = std::min(std::max(pr, 1e-6f), 1.0f - 1e-6f);
+        return std::log(pr / (1.0f - pr));
+    }
+    const float m = s2 > 0 ? (float)(s1 / s2) : 0.0f;
+    if (p.objective == OBJ_POISSON || p.objective == OBJ_TWEEDIE) {
+        if (!(m > 0)) invalid(objective_name(p.objective) + " requires a positive label mean");
+        return std::log(m);
+    }
+    return m;
+}
+
+// Objectives whose base score is a sum over every row (the device computes
+// it with the label checks, k_label_stats); the others take a subsample
+// quantile or class counts on the host.
+static bool sums_base(const Params &p) {
+    return p.objective != OBJ_MAE && p.objective != OBJ_QUANTILE &&
+           p.objective != OBJ_MULTICLASS;
+}
+
 static float base_score(const Params &p, const float *y, const float *w, int64_t n) {
     if (p.objective == OBJ_MAE || p.objective == OBJ_QUANTILE) {   // :786-794, :798-801
         const float q = p.objective == OBJ_MAE ? 0.5f : p.alpha;
@@ -804,25 +829,16 @@ static float base_score(const Params &p, const float *y, const float *w, int64_t
             const double wi = w ? (double)w[i] : 1.0;
             if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
         });
-        double pos = 0, tot = 0;
-        for (int64_t k = 0; k < nblocks; ++k) { pos += s1[(size_t)k]; tot += s2[(size_t)k]; }
-        float pr = (float)(pos / std::max(tot, 1e-12));
-        pr = std::min(std::max(pr, 1e-6f), 1.0f - 1e-6f);
-        return std::log(pr / (1.0f - pr));
+    } else {
+        sum_blocks(n, s1.data(), s2.data(), [&](int64_t i, double &num, double &den) {
+            const double wi = w ? (double)w[i] : 1.0;
+            num += wi * (double)y[i];
+            den += wi;
+        });
     }
-    sum_blocks(n, s1.data(), s2.data(), [&](int64_t i, double &num, double &den) {
-        const double wi = w ? (double)w[i] : 1.0;
-        num += wi * (double)y[i];
-        den += wi;
-    });
-    double num = 0, den = 0;
-    for (int64_t k = 0; k < nblocks; ++k) { num += s1[(size_t)k]; den += s2[(size_t)k]; }
-    float m = den > 0 ? (float)(num / den) : 0.0f;
-    if (p.objective == OBJ_POISSON || p.objective == OBJ_TWEEDIE) {
-        if (!(m > 0)) invalid(objective_name(p.objective) + " requires a positive label mean");
-        return std::log(m);
-    }
-    return m;
+    double a = 0, b = 0;
+    for (int64_t k = 0; k < nblocks; ++k) { a += s1[(size_t)k]; b += s2[(size_t)k]; }
+    return base_from_sums(p, a, b);
 }
 
 static std::string effective_metric(const Params &p) {
@@ -1077,8 +1093,10 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.preds.alloc((size_t)rows * (size_t)K);
     if (w) {
         t.has_weights = true;
-        t.weights.alloc((size_t)rows);
-        upload(t.weights.ptr, w, (size_t)rows * 4, s);
+        if (!t.weights_ready) {
+            t.weights.alloc((size_t)rows);
+            upload(t.weights.ptr, w, (size_t)rows * 4, s);
+        }
     }
     t.base_scores = bases ? *bases : base_scores_of(p, y, w, rows);
     t.base = K > 1 ? 0.0f : t.base_scores[0];
@@ -1291,10 +1309,13 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
     if (!x || !y || rows <= 0 || cols <= 0) internal("null or empty training data");
     Phase ph_all("fit setup");
     validate_params(pin);
-    // The per-row checks (labels, weights) and the base scores run on a host
-    // thread while the device is set up and the features binned.  The checks
-    // keep the reference's order: a later check's error is reported only when
-    // the row checks pass.
+    // The per-row checks (labels, weights) and the base scores: for objectives
+    // whose base score sums every row, on the device right after the labels
+    // arrive (k_label_stats); for the others on a host thread while the
+    // device is set up and the features binned.  The checks keep the
+    // reference's order: a later check's error is reported only when the row
+    // checks pass.
+    const bool dev_rows = sums_base(pin);
     struct HostPrep {
         std::thread th;
         std::exception_ptr err;
@@ -1302,15 +1323,17 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
         void join() { if (th.joinable()) th.join(); }
         ~HostPrep() { join(); }
     } prep;
-    prep.th = std::thread([&] {
-        try {
-            Phase ph("validate inputs");
-            validate_rows(pin, rows, y, w, xv, vrows, yv);
-            prep.bases = base_scores_of(pin, y, w, rows);
-        } catch (...) {
-            prep.err = std::current_exception();
-        }
-    });
+    if (!dev_rows) {
+        prep.th = std::thread([&] {
+            try {
+                Phase ph("validate inputs");
+                validate_rows(pin, rows, y, w, xv, vrows, yv);
+                prep.bases = base_scores_of(pin, y, w, rows);
+            } catch (...) {
+                prep.err = std::current_exception();
+            }
+        });
+    }
     try {
         validate_shape(pin, rows, cols);
         auto tr = std::make_unique<Trainer>();
@@ -1372,6 +1395,7 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
         }
 
         // --- binning on the device: (upload,) quantile edges, bin_data --------
+        std::vector<mbk::LabelStats> row_stats;       // the device row checks' blocks
         double t0 = now_s();
         {
             DevBuf<float> xd;
@@ -1407,10 +1431,30 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
                                         t.bins_fm.ptr));
             t.edges.resize((size_t)cols * ne);
             MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+            hipStream_t cs2 = t.dev->copy_stream;
             t.labels.alloc((size_t)rows);
-            upload(t.labels.ptr, y, (size_t)rows * 4, t.dev->copy_stream);
-            MB_HIP(hipStreamSynchronize(t.dev->copy_stream));
+            upload(t.labels.ptr, y, (size_t)rows * 4, cs2);
             t.labels_ready = true;
+            if (dev_rows) {
+                // the row checks and the base score's sums, on the device
+                if (w) {
+                    t.weights.alloc((size_t)rows);
+                    upload(t.weights.ptr, w, (size_t)rows * 4, cs2);
+                    t.weights_ready = true;
+                }
+                const size_t nblk = mbk::label_stats_blocks(rows);
+                DevBuf<mbk::LabelStats> ls;
+                ls.pooled = true;
+                ls.alloc(nblk);
+                MB_HIP(mbk::launch_label_stats(cs2, p.objective, p.num_classes, t.labels.ptr,
+                                               w ? t.weights.ptr : nullptr, rows,
+                                               p.scale_pos_weight, ls.ptr));
+                row_stats.resize(nblk);
+                MB_HIP(hipMemcpyAsync(row_stats.data(), ls.ptr, nblk * sizeof(mbk::LabelStats),
+                                      hipMemcpyDeviceToHost, cs2));
+                MB_HIP(hipStreamSynchronize(cs2));
+            }
+            MB_HIP(hipStreamSynchronize(cs2));
             if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
             MB_HIP(hipStreamSynchronize(s));
             t.t_edges = now_s() - te;
@@ -1418,6 +1462,23 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
         t.t_bin = now_s() - t0 - t.t_edges;              // the feature upload, if any
         prep.join();
         if (prep.err) std::rethrow_exception(prep.err);
+        if (dev_rows) {
+            // labels, then weights, then the validation labels (validate_rows)
+            int64_t bad_y = INT64_MAX, bad_w = INT64_MAX;
+            double s1 = 0, s2 = 0;
+            for (const mbk::LabelStats &b : row_stats) {
+                bad_y = std::min(bad_y, b.bad_label);
+                bad_w = std::min(bad_w, b.bad_weight);
+                s1 += b.s1;
+                s2 += b.s2;
+            }
+            if (bad_y != INT64_MAX) check_label(p, y, bad_y);
+            if (bad_w != INT64_MAX)
+                invalid("weight at row " + std::to_string(bad_w) + " is " + swift_float(w[bad_w]) +
+                        "; weights must be finite and >= 0");
+            if (xv && yv && vrows > 0) validate_labels(p, yv, vrows);
+            prep.bases = {base_from_sums(p, s1, s2)};
+        }
         Phase ph_rest("labels, buffers");
         if (leak.th.joinable()) leak.th.join();
         if (leak_error) std::rethrow_exception(leak_error);
@@ -1445,6 +1506,7 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
         // the row checks come first in the reference's order
         prep.join();
         if (prep.err) std::rethrow_exception(prep.err);
+        if (dev_rows) validate_rows(pin, rows, y, w, xv, vrows, yv);
         throw;
     }
 }

@@ -160,49 +160,54 @@ void orc_bin_matrix(const float *x, int64_t rows, int32_t cols, int64_t rs, int6
 /* rounded once (the reference uses vDSP, whose order is unspecified).      */
 /* ------------------------------------------------------------------------ */
 
-/* Sums over every row are taken in blocks of 65,536 rows: each block in row
- * order in double, then the block sums in block order (the reference's vDSP
- * sums leave the order unspecified). */
+/* Sums over every row are taken in blocks of 65,536 rows, each block in a
+ * fixed order: 64 partial sums in double, partial l adding rows l, l + 64,
+ * l + 128, ... of the block in row order, then partial l adds partial l + s
+ * for s = 32, 16, 8, 4, 2, 1 (partial 0 is the block's sum); then the block
+ * sums in block order (the reference's vDSP sums leave the order
+ * unspecified; the library's device reduction uses this one). */
 #define ORC_SUM_BLOCK 65536
+
+static void orc_block_sums(const float *y, const float *w, int64_t rows, int32_t obj, double spw,
+                           int64_t b, double *out1, double *out2) {
+    double a1[64], a2[64];
+    for (int l = 0; l < 64; ++l) { a1[l] = 0.0; a2[l] = 0.0; }
+    const int64_t lo = b * ORC_SUM_BLOCK;
+    const int64_t hi = lo + ORC_SUM_BLOCK < rows ? lo + ORC_SUM_BLOCK : rows;
+    for (int64_t r = lo; r < hi; r += 64) {
+        for (int l = 0; l < 64 && r + l < hi; ++l) {
+            const int64_t i = r + l;
+            const double wi = w ? (double)w[i] : 1.0;
+            if (obj == ORC_OBJ_LOGISTIC) {
+                if (y[i] > 0.5f) { a1[l] += wi * spw; a2[l] += wi * spw; } else a2[l] += wi;
+            } else {
+                a1[l] += wi * (double)y[i];
+                a2[l] += wi;
+            }
+        }
+    }
+    for (int s = 32; s >= 1; s >>= 1)
+        for (int l = 0; l < s; ++l) { a1[l] += a1[l + s]; a2[l] += a2[l + s]; }
+    *out1 = a1[0];
+    *out2 = a2[0];
+}
 
 float orc_base_score(const float *y, const float *w, int64_t rows, int32_t obj, float spw) {
     const int64_t nblk = (rows + ORC_SUM_BLOCK - 1) / ORC_SUM_BLOCK;
     double *s1 = (double *)calloc((size_t)(nblk > 0 ? nblk : 1), sizeof(double));
     double *s2 = (double *)calloc((size_t)(nblk > 0 ? nblk : 1), sizeof(double));
-    if (obj == ORC_OBJ_LOGISTIC) {
 #pragma omp parallel for schedule(dynamic, 1)
-        for (int64_t b = 0; b < nblk; ++b) {
-            double pos = 0, tot = 0;
-            const int64_t hi = (b + 1) * ORC_SUM_BLOCK < rows ? (b + 1) * ORC_SUM_BLOCK : rows;
-            for (int64_t i = b * ORC_SUM_BLOCK; i < hi; ++i) {
-                double wi = w ? (double)w[i] : 1.0;
-                if (y[i] > 0.5f) { pos += wi * spw; tot += wi * spw; } else tot += wi;
-            }
-            s1[b] = pos; s2[b] = tot;
-        }
-        double pos = 0, tot = 0;
-        for (int64_t b = 0; b < nblk; ++b) { pos += s1[b]; tot += s2[b]; }
-        free(s1); free(s2);
-        float p = (float)(pos / (tot > 1e-12 ? tot : 1e-12));
+    for (int64_t b = 0; b < nblk; ++b) orc_block_sums(y, w, rows, obj, (double)spw, b, &s1[b], &s2[b]);
+    double a = 0, c = 0;
+    for (int64_t b = 0; b < nblk; ++b) { a += s1[b]; c += s2[b]; }
+    free(s1); free(s2);
+    if (obj == ORC_OBJ_LOGISTIC) {
+        float p = (float)(a / (c > 1e-12 ? c : 1e-12));
         if (p < 1e-6f) p = 1e-6f;
         if (p > 1.0f - 1e-6f) p = 1.0f - 1e-6f;
         return logf(p / (1.0f - p));
     }
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int64_t b = 0; b < nblk; ++b) {
-        double num = 0, den = 0;
-        const int64_t hi = (b + 1) * ORC_SUM_BLOCK < rows ? (b + 1) * ORC_SUM_BLOCK : rows;
-        for (int64_t i = b * ORC_SUM_BLOCK; i < hi; ++i) {
-            double wi = w ? (double)w[i] : 1.0;
-            num += wi * (double)y[i];
-            den += wi;
-        }
-        s1[b] = num; s2[b] = den;
-    }
-    double num = 0, den = 0;
-    for (int64_t b = 0; b < nblk; ++b) { num += s1[b]; den += s2[b]; }
-    free(s1); free(s2);
-    float m = den > 0 ? (float)(num / den) : 0.0f;
+    float m = c > 0 ? (float)(a / c) : 0.0f;
     if (obj == ORC_OBJ_POISSON || obj == ORC_OBJ_TWEEDIE) return logf(m);
     return m;
 }

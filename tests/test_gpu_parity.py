@@ -1062,3 +1062,65 @@ def test_treeshap_wide_data_matches_oracle():
     assert c.shape == (rows, cols + 1)
     want = O.treeshap(model_io.forest_from_json(obj), obj["baseScore"], obj["numBins"], x)
     assert np.allclose(c, want, rtol=1e-5, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# Row checks and the base score's sums on the device (k_label_stats)
+# --------------------------------------------------------------------------
+
+def test_device_row_checks_messages():
+    # the first offending row over every block, with the reference's message
+    # (Booster.swift:1724-1765); labels before weights before categoricals
+    rows = 200_000
+    x = np.random.default_rng(1).random((3, rows), dtype=np.float32)
+    y = np.zeros(rows, np.float32)
+    bad = y.copy()
+    bad[[150_001, 170_000]] = np.nan
+    with pytest.raises(mb.MacBoostError, match=r"label at row 150001 is nan; labels must be finite"):
+        mb.train({"num_trees": 1}, x, bad, feature_major=True)
+    yb = (np.arange(rows) % 2).astype(np.float32)
+    yb[65_536] = 2.0
+    with pytest.raises(mb.MacBoostError,
+                       match=r"label at row 65536 is 2.0; binary objective requires labels in \{0, 1\}"):
+        mb.train({"num_trees": 1, "objective": "binary"}, x, yb, feature_major=True)
+    w = np.ones(rows, np.float32)
+    w[[99_999, 131_072]] = -1.0
+    with pytest.raises(mb.MacBoostError, match=r"weight at row 99999 is -1.0; weights must be finite"):
+        mb.train({"num_trees": 1}, x, y, feature_major=True, sample_weight=w)
+    # a bad label wins over a bad weight and over a bad categorical value
+    xc = x.copy()
+    xc[0, 5] = 999.0
+    with pytest.raises(mb.MacBoostError, match=r"label at row 150001 is nan"):
+        mb.train({"num_trees": 1, "categorical_features": [0]}, xc, bad, feature_major=True,
+                 sample_weight=w)
+
+
+@pytest.mark.parametrize("case", ["cancel", "l2", "logistic_w", "poisson"])
+def test_device_base_score_matches_oracle(case):
+    rng = np.random.default_rng(11)
+    rows = 130 if case == "cancel" else 200_003
+    x = rng.random((2, rows), dtype=np.float32)
+    w = None
+    params = {"num_trees": 1, "max_depth": 2}
+    if case == "cancel":
+        y = np.ones(rows, np.float32)
+        y[0], y[64] = 1e17, -1e17
+        obj = O.OBJ_L2
+    elif case == "l2":
+        y = (rng.standard_normal(rows) * 1e3 + 0.1).astype(np.float32)
+        obj = O.OBJ_L2
+    elif case == "logistic_w":
+        y = (rng.random(rows) < 0.3).astype(np.float32)
+        w = rng.random(rows).astype(np.float32)
+        params.update(objective="binary", scale_pos_weight=2.5)
+        obj = O.OBJ_LOGISTIC
+    else:
+        y = rng.poisson(3.0, rows).astype(np.float32)
+        params.update(objective="poisson")
+        obj = O.OBJ_POISSON
+    h = mb.train(params, x, y, feature_major=True, sample_weight=w)
+    got = np.float32(model_io.saved_model(h)["baseScore"])
+    spw = 2.5 if case == "logistic_w" else 1.0
+    assert got == np.float32(O.base_score(y, w, obj, spw))
+    if case == "cancel":
+        assert got == np.float32(128 / 130)

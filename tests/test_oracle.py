@@ -621,6 +621,88 @@ def test_label_quantile_base_score(oracle, rows, q):
     assert O.base_score(y, objective=obj, alpha=q) == want
 
 
+# --------------------------------------------------------------------------
+# Base score of the summing objectives (Booster.swift:798-830)
+# --------------------------------------------------------------------------
+
+def _ulp32(v):
+    v = np.float32(v)
+    return float(np.spacing(abs(v)))
+
+
+def _block_order_sum(vals):
+    # the fixed order: per 65,536-row block, 64 lane sums (lane l: rows l,
+    # l + 64, ... in order), lanes folded l += l + s for s = 32 .. 1, then the
+    # blocks in order
+    total = 0.0
+    for b0 in range(0, len(vals), 65536):
+        blk = vals[b0:b0 + 65536]
+        lanes = [0.0] * 64
+        for i, v in enumerate(blk):
+            lanes[i % 64] += float(v)
+        s = 32
+        while s >= 1:
+            for l in range(s):
+                lanes[l] += lanes[l + s]
+            s //= 2
+        total += lanes[0]
+    return total
+
+
+def test_base_score_integer_labels_exact(oracle):
+    # integer labels: every partial sum is exact, so the mean is the exact one
+    rows = 200_003
+    y = np.random.default_rng(3).integers(-50, 51, rows).astype(np.float32)
+    exact = math.fsum(y.astype(np.float64))
+    assert O.base_score(y) == np.float32(exact / rows)
+    w = np.random.default_rng(4).integers(0, 4, rows).astype(np.float32)
+    num = math.fsum((w.astype(np.float64) * y.astype(np.float64)))
+    den = math.fsum(w.astype(np.float64))
+    assert O.base_score(y, w) == np.float32(num / den)
+
+
+@pytest.mark.parametrize("rows", [1, 63, 65_537, 200_000])
+def test_base_score_mean_order(oracle, rows):
+    # random labels: within one float ulp of the exact mean, and equal to the
+    # fixed-order double sum restated in Python
+    y = (np.random.default_rng(rows).standard_normal(rows) * 1e3 + 0.1).astype(np.float32)
+    got = O.base_score(y)
+    exact = math.fsum(y.astype(np.float64)) / rows
+    assert abs(float(got) - exact) <= _ulp32(exact)
+    if rows <= 65_537:
+        assert got == np.float32(_block_order_sum(y) / rows)
+
+
+def test_base_score_cancellation_pins_order(oracle):
+    # 1e17 and -1e17 at rows 0 and 64 (the same lane) cancel before any 1.0
+    # meets them: the fixed order keeps all 128 ones; a row-order sum loses the
+    # 63 ones added to 1e17 (half its ulp is 8), a pairwise sum loses others
+    y = np.ones(130, np.float32)
+    y[0], y[64] = 1e17, -1e17
+    assert O.base_score(y) == np.float32(128 / 130)
+    row_order = 0.0
+    for v in y:
+        row_order += float(v)
+    assert np.float32(row_order / 130) != np.float32(128 / 130)
+
+
+def test_base_score_logistic_and_log_link(oracle):
+    rows = 150_000
+    rng = np.random.default_rng(9)
+    y = (rng.random(rows) < 0.3).astype(np.float32)
+    w = rng.random(rows).astype(np.float32)
+    spw = 2.5
+    pos = math.fsum(w[y > 0.5].astype(np.float64) * spw)
+    tot = pos + math.fsum(w[y <= 0.5].astype(np.float64))
+    p = np.float32(pos / tot)
+    want = np.log(p / (np.float32(1) - p))
+    got = O.base_score(y, w, O.OBJ_LOGISTIC, spw)
+    assert abs(got - want) <= 2 * _ulp32(want)
+    yp = rng.poisson(3.0, rows).astype(np.float32)
+    assert O.base_score(yp, objective=O.OBJ_POISSON) == np.log(
+        np.float32(math.fsum(yp.astype(np.float64)) / rows))
+
+
 def _stump_rows(m, x):
     """Rows going left at the root of tree 0 (numeric split, raw values)."""
     f, thr = m.forest.feature[0, 0], m.forest.threshold[0, 0]
