@@ -2317,13 +2317,15 @@ hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active
 }
 
 // Plan level d from level d-1's routed counts (decide_splits phase 2,
-// Shaders.swift:1454-1488, with counts from the partition).  Thread p owns
-// parent p (at most PLAN_MAX_PAIRS parents, so one pass); what later steps
-// read back goes through LDS.
-__global__ __launch_bounds__(1024) void k_plan_level(
-    Shape sh, LevelArgs la, uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
-    const uint32_t *seg_start_prev, uint32_t *seg_start_next, uint32_t *count,
-    const uint64_t *cursors, const TreeOut out, Pair *pairs, HistItem *items) {
+// Shaders.swift:1454-1488, with counts from the partition), run by one
+// 1024-thread workgroup.  Thread p owns parent p (at most PLAN_MAX_PAIRS
+// parents, so one pass); what later steps read back goes through LDS.  The
+// partition cursors are read at device scope: the partition's last
+// workgroup plans while the kernel that updated them is still resident.
+__device__ void plan_level(const Shape &sh, const LevelArgs &la, uint32_t target_items,
+                           uint32_t min_chunk, TreeCtl *ctl, const uint32_t *seg_start_prev,
+                           uint32_t *seg_start_next, uint32_t *count, const uint64_t *cursors,
+                           const TreeOut &out, Pair *pairs, HistItem *items) {
     __shared__ uint32_t wave_tot[17];
     __shared__ uint32_t s_active;
     __shared__ uint32_t s_idx[PLAN_MAX_PAIRS];       // split flag, then pair index
@@ -2342,7 +2344,9 @@ __global__ __launch_bounds__(1024) void k_plan_level(
         const uint32_t n = ls_prev + p;
         const int32_t feat = out.split[n].feature;
         const uint32_t cnt = count[n];
-        const uint32_t left = (uint32_t)cursors[(size_t)p * CURSOR_STRIDE];
+        const uint32_t left = (uint32_t)__hip_atomic_load(&cursors[(size_t)p * CURSOR_STRIDE],
+                                                          __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
         seg = seg_start_prev[p];
         split = feat >= 0 && cnt >= 1;
         cl = split ? left : 0u;
@@ -2385,6 +2389,14 @@ __global__ __launch_bounds__(1024) void k_plan_level(
     }
     write_items(sh, ctl, la.level, pairs, items, s_cnt, s_seg, s_first, num_pairs, target_items,
                 min_chunk, wave_tot);
+}
+
+__global__ __launch_bounds__(1024) void k_plan_level(
+    Shape sh, LevelArgs la, uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
+    const uint32_t *seg_start_prev, uint32_t *seg_start_next, uint32_t *count,
+    const uint64_t *cursors, const TreeOut out, Pair *pairs, HistItem *items) {
+    plan_level(sh, la, target_items, min_chunk, ctl, seg_start_prev, seg_start_next, count,
+               cursors, out, pairs, items);
 }
 
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,
@@ -2513,9 +2525,8 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 // wavefront slice comes from a ballot at store time.
 __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
-    Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start,
-    const uint32_t *__restrict__ count, const TreeOut out, uint64_t *cursors,
-    int write_entries) {
+    Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start, uint32_t *count,
+    const TreeOut out, uint64_t *cursors, int write_entries, RoutePlan rp, int has_plan) {
     extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
     __shared__ uint32_t s_mask[2][8];
     __shared__ uint32_t wave_tot[PART_WAVES + 1];
@@ -2531,7 +2542,13 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     __syncthreads();
     const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
     uint32_t b = blockIdx.x;
-    if (b >= total_blocks) return;                   // uniform per block
+    if (b >= total_blocks) {                         // uniform per block
+        // nothing to partition: the first workgroup plans alone
+        if (has_plan && total_blocks == 0 && blockIdx.x == 0)
+            plan_level(sh, rp.next, rp.target_items, rp.min_chunk, rp.ctl, seg_start, rp.seg_next,
+                       count, cursors, out, rp.pairs, rp.items);
+        return;
+    }
 
     // logical block b: its node slot, segment, count, first entry and split
     struct Blk {
@@ -2645,17 +2662,38 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         buf ^= 1;
         b = bn;
     }
+    if (has_plan) {
+        // the last of the busy workgroups plans the next level.  Every cursor
+        // add of a workgroup has returned before its count add, and the
+        // planner reads the cursors at device scope.
+        __shared__ uint32_t s_last;
+        const uint32_t busy = min(gridDim.x, total_blocks);
+        if (tid == 0) s_last = atomicAdd(rp.done, 1u) == busy - 1u ? 1u : 0u;
+        __syncthreads();
+        if (s_last) {
+            if (tid == 0) atomicExch(rp.done, 0u);
+            plan_level(sh, rp.next, rp.target_items, rp.min_chunk, rp.ctl, seg_start, rp.seg_next,
+                       count, cursors, out, rp.pairs, rp.items);
+        }
+    }
 }
 
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
-                        const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
-                        uint64_t *cursors, uint32_t max_blocks, bool write_entries) {
+                        const uint32_t *seg_start, uint32_t *count, const TreeOut out,
+                        uint64_t *cursors, uint32_t max_blocks, bool write_entries,
+                        const RoutePlan *plan) {
     // cursors were zeroed by this level's k_decide
+    if (max_blocks < 1) return hipErrorInvalidValue;
+    RoutePlan rp{};
+    if (plan) {
+        if ((plan->next.num_level >> 1) > PLAN_MAX_PAIRS || !plan->done) return hipErrorInvalidValue;
+        rp = *plan;
+    }
     const size_t lds = (size_t)la.num_level * sizeof(uint32_t);
     hipLaunchKernelGGL(k_route, dim3(max_blocks), dim3(PART_THREADS), lds, s, sh, la, bins_fm,
                        order_in, order_out, seg_start, count, out, cursors,
-                       write_entries ? 1 : 0);
+                       write_entries ? 1 : 0, rp, plan ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -347,10 +347,24 @@ hipError_t launch_renew(hipStream_t s, const uint8_t *bins_fm, int64_t rows, int
 // is the persistent grid (any size >= 1; each block takes every max_blocks-th
 // of the level's PART_ENTRIES-entry blocks).  write_entries = false only
 // counts (terminal level).
+// With plan, the partition's last workgroup then plans the next level as
+// launch_plan_level(plan->next, ...) would, from seg_start into
+// plan->seg_next; plan->done is one u32, zero before the launch and zero
+// again after it.
+struct RoutePlan {
+    LevelArgs next;
+    uint32_t target_items, min_chunk;
+    TreeCtl *ctl;
+    uint32_t *seg_next;
+    Pair *pairs;
+    HistItem *items;
+    uint32_t *done;
+};
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
-                        const uint32_t *seg_start, const uint32_t *count, const TreeOut out,
-                        uint64_t *cursors, uint32_t max_blocks, bool write_entries);
+                        const uint32_t *seg_start, uint32_t *count, const TreeOut out,
+                        uint64_t *cursors, uint32_t max_blocks, bool write_entries,
+                        const RoutePlan *plan = nullptr);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,

@@ -502,6 +502,7 @@ struct Trainer {
     int walk_gparts = 0;
     bool kept_walk = false;
     DevBuf<uint64_t> route_cursor;
+    DevBuf<uint32_t> route_done;    // the partition's finished-workgroup count (zero between launches)
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
     DevBuf<mbk::HistItem> items;
@@ -552,6 +553,12 @@ struct Trainer {
     bool prof_tree(int tree) const {
         return profiling && (tree - prof_first_tree) % prof_every == 0;
     }
+    // level `next`'s planning, run by the partition's last workgroup
+    mbk::RoutePlan route_plan(const mbk::LevelArgs &next, uint32_t *seg_next) {
+        return mbk::RoutePlan{next,        (uint32_t)target_items, (uint32_t)min_chunk,
+                              ctl.ptr,     seg_next,               pairs.ptr,
+                              items.ptr,   route_done.ptr};
+    }
     struct HistEvent { hipEvent_t start, end; int level; };
     std::vector<HistEvent> events;
     int64_t prof_launches = 0;
@@ -583,6 +590,7 @@ struct Trainer {
         for (DevBuf<int64_t> *b : {&hist_a, &hist_b, &node_g, &node_h}) b->pooled = true;
         order_a.pooled = order_b.pooled = partials.pooled = items.pooled = true;
         mono.pooled = route_cursor.pooled = pairs.pooled = results.pooled = true;
+        route_done.pooled = true;
         bounds.pooled = ctl.pooled = true;
         lw_state.pooled = lw_open.pooled = lwb_state.pooled = lwb_cand.pooled = true;
         spec_split.pooled = true;
@@ -1164,6 +1172,8 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         2 * (int64_t)t.dev->num_cus,
         (rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES + t.max_level_nodes);
     t.route_cursor.alloc((size_t)t.max_level_nodes * mbk::CURSOR_STRIDE);
+    t.route_done.alloc(1);
+    MB_HIP(hipMemsetAsync(t.route_done.ptr, 0, sizeof(uint32_t), t.dev->stream));
 
     // histogram work decomposition
     const size_t lds = mbk::hist_lds_size();
@@ -1782,13 +1792,10 @@ static void grow_levelwise(Trainer &t, int tree) {
         if (terminal) {
             // a sampled tree counts its kept rows with the partition; every
             // row's prediction then comes from one walk (Booster.swift:1568-1580)
+            const mbk::RoutePlan rp = t.route_plan(ln, seg_next);
             MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
                                      t.count.ptr, out, t.route_cursor.ptr,
-                                     t.route_grid, false));
-            MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items,
-                                          (uint32_t)t.min_chunk, ctl, seg_cur, seg_next,
-                                          t.count.ptr, t.route_cursor.ptr, out, t.pairs.ptr,
-                                          t.items.ptr));
+                                     t.route_grid, false, &rp));
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, true));
             if (t.renewal) renew_tree(t, out, nullptr);
@@ -1796,12 +1803,10 @@ static void grow_levelwise(Trainer &t, int tree) {
                                               t.preds_cur));
             break;
         }
+        const mbk::RoutePlan rp = t.route_plan(ln, seg_next);
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
                                  t.count.ptr, out, t.route_cursor.ptr,
-                                 t.route_grid, true));
-        MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
-                                      ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr, out,
-                                      t.pairs.ptr, t.items.ptr));
+                                 t.route_grid, true, &rp));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
@@ -1966,11 +1971,9 @@ static void grow_leafwise_rounds(Trainer &t, int tree) {
         mbk::LevelArgs lp{r, (uint32_t)((1u << r) - 1), 1u << r, last ? 1u : 0u};
         mbk::LevelArgs ln{r + 1, (uint32_t)((1u << (r + 1)) - 1), 1u << (r + 1), last ? 1u : 0u};
         // the deepest children are never evaluated: count them, move nothing
+        const mbk::RoutePlan rp = t.route_plan(ln, seg_next);
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
-                                 t.count.ptr, spec, t.route_cursor.ptr, t.route_grid, !last));
-        MB_HIP(mbk::launch_plan_level(s, sh, ln, (uint32_t)t.target_items, (uint32_t)t.min_chunk,
-                                      ctl, seg_cur, seg_next, t.count.ptr, t.route_cursor.ptr,
-                                      spec, t.pairs.ptr, t.items.ptr));
+                                 t.count.ptr, spec, t.route_cursor.ptr, t.route_grid, !last, &rp));
         if (last) break;
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
