@@ -1241,7 +1241,8 @@ hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, Tr
 __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__restrict__ preds,
                                                   const float *__restrict__ labels,
                                                   const float *__restrict__ weights, int64_t rows,
-                                                  const TreeCtl *ctl, Entry *__restrict__ order) {
+                                                  const TreeCtl *ctl, Entry *__restrict__ order,
+                                                  int implicit_rows) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
@@ -1251,17 +1252,19 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
     row_grad_at(gp, preds, labels, weights, i, g, h);
     const int qg = (int)rintf(g * gscale);
     const uint32_t qh = (uint32_t)rintf(h * hscale);
-    Entry e;
-    e.row = (uint32_t)i;
-    e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
-    store_entry_nt(order + i, e);
+    const uint32_t ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
+    if (implicit_rows) {
+        __builtin_nontemporal_store(ghq, reinterpret_cast<uint32_t *>(order) + i);
+    } else {
+        store_entry_nt(order + i, Entry{(uint32_t)i, ghq});
+    }
 }
 
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           const TreeCtl *ctl, Entry *order) {
+                           const TreeCtl *ctl, Entry *order, bool implicit_rows) {
     hipLaunchKernelGGL(k_quantize, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, gp,
-                       preds, labels, weights, rows, ctl, order);
+                       preds, labels, weights, rows, ctl, order, implicit_rows ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1344,7 +1347,9 @@ __device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0
 // lay: where each tile's rows sit (the gather layout, or the planar root
 // copy, whose last tile's loads run into the next row: those bytes land in
 // padding columns, which are never reduced).
-template <int W>
+// IMPLICIT: order holds one u32 packed (qg, qh) per row of the root, entry j
+// being row j (k_quantize's implicit form).
+template <int W, bool IMPLICIT>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
                                                        const Entry *__restrict__ order,
                                                        const HistItem *__restrict__ items,
@@ -1397,13 +1402,19 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         const size_t row_bytes =
             (size_t)((int32_t)item.tile == lay.last_tile ? lay.last_stride : lay.stride);
         const Entry *ent = order + item.start;
+        const uint32_t *ent_q = reinterpret_cast<const uint32_t *>(order) + item.start;
+        // entry j of the item (IMPLICIT: row start + j with its packed word)
+        auto entry = [&](uint32_t j) {
+            if constexpr (IMPLICIT) return Entry{item.start + j, ent_q[j]};
+            else return ent[j];
+        };
         const uint32_t g0 = (uint32_t)wave * RPB;
         // loads past the item's end read its last entry (in bounds); their
         // rows are given value 0 when processed
         Entry er[ER];
         RowRaw<P> dr[DR];
 #pragma unroll
-        for (int k = 0; k < ER; ++k) er[k] = ent[min(g0 + (uint32_t)k * stride + rl, last)];
+        for (int k = 0; k < ER; ++k) er[k] = entry(min(g0 + (uint32_t)k * stride + rl, last));
 #pragma unroll
         for (int k = 0; k < DR; ++k) dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * row_bytes, cx);
         auto process = [&](uint32_t g, const Entry &e, const RowRaw<P> &raw) {
@@ -1431,7 +1442,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                 process(g, er[k], dr[k % DR]);
                 // refill: data for batch +DR (its entry is already held), entry for batch +ER
                 dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * row_bytes, cx);
-                er[k] = ent[min(g + (uint32_t)ER * stride + rl, last)];
+                er[k] = entry(min(g + (uint32_t)ER * stride + rl, last));
             }
         }
         // tail: fewer than ER batches left; entries are held, data up to DR ahead
@@ -1485,7 +1496,8 @@ size_t planar_bytes(const Shape &sh) {
 
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, const Entry *order,
                        const HistItem *items, const TreeCtl *ctl, uint64_t *partials, int grid,
-                       const HistLayout *layout, hipEvent_t start, hipEvent_t stop) {
+                       const HistLayout *layout, hipEvent_t start, hipEvent_t stop,
+                       bool implicit_rows) {
     const HistLayout lay = layout ? *layout : gather_layout(sh);
     if (layout) {
         // the planar copy: 64-wide tiles, every stride a 16-B multiple
@@ -1496,21 +1508,29 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
             return hipErrorInvalidValue;
     }
     switch (sh.tile_w) {
+#define MBK_COMMA ,
+#define MBK_HIST_LAUNCH(KERN)                                                                    \
+    {                                                                                            \
+        auto *kern = &KERN;                                                                      \
+        if (start || stop)                                                                       \
+            hipExtLaunchKernelGGL(kern, dim3(grid), dim3(HIST_THREADS), 0, s, start, stop, 0,    \
+                                  tiled, order, items, ctl, partials, lay, sh.num_bins, sh.cols); \
+        else                                                                                     \
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order, items,  \
+                               ctl, partials, lay, sh.num_bins, sh.cols);                        \
+    }
 #define MBK_HIST_CASE(WW)                                                                        \
     case WW:                                                                                     \
-        if (start || stop)                                                                       \
-            hipExtLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, start, stop, \
-                                  0, tiled, order, items, ctl, partials, lay, sh.num_bins,       \
-                                  sh.cols);                                                      \
-        else                                                                                     \
-            hipLaunchKernelGGL(k_hist<WW>, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order,   \
-                               items, ctl, partials, lay, sh.num_bins, sh.cols);                 \
+        if (implicit_rows) MBK_HIST_LAUNCH(k_hist<WW MBK_COMMA true>)                           \
+        else MBK_HIST_LAUNCH(k_hist<WW MBK_COMMA false>)                                         \
         break;
         MBK_HIST_CASE(8)
         MBK_HIST_CASE(16)
         MBK_HIST_CASE(32)
         MBK_HIST_CASE(64)
 #undef MBK_HIST_CASE
+#undef MBK_HIST_LAUNCH
+#undef MBK_COMMA
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -2523,6 +2543,7 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 // entry k * PART_THREADS + t of the logical block; a row's left flag lives
 // as bit k of a per-thread mask, and its rank among the left rows of its
 // wavefront slice comes from a ballot at store time.
+template <bool IMPLICIT>
 __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start, uint32_t *count,
@@ -2571,12 +2592,18 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         k.sp = out.split[n];
     };
     auto load_entries = [&](const Blk &k, Entry (&e)[PART_PER_THREAD]) {
-        const Entry *src = order_in + k.start + k.first;
+        const uint32_t e0 = k.start + k.first;
+        const Entry *src = order_in + e0;
+        // implicit input: entry j is row j with its packed word
+        const uint32_t *src_q = reinterpret_cast<const uint32_t *>(order_in) + e0;
 #pragma unroll
         for (int j = 0; j < PART_PER_THREAD; ++j) {
             const uint32_t i = (uint32_t)(j * PART_THREADS + tid);
             e[j] = Entry{0u, 0u};
-            if (i < k.nvalid) e[j] = load_entry_nt(src + i);
+            if (i < k.nvalid) {
+                if constexpr (IMPLICIT) e[j] = Entry{e0 + i, __builtin_nontemporal_load(src_q + i)};
+                else e[j] = load_entry_nt(src + i);
+            }
         }
     };
 
@@ -2682,7 +2709,7 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, uint32_t *count, const TreeOut out,
                         uint64_t *cursors, uint32_t max_blocks, bool write_entries,
-                        const RoutePlan *plan) {
+                        const RoutePlan *plan, bool implicit_in) {
     // cursors were zeroed by this level's k_decide
     if (max_blocks < 1) return hipErrorInvalidValue;
     RoutePlan rp{};
@@ -2691,7 +2718,8 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
         rp = *plan;
     }
     const size_t lds = (size_t)la.num_level * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_route, dim3(max_blocks), dim3(PART_THREADS), lds, s, sh, la, bins_fm,
+    auto *kern = implicit_in ? &k_route<true> : &k_route<false>;
+    hipLaunchKernelGGL(kern, dim3(max_blocks), dim3(PART_THREADS), lds, s, sh, la, bins_fm,
                        order_in, order_out, seg_start, count, out, cursors,
                        write_entries ? 1 : 0, rp, plan ? 1 : 0);
     return hipGetLastError();

@@ -228,10 +228,12 @@ struct SampleParams {
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
                          Entry *order, float *h_kept, uint8_t *kept);
-// Every row quantised with ctl->max_gh into order[i] = {i, packed (qg, qh)}.
+// Every row quantised with ctl->max_gh into order[i] = {i, packed (qg, qh)};
+// with implicit_rows, into the u32 words ((uint32_t *)order)[i] = packed
+// (qg, qh) only: the root's rows in order, row i being entry i.
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           const TreeCtl *ctl, Entry *order);
+                           const TreeCtl *ctl, Entry *order, bool implicit_rows = false);
 
 // Where the histogram kernel finds tile t of row r: at
 // base + t * tile_step + r * (t == last_tile ? last_stride : stride).
@@ -253,10 +255,13 @@ size_t planar_bytes(const Shape &sh);    // including 64 zero bytes of overread
 // Histogram items -> packed partials [item][B][W] (64-bit words, see
 // HIST_QH_BITS).  layout null: the gather layout.  With start / stop events
 // (created by the caller), they take the kernel's own dispatch timestamps.
+// implicit_rows: order holds launch_quantize's implicit u32 words (the root
+// of an unsampled tree; entry j is row j).
 hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled,
                        const Entry *order, const HistItem *items, const TreeCtl *ctl,
                        uint64_t *partials, int grid, const HistLayout *layout = nullptr,
-                       hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+                       hipEvent_t start = nullptr, hipEvent_t stop = nullptr,
+                       bool implicit_rows = false);
 size_t hist_lds_size();   // static LDS of one histogram workgroup
 // Planar copy of the gather layout for the root pass over every row; out
 // holds planar_bytes(sh) bytes (the last tile's loads run up to 16 B past its
@@ -360,11 +365,13 @@ struct RoutePlan {
     HistItem *items;
     uint32_t *done;
 };
+// implicit_in: order_in holds launch_quantize's implicit u32 words (the
+// root level of an unsampled tree).
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, uint32_t *count, const TreeOut out,
                         uint64_t *cursors, uint32_t max_blocks, bool write_entries,
-                        const RoutePlan *plan = nullptr);
+                        const RoutePlan *plan = nullptr, bool implicit_in = false);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,

@@ -1682,7 +1682,7 @@ static mbk::SampleParams sample_params(const Trainer &t, int tree) {
 // Gradients, maxima and the tree's order entries: every row quantised, or
 // the rows a GOSS / bagging tree keeps (their count stays on the device).
 static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *order,
-                         uint8_t *kept = nullptr) {
+                         uint8_t *kept = nullptr, bool implicit_rows = false) {
     hipStream_t s = t.dev->stream;
     const bool sampled = tree_sampled(t.p, tree);
     MB_HIP(mbk::launch_tree_init(s, ctl));
@@ -1702,7 +1702,7 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
                                   t.samp_h_kept.ptr, kept));
     else
         MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
-                                    ctl, order));
+                                    ctl, order, implicit_rows));
     return sampled;
 }
 
@@ -1734,8 +1734,10 @@ static void grow_levelwise(Trainer &t, int tree) {
     if (const uint8_t *m = tree_feature_mask(t, tree))
         MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
     mbk::TreeCtl *ctl = t.ctl.ptr;
+    // an unsampled root holds every row in order: its entries are the rows'
+    // packed words only (row = entry index) until the first partition
     const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr,
-                                      t.kept_walk ? t.kept.ptr : nullptr);
+                                      t.kept_walk ? t.kept.ptr : nullptr, true);
     MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
                                  (uint32_t)t.target_items,
                                  (uint32_t)t.min_chunk, ctl, t.seg_a.ptr, t.count.ptr, t.pairs.ptr,
@@ -1755,7 +1757,8 @@ static void grow_levelwise(Trainer &t, int tree) {
         const bool planar = level == 0 && !sampled && t.has_root_copy;
         MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
-                                planar ? &t.root_layout : nullptr, e0, e1));
+                                planar ? &t.root_layout : nullptr, e0, e1,
+                                level == 0 && !sampled));
         if (e0) t.events.push_back({e0, e1, level});
     };
 
@@ -1806,7 +1809,7 @@ static void grow_levelwise(Trainer &t, int tree) {
         const mbk::RoutePlan rp = t.route_plan(ln, seg_next);
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
                                  t.count.ptr, out, t.route_cursor.ptr,
-                                 t.route_grid, true, &rp));
+                                 t.route_grid, true, &rp, d == 1 && !sampled));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
