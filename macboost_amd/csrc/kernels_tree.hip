@@ -1647,7 +1647,7 @@ hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint
                          const TreeCtl *ctl, bool derive) {
     const uint32_t cells = (uint32_t)(sh.num_bins * sh.tile_w);
     const int dv = derive ? 1 : 0;
-    if (max_pairs >= 16) {                           // measured: S = 4 is faster below
+    if (max_pairs >= 32) {                           // measured: S = 4 is faster below
         const uint32_t bpt = (cells + 255) / 256;
         hipLaunchKernelGGL(k_reduce<1>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
                            0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
@@ -2039,6 +2039,10 @@ __device__ void decide_node(const Shape &sh, const SplitParams &sp, const LevelA
         }
         return;
     }
+    // the node's sums and bounds load while the feature argmax runs
+    const uint32_t mgb = ctl->max_gh[0], mhb = ctl->max_gh[1];
+    const int64_t Gt = node_g[n], Ht = node_h[n];
+    const float2 pb = bounds[n];
     float bg = -INFINITY;
     int bf = 0x7FFFFFFF;
     for (int f = lane; f < F; f += 64) {
@@ -2047,9 +2051,8 @@ __device__ void decide_node(const Shape &sh, const SplitParams &sp, const LevelA
     }
     wave_argmax(bg, bf);
     if (lane != 0) return;
-    const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
-    const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
-    const int64_t Gt = node_g[n], Ht = node_h[n];
+    const float g_inv = f32_from_bits(mgb) / 32767.0f;
+    const float h_inv = f32_from_bits(mhb) / 127.0f;
     if (bf != 0x7FFFFFFF && isfinite(bg) && bg > sp.min_split_gain) {
         const SplitResult r = results[(size_t)local * F + bf];
         NodeSplit ns = {bf, r.bin, r.flags};
@@ -2062,7 +2065,6 @@ __device__ void decide_node(const Shape &sh, const SplitParams &sp, const LevelA
         node_g[lc] = r.gl_int; node_h[lc] = r.hl_int;
         node_g[rc] = Gt - r.gl_int; node_h[rc] = Ht - r.hl_int;
         // monotone bounds (Shaders.swift:1424-1443)
-        const float2 pb = bounds[n];
         float2 lb = pb, rb = pb;
         const int cst = cat ? 0 : (int)monotone[bf];
         if (cst != 0) {
@@ -2079,9 +2081,8 @@ __device__ void decide_node(const Shape &sh, const SplitParams &sp, const LevelA
         NodeSplit leaf = {-1, 0, 0};
         out.split[n] = leaf;
         out.gain[n] = 0.0f;
-        const float2 bb = bounds[n];
         const float G = (float)Gt * g_inv, H = (float)Ht * h_inv;
-        out.leaf[n] = sp.learning_rate * clampf(-G / (H + sp.lambda), bb.x, bb.y);
+        out.leaf[n] = sp.learning_rate * clampf(-G / (H + sp.lambda), pb.x, pb.y);
     }
 }
 
