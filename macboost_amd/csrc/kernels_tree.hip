@@ -890,6 +890,38 @@ __global__ __launch_bounds__(64) void k_grad_max_final(const uint32_t *__restric
     }
 }
 
+// A tree's start in one single-wavefront launch: the previous tree's control
+// block copied to ctl_out (when given), the block zeroed, and (with partial)
+// the gradient maxima reduced into it as k_grad_max_final does.
+static_assert(sizeof(TreeCtl) % 4 == 0 && sizeof(TreeCtl) / 4 <= 64, "one word per lane");
+
+__global__ __launch_bounds__(64) void k_tree_start(TreeCtl *ctl, TreeCtl *ctl_out,
+                                                   const uint32_t *__restrict__ partial,
+                                                   int nparts) {
+    constexpr uint32_t CW = sizeof(TreeCtl) / 4;
+    uint32_t *w = reinterpret_cast<uint32_t *>(ctl);
+    if (threadIdx.x < CW) {
+        const uint32_t v = w[threadIdx.x];           // each lane owns one word
+        if (ctl_out) reinterpret_cast<uint32_t *>(ctl_out)[threadIdx.x] = v;
+        w[threadIdx.x] = 0u;
+    }
+    if (partial) {
+        __shared__ uint2 bc;
+        const uint2 m = reduce_partial_max(partial, nparts, &bc);
+        if (threadIdx.x == 0) {                      // after lanes 0 and 1 zeroed these words
+            ctl->max_gh[0] = m.x;
+            ctl->max_gh[1] = m.y;
+        }
+    }
+}
+
+hipError_t launch_tree_start(hipStream_t s, TreeCtl *ctl, TreeCtl *ctl_out,
+                             const uint32_t *partial, int nparts) {
+    hipLaunchKernelGGL(k_tree_start, dim3(1), dim3(64), 0, s, ctl, ctl_out, partial,
+                       partial ? nparts : 0);
+    return hipGetLastError();
+}
+
 static int grad_max_blocks(int64_t rows) {
     const int64_t quads = (rows + 3) / 4;
     return (int)std::max<int64_t>(

@@ -176,6 +176,11 @@ hipError_t launch_edges(hipStream_t s, const float *x, int64_t rows, int32_t col
                         uint32_t *keys_b, uint32_t *counts, float *edges);
 
 hipError_t launch_tree_init(hipStream_t s, TreeCtl *ctl);
+// launch_tree_init in one launch with two neighbours: the previous tree's
+// control block first copied to ctl_out (unless null), and with partial the
+// gradient maxima reduced as launch_grad_max_final would.
+hipError_t launch_tree_start(hipStream_t s, TreeCtl *ctl, TreeCtl *ctl_out,
+                             const uint32_t *partial, int nparts);
 
 // Per LABEL block of training rows (k_label_stats): the base score's two
 // double sums and the first rejected label / weight row (INT64_MAX: none).

@@ -513,6 +513,7 @@ struct Trainer {
     DevBuf<int64_t> node_g, node_h;
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
+    int ctl_pending = -1;           // tree whose ctl is not yet copied into ctl_hist
     // warm start: the init model's trees prefix the ensemble and its raw
     // scores seed preds (Booster.swift:849-866, :890-891)
     std::vector<Tree> init_trees;
@@ -1685,11 +1686,15 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
                          uint8_t *kept = nullptr, bool implicit_rows = false) {
     hipStream_t s = t.dev->stream;
     const bool sampled = tree_sampled(t.p, tree);
-    MB_HIP(mbk::launch_tree_init(s, ctl));
+    // the previous tree's control block goes to ctl_hist, then this tree's
+    // starts from zero; when the previous tree's walk computed these
+    // gradients (and stored g, h for a sampled tree), only the maxima's final
+    // reduction is left, done in the same launch
+    mbk::TreeCtl *prev = t.ctl_pending >= 0 ? t.ctl_hist.ptr + t.ctl_pending : nullptr;
+    t.ctl_pending = -1;
+    MB_HIP(mbk::launch_tree_start(s, ctl, prev, t.walk_gparts > 0 ? t.gmax_part.ptr : nullptr,
+                                  t.walk_gparts));
     if (t.walk_gparts > 0) {
-        // the previous tree's walk computed these gradients (and stored g, h
-        // for a sampled tree): only the maxima's final reduction is left
-        MB_HIP(mbk::launch_grad_max_final(s, t.gmax_part.ptr, t.walk_gparts, ctl));
         t.walk_gparts = 0;
     } else {
         MB_HIP(mbk::launch_grad_max(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
@@ -1825,8 +1830,7 @@ static void grow_levelwise(Trainer &t, int tree) {
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
                                           t.vpreds_cur));
-    MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, ctl, sizeof(mbk::TreeCtl),
-                          hipMemcpyDeviceToDevice, s));
+    t.ctl_pending = tree;                            // copied by the next tree's start
 }
 
 static void finish_leafwise(Trainer &t, int tree, const mbk::TreeOut &out,
@@ -1913,8 +1917,7 @@ static void finish_leafwise(Trainer &t, int tree, const mbk::TreeOut &out, bool 
             MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, dout,
                                               t.vpreds_cur));
     }
-    MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + tree, t.ctl.ptr, sizeof(mbk::TreeCtl),
-                          hipMemcpyDeviceToDevice, s));
+    t.ctl_pending = tree;                            // copied by the next tree's start
 }
 
 // Leaf-wise growth in depth rounds (trees of depth <= LWB_MAX_DEPTH): the
@@ -2063,6 +2066,11 @@ void trainer_grow(Trainer *tp, int num_trees) {
             }
         }
         if (t.p.verbose && !line.empty()) std::printf("%s\n", line.c_str());
+    }
+    if (t.ctl_pending >= 0) {                        // the last tree's control block
+        MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + t.ctl_pending, t.ctl.ptr, sizeof(mbk::TreeCtl),
+                              hipMemcpyDeviceToDevice, s));
+        t.ctl_pending = -1;
     }
     MB_HIP(hipStreamSynchronize(s));
     if (t.grown > first_tree) {
