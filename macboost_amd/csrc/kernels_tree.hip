@@ -1218,6 +1218,8 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
     }
 }
 
+__device__ void plan_root(const RootPlan &rp);
+
 // Quantise the kept entries with the weighted maxima (quantize_gradients,
 // Shaders.swift:176-192, over amplified gradients): ghq holds g * w on entry.
 // The weighted maxima are in the control block; block 0 also zeroes the |g|
@@ -1225,9 +1227,12 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
 __global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
                                                           uint32_t *__restrict__ buckets,
                                                           Entry *__restrict__ order,
-                                                          const float *__restrict__ h_kept) {
-    if (blockIdx.x == 0)
+                                                          const float *__restrict__ h_kept,
+                                                          RootPlan rp, int has_plan) {
+    if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) buckets[k] = 0;
+        if (has_plan) plan_root(rp);                 // overlaps the other workgroups' rows
+    }
     const uint32_t n = ctl->sampled;
     const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
     const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
@@ -1244,7 +1249,7 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
 
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
-                         Entry *order, float *h_kept, uint8_t *kept) {
+                         Entry *order, float *h_kept, uint8_t *kept, const RootPlan *plan) {
     if (((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(h)) & 15u) != 0)
         return hipErrorInvalidValue;                 // the passes read 16-B quads
     const int64_t quads = (rows + 3) / 4;
@@ -1264,7 +1269,7 @@ hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, Tr
     const unsigned qblocks =
         (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
     hipLaunchKernelGGL(k_quantize_sampled, dim3(qblocks), dim3(256), 0, s, ctl, buckets, order,
-                       h_kept);
+                       h_kept, plan ? *plan : RootPlan{}, plan ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1274,7 +1279,8 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
                                                   const float *__restrict__ labels,
                                                   const float *__restrict__ weights, int64_t rows,
                                                   const TreeCtl *ctl, Entry *__restrict__ order,
-                                                  int implicit_rows) {
+                                                  int implicit_rows, RootPlan rp, int has_plan) {
+    if (has_plan && blockIdx.x == 0) plan_root(rp);  // overlaps the other workgroups' rows
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
@@ -1294,9 +1300,11 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
 
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           const TreeCtl *ctl, Entry *order, bool implicit_rows) {
+                           const TreeCtl *ctl, Entry *order, bool implicit_rows,
+                           const RootPlan *plan) {
     hipLaunchKernelGGL(k_quantize, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, gp,
-                       preds, labels, weights, rows, ctl, order, implicit_rows ? 1 : 0);
+                       preds, labels, weights, rows, ctl, order, implicit_rows ? 1 : 0,
+                       plan ? *plan : RootPlan{}, plan ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -2333,39 +2341,35 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     }
 }
 
-__global__ __launch_bounds__(1024) void k_plan_root(Shape sh, uint32_t rows_active,
-                                                    uint32_t target_items, uint32_t min_chunk,
-                                                    TreeCtl *ctl, uint32_t *seg_start,
-                                                    uint32_t *count, Pair *pairs, HistItem *items,
-                                                    float *cover, float2 *bounds, float lo,
-                                                    float hi) {
+// The root's plan, by one workgroup of any size (a multiple of 64, at most
+// 1024 threads).
+__device__ void plan_root(const RootPlan &rp) {
     __shared__ uint32_t wave_tot[17];
     __shared__ uint32_t s_cnt[1], s_seg[1], s_first[1];
     if (threadIdx.x == 0) {
-        if (rows_active == NONE) rows_active = ctl->sampled;   // a sampled tree's kept rows
-        count[0] = rows_active;
-        seg_start[0] = 0;
-        ctl->level_active[0] = rows_active;
-        ctl->num_pairs = 1;
-        cover[0] = (float)rows_active;
-        bounds[0] = make_float2(lo, hi);
+        uint32_t rows_active = rp.rows_active;
+        if (rows_active == NONE) rows_active = rp.ctl->sampled;   // a sampled tree's kept rows
+        rp.count[0] = rows_active;
+        rp.seg_start[0] = 0;
+        rp.ctl->level_active[0] = rows_active;
+        rp.ctl->num_pairs = 1;
+        rp.cover[0] = (float)rows_active;
+        rp.bounds[0] = make_float2(rp.lo, rp.hi);
         Pair p = {};
         p.built = 0; p.derived = NONE; p.parent = NONE;
-        pairs[0] = p;
+        rp.pairs[0] = p;
         s_cnt[0] = rows_active;
         s_seg[0] = 0;
     }
     __syncthreads();
-    write_items(sh, ctl, 0, pairs, items, s_cnt, s_seg, s_first, 1, target_items, min_chunk,
-                wave_tot);
+    write_items(rp.sh, rp.ctl, 0, rp.pairs, rp.items, s_cnt, s_seg, s_first, 1, rp.target_items,
+                rp.min_chunk, wave_tot);
 }
 
-hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active,
-                            uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
-                            uint32_t *seg_start, uint32_t *count, Pair *pairs, HistItem *items,
-                            float *cover, float2 *bounds, float lo, float hi) {
-    hipLaunchKernelGGL(k_plan_root, dim3(1), dim3(1024), 0, s, sh, rows_active, target_items,
-                       min_chunk, ctl, seg_start, count, pairs, items, cover, bounds, lo, hi);
+__global__ __launch_bounds__(1024) void k_plan_root(RootPlan rp) { plan_root(rp); }
+
+hipError_t launch_plan_root(hipStream_t s, const RootPlan &plan) {
+    hipLaunchKernelGGL(k_plan_root, dim3(1), dim3(1024), 0, s, plan);
     return hipGetLastError();
 }
 

@@ -230,15 +230,35 @@ struct SampleParams {
     uint32_t seed;           // tree index + 1
     uint32_t pad[3];
 };
+// The root level's plan (launch_plan_root's arguments): the root node's
+// count, segment, cover, bounds, its one pair and its histogram items.
+// rows_active == NONE takes ctl->sampled (a sampled tree's kept rows).
+struct RootPlan {
+    Shape sh;
+    uint32_t rows_active, target_items, min_chunk, pad;
+    TreeCtl *ctl;
+    uint32_t *seg_start, *count;
+    Pair *pairs;
+    HistItem *items;
+    float *cover;
+    float2 *bounds;
+    float lo, hi;
+};
+// With plan non-null the last pass (the kept rows' quantiser) also plans the
+// root, in its first workgroup.
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
-                         Entry *order, float *h_kept, uint8_t *kept);
+                         Entry *order, float *h_kept, uint8_t *kept,
+                         const RootPlan *plan = nullptr);
 // Every row quantised with ctl->max_gh into order[i] = {i, packed (qg, qh)};
 // with implicit_rows, into the u32 words ((uint32_t *)order)[i] = packed
-// (qg, qh) only: the root's rows in order, row i being entry i.
+// (qg, qh) only: the root's rows in order, row i being entry i.  With plan
+// non-null the first workgroup also plans the root (plan->rows_active rows)
+// while the others quantise.
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
-                           const TreeCtl *ctl, Entry *order, bool implicit_rows = false);
+                           const TreeCtl *ctl, Entry *order, bool implicit_rows = false,
+                           const RootPlan *plan = nullptr);
 
 // Where the histogram kernel finds tile t of row r: at
 // base + t * tile_step + r * (t == last_tile ? last_stride : stride).
@@ -314,11 +334,7 @@ hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams 
                               int64_t *node_g, int64_t *node_h, uint32_t level_start,
                               SplitResult *results);
 
-hipError_t launch_plan_root(hipStream_t s, const Shape &sh, uint32_t rows_active,
-                            uint32_t target_items, uint32_t min_chunk, TreeCtl *ctl,
-                            uint32_t *seg_start, uint32_t *count, Pair *pairs,
-                            HistItem *items, float *cover, float2 *bounds,
-                            float root_lo, float root_hi);
+hipError_t launch_plan_root(hipStream_t s, const RootPlan &plan);
 
 hipError_t launch_decide(hipStream_t s, const Shape &sh, const SplitParams &sp,
                          const LevelArgs &la, const SplitResult *results,

@@ -132,8 +132,10 @@ extern "C" int mbk_node_hist_split_noalloc(mbk_context *ctx, const uint8_t *bins
         const mbk::SplitParams sp{lambda, min_child_hess, 0.0f, cat_smooth, 0.1f, 1};
         hipLaunchKernelGGL(k_noalloc_setup, dim3(1), dim3(256), 0, s, base, max_gh, cols);
         MB_HIP(hipGetLastError());
-        MB_HIP(mbk::launch_plan_root(s, sh, (uint32_t)n, target, min_chunk, ctl, seg, count,
-                                     pairs, items_d, cover, bounds, -INFINITY, INFINITY));
+        const mbk::RootPlan rp{sh,      (uint32_t)n, target, min_chunk, 0u,     ctl,
+                               seg,     count,       pairs,  items_d,   cover,  bounds,
+                               -INFINITY, INFINITY};
+        MB_HIP(mbk::launch_plan_root(s, rp));
         MB_HIP(mbk::launch_hist(s, sh, bins_tiled, reinterpret_cast<const mbk::Entry *>(entries),
                                 items_d, ctl, partials, (int)std::max<uint32_t>(target, 1)));
         MB_HIP(mbk::launch_split(s, sh, sp, pairs, 1, partials, node_g, hist_out,

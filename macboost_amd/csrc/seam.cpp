@@ -159,6 +159,25 @@ void check_shape(const mbk_tree_shape *shape) {
     need(shape->max_depth >= 1 && shape->max_depth <= 12, "maxDepth must be in 1...12");
 }
 
+// The root plan of a tree of `rows` entries over the scratch of t.
+mbk::RootPlan root_plan(const TreeScratch &t, uint32_t rows, float *cover) {
+    mbk::RootPlan rp{};
+    rp.sh = t.sh;
+    rp.rows_active = rows;
+    rp.target_items = t.target_items;
+    rp.min_chunk = t.min_chunk;
+    rp.ctl = t.ctl.ptr;
+    rp.seg_start = t.seg_cur;
+    rp.count = t.count.ptr;
+    rp.pairs = t.pairs.ptr;
+    rp.items = t.items.ptr;
+    rp.cover = cover;
+    rp.bounds = t.bounds.ptr;
+    rp.lo = -INFINITY;
+    rp.hi = INFINITY;
+    return rp;
+}
+
 TreeScratch &tree_at(mbk_context *ctx, int32_t level, bool planned_level) {
     need(ctx != nullptr, "null kernel-seam context");
     TreeScratch &t = ctx->scratch.tree;
@@ -313,9 +332,7 @@ int mbk_tree_begin(mbk_context *ctx, const mbk_tree_shape *shape, const uint32_t
         MB_HIP(hipMemcpyAsync(t.ctl.ptr->max_gh, max_gh, 8, hipMemcpyDeviceToDevice, s));
         t.seg_cur = t.seg_a.ptr;
         t.seg_next = t.seg_b.ptr;
-        MB_HIP(mbk::launch_plan_root(s, t.sh, (uint32_t)n_entries, t.target_items, t.min_chunk,
-                                     t.ctl.ptr, t.seg_cur, t.count.ptr, t.pairs.ptr, t.items.ptr,
-                                     out.cover, t.bounds.ptr, -INFINITY, INFINITY));
+        MB_HIP(mbk::launch_plan_root(s, root_plan(t, (uint32_t)n_entries, out.cover)));
         t.active = true;
         t.planned = 0;
         t.decided = -1;
@@ -469,9 +486,7 @@ int mbk_node_hist_split(mbk_context *ctx, const uint8_t *bins_tiled, int64_t row
         MB_HIP(hipMemcpyAsync(t.ctl.ptr->max_gh, max_gh, 8, hipMemcpyDeviceToDevice, s));
         t.seg_cur = t.seg_a.ptr;
         t.seg_next = t.seg_b.ptr;
-        MB_HIP(mbk::launch_plan_root(s, t.sh, (uint32_t)n, t.target_items, t.min_chunk, t.ctl.ptr,
-                                     t.seg_cur, t.count.ptr, t.pairs.ptr, t.items.ptr,
-                                     t.cover1.ptr, t.bounds.ptr, -INFINITY, INFINITY));
+        MB_HIP(mbk::launch_plan_root(s, root_plan(t, (uint32_t)n, t.cover1.ptr)));
         t.active = true;
         t.planned = 0;
         t.decided = -1;

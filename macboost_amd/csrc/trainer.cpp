@@ -1682,10 +1682,31 @@ static mbk::SampleParams sample_params(const Trainer &t, int tree) {
 
 // Gradients, maxima and the tree's order entries: every row quantised, or
 // the rows a GOSS / bagging tree keeps (their count stays on the device).
+// With root_cover non-null the pass that writes the root's entries also plans
+// the root level (its first workgroup, while the others quantise), in place
+// of a separate launch_plan_root after it.
 static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *order,
-                         uint8_t *kept = nullptr, bool implicit_rows = false) {
+                         uint8_t *kept = nullptr, bool implicit_rows = false,
+                         float *root_cover = nullptr) {
     hipStream_t s = t.dev->stream;
     const bool sampled = tree_sampled(t.p, tree);
+    mbk::RootPlan rp{};
+    if (root_cover) {
+        rp.sh = t.sh;
+        rp.rows_active = sampled ? mbk::NONE : (uint32_t)t.rows;
+        rp.target_items = (uint32_t)t.target_items;
+        rp.min_chunk = (uint32_t)t.min_chunk;
+        rp.ctl = ctl;
+        rp.seg_start = t.seg_a.ptr;
+        rp.count = t.count.ptr;
+        rp.pairs = t.pairs.ptr;
+        rp.items = t.items.ptr;
+        rp.cover = root_cover;
+        rp.bounds = t.bounds.ptr;
+        rp.lo = -INFINITY;
+        rp.hi = INFINITY;
+    }
+    const mbk::RootPlan *plan = root_cover ? &rp : nullptr;
     // the previous tree's control block goes to ctl_hist, then this tree's
     // starts from zero; when the previous tree's walk computed these
     // gradients (and stored g, h for a sampled tree), only the maxima's final
@@ -1704,10 +1725,10 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     if (sampled)
         MB_HIP(mbk::launch_sample(s, sample_params(t, tree), t.rows, ctl, t.goss_buckets.ptr,
                                   t.gmax_part.ptr, t.samp_g.ptr, t.samp_h.ptr, order,
-                                  t.samp_h_kept.ptr, kept));
+                                  t.samp_h_kept.ptr, kept, plan));
     else
         MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
-                                    ctl, order, implicit_rows));
+                                    ctl, order, implicit_rows, plan));
     return sampled;
 }
 
@@ -1742,11 +1763,7 @@ static void grow_levelwise(Trainer &t, int tree) {
     // an unsampled root holds every row in order: its entries are the rows'
     // packed words only (row = entry index) until the first partition
     const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr,
-                                      t.kept_walk ? t.kept.ptr : nullptr, true);
-    MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
-                                 (uint32_t)t.target_items,
-                                 (uint32_t)t.min_chunk, ctl, t.seg_a.ptr, t.count.ptr, t.pairs.ptr,
-                                 t.items.ptr, out.cover, t.bounds.ptr, -INFINITY, INFINITY));
+                                      t.kept_walk ? t.kept.ptr : nullptr, true, out.cover);
     mbk::Entry *ord_cur = t.order_a.ptr, *ord_next = t.order_b.ptr;
     uint32_t *seg_cur = t.seg_a.ptr, *seg_next = t.seg_b.ptr;
     int64_t *h_cur = t.hist_a.ptr, *h_prev = t.hist_b.ptr;
@@ -1933,13 +1950,9 @@ static void grow_leafwise_rounds(Trainer &t, int tree) {
     if (const uint8_t *m = tree_feature_mask(t, tree))
         MB_HIP(hipMemcpyAsync(t.feat_mask.ptr, m, (size_t)t.cols, hipMemcpyHostToDevice, s));
     mbk::TreeCtl *ctl = t.ctl.ptr;
-    const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr);
     mbk::TreeOut spec{t.spec_split.ptr, t.spec_cover.ptr, t.spec_cover.ptr, t.spec_cover.ptr,
                       t.spec_mask.ptr};
-    MB_HIP(mbk::launch_plan_root(s, sh, sampled ? mbk::NONE : (uint32_t)t.rows,
-                                 (uint32_t)t.target_items, (uint32_t)t.min_chunk, ctl, t.seg_a.ptr,
-                                 t.count.ptr, t.pairs.ptr, t.items.ptr, spec.cover, t.bounds.ptr,
-                                 -INFINITY, INFINITY));
+    const bool sampled = tree_entries(t, tree, ctl, t.order_a.ptr, nullptr, false, spec.cover);
     // the two halves of the leaf-wise order buffer alternate by depth
     mbk::Entry *ord_cur = t.order_a.ptr, *ord_next = t.order_a.ptr + t.rows;
     uint32_t *seg_cur = t.seg_a.ptr, *seg_next = t.seg_b.ptr;
