@@ -1220,6 +1220,25 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
 
 __device__ void plan_root(const RootPlan &rp);
 
+// Covers of the level's nodes from count; with zero_empty, empty nodes' leaves
+// become 0 (final_fixup_node is k_final_fixup's per-node step).
+__device__ __forceinline__ void final_fixup_node(const LevelArgs &la, const uint32_t *count,
+                                                 const TreeOut &out, int zero_empty,
+                                                 uint32_t local) {
+    const uint32_t n = la.level_start + local;
+    const uint32_t c = count[n];
+    out.cover[n] = (float)c;
+    if (c == 0 && zero_empty) out.leaf[n] = 0.0f;
+}
+
+// The root pass's first workgroup: the previous tree's fixup, then the root plan.
+__device__ void root_pass_block0(const RootPlan &rp, int has_plan, const PendingFixup &fx) {
+    if (fx.active)
+        for (uint32_t k = threadIdx.x; k < fx.la.num_level; k += blockDim.x)
+            final_fixup_node(fx.la, fx.count, fx.out, fx.zero_empty, k);
+    if (has_plan) plan_root(rp);
+}
+
 // Quantise the kept entries with the weighted maxima (quantize_gradients,
 // Shaders.swift:176-192, over amplified gradients): ghq holds g * w on entry.
 // The weighted maxima are in the control block; block 0 also zeroes the |g|
@@ -1228,10 +1247,11 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
                                                           uint32_t *__restrict__ buckets,
                                                           Entry *__restrict__ order,
                                                           const float *__restrict__ h_kept,
-                                                          RootPlan rp, int has_plan) {
+                                                          RootPlan rp, int has_plan,
+                                                          PendingFixup fx) {
     if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) buckets[k] = 0;
-        if (has_plan) plan_root(rp);                 // overlaps the other workgroups' rows
+        root_pass_block0(rp, has_plan, fx);          // overlaps the other workgroups' rows
     }
     const uint32_t n = ctl->sampled;
     const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
@@ -1249,7 +1269,8 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
 
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
-                         Entry *order, float *h_kept, uint8_t *kept, const RootPlan *plan) {
+                         Entry *order, float *h_kept, uint8_t *kept, const RootPlan *plan,
+                         const PendingFixup *fix) {
     if (((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(h)) & 15u) != 0)
         return hipErrorInvalidValue;                 // the passes read 16-B quads
     const int64_t quads = (rows + 3) / 4;
@@ -1269,7 +1290,8 @@ hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, Tr
     const unsigned qblocks =
         (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
     hipLaunchKernelGGL(k_quantize_sampled, dim3(qblocks), dim3(256), 0, s, ctl, buckets, order,
-                       h_kept, plan ? *plan : RootPlan{}, plan ? 1 : 0);
+                       h_kept, plan ? *plan : RootPlan{}, plan ? 1 : 0,
+                       fix ? *fix : PendingFixup{});
     return hipGetLastError();
 }
 
@@ -1279,8 +1301,9 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
                                                   const float *__restrict__ labels,
                                                   const float *__restrict__ weights, int64_t rows,
                                                   const TreeCtl *ctl, Entry *__restrict__ order,
-                                                  int implicit_rows, RootPlan rp, int has_plan) {
-    if (has_plan && blockIdx.x == 0) plan_root(rp);  // overlaps the other workgroups' rows
+                                                  int implicit_rows, RootPlan rp, int has_plan,
+                                                  PendingFixup fx) {
+    if (blockIdx.x == 0) root_pass_block0(rp, has_plan, fx);   // overlaps the other workgroups
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
@@ -1301,10 +1324,10 @@ __global__ __launch_bounds__(256) void k_quantize(GradParams gp, const float *__
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order, bool implicit_rows,
-                           const RootPlan *plan) {
+                           const RootPlan *plan, const PendingFixup *fix) {
     hipLaunchKernelGGL(k_quantize, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, gp,
                        preds, labels, weights, rows, ctl, order, implicit_rows ? 1 : 0,
-                       plan ? *plan : RootPlan{}, plan ? 1 : 0);
+                       plan ? *plan : RootPlan{}, plan ? 1 : 0, fix ? *fix : PendingFixup{});
     return hipGetLastError();
 }
 
@@ -2194,10 +2217,7 @@ __global__ void k_final_fixup(LevelArgs la, const uint32_t *count, TreeOut out,
                               int zero_empty) {
     const uint32_t local = blockIdx.x * blockDim.x + threadIdx.x;
     if (local >= la.num_level) return;
-    const uint32_t n = la.level_start + local;
-    const uint32_t c = count[n];
-    out.cover[n] = (float)c;
-    if (c == 0 && zero_empty) out.leaf[n] = 0.0f;
+    final_fixup_node(la, count, out, zero_empty, local);
 }
 
 hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t *count,

@@ -230,6 +230,31 @@ struct SampleParams {
     uint32_t seed;           // tree index + 1
     uint32_t pad[3];
 };
+// Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
+struct LevelArgs {
+    int32_t level;           // d
+    uint32_t level_start;    // heap index of the level's first node
+    uint32_t num_level;      // 2^d
+    uint32_t terminal;       // 1: children of the routed level are final leaves
+};
+
+struct TreeOut {             // one tree's model arrays (heap layout)
+    NodeSplit *split;
+    float *leaf;
+    float *gain;
+    float *cover;
+    uint32_t *mask;          // 8 words per node
+};
+
+// A finished tree's deepest-level fixup (launch_final_fixup's arguments) left
+// to the next tree's root pass; active == 0: none.
+struct PendingFixup {
+    LevelArgs la;
+    const uint32_t *count;
+    TreeOut out;
+    int32_t zero_empty, active;
+};
+
 // The root level's plan (launch_plan_root's arguments): the root node's
 // count, segment, cover, bounds, its one pair and its histogram items.
 // rows_active == NONE takes ctl->sampled (a sampled tree's kept rows).
@@ -245,20 +270,22 @@ struct RootPlan {
     float lo, hi;
 };
 // With plan non-null the last pass (the kept rows' quantiser) also plans the
-// root, in its first workgroup.
+// root, in its first workgroup; with fix non-null that workgroup first does
+// the previous tree's deepest-level fixup.
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
                          Entry *order, float *h_kept, uint8_t *kept,
-                         const RootPlan *plan = nullptr);
+                         const RootPlan *plan = nullptr, const PendingFixup *fix = nullptr);
 // Every row quantised with ctl->max_gh into order[i] = {i, packed (qg, qh)};
 // with implicit_rows, into the u32 words ((uint32_t *)order)[i] = packed
 // (qg, qh) only: the root's rows in order, row i being entry i.  With plan
 // non-null the first workgroup also plans the root (plan->rows_active rows)
-// while the others quantise.
+// while the others quantise, after the previous tree's fixup when fix is
+// non-null.
 hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *preds,
                            const float *labels, const float *weights, int64_t rows,
                            const TreeCtl *ctl, Entry *order, bool implicit_rows = false,
-                           const RootPlan *plan = nullptr);
+                           const RootPlan *plan = nullptr, const PendingFixup *fix = nullptr);
 
 // Where the histogram kernel finds tile t of row r: at
 // base + t * tile_step + r * (t == last_tile ? last_stride : stride).
@@ -293,22 +320,6 @@ size_t hist_lds_size();   // static LDS of one histogram workgroup
 // rows into the zeroed tail, and into the next row's bytes, which land in
 // padding columns).
 hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled, uint8_t *out);
-
-// Per-level view of the heap: level d holds nodes [2^d - 1, 2^(d+1) - 1).
-struct LevelArgs {
-    int32_t level;           // d
-    uint32_t level_start;    // heap index of the level's first node
-    uint32_t num_level;      // 2^d
-    uint32_t terminal;       // 1: children of the routed level are final leaves
-};
-
-struct TreeOut {             // one tree's model arrays (heap layout)
-    NodeSplit *split;
-    float *leaf;
-    float *gain;
-    float *cover;
-    uint32_t *mask;          // 8 words per node
-};
 
 // Reduce partials into hist_cur [node][B][F][g,h] (int64), derive siblings
 // from hist_prev, then search splits for both nodes of each pair.

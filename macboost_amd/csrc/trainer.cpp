@@ -514,6 +514,9 @@ struct Trainer {
     DevBuf<float2> bounds;
     DevBuf<mbk::TreeCtl> ctl, ctl_hist;
     int ctl_pending = -1;           // tree whose ctl is not yet copied into ctl_hist
+    // a finished tree's deepest covers (and empty leaves), written by the next
+    // tree's root pass or at the end of the grow call
+    mbk::PendingFixup fix_pending{};
     // warm start: the init model's trees prefix the ensemble and its raw
     // scores seed preds (Booster.swift:849-866, :890-891)
     std::vector<Tree> init_trees;
@@ -1707,6 +1710,15 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
         rp.hi = INFINITY;
     }
     const mbk::RootPlan *plan = root_cover ? &rp : nullptr;
+    // the previous tree's deferred fixup: in this root pass's first workgroup
+    // when there is one, else on its own
+    mbk::PendingFixup fix = t.fix_pending;
+    t.fix_pending.active = 0;
+    if (fix.active && !plan) {
+        MB_HIP(mbk::launch_final_fixup(s, fix.la, fix.count, fix.out, fix.zero_empty != 0));
+        fix.active = 0;
+    }
+    const mbk::PendingFixup *fixp = fix.active ? &fix : nullptr;
     // the previous tree's control block goes to ctl_hist, then this tree's
     // starts from zero; when the previous tree's walk computed these
     // gradients (and stored g, h for a sampled tree), only the maxima's final
@@ -1725,10 +1737,10 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     if (sampled)
         MB_HIP(mbk::launch_sample(s, sample_params(t, tree), t.rows, ctl, t.goss_buckets.ptr,
                                   t.gmax_part.ptr, t.samp_g.ptr, t.samp_h.ptr, order,
-                                  t.samp_h_kept.ptr, kept, plan));
+                                  t.samp_h_kept.ptr, kept, plan, fixp));
     else
         MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
-                                    ctl, order, implicit_rows, plan));
+                                    ctl, order, implicit_rows, plan, fixp));
     return sampled;
 }
 
@@ -1804,6 +1816,13 @@ static void grow_levelwise(Trainer &t, int tree) {
             MB_HIP(mbk::launch_final_leaves(s, t.sp, ln, t.count.ptr, t.node_g.ptr, t.node_h.ptr,
                                             t.bounds.ptr, ctl, out, false));
             training_walk(t, tree, out, t.count.ptr, sampled ? t.kept.ptr : nullptr);
+            if (!t.renewal && !t.has_valid) {
+                // nothing of this tree reads the deepest covers or leaves
+                // again before the next tree's root pass, which writes them
+                // (the validation walk and leaf renewal below do)
+                t.fix_pending = mbk::PendingFixup{ln, t.count.ptr, out, 1, 1};
+                break;
+            }
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
             if (t.renewal) {
                 // residuals before the tree (routing applies nothing), then
@@ -2079,6 +2098,11 @@ void trainer_grow(Trainer *tp, int num_trees) {
             }
         }
         if (t.p.verbose && !line.empty()) std::printf("%s\n", line.c_str());
+    }
+    if (t.fix_pending.active) {                      // the last tree's deepest covers
+        const mbk::PendingFixup &f = t.fix_pending;
+        MB_HIP(mbk::launch_final_fixup(s, f.la, f.count, f.out, f.zero_empty != 0));
+        t.fix_pending.active = 0;
     }
     if (t.ctl_pending >= 0) {                        // the last tree's control block
         MB_HIP(hipMemcpyAsync(t.ctl_hist.ptr + t.ctl_pending, t.ctl.ptr, sizeof(mbk::TreeCtl),
