@@ -596,6 +596,35 @@ def test_goss_and_bagging_identical_trees(params):
 
 
 @pytest.mark.parametrize("params", [
+    {"num_trees": 8, "max_depth": 6, "monotone_constraints": [0, 0, 0, 1, 0, -1]},
+    {"num_trees": 8, "max_depth": 5, "learning_rate": 0.5, "goss": True,
+     "objective": "binary"},
+])
+def test_trees_grown_in_several_calls_equal_one_call(params):
+    # A level-wise tree's deepest covers (and empty leaves) are written by the
+    # next tree's first pass, or at the end of the grow call when it is the
+    # last: a model grown 3 + 4 + 1 trees at a time equals one grown at once
+    # and the oracle's, in every array.
+    x, y = O.friedman(15_000, 6, 101)
+    if params.get("objective") == "binary":
+        y = (y > np.median(y)).astype(np.float32)
+    cfg = {k: v for k, v in params.items() if k != "num_trees"}
+    models = []
+    for steps in ([8], [3, 4, 1]):
+        tr = mb.Trainer(cfg, x, y, feature_major=True)
+        try:
+            for n in steps:
+                tr.grow(n)
+            models.append(model_io.saved_model(tr.booster()))
+        finally:
+            tr.close()
+    assert models[0] == models[1]
+    ref = oracle_fit(x, y, params)
+    got = model_io.forest_from_json(models[1], ref.forest.nodes_per_tree)
+    model_io.assert_same_forest(got, ref.forest, with_cats=False)
+
+
+@pytest.mark.parametrize("params", [
     {"goss": True, "min_child_weight": 0.0},
     {"subsample": 0.6, "min_child_weight": 0.0, "min_split_gain": -1.0},
 ])
