@@ -376,9 +376,10 @@ hipError_t launch_tile8_to_layouts(hipStream_t s, const uint64_t *in, int64_t ro
 // ---------------------------------------------------------------------------
 // quantile edges on the device (Binner.swift:25-56): per feature, the stride
 // subsample of non-NaN values, sorted, edge k = sample[min(m-1, (k+1)*m/dataBins)].
-// The sample becomes order-preserving u32 keys (one thread per sample),
-// then one 1024-thread workgroup per feature radix-sorts them (stable LSD,
-// 4-bit digits) and the edges are read at their ranks.
+// The sample becomes order-preserving u32 keys (one thread per sample), a
+// stable LSD radix sort over position chunks of each column orders them
+// (4-bit digits, count and scatter launches per pass) and the edges are read
+// at their ranks.
 // ---------------------------------------------------------------------------
 
 constexpr int EDGE_THREADS = 1024;
@@ -2231,7 +2232,8 @@ hipError_t launch_final_fixup(hipStream_t s, const LevelArgs &la, const uint32_t
 // level planning (single workgroup): segment layout, sibling pairs, items
 // ---------------------------------------------------------------------------
 
-// Exclusive scan of v[0..n) in place by one 1024-thread block; returns total.
+// Exclusive scan of v[0..n) in place by one block (a multiple of 64 threads,
+// at most 1024); returns total.
 __device__ uint32_t block_exclusive_scan(uint32_t *v, uint32_t n, uint32_t *wave_tot) {
     const int tid = threadIdx.x;
     const int w = tid >> 6, nw = blockDim.x >> 6;
