@@ -985,30 +985,60 @@ constexpr int GOSS_HIST_THREADS = 1024;
 constexpr int GOSS_HIST_BLOCKS = 256;
 
 __global__ __launch_bounds__(GOSS_HIST_THREADS) void k_goss_hist(const float *__restrict__ g,
-                                                                 int64_t rows, const TreeCtl *ctl,
-                                                                 uint32_t *buckets) {
+                                                                 int64_t rows, TreeCtl *ctl,
+                                                                 uint32_t *buckets,
+                                                                 TreeCtl *ctl_out,
+                                                                 const uint32_t *walk_part,
+                                                                 int walk_nparts) {
     constexpr int WAVES = GOSS_HIST_THREADS / 64;
     __shared__ uint32_t lb[WAVES][GOSS_BUCKETS];
     for (int k = threadIdx.x; k < WAVES * GOSS_BUCKETS; k += blockDim.x) (&lb[0][0])[k] = 0;
-    __syncthreads();
-    const float mg = f32_from_bits(ctl->max_gh[0]);
+    if (walk_part && blockIdx.x == 0 && threadIdx.x < sizeof(TreeCtl) / 4) {
+        // the tree's start (k_tree_start): the previous tree's control block
+        // copied out, this one zeroed; its maxima are stored below
+        uint32_t *w = reinterpret_cast<uint32_t *>(ctl);
+        const uint32_t v = w[threadIdx.x];
+        if (ctl_out) reinterpret_cast<uint32_t *>(ctl_out)[threadIdx.x] = v;
+        w[threadIdx.x] = 0u;
+    }
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const float4 *g4 = reinterpret_cast<const float4 *>(g);
+    const int64_t nq = rows >> 2;
+    // the first two quads load while the maxima are found
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const bool first = t0 < nq, second = t0 + stride < nq;
+    const float4 a0 = first ? g4[t0] : zero4;
+    const float4 b0 = second ? g4[t0 + stride] : zero4;
+    float mg;
+    if (walk_part) {
+        // max |g| from the training walk's per-block maxima, in every block
+        __shared__ uint2 bc;
+        const uint2 m = reduce_partial_max(walk_part, walk_nparts, &bc);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {   // after the zeroing (barrier above)
+            ctl->max_gh[0] = m.x;
+            ctl->max_gh[1] = m.y;
+        }
+        mg = f32_from_bits(m.x);
+    } else {
+        __syncthreads();
+        mg = f32_from_bits(ctl->max_gh[0]);
+    }
     uint32_t *mine = lb[threadIdx.x >> 6];
     auto add = [&](float v) {
         const uint32_t b = (uint32_t)(fabsf(v) / mg * (float)GOSS_BUCKETS);
         atomicAdd(&mine[min(b, (uint32_t)(GOSS_BUCKETS - 1))], 1u);
     };
     if (mg > 0.0f) {
-        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-        const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-        const float4 *g4 = reinterpret_cast<const float4 *>(g);
-        const int64_t nq = rows >> 2;
-        for (int64_t q = t0; q < nq; q += 2 * stride) {
-            const bool second = q + stride < nq;
+        if (first) { add(a0.x); add(a0.y); add(a0.z); add(a0.w); }
+        if (second) { add(b0.x); add(b0.y); add(b0.z); add(b0.w); }
+        for (int64_t q = t0 + 2 * stride; q < nq; q += 2 * stride) {
+            const bool sec = q + stride < nq;
             const float4 a = g4[q];
-            float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (second) b = g4[q + stride];
+            float4 b = zero4;
+            if (sec) b = g4[q + stride];
             add(a.x); add(a.y); add(a.z); add(a.w);
-            if (second) { add(b.x); add(b.y); add(b.z); add(b.w); }
+            if (sec) { add(b.x); add(b.y); add(b.z); add(b.w); }
         }
         for (int64_t i = (nq << 2) + t0; i < rows; i += stride) add(g[i]);
     }
@@ -1242,25 +1272,46 @@ __device__ void root_pass_block0(const RootPlan &rp, int has_plan, const Pending
 
 // Quantise the kept entries with the weighted maxima (quantize_gradients,
 // Shaders.swift:176-192, over amplified gradients): ghq holds g * w on entry.
-// The weighted maxima are in the control block; block 0 also zeroes the |g|
-// histogram for the next tree.
-__global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
+// Every block reduces the selection's per-block weighted maxima (partial,
+// nparts pairs) itself once its first entries are loading, as
+// k_grad_max_final would, and block 0 stores them in the control block for
+// the split search; block 0 also zeroes the |g| histogram for the next tree.
+__global__ __launch_bounds__(256) void k_quantize_sampled(TreeCtl *ctl,
                                                           uint32_t *__restrict__ buckets,
                                                           Entry *__restrict__ order,
                                                           const float *__restrict__ h_kept,
-                                                          RootPlan rp, int has_plan,
+                                                          const uint32_t *__restrict__ partial,
+                                                          int nparts, RootPlan rp, int has_plan,
                                                           PendingFixup fx) {
     if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) buckets[k] = 0;
         root_pass_block0(rp, has_plan, fx);          // overlaps the other workgroups' rows
     }
     const uint32_t n = ctl->sampled;
-    const float mg = f32_from_bits(ctl->max_gh[0]), mh = f32_from_bits(ctl->max_gh[1]);
+    const uint32_t i0 = blockIdx.x * blockDim.x + threadIdx.x, step = gridDim.x * blockDim.x;
+    Entry e0{0u, 0u};
+    float hw0 = 0.0f;
+    if (i0 < n) {
+        e0 = load_entry_nt(order + i0);
+        hw0 = __builtin_nontemporal_load(h_kept + i0);
+    }
+    __shared__ uint2 bc;
+    const uint2 m = reduce_partial_max(partial, nparts, &bc);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        ctl->max_gh[0] = m.x;
+        ctl->max_gh[1] = m.y;
+    }
+    const float mg = f32_from_bits(m.x), mh = f32_from_bits(m.y);
     const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
     const float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        Entry e = load_entry_nt(order + i);
-        const float gw = __uint_as_float(e.ghq), hw = __builtin_nontemporal_load(h_kept + i);
+    for (uint32_t i = i0; i < n; i += step) {
+        Entry e = e0;
+        float hw = hw0;
+        if (i != i0) {
+            e = load_entry_nt(order + i);
+            hw = __builtin_nontemporal_load(h_kept + i);
+        }
+        const float gw = __uint_as_float(e.ghq);
         const int qg = (int)rintf(gw * gscale);
         const uint32_t qh = (uint32_t)rintf(hw * hscale);
         e.ghq = ((uint32_t)(qg & 0xFFFF) << 16) | (qh & 0x7Fu);
@@ -1271,27 +1322,31 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(const TreeCtl *ctl,
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
                          Entry *order, float *h_kept, uint8_t *kept, const RootPlan *plan,
-                         const PendingFixup *fix) {
+                         const PendingFixup *fix, TreeCtl *ctl_prev, const uint32_t *walk_part,
+                         int walk_nparts) {
     if (((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(h)) & 15u) != 0)
         return hipErrorInvalidValue;                 // the passes read 16-B quads
     const int64_t quads = (rows + 3) / 4;
     const unsigned hist_blocks = (unsigned)std::max<int64_t>(
         1, std::min<int64_t>(GOSS_HIST_BLOCKS,
                              (quads + 2 * GOSS_HIST_THREADS - 1) / (2 * GOSS_HIST_THREADS)));
-    if (sp.goss && sp.top_count > 0)
+    if (sp.goss && sp.top_count > 0) {
         hipLaunchKernelGGL(k_goss_hist, dim3(hist_blocks), dim3(GOSS_HIST_THREADS), 0, s, g, rows,
-                           ctl, buckets);
+                           ctl, buckets, ctl_prev, walk_part, walk_part ? walk_nparts : 0);
+    } else if (walk_part) {
+        hipLaunchKernelGGL(k_tree_start, dim3(1), dim3(64), 0, s, ctl, ctl_prev, walk_part,
+                           walk_nparts);
+    }
     const int64_t blocks = std::max<int64_t>(
         1, std::min<int64_t>((rows + SEL_CHUNK - 1) / SEL_CHUNK, SAMPLE_MAX_BLOCKS));
     hipLaunchKernelGGL(k_goss_select, dim3((unsigned)blocks), dim3(SEL_THREADS), 0, s, sp, g, h,
                        rows, buckets, ctl, partial, order, h_kept, kept);
-    hipLaunchKernelGGL(k_grad_max_final, dim3(1), dim3(64), 0, s, partial, (int)blocks, ctl);
     // the kept count is known only on the device: a fixed grid strides over it
     // (a rows-sized grid of mostly idle blocks measured 7 us slower)
     const unsigned qblocks =
         (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
     hipLaunchKernelGGL(k_quantize_sampled, dim3(qblocks), dim3(256), 0, s, ctl, buckets, order,
-                       h_kept, plan ? *plan : RootPlan{}, plan ? 1 : 0,
+                       h_kept, partial, (int)blocks, plan ? *plan : RootPlan{}, plan ? 1 : 0,
                        fix ? *fix : PendingFixup{});
     return hipGetLastError();
 }

@@ -271,11 +271,16 @@ struct RootPlan {
 };
 // With plan non-null the last pass (the kept rows' quantiser) also plans the
 // root, in its first workgroup; with fix non-null that workgroup first does
-// the previous tree's deepest-level fixup.
+// the previous tree's deepest-level fixup.  With walk_part non-null the tree's
+// start (launch_tree_start(ctl, ctl_prev, walk_part, walk_nparts)) is left to
+// the first pass, which does it itself.  partial is scratch for
+// grad_max_scratch_words() words and may be walk_part.
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
                          uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
                          Entry *order, float *h_kept, uint8_t *kept,
-                         const RootPlan *plan = nullptr, const PendingFixup *fix = nullptr);
+                         const RootPlan *plan = nullptr, const PendingFixup *fix = nullptr,
+                         TreeCtl *ctl_prev = nullptr, const uint32_t *walk_part = nullptr,
+                         int walk_nparts = 0);
 // Every row quantised with ctl->max_gh into order[i] = {i, packed (qg, qh)};
 // with implicit_rows, into the u32 words ((uint32_t *)order)[i] = packed
 // (qg, qh) only: the root's rows in order, row i being entry i.  With plan

@@ -1725,8 +1725,13 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     // reduction is left, done in the same launch
     mbk::TreeCtl *prev = t.ctl_pending >= 0 ? t.ctl_hist.ptr + t.ctl_pending : nullptr;
     t.ctl_pending = -1;
-    MB_HIP(mbk::launch_tree_start(s, ctl, prev, t.walk_gparts > 0 ? t.gmax_part.ptr : nullptr,
-                                  t.walk_gparts));
+    // a sampled tree whose gradients the walk computed leaves its start to the
+    // sampling's first pass
+    const int walk_parts = t.walk_gparts;
+    const bool start_in_sample = sampled && walk_parts > 0;
+    if (!start_in_sample)
+        MB_HIP(mbk::launch_tree_start(s, ctl, prev, walk_parts > 0 ? t.gmax_part.ptr : nullptr,
+                                      walk_parts));
     if (t.walk_gparts > 0) {
         t.walk_gparts = 0;
     } else {
@@ -1737,7 +1742,9 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     if (sampled)
         MB_HIP(mbk::launch_sample(s, sample_params(t, tree), t.rows, ctl, t.goss_buckets.ptr,
                                   t.gmax_part.ptr, t.samp_g.ptr, t.samp_h.ptr, order,
-                                  t.samp_h_kept.ptr, kept, plan, fixp));
+                                  t.samp_h_kept.ptr, kept, plan, fixp,
+                                  start_in_sample ? prev : nullptr,
+                                  start_in_sample ? t.gmax_part.ptr : nullptr, walk_parts));
     else
         MB_HIP(mbk::launch_quantize(s, t.gp, t.preds.ptr, t.labels.ptr, t.weights.ptr, t.rows,
                                     ctl, order, implicit_rows, plan, fixp));
