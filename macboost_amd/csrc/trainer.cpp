@@ -1941,8 +1941,10 @@ static void finish_leafwise(Trainer &t, int tree, const mbk::TreeOut &out, bool 
     } else {
         training_walk(t, tree, out, deep_counts ? t.count.ptr : nullptr, nullptr);
         if (deep_counts) {
+            // the depth-D covers, which nothing reads before the next tree's
+            // root pass writes them (or the end of the grow call)
             const mbk::LevelArgs ld{t.D, (uint32_t)((1u << t.D) - 1), 1u << t.D, 1u};
-            MB_HIP(mbk::launch_final_fixup(s, ld, t.count.ptr, out, false));
+            t.fix_pending = mbk::PendingFixup{ld, t.count.ptr, out, 0, 1};
         }
     }
     if (t.has_valid)

@@ -599,6 +599,7 @@ def test_goss_and_bagging_identical_trees(params):
     {"num_trees": 8, "max_depth": 6, "monotone_constraints": [0, 0, 0, 1, 0, -1]},
     {"num_trees": 8, "max_depth": 5, "learning_rate": 0.5, "goss": True,
      "objective": "binary"},
+    {"num_trees": 8, "max_depth": 6, "num_leaves": 23},
 ])
 def test_trees_grown_in_several_calls_equal_one_call(params):
     # A level-wise tree's deepest covers (and empty leaves) are written by the
