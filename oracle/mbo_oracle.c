@@ -94,11 +94,15 @@ static int cmp_float(const void *a, const void *b) {
     return (x > y) - (x < y);
 }
 
-void orc_compute_edges(const float *x, int64_t rows, int32_t cols, int64_t rs,
-                       int64_t cs, int32_t num_bins, const uint8_t *is_cat,
-                       int64_t sample_cap, float *edges) {
+void orc_compute_edges_planted(const float *x, int64_t rows, int32_t cols, int64_t rs,
+                               int64_t cs, int32_t num_bins, const uint8_t *is_cat,
+                               int64_t sample_cap, float *edges, int32_t plant) {
+    /* Binner.swift:27-30: dataBins = numBins - 1 (the last bin is the missing
+     * bin), numEdges = dataBins - 1, step = max(1, rows / sampleCap). */
     int32_t data_bins = num_bins - 1, num_edges = data_bins - 1;
     int64_t step = rows / sample_cap;
+    if (plant == ORC_PLANT_EDGE_CEIL) step = (rows + sample_cap - 1) / sample_cap;
+    if (plant == ORC_PLANT_EDGE_NOSTRIDE) step = 1;
     if (step < 1) step = 1;
     memset(edges, 0, sizeof(float) * (size_t)cols * (size_t)num_edges);
 #pragma omp parallel
@@ -106,22 +110,36 @@ void orc_compute_edges(const float *x, int64_t rows, int32_t cols, int64_t rs,
         float *sample = (float *)malloc(sizeof(float) * (size_t)(rows / step + 1));
 #pragma omp for schedule(dynamic, 1)
         for (int32_t f = 0; f < cols; ++f) {
-            if (is_cat && is_cat[f]) continue;
+            if (is_cat && is_cat[f]) continue;        /* Binner.swift:36 */
+            /* Binner.swift:37-44: rows 0, step, 2*step, ... ; NaN skipped */
             int64_t m = 0;
             for (int64_t i = 0; i < rows; i += step) {
                 float v = x[i * rs + (int64_t)f * cs];
                 if (!isnan(v)) sample[m++] = v;
             }
-            if (m == 0) continue;                     /* all-NaN column */
+            if (m == 0) continue;                     /* all-NaN column: edges stay 0 */
             qsort(sample, (size_t)m, sizeof(float), cmp_float);
+            /* Binner.swift:48-51: edge k = sample[min(m-1, (k+1)*m / dataBins)];
+             * k + 1 <= dataBins - 1, so the index never passes m - 1 */
             for (int32_t k = 0; k < num_edges; ++k) {
-                int64_t idx = ((int64_t)(k + 1) * m) / data_bins;
+                int64_t num = (int64_t)(k + 1) * m, den = data_bins;
+                if (plant == ORC_PLANT_EDGE_K) num = (int64_t)k * m;
+                if (plant == ORC_PLANT_EDGE_K2) num = (int64_t)(k + 2) * m;
+                if (plant == ORC_PLANT_EDGE_NUMBINS) den = num_bins;
+                if (plant == ORC_PLANT_EDGE_M1) num = (int64_t)(k + 1) * (m - 1);
+                int64_t idx = num / den;
                 if (idx > m - 1) idx = m - 1;
                 edges[(int64_t)f * num_edges + k] = sample[idx];
             }
         }
         free(sample);
     }
+}
+
+void orc_compute_edges(const float *x, int64_t rows, int32_t cols, int64_t rs,
+                       int64_t cs, int32_t num_bins, const uint8_t *is_cat,
+                       int64_t sample_cap, float *edges) {
+    orc_compute_edges_planted(x, rows, cols, rs, cs, num_bins, is_cat, sample_cap, edges, 0);
 }
 
 uint8_t orc_bin_value(float v, const float *e, int32_t num_bins, int is_cat) {

@@ -56,6 +56,13 @@ typedef struct {
  * Never set outside tests/. */
 #define ORC_PLANT_FIFO_PICK 1      /* leaf-wise: first open leaf with gain > min, not the best */
 #define ORC_PLANT_GOSS_NO_SEED 2   /* GOSS/bagging keep hash without the tree seed */
+/* quantile edges (orc_compute_edges_planted only) */
+#define ORC_PLANT_EDGE_K 3         /* edge k = sample[k*m/dataBins]: one quantile early */
+#define ORC_PLANT_EDGE_K2 4        /* edge k = sample[(k+2)*m/dataBins]: one quantile late */
+#define ORC_PLANT_EDGE_NUMBINS 5   /* divides by numBins, not numBins - 1 */
+#define ORC_PLANT_EDGE_M1 6        /* (k+1)*(m-1)/dataBins: the last index, not the count */
+#define ORC_PLANT_EDGE_CEIL 7      /* stride ceil(rows / sampleCap), not the floor */
+#define ORC_PLANT_EDGE_NOSTRIDE 8  /* every row sampled */
 
 /* OpenMP threads used by every parallel loop (<= 0: all processors). */
 void orc_set_threads(int32_t n);
@@ -96,6 +103,11 @@ void orc_friedman(int64_t rows, int32_t cols, uint64_t seed, float noise,
 void orc_compute_edges(const float *x, int64_t rows, int32_t cols,
                        int64_t row_stride, int64_t col_stride, int32_t num_bins,
                        const uint8_t *is_cat, int64_t sample_cap, float *edges);
+/* TEST ONLY: orc_compute_edges with a planted mistake (ORC_PLANT_EDGE_*; 0 = faithful). */
+void orc_compute_edges_planted(const float *x, int64_t rows, int32_t cols,
+                               int64_t row_stride, int64_t col_stride, int32_t num_bins,
+                               const uint8_t *is_cat, int64_t sample_cap, float *edges,
+                               int32_t plant);
 uint8_t orc_bin_value(float v, const float *edges_f, int32_t num_bins, int is_cat);
 void orc_bin_matrix(const float *x, int64_t rows, int32_t cols, int64_t row_stride,
                     int64_t col_stride, const float *edges, const uint8_t *is_cat,

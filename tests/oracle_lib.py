@@ -19,6 +19,12 @@ LIB_PATH = ROOT / "oracle" / "liboracle.so"
 # planted mistakes (oracle/mbo_oracle.h ORC_PLANT_*): tests only
 PLANT_FIFO_PICK = 1
 PLANT_GOSS_NO_SEED = 2
+PLANT_EDGE_K = 3
+PLANT_EDGE_K2 = 4
+PLANT_EDGE_NUMBINS = 5
+PLANT_EDGE_M1 = 6
+PLANT_EDGE_CEIL = 7
+PLANT_EDGE_NOSTRIDE = 8
 
 FLAG_DEFAULT_LEFT = 1
 FLAG_CATEGORICAL = 2
@@ -99,6 +105,8 @@ def _configure(l: ctypes.CDLL) -> None:
     l.orc_splitmix_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
     l.orc_friedman.argtypes = [_I64, _I32, ctypes.c_uint64, _F, _P, _P]
     l.orc_compute_edges.argtypes = [_P, _I64, _I32, _I64, _I64, _I32, _P, _I64, _P]
+    l.orc_compute_edges_planted.argtypes = [_P, _I64, _I32, _I64, _I64, _I32, _P, _I64, _P,
+                                            _I32]
     l.orc_bin_matrix.argtypes = [_P, _I64, _I32, _I64, _I64, _P, _P, _I32, _P]
     l.orc_base_score.restype = _F
     l.orc_base_score.argtypes = [_P, _P, _I64, _I32, _F]
@@ -147,13 +155,26 @@ def friedman(rows: int, cols: int, seed: int, noise: float = 1.0):
     return x, y
 
 
-def compute_edges(x_fm: np.ndarray, num_bins: int, is_cat=None, sample_cap: int = 200_000):
+def compute_edges(x_fm: np.ndarray, num_bins: int, is_cat=None, sample_cap: int = 200_000,
+                  plant: int = 0, row_major: bool = False):
+    """Quantile edges of a feature-major [cols, rows] matrix; row_major reads the
+    transposed copy through the row/column strides instead. plant != 0 (tests only)
+    plants one of the PLANT_EDGE_* mistakes."""
     cols, rows = x_fm.shape
-    x_fm = np.ascontiguousarray(x_fm, dtype=np.float32)
+    if row_major:
+        x = np.ascontiguousarray(np.asarray(x_fm, dtype=np.float32).T)
+        rs, cs = cols, 1
+    else:
+        x = np.ascontiguousarray(x_fm, dtype=np.float32)
+        rs, cs = 1, rows
     cat = None if is_cat is None else np.ascontiguousarray(is_cat, dtype=np.uint8)
     edges = np.zeros((cols, num_bins - 2), dtype=np.float32)
-    lib().orc_compute_edges(_ptr(x_fm), rows, cols, 1, rows, num_bins, _ptr(cat), sample_cap,
-                            _ptr(edges))
+    if plant:
+        lib().orc_compute_edges_planted(_ptr(x), rows, cols, rs, cs, num_bins, _ptr(cat),
+                                        sample_cap, _ptr(edges), plant)
+    else:
+        lib().orc_compute_edges(_ptr(x), rows, cols, rs, cs, num_bins, _ptr(cat), sample_cap,
+                                _ptr(edges))
     return edges
 
 

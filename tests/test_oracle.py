@@ -77,6 +77,101 @@ def test_edges_quantiles_and_bin_invariant(oracle):
     assert num[0, 0] == nb - 1                              # NaN -> missing bin
 
 
+def _perm_column_with_holes(m, nan_holes, seed):
+    """A column whose non-NaN values are a permutation of 0..m-1, with NaN at
+    nan_holes random rows: its sorted sample is exactly 0..m-1."""
+    rng = np.random.default_rng(seed)
+    col = np.full(m + nan_holes, np.nan, np.float32)
+    live = np.sort(rng.choice(m + nan_holes, size=m, replace=False))
+    col[live] = rng.permutation(m).astype(np.float32)
+    return col
+
+
+def _edges_rule(sorted_sample, num_bins):
+    # Binner.swift:48-51 on a known sorted sample: edge k = sample[min(m-1, (k+1)m/(B-1))]
+    m = len(sorted_sample)
+    return np.array([sorted_sample[min(m - 1, (k + 1) * m // (num_bins - 1))]
+                     for k in range(num_bins - 2)], np.float32)
+
+
+_PERM_CASES = [(m, nb) for nb in (4, 64, 256) for m in (7, 37, 254, 1000, 4999)]
+
+
+@pytest.mark.parametrize("plant", [0, O.PLANT_EDGE_K, O.PLANT_EDGE_K2, O.PLANT_EDGE_NUMBINS,
+                                   O.PLANT_EDGE_M1])
+def test_edges_index_rule_known_answers(oracle, plant):
+    # A permuted 0..m-1 column with NaN holes, fewer rows than the sample cap
+    # (step 1): edge k must be exactly min(m-1, floor((k+1)m/(B-1))) at B = 4, 64
+    # and 256 (Binner.swift:48-51). Each planted index mistake fails some case.
+    mismatches = 0
+    for i, (m, nb) in enumerate(_PERM_CASES):
+        col = _perm_column_with_holes(m, nan_holes=m // 3 + 1, seed=100 + i)
+        want = np.array([min(m - 1, (k + 1) * m // (nb - 1)) for k in range(nb - 2)],
+                        np.float32)
+        for row_major in (False, True):
+            got = O.compute_edges(col[None, :], nb, plant=plant, row_major=row_major)[0]
+            mismatches += not np.array_equal(got, want)
+    if plant == 0:
+        assert mismatches == 0
+    else:
+        assert mismatches > 0, f"planted edge mistake {plant} passed every known answer"
+
+
+@pytest.mark.parametrize("plant", [0, O.PLANT_EDGE_CEIL, O.PLANT_EDGE_NOSTRIDE])
+def test_edges_stride_known_answers(oracle, plant):
+    # Binner.swift:30, :37-44: step = max(1, rows / sampleCap), rows 0, step, 2 step,
+    # ... are sampled, NaN skipped. Rows on the stride hold a descending ramp, with
+    # every 7th of them NaN; rows off it hold values above 1e9 that no edge may
+    # show. The sample is then known exactly. 600,001 rows at the default cap
+    # (step 3), and floor-vs-ceil boundaries at small caps.
+    cases = [(600_001, 200_000), (2_999, 1_000), (4_000, 1_000), (3_999, 1_000),
+             (999, 1_000), (1_001, 1_000)]
+    mismatches = 0
+    for rows, cap in cases:
+        step = max(1, rows // cap)
+        i = np.arange(rows, dtype=np.int64)
+        col = (1e9 + i).astype(np.float32)
+        on = i % step == 0
+        col[on] = (rows - i[on]).astype(np.float32)
+        j = i // step
+        col[on & (j % 7 == 3)] = np.nan
+        sample = np.sort(col[on & ~np.isnan(col)])
+        assert sample.max() < 1e9 and np.all(np.diff(sample) > 0)
+        for nb in (4, 64, 256):
+            want = _edges_rule(sample, nb)
+            got = O.compute_edges(col[None, :], nb, sample_cap=cap, plant=plant)[0]
+            mismatches += not np.array_equal(got, want)
+    if plant == 0:
+        assert mismatches == 0
+    else:
+        assert mismatches > 0, f"planted stride mistake {plant} passed every known answer"
+
+
+def test_edges_sample_is_exactly_the_stride_multiples(oracle):
+    # A column of 1,000,003 rows holding its row index (exact in f32): step =
+    # 1,000,003 / 200,000 = 5, so the sample is 0, 5, ..., 1,000,000 (m = 200,001)
+    # and edge k = 5 * floor((k+1) * 200,001 / (B-1)).
+    rows = 1_000_003
+    col = np.arange(rows, dtype=np.float32)
+    for nb in (4, 64, 256):
+        got = O.compute_edges(col[None, :], nb)[0]
+        m = 200_001
+        want = np.array([5 * min(m - 1, (k + 1) * m // (nb - 1)) for k in range(nb - 2)],
+                        np.float32)
+        assert np.array_equal(got, want)
+        assert np.all(got % 5 == 0)
+
+
+def test_edges_all_nan_and_categorical_columns_stay_zero(oracle):
+    # Binner.swift:36 (categorical: no edges) and :45 (all-NaN column: skipped);
+    # the edge buffer is zero-initialised (:31).
+    col = np.arange(100, dtype=np.float32)
+    x = np.stack([np.full(100, np.nan, np.float32), col, col])
+    e = O.compute_edges(x, 16, is_cat=[0, 0, 1])
+    assert np.all(e[0] == 0) and np.all(e[2] == 0)
+    assert np.array_equal(e[1], _edges_rule(col, 16))
+
+
 def test_quantize_range(oracle):
     rng = np.random.default_rng(1)
     preds = rng.normal(size=5000).astype(np.float32)
