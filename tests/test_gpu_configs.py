@@ -1,16 +1,23 @@
 """GPU parity at the benchmark configurations' own shapes, through the C ABI.
 
 * 10M x 100 Friedman #1, 256 bins: leaf-wise with 63 leaves (2 trees) and
-  level-wise depth 6 (1 tree), every model array equal to the oracle's.  The
-  root segment (10M entries) is larger than the leaf-wise partition grid
-  (512 blocks x 8,192 entries), so the grid-stride partition and the plan run
-  by the block that completes it are exercised, as is the planar root copy.
+  level-wise depth 6 (1 tree), every model array equal to the oracle's.  A
+  63-leaf depth-6 tree grows in depth rounds on the level-wise partition; the
+  level-wise tree also reads the planar root copy.
+* 5M x 20 Friedman #1, leaf-wise with 63 leaves and max_depth 10 (2 trees):
+  trees deeper than 8 grow one leaf per step, and the root segment (5M
+  entries) is larger than the per-step partition grid (512 blocks x 8,192
+  entries), so its grid-stride loop and the plan run by the block that
+  reserves a segment's last entries are compared with the oracle.
+* HIGGS-like 10.5M x 28 logistic (the training 10M rows): 2 plain trees, and
+  4 GOSS (0.2, 0.1) trees at learning rate 0.5, whose trees 2 and 3 sample
+  their rows past the ceil(1/lr) = 2 warm-up trees.
 * 100 leaf-wise trees on the same data: 500k held-out rows predicted bit for
   bit against the oracle's predictCPU restatement, and TreeSHAP of 200k rows
   within 1e-5 relative of the oracle on 2,000 of them (every 100th), with all
   200k rows summing to their predictions.
-* HIGGS-like 10M x 28 logistic with GOSS (0.2, 0.1): the 200k-row leg, past
-  the ceil(1/lr) = 10 warm-up trees.
+* HIGGS-like 200k x 28 logistic with GOSS (0.2, 0.1): 20 trees, past the
+  ceil(1/lr) = 10 warm-up trees.
 * 1M x 100 with 20 categorical columns and 20% NaN, with the 200k-row
   validation set scored after every tree: the per-iteration metric and the
   best iteration equal the oracle's.
@@ -101,6 +108,51 @@ def test_c5_predict_500k_bitexact_and_treeshap(friedman10m):
     # every row's contributions sum to its raw prediction
     s = c.astype(np.float64).sum(axis=1)
     assert np.max(np.abs(s - got[:200_000])) < 1e-3
+
+
+def test_leafwise_per_step_depth10_large_root_segment():
+    # LeafWiseTests.swift:205-217 grows best-first trees to a depth limit; past
+    # depth 8 this library grows them one leaf per step.
+    rows, cols = 5_000_000, 20
+    assert rows > 512 * 8192
+    O.set_threads(0)
+    say(f"{rows} x {cols} leaf-wise 63 leaves, max_depth 10, 2 trees: GPU vs oracle")
+    x, y = mb.friedman(rows, cols, 7)
+    edges = O.compute_edges(x, 256)
+    bins = O.bin_matrix(x, edges, 256)
+    _, ref = _compare(x, y, edges, bins, {"num_trees": 2, "max_depth": 10, "num_leaves": 63,
+                                          "num_bins": 256})
+    assert ((ref.forest.feature >= 0).sum(axis=1) == 62).all()
+    # best-first went past depth 6 somewhere (a node index beyond a depth-6 heap)
+    deep = [np.nonzero(ref.forest.feature[t] >= 0)[0].max() for t in range(2)]
+    assert max(deep) >= 127
+
+
+@pytest.fixture(scope="module")
+def higgs10m():
+    say("generating HIGGS-like 10.5M x 28 (seed 42), training rows 10M")
+    x, y = D.c4_higgs_like(10_500_000, 42)
+    return np.ascontiguousarray(x[:, :10_000_000]), np.ascontiguousarray(y[:10_000_000])
+
+
+def test_c4_10m_plain_identical_trees(higgs10m):
+    # README.md:62: HIGGS 10.5M x 28, binary logistic, 256 bins, depth 6
+    x, y = higgs10m
+    say("HIGGS-like 10M x 28 logistic, 2 trees: GPU vs oracle")
+    O.set_threads(0)
+    check_identical(x, y, {"num_trees": 2, "max_depth": 6, "num_bins": 256,
+                           "objective": "binary"})
+
+
+def test_c4_10m_goss_identical_trees(higgs10m):
+    # GOSSTests.swift:85-110; README.md:63: GOSS (0.2, 0.1). At lr 0.5 the
+    # warm-up is ceil(1/0.5) = 2 trees, so trees 2 and 3 sample their rows.
+    x, y = higgs10m
+    say("HIGGS-like 10M x 28 logistic + GOSS(0.2, 0.1), lr 0.5, 4 trees: GPU vs oracle")
+    O.set_threads(0)
+    check_identical(x, y, {"num_trees": 4, "max_depth": 6, "num_bins": 256,
+                           "objective": "binary", "learning_rate": 0.5, "goss": True,
+                           "goss_top_rate": 0.2, "goss_other_rate": 0.1})
 
 
 def test_c4_goss_identical_trees():
