@@ -1393,27 +1393,35 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 // Every lane owns one row of the item and a plane of P = min(W, 32) features
 // of that row (W = 64: two lanes per row, one per 32-feature half; W <= 32:
 // one row per lane).  At step s (0 <= s < P) lane r adds its row's value to
-// feature (r & (P-1)) ^ s of its plane, so the 64 lanes of one ds_add_u64
-// always hit 64 distinct cells, spread evenly over the LDS banks, and the
-// row's packed (qg, qh) word never leaves the lane.  The LDS histogram is two
-// planes of [256 bins][32 columns] u64 (128 KiB); cell (plane, bin, column)
-// sits at byte address plane*65536 + bin*256 + column*8, which one v_perm_b32
-// assembles from the bin byte and a per-lane column word.  Each lane gathers
-// its P bytes with 16B loads whose chunk order, and then dword order, are
-// permuted once per row so that step s reads a fixed register and byte.
-// Columns hold feature c (W = 64: 32*plane + c) or copy c / W of feature
-// c % W (W <= 32), summed when the item is flushed.  Loads are pipelined:
-// data three batches ahead, entries nine.
+// feature (r & (P-1)) ^ s of its plane, so the 32 lanes of each half-wave hit
+// 32 distinct cells, one per bank pair, and the row's packed (qg, qh) word
+// never leaves the lane.  (A ds_add_u64 is served one half-wave at a time:
+// the two halves may share cells at no cost, while a 2-way bank conflict
+// inside a half costs 30%.)  The LDS histogram is two planes of [256 bins][32
+// columns] u64 (128 KiB); cell (plane, bin, column) sits at byte address
+// plane*65536 + bin*256 + column*8, which one v_perm_b32 assembles from the
+// bin byte and a per-lane column word.  Each lane gathers its P bytes with 16B
+// loads whose chunk order, and then dword order, are permuted once per row so
+// that step s reads a fixed register and byte.  Columns hold feature c (W = 64:
+// 32*plane + c; W = 32: plane 0, shared by both halves) or copy c / W of
+// feature c % W (W <= 16), summed when the item is flushed.
+//
+// Extras (W = 32, Shape::extras): tile t also adds E_t <= 2 features of the
+// last layout tile, from one dword per row.  Plane 1 then holds 32 / E_t
+// copies of them: at extra step j lane r adds to column (r & 31) ^ j, whose
+// low bit (E_t = 2) names the extra feature, so each half-wave again hits 32
+// distinct bank pairs.  Loads are pipelined: data three batches ahead,
+// entries nine.
 // ---------------------------------------------------------------------------
 
 constexpr int HIST_THREADS = 1024;
 constexpr int HIST_LDS_BYTES = 2 * 256 * 32 * 8;     // two planes of [256][32] u64, static
 // ring depths chosen by measurement (3 / 9 beat 2..6 / 6..15 at 10M x 100:
 // deeper data rings cost L2 reuse between the two tiles of a row)
-constexpr int HIST_DATA_RING = 3;
-constexpr int HIST_ENTRY_RING = 9;
-static_assert(HIST_ENTRY_RING > HIST_DATA_RING, "a data refill needs the entry DR batches ahead");
-static_assert(HIST_ENTRY_RING % HIST_DATA_RING == 0, "batch k of every round uses data slot k % DR");
+// (per lanes-per-row mode below: 3 / 9 with two lanes per row, 4 / 8 with four;
+// at four lanes per row 4 to 8 data batches measured the same)
+template <int LPR> constexpr int hist_data_ring() { return LPR == 4 ? 4 : 3; }
+template <int LPR> constexpr int hist_entry_ring() { return LPR == 4 ? 8 : 9; }
 // true: the per-lane LDS column words sit in a 32-register table; false: each
 // is rebuilt with one XOR per update (frees the table's registers)
 constexpr bool HIST_COLW_TABLE = true;
@@ -1468,27 +1476,41 @@ __device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0
 // padding columns, which are never reduced).
 // IMPLICIT: order holds one u32 packed (qg, qh) per row of the root, entry j
 // being row j (k_quantize's implicit form).
-template <int W, bool IMPLICIT>
+// LPR: lanes per row of a 64-wide tile.  2: 32 features per lane (the planar
+// root, whose rows are contiguous); 4: 16 per lane, so one 16-B load
+// instruction covers a gathered row's whole tile (-4% on deep levels at
+// 10M x 100 against 2, which needs two).  Narrower tiles: one row per lane.
+template <int W, int LPR, bool IMPLICIT>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
                                                        const Entry *__restrict__ order,
                                                        const HistItem *__restrict__ items,
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
-                                                       HistLayout lay, int32_t nb, int32_t cols) {
-    constexpr int P = W >= 32 ? 32 : W;              // features per lane
-    constexpr int RPB = W == 64 ? 32 : 64;           // rows per wavefront batch
-    constexpr int DR = HIST_DATA_RING, ER = HIST_ENTRY_RING;
+                                                       HistLayout lay, Shape sh) {
+    static_assert(W == 64 ? (LPR == 2 || LPR == 4) : LPR == 1, "lanes per row");
+    constexpr int P = W / LPR > 32 ? 32 : W / LPR;   // features per lane
+    constexpr int RPB = 64 / LPR;                    // rows per wavefront batch
+    constexpr bool XTRA = W == 32;                   // extras possible (plane 1 free)
+    constexpr int DR = hist_data_ring<LPR>(), ER = hist_entry_ring<LPR>();
+    static_assert(ER > DR, "a data refill needs the entry DR batches ahead");
+    static_assert(ER % DR == 0, "batch k of every round uses data slot k % DR");
     __shared__ uint64_t hist_lds[HIST_LDS_BYTES / 8];
+    const int32_t nb = sh.num_bins, cols = sh.cols, PW = sh.part_w;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: loop bounds stay uniform
     const uint32_t nwaves = HIST_THREADS / 64;
-    const uint32_t rl = W == 64 ? (uint32_t)(lane & 31) : (uint32_t)lane;
-    const uint32_t byte_off = W == 64 ? (uint32_t)(lane >> 5) * 32u : 0u;
+    // lane = q * RPB + rl: row rl of the batch, features q*P .. q*P + P-1
+    const uint32_t rl = (uint32_t)lane % (uint32_t)RPB, q = (uint32_t)lane / (uint32_t)RPB;
+    const uint32_t byte_off = W == 64 ? q * (uint32_t)P : 0u;
     const uint32_t m = ((uint32_t)lane & (uint32_t)(P - 1)) >> 2;
     const uint32_t cx = P == 32 ? (m >> 2) : 0u;
     const bool b0 = (m & 1u) != 0, b1 = (m & 2u) != 0;
-    const uint32_t colbase = ((uint32_t)(lane >> 5) << 16) | (((uint32_t)lane & 31u) << 3);
+    // W = 64: feature q*P + x sits in plane (q*P) >> 5, column ((q*P) & 31) + x
+    const uint32_t colbase =
+        W == 64 ? (((q * (uint32_t)P) >> 5) << 16) | ((((q * (uint32_t)P) & 31u) + rl) << 3)
+        : W == 32 ? (((uint32_t)lane & 31u) << 3)
+                  : (((uint32_t)(lane >> 5) << 16) | (((uint32_t)lane & 31u) << 3));
     uint32_t colw[HIST_COLW_TABLE ? P : 1];
     if constexpr (HIST_COLW_TABLE) {
 #pragma unroll
@@ -1498,18 +1520,20 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 #pragma unroll
     for (int t = 0; t < 4; ++t)
         sel[t] = 0x0C020000u | ((4u + (((uint32_t)lane & 3u) ^ (uint32_t)t)) << 8);
+    // extra step j: plane 1, column (lane & 31) ^ j
+    const uint32_t cwx0 = 0x10000u | (((uint32_t)lane & 31u) << 3);
+    const uint32_t cwx1 = cwx0 ^ 8u;
     char *lds = reinterpret_cast<char *>(hist_lds);
     const uint32_t stride = nwaves * RPB;
     const uint32_t nitems = ctl->num_items;
     // Items are chunk-major (the tiles of one row chunk are adjacent).  With
-    // workgroups dispatched round-robin over 8 XCDs, block b = 16q + 8h + x
-    // runs on XCD x and takes item 16q + 2x + h, so both tiles of a chunk read
-    // the same 128B row lines through one L2.
+    // workgroups dispatched round-robin over 8 XCDs (block b on XCD b % 8),
+    // XCD x takes the contiguous items x*G/8 .. (x+1)*G/8 - 1 of each round of
+    // G, so the tile items of a chunk read the same row lines through one L2
+    // (always at 2 tiles per chunk; at 3, all but the chunks split by a range
+    // boundary).
     uint32_t slot = blockIdx.x;
-    if ((gridDim.x & 15u) == 0) {
-        const uint32_t q = blockIdx.x >> 4, h = (blockIdx.x >> 3) & 1u, x = blockIdx.x & 7u;
-        slot = (q << 4) + (x << 1) + h;
-    }
+    if ((gridDim.x & 7u) == 0) slot = (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);
     for (uint32_t it = slot; it < nitems; it += gridDim.x) {
         const HistItem item = items[it];
         const uint32_t cnt = item.count;            // >= 1
@@ -1522,21 +1546,39 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
             (size_t)((int32_t)item.tile == lay.last_tile ? lay.last_stride : lay.stride);
         const Entry *ent = order + item.start;
         const uint32_t *ent_q = reinterpret_cast<const uint32_t *>(order) + item.start;
+        // the item's extras: count, first, and the per-lane byte selectors
+        const int32_t ne = XTRA ? tile_extra_count(sh, (int32_t)item.tile) : 0;
+        const int32_t xf = XTRA ? tile_extra_first(sh, (int32_t)item.tile) : 0;
+        const uint32_t *xsrc = reinterpret_cast<const uint32_t *>(
+            tiled + lay.x_off + (size_t)(xf & ~3));
+        const size_t xs4 = (size_t)(lay.x_stride >> 2);
+        const uint32_t xb = (uint32_t)(xf & 3);
+        const uint32_t e0 = ne == 2 ? ((uint32_t)lane & 1u) : 0u;
+        const uint32_t selx0 = 0x0C020000u | ((4u + xb + e0) << 8);
+        const uint32_t selx1 = 0x0C020000u | ((4u + xb + (e0 ^ 1u)) << 8);
         // entry j of the item (IMPLICIT: row start + j with its packed word)
         auto entry = [&](uint32_t j) {
             if constexpr (IMPLICIT) return Entry{item.start + j, ent_q[j]};
             else return ent[j];
+        };
+        auto load_x = [&](uint32_t row) -> uint32_t {
+            if constexpr (XTRA) return ne ? xsrc[(size_t)row * xs4] : 0u;
+            else return 0u;
         };
         const uint32_t g0 = (uint32_t)wave * RPB;
         // loads past the item's end read its last entry (in bounds); their
         // rows are given value 0 when processed
         Entry er[ER];
         RowRaw<P> dr[DR];
+        uint32_t xr[XTRA ? DR : 1];
 #pragma unroll
         for (int k = 0; k < ER; ++k) er[k] = entry(min(g0 + (uint32_t)k * stride + rl, last));
 #pragma unroll
-        for (int k = 0; k < DR; ++k) dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * row_bytes, cx);
-        auto process = [&](uint32_t g, const Entry &e, const RowRaw<P> &raw) {
+        for (int k = 0; k < DR; ++k) {
+            dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * row_bytes, cx);
+            if constexpr (XTRA) xr[k] = load_x(er[k].row);
+        }
+        auto process = [&](uint32_t g, const Entry &e, const RowRaw<P> &raw, uint32_t x) {
             // rows past the item's end carry value 0
             const uint32_t ghq = g + rl < cnt ? e.ghq : 0u;
             const int32_t qg = (int32_t)(int16_t)(uint16_t)(ghq >> 16);
@@ -1550,6 +1592,16 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                 const uint32_t addr = __builtin_amdgcn_perm(cur.d[s >> 2], cw, sel[s & 3]);
                 atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
             }
+            if constexpr (XTRA) {
+                if (ne >= 1) {                       // uniform per item
+                    const uint32_t addr = __builtin_amdgcn_perm(x, cwx0, selx0);
+                    atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
+                }
+                if (ne >= 2) {
+                    const uint32_t addr = __builtin_amdgcn_perm(x, cwx1, selx1);
+                    atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
+                }
+            }
         };
         // main rounds: all ER batches exist, no exits inside the round, so the
         // refill loads stay where they are issued
@@ -1558,9 +1610,10 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 #pragma unroll
             for (int k = 0; k < ER; ++k) {
                 const uint32_t g = base + (uint32_t)k * stride;
-                process(g, er[k], dr[k % DR]);
+                process(g, er[k], dr[k % DR], XTRA ? xr[XTRA ? k % DR : 0] : 0u);
                 // refill: data for batch +DR (its entry is already held), entry for batch +ER
                 dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * row_bytes, cx);
+                if constexpr (XTRA) xr[k % DR] = load_x(er[(k + DR) % ER].row);
                 er[k] = entry(min(g + (uint32_t)ER * stride + rl, last));
             }
         }
@@ -1569,27 +1622,37 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         for (int k = 0; k < ER; ++k) {
             const uint32_t g = base + (uint32_t)k * stride;
             if (g >= cnt) break;                     // uniform per wavefront
-            process(g, er[k], dr[k % DR]);
-            if (k + DR < ER)
+            process(g, er[k], dr[k % DR], XTRA ? xr[XTRA ? k % DR : 0] : 0u);
+            if (k + DR < ER) {
                 dr[k % DR] = load_row_raw<P>(tile + (size_t)er[(k + DR) % ER].row * row_bytes, cx);
+                if constexpr (XTRA) xr[k % DR] = load_x(er[(k + DR) % ER].row);
+            }
         }
         __syncthreads();
-        // flush to the item's partial, layout [nb][W]; the last tile's padding
-        // columns are neither written nor read
-        uint64_t *out = partials + (size_t)it * (size_t)(nb * W);
+        // flush to the item's partial, layout [nb][PW]; padding columns (past
+        // the last feature, or extras the tile does not carry) are neither
+        // written nor read
+        uint64_t *out = partials + (size_t)it * (size_t)(nb * PW);
         const int wreal = min(W, cols - (int)item.tile * W);
-        for (int k = tid; k < nb * W; k += HIST_THREADS) {
-            const int b = k / W, f = k % W;
-            if (f >= wreal) continue;
-            uint64_t acc;
-            if constexpr (W == 64) {
-                acc = hist_lds[(f >> 5) * 8192 + b * 32 + (f & 31)];
-            } else {
-                constexpr int CPP = 32 / W;          // copies per plane
-                acc = 0;
+        for (int k = tid; k < nb * PW; k += HIST_THREADS) {
+            const int b = k / PW, f = k % PW;
+            uint64_t acc = 0;
+            if (f < W) {
+                if (f >= wreal) continue;
+                if constexpr (W == 64) {
+                    acc = hist_lds[(f >> 5) * 8192 + b * 32 + (f & 31)];
+                } else if constexpr (W == 32) {
+                    acc = hist_lds[b * 32 + f];
+                } else {
+                    constexpr int CPP = 32 / W;      // copies per plane
 #pragma unroll
-                for (int c = 0; c < 64 / W; ++c)
-                    acc += hist_lds[(c / CPP) * 8192 + b * 32 + (c % CPP) * W + f];
+                    for (int c = 0; c < 64 / W; ++c)
+                        acc += hist_lds[(c / CPP) * 8192 + b * 32 + (c % CPP) * W + f];
+                }
+            } else {
+                const int e = f - W;                 // extra e: plane 1, columns q with q % ne == e
+                if (e >= ne) continue;
+                for (int q = e; q < 32; q += ne) acc += hist_lds[8192 + b * 32 + q];
             }
             __builtin_nontemporal_store(acc, &out[k]);   // read once, by k_reduce
         }
@@ -1600,16 +1663,31 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 
 HistLayout gather_layout(const Shape &sh) {
     const int32_t row = sh.num_tiles * sh.tile_w;
-    return HistLayout{(int64_t)sh.tile_w, row, row, sh.num_tiles - 1};
+    return HistLayout{(int64_t)sh.tile_w, row, row, sh.num_tiles - 1, row,
+                      (int64_t)sh.hist_tiles * sh.tile_w};
+}
+
+// Bytes of the extras plane per row: the extras rounded up to a dword.
+static int32_t extras_pitch(const Shape &sh) { return (sh.extras + 3) / 4 * 4; }
+
+bool has_planar_layout(const Shape &sh) {
+    if (sh.tile_w == 32) return sh.extras > 0;
+    if (sh.tile_w != 64 || sh.num_tiles < 2) return false;
+    const int32_t last_feats = sh.cols - (sh.num_tiles - 1) * 64;
+    return (last_feats + 15) / 16 * 16 < 64;         // else the copy saves nothing
 }
 
 HistLayout planar_layout(const Shape &sh) {
+    if (sh.tile_w == 32)
+        return HistLayout{sh.rows * 32, 32, 32, sh.num_tiles - 1, extras_pitch(sh),
+                          (int64_t)sh.hist_tiles * sh.rows * 32};
     const int32_t last_feats = sh.cols - (sh.num_tiles - 1) * 64;
-    return HistLayout{sh.rows * 64, 64, (last_feats + 15) / 16 * 16, sh.num_tiles - 1};
+    return HistLayout{sh.rows * 64, 64, (last_feats + 15) / 16 * 16, sh.num_tiles - 1, 0, 0};
 }
 
 size_t planar_bytes(const Shape &sh) {
     const HistLayout l = planar_layout(sh);
+    if (sh.tile_w == 32) return (size_t)l.x_off + (size_t)sh.rows * (size_t)l.x_stride + 64;
     return (size_t)l.last_tile * (size_t)l.tile_step + (size_t)sh.rows * (size_t)l.last_stride + 64;
 }
 
@@ -1618,12 +1696,15 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
                        const HistLayout *layout, hipEvent_t start, hipEvent_t stop,
                        bool implicit_rows) {
     const HistLayout lay = layout ? *layout : gather_layout(sh);
+    if (sh.hist_tiles < 1 || sh.part_w < sh.tile_w ||
+        (sh.extras > 0 && (sh.tile_w != 32 || sh.hist_tiles != sh.num_tiles - 1)))
+        return hipErrorInvalidValue;
     if (layout) {
-        // the planar copy: 64-wide tiles, every stride a 16-B multiple
+        // the planar copy, exactly as planar_layout lays it out
         const HistLayout p = planar_layout(sh);
-        if (sh.tile_w != 64 || sh.num_tiles < 2 || lay.tile_step != p.tile_step ||
-            lay.stride != p.stride || lay.last_stride != p.last_stride ||
-            lay.last_tile != p.last_tile)
+        if (!has_planar_layout(sh) || lay.tile_step != p.tile_step || lay.stride != p.stride ||
+            lay.last_stride != p.last_stride || lay.last_tile != p.last_tile ||
+            lay.x_stride != p.x_stride || lay.x_off != p.x_off)
             return hipErrorInvalidValue;
     }
     switch (sh.tile_w) {
@@ -1633,20 +1714,21 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
         auto *kern = &KERN;                                                                      \
         if (start || stop)                                                                       \
             hipExtLaunchKernelGGL(kern, dim3(grid), dim3(HIST_THREADS), 0, s, start, stop, 0,    \
-                                  tiled, order, items, ctl, partials, lay, sh.num_bins, sh.cols); \
+                                  tiled, order, items, ctl, partials, lay, sh);                  \
         else                                                                                     \
             hipLaunchKernelGGL(kern, dim3(grid), dim3(HIST_THREADS), 0, s, tiled, order, items,  \
-                               ctl, partials, lay, sh.num_bins, sh.cols);                        \
+                               ctl, partials, lay, sh);                                          \
     }
-#define MBK_HIST_CASE(WW)                                                                        \
-    case WW:                                                                                     \
-        if (implicit_rows) MBK_HIST_LAUNCH(k_hist<WW MBK_COMMA true>)                           \
-        else MBK_HIST_LAUNCH(k_hist<WW MBK_COMMA false>)                                         \
+#define MBK_HIST_CASE(WW, LL)                                                                    \
+        if (implicit_rows) MBK_HIST_LAUNCH(k_hist<WW MBK_COMMA LL MBK_COMMA true>)              \
+        else MBK_HIST_LAUNCH(k_hist<WW MBK_COMMA LL MBK_COMMA false>)                            \
         break;
-        MBK_HIST_CASE(8)
-        MBK_HIST_CASE(16)
-        MBK_HIST_CASE(32)
-        MBK_HIST_CASE(64)
+    case 8: MBK_HIST_CASE(8, 1)
+    case 16: MBK_HIST_CASE(16, 1)
+    case 32: MBK_HIST_CASE(32, 1)
+    case 64:
+        if (layout) { MBK_HIST_CASE(64, 2) }         // planar rows: contiguous, two lanes per row
+        else { MBK_HIST_CASE(64, 4) }                // gathered rows: one load per row and tile
 #undef MBK_HIST_CASE
 #undef MBK_HIST_LAUNCH
 #undef MBK_COMMA
@@ -1676,10 +1758,44 @@ __global__ __launch_bounds__(256) void k_planar_rows(const uint8_t *__restrict__
         *reinterpret_cast<const uint4 *>(tiled + r * row_bytes + (int64_t)j * 16);
 }
 
-hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled, uint8_t *out) {
-    if (sh.tile_w != 64 || sh.num_tiles < 2) return hipErrorInvalidValue;
+// The 32-wide form with extras: item j < 2 (T - 1) of row r copies 16-B chunk
+// j to tile j / 2's plane, item 2 (T - 1) copies the row's extra bytes (from
+// the last tile, in dwords) to the extras plane.
+__global__ __launch_bounds__(256) void k_planar_rows32(const uint8_t *__restrict__ tiled,
+                                                       int64_t rows, int32_t row_bytes,
+                                                       int32_t main_tiles, HistLayout lay,
+                                                       uint8_t *__restrict__ out) {
+    const int32_t per_row = 2 * main_tiles + 1;
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= rows * per_row) return;
+    const int64_t r = k / per_row;
+    const int32_t j = (int32_t)(k - r * per_row);
+    const uint8_t *src = tiled + r * row_bytes;
+    if (j < 2 * main_tiles) {
+        *reinterpret_cast<uint4 *>(out + (int64_t)(j >> 1) * lay.tile_step + r * 32 + (j & 1) * 16) =
+            *reinterpret_cast<const uint4 *>(src + (int64_t)j * 16);
+        return;
+    }
+    const uint32_t *xs = reinterpret_cast<const uint32_t *>(src + (int64_t)main_tiles * 32);
+    uint32_t *xd = reinterpret_cast<uint32_t *>(out + lay.x_off + r * lay.x_stride);
+    for (int32_t w = 0; w < lay.x_stride / 4; ++w) xd[w] = xs[w];
+}
+
+hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled,
+                              int32_t row_bytes, uint8_t *out) {
+    if (!has_planar_layout(sh)) return hipErrorInvalidValue;
     const HistLayout lay = planar_layout(sh);
-    const int32_t row_bytes = sh.num_tiles * sh.tile_w;
+    // the source rows must hold every byte a copy reads (feature f at byte f)
+    const int32_t need = sh.tile_w == 32 ? sh.hist_tiles * 32 + lay.x_stride
+                                         : sh.num_tiles * sh.tile_w;
+    if (row_bytes < need || row_bytes % 16 != 0) return hipErrorInvalidValue;
+    if (sh.tile_w == 32) {
+        const int64_t n = sh.rows * (2 * sh.hist_tiles + 1);
+        if (n <= 0) return hipSuccess;
+        hipLaunchKernelGGL(k_planar_rows32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           tiled, sh.rows, row_bytes, sh.hist_tiles, lay, out);
+        return hipGetLastError();
+    }
     const int64_t n = sh.rows * (4 * lay.last_tile + lay.last_stride / 16);
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_planar_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, tiled,
@@ -1704,18 +1820,20 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
                                                 uint32_t blocks_per_tile, int derive) {
     constexpr int CELLS = 256 / S;
     __shared__ int64_t red[S > 1 ? S : 1][CELLS][2];
-    const int W = sh.tile_w, nb = sh.num_bins, F = sh.cols, T = sh.num_tiles;
+    const int PW = sh.part_w, nb = sh.num_bins, F = sh.cols, T = sh.hist_tiles;
     const uint32_t bpt = blockIdx.x % blocks_per_tile;
     const uint32_t rest = blockIdx.x / blocks_per_tile;
     const int tile = (int)(rest % (uint32_t)T);
     const uint32_t pair_idx = rest / (uint32_t)T;
     if (pair_idx >= ctl->num_pairs) return;          // uniform per block
     const int kk = threadIdx.x % CELLS, slice = threadIdx.x / CELLS;
-    const int k = (int)bpt * CELLS + kk;             // (bin, feature) index in the tile
+    const int k = (int)bpt * CELLS + kk;             // (bin, column) index in the item partial
     const Pair pr = pairs[pair_idx];
+    // the column's feature (main or extra), -1 for padding: those hold no partials
+    const int f = k < nb * PW ? partial_feature(sh, tile, k % PW) : -1;
     int64_t g = 0, h = 0;
-    if (k < nb * W && tile * W + k % W < F) {         // padding columns hold no partials
-        const size_t stride = (size_t)(nb * W);
+    if (f >= 0) {
+        const size_t stride = (size_t)(nb * PW);
         const size_t cstride = (size_t)T * stride;   // between chunks of one (pair, tile)
         const uint64_t *src = partials + ((size_t)pr.item_first + (size_t)tile) * stride + k;
         constexpr uint64_t HMASK = (1ull << HIST_QH_BITS) - 1;
@@ -1747,9 +1865,8 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
         if (slice != 0) return;
         for (int s2 = 1; s2 < S; ++s2) { g += red[s2][kk][0]; h += red[s2][kk][1]; }
     }
-    if (k >= nb * W) return;
-    const int b = k / W, fl = k % W, f = tile * W + fl;
-    if (f >= F) return;
+    if (f < 0) return;
+    const int b = k / PW;
     int64_t *hb = hist_cur + (((size_t)pr.built * nb + b) * F + f) * 2;
     hb[0] = g;
     hb[1] = h;
@@ -1764,15 +1881,15 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
 hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
                          const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
                          const TreeCtl *ctl, bool derive) {
-    const uint32_t cells = (uint32_t)(sh.num_bins * sh.tile_w);
+    const uint32_t cells = (uint32_t)(sh.num_bins * sh.part_w);
     const int dv = derive ? 1 : 0;
     if (max_pairs >= 32) {                           // measured: S = 4 is faster below
         const uint32_t bpt = (cells + 255) / 256;
-        hipLaunchKernelGGL(k_reduce<1>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
+        hipLaunchKernelGGL(k_reduce<1>, dim3(max_pairs * (uint32_t)sh.hist_tiles * bpt), dim3(256),
                            0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
     } else {
         const uint32_t bpt = (cells + 63) / 64;
-        hipLaunchKernelGGL(k_reduce<4>, dim3(max_pairs * (uint32_t)sh.num_tiles * bpt), dim3(256),
+        hipLaunchKernelGGL(k_reduce<4>, dim3(max_pairs * (uint32_t)sh.hist_tiles * bpt), dim3(256),
                            0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
     }
     return hipGetLastError();
@@ -2339,7 +2456,7 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
     __syncthreads();
     if (tid == 0) {
         const uint64_t total = s_total;
-        const uint32_t c = item_chunk(total, num_pairs, sh.num_tiles, target_items, min_chunk);
+        const uint32_t c = item_chunk(total, num_pairs, sh.hist_tiles, target_items, min_chunk);
         s_chunk = c;
         ctl->chunk = c;
         if (accumulate) ctl->level_built[level] += (uint32_t)total;
@@ -2355,8 +2472,8 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         // rows into equal chunks of at most c'.
         // (32-bit arithmetic: 64-bit divisions in the loop cost microseconds)
         const uint32_t n = (uint32_t)tid < num_pairs ? s_cnt[tid] : 0u;
-        const uint32_t K = (uint32_t)(item_budget(s_total, num_pairs, sh.num_tiles,
-                                                  target_items) / (uint64_t)sh.num_tiles);
+        const uint32_t K = (uint32_t)(item_budget(s_total, num_pairs, sh.hist_tiles,
+                                                  target_items) / (uint64_t)sh.hist_tiles);
         uint32_t hi = s_chunk;
         uint32_t lo = s_total / K + (s_total % K != 0u);
         if (lo < min_chunk) lo = min_chunk;
@@ -2380,7 +2497,7 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
         const uint32_t pc = pair_chunk(s_cnt[k]);
         const uint32_t nch = (s_cnt[k] + pc - 1) / pc;
         pairs[k].nchunks = nch;
-        s_first[k] = nch * (uint32_t)sh.num_tiles;
+        s_first[k] = nch * (uint32_t)sh.hist_tiles;
     }
     __syncthreads();
     const uint32_t total_items = block_exclusive_scan(s_first, num_pairs, wave_tot);
@@ -2407,7 +2524,7 @@ __device__ void write_items(const Shape &sh, TreeCtl *ctl, int level, Pair *pair
             if (s_first[mid] <= it) lo = mid; else hi = mid - 1;
         }
         const uint32_t rel = it - s_first[lo];
-        const uint32_t t = rel % (uint32_t)sh.num_tiles, c = rel / (uint32_t)sh.num_tiles;
+        const uint32_t t = rel % (uint32_t)sh.hist_tiles, c = rel / (uint32_t)sh.hist_tiles;
         const uint32_t pc = pair_chunk(s_cnt[lo]);
         HistItem h;
         h.pair = lo;
@@ -3336,9 +3453,9 @@ __device__ void lw_plan_block(const Shape &sh, const LWArgs &a, const LWPick &q,
     const bool small_left = left <= right;
     const uint32_t seg_s = small_left ? q.dst : q.dst + left;
     const uint32_t cnt_s = small_left ? left : right;
-    const uint32_t T = (uint32_t)sh.num_tiles;
+    const uint32_t T = (uint32_t)sh.hist_tiles;
     const uint32_t chunk =
-        can_eval ? item_chunk(cnt_s, 1, sh.num_tiles, a.target_items, a.min_chunk) : 1u;
+        can_eval ? item_chunk(cnt_s, 1, sh.hist_tiles, a.target_items, a.min_chunk) : 1u;
     const uint32_t nch = can_eval ? (cnt_s + chunk - 1) / chunk : 0u;
     const uint32_t n_items = nch * T;
     const bool fits = n_items <= sh.item_cap;

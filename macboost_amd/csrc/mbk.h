@@ -100,7 +100,8 @@ struct Pair {
 };
 constexpr uint32_t NONE = 0xFFFFFFFFu;
 
-// Global per-fit constants.
+// Global per-fit constants.  The histogram's own tiling (hist_tiles,
+// extras, part_w) is derived from the layout's by set_hist_tiling.
 struct Shape {
     int64_t rows;        // N
     int32_t cols;        // F
@@ -108,8 +109,50 @@ struct Shape {
     int32_t tile_w;      // W, features per row tile of the gather layout
     int32_t num_tiles;   // T = ceil(F / W)
     uint32_t item_cap;   // capacity of the histogram item list and its partials
-    uint32_t pad;
+    int32_t hist_tiles;  // histogram items per row chunk: T, or T - 1 with extras
+    int32_t extras;      // features of the last layout tile folded into the others (0: none)
+    int32_t part_w;      // columns of one item's partial: W, or W + 1 / W + 2 with extras
 };
+
+// Histogram tiling.  A 32-wide tile costs one ds_add_u64 per 64 rows and
+// feature (one row per lane), so the LDS work of a row is its tile count x 32.
+// When the last layout tile holds few features (R <= 2 (T - 1), e.g. 4 of 32
+// at F = 100), they are not given an item of their own: main tile t also adds
+// E_t of them (E_t in {0, 1, 2}; the first max(0, R - (T-1)) tiles take 2),
+// which at F = 100 is 34 + 33 + 33 adds per 64 rows instead of 4 x 32.
+__host__ __device__ inline int32_t tile_extra_count(const Shape &sh, int32_t t) {
+    if (sh.extras == 0) return 0;
+    const int32_t e2 = sh.extras > sh.hist_tiles ? sh.extras - sh.hist_tiles : 0;
+    return t < e2 ? 2 : (t < sh.extras - e2 ? 1 : 0);
+}
+// First extra feature of tile t, relative to the last layout tile's first
+// feature (hist_tiles * W): tiles with two extras take even offsets.
+__host__ __device__ inline int32_t tile_extra_first(const Shape &sh, int32_t t) {
+    const int32_t e2 = sh.extras > sh.hist_tiles ? sh.extras - sh.hist_tiles : 0;
+    return t + (t < e2 ? t : e2);
+}
+// The feature that column c of tile t's partial holds, or -1 (padding).
+__host__ __device__ inline int32_t partial_feature(const Shape &sh, int32_t t, int32_t c) {
+    if (c < sh.tile_w) {
+        const int32_t f = t * sh.tile_w + c;
+        return f < sh.cols ? f : -1;
+    }
+    const int32_t e = c - sh.tile_w;
+    return e < tile_extra_count(sh, t)
+        ? sh.hist_tiles * sh.tile_w + tile_extra_first(sh, t) + e : -1;
+}
+inline void set_hist_tiling(Shape &sh) {
+    const int32_t last = sh.cols - (sh.num_tiles - 1) * sh.tile_w;   // features of the last tile
+    if (sh.tile_w == 32 && sh.num_tiles >= 2 && last <= 2 * (sh.num_tiles - 1)) {
+        sh.hist_tiles = sh.num_tiles - 1;
+        sh.extras = last;
+        sh.part_w = sh.tile_w + (last > sh.hist_tiles ? 2 : 1);
+    } else {
+        sh.hist_tiles = sh.num_tiles;
+        sh.extras = 0;
+        sh.part_w = sh.tile_w;
+    }
+}
 
 struct SplitParams {
     float lambda;
@@ -293,23 +336,31 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
                            const RootPlan *plan = nullptr, const PendingFixup *fix = nullptr);
 
 // Where the histogram kernel finds tile t of row r: at
-// base + t * tile_step + r * (t == last_tile ? last_stride : stride).
+// base + t * tile_step + r * (t == last_tile ? last_stride : stride); with
+// extras, the dword holding row r's extra bytes f0..f0+3 (f0 a multiple of 4)
+// at base + x_off + r * x_stride + f0.
 struct HistLayout {
     int64_t tile_step;
     int32_t stride;
     int32_t last_stride;
     int32_t last_tile;
+    int32_t x_stride;
+    int64_t x_off;
 };
-// The gather layout [rows][T][W]: tile_step W, both strides T * W.
+// The gather layout [rows][T][W]: tile_step W, both strides T * W; the
+// extras are the last tile's bytes of the row.
 HistLayout gather_layout(const Shape &sh);
-// The planar root copy [T][rows][...] (launch_planar_rows): tile t < T - 1 at
-// t * rows * 64 with stride 64, the last tile with stride ceil(F_last/16)*16.
-// Each tile's bytes are then contiguous, so the two tile workgroups of a row
-// chunk stream their own planes.  Only for W = 64 and T >= 2.
+// The planar root copy (launch_planar_rows).  W = 64, T >= 2: [T][rows][...],
+// tile t < T - 1 at t * rows * 64 with stride 64, the last tile with stride
+// ceil(F_last/16)*16.  W = 32 with extras: [T-1][rows][32] plus one plane of
+// each row's extra bytes, padded to a multiple of 4.  Each tile's bytes are
+// then contiguous, so the tile workgroups of a row chunk stream their own
+// planes.
+bool has_planar_layout(const Shape &sh);
 HistLayout planar_layout(const Shape &sh);
 size_t planar_bytes(const Shape &sh);    // including 64 zero bytes of overread
 
-// Histogram items -> packed partials [item][B][W] (64-bit words, see
+// Histogram items -> packed partials [item][B][part_w] (64-bit words, see
 // HIST_QH_BITS).  layout null: the gather layout.  With start / stop events
 // (created by the caller), they take the kernel's own dispatch timestamps.
 // implicit_rows: order holds launch_quantize's implicit u32 words (the root
@@ -324,7 +375,10 @@ size_t hist_lds_size();   // static LDS of one histogram workgroup
 // holds planar_bytes(sh) bytes (the last tile's loads run up to 16 B past its
 // rows into the zeroed tail, and into the next row's bytes, which land in
 // padding columns).
-hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled, uint8_t *out);
+// tiled: rows of row_bytes bytes holding feature f at byte f (the gather
+// layout of any tile width: its tiles are contiguous and all but the last full).
+hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *tiled,
+                              int32_t row_bytes, uint8_t *out);
 
 // Reduce partials into hist_cur [node][B][F][g,h] (int64), derive siblings
 // from hist_prev, then search splits for both nodes of each pair.

@@ -98,10 +98,13 @@ extern "C" int mbk_node_hist_split_noalloc(mbk_context *ctx, const uint8_t *bins
         if (n < 0 || n > 0xFFFFFFF0LL) mb::invalid("row count out of range");
         if (rows < 0 || !bins_tiled || !entries || !max_gh || !hist_out || !results)
             mb::invalid("null or empty argument");
-        const int32_t T = (cols + tile_width - 1) / tile_width;
+        mbk::Shape sh{std::max<int64_t>(rows, n), cols, num_bins, tile_width,
+                      (cols + tile_width - 1) / tile_width, 0u, 0, 0, 0};
+        mbk::set_hist_tiling(sh);
+        const int32_t T = sh.hist_tiles;             // histogram items per row chunk
         // items of the node: the planner's budget for it, an upper bound on
         // what it plans, must fit both the item list and the partial histograms
-        const size_t per_item = (size_t)tile_width * (size_t)num_bins * sizeof(uint64_t);
+        const size_t per_item = (size_t)sh.part_w * (size_t)num_bins * sizeof(uint64_t);
         const size_t cap = std::min(MAX_ITEMS, (SCRATCH_BYTES - OFF_PARTIALS) / per_item);
         const uint32_t target = (uint32_t)std::min<size_t>(256, cap / 2 > 0 ? cap / 2 : 1);
         const uint32_t min_chunk = 2048;
@@ -127,8 +130,7 @@ extern "C" int mbk_node_hist_split_noalloc(mbk_context *ctx, const uint8_t *bins
         const auto *no_cat = reinterpret_cast<const uint8_t *>(base + OFF_NO_CAT);
         const auto *no_mono = reinterpret_cast<const int8_t *>(base + OFF_NO_MONO);
         const auto *all_feats = reinterpret_cast<const uint8_t *>(base + OFF_ALL_FEATS);
-        const mbk::Shape sh{std::max<int64_t>(rows, n), cols, num_bins, tile_width, T,
-                            (uint32_t)cap, 0u};
+        sh.item_cap = (uint32_t)cap;
         const mbk::SplitParams sp{lambda, min_child_hess, 0.0f, cat_smooth, 0.1f, 1};
         hipLaunchKernelGGL(k_noalloc_setup, dim3(1), dim3(256), 0, s, base, max_gh, cols);
         MB_HIP(hipGetLastError());

@@ -119,7 +119,9 @@ void reserve_tree(mbk_context *ctx, const mbk_tree_shape &shape) {
     TreeScratch &t = ctx->scratch.tree;
     const int64_t rows = shape.rows;
     const int32_t cols = shape.cols, nb = shape.num_bins, W = shape.tile_width, D = shape.max_depth;
-    const int32_t T = (cols + W - 1) / W;
+    mbk::Shape sh{rows, cols, nb, W, (cols + W - 1) / W, 0u, 0, 0, 0};
+    mbk::set_hist_tiling(sh);
+    const int32_t T = sh.hist_tiles;                 // histogram items per row chunk
     const int64_t level_nodes = (int64_t)1 << (D - 1), total_nodes = ((int64_t)1 << (D + 1)) - 1;
     const size_t lds = mbk::hist_lds_size();
     const int wg_per_cu = (int)std::min<size_t>(2, std::max<size_t>(1, (160 * 1024) / lds));
@@ -141,10 +143,11 @@ void reserve_tree(mbk_context *ctx, const mbk_tree_shape &shape) {
     reserve(t.cursors, (size_t)level_nodes * mbk::CURSOR_STRIDE);
     reserve(t.pairs, (size_t)level_nodes);
     reserve(t.items, (size_t)items);
-    reserve(t.partials, (size_t)items * (size_t)W * (size_t)nb);
+    reserve(t.partials, (size_t)items * (size_t)sh.part_w * (size_t)nb);
     reserve(t.cover1, 1);
     ensure_defaults(ctx, cols);
-    t.sh = mbk::Shape{rows, cols, nb, W, T, (uint32_t)items, 0u};
+    sh.item_cap = (uint32_t)items;
+    t.sh = sh;
     t.D = D;
 }
 

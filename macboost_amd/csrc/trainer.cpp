@@ -468,6 +468,7 @@ struct Trainer {
     std::vector<std::string> feature_names;
     std::unique_ptr<Device> dev;
     mbk::Shape sh{};
+    mbk::Shape sh_root{};          // the unsampled root's histogram shape (its planar copy)
     mbk::SplitParams sp{};
     mbk::GradParams gp{};
     int D = 6, total_nodes = 0, max_level_nodes = 1;
@@ -992,9 +993,12 @@ static void setup_shape(Trainer &t, int64_t rows, int64_t cols) {
     if (p.has_allowed)
         for (int64_t f = 0; f < cols; ++f) t.mask_base[(size_t)f] = p.allowed.count((int)f) ? 1 : 0;
 
-    // gather-layout tile width: features per row tile
-    // 64 features per tile fills a wavefront (one lane per feature); narrower
-    // matrices use the smallest tile that holds all features.
+    // gather-layout tile width: features per row tile.  64 features per tile
+    // for wide matrices (four lanes per gathered row, so one load covers a
+    // row's tile); narrower matrices use the smallest tile that holds all
+    // features.  (32-wide tiles with the last tile folded in cost fewer LDS adds
+    // but three L2 requests per row and item: slower on the gathered levels,
+    // faster on the streamed root, which uses them; see root_shape.)
     int tile_w = cols > 32 ? 64 : cols > 16 ? 32 : cols > 8 ? 16 : 8;
     if (const char *e = std::getenv("MACBOOST_TILE_W")) tile_w = std::atoi(e);
     if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) tile_w = 64;
@@ -1003,6 +1007,8 @@ static void setup_shape(Trainer &t, int64_t rows, int64_t cols) {
     t.sh.num_bins = p.num_bins;
     t.sh.tile_w = tile_w;
     t.sh.num_tiles = (int)((cols + tile_w - 1) / tile_w);
+    mbk::set_hist_tiling(t.sh);
+    t.sh_root = t.sh;
     t.sp.lambda = p.lambda;
     t.sp.min_child_hess = p.min_child_hess;
     t.sp.min_split_gain = p.min_split_gain;
@@ -1044,24 +1050,40 @@ static void bin_valid(Trainer &t, const float *xv, int64_t vrows, const float *e
 }
 
 // Labels, weights, predictions and the tree-build buffers.
-// The root histogram streams every row.  With 64-wide tiles the gather layout
-// holds T * 64 B per row although the features fill only ceil(F/16)*16 of
-// them (112 of 128 at F = 100), and the two tile workgroups of a row chunk
-// read halves of the same lines.  The planar copy stores each tile's bytes
-// contiguously at that width, so each workgroup streams its own plane.
+// The root histogram streams every row.  The gather layout holds T * W B per
+// row although the features fill fewer (100 of 128 at F = 100), and the tile
+// workgroups of a row chunk read parts of the same lines.  The planar copy
+// stores each tile's bytes contiguously (64-wide tiles: the last one at
+// ceil(F_last/16)*16 B; 32-wide tiles with extras: the extras in a plane of
+// their own), so each workgroup streams its own plane.
+// The root's histogram shape: over the planar copy, 32-wide tiles with the
+// last tile's features folded in when that applies (F = 100: 34 + 33 + 33 LDS
+// adds per 64 rows instead of 128; 223 against 244 us for the 10M-row root),
+// else the gather shape.  The copy reads feature f at byte f of a gather row,
+// which holds for every tile width.
+static mbk::Shape root_shape(const Trainer &t) {
+    mbk::Shape r = t.sh;
+    r.tile_w = 32;
+    r.num_tiles = (t.sh.cols + 31) / 32;
+    mbk::set_hist_tiling(r);
+    const int32_t row_bytes = t.sh.num_tiles * t.sh.tile_w;
+    if (r.extras > 0 && r.hist_tiles * 32 + (r.extras + 3) / 4 * 4 <= row_bytes) return r;
+    return t.sh;
+}
+
 static void build_root_copy(Trainer &t) {
     t.has_root_copy = false;
-    if (t.sh.tile_w != 64 || t.sh.num_tiles < 2) return;
-    const mbk::HistLayout lay = mbk::planar_layout(t.sh);
-    if (lay.last_stride >= 64) return;
+    if (!mbk::has_planar_layout(t.sh_root)) return;
+    const mbk::HistLayout lay = mbk::planar_layout(t.sh_root);
     hipStream_t s = t.dev->stream;
-    const size_t bytes = mbk::planar_bytes(t.sh);
+    const size_t bytes = mbk::planar_bytes(t.sh_root);
     // an optimisation only: skipped unless it leaves 1/16 of the device free
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) != hipSuccess || free_b < bytes + (total_b >> 4)) return;
     t.bins_root.alloc(bytes);
     MB_HIP(hipMemsetAsync(t.bins_root.ptr + bytes - 64, 0, 64, s));
-    MB_HIP(mbk::launch_planar_rows(s, t.sh, t.bins_tiled.ptr, t.bins_root.ptr));
+    MB_HIP(mbk::launch_planar_rows(s, t.sh_root, t.bins_tiled.ptr,
+                                   t.sh.num_tiles * t.sh.tile_w, t.bins_root.ptr));
     t.root_layout = lay;
     t.has_root_copy = true;
 }
@@ -1089,7 +1111,6 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     const Params &p = t.p;
     hipStream_t s = t.dev->stream;
     const int64_t rows = t.rows, cols = t.cols, vrows = t.vrows;
-    const int tile_w = t.sh.tile_w;
     t.gp.has_weights = w ? 1 : 0;
     // --- persistent buffers ---------------------------------------------
     t.K = p.objective == OBJ_MULTICLASS ? p.num_classes : 1;
@@ -1185,16 +1206,20 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.hist_grid = t.dev->num_cus * wg_per_cu;
     t.target_items = t.hist_grid;
     t.min_chunk = 2048;
-    const int64_t T = t.sh.num_tiles;
     // a level's items: T*ceil(count/chunk) summed over its built nodes, at most
     // target*rounds + T*nodes, where target*rounds <= T*rows/HIST_CHUNK_MAX + target
-    int64_t max_items = T * ((rows + mbk::HIST_CHUNK_MAX - 1) / mbk::HIST_CHUNK_MAX) +
-                        t.target_items + 1 + T * (int64_t)t.max_level_nodes;
-    max_items = std::min<int64_t>(max_items, T * ((rows + t.min_chunk - 1) / t.min_chunk +
-                                                  t.max_level_nodes + 1));
-    t.sh.item_cap = (uint32_t)max_items;
-    t.partials.alloc((size_t)max_items * (size_t)tile_w * (size_t)p.num_bins);
-    t.items.alloc((size_t)max_items);
+    auto max_items_of = [&](int64_t T, int64_t nodes) {
+        const int64_t m = T * ((rows + mbk::HIST_CHUNK_MAX - 1) / mbk::HIST_CHUNK_MAX) +
+                          t.target_items + 1 + T * nodes;
+        return std::min<int64_t>(m, T * ((rows + t.min_chunk - 1) / t.min_chunk + nodes + 1));
+    };
+    t.sh_root = root_shape(t);
+    t.sh.item_cap = (uint32_t)max_items_of(t.sh.hist_tiles, t.max_level_nodes);
+    t.sh_root.item_cap = (uint32_t)max_items_of(t.sh_root.hist_tiles, t.max_level_nodes);
+    t.partials.alloc(std::max((size_t)t.sh.item_cap * (size_t)t.sh.part_w,
+                              (size_t)t.sh_root.item_cap * (size_t)t.sh_root.part_w) *
+                     (size_t)p.num_bins);
+    t.items.alloc((size_t)std::max(t.sh.item_cap, t.sh_root.item_cap));
     t.pairs.alloc((size_t)t.max_level_nodes);
     // Leaf-wise trees up to depth LWB_MAX_DEPTH grow in depth rounds on the
     // level-wise buffers, unless two levels of histograms would pass 4 GiB
@@ -1695,7 +1720,7 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     const bool sampled = tree_sampled(t.p, tree);
     mbk::RootPlan rp{};
     if (root_cover) {
-        rp.sh = t.sh;
+        rp.sh = sampled || !t.has_root_copy ? t.sh : t.sh_root;
         rp.rows_active = sampled ? mbk::NONE : (uint32_t)t.rows;
         rp.target_items = (uint32_t)t.target_items;
         rp.min_chunk = (uint32_t)t.min_chunk;
@@ -1796,16 +1821,18 @@ static void grow_levelwise(Trainer &t, int tree) {
         }
         // an unsampled root streams every row: the planar copy when there is one
         const bool planar = level == 0 && !sampled && t.has_root_copy;
-        MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
+        MB_HIP(mbk::launch_hist(s, planar ? t.sh_root : sh,
+                                planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
                                 planar ? &t.root_layout : nullptr, e0, e1,
                                 level == 0 && !sampled));
         if (e0) t.events.push_back({e0, e1, level});
     };
+    const mbk::Shape &sh0 = !sampled && t.has_root_copy ? t.sh_root : sh;   // the root's
 
     // level 0
     hist(ord_cur, 0);
-    MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
+    MB_HIP(mbk::launch_split(s, sh0, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
                              t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
                              t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
     mbk::LevelArgs l0{0, 0, 1, 0};
@@ -1891,7 +1918,8 @@ static void grow_leafwise(Trainer &t, int tree) {
     mbk::TreeCtl *ctl = t.ctl.ptr;
     mbk::Entry *order = t.order_a.ptr;
     const bool sampled = tree_entries(t, tree, ctl, order);
-    MB_HIP(mbk::launch_lw_init(s, sh, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
+    const mbk::Shape &sh0 = !sampled && t.has_root_copy ? t.sh_root : sh;   // the root's
+    MB_HIP(mbk::launch_lw_init(s, sh0, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
                                t.count.ptr, t.pairs.ptr, t.items.ptr, out,
                                sampled));
     auto build = [&](int step) {
@@ -1901,11 +1929,12 @@ static void grow_leafwise(Trainer &t, int tree) {
             e1 = acquire_event();
         }
         const bool planar = step == 0 && !sampled && t.has_root_copy;
-        MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, order,
+        const mbk::Shape &shs = planar ? sh0 : sh;
+        MB_HIP(mbk::launch_hist(s, shs, planar ? t.bins_root.ptr : t.bins_tiled.ptr, order,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
                                 planar ? &t.root_layout : nullptr, e0, e1));
         if (e0) t.events.push_back({e0, e1, std::min(step, 15)});
-        MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, t.hist_a.ptr,
+        MB_HIP(mbk::launch_split(s, shs, t.sp, t.pairs.ptr, 1, t.partials.ptr, t.hist_a.ptr,
                                  t.hist_a.ptr, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
                                  t.count.ptr, t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
     };
@@ -1992,11 +2021,13 @@ static void grow_leafwise_rounds(Trainer &t, int tree) {
             e1 = acquire_event();
         }
         const bool planar = level == 0 && !sampled && t.has_root_copy;
-        MB_HIP(mbk::launch_hist(s, sh, planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
+        MB_HIP(mbk::launch_hist(s, planar ? t.sh_root : sh,
+                                planar ? t.bins_root.ptr : t.bins_tiled.ptr, ord,
                                 t.items.ptr, ctl, t.partials.ptr, t.hist_grid,
                                 planar ? &t.root_layout : nullptr, e0, e1));
         if (e0) t.events.push_back({e0, e1, level});
     };
+    const mbk::Shape &sh0 = !sampled && t.has_root_copy ? t.sh_root : sh;   // the root's
     // unsampled trees without renewal: the training walk counts the deepest
     // rows, so the last round partitions nothing
     mbk::LWBArgs la = t.lwb;
@@ -2008,7 +2039,7 @@ static void grow_leafwise_rounds(Trainer &t, int tree) {
                                       out));
     };
     hist(ord_cur, 0);
-    MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
+    MB_HIP(mbk::launch_split(s, sh0, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
                              t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
                              t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
     for (int r = 0; r < t.D; ++r) {

@@ -202,11 +202,16 @@ def test_quantize_matches_oracle(ctx, objective, offset):
     assert np.array_equal(ent[:, 1], want)
 
 
-@pytest.mark.parametrize("tile_w,nb,n", [(8, 256, 70_000), (32, 64, 150_001), (64, 256, 2500),
-                                         (16, 17, 9000)])
-def test_node_hist_and_splits_match_oracle(ctx, tile_w, nb, n):
-    rng = np.random.default_rng(tile_w + nb)
-    rows, cols = 200_000, 45
+# 32-wide tiles whose last tile holds few features fold them into the other
+# tiles' items (Shape::extras): 34 columns = one item with 2 extras, 65 = (1, 0),
+# 99 = (1, 1, 1), 100 = (2, 1, 1); 45 keeps a tile of its own.
+@pytest.mark.parametrize("tile_w,nb,n,cols", [(8, 256, 70_000, 45), (32, 64, 150_001, 45),
+                                              (64, 256, 2500, 45), (16, 17, 9000, 45),
+                                              (32, 256, 150_001, 100), (32, 64, 70_000, 34),
+                                              (32, 256, 20_000, 65), (32, 17, 5000, 99)])
+def test_node_hist_and_splits_match_oracle(ctx, tile_w, nb, n, cols):
+    rng = np.random.default_rng(tile_w + nb + cols)
+    rows = 200_000
     bins = rng.integers(0, nb, size=(cols, rows)).astype(np.uint8)
     bins[3, rng.random(rows) < 0.3] = nb - 1              # missing values
     bins[4] = rng.integers(0, 5, size=rows)               # low-cardinality categorical
@@ -347,7 +352,7 @@ def _assert_tree_equals_oracle(got, ref, t, edges, nb):
     assert np.array_equal(thr, f.threshold[t][num])
 
 
-@pytest.mark.parametrize("shape", ["mixed", "wide"])
+@pytest.mark.parametrize("shape", ["mixed", "wide", "wide32"])
 def test_trees_grown_through_the_seam_equal_the_oracle(ctx, shape):
     # fitImpl's level loop on the kernel seam alone (Booster.swift:1467-1648):
     # quantile edges, binning, then per tree quantise -> begin -> per level
@@ -359,8 +364,9 @@ def test_trees_grown_through_the_seam_equal_the_oracle(ctx, shape):
         is_cat, nb, tile_w, depth = [0] * 6 + [1], 64, 8, 5
         mono = np.array([0, 0, 0, 1, 0, 0, 0], np.int8)
     else:
+        # wide32: 32-wide tiles, the last tile's 4 features folded into the others
         x, y = mb.friedman(60_000, 100, 17)
-        is_cat, nb, tile_w, depth = [0] * 100, 256, 64, 6
+        is_cat, nb, tile_w, depth = [0] * 100, 256, (64 if shape == "wide" else 32), 6
         mono = np.zeros(100, np.int8)
     cols, rows = x.shape
     trees = 3

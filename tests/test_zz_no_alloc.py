@@ -59,6 +59,7 @@ def test_noalloc_equals_the_allocating_entry_point():
     rng = np.random.default_rng(2024)
     cases = [(400_000, 100, 256, 64, 350_000),   # many items
              (60_000, 100, 256, 64, 7_001),      # smaller: the array keeps the last call's bytes
+             (100_000, 100, 256, 32, 90_000),    # 32-wide tiles, the last tile folded in
              (9_000, 13, 64, 16, 5_000),         # another tile width and bin count
              (2_000, 5, 17, 8, 0)]               # an empty node
     for rows, cols, nb, tile_w, n in cases:
