@@ -3,29 +3,29 @@
 
 Headline (the metric's workload): Friedman #1 regression, 10M rows x 100 fp32
 features, 256 bins, level-wise depth 6, lr 0.1, L2, 100 trees.  A step is one
-complete fit of those 100 trees through mbk_fit with the raw features already
-resident in HBM: device quantile edges, binning, the 100 trees and the
-readback of the model, i.e. everything FitTimings.total covers
-(Booster.swift:506, :1699) except the host-to-device copy of X.  W untimed
-fits, then K timed fits; value = 100 * K / seconds (trees/s).  The held-out
-RMSE after those 100 trees is reported (the reference: 1.033, README.md:73).
+complete macboost_train call from host memory, i.e. everything
+FitTimings.total covers (Booster.swift:505-506, :564-565, :1699): the 4 GB
+host-to-device copy of X, device quantile edges, binning, the 100 trees and
+the readback of the model.  W untimed steps, then K timed steps, each timed
+on its own; value = 100 / the median step (trees/s).  The held-out RMSE after
+those 100 trees is reported (the reference: 1.033, README.md:73).
 
 Also reported:
 * roofline: the histogram kernel, algorithmic bytes (sum over built nodes of
   rows * (features + 4)) over its HIP-event time on the trainer's stream,
-  measured inside the timed fits; traffic from the committed rocprofv3
+  measured inside the timed steps; traffic from the committed rocprofv3
   FETCH_SIZE / WRITE_SIZE summary;
-* the same fit through macboost_train from host memory (PCIe included), and
-  the rate with the binned matrix already resident (trees only);
+* the same fit with X already resident in HBM (mbk_fit), and the rate with
+  the binned matrix resident (trees only);
 * the small (20k x 100, 64 bins) and 1M x 100 Friedman workloads, the NaN +
   categorical workload with per-iteration validation, the HIGGS-like
   logistic workload plain and with GOSS, and leaf-wise growth (63 leaves)
   with 500k-row batch predict and 200k-row TreeSHAP;
 * CPU baselines on this host: the oracle (tests/oracle_lib.py, OpenMP over
   the host cores, results identical at any thread count) on the headline
-  workload (binning + a prefix of trees, extrapolated), the 20k workload on
-  one core in full, the 1M workload on every core (binning + a 20-tree
-  prefix, extrapolated), and batch predict and TreeSHAP on every core.
+  workload (binning + a prefix of trees, extrapolated), the 20k and 1M
+  workloads on one core in full, and batch predict and TreeSHAP on every
+  core.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -70,26 +70,46 @@ def headline(mb, ctx, args):
     rows, cols, trees = args.rows, args.cols, 100
     log(f"generating Friedman #1 {rows} x {cols} (seed 42)")
     x, y = mb.friedman(rows, cols, 42)
-    t0 = time.perf_counter()
-    x_dev = ctx.upload(x)
-    ctx.sync()
-    log(f"X resident in HBM ({x.nbytes / 1e9:.1f} GB, {time.perf_counter() - t0:.2f}s)")
     params = dict(LEVELWISE, num_trees=trees)
     for _ in range(args.warmup):
-        ctx.fit(params, x_dev, rows, cols, y)
-    log(f"{args.warmup} warm-up fits done")
+        mb.train(params, x, y, feature_major=True)
+    log(f"{args.warmup} warm-up steps done")
     # the histogram launches of every PROFILE_EVERY-th tree carry their own
     # dispatch timestamps (a timestamped launch costs a few microseconds more)
-    ctx.profile(True, every=args.profile_every)
-    sec, h = time_fits(ctx, params, x_dev, rows, cols, y, args.steps)
-    ctx.profile(False)
-    launches, hist_ms, hist_bytes, built, level_ms = ctx.hist_stats(16)
-    value = trees / sec
-    log(f"{args.steps} fits of {trees} trees: {sec * 1e3:.1f} ms per fit = {value:.1f} trees/s")
+    mb.profile_train(True, every=args.profile_every)
+    times, h = [], None
+    ctx.sync()
+    t_all = time.perf_counter()
+    for k in range(args.steps):
+        t0 = time.perf_counter()
+        h = mb.train(params, x, y, feature_major=True)     # returns after the model readback
+        times.append(time.perf_counter() - t0)
+        log(f"step {k}: {times[-1] * 1e3:.1f} ms")
+    ctx.sync()
+    total = time.perf_counter() - t_all
+    mb.profile_train(False)
+    stats = mb.train_hist_stats(16)
+    med = float(np.median(times))
+    value = trees / med
+    log(f"{args.steps} complete fits of {trees} trees from host memory: median "
+        f"{med * 1e3:.1f} ms (mean {total / args.steps * 1e3:.1f}) = {value:.1f} trees/s")
     xv, yv = mb.friedman(200_000, cols, 42 + 999)
     valid = rmse(mb.predict(h, xv, feature_major=True), yv)
     log(f"held-out RMSE after {mb.num_trees(h)} trees: {valid:.4f}")
-    return x, y, x_dev, sec, value, valid, (launches, hist_ms, hist_bytes, built, level_ms)
+    return x, y, times, total, value, valid, stats
+
+
+def x_resident(mb, ctx, x, y, rows, cols, steps):
+    """The same fit through mbk_fit with X already in HBM (no PCIe copy)."""
+    x_dev = ctx.upload(x)
+    ctx.sync()
+    params = dict(LEVELWISE, num_trees=100)
+    ctx.fit(params, x_dev, rows, cols, y)
+    sec, _ = time_fits(ctx, params, x_dev, rows, cols, y, steps)
+    log(f"X resident in HBM: {sec * 1e3:.1f} ms per fit = {100 / sec:.1f} trees/s")
+    return x_dev, {"fit_seconds": sec, "trees_per_s": 100 / sec, "fits": steps,
+                   "note": "mbk_fit on device-resident features: edges, binning, trees, "
+                           "model readback; no host-to-device copy of X"}
 
 
 def roofline_of(stats, rows, cols, steps, trees, every):
@@ -130,25 +150,24 @@ def roofline_of(stats, rows, cols, steps, trees, every):
 def headline_extras(mb, x, y, rows, cols):
     out = {}
     params = dict(LEVELWISE, num_trees=100)
-    t0 = time.perf_counter()
-    h = mb.train(params, x, y, feature_major=True)
-    out["fit_seconds_pcie_inclusive"] = time.perf_counter() - t0
-    del h
-    log(f"macboost_train from host memory (PCIe included): "
-        f"{out['fit_seconds_pcie_inclusive']:.3f}s")
     tr = mb.Trainer(dict(params, num_trees=110), x, y, feature_major=True)
+    e, b = tr.setup_seconds()
+    out["setup_seconds"] = {"upload": b, "edges_and_binning": e}
     tr.grow(10)
     t0 = time.perf_counter()
     tr.grow(100)
     el = time.perf_counter() - t0
     tr.close()
     out["trees_per_s_bins_resident"] = 100 / el
-    log(f"trees only, bins resident: {100 / el:.1f} trees/s")
+    log(f"trees only, bins resident: {100 / el:.1f} trees/s (setup: upload {b * 1e3:.1f} ms, "
+        f"edges + binning {e * 1e3:.1f} ms)")
     return out
 
 
-def small_and_1m(mb, ctx, with_cpu):
-    """The 20k x 100 (64 bins) and 1M x 100 Friedman workloads, 100 trees."""
+def small_and_1m(mb, ctx, with_cpu, c2_cpu_full=False):
+    """The 20k x 100 (64 bins) and 1M x 100 Friedman workloads, 100 trees.  The
+    oracle runs on one core: the 20k workload in full, the 1M one with a
+    20-tree prefix extrapolated (in full with c2_cpu_full)."""
     out = {}
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as O
@@ -174,11 +193,11 @@ def small_and_1m(mb, ctx, with_cpu):
         log(f"{name}: {sec * 1e3:.1f} ms per 100-tree fit ({100 / sec:.0f} trees/s), "
             f"PCIe-inclusive {pcie * 1e3:.1f} ms, valid RMSE {r['valid_rmse']:.4f}")
         if with_cpu:
-            # the small workload in full on one thread; the 1M one on every
-            # thread, binning and a 20-tree prefix, extrapolated to 100 trees
+            # one thread: the small workload in full; the 1M one binning and a
+            # 20-tree prefix, extrapolated to 100 trees (or in full)
             small = rows <= 20_000
-            O.set_threads(1 if small else 0)
-            threads, ntrees = O.get_threads(), 100 if small else 20
+            O.set_threads(1)
+            threads, ntrees = O.get_threads(), 100 if small or c2_cpu_full else 20
             t0 = time.perf_counter()
             edges = O.compute_edges(x, nb)
             bins = O.bin_matrix(x, edges, nb)
@@ -191,9 +210,9 @@ def small_and_1m(mb, ctx, with_cpu):
             r["cpu_oracle"] = {"fit_seconds": fit100, "trees_per_s": 100 / fit100,
                                "threads": threads, "binning_seconds": t_bin,
                                "trees_timed": ntrees, "trees_seconds": t_fit,
-                               "note": "edges + binning + 100 trees in full" if small else
+                               "note": "edges + binning + 100 trees in full" if ntrees == 100 else
                                        "edges + binning + 20 trees timed, 100 extrapolated"}
-            if small:
+            if ntrees == 100:
                 r["cpu_oracle"]["valid_rmse"] = rmse(
                     O.predict(m.forest, m.base_score, nb, xt), yt)
             log(f"{name}: oracle on {threads} thread(s): 100-tree fit {fit100:.2f}s")
@@ -344,6 +363,9 @@ def main():
     ap.add_argument("--profile-every", type=int, default=PROFILE_EVERY,
                     help="time the histogram launches of every k-th tree of the timed fits")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--c2-cpu-full", action="store_true",
+                    help="time the 1M-row workload's oracle on one core for all 100 trees "
+                         "(about 2 minutes)")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline fits (no other workloads)")
     ap.add_argument("--only", choices=["small_1m", "mixed", "higgs"],
@@ -358,41 +380,47 @@ def main():
     import macboost_amd as mb
     ctx = mb.Context(0)
     if args.only:
-        run = {"small_1m": lambda: small_and_1m(mb, ctx, not args.no_cpu),
+        run = {"small_1m": lambda: small_and_1m(mb, ctx, not args.no_cpu, args.c2_cpu_full),
                "mixed": lambda: mixed_1m(mb, ctx), "higgs": lambda: higgs(mb, ctx)}[args.only]
         print(json.dumps({"only": args.only, **run()}), flush=True)
         return
     rows, cols = args.rows, args.cols
-    x, y, x_dev, sec, value, valid, stats = headline(mb, ctx, args)
+    x, y, times, total, value, valid, stats = headline(mb, ctx, args)
     roofline = roofline_of(stats, rows, cols, args.steps, 100, args.profile_every)
-    extras = {}
+    med = float(np.median(times))
+    x_dev, resident = x_resident(mb, ctx, x, y, rows, cols, 5)
+    extras = {"x_resident": resident}
     if not args.no_extras:
         extras.update(headline_extras(mb, x, y, rows, cols))
         extras["leafwise_predict_treeshap"] = leafwise_predict_shap(
             mb, ctx, x_dev, rows, cols, y, not args.no_cpu)
-        extras["small_and_1m"] = small_and_1m(mb, ctx, not args.no_cpu)
+        extras["small_and_1m"] = small_and_1m(mb, ctx, not args.no_cpu, args.c2_cpu_full)
         extras["mixed_and_higgs"] = {**mixed_1m(mb, ctx), **higgs(mb, ctx)}
     cpu = None if args.no_cpu else cpu_baseline(x, y, rows, cols, args.cpu_trees)
     out = {
         "metric": "trees/s fitting 10M×100 depth-6; histogram HBM GB/s as % of peak",
         "value": value, "unit": "trees/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": sec * 1e3,
+        "warmup": args.warmup, "ms_per_step": med * 1e3,
         "higher_is_better": True, "scaling": "weak",
         "vs_baseline": value / REFERENCE_TREES_PER_S,
         "dtype": "u8 bins, int64 histograms, f32 gains", "data": "synthetic",
         "config": {"workload": "friedman1-regression-levelwise", "rows": rows, "features": cols,
                    "bins": 256, "max_depth": 6, "learning_rate": 0.1, "objective": "l2",
                    "trees_per_fit": 100, "parallelism": "single-gpu",
-                   "step": "one complete 100-tree fit with X resident in HBM: device edges, "
-                           "binning, trees, model readback"},
+                   "step": "one complete 100-tree macboost_train from host memory: the 4 GB "
+                           "host-to-device copy of X, device edges, binning, trees, model "
+                           "readback"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "rows_per_s": rows * value,
-        "fit_seconds_100_trees": sec,
+        "step_ms": [t * 1e3 for t in times],
+        "mean_ms_per_step": total / args.steps * 1e3,
+        "fit_seconds_100_trees": med,
         "valid_rmse_after_100_trees": valid,
         "reference_valid_rmse": 1.033,
         "vs_baseline_basis": "value / (100 trees / 3.9 s), the reference's 10M x 100 fit on an "
-                             "M4 Max (README.md:73), which also includes binning",
+                             "M4 Max (README.md:73), which also copies X into a device buffer "
+                             "and bins it",
         "host_nproc": os.cpu_count(),
         **extras,
     }

@@ -316,6 +316,14 @@ int mbx_trainer_level_stats(void *trainer, int32_t max_levels, int64_t *built, i
 int mbx_context_profile(mbk_context *ctx, int32_t enable, char **err);
 int mbx_context_hist_stats(mbk_context *ctx, int32_t max_levels, int64_t *launches, double *ms,
                            double *bytes, int64_t *built, double *level_ms, char **err);
+/* The same instrumentation for every macboost_train call of the process
+ * from now on: k >= 1 on for every k-th tree of each fit (clearing the
+ * totals when it was off), 0 off.  Totals as for mbx_context_hist_stats, added
+ * up over the fits since it was turned on.  No counterpart in the reference:
+ * it serves timing harnesses that measure the public entry point. */
+int mbx_profile_global(int32_t enable, char **err);
+int mbx_profile_global_stats(int32_t max_levels, int64_t *launches, double *ms, double *bytes,
+                             int64_t *built, double *level_ms, char **err);
 /* Wall-clock seconds of the last mbx_trainer_create phases: edges_s the
  * device quantile edges and binning (the label upload overlaps them), bin_s
  * the upload of host features before them (0 for device features). */

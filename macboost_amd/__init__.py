@@ -7,6 +7,6 @@ entry points as the reference binding (python/macboost/_core.py).
 from ._core import (  # noqa: F401
     Context, Dataset, MacBoostError, Trainer, best_iteration, eval_history,
     feature_importance, friedman,
-    load, num_classes, num_features, num_trees, predict, predict_contrib, save,
-    select_features, train, train_dataset, version, warnings,
+    load, num_classes, num_features, num_trees, predict, predict_contrib, profile_train, save,
+    select_features, train, train_dataset, train_hist_stats, version, warnings,
 )

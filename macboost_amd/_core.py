@@ -191,6 +191,12 @@ def _configure(l):
     l.mbx_context_hist_stats.argtypes = [_P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64),
                                          ctypes.POINTER(ctypes.c_double),
                                          ctypes.POINTER(ctypes.c_double), _P, _P, _c_char_pp]
+    l.mbx_profile_global.restype = ctypes.c_int
+    l.mbx_profile_global.argtypes = [ctypes.c_int32, _c_char_pp]
+    l.mbx_profile_global_stats.restype = ctypes.c_int
+    l.mbx_profile_global_stats.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_int64),
+                                           ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_double), _P, _P, _c_char_pp]
     l.mbx_eval_history.restype = ctypes.c_int64
     l.mbx_eval_history.argtypes = [_P, _P, ctypes.c_int64]
     l.mbx_version.restype = ctypes.c_char_p
@@ -231,6 +237,7 @@ EXPORTED = (
     "mbx_version", "mbx_dataset_make", "mbx_dataset_save", "mbx_dataset_load",
     "mbx_dataset_info", "mbx_dataset_copy", "mbx_dataset_feature_names", "mbx_dataset_train",
     "mbx_dataset_free", "mbx_eval_history", "mbx_context_profile", "mbx_context_hist_stats",
+    "mbx_profile_global", "mbx_profile_global_stats",
 )
 
 
@@ -439,6 +446,28 @@ def friedman(rows: int, cols: int, seed: int, noise: float = 1.0):
     lib().mbx_friedman(rows, cols, ctypes.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), noise,
                        x.ctypes.data, y.ctypes.data)
     return x, y
+
+
+def profile_train(enable: bool = True, every: int = 1) -> None:
+    """HIP-event timing of the histogram launches of every every-th tree of
+    each later train() call in this process (enable=False stops it)."""
+    err = ctypes.c_char_p()
+    if lib().mbx_profile_global(max(1, every) if enable else 0, ctypes.byref(err)) != 0:
+        raise MacBoostError(_take_error(err))
+
+
+def train_hist_stats(levels: int = 16):
+    """(launches, ms, algorithmic bytes, built rows per level, ms per level) of
+    the histogram kernel over the train() calls timed since profile_train()."""
+    n, ms, b = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+    built = np.zeros(levels, np.int64)
+    lms = np.zeros(levels, np.float64)
+    err = ctypes.c_char_p()
+    if lib().mbx_profile_global_stats(levels, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(b),
+                                      built.ctypes.data, lms.ctypes.data,
+                                      ctypes.byref(err)) != 0:
+        raise MacBoostError(_take_error(err))
+    return int(n.value), float(ms.value), float(b.value), built, lms
 
 
 class Trainer:

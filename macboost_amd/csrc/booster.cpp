@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <fstream>
 #include <sstream>
 #include <thread>
@@ -550,6 +551,44 @@ using mb::Booster;
 using mb::guarded;
 using mb::set_err;
 
+namespace {
+// Process-wide histogram instrumentation of macboost_train (mbx_profile_global):
+// every k-th tree of each later fit times its histogram launches with their own
+// dispatch timestamps; the totals add up over the fits.
+struct GlobalProfile {
+    std::mutex m;
+    int every = 0;                 // 0: off
+    int64_t launches = 0;
+    double ms = 0.0, bytes = 0.0;
+    int64_t built[16] = {};
+    double level_ms[16] = {};
+};
+GlobalProfile &global_profile() {
+    static GlobalProfile g;
+    return g;
+}
+int global_profile_every() {
+    GlobalProfile &g = global_profile();
+    std::lock_guard<std::mutex> lock(g.m);
+    return g.every;
+}
+void global_profile_add(mb::Trainer *t) {
+    int64_t n = 0, built[16];
+    double ms = 0, bytes = 0, lms[16];
+    mb::trainer_hist_stats(t, &n, &ms, &bytes);
+    mb::trainer_level_stats(t, 16, built, nullptr, lms);
+    GlobalProfile &g = global_profile();
+    std::lock_guard<std::mutex> lock(g.m);
+    g.launches += n;
+    g.ms += ms;
+    g.bytes += bytes;
+    for (int d = 0; d < 16; ++d) {
+        g.built[d] += built[d];
+        g.level_ms[d] += lms[d];
+    }
+}
+}  // namespace
+
 
 extern "C" {
 
@@ -559,11 +598,14 @@ void *macboost_train(const char *params_json, const float *x, int64_t rows, int6
     return guarded(err, [&]() -> void * {
         if (!x || !y || rows <= 0 || cols <= 0) mb::internal("null or empty training data");
         mb::Params p = mb::parse_params(params_json);
+        const int prof = global_profile_every();
         mb::Trainer *t = mb::trainer_create(p, x, rows, cols, row_major != 0, y, w, x_valid,
                                             valid_rows, y_valid);
         try {
+            if (prof > 0) mb::trainer_profile(t, prof);
             mb::trainer_grow(t, p.num_trees * mb::trainer_classes(t));
             Booster *b = mb::trainer_booster(t);
+            if (prof > 0) global_profile_add(t);
             mb::trainer_free(t);
             return b;
         } catch (...) {
@@ -696,6 +738,39 @@ int mbx_trainer_grow(void *trainer, int32_t num_trees, char **err) {
     if (!trainer) { set_err(err, "null argument"); return -1; }
     return guarded(err, [&]() -> int {
         mb::trainer_grow(static_cast<mb::Trainer *>(trainer), num_trees);
+        return 0;
+    }, -1);
+}
+
+int mbx_profile_global(int32_t enable, char **err) {
+    return guarded(err, [&]() -> int {
+        GlobalProfile &g = global_profile();
+        std::lock_guard<std::mutex> lock(g.m);
+        if (enable > 0 && g.every == 0) {
+            g.launches = 0;
+            g.ms = g.bytes = 0.0;
+            for (int d = 0; d < 16; ++d) {
+                g.built[d] = 0;
+                g.level_ms[d] = 0.0;
+            }
+        }
+        g.every = enable > 0 ? enable : 0;
+        return 0;
+    }, -1);
+}
+
+int mbx_profile_global_stats(int32_t max_levels, int64_t *launches, double *ms, double *bytes,
+                             int64_t *built, double *level_ms, char **err) {
+    return guarded(err, [&]() -> int {
+        GlobalProfile &g = global_profile();
+        std::lock_guard<std::mutex> lock(g.m);
+        if (launches) *launches = g.launches;
+        if (ms) *ms = g.ms;
+        if (bytes) *bytes = g.bytes;
+        for (int d = 0; d < max_levels; ++d) {
+            if (built) built[d] = d < 16 ? g.built[d] : 0;
+            if (level_ms) level_ms[d] = d < 16 ? g.level_ms[d] : 0.0;
+        }
         return 0;
     }, -1);
 }

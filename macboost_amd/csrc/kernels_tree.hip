@@ -134,17 +134,19 @@ template <int W>
 __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
     const float *__restrict__ x, int64_t rows, int32_t cols, int64_t rs, int64_t cs,
     const float *__restrict__ edges, const uint8_t *__restrict__ is_cat, int32_t nb, int32_t T,
-    uint8_t *__restrict__ tiled, uint8_t *__restrict__ fm, int vec_rows) {
+    int32_t t_first, int32_t t_count, uint8_t *__restrict__ tiled, uint8_t *__restrict__ fm,
+    int vec_rows) {
     constexpr int G = W < 16 ? W : 16;               // features per pass
     __shared__ float e_lds[W * 256];                 // [feature][BFS slot 1..255], slot 0 unused
     const int tid = threadIdx.x;
     const int ne = nb - 2, data_bins = nb - 1;
-    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8): the T
-    // tiles of a row block are blocks xcd + 8 (q T + t), all on one XCD, so
-    // the pieces of a row's T*W bytes merge in that XCD's L2.
+    // Workgroups go to the 8 XCDs round-robin (block b to XCD b % 8): the
+    // tiles t_first .. t_first + t_count - 1 of a row block are blocks
+    // xcd + 8 (q t_count + t), all on one XCD, so the pieces of a row's bytes
+    // merge in that XCD's L2.
     const uint32_t xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
-    const int t = (int)(k8 % (uint32_t)T);
-    const int64_t row_block = (int64_t)(k8 / (uint32_t)T) * 8 + xcd;
+    const int t = t_first + (int)(k8 % (uint32_t)t_count);
+    const int64_t row_block = (int64_t)(k8 / (uint32_t)t_count) * 8 + xcd;
     if (row_block * BIN_ROWS >= rows) return;         // grid padding (whole block)
     const int f0 = t * W;
     const int nf = max(0, min(W, cols - f0));         // real features of the tile
@@ -241,16 +243,26 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            int64_t rs, int64_t cs, const float *edges, const uint8_t *is_cat,
                            int32_t nb, int32_t tile_w, int32_t num_tiles, uint8_t *tiled,
                            uint8_t *fm) {
+    return launch_bin_tiles(s, x, rows, cols, rs, cs, edges, is_cat, nb, tile_w, num_tiles, 0,
+                            num_tiles, tiled, fm);
+}
+
+hipError_t launch_bin_tiles(hipStream_t s, const float *x, int64_t rows, int32_t cols,
+                            int64_t rs, int64_t cs, const float *edges, const uint8_t *is_cat,
+                            int32_t nb, int32_t tile_w, int32_t num_tiles, int32_t tile_first,
+                            int32_t tile_count, uint8_t *tiled, uint8_t *fm) {
     if (nb < 4 || nb > 256 || rows <= 0) return rows == 0 ? hipSuccess : hipErrorInvalidValue;
     if (tile_w != 8 && tile_w != 16 && tile_w != 32 && tile_w != 64) return hipErrorInvalidValue;
     if (num_tiles < 1 || (int64_t)num_tiles * tile_w < cols) return hipErrorInvalidValue;
-    const int64_t nblk = ((rows + BIN_ROWS - 1) / BIN_ROWS + 7) / 8 * 8 * (int64_t)num_tiles;
+    if (tile_first < 0 || tile_count < 1 || tile_first + tile_count > num_tiles)
+        return hipErrorInvalidValue;
+    const int64_t nblk = ((rows + BIN_ROWS - 1) / BIN_ROWS + 7) / 8 * 8 * (int64_t)tile_count;
     if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)nblk);
     const int vec_rows = cs == 1 && (rs & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 #define MBK_BIN(WW)                                                                             \
     hipLaunchKernelGGL(k_bin_data<WW>, grid, dim3(BIN_THREADS), 0, s, x, rows, cols, rs, cs, edges, \
-                       is_cat, nb, num_tiles, tiled, fm, vec_rows)
+                       is_cat, nb, num_tiles, tile_first, tile_count, tiled, fm, vec_rows)
     if (tile_w == 64) MBK_BIN(64);
     else if (tile_w == 32) MBK_BIN(32);
     else if (tile_w == 16) MBK_BIN(16);
@@ -1418,8 +1430,8 @@ constexpr int HIST_THREADS = 1024;
 constexpr int HIST_LDS_BYTES = 2 * 256 * 32 * 8;     // two planes of [256][32] u64, static
 // ring depths chosen by measurement (3 / 9 beat 2..6 / 6..15 at 10M x 100:
 // deeper data rings cost L2 reuse between the two tiles of a row)
-// (per lanes-per-row mode below: 3 / 9 with two lanes per row, 4 / 8 with four;
-// at four lanes per row 4 to 8 data batches measured the same)
+// (per lanes-per-row mode below: 3 / 9 with two lanes per 64-wide row, 4 / 8
+// with four; at four, 4 to 8 data batches measured the same)
 template <int LPR> constexpr int hist_data_ring() { return LPR == 4 ? 4 : 3; }
 template <int LPR> constexpr int hist_entry_ring() { return LPR == 4 ? 8 : 9; }
 // true: the per-lane LDS column words sit in a 32-register table; false: each
@@ -1478,8 +1490,8 @@ __device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0
 // being row j (k_quantize's implicit form).
 // LPR: lanes per row of a 64-wide tile.  2: 32 features per lane (the planar
 // root, whose rows are contiguous); 4: 16 per lane, so one 16-B load
-// instruction covers a gathered row's whole tile (-4% on deep levels at
-// 10M x 100 against 2, which needs two).  Narrower tiles: one row per lane.
+// instruction covers a gathered row's whole tile (-4% on deep levels at 10M x
+// 100 against 2, which needs two).  Narrower tiles: one row per lane.
 template <int W, int LPR, bool IMPLICIT>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
                                                        const Entry *__restrict__ order,
@@ -1494,7 +1506,8 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
     constexpr int DR = hist_data_ring<LPR>(), ER = hist_entry_ring<LPR>();
     static_assert(ER > DR, "a data refill needs the entry DR batches ahead");
     static_assert(ER % DR == 0, "batch k of every round uses data slot k % DR");
-    __shared__ uint64_t hist_lds[HIST_LDS_BYTES / 8];
+    constexpr int LDS_BYTES = HIST_LDS_BYTES;
+    __shared__ uint64_t hist_lds[LDS_BYTES / 8];
     const int32_t nb = sh.num_bins, cols = sh.cols, PW = sh.part_w;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1502,14 +1515,17 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
     const uint32_t nwaves = HIST_THREADS / 64;
     // lane = q * RPB + rl: row rl of the batch, features q*P .. q*P + P-1
     const uint32_t rl = (uint32_t)lane % (uint32_t)RPB, q = (uint32_t)lane / (uint32_t)RPB;
-    const uint32_t byte_off = W == 64 ? q * (uint32_t)P : 0u;
-    const uint32_t m = ((uint32_t)lane & (uint32_t)(P - 1)) >> 2;
+    const uint32_t byte_off = q * (uint32_t)P;
+    // x: the lane's rotation; at step s it adds byte (feature) x ^ s of its P
+    const uint32_t x = (uint32_t)lane & (uint32_t)(P - 1);
+    const uint32_t m = x >> 2;
     const uint32_t cx = P == 32 ? (m >> 2) : 0u;
     const bool b0 = (m & 1u) != 0, b1 = (m & 2u) != 0;
-    // W = 64: feature q*P + x sits in plane (q*P) >> 5, column ((q*P) & 31) + x
+    // W = 64: feature q*P + x sits in plane (q*P) >> 5, column ((q*P) & 31) + x;
+    // W = 32: plane 0, column q*P + x (both halves share it)
     const uint32_t colbase =
         W == 64 ? (((q * (uint32_t)P) >> 5) << 16) | ((((q * (uint32_t)P) & 31u) + rl) << 3)
-        : W == 32 ? (((uint32_t)lane & 31u) << 3)
+        : W == 32 ? ((q * (uint32_t)P + x) << 3)
                   : (((uint32_t)(lane >> 5) << 16) | (((uint32_t)lane & 31u) << 3));
     uint32_t colw[HIST_COLW_TABLE ? P : 1];
     if constexpr (HIST_COLW_TABLE) {
@@ -1519,7 +1535,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
     uint32_t sel[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-        sel[t] = 0x0C020000u | ((4u + (((uint32_t)lane & 3u) ^ (uint32_t)t)) << 8);
+        sel[t] = 0x0C020000u | ((4u + ((x & 3u) ^ (uint32_t)t)) << 8);
     // extra step j: plane 1, column (lane & 31) ^ j
     const uint32_t cwx0 = 0x10000u | (((uint32_t)lane & 31u) << 3);
     const uint32_t cwx1 = cwx0 ^ 8u;
@@ -1538,7 +1554,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         const HistItem item = items[it];
         const uint32_t cnt = item.count;            // >= 1
         const uint32_t last = cnt - 1;
-        for (int k = tid; k < HIST_LDS_BYTES / 16; k += HIST_THREADS)
+        for (int k = tid; k < LDS_BYTES / 16; k += HIST_THREADS)
             reinterpret_cast<uint4 *>(hist_lds)[k] = make_uint4(0, 0, 0, 0);
         __syncthreads();
         const uint8_t *tile = tiled + (size_t)item.tile * (size_t)lay.tile_step + byte_off;
@@ -1649,10 +1665,12 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                     for (int c = 0; c < 64 / W; ++c)
                         acc += hist_lds[(c / CPP) * 8192 + b * 32 + (c % CPP) * W + f];
                 }
-            } else {
-                const int e = f - W;                 // extra e: plane 1, columns q with q % ne == e
+            } else if constexpr (XTRA) {
+                const int e = f - W;                 // extra e: plane 1, columns c with c % ne == e
                 if (e >= ne) continue;
-                for (int q = e; q < 32; q += ne) acc += hist_lds[8192 + b * 32 + q];
+                for (int c = e; c < 32; c += ne) acc += hist_lds[8192 + b * 32 + c];
+            } else {
+                continue;                            // no extras without plane 1
             }
             __builtin_nontemporal_store(acc, &out[k]);   // read once, by k_reduce
         }

@@ -141,9 +141,9 @@ __host__ __device__ inline int32_t partial_feature(const Shape &sh, int32_t t, i
     return e < tile_extra_count(sh, t)
         ? sh.hist_tiles * sh.tile_w + tile_extra_first(sh, t) + e : -1;
 }
-inline void set_hist_tiling(Shape &sh) {
+inline void set_hist_tiling(Shape &sh, bool fold = true) {
     const int32_t last = sh.cols - (sh.num_tiles - 1) * sh.tile_w;   // features of the last tile
-    if (sh.tile_w == 32 && sh.num_tiles >= 2 && last <= 2 * (sh.num_tiles - 1)) {
+    if (fold && sh.tile_w == 32 && sh.num_tiles >= 2 && last <= 2 * (sh.num_tiles - 1)) {
         sh.hist_tiles = sh.num_tiles - 1;
         sh.extras = last;
         sh.part_w = sh.tile_w + (last > sh.hist_tiles ? 2 : 1);
@@ -184,6 +184,11 @@ hipError_t launch_bin_data(hipStream_t s, const float *x, int64_t rows, int32_t 
                            int64_t row_stride, int64_t col_stride, const float *edges,
                            const uint8_t *is_cat, int32_t num_bins, int32_t tile_w,
                            int32_t num_tiles, uint8_t *bins_tiled, uint8_t *bins_fm);
+// Tiles tile_first .. tile_first + tile_count - 1 only (the others untouched).
+hipError_t launch_bin_tiles(hipStream_t s, const float *x, int64_t rows, int32_t cols,
+                            int64_t rs, int64_t cs, const float *edges, const uint8_t *is_cat,
+                            int32_t nb, int32_t tile_w, int32_t num_tiles, int32_t tile_first,
+                            int32_t tile_count, uint8_t *tiled, uint8_t *fm);
 
 // Checks of device-resident raw features: a strided row sample
 // out[k * cols + f] = x[(k * step) * rs + f * cs] (k < m), and the categorical
@@ -370,7 +375,7 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *bins_tiled
                        uint64_t *partials, int grid, const HistLayout *layout = nullptr,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr,
                        bool implicit_rows = false);
-size_t hist_lds_size();   // static LDS of one histogram workgroup
+size_t hist_lds_size();   // static LDS of one histogram workgroup (one per CU)
 // Planar copy of the gather layout for the root pass over every row; out
 // holds planar_bytes(sh) bytes (the last tile's loads run up to 16 B past its
 // rows into the zeroed tail, and into the next row's bytes, which land in

@@ -123,9 +123,7 @@ void reserve_tree(mbk_context *ctx, const mbk_tree_shape &shape) {
     mbk::set_hist_tiling(sh);
     const int32_t T = sh.hist_tiles;                 // histogram items per row chunk
     const int64_t level_nodes = (int64_t)1 << (D - 1), total_nodes = ((int64_t)1 << (D + 1)) - 1;
-    const size_t lds = mbk::hist_lds_size();
-    const int wg_per_cu = (int)std::min<size_t>(2, std::max<size_t>(1, (160 * 1024) / lds));
-    t.hist_grid = ctx->dev->num_cus * wg_per_cu;
+    t.hist_grid = ctx->dev->num_cus;                 // one histogram workgroup per CU
     t.target_items = (uint32_t)t.hist_grid;
     t.min_chunk = 2048;
     int64_t items = T * ((rows + mbk::HIST_CHUNK_MAX - 1) / mbk::HIST_CHUNK_MAX) +

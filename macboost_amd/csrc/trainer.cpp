@@ -1007,7 +1007,9 @@ static void setup_shape(Trainer &t, int64_t rows, int64_t cols) {
     t.sh.num_bins = p.num_bins;
     t.sh.tile_w = tile_w;
     t.sh.num_tiles = (int)((cols + tile_w - 1) / tile_w);
-    mbk::set_hist_tiling(t.sh);
+    // gathered levels never fold: the extras' loads cost more L2 requests there
+    // than their saved LDS adds gain
+    mbk::set_hist_tiling(t.sh, false);
     t.sh_root = t.sh;
     t.sp.lambda = p.lambda;
     t.sp.min_child_hess = p.min_child_hess;
@@ -1200,22 +1202,22 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.route_done.alloc(1);
     MB_HIP(hipMemsetAsync(t.route_done.ptr, 0, sizeof(uint32_t), t.dev->stream));
 
-    // histogram work decomposition
-    const size_t lds = mbk::hist_lds_size();
-    int wg_per_cu = (int)std::min<size_t>(2, std::max<size_t>(1, (160 * 1024) / lds));
-    t.hist_grid = t.dev->num_cus * wg_per_cu;
+    // histogram work decomposition: one workgroup per CU (128 KiB of LDS),
+    // one item per workgroup and round
+    t.hist_grid = t.dev->num_cus;
     t.target_items = t.hist_grid;
     t.min_chunk = 2048;
     // a level's items: T*ceil(count/chunk) summed over its built nodes, at most
     // target*rounds + T*nodes, where target*rounds <= T*rows/HIST_CHUNK_MAX + target
-    auto max_items_of = [&](int64_t T, int64_t nodes) {
+    auto max_items_of = [&](int64_t T, int64_t nodes, int64_t target) {
         const int64_t m = T * ((rows + mbk::HIST_CHUNK_MAX - 1) / mbk::HIST_CHUNK_MAX) +
-                          t.target_items + 1 + T * nodes;
+                          target + 1 + T * nodes;
         return std::min<int64_t>(m, T * ((rows + t.min_chunk - 1) / t.min_chunk + nodes + 1));
     };
     t.sh_root = root_shape(t);
-    t.sh.item_cap = (uint32_t)max_items_of(t.sh.hist_tiles, t.max_level_nodes);
-    t.sh_root.item_cap = (uint32_t)max_items_of(t.sh_root.hist_tiles, t.max_level_nodes);
+    t.sh.item_cap = (uint32_t)max_items_of(t.sh.hist_tiles, t.max_level_nodes, t.target_items);
+    t.sh_root.item_cap = (uint32_t)max_items_of(t.sh_root.hist_tiles, t.max_level_nodes,
+                                                t.target_items);
     t.partials.alloc(std::max((size_t)t.sh.item_cap * (size_t)t.sh.part_w,
                               (size_t)t.sh_root.item_cap * (size_t)t.sh_root.part_w) *
                      (size_t)p.num_bins);
@@ -1435,13 +1437,17 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
 
         // --- binning on the device: (upload,) quantile edges, bin_data --------
         std::vector<mbk::LabelStats> row_stats;       // the device row checks' blocks
-        double t0 = now_s();
+        double t0 = now_s(), te = t0;
+        struct Events {                              // destroyed after the streams drained
+            std::vector<hipEvent_t> ev;
+            ~Events() { for (hipEvent_t e : ev) (void)hipEventDestroy(e); }
+        } tile_ready;
         {
-            DevBuf<float> xd;
+            DevBuf<float> xd;                           // host features: kept in the cache
+            xd.pooled = true;                           // (no 4 GB hipMalloc / hipFree per fit)
             const float *xsrc = x;
             if (!x_on_device) {
                 xd.alloc((size_t)rows * (size_t)cols);
-                upload(xd.ptr, x, xd.bytes(), s);
                 xsrc = xd.ptr;
             }
             const size_t ne = (size_t)p.num_bins - 2;
@@ -1451,23 +1457,54 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
             const size_t cap = mbk::edge_sample_cap(rows);
             DevBuf<uint32_t> ka, kb, cnt;               // released after the stream drained
             ka.pooled = kb.pooled = cnt.pooled = true;
-            const double te = now_s();
-            {
-                Phase ph("quantile edges");
-                ka.alloc((size_t)cols * cap);
-                kb.alloc((size_t)cols * cap);
-                cnt.alloc((size_t)cols);
-                MB_HIP(mbk::launch_edges(s, xsrc, rows, (int)cols, rs, cs, p.num_bins, t.is_cat.ptr,
-                                         ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
-            }
-            // binning follows the edges on the device; meanwhile the labels
-            // cross PCIe on the copy stream and the edges come back to the host
-            Phase ph("bin data");
+            ka.alloc((size_t)cols * cap);
+            kb.alloc((size_t)cols * cap);
+            cnt.alloc((size_t)cols);
             t.bins_tiled.alloc((size_t)t.sh.num_tiles * (size_t)rows * (size_t)tile_w);
             t.bins_fm.alloc((size_t)rows * (size_t)cols);
-            MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
-                                        p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
-                                        t.bins_fm.ptr));
+            const int T = t.sh.num_tiles;
+            if (!x_on_device && !row_major && T > 1) {
+                // Feature-major host features arrive one tile's columns at a
+                // time on the copy stream; each tile's quantile edges and
+                // binning run on the compute stream while the next tile's
+                // columns cross PCIe, so only the last tile's work follows the
+                // upload (FitTimings' prep + bin, Booster.swift:564-566, with
+                // the copy overlapped).
+                Phase ph("upload + edges + bin data, by tile");
+                hipStream_t cps = t.dev->copy_stream;
+                for (int tt = 0; tt < T; ++tt) {
+                    const int64_t c0 = (int64_t)tt * tile_w;
+                    const int64_t nc = std::min<int64_t>(tile_w, cols - c0);
+                    upload(xd.ptr + c0 * rows, x + c0 * rows, (size_t)(nc * rows) * sizeof(float),
+                           cps);
+                    hipEvent_t ev = nullptr;
+                    MB_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+                    tile_ready.ev.push_back(ev);
+                    MB_HIP(hipEventRecord(ev, cps));
+                    MB_HIP(hipStreamWaitEvent(s, ev, 0));
+                    MB_HIP(mbk::launch_edges(s, xd.ptr + c0 * rows, rows, (int)nc, 1, rows,
+                                             p.num_bins, t.is_cat.ptr + c0, ka.ptr, kb.ptr, cnt.ptr,
+                                             ed.ptr + c0 * (int64_t)ne));
+                    MB_HIP(mbk::launch_bin_tiles(s, xd.ptr, rows, (int)cols, 1, rows, ed.ptr,
+                                                 t.is_cat.ptr, p.num_bins, tile_w, T, tt, 1,
+                                                 t.bins_tiled.ptr, t.bins_fm.ptr));
+                }
+                te = now_s();
+            } else {
+                if (!x_on_device) upload(xd.ptr, x, xd.bytes(), s);
+                te = now_s();
+                {
+                    Phase ph("quantile edges");
+                    MB_HIP(mbk::launch_edges(s, xsrc, rows, (int)cols, rs, cs, p.num_bins,
+                                             t.is_cat.ptr, ka.ptr, kb.ptr, cnt.ptr, ed.ptr));
+                }
+                // binning follows the edges on the device; meanwhile the labels
+                // cross PCIe on the copy stream and the edges come back to the host
+                Phase ph("bin data");
+                MB_HIP(mbk::launch_bin_data(s, xsrc, rows, (int)cols, rs, cs, ed.ptr, t.is_cat.ptr,
+                                            p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
+                                            t.bins_fm.ptr));
+            }
             t.edges.resize((size_t)cols * ne);
             MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
             hipStream_t cs2 = t.dev->copy_stream;
@@ -1720,7 +1757,8 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     const bool sampled = tree_sampled(t.p, tree);
     mbk::RootPlan rp{};
     if (root_cover) {
-        rp.sh = sampled || !t.has_root_copy ? t.sh : t.sh_root;
+        const bool planar = !sampled && t.has_root_copy;
+        rp.sh = planar ? t.sh_root : t.sh;
         rp.rows_active = sampled ? mbk::NONE : (uint32_t)t.rows;
         rp.target_items = (uint32_t)t.target_items;
         rp.min_chunk = (uint32_t)t.min_chunk;
@@ -1918,7 +1956,8 @@ static void grow_leafwise(Trainer &t, int tree) {
     mbk::TreeCtl *ctl = t.ctl.ptr;
     mbk::Entry *order = t.order_a.ptr;
     const bool sampled = tree_entries(t, tree, ctl, order);
-    const mbk::Shape &sh0 = !sampled && t.has_root_copy ? t.sh_root : sh;   // the root's
+    const bool planar0 = !sampled && t.has_root_copy;
+    const mbk::Shape &sh0 = planar0 ? t.sh_root : sh;   // the root's
     MB_HIP(mbk::launch_lw_init(s, sh0, t.lw, ctl, t.lw_state.ptr, t.lw_open.ptr, t.seg_a.ptr,
                                t.count.ptr, t.pairs.ptr, t.items.ptr, out,
                                sampled));
