@@ -20,6 +20,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <type_traits>
 
 namespace mbk {
 
@@ -31,15 +32,37 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
 __device__ __forceinline__ float f32_from_bits(uint32_t u) { return __uint_as_float(u); }
 
+// One DPP move of a 32- or 64-bit value (64-bit: both halves with the same
+// control); lanes without a source, or outside row_mask / bank_mask, get 0.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ uint64_t dpp_move(uint64_t v) {
+    const uint32_t lo = dpp_move<CTRL, ROW_MASK, BANK_MASK>((uint32_t)v);
+    const uint32_t hi = dpp_move<CTRL, ROW_MASK, BANK_MASK>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Inclusive wavefront prefix sum of integers with DPP: row_shr 1, 2, 4, 8
+// scan each row of 16 lanes (Hillis-Steele; a lane without a source adds 0),
+// then row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, and
+// row_bcast:31 adds lane 31's to rows 2 and 3.  Six steps, no LDS round trip
+// (a __shfl_up scan is six ds_bpermute round trips).  Integer addition, so
+// the result is the exact prefix sum whatever the order.
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_scan(T v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        T t = __shfl_up(v, o, 64);
-        if (lane >= o) v += t;
-    }
-    return v;
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit integers");
+    using U = typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type;
+    U u = (U)v;
+    u += dpp_move<0x111, 0xf, 0xf>(u);               // row_shr:1
+    u += dpp_move<0x112, 0xf, 0xf>(u);               // row_shr:2
+    u += dpp_move<0x114, 0xf, 0xf>(u);               // row_shr:4
+    u += dpp_move<0x118, 0xf, 0xf>(u);               // row_shr:8
+    u += dpp_move<0x142, 0xa, 0xf>(u);               // row_bcast:15 into rows 1 and 3
+    u += dpp_move<0x143, 0xc, 0xf>(u);               // row_bcast:31 into rows 2 and 3
+    return (T)u;
 }
 
 template <typename T>
