@@ -518,6 +518,8 @@ struct Trainer {
     // a finished tree's deepest covers (and empty leaves), written by the next
     // tree's root pass or at the end of the grow call
     mbk::PendingFixup fix_pending{};
+    int fix_tree = -1;             // the tree fix_pending belongs to (its out is rebuilt on use:
+                                   // ensure_capacity may have moved the model arrays since)
     // warm start: the init model's trees prefix the ensemble and its raw
     // scores seed preds (Booster.swift:849-866, :890-891)
     std::vector<Tree> init_trees;
@@ -1777,6 +1779,7 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     // when there is one, else on its own
     mbk::PendingFixup fix = t.fix_pending;
     t.fix_pending.active = 0;
+    if (fix.active) fix.out = t.tree_out(t.fix_tree);
     if (fix.active && !plan) {
         MB_HIP(mbk::launch_final_fixup(s, fix.la, fix.count, fix.out, fix.zero_empty != 0));
         fix.active = 0;
@@ -1893,6 +1896,7 @@ static void grow_levelwise(Trainer &t, int tree) {
                 // again before the next tree's root pass, which writes them
                 // (the validation walk and leaf renewal below do)
                 t.fix_pending = mbk::PendingFixup{ln, t.count.ptr, out, 1, 1};
+                t.fix_tree = tree;
                 break;
             }
             MB_HIP(mbk::launch_final_fixup(s, ln, t.count.ptr, out));
@@ -2013,6 +2017,7 @@ static void finish_leafwise(Trainer &t, int tree, const mbk::TreeOut &out, bool 
             // root pass writes them (or the end of the grow call)
             const mbk::LevelArgs ld{t.D, (uint32_t)((1u << t.D) - 1), 1u << t.D, 1u};
             t.fix_pending = mbk::PendingFixup{ld, t.count.ptr, out, 0, 1};
+            t.fix_tree = tree;
         }
     }
     if (t.has_valid)
@@ -2180,7 +2185,8 @@ void trainer_grow(Trainer *tp, int num_trees) {
     }
     if (t.fix_pending.active) {                      // the last tree's deepest covers
         const mbk::PendingFixup &f = t.fix_pending;
-        MB_HIP(mbk::launch_final_fixup(s, f.la, f.count, f.out, f.zero_empty != 0));
+        MB_HIP(mbk::launch_final_fixup(s, f.la, f.count, t.tree_out(t.fix_tree),
+                                       f.zero_empty != 0));
         t.fix_pending.active = 0;
     }
     if (t.ctl_pending >= 0) {                        // the last tree's control block
