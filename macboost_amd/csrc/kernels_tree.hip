@@ -1447,6 +1447,15 @@ hipError_t launch_quantize(hipStream_t s, const GradParams &gp, const float *pre
 // low bit (E_t = 2) names the extra feature, so each half-wave again hits 32
 // distinct bank pairs.  Loads are pipelined: data three batches ahead,
 // entries nine.
+//
+// Paired 32-wide tiles (W = 32, two lanes per row, for gathered rows): lane
+// 2r + q holds features 16q .. 16q+15 of row r, so one 16-B load per lane
+// brings the tile and a half-wave holds 16 rows x both halves.  At step s lane
+// (r, q) adds feature 16q + ((r & 15) ^ s) to plane 0, column 16q + ((r & 15)
+// ^ s): 32 distinct bank pairs per half-wave, 16 steps per 32 rows.  Extras
+// (E_t <= 2) take one more step: lane (r, q) adds extra q to plane 1, column
+// 16q + (r & 15), i.e. 16 copies per extra (lanes with q >= E_t fill columns
+// of an extra the tile does not carry, which the flush never reads).
 // ---------------------------------------------------------------------------
 
 constexpr int HIST_THREADS = 1024;
@@ -1455,8 +1464,8 @@ constexpr int HIST_LDS_BYTES = 2 * 256 * 32 * 8;     // two planes of [256][32] 
 // deeper data rings cost L2 reuse between the two tiles of a row)
 // (per lanes-per-row mode below: 3 / 9 with two lanes per 64-wide row, 4 / 8
 // with four; at four, 4 to 8 data batches measured the same)
-template <int LPR> constexpr int hist_data_ring() { return LPR == 4 ? 4 : 3; }
-template <int LPR> constexpr int hist_entry_ring() { return LPR == 4 ? 8 : 9; }
+template <int W, int LPR> constexpr int hist_data_ring() { return W / LPR == 16 ? 4 : 3; }
+template <int W, int LPR> constexpr int hist_entry_ring() { return W / LPR == 16 ? 8 : 9; }
 // true: the per-lane LDS column words sit in a 32-register table; false: each
 // is rebuilt with one XOR per update (frees the table's registers)
 constexpr bool HIST_COLW_TABLE = true;
@@ -1514,7 +1523,8 @@ __device__ __forceinline__ RowRaw<P> permute_dwords(const RowRaw<P> &in, bool b0
 // LPR: lanes per row of a 64-wide tile.  2: 32 features per lane (the planar
 // root, whose rows are contiguous); 4: 16 per lane, so one 16-B load
 // instruction covers a gathered row's whole tile (-4% on deep levels at 10M x
-// 100 against 2, which needs two).  Narrower tiles: one row per lane.
+// 100 against 2, which needs two).  32-wide tiles: 1 (one row per lane) or 2
+// (paired, above).  Narrower tiles: one row per lane.
 template <int W, int LPR, bool IMPLICIT>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict__ tiled,
                                                        const Entry *__restrict__ order,
@@ -1522,11 +1532,15 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                                                        const TreeCtl *ctl,
                                                        uint64_t *__restrict__ partials,
                                                        HistLayout lay, Shape sh) {
-    static_assert(W == 64 ? (LPR == 2 || LPR == 4) : LPR == 1, "lanes per row");
+    static_assert(W == 64   ? (LPR == 2 || LPR == 4)
+                  : W == 32 ? (LPR == 1 || LPR == 2)
+                            : LPR == 1,
+                  "lanes per row");
     constexpr int P = W / LPR > 32 ? 32 : W / LPR;   // features per lane
     constexpr int RPB = 64 / LPR;                    // rows per wavefront batch
     constexpr bool XTRA = W == 32;                   // extras possible (plane 1 free)
-    constexpr int DR = hist_data_ring<LPR>(), ER = hist_entry_ring<LPR>();
+    constexpr bool PAIRED = W == 32 && LPR == 2;     // lane 2r + q: row r, half q
+    constexpr int DR = hist_data_ring<W, LPR>(), ER = hist_entry_ring<W, LPR>();
     static_assert(ER > DR, "a data refill needs the entry DR batches ahead");
     static_assert(ER % DR == 0, "batch k of every round uses data slot k % DR");
     constexpr int LDS_BYTES = HIST_LDS_BYTES;
@@ -1536,16 +1550,18 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: loop bounds stay uniform
     const uint32_t nwaves = HIST_THREADS / 64;
-    // lane = q * RPB + rl: row rl of the batch, features q*P .. q*P + P-1
-    const uint32_t rl = (uint32_t)lane % (uint32_t)RPB, q = (uint32_t)lane / (uint32_t)RPB;
+    // lane = q * RPB + rl (paired: 2 * rl + q): row rl of the batch, features
+    // q*P .. q*P + P-1
+    const uint32_t rl = PAIRED ? (uint32_t)lane >> 1 : (uint32_t)lane % (uint32_t)RPB;
+    const uint32_t q = PAIRED ? (uint32_t)lane & 1u : (uint32_t)lane / (uint32_t)RPB;
     const uint32_t byte_off = q * (uint32_t)P;
     // x: the lane's rotation; at step s it adds byte (feature) x ^ s of its P
-    const uint32_t x = (uint32_t)lane & (uint32_t)(P - 1);
+    const uint32_t x = PAIRED ? rl & (uint32_t)(P - 1) : (uint32_t)lane & (uint32_t)(P - 1);
     const uint32_t m = x >> 2;
     const uint32_t cx = P == 32 ? (m >> 2) : 0u;
     const bool b0 = (m & 1u) != 0, b1 = (m & 2u) != 0;
     // W = 64: feature q*P + x sits in plane (q*P) >> 5, column ((q*P) & 31) + x;
-    // W = 32: plane 0, column q*P + x (both halves share it)
+    // W = 32: plane 0, column q*P + x (both half-waves share it)
     const uint32_t colbase =
         W == 64 ? (((q * (uint32_t)P) >> 5) << 16) | ((((q * (uint32_t)P) & 31u) + rl) << 3)
         : W == 32 ? ((q * (uint32_t)P + x) << 3)
@@ -1559,8 +1575,10 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
 #pragma unroll
     for (int t = 0; t < 4; ++t)
         sel[t] = 0x0C020000u | ((4u + ((x & 3u) ^ (uint32_t)t)) << 8);
-    // extra step j: plane 1, column (lane & 31) ^ j
-    const uint32_t cwx0 = 0x10000u | (((uint32_t)lane & 31u) << 3);
+    // extra step j: plane 1, column (lane & 31) ^ j (paired: one step, column
+    // 16q + x)
+    const uint32_t cwx0 = PAIRED ? 0x10000u | ((q * 16u + x) << 3)
+                                 : 0x10000u | (((uint32_t)lane & 31u) << 3);
     const uint32_t cwx1 = cwx0 ^ 8u;
     char *lds = reinterpret_cast<char *>(hist_lds);
     const uint32_t stride = nwaves * RPB;
@@ -1592,8 +1610,9 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
             tiled + lay.x_off + (size_t)(xf & ~3));
         const size_t xs4 = (size_t)(lay.x_stride >> 2);
         const uint32_t xb = (uint32_t)(xf & 3);
-        const uint32_t e0 = ne == 2 ? ((uint32_t)lane & 1u) : 0u;
-        const uint32_t selx0 = 0x0C020000u | ((4u + xb + e0) << 8);
+        // paired: lane q adds extra q (byte 3 at most: the dword's last)
+        const uint32_t e0 = PAIRED ? q : ne == 2 ? ((uint32_t)lane & 1u) : 0u;
+        const uint32_t selx0 = 0x0C020000u | ((4u + min(xb + e0, 3u)) << 8);
         const uint32_t selx1 = 0x0C020000u | ((4u + xb + (e0 ^ 1u)) << 8);
         // entry j of the item (IMPLICIT: row start + j with its packed word)
         auto entry = [&](uint32_t j) {
@@ -1636,7 +1655,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                     const uint32_t addr = __builtin_amdgcn_perm(x, cwx0, selx0);
                     atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
                 }
-                if (ne >= 2) {
+                if (!PAIRED && ne >= 2) {
                     const uint32_t addr = __builtin_amdgcn_perm(x, cwx1, selx1);
                     atomicAdd(reinterpret_cast<unsigned long long *>(lds + addr), v);
                 }
@@ -1689,9 +1708,16 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
                         acc += hist_lds[(c / CPP) * 8192 + b * 32 + (c % CPP) * W + f];
                 }
             } else if constexpr (XTRA) {
-                const int e = f - W;                 // extra e: plane 1, columns c with c % ne == e
+                // extra e: plane 1, columns c with c % ne == e (paired: 16e .. 16e+15)
+                const int e = f - W;
                 if (e >= ne) continue;
-                for (int c = e; c < 32; c += ne) acc += hist_lds[8192 + b * 32 + c];
+                if constexpr (PAIRED) {
+                    const uint64_t *src = hist_lds + 8192 + b * 32 + 16 * e;
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) acc += src[c];
+                } else {
+                    for (int c = e; c < 32; c += ne) acc += hist_lds[8192 + b * 32 + c];
+                }
             } else {
                 continue;                            // no extras without plane 1
             }
@@ -1766,7 +1792,16 @@ hipError_t launch_hist(hipStream_t s, const Shape &sh, const uint8_t *tiled, con
         break;
     case 8: MBK_HIST_CASE(8, 1)
     case 16: MBK_HIST_CASE(16, 1)
-    case 32: MBK_HIST_CASE(32, 1)
+    case 32:
+        // gathered rows of an ordered level: two lanes per row (one 16-B load
+        // each; HIGGS-like 10M x 28: levels 1-5 together -3%); streamed rows
+        // (planar copy, or the implicit root, 3% faster): one row per lane
+        if (layout || implicit_rows) {
+            MBK_HIST_CASE(32, 1)
+        } else {
+            MBK_HIST_LAUNCH(k_hist<32 MBK_COMMA 2 MBK_COMMA false>)
+            break;
+        }
     case 64:
         if (layout) { MBK_HIST_CASE(64, 2) }         // planar rows: contiguous, two lanes per row
         else { MBK_HIST_CASE(64, 4) }                // gathered rows: one load per row and tile
