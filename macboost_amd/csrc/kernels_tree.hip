@@ -65,17 +65,42 @@ __device__ __forceinline__ T wave_inclusive_scan(T v) {
     return (T)u;
 }
 
+// Lane 63's value in every lane (two readlanes for 64 bits).
+template <typename T>
+__device__ __forceinline__ T wave_last(T v) {
+    if constexpr (sizeof(T) == 8) {
+        const uint64_t u = (uint64_t)v;
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+        return (T)(((uint64_t)hi << 32) | lo);
+    } else {
+        return (T)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    }
+}
+
+// Wavefront totals in every lane, from the DPP scan's lane 63 (integer sums
+// and maxima: exact in any order).  Every lane of the wavefront must be active.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    static_assert(std::is_integral<T>::value, "integer sums only");
+    return wave_last(wave_inclusive_scan(v));
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-    return v;
+    // lanes without a source read 0, the identity of an unsigned max
+    v = max(v, dpp_move<0x111, 0xf, 0xf>(v));        // row_shr:1
+    v = max(v, dpp_move<0x112, 0xf, 0xf>(v));        // row_shr:2
+    v = max(v, dpp_move<0x114, 0xf, 0xf>(v));        // row_shr:4
+    v = max(v, dpp_move<0x118, 0xf, 0xf>(v));        // row_shr:8
+    v = max(v, dpp_move<0x142, 0xa, 0xf>(v));        // row_bcast:15
+    v = max(v, dpp_move<0x143, 0xc, 0xf>(v));        // row_bcast:31
+    return wave_last(v);
+}
+
+// Set bits of mask in the lanes below this one.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
 // Lexicographic argmax on (gain desc, seq asc); invalid = (-inf, INT_MAX).
@@ -1146,13 +1171,15 @@ __device__ __forceinline__ Entry load_entry_nt(const Entry *p) {
 // Keep rows with |g| >= threshold (weight 1) and a hashed uniform sample of
 // the rest (weight sp.weight).  512 threads take a 16384-row chunk, thread t
 // the quads k * 512 + t (k < 8) of g and h, so each load instruction reads
-// 4 KiB of contiguous rows.  A thread keeps its 32 keep / amplified decisions
+// 8 KiB of contiguous rows.  A thread keeps its 32 keep / amplified decisions
 // as bit masks; the block scans the per-thread counts, takes one cursor add
-// per chunk (adds to one address serialize, so chunks are large), stages the
-// kept rows' chunk offsets (14 bits, amplified flag in bit 15) in LDS and
-// then writes, contiguously, the entries {row, f32 bits of g * w} and
-// h_kept = h * w.  Per-block maxima of |g| * w and h * w go to
-// partial; with kept non-null, kept[i] = 1 for a kept row and 0 otherwise.
+// per chunk (adds to one address serialize, so chunks are large; 32768-row
+// chunks of 1024 threads measured 0.7 ms per HIGGS-like GOSS fit slower),
+// stages the kept rows' chunk offsets (14 bits, amplified flag in bit 15) in
+// LDS and then writes, contiguously, the entries
+// {row, f32 bits of g * w} and h_kept = h * w.  Each block's maxima of |g| * w
+// and h * w go into ctl->sample_max (atomic max of f32 bits: the values are
+// >= 0); with kept non-null, kept[i] = 1 for a kept row and 0 otherwise.
 // The entry order inside a chunk follows the staging, not the row order;
 // every consumer sums integers or partitions stably, so the tree does not
 // depend on it.
@@ -1163,8 +1190,8 @@ static_assert(SEL_CHUNK <= (1 << 15), "chunk offsets fit 15 bits");
 
 __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
     SampleParams sp, const float *__restrict__ g, const float *__restrict__ h, int64_t rows,
-    const uint32_t *__restrict__ buckets, TreeCtl *ctl, uint32_t *__restrict__ partial,
-    Entry *__restrict__ order, float *__restrict__ h_kept, uint8_t *__restrict__ kept) {
+    const uint32_t *__restrict__ buckets, TreeCtl *ctl, Entry *__restrict__ order,
+    float *__restrict__ h_kept, uint8_t *__restrict__ kept) {
     __shared__ uint16_t s_off[SEL_CHUNK];
     __shared__ uint32_t s_wave[SEL_THREADS / 64];
     __shared__ uint32_t s_base, s_total, s_thr;
@@ -1279,8 +1306,8 @@ __global__ __launch_bounds__(SEL_THREADS) void k_goss_select(
     if (tid == 0) {
         uint32_t a = red[0][0], b = red[1][0];
         for (int k = 1; k < SEL_THREADS / 64; ++k) { a = max(a, red[0][k]); b = max(b, red[1][k]); }
-        partial[2 * blockIdx.x] = a;
-        partial[2 * blockIdx.x + 1] = b;
+        if (a) atomicMax(&ctl->sample_max[0], a);
+        if (b) atomicMax(&ctl->sample_max[1], b);
     }
 }
 
@@ -1307,16 +1334,14 @@ __device__ void root_pass_block0(const RootPlan &rp, int has_plan, const Pending
 
 // Quantise the kept entries with the weighted maxima (quantize_gradients,
 // Shaders.swift:176-192, over amplified gradients): ghq holds g * w on entry.
-// Every block reduces the selection's per-block weighted maxima (partial,
-// nparts pairs) itself once its first entries are loading, as
-// k_grad_max_final would, and block 0 stores them in the control block for
-// the split search; block 0 also zeroes the |g| histogram for the next tree.
+// The selection left the maxima in ctl->sample_max; block 0 stores them as
+// the tree's max_gh for the split search and zeroes the |g| histogram for
+// the next tree.
 __global__ __launch_bounds__(256) void k_quantize_sampled(TreeCtl *ctl,
                                                           uint32_t *__restrict__ buckets,
                                                           Entry *__restrict__ order,
                                                           const float *__restrict__ h_kept,
-                                                          const uint32_t *__restrict__ partial,
-                                                          int nparts, RootPlan rp, int has_plan,
+                                                          RootPlan rp, int has_plan,
                                                           PendingFixup fx) {
     if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < GOSS_BUCKETS; k += blockDim.x) buckets[k] = 0;
@@ -1330,13 +1355,12 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(TreeCtl *ctl,
         e0 = load_entry_nt(order + i0);
         hw0 = __builtin_nontemporal_load(h_kept + i0);
     }
-    __shared__ uint2 bc;
-    const uint2 m = reduce_partial_max(partial, nparts, &bc);
+    const uint32_t mgb = ctl->sample_max[0], mhb = ctl->sample_max[1];
     if (blockIdx.x == 0 && threadIdx.x == 0) {
-        ctl->max_gh[0] = m.x;
-        ctl->max_gh[1] = m.y;
+        ctl->max_gh[0] = mgb;
+        ctl->max_gh[1] = mhb;
     }
-    const float mg = f32_from_bits(m.x), mh = f32_from_bits(m.y);
+    const float mg = f32_from_bits(mgb), mh = f32_from_bits(mhb);
     const float gscale = mg > 0.0f ? 32767.0f / mg : 0.0f;
     const float hscale = mh > 0.0f ? 127.0f / mh : 0.0f;
     for (uint32_t i = i0; i < n; i += step) {
@@ -1355,7 +1379,7 @@ __global__ __launch_bounds__(256) void k_quantize_sampled(TreeCtl *ctl,
 }
 
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
-                         uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
+                         uint32_t *buckets, const float *g, const float *h,
                          Entry *order, float *h_kept, uint8_t *kept, const RootPlan *plan,
                          const PendingFixup *fix, TreeCtl *ctl_prev, const uint32_t *walk_part,
                          int walk_nparts) {
@@ -1375,13 +1399,13 @@ hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, Tr
     const int64_t blocks = std::max<int64_t>(
         1, std::min<int64_t>((rows + SEL_CHUNK - 1) / SEL_CHUNK, SAMPLE_MAX_BLOCKS));
     hipLaunchKernelGGL(k_goss_select, dim3((unsigned)blocks), dim3(SEL_THREADS), 0, s, sp, g, h,
-                       rows, buckets, ctl, partial, order, h_kept, kept);
+                       rows, buckets, ctl, order, h_kept, kept);
     // the kept count is known only on the device: a fixed grid strides over it
     // (a rows-sized grid of mostly idle blocks measured 7 us slower)
     const unsigned qblocks =
         (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (rows + 255) / 256));
     hipLaunchKernelGGL(k_quantize_sampled, dim3(qblocks), dim3(256), 0, s, ctl, buckets, order,
-                       h_kept, partial, (int)blocks, plan ? *plan : RootPlan{}, plan ? 1 : 0,
+                       h_kept, plan ? *plan : RootPlan{}, plan ? 1 : 0,
                        fix ? *fix : PendingFixup{});
     return hipGetLastError();
 }
@@ -2643,9 +2667,139 @@ hipError_t launch_plan_root(hipStream_t s, const RootPlan &plan) {
     return hipGetLastError();
 }
 
+// plan_level for at most 64 parents, by one wavefront (lane p: parent p,
+// then pair p): the same outputs with no workgroup barrier.  Pair records are
+// written whole by their own lane, after the chunking.
+__device__ void plan_level_wave(const Shape &sh, const LevelArgs &la, uint32_t target_items,
+                                uint32_t min_chunk, TreeCtl *ctl, const uint32_t *seg_start_prev,
+                                uint32_t *seg_start_next, uint32_t *count,
+                                const uint64_t *cursors, const TreeOut &out, Pair *pairs,
+                                HistItem *items) {
+    __shared__ uint32_t w_cnt[64], w_seg[64], w_first[64], w_parent[64];
+    const uint32_t lane = (uint32_t)lane_id();
+    const uint32_t num_prev = la.num_level >> 1;
+    const uint32_t ls_prev = (la.level_start - 1) >> 1;
+    const bool mine = lane < num_prev;
+    bool split = false;
+    uint32_t cl = 0, cr = 0, seg = 0;
+    if (mine) {
+        const uint32_t n = ls_prev + lane;
+        const int32_t feat = out.split[n].feature;
+        const uint32_t cnt = count[n];
+        const uint32_t left = (uint32_t)__hip_atomic_load(&cursors[(size_t)lane * CURSOR_STRIDE],
+                                                          __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+        seg = seg_start_prev[lane];
+        split = feat >= 0 && cnt >= 1;
+        cl = split ? left : 0u;
+        cr = split ? cnt - left : 0u;
+        count[la.level_start + 2 * lane] = cl;
+        count[la.level_start + 2 * lane + 1] = cr;
+        out.cover[la.level_start + 2 * lane] = (float)cl;
+        out.cover[la.level_start + 2 * lane + 1] = (float)cr;
+        seg_start_next[2 * lane] = seg;
+        seg_start_next[2 * lane + 1] = seg + cl;
+    }
+    const uint32_t act = wave_sum(cl + cr);
+    if (lane == 0) ctl->level_active[la.level] = act;
+    if (la.terminal) {
+        if (lane == 0) { ctl->num_pairs = 0; ctl->num_items = 0; }
+        return;
+    }
+    // sibling pairs for split parents, in parent order: the smaller child
+    // builds, ties go left
+    const uint64_t bal = __ballot(mine && split);
+    const uint32_t num_pairs = (uint32_t)__popcll(bal);
+    if (mine && split) {
+        const uint32_t k = lanes_below(bal);
+        const bool left_built = cl <= cr;
+        w_cnt[k] = left_built ? cl : cr;
+        w_seg[k] = left_built ? seg : seg + cl;
+        w_parent[k] = lane | (left_built ? 0x80000000u : 0u);
+    }
+    if (lane == 0) ctl->num_pairs = num_pairs;
+    if (num_pairs == 0) {
+        if (lane == 0) ctl->num_items = 0;
+        return;
+    }
+    wave_lds_sync();
+    // lane k: pair k's built rows -> the level's chunk (write_items' rules)
+    const bool own = lane < num_pairs;
+    const uint32_t n = own ? w_cnt[lane] : 0u;
+    const uint32_t total = wave_sum(n);
+    const uint32_t c = item_chunk(total, num_pairs, sh.hist_tiles, target_items, min_chunk);
+    if (lane == 0) {
+        ctl->chunk = c;
+        ctl->level_built[la.level] = total;
+    }
+    // the balance of write_items: the smallest chunk whose per-pair chunk
+    // counts fit the item budget
+    const uint32_t K = (uint32_t)(item_budget(total, num_pairs, sh.hist_tiles, target_items) /
+                                  (uint64_t)sh.hist_tiles);
+    uint32_t hi = c;
+    uint32_t lo = total / K + (total % K != 0u);
+    if (lo < min_chunk) lo = min_chunk;
+    if (lo > hi) lo = hi;
+    while (lo < hi) {                                // uniform across the wavefront
+        const uint32_t mid = lo + (hi - lo) / 2;
+        const uint32_t q = n / mid;
+        if (wave_sum(q + (n - q * mid != 0u)) <= K) hi = mid; else lo = mid + 1;
+    }
+    const uint32_t chunk = lo;
+    auto pair_chunk = [&](uint32_t cnt) {
+        const uint32_t parts = (cnt + chunk - 1) / chunk;
+        return parts ? (cnt + parts - 1) / parts : chunk;
+    };
+    const uint32_t pc = pair_chunk(n);
+    const uint32_t nch = own ? (n + pc - 1) / pc : 0u;
+    const uint32_t nit = nch * (uint32_t)sh.hist_tiles;
+    const uint32_t inc = wave_inclusive_scan(nit);
+    const uint32_t first = inc - nit;
+    const uint32_t total_items = wave_last(inc);
+    const bool fits = total_items <= sh.item_cap;
+    if (own) {
+        const uint32_t par = w_parent[lane];
+        const uint32_t p = par & 0x7FFFFFFFu;
+        const bool left_built = (par >> 31) != 0;
+        Pair pr = {};
+        pr.built = left_built ? 2 * p : 2 * p + 1;
+        pr.derived = left_built ? 2 * p + 1 : 2 * p;
+        pr.parent = p;
+        // an overflowing level gets no items; the host reports it after the tree
+        pr.item_first = fits ? first : 0u;
+        pr.nchunks = fits ? nch : 0u;
+        pairs[lane] = pr;
+        w_first[lane] = first;
+    }
+    if (!fits) {
+        if (lane == 0) { ctl->num_items = 0; ctl->overflow = 1; }
+        return;
+    }
+    if (lane == 0) ctl->num_items = total_items;
+    wave_lds_sync();
+    for (uint32_t it = lane; it < total_items; it += 64) {
+        // owning pair: the last k with w_first[k] <= it
+        uint32_t a = 0, b = num_pairs - 1;
+        while (a < b) {
+            const uint32_t m = (a + b + 1) >> 1;
+            if (w_first[m] <= it) a = m; else b = m - 1;
+        }
+        const uint32_t rel = it - w_first[a];
+        const uint32_t t = rel % (uint32_t)sh.hist_tiles, ci = rel / (uint32_t)sh.hist_tiles;
+        const uint32_t cnt = w_cnt[a];
+        const uint32_t pca = pair_chunk(cnt);
+        HistItem h;
+        h.pair = a;
+        h.tile = t;
+        h.start = w_seg[a] + ci * pca;
+        h.count = min(pca, cnt - ci * pca);
+        items[it] = h;
+    }
+}
+
 // Plan level d from level d-1's routed counts (decide_splits phase 2,
 // Shaders.swift:1454-1488, with counts from the partition), run by one
-// 1024-thread workgroup.  Thread p owns parent p (at most PLAN_MAX_PAIRS
+// 1024-thread workgroup (at most 64 parents: by its first wavefront alone).  Thread p owns parent p (at most PLAN_MAX_PAIRS
 // parents, so one pass); what later steps read back goes through LDS.  The
 // partition cursors are read at device scope: the partition's last
 // workgroup plans while the kernel that updated them is still resident.
@@ -2660,6 +2814,12 @@ __device__ void plan_level(const Shape &sh, const LevelArgs &la, uint32_t target
     const int tid = threadIdx.x;
     const uint32_t num_prev = la.num_level >> 1;
     const uint32_t ls_prev = (la.level_start - 1) >> 1;   // (2^d - 1 - 1) / 2 = 2^(d-1) - 1
+    if (num_prev <= 64) {                            // uniform
+        if (tid < 64)
+            plan_level_wave(sh, la, target_items, min_chunk, ctl, seg_start_prev, seg_start_next,
+                            count, cursors, out, pairs, items);
+        return;
+    }
     if (tid == 0) s_active = 0;
     // children of a split node share its interval: left [start, start+L),
     // right [start+L, start+count), with L from the partition's left cursor
@@ -2831,12 +2991,6 @@ __device__ __forceinline__ bool route_block(const NodeSplit sp, const uint32_t *
     if (base_l + base_r + nvalid != cnt) return false;
     if (left_total) *left_total = base_l + tot[PART_SLICES];
     return true;
-}
-
-// Lanes below this one in the wavefront.
-__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
 // A persistent grid: each block computes the level's block prefix once and

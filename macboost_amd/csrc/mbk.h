@@ -172,6 +172,7 @@ struct TreeCtl {
     uint32_t overflow;       // 1 when a level needed more items than Shape::item_cap
     uint32_t sampled;        // rows kept by GOSS / bagging for this tree
     uint32_t sample_thr;     // f32 bits of the GOSS keep threshold on |g|
+    uint32_t sample_max[2];  // f32 bits of max |g|*w and max h*w over the kept rows
     uint32_t level_active[16];  // live order entries per level
     uint32_t level_built[16];   // rows of built (histogrammed) nodes per level
 };
@@ -321,10 +322,9 @@ struct RootPlan {
 // root, in its first workgroup; with fix non-null that workgroup first does
 // the previous tree's deepest-level fixup.  With walk_part non-null the tree's
 // start (launch_tree_start(ctl, ctl_prev, walk_part, walk_nparts)) is left to
-// the first pass, which does it itself.  partial is scratch for
-// grad_max_scratch_words() words and may be walk_part.
+// the first pass, which does it itself.
 hipError_t launch_sample(hipStream_t s, const SampleParams &sp, int64_t rows, TreeCtl *ctl,
-                         uint32_t *buckets, uint32_t *partial, const float *g, const float *h,
+                         uint32_t *buckets, const float *g, const float *h,
                          Entry *order, float *h_kept, uint8_t *kept,
                          const RootPlan *plan = nullptr, const PendingFixup *fix = nullptr,
                          TreeCtl *ctl_prev = nullptr, const uint32_t *walk_part = nullptr,

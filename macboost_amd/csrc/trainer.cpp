@@ -1808,7 +1808,7 @@ static bool tree_entries(Trainer &t, int tree, mbk::TreeCtl *ctl, mbk::Entry *or
     }
     if (sampled)
         MB_HIP(mbk::launch_sample(s, sample_params(t, tree), t.rows, ctl, t.goss_buckets.ptr,
-                                  t.gmax_part.ptr, t.samp_g.ptr, t.samp_h.ptr, order,
+                                  t.samp_g.ptr, t.samp_h.ptr, order,
                                   t.samp_h_kept.ptr, kept, plan, fixp,
                                   start_in_sample ? prev : nullptr,
                                   start_in_sample ? t.gmax_part.ptr : nullptr, walk_parts));
