@@ -119,9 +119,10 @@ std::unique_ptr<Device> acquire_device(int device_id);
 void release_device(std::unique_ptr<Device> d);
 
 // Host -> device copy of a pageable buffer on stream s.  Copies of 4 MB or
-// more go through pinned staging (in at least four pieces, host fills
-// overlapping the DMA) and have completed on return; smaller ones are one
-// hipMemcpyAsync.
+// more go through pinned staging (host fills overlapping the DMA of the other
+// buffer): on return the source has been read and the copy is queued on s
+// (work queued on s after it sees the data; other streams must wait for s);
+// smaller ones are one hipMemcpyAsync.
 void upload(void *dst, const void *src, size_t bytes, hipStream_t s);
 // Device -> host copy into a pageable buffer after the work queued on s;
 // complete on return (64 MB or more through the pinned staging buffers).
