@@ -1653,12 +1653,21 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(const uint8_t *__restrict
         Entry er[ER];
         RowRaw<P> dr[DR];
         uint32_t xr[XTRA ? DR : 1];
+        // Prologue in the main loop's issue order: the entries the first
+        // data loads need, then each data batch followed by the entry ER - DR
+        // batches after it.  Memory waits count loads in issue order, so at
+        // the loop head both paths then leave the same loads outstanding and
+        // the compiler's merged wait counts are the steady state's (issued
+        // entries-first, the first batches of every round waited with data
+        // only one or two batches ahead: deep levels 1% slower).
 #pragma unroll
-        for (int k = 0; k < ER; ++k) er[k] = entry(min(g0 + (uint32_t)k * stride + rl, last));
+        for (int k = 0; k < ER - DR; ++k) er[k] = entry(min(g0 + (uint32_t)k * stride + rl, last));
 #pragma unroll
         for (int k = 0; k < DR; ++k) {
             dr[k] = load_row_raw<P>(tile + (size_t)er[k].row * row_bytes, cx);
             if constexpr (XTRA) xr[k] = load_x(er[k].row);
+            er[ER - DR + k] = entry(min(g0 + (uint32_t)(ER - DR + k) * stride + rl, last));
+            __builtin_amdgcn_sched_barrier(0);       // keep this issue order
         }
         auto process = [&](uint32_t g, const Entry &e, const RowRaw<P> &raw, uint32_t x) {
             // rows past the item's end carry value 0
