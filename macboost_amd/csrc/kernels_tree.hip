@@ -3024,12 +3024,44 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     __shared__ uint32_t tot[PART_SLICES + 1];
     __shared__ uint64_t s_base;
     const int tid = threadIdx.x, w = tid >> 6, lane = lane_id();
-    // blocks per split node of the routed level, and their prefix
-    for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
-        const uint32_t nn = la.level_start + l;
-        const bool split = out.split[nn].feature >= 0 && count[nn] >= 1;
-        blk_prefix[l] = split ? (count[nn] + PART_BLOCK - 1) / PART_BLOCK : 0u;
+    // Logical block size: the level's live entries spread over whole rounds of
+    // the grid (at most PART_BLOCK each, a multiple of 64), so every workgroup
+    // takes about the same number of entries instead of a last round of
+    // 8,192-entry blocks on part of the grid.  Each split node adds at most one
+    // partial block, which the rounds reserve.
+    __shared__ uint32_t s_live, s_nsplit, s_bsz;
+    if (tid == 0) { s_live = 0; s_nsplit = 0; }
+    __syncthreads();
+    {
+        uint32_t live = 0, nsplit = 0;
+        for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
+            const uint32_t nn = la.level_start + l;
+            const bool split = out.split[nn].feature >= 0 && count[nn] >= 1;
+            blk_prefix[l] = split ? count[nn] : 0u;
+            live += blk_prefix[l];
+            nsplit += split ? 1u : 0u;
+        }
+        live = wave_sum(live);
+        nsplit = wave_sum(nsplit);
+        if (lane == 0 && (live | nsplit)) {
+            atomicAdd(&s_live, live);
+            atomicAdd(&s_nsplit, nsplit);
+        }
     }
+    __syncthreads();
+    if (tid == 0) {
+        const uint64_t live = s_live, nsplit = s_nsplit, g = gridDim.x;
+        const uint64_t rounds = ((live + PART_BLOCK - 1) / PART_BLOCK + nsplit + g - 1) / g;
+        const uint64_t slots = rounds * g > nsplit ? rounds * g - nsplit : 1;
+        uint64_t bsz = (live + slots - 1) / slots;
+        bsz = (bsz + 63) / 64 * 64;
+        s_bsz = (uint32_t)(bsz < 64 ? 64 : bsz > PART_BLOCK ? PART_BLOCK : bsz);
+    }
+    __syncthreads();
+    const uint32_t bsz = s_bsz;
+    // blocks per split node of the routed level, and their prefix
+    for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS)
+        blk_prefix[l] = (blk_prefix[l] + bsz - 1) / bsz;
     __syncthreads();
     const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
     uint32_t b = blockIdx.x;
@@ -3057,8 +3089,8 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         k.l = lo;
         k.start = seg_start[lo];
         k.cnt = count[n];
-        k.first = (bb - blk_prefix[lo]) * PART_BLOCK;
-        k.nvalid = min((uint32_t)PART_BLOCK, k.cnt - k.first);
+        k.first = (bb - blk_prefix[lo]) * bsz;
+        k.nvalid = min(bsz, k.cnt - k.first);
         k.sp = out.split[n];
     };
     auto load_entries = [&](const Blk &k, Entry (&e)[PART_PER_THREAD]) {
