@@ -483,6 +483,27 @@ __device__ __forceinline__ float key_float(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
+constexpr int KEY_STRIDE = SPLIT_KEY_STRIDE;
+
+// A node's split-search key: the ordered gain of one feature's best split
+// above, the complement of the feature below, so the 64-bit maximum over the
+// node's features is decide_splits' argmax (Shaders.swift:1386-1400): the
+// largest gain, the lowest feature among equal gains.  0 is no candidate:
+// NaN and -inf gains never win that argmax.
+__device__ __forceinline__ uint64_t split_key(float gain, int f) {
+    if (!(gain > -INFINITY)) return 0;
+    return ((uint64_t)gain_key(gain) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)f);
+}
+__device__ __forceinline__ int key_feature(uint64_t k) {
+    return k ? (int)(0xFFFFFFFFu - (uint32_t)k) : -1;
+}
+// Whether a node of cnt rows splits: decide_node's test on its key.
+__device__ __forceinline__ bool key_splits(uint64_t k, uint32_t cnt, float min_split_gain) {
+    if (k == 0 || cnt < 1) return false;
+    const float g = key_float((uint32_t)(k >> 32));
+    return isfinite(g) && g > min_split_gain;
+}
+
 // Sample keys: thread s converts sample s (row s * step) of column blockIdx.y
 // into its order-preserving key, NaN into 0xFFFFFFFF (above every number's
 // key, so NaNs sort last and the first m sorted keys are the sample's m
@@ -1926,9 +1947,19 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
                                                 const uint64_t *__restrict__ partials,
                                                 const int64_t *__restrict__ hist_prev,
                                                 int64_t *__restrict__ hist_cur, const TreeCtl *ctl,
-                                                uint32_t blocks_per_tile, int derive) {
+                                                uint32_t blocks_per_tile, int derive,
+                                                uint64_t *keys, uint64_t *cursors,
+                                                uint32_t nzero) {
     constexpr int CELLS = 256 / S;
     __shared__ int64_t red[S > 1 ? S : 1][CELLS][2];
+    if (blockIdx.x == 0) {
+        // the level's split keys (maxima from the split search next) and
+        // partition cursors (used by the next partition) start from zero
+        for (uint32_t l = threadIdx.x; l < nzero; l += blockDim.x) {
+            if (keys) keys[(size_t)l * KEY_STRIDE] = 0;
+            if (cursors) cursors[(size_t)l * CURSOR_STRIDE] = 0;
+        }
+    }
     const int PW = sh.part_w, nb = sh.num_bins, F = sh.cols, T = sh.hist_tiles;
     const uint32_t bpt = blockIdx.x % blocks_per_tile;
     const uint32_t rest = blockIdx.x / blocks_per_tile;
@@ -1989,17 +2020,21 @@ __global__ __launch_bounds__(256) void k_reduce(Shape sh, const Pair *__restrict
 
 hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
                          const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
-                         const TreeCtl *ctl, bool derive) {
+                         const TreeCtl *ctl, bool derive, uint64_t *keys, uint64_t *cursors,
+                         uint32_t nzero) {
     const uint32_t cells = (uint32_t)(sh.num_bins * sh.part_w);
     const int dv = derive ? 1 : 0;
+    if (!keys && !cursors) nzero = 0;
     if (max_pairs >= 32) {                           // measured: S = 4 is faster below
         const uint32_t bpt = (cells + 255) / 256;
         hipLaunchKernelGGL(k_reduce<1>, dim3(max_pairs * (uint32_t)sh.hist_tiles * bpt), dim3(256),
-                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
+                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv, keys,
+                           cursors, nzero);
     } else {
         const uint32_t bpt = (cells + 63) / 64;
         hipLaunchKernelGGL(k_reduce<4>, dim3(max_pairs * (uint32_t)sh.hist_tiles * bpt), dim3(256),
-                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv);
+                           0, s, sh, pairs, partials, hist_prev, hist_cur, ctl, bpt, dv, keys,
+                           cursors, nzero);
     }
     return hipGetLastError();
 }
@@ -2053,8 +2088,9 @@ struct CatScratch {
 
 // Best split of one node's feature histogram held as 4 consecutive bins per
 // lane (bins 4*lane .. 4*lane+3).  Mirrors find_splits (Shaders.swift:396-463)
-// with exact integer prefix sums.  Returns the result in lane 0's `out`.
-__device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32_t nb,
+// with exact integer prefix sums.  Writes the result through dst (one lane)
+// and returns its gain in every lane (-inf: no valid split).
+__device__ float node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32_t nb,
                            bool is_cat, int cst, float g_inv, float h_inv, const SplitParams &sp,
                            CatScratch *cs, SplitResult *dst) {
     const int lane = lane_id();
@@ -2136,13 +2172,14 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
                 r.gain = -INFINITY;
                 *dst = r;
             }
+            return -INFINITY;
         } else if (ws == best_seq && best_gain == wg) {
             SplitResult r = {};
             r.gain = best_gain; r.bin = best_bin; r.gl = best_gl; r.hl = best_hl;
             r.flags = best_flags; r.gl_int = best_gli; r.hl_int = best_hli;
             *dst = r;
         }
-        return;
+        return wg;
     }
 
     // Categorical: non-empty bins (missing included) stably sorted by
@@ -2217,7 +2254,7 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
             r.gain = -INFINITY;
             *dst = r;
         }
-        return;
+        return -INFINITY;
     }
     const int k = ws + 1;                            // left subset size
 #pragma unroll
@@ -2232,6 +2269,7 @@ __device__ void node_split(const int64_t (&hg)[4], const int64_t (&hh)[4], int32
         for (int w = 0; w < 8; ++w) r.mask[w] = cs->mask[w];
         *dst = r;
     }
+    return wg;
 }
 
 // One workgroup per (sibling pair, 4 features), one wavefront per (side,
@@ -2259,7 +2297,8 @@ __global__ __launch_bounds__(SPLIT_THREADS) void k_split(Shape sh, SplitParams s
                                                          const TreeCtl *ctl, const uint32_t *count,
                                                          int64_t *node_g, int64_t *node_h,
                                                          uint32_t level_start,
-                                                         SplitResult *__restrict__ results) {
+                                                         SplitResult *__restrict__ results,
+                                                         uint64_t *keys) {
     __shared__ __align__(16) unsigned char split_lds[SPLIT_LDS_BYTES];
     int64_t *stage = reinterpret_cast<int64_t *>(split_lds);      // [side][bin][SPLIT_ROW]
     CatScratch *cs_all = reinterpret_cast<CatScratch *>(split_lds);
@@ -2276,6 +2315,8 @@ __global__ __launch_bounds__(SPLIT_THREADS) void k_split(Shape sh, SplitParams s
     const int f = f0 + fw;
     const uint32_t local = side == 0 ? pr.built : pr.derived;
     const bool active = fw < nf && local != NONE;
+    __shared__ unsigned long long s_key[2];          // the workgroup's best key per side
+    if (tid < 2) s_key[tid] = 0;
     // stage both sides' rows (a side without a node stages zeros)
     const int row = 2 * nf;
     int64_t v[SPLIT_STAGE_PER_THREAD];
@@ -2308,25 +2349,40 @@ __global__ __launch_bounds__(SPLIT_THREADS) void k_split(Shape sh, SplitParams s
         }
     }
     __syncthreads();                                 // the stage becomes split scratch
-    if (!active) return;                             // uniform per wavefront
-    const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
-    const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
-    const bool cat = is_cat[f] != 0;
-    const int cst = cat ? 0 : (int)monotone[f];
-    const bool allowed = feat_mask[f] != 0;
-    const uint32_t abs_n = level_start + local;
-    if (f == 0) {
-        const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
-        const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
-        if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
+    if (active) {                                    // uniform per wavefront
+        const float g_inv = f32_from_bits(ctl->max_gh[0]) / 32767.0f;
+        const float h_inv = f32_from_bits(ctl->max_gh[1]) / 127.0f;
+        const bool cat = is_cat[f] != 0;
+        const int cst = cat ? 0 : (int)monotone[f];
+        const bool allowed = feat_mask[f] != 0;
+        const uint32_t abs_n = level_start + local;
+        if (f == 0) {
+            const int64_t G = wave_sum(hg[0] + hg[1] + hg[2] + hg[3]);
+            const int64_t H = wave_sum(hh[0] + hh[1] + hh[2] + hh[3]);
+            if (lane == 0) { node_g[abs_n] = G; node_h[abs_n] = H; }
+        }
+        SplitResult *dst = results + (size_t)local * F + f;
+        if (allowed && count[abs_n] >= 1) {
+            const float g = node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs_all[w], dst);
+            const uint64_t k = keys ? split_key(g, f) : 0;
+            if (lane == 0 && k) atomicMax(&s_key[side], (unsigned long long)k);
+        } else if (lane == 0) {
+            SplitResult r = {};
+            r.gain = -INFINITY;
+            *dst = r;
+        }
     }
-    SplitResult *dst = results + (size_t)local * F + f;
-    if (allowed && count[abs_n] >= 1) {
-        node_split(hg, hh, nb, cat, cst, g_inv, h_inv, sp, &cs_all[w], dst);
-    } else if (lane == 0) {
-        SplitResult r = {};
-        r.gain = -INFINITY;
-        *dst = r;
+    if (keys) {                                      // uniform
+        // the node's argmax over features, for the next partition's
+        // decisions: one global maximum per workgroup and side (each node's
+        // key on its own 128-B line; same-line atomics serialize)
+        __syncthreads();
+        if (tid < 2) {
+            const uint32_t node = tid == 0 ? pr.built : pr.derived;
+            if (node != NONE && s_key[tid])
+                atomicMax(reinterpret_cast<unsigned long long *>(&keys[(size_t)node * KEY_STRIDE]),
+                          s_key[tid]);
+        }
     }
 }
 
@@ -2335,12 +2391,14 @@ hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp, c
                         int64_t *hist_cur, const uint8_t *is_cat, const int8_t *monotone,
                         const uint8_t *feat_mask, const TreeCtl *ctl, const uint32_t *count,
                         int64_t *node_g, int64_t *node_h, uint32_t level_start,
-                        SplitResult *results) {
+                        SplitResult *results, uint64_t *keys, uint64_t *cursors) {
     if (sh.num_bins > 256) return hipErrorInvalidValue;
-    hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl, true);
+    // level_start = 2^d - 1: the level holds level_start + 1 nodes
+    hipError_t e = launch_reduce(s, sh, pairs, max_pairs, partials, hist_prev, hist_cur, ctl, true,
+                                 keys, cursors, level_start + 1);
     if (e != hipSuccess) return e;
     return launch_find_splits(s, sh, sp, pairs, max_pairs, hist_cur, is_cat, monotone, feat_mask,
-                              ctl, count, node_g, node_h, level_start, results);
+                              ctl, count, node_g, node_h, level_start, results, keys);
 }
 
 hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams &sp,
@@ -2348,18 +2406,24 @@ hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams 
                               const uint8_t *is_cat, const int8_t *monotone,
                               const uint8_t *feat_mask, const TreeCtl *ctl, const uint32_t *count,
                               int64_t *node_g, int64_t *node_h, uint32_t level_start,
-                              SplitResult *results) {
+                              SplitResult *results, uint64_t *keys) {
     if (sh.num_bins > 256) return hipErrorInvalidValue;
     const uint32_t groups = (uint32_t)((sh.cols + SPLIT_FEATS - 1) / SPLIT_FEATS);
     hipLaunchKernelGGL(k_split, dim3(max_pairs * groups), dim3(SPLIT_THREADS), 0, s, sh, sp, pairs,
                        hist_cur, is_cat, monotone, feat_mask, ctl, count, node_g, node_h,
-                       level_start, results);
+                       level_start, results, keys);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // decisions: one wavefront per node (decide_splits phase 1, :1386-1451)
 // ---------------------------------------------------------------------------
+
+__device__ void decide_apply(const SplitParams &sp, int F, uint32_t n, uint32_t local, int bf,
+                             float bg, const SplitResult *__restrict__ results, int64_t Gt,
+                             int64_t Ht, float2 pb, uint32_t mgb, uint32_t mhb, int64_t *node_g,
+                             int64_t *node_h, float2 *bounds, const int8_t *monotone,
+                             const TreeOut &out);
 
 // decide_splits for node `local` of level la (Shaders.swift:1342-1452), run by
 // one wavefront: argmax over features, then the node's split or leaf, the
@@ -2396,9 +2460,21 @@ __device__ void decide_node(const Shape &sh, const SplitParams &sp, const LevelA
     }
     wave_argmax(bg, bf);
     if (lane != 0) return;
+    decide_apply(sp, F, n, local, bf == 0x7FFFFFFF ? -1 : bf, bg, results, Gt, Ht, pb, mgb, mhb,
+                 node_g, node_h, bounds, monotone, out);
+}
+
+// decide_splits' outcome for node n (level-local `local`) once its best
+// feature bf (-1: none) and gain bg are known, by one lane: the node's split
+// or leaf, the children's sums and monotone bounds (Shaders.swift:1401-1451).
+__device__ void decide_apply(const SplitParams &sp, int F, uint32_t n, uint32_t local, int bf,
+                             float bg, const SplitResult *__restrict__ results, int64_t Gt,
+                             int64_t Ht, float2 pb, uint32_t mgb, uint32_t mhb, int64_t *node_g,
+                             int64_t *node_h, float2 *bounds, const int8_t *monotone,
+                             const TreeOut &out) {
     const float g_inv = f32_from_bits(mgb) / 32767.0f;
     const float h_inv = f32_from_bits(mhb) / 127.0f;
-    if (bf != 0x7FFFFFFF && isfinite(bg) && bg > sp.min_split_gain) {
+    if (bf >= 0 && isfinite(bg) && bg > sp.min_split_gain) {
         const SplitResult r = results[(size_t)local * F + bf];
         NodeSplit ns = {bf, r.bin, r.flags};
         out.split[n] = ns;
@@ -2683,7 +2759,7 @@ __device__ void plan_level_wave(const Shape &sh, const LevelArgs &la, uint32_t t
                                 uint32_t min_chunk, TreeCtl *ctl, const uint32_t *seg_start_prev,
                                 uint32_t *seg_start_next, uint32_t *count,
                                 const uint64_t *cursors, const TreeOut &out, Pair *pairs,
-                                HistItem *items) {
+                                HistItem *items, const uint64_t *keys, float min_split_gain) {
     __shared__ uint32_t w_cnt[64], w_seg[64], w_first[64], w_parent[64];
     const uint32_t lane = (uint32_t)lane_id();
     const uint32_t num_prev = la.num_level >> 1;
@@ -2693,13 +2769,15 @@ __device__ void plan_level_wave(const Shape &sh, const LevelArgs &la, uint32_t t
     uint32_t cl = 0, cr = 0, seg = 0;
     if (mine) {
         const uint32_t n = ls_prev + lane;
-        const int32_t feat = out.split[n].feature;
         const uint32_t cnt = count[n];
         const uint32_t left = (uint32_t)__hip_atomic_load(&cursors[(size_t)lane * CURSOR_STRIDE],
                                                           __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT);
         seg = seg_start_prev[lane];
-        split = feat >= 0 && cnt >= 1;
+        // parents decided in this pass carry keys (their model arrays are
+        // written by other workgroups of it)
+        split = keys ? key_splits(keys[(size_t)lane * KEY_STRIDE], cnt, min_split_gain)
+                     : out.split[n].feature >= 0 && cnt >= 1;
         cl = split ? left : 0u;
         cr = split ? cnt - left : 0u;
         count[la.level_start + 2 * lane] = cl;
@@ -2815,7 +2893,8 @@ __device__ void plan_level_wave(const Shape &sh, const LevelArgs &la, uint32_t t
 __device__ void plan_level(const Shape &sh, const LevelArgs &la, uint32_t target_items,
                            uint32_t min_chunk, TreeCtl *ctl, const uint32_t *seg_start_prev,
                            uint32_t *seg_start_next, uint32_t *count, const uint64_t *cursors,
-                           const TreeOut &out, Pair *pairs, HistItem *items) {
+                           const TreeOut &out, Pair *pairs, HistItem *items,
+                           const uint64_t *keys = nullptr, float min_split_gain = 0.0f) {
     __shared__ uint32_t wave_tot[17];
     __shared__ uint32_t s_active;
     __shared__ uint32_t s_idx[PLAN_MAX_PAIRS];       // split flag, then pair index
@@ -2826,7 +2905,7 @@ __device__ void plan_level(const Shape &sh, const LevelArgs &la, uint32_t target
     if (num_prev <= 64) {                            // uniform
         if (tid < 64)
             plan_level_wave(sh, la, target_items, min_chunk, ctl, seg_start_prev, seg_start_next,
-                            count, cursors, out, pairs, items);
+                            count, cursors, out, pairs, items, keys, min_split_gain);
         return;
     }
     if (tid == 0) s_active = 0;
@@ -2838,13 +2917,13 @@ __device__ void plan_level(const Shape &sh, const LevelArgs &la, uint32_t target
     uint32_t cl = 0, cr = 0, seg = 0;
     if (mine) {
         const uint32_t n = ls_prev + p;
-        const int32_t feat = out.split[n].feature;
         const uint32_t cnt = count[n];
         const uint32_t left = (uint32_t)__hip_atomic_load(&cursors[(size_t)p * CURSOR_STRIDE],
                                                           __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT);
         seg = seg_start_prev[p];
-        split = feat >= 0 && cnt >= 1;
+        split = keys ? key_splits(keys[(size_t)p * KEY_STRIDE], cnt, min_split_gain)
+                     : out.split[n].feature >= 0 && cnt >= 1;
         cl = split ? left : 0u;
         cr = split ? cnt - left : 0u;
         count[la.level_start + 2 * p] = cl;
@@ -3017,7 +3096,8 @@ template <bool IMPLICIT>
 __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     Shape sh, LevelArgs la, const uint8_t *__restrict__ bins_fm, const Entry *__restrict__ order_in,
     Entry *__restrict__ order_out, const uint32_t *__restrict__ seg_start, uint32_t *count,
-    const TreeOut out, uint64_t *cursors, int write_entries, RoutePlan rp, int has_plan) {
+    const TreeOut out, uint64_t *cursors, int write_entries, RoutePlan rp, int has_plan,
+    RouteDecide rd, int has_decide) {
     extern __shared__ uint32_t blk_prefix[];         // [num_level]: first block of each node
     __shared__ uint32_t s_mask[2][8];
     __shared__ uint32_t wave_tot[PART_WAVES + 1];
@@ -3036,7 +3116,9 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         uint32_t live = 0, nsplit = 0;
         for (uint32_t l = threadIdx.x; l < la.num_level; l += PART_THREADS) {
             const uint32_t nn = la.level_start + l;
-            const bool split = out.split[nn].feature >= 0 && count[nn] >= 1;
+            const bool split = has_decide ? key_splits(rd.keys[(size_t)l * KEY_STRIDE], count[nn],
+                                                       rd.sp.min_split_gain)
+                                          : out.split[nn].feature >= 0 && count[nn] >= 1;
             blk_prefix[l] = split ? count[nn] : 0u;
             live += blk_prefix[l];
             nsplit += split ? 1u : 0u;
@@ -3064,12 +3146,35 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         blk_prefix[l] = (blk_prefix[l] + bsz - 1) / bsz;
     __syncthreads();
     const uint32_t total_blocks = block_exclusive_scan(blk_prefix, la.num_level, wave_tot);
+    const uint64_t *keys = has_decide ? rd.keys : nullptr;
+    // decide mode: node l's model arrays, children's sums and bounds, by
+    // workgroup l % gridDim.x before its blocks (nothing in this pass reads
+    // them: routing and the planner take the splits from the keys; made at
+    // the end instead, they lengthened the pass's tail: 10M x 100 fit +0.3 ms)
+    auto decide_mine = [&]() {
+        if (!has_decide || tid != 0) return;
+        for (uint32_t l = blockIdx.x; l < la.num_level; l += gridDim.x) {
+            const uint32_t n = la.level_start + l;
+            if (count[n] < 1) {
+                out.split[n] = NodeSplit{-1, 0, 0};
+                out.leaf[n] = 0.0f;
+                out.gain[n] = 0.0f;
+                continue;
+            }
+            const uint64_t k = rd.keys[(size_t)l * KEY_STRIDE];
+            const float bg = k ? key_float((uint32_t)(k >> 32)) : -INFINITY;
+            decide_apply(rd.sp, rd.cols, n, l, key_feature(k), bg, rd.results, rd.node_g[n],
+                         rd.node_h[n], rd.bounds[n], rd.ctl->max_gh[0], rd.ctl->max_gh[1],
+                         rd.node_g, rd.node_h, rd.bounds, rd.monotone, out);
+        }
+    };
+    decide_mine();
     uint32_t b = blockIdx.x;
     if (b >= total_blocks) {                         // uniform per block
         // nothing to partition: the first workgroup plans alone
         if (has_plan && total_blocks == 0 && blockIdx.x == 0)
             plan_level(sh, rp.next, rp.target_items, rp.min_chunk, rp.ctl, seg_start, rp.seg_next,
-                       count, cursors, out, rp.pairs, rp.items);
+                       count, cursors, out, rp.pairs, rp.items, keys, rd.sp.min_split_gain);
         return;
     }
 
@@ -3091,7 +3196,20 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         k.cnt = count[n];
         k.first = (bb - blk_prefix[lo]) * bsz;
         k.nvalid = min(bsz, k.cnt - k.first);
-        k.sp = out.split[n];
+        if (has_decide) {
+            const int f = key_feature(rd.keys[(size_t)lo * KEY_STRIDE]);
+            const SplitResult *r = rd.results + (size_t)lo * rd.cols + f;
+            k.sp = NodeSplit{f, r->bin, r->flags};
+        } else {
+            k.sp = out.split[n];
+        }
+    };
+    // word w of the node's category mask (decide_node's: the winning
+    // feature's subset for a categorical split, else zeros)
+    auto mask_word = [&](const Blk &k, int wd) -> uint32_t {
+        if (!has_decide) return out.mask[(size_t)(la.level_start + k.l) * 8 + wd];
+        if (!(k.sp.flags & FLAG_CATEGORICAL)) return 0u;
+        return rd.results[(size_t)k.l * rd.cols + k.sp.feature].mask[wd];
     };
     auto load_entries = [&](const Blk &k, Entry (&e)[PART_PER_THREAD]) {
         const uint32_t e0 = k.start + k.first;
@@ -3112,7 +3230,7 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
     Blk cur;
     Entry e[PART_PER_THREAD];
     locate(b, cur);
-    if (tid < 8) s_mask[0][tid] = out.mask[(size_t)(la.level_start + cur.l) * 8 + tid];
+    if (tid < 8) s_mask[0][tid] = mask_word(cur, tid);
     load_entries(cur, e);
     int buf = 0;
     __syncthreads();
@@ -3163,8 +3281,7 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         Entry en[PART_PER_THREAD];
         if (has_next) {
             locate(bn, nxt);
-            if (tid < 8)
-                s_mask[buf ^ 1][tid] = out.mask[(size_t)(la.level_start + nxt.l) * 8 + tid];
+            if (tid < 8) s_mask[buf ^ 1][tid] = mask_word(nxt, tid);
             load_entries(nxt, en);
         }
         if (tid == 63) s_base = old;
@@ -3202,7 +3319,7 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         if (s_last) {
             if (tid == 0) atomicExch(rp.done, 0u);
             plan_level(sh, rp.next, rp.target_items, rp.min_chunk, rp.ctl, seg_start, rp.seg_next,
-                       count, cursors, out, rp.pairs, rp.items);
+                       count, cursors, out, rp.pairs, rp.items, keys, rd.sp.min_split_gain);
         }
     }
 }
@@ -3211,9 +3328,12 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, uint32_t *count, const TreeOut out,
                         uint64_t *cursors, uint32_t max_blocks, bool write_entries,
-                        const RoutePlan *plan, bool implicit_in) {
-    // cursors were zeroed by this level's k_decide
+                        const RoutePlan *plan, bool implicit_in, const RouteDecide *decide) {
+    // cursors were zeroed by this level's k_decide (or, with decide, by
+    // launch_split's reduction)
     if (max_blocks < 1) return hipErrorInvalidValue;
+    if (decide && (!decide->keys || !decide->results || !decide->ctl || decide->cols < 1))
+        return hipErrorInvalidValue;
     RoutePlan rp{};
     if (plan) {
         if ((plan->next.num_level >> 1) > PLAN_MAX_PAIRS || !plan->done) return hipErrorInvalidValue;
@@ -3223,7 +3343,8 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
     auto *kern = implicit_in ? &k_route<true> : &k_route<false>;
     hipLaunchKernelGGL(kern, dim3(max_blocks), dim3(PART_THREADS), lds, s, sh, la, bins_fm,
                        order_in, order_out, seg_start, count, out, cursors,
-                       write_entries ? 1 : 0, rp, plan ? 1 : 0);
+                       write_entries ? 1 : 0, rp, plan ? 1 : 0, decide ? *decide : RouteDecide{},
+                       decide ? 1 : 0);
     return hipGetLastError();
 }
 

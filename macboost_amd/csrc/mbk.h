@@ -12,6 +12,7 @@ constexpr uint32_t FLAG_CATEGORICAL = 2u;
 
 constexpr int PART_ENTRIES = 8192;    // entries per partition block
 constexpr int CURSOR_STRIDE = 16;     // u64 words per node cursor (one 128-B line each)
+constexpr int SPLIT_KEY_STRIDE = 16;  // u64 words per node split key (one 128-B line each)
 
 // Packed histogram word: (sum of qg) << HIST_QH_BITS + (sum of qh), as a
 // 64-bit two's-complement sum.  A histogram item accumulates at most
@@ -387,19 +388,25 @@ hipError_t launch_planar_rows(hipStream_t s, const Shape &sh, const uint8_t *til
 
 // Reduce partials into hist_cur [node][B][F][g,h] (int64), derive siblings
 // from hist_prev, then search splits for both nodes of each pair.
+// With keys (level-local, node l's at keys[l * SPLIT_KEY_STRIDE]) every node's
+// best (gain, feature) is also left there as a split_key maximum, for the next
+// partition to decide the level (launch_route with RouteDecide) in place of
+// launch_decide; cursors (non-null) are then zeroed for that partition.
 hipError_t launch_split(hipStream_t s, const Shape &sh, const SplitParams &sp,
                         const Pair *pairs, uint32_t max_pairs, const uint64_t *partials,
                         const int64_t *hist_prev, int64_t *hist_cur, const uint8_t *is_cat,
                         const int8_t *monotone, const uint8_t *feat_mask,
                         const TreeCtl *ctl, const uint32_t *count, int64_t *node_g,
-                        int64_t *node_h, uint32_t level_start, SplitResult *results);
+                        int64_t *node_h, uint32_t level_start, SplitResult *results,
+                        uint64_t *keys = nullptr, uint64_t *cursors = nullptr);
 
 // The two halves of launch_split, for the kernel seam: partials -> built
 // histograms (and, with derive, the derived siblings), and the split search
 // over histograms already in hist_cur; plus the subtraction on its own.
 hipError_t launch_reduce(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
                          const uint64_t *partials, const int64_t *hist_prev, int64_t *hist_cur,
-                         const TreeCtl *ctl, bool derive);
+                         const TreeCtl *ctl, bool derive, uint64_t *keys = nullptr,
+                         uint64_t *cursors = nullptr, uint32_t nzero = 0);
 hipError_t launch_subtract(hipStream_t s, const Shape &sh, const Pair *pairs, uint32_t max_pairs,
                            const int64_t *hist_prev, int64_t *hist_cur, const TreeCtl *ctl);
 hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams &sp,
@@ -407,7 +414,7 @@ hipError_t launch_find_splits(hipStream_t s, const Shape &sh, const SplitParams 
                               const uint8_t *is_cat, const int8_t *monotone,
                               const uint8_t *feat_mask, const TreeCtl *ctl, const uint32_t *count,
                               int64_t *node_g, int64_t *node_h, uint32_t level_start,
-                              SplitResult *results);
+                              SplitResult *results, uint64_t *keys = nullptr);
 
 hipError_t launch_plan_root(hipStream_t s, const RootPlan &plan);
 
@@ -461,13 +468,29 @@ struct RoutePlan {
     HistItem *items;
     uint32_t *done;
 };
+// With decide, the routed level has not been decided yet (launch_split left
+// its keys, no launch_decide ran): every workgroup takes each node's split
+// from its key and the winning feature's SplitResult, and the nodes' model
+// arrays, children's sums and bounds are written here, as launch_decide
+// would (the level's cursors were zeroed by launch_split).
+struct RouteDecide {
+    const uint64_t *keys;           // node l's split_key maximum at l * SPLIT_KEY_STRIDE
+    const SplitResult *results;     // [level nodes][F]
+    SplitParams sp;
+    int32_t cols;
+    int64_t *node_g, *node_h;
+    float2 *bounds;
+    const int8_t *monotone;
+    const TreeCtl *ctl;
+};
 // implicit_in: order_in holds launch_quantize's implicit u32 words (the
 // root level of an unsampled tree).
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, uint32_t *count, const TreeOut out,
                         uint64_t *cursors, uint32_t max_blocks, bool write_entries,
-                        const RoutePlan *plan = nullptr, bool implicit_in = false);
+                        const RoutePlan *plan = nullptr, bool implicit_in = false,
+                        const RouteDecide *decide = nullptr);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,

@@ -535,6 +535,9 @@ struct Trainer {
     int walk_gparts = 0;
     bool kept_walk = false;
     DevBuf<uint64_t> route_cursor;
+    // level-wise: each node's best (gain, feature) key from the split search,
+    // for decisions made inside the next partition
+    DevBuf<uint64_t> split_keys;
     DevBuf<uint32_t> route_done;    // the partition's finished-workgroup count (zero between launches)
     uint32_t route_grid = 1;
     DevBuf<uint64_t> partials;
@@ -1234,6 +1237,7 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
         2 * (int64_t)t.dev->num_cus,
         (rows + mbk::PART_ENTRIES - 1) / mbk::PART_ENTRIES + t.max_level_nodes);
     t.route_cursor.alloc((size_t)t.max_level_nodes * mbk::CURSOR_STRIDE);
+    t.split_keys.alloc((size_t)t.max_level_nodes * mbk::SPLIT_KEY_STRIDE);
     t.route_done.alloc(1);
     MB_HIP(hipMemsetAsync(t.route_done.ptr, 0, sizeof(uint32_t), t.dev->stream));
 
@@ -1904,14 +1908,29 @@ static void grow_levelwise(Trainer &t, int tree) {
     };
     const mbk::Shape &sh0 = !sampled && t.has_root_copy ? t.sh_root : sh;   // the root's
 
+    // A level whose next partition is not the last one is decided inside that
+    // partition (launch_route with RouteDecide) from the split search's keys:
+    // one launch less per level.  The deepest split level keeps its decision
+    // launch, which the final leaves and the walk read.
+    const mbk::RouteDecide rd{t.split_keys.ptr, t.results.ptr, t.sp,       t.cols,
+                              t.node_g.ptr,     t.node_h.ptr,  t.bounds.ptr, t.mono.ptr, ctl};
+    auto split_level = [&](const mbk::Shape &shl, uint32_t pairs, const int64_t *hp, int64_t *hc,
+                           const mbk::LevelArgs &la) {
+        const bool fold = la.level + 1 < t.D;
+        MB_HIP(mbk::launch_split(s, shl, t.sp, t.pairs.ptr, pairs, t.partials.ptr, hp, hc,
+                                 t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
+                                 t.node_g.ptr, t.node_h.ptr, la.level_start, t.results.ptr,
+                                 fold ? t.split_keys.ptr : nullptr,
+                                 fold ? t.route_cursor.ptr : nullptr));
+        if (!fold)
+            MB_HIP(mbk::launch_decide(s, sh, t.sp, la, t.results.ptr, t.count.ptr, t.node_g.ptr,
+                                      t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl,
+                                      t.route_cursor.ptr, out));
+    };
+
     // level 0
     hist(ord_cur, 0);
-    MB_HIP(mbk::launch_split(s, sh0, t.sp, t.pairs.ptr, 1, t.partials.ptr, h_prev, h_cur,
-                             t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl, t.count.ptr,
-                             t.node_g.ptr, t.node_h.ptr, 0, t.results.ptr));
-    mbk::LevelArgs l0{0, 0, 1, 0};
-    MB_HIP(mbk::launch_decide(s, sh, t.sp, l0, t.results.ptr, t.count.ptr, t.node_g.ptr,
-                              t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.route_cursor.ptr, out));
+    split_level(sh0, 1, h_prev, h_cur, mbk::LevelArgs{0, 0, 1, 0});
     for (int d = 1; d <= t.D; ++d) {
         const bool terminal = d == t.D;
         mbk::LevelArgs lp{d - 1, (uint32_t)((1u << (d - 1)) - 1), 1u << (d - 1), terminal ? 1u : 0u};
@@ -1956,21 +1975,16 @@ static void grow_levelwise(Trainer &t, int tree) {
                                               t.preds_cur));
             break;
         }
+        // non-terminal here, so level d - 1 was decided by this partition's keys
         const mbk::RoutePlan rp = t.route_plan(ln, seg_next);
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
                                  t.count.ptr, out, t.route_cursor.ptr,
-                                 t.route_grid, true, &rp, d == 1 && !sampled));
+                                 t.route_grid, true, &rp, d == 1 && !sampled, &rd));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
         hist(ord_cur, d);
-        MB_HIP(mbk::launch_split(s, sh, t.sp, t.pairs.ptr, 1u << (d - 1), t.partials.ptr, h_prev,
-                                 h_cur, t.is_cat.ptr, t.mono.ptr, t.feat_mask.ptr, ctl,
-                                 t.count.ptr, t.node_g.ptr, t.node_h.ptr, ln.level_start,
-                                 t.results.ptr));
-        MB_HIP(mbk::launch_decide(s, sh, t.sp, ln, t.results.ptr, t.count.ptr, t.node_g.ptr,
-                                  t.node_h.ptr, t.bounds.ptr, t.mono.ptr, ctl, t.route_cursor.ptr,
-                                  out));
+        split_level(sh, 1u << (d - 1), h_prev, h_cur, ln);
     }
     if (t.has_valid)
         MB_HIP(mbk::launch_predict_binned(s, t.vbins_fm.ptr, t.vrows, t.nb, t.D, out,
