@@ -514,6 +514,33 @@ def test_reference_known_answers_on_gpu():
     assert np.all(np.abs(mb.predict(h, x, feature_major=True) - 3.25) < 1e-4)
 
 
+@pytest.mark.parametrize("min_split_gain", [0.0, 40.0])
+def test_levelwise_equal_gains_and_min_split_gain_identical(min_split_gain):
+    # Duplicated columns give every node's split search exactly equal gains on
+    # two or three features (numeric with NaN holes, and categorical): the
+    # level's decision must take the lowest feature, as decide_splits' argmax
+    # does.  A positive min_split_gain turns nodes whose best gain falls below
+    # it into leaves at every level (checked against the oracle in every array).
+    rng = np.random.default_rng(77)
+    n = 9000
+    base = rng.random((3, n), dtype=np.float32)
+    base[1, rng.random(n) < 0.15] = np.nan
+    cat = rng.integers(0, 9, n).astype(np.float32)
+    x = np.stack([base[0], base[1], cat, base[0], base[2], base[1], cat, base[0]])
+    y = (10 * base[0] + 5 * np.nan_to_num(base[1], nan=0.7) + (cat % 3) * 2
+         + rng.standard_normal(n)).astype(np.float32)
+    params = {"num_trees": 8, "max_depth": 6, "num_bins": 64,
+              "categorical_features": [2, 6], "min_split_gain": min_split_gain}
+    _, ref = check_identical(np.ascontiguousarray(x), y, params, is_cat=[0, 0, 1, 0, 0, 0, 1, 0])
+    used = set(int(f) for f in ref.forest.feature.ravel() if f >= 0)
+    assert used and used <= {0, 1, 2, 4}              # never a later copy
+    if min_split_gain > 0:
+        # nodes stop early: fewer splits than the same trees without the floor
+        free = oracle_fit(np.ascontiguousarray(x), y, dict(params, min_split_gain=0.0),
+                          [0, 0, 1, 0, 0, 0, 1, 0])
+        assert (ref.forest.feature >= 0).sum() < (free.forest.feature >= 0).sum()
+
+
 def test_depth_extremes_identical():
     x, y = O.friedman(3000, 5, 221)
     check_identical(x, y, {"num_trees": 4, "max_depth": 12, "num_bins": 32})
