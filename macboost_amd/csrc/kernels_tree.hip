@@ -3178,9 +3178,10 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         return;
     }
 
-    // logical block b: its node slot, segment, count, first entry and split
+    // logical block b: its node slot, segment, count, first entry, split and
+    // the sides whose entries are written (bit 0 left, bit 1 right)
     struct Blk {
-        uint32_t l, start, cnt, first, nvalid;
+        uint32_t l, start, cnt, first, nvalid, sides;
         NodeSplit sp;
     };
     auto locate = [&](uint32_t bb, Blk &k) {
@@ -3196,10 +3197,13 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
         k.cnt = count[n];
         k.first = (bb - blk_prefix[lo]) * bsz;
         k.nvalid = min(bsz, k.cnt - k.first);
+        k.sides = 3u;
         if (has_decide) {
             const int f = key_feature(rd.keys[(size_t)lo * KEY_STRIDE]);
             const SplitResult *r = rd.results + (size_t)lo * rd.cols + f;
             k.sp = NodeSplit{f, r->bin, r->flags};
+            if (write_entries == 2)                  // the plan's built child only
+                k.sides = r->hl_int <= rd.node_h[n] - r->hl_int ? 1u : 2u;
         } else {
             k.sp = out.split[n];
         }
@@ -3295,7 +3299,7 @@ __global__ __launch_bounds__(PART_THREADS, 8) void k_route(
                 const bool is_left = (left >> j) & 1u;
                 const uint32_t le =
                     tot[j * PART_WAVES + w] + lanes_below(__ballot(is_left));
-                if (i >= cur.nvalid) continue;
+                if (i >= cur.nvalid || !(cur.sides & (is_left ? 1u : 2u))) continue;
                 const uint32_t pos = is_left ? base_l + le : cur.cnt - 1u - (base_r + (i - le));
                 store_entry_nt(dst + pos, e[j]);
             }
@@ -3328,12 +3332,14 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, uint32_t *count, const TreeOut out,
                         uint64_t *cursors, uint32_t max_blocks, bool write_entries,
-                        const RoutePlan *plan, bool implicit_in, const RouteDecide *decide) {
+                        const RoutePlan *plan, bool implicit_in, const RouteDecide *decide,
+                        bool built_only) {
     // cursors were zeroed by this level's k_decide (or, with decide, by
     // launch_split's reduction)
     if (max_blocks < 1) return hipErrorInvalidValue;
     if (decide && (!decide->keys || !decide->results || !decide->ctl || decide->cols < 1))
         return hipErrorInvalidValue;
+    if (built_only && (!decide || !write_entries)) return hipErrorInvalidValue;
     RoutePlan rp{};
     if (plan) {
         if ((plan->next.num_level >> 1) > PLAN_MAX_PAIRS || !plan->done) return hipErrorInvalidValue;
@@ -3343,7 +3349,8 @@ hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
     auto *kern = implicit_in ? &k_route<true> : &k_route<false>;
     hipLaunchKernelGGL(kern, dim3(max_blocks), dim3(PART_THREADS), lds, s, sh, la, bins_fm,
                        order_in, order_out, seg_start, count, out, cursors,
-                       write_entries ? 1 : 0, rp, plan ? 1 : 0, decide ? *decide : RouteDecide{},
+                       write_entries ? (built_only ? 2 : 1) : 0, rp, plan ? 1 : 0,
+                       decide ? *decide : RouteDecide{},
                        decide ? 1 : 0);
     return hipGetLastError();
 }

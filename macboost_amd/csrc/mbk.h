@@ -485,12 +485,19 @@ struct RouteDecide {
 };
 // implicit_in: order_in holds launch_quantize's implicit u32 words (the
 // root level of an unsampled tree).
+// built_only (with decide and write_entries): of each split node only the
+// child that the next level's plan builds gets its entries written, the
+// child with the smaller integer hessian sum (ties left).  Only for the last
+// partition before the deepest split level, whose other children's entries
+// nothing reads, and only when every entry's quantised hessian is the same,
+// so that the smaller hessian sum is the smaller row count, the child the
+// plan builds.
 hipError_t launch_route(hipStream_t s, const Shape &sh, const LevelArgs &la,
                         const uint8_t *bins_fm, const Entry *order_in, Entry *order_out,
                         const uint32_t *seg_start, uint32_t *count, const TreeOut out,
                         uint64_t *cursors, uint32_t max_blocks, bool write_entries,
                         const RoutePlan *plan = nullptr, bool implicit_in = false,
-                        const RouteDecide *decide = nullptr);
+                        const RouteDecide *decide = nullptr, bool built_only = false);
 
 // la = the level being planned (d); reads level d-1's routed counts.
 hipError_t launch_plan_level(hipStream_t s, const Shape &sh, const LevelArgs &la,

@@ -1928,6 +1928,12 @@ static void grow_levelwise(Trainer &t, int tree) {
                                       t.route_cursor.ptr, out));
     };
 
+    // h = 1 for every row and no weights: every entry's quantised hessian is
+    // 127, so a child's integer hessian sum orders children as its row count
+    const int obj = t.p.objective;
+    const bool unit_hess = !t.gp.has_weights && (obj == OBJ_L2 || obj == OBJ_MAE ||
+                                                 obj == OBJ_HUBER || obj == OBJ_QUANTILE);
+
     // level 0
     hist(ord_cur, 0);
     split_level(sh0, 1, h_prev, h_cur, mbk::LevelArgs{0, 0, 1, 0});
@@ -1975,11 +1981,16 @@ static void grow_levelwise(Trainer &t, int tree) {
                                               t.preds_cur));
             break;
         }
-        // non-terminal here, so level d - 1 was decided by this partition's keys
+        // non-terminal here, so level d - 1 was decided by this partition's keys.
+        // Before the deepest split level only the children that level builds
+        // are read again (an unsampled tree's deepest rows are counted by the
+        // walk), so only their entries are written when the hessian sums
+        // name them.
         const mbk::RoutePlan rp = t.route_plan(ln, seg_next);
+        const bool built_only = d == t.D - 1 && !sampled && unit_hess;
         MB_HIP(mbk::launch_route(s, sh, lp, t.bins_fm.ptr, ord_cur, ord_next, seg_cur,
-                                 t.count.ptr, out, t.route_cursor.ptr,
-                                 t.route_grid, true, &rp, d == 1 && !sampled, &rd));
+                                 t.count.ptr, out, t.route_cursor.ptr, t.route_grid, true, &rp,
+                                 d == 1 && !sampled, &rd, built_only));
         std::swap(ord_cur, ord_next);
         std::swap(seg_cur, seg_next);
         std::swap(h_cur, h_prev);
