@@ -547,6 +547,34 @@ def test_depth_extremes_identical():
     check_identical(x, y, {"num_trees": 10, "max_depth": 1, "num_bins": 4})
 
 
+@pytest.mark.parametrize("depth,objective", [(2, "regression"), (3, "regression"), (3, "huber"),
+                                             (4, "mae"), (5, "regression")])
+def test_shallow_levelwise_partitions_identical(depth, objective):
+    # Unsampled, unweighted trees with h = 1 for every row: the root partition
+    # writes only its built child's entries, the level-1 partition (depth >= 3)
+    # takes every row from the root's implicit words, and the partition before
+    # the deepest split level writes only the children that level builds.
+    # Categorical and NaN-holed columns at the root and level 1; a row count
+    # of many partition blocks that is not a multiple of 64.
+    rng = np.random.default_rng(depth * 31 + len(objective))
+    n = 150_001
+    num = rng.random((5, n), dtype=np.float32)
+    num[rng.random((5, n)) < 0.1] = np.nan
+    cat = rng.integers(0, 20, (2, n)).astype(np.float32)
+    x = np.ascontiguousarray(np.concatenate([num[:3], cat[:1], num[3:], cat[1:]]))
+    y = (4 * np.nan_to_num(num[0], nan=0.3) + 1.5 * (cat[0] % 4) + 2 * np.nan_to_num(num[1])
+         + (cat[1] % 3) + rng.standard_normal(n)).astype(np.float32)
+    params = {"num_trees": 4, "max_depth": depth, "num_bins": 64, "objective": objective,
+              "categorical_features": [3, 6]}
+    if objective == "huber":
+        params["alpha"] = 1.0
+    _, ref = check_identical(x, y, params, is_cat=[0, 0, 0, 1, 0, 0, 1])
+    # both a categorical and a numeric split among the root and level-1 splits
+    top = ref.forest.feature[:, :3].ravel()
+    assert set(int(f) for f in top if f >= 0) & {3, 6}
+    assert set(int(f) for f in top if f >= 0) - {3, 6}
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1), (2, 3), (5, 9), (63, 17), (64, 33), (65, 65),
                                        (130, 100), (8193, 4)])
 def test_tiny_and_ragged_shapes_identical(rows, cols):
