@@ -33,7 +33,7 @@ def gpu_fit(x_fm, y, params, **kw):
     return h, obj
 
 
-def oracle_fit(x_fm, y, params, is_cat=None):
+def oracle_fit(x_fm, y, params, is_cat=None, w=None):
     p = dict(params)
     kw = dict(num_trees=p.pop("num_trees", 100), max_depth=p.pop("max_depth", 6),
               num_leaves=p.pop("num_leaves", 0), learning_rate=p.pop("learning_rate", 0.1),
@@ -63,12 +63,12 @@ def oracle_fit(x_fm, y, params, is_cat=None):
         if key in p:
             kw[key] = p.pop(key)
     assert not p, p
-    return O.fit_raw(x_fm, y, num_bins=nb, is_cat=is_cat, monotone=mono, **kw)
+    return O.fit_raw(x_fm, y, num_bins=nb, is_cat=is_cat, monotone=mono, w=w, **kw)
 
 
-def check_identical(x_fm, y, params, is_cat=None, x_test=None):
-    h, obj = gpu_fit(x_fm, y, params)
-    ref = oracle_fit(x_fm, y, params, is_cat)
+def check_identical(x_fm, y, params, is_cat=None, x_test=None, w=None):
+    h, obj = gpu_fit(x_fm, y, params, sample_weight=w)
+    ref = oracle_fit(x_fm, y, params, is_cat, w)
     nodes = ref.forest.nodes_per_tree
     got = model_io.forest_from_json(obj, nodes)
     assert np.float32(obj["baseScore"]) == np.float32(ref.base_score)

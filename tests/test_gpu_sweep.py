@@ -5,12 +5,13 @@ objective (L2, logistic, L1, quantile, Huber, Poisson, Tweedie), depth 1-9,
 level-wise or leaf-wise, 4-256 bins, categorical and NaN-holed columns,
 min_split_gain / lambda / min_child_weight, GOSS or bagging, feature
 fraction and monotone constraints; the GPU model must equal the oracle's in
-every array and its training predictions bit for bit (check_identical).
+every array and its training predictions bit for bit (check_identical).  The
+same draws with sample weights (zeros included), and multiclass draws.
 """
 import numpy as np
 import pytest
 
-from test_gpu_parity import check_identical
+from test_gpu_parity import check_identical, check_identical_mc
 
 pytestmark = pytest.mark.gpu
 
@@ -74,3 +75,27 @@ def draw_case(seed):
 def test_random_settings_identical(case):
     x, y, params, is_cat = draw_case(20261202 + case)
     check_identical(x, y, params, is_cat=is_cat)
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_random_weighted_settings_identical(case):
+    x, y, params, is_cat = draw_case(20261302 + case)
+    rng = np.random.default_rng(case)
+    w = (rng.random(y.shape[0]) * 2.0).astype(np.float32)
+    w[rng.random(y.shape[0]) < 0.1] = 0.0             # rows that count for nothing
+    check_identical(x, y, params, is_cat=is_cat, w=w)
+
+
+@pytest.mark.parametrize("case", range(15))
+def test_random_multiclass_settings_identical(case):
+    x, _, params, is_cat = draw_case(20261402 + case)
+    rng = np.random.default_rng(1000 + case)
+    k = int(rng.integers(3, 6))
+    base = np.nan_to_num(x[0], nan=0.5) + 0.3 * rng.standard_normal(x.shape[1])
+    y = np.clip((base * k).astype(np.int64), 0, k - 1).astype(np.float32)
+    # GOSS with multiclass is rejected, as the reference rejects it
+    params = {key: v for key, v in params.items()
+              if key not in ("objective", "alpha", "tweedie_variance_power", "goss",
+                             "goss_top_rate", "goss_other_rate")}
+    params.update(objective="multiclass", num_class=k)
+    check_identical_mc(x, y, params, is_cat=is_cat)
