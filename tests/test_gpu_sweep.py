@@ -6,12 +6,16 @@ level-wise or leaf-wise, 4-256 bins, categorical and NaN-holed columns,
 min_split_gain / lambda / min_child_weight, GOSS or bagging, feature
 fraction and monotone constraints; the GPU model must equal the oracle's in
 every array and its training predictions bit for bit (check_identical).  The
-same draws with sample weights (zeros included), and multiclass draws.
+same draws with sample weights (zeros included), multiclass draws, and the
+TreeSHAP values of drawn models (within 1e-5 relative of the oracle's).
 """
 import numpy as np
 import pytest
 
-from test_gpu_parity import check_identical, check_identical_mc
+import macboost_amd as mb
+import model_io
+import oracle_lib as O
+from test_gpu_parity import check_identical, check_identical_mc, gpu_fit
 
 pytestmark = pytest.mark.gpu
 
@@ -99,3 +103,14 @@ def test_random_multiclass_settings_identical(case):
                              "goss_top_rate", "goss_other_rate")}
     params.update(objective="multiclass", num_class=k)
     check_identical_mc(x, y, params, is_cat=is_cat)
+
+
+@pytest.mark.parametrize("case", range(20))
+def test_random_settings_treeshap(case):
+    x, y, params, _ = draw_case(20261502 + case)
+    rows = min(x.shape[1], 1500)
+    h, obj = gpu_fit(x, y, params)
+    xs = np.ascontiguousarray(x[:, :rows])
+    got = mb.predict_contrib(h, xs, feature_major=True)
+    want = O.treeshap(model_io.forest_from_json(obj), obj["baseScore"], obj["numBins"], xs)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
