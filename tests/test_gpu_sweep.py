@@ -5,7 +5,8 @@ objective (L2, logistic, L1, quantile, Huber, Poisson, Tweedie), depth 1-9,
 level-wise or leaf-wise, 4-256 bins, categorical and NaN-holed columns,
 min_split_gain / lambda / min_child_weight, GOSS or bagging, feature
 fraction and monotone constraints; the GPU model must equal the oracle's in
-every array and its training predictions bit for bit (check_identical).  The
+every array, and its predictions on the training rows and on held-out rows
+(unseen categories, NaN) bit for bit (check_identical).  The
 same draws with sample weights (zeros included), multiclass draws, and the
 TreeSHAP values of drawn models (within 1e-5 relative of the oracle's).
 """
@@ -75,10 +76,23 @@ def draw_case(seed):
     return np.ascontiguousarray(x), y, p, [1 if i in cats else 0 for i in range(f)]
 
 
+def held_out(x, is_cat, seed):
+    # 500 held-out rows: values past the training range, NaN holes, and for
+    # categorical columns unseen, negative and non-integer codes
+    rng = np.random.default_rng(seed)
+    f = x.shape[0]
+    xt = (rng.random((f, 500)) * 1.4 - 0.2).astype(np.float32)
+    xt[rng.random((f, 500)) < 0.2] = np.nan
+    for c in range(f):
+        if is_cat[c]:
+            xt[c] = (rng.integers(-2, 300, 500) + rng.choice([0.0, 0.3, 0.5], 500)).astype(np.float32)
+    return np.ascontiguousarray(xt)
+
+
 @pytest.mark.parametrize("case", range(80))
 def test_random_settings_identical(case):
     x, y, params, is_cat = draw_case(20261202 + case)
-    check_identical(x, y, params, is_cat=is_cat)
+    check_identical(x, y, params, is_cat=is_cat, x_test=held_out(x, is_cat, case))
 
 
 @pytest.mark.parametrize("case", range(30))
