@@ -1325,7 +1325,7 @@ static void setup_buffers(Trainer &t, const float *y, const float *w, const floa
     t.seg_b.alloc((size_t)1 << t.D);
     t.ctl.alloc(1);
     t.ensure_capacity(std::max(1, p.num_trees));
-    build_root_copy(t);
+    if (!t.has_root_copy) build_root_copy(t);   // (create_raw builds it after the binning)
     MB_HIP(hipStreamSynchronize(s));
     t.best_metric = effective_metric(p) == "auc" ? -INFINITY : INFINITY;
 }
@@ -1544,8 +1544,11 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
                                             p.num_bins, tile_w, t.sh.num_tiles, t.bins_tiled.ptr,
                                             t.bins_fm.ptr));
             }
-            t.edges.resize((size_t)cols * ne);
-            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
+            // the root pass's planar copy follows the binning on the compute
+            // stream, and the labels cross PCIe and are checked meanwhile; the
+            // edges' copy to the host waits for both kernels
+            t.sh_root = root_shape(t);
+            build_root_copy(t);
             hipStream_t cs2 = t.dev->copy_stream;
             t.labels.alloc((size_t)rows);
             upload(t.labels.ptr, y, (size_t)rows * 4, cs2);
@@ -1569,6 +1572,8 @@ static Trainer *create_raw(const Params &pin, const float *x, bool x_on_device, 
                                       hipMemcpyDeviceToHost, cs2));
                 MB_HIP(hipStreamSynchronize(cs2));
             }
+            t.edges.resize((size_t)cols * ne);
+            MB_HIP(hipMemcpyAsync(t.edges.data(), ed.ptr, t.edges.size() * 4, hipMemcpyDeviceToHost, s));
             MB_HIP(hipStreamSynchronize(cs2));
             if (xv && yv && vrows > 0) bin_valid(t, xv, vrows, ed.ptr);
             MB_HIP(hipStreamSynchronize(s));
