@@ -236,11 +236,21 @@ __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
         uint32_t seg[W / 4];                          // the row's W tile bytes
 #pragma unroll 1
         for (int c = 0; c < W; c += G) {
+            if (c >= nf) {                            // a last tile's padding: zeros, no search
+#pragma unroll
+                for (int q = 0; q < G / 4; ++q) seg[c / 4 + q] = 0u;
+                continue;
+            }
             float v[G];
             load(r, c, v);
             uint32_t b[G];
 #pragma unroll
             for (int k0 = 0; k0 < G; k0 += 4) {
+                if (c + k0 >= nf) {                   // padding features of this pass
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b[k0 + j] = 0u;
+                    continue;
+                }
                 uint32_t ix[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) ix[j] = 1;
