@@ -175,7 +175,7 @@ __device__ __forceinline__ void row_grad_at(const GradParams &gp, const float *_
 // gather layout needs no clearing.
 // ---------------------------------------------------------------------------
 
-constexpr int BIN_THREADS = 512;
+constexpr int BIN_THREADS = 1024;
 constexpr int BIN_ROWS = 4096;                        // rows per block
 
 template <int W>
