@@ -166,12 +166,12 @@ __device__ __forceinline__ void row_grad_at(const GradParams &gp, const float *_
 // one byte per lane, 64 consecutive bytes per wavefront store.  A value's bin
 // is the number of edges below it, lower_bound(edges, v) for the
 // non-decreasing quantile edges (the reference's binary search).  Each
-// feature's edges sit in LDS in breadth-first (Eytzinger) order of the
-// perfect search tree over the 255 slots (+inf padded): search step k reads
-// slots [2^k, 2^(k+1)), a contiguous range, so the lanes of a wavefront hit
-// distinct banks where sorted order put every step's candidates in one bank.
-// Eight steps of one LDS read, compare and index update; slot i - 256 at the
-// end is the bin.  Tiles past the last feature write zero bytes, so the
+// feature's edges sit in LDS as the perfect 4-ary search tree over the 256
+// bins (255 keys, +inf padded) in breadth-first order, three keys per node:
+// four dependent steps of three independent LDS reads and compares (where a
+// binary tree needs eight dependent reads), each level's nodes contiguous so
+// the lanes of a wavefront spread over the banks; the final node's index in
+// the leaf level is the bin.  Tiles past the last feature write zero bytes, so the
 // gather layout needs no clearing.
 // ---------------------------------------------------------------------------
 
@@ -201,11 +201,15 @@ __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
     for (int k = tid; k < W * 256; k += BIN_THREADS) {
         const int f = k >> 8, i = k & 255;
         float val = INFINITY;
-        if (i > 0 && f < nf) {
-            // BFS slot i of a perfect tree of height 8 holds the sorted slot of
-            // in-order rank ((2q + 1) << (7 - L)), L = depth of i, q = i - 2^L
-            const int L = 31 - __clz(i);
-            const int j = ((2 * (i - (1 << L)) + 1) << (7 - L)) - 1;
+        if (i < 255 && f < nf) {
+            // slot i is key kk (1..3) of node n = i / 3 of the perfect 4-ary
+            // tree over the 256 bins in breadth-first order: node n at depth L,
+            // position q in its level, splits its span of s = 256 / 4^L bins
+            // at q s + kk s / 4, i.e. holds sorted edge q s + kk s / 4 - 1
+            const int n = i / 3, kk = i - 3 * n + 1;
+            const int L = n == 0 ? 0 : n < 5 ? 1 : n < 21 ? 2 : 3;
+            const int q = n - ((1 << (2 * L)) - 1) / 3, span = 256 >> (2 * L);
+            const int j = q * span + kk * (span >> 2) - 1;
             if (j < ne) val = edges[(int64_t)(f0 + f) * ne + j];
         }
         e_lds[k] = val;
@@ -233,12 +237,21 @@ __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
         }
     };
     for (int64_t r = blk0 + tid; r < blk1; r += BIN_THREADS) {
-        uint32_t seg[W / 4];                          // the row's W tile bytes
+        // the row's W tile bytes: each pass shifts its G bytes in at the end,
+        // so after the W / G passes they are in order (fixed register indexes
+        // in a loop the compiler keeps rolled)
+        uint32_t seg[W / 4];
+        auto shift_in = [&](const uint32_t (&w4)[G / 4]) {
+#pragma unroll
+            for (int q = 0; q + G / 4 < W / 4; ++q) seg[q] = seg[q + G / 4];
+#pragma unroll
+            for (int q = 0; q < G / 4; ++q) seg[W / 4 - G / 4 + q] = w4[q];
+        };
 #pragma unroll 1
         for (int c = 0; c < W; c += G) {
             if (c >= nf) {                            // a last tile's padding: zeros, no search
-#pragma unroll
-                for (int q = 0; q < G / 4; ++q) seg[c / 4 + q] = 0u;
+                const uint32_t zero[G / 4] = {};
+                shift_in(zero);
                 continue;
             }
             float v[G];
@@ -251,20 +264,26 @@ __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
                     for (int j = 0; j < 4; ++j) b[k0 + j] = 0u;
                     continue;
                 }
+                // four levels of three comparisons: the child 4 n + 1 + (keys
+                // below v); the leaf's index in its level is the bin
                 uint32_t ix[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) ix[j] = 1;
+                for (int j = 0; j < 4; ++j) ix[j] = 0;
 #pragma unroll
-                for (int step = 0; step < 8; ++step) {
+                for (int level = 0; level < 4; ++level) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        ix[j] = 2 * ix[j] + (v[k0 + j] > e_lds[(c + k0 + j) * 256 + (int)ix[j]] ? 1u : 0u);
+                    for (int j = 0; j < 4; ++j) {
+                        const float *nk = e_lds + (c + k0 + j) * 256 + 3 * (int)ix[j];
+                        const float x = v[k0 + j];
+                        ix[j] = 4 * ix[j] + 1 + (x > nk[0] ? 1u : 0u) + (x > nk[1] ? 1u : 0u) +
+                                (x > nk[2] ? 1u : 0u);
+                    }
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int k = k0 + j;
                     const float val = v[k];
-                    uint32_t bb = ix[j] - 256u;
+                    uint32_t bb = ix[j] - 85u;               // 85 = (4^4 - 1) / 3
                     if (isnan(val)) {
                         bb = (uint32_t)data_bins;
                     } else if ((cat_bits >> (c + k)) & 1u) {
@@ -275,9 +294,11 @@ __global__ __launch_bounds__(BIN_THREADS) void k_bin_data(
                     b[k] = c + k < nf ? bb : 0u;
                 }
             }
+            uint32_t w4[G / 4];
 #pragma unroll
             for (int q = 0; q < G / 4; ++q)
-                seg[c / 4 + q] = b[4 * q] | (b[4 * q + 1] << 8) | (b[4 * q + 2] << 16) | (b[4 * q + 3] << 24);
+                w4[q] = b[4 * q] | (b[4 * q + 1] << 8) | (b[4 * q + 2] << 16) | (b[4 * q + 3] << 24);
+            shift_in(w4);
 #pragma unroll
             for (int k = 0; k < G; ++k)
                 if (c + k < nf) fm[(int64_t)(f0 + c + k) * rows + r] = (uint8_t)b[k];
